@@ -1,0 +1,274 @@
+#!/usr/bin/env python3
+"""Benchmark: one forward+backward rasterization step on one MI355X.
+
+Workload: 1,000,000 Gaussians, SH degree 3,
+one 1280x720 pinhole camera, gsplat_amd.rasterization() with the API defaults
+(packed=True, 16x16 tiles), L1 loss against a random target, backward to all
+Gaussian parameters.  Synthetic seeded data (gsplat_amd._helper.make_scene).
+
+Prints ONE JSON line (rank 0).  Besides ms/step it reports Mpix/s, a
+per-stage breakdown (HIP events around every C-ABI entry point, measured in a
+separate pass), the roofline of the dominant kernel (HIP events around that
+kernel inside the timed steps) and a CPU baseline: the host oracle pipeline
+(oracle/torch_ref.py, float32, autograd) timed on this machine's cores on a
+strided sample of the tiles, scaled to the full image.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "ms per fwd+bwd step @1M Gaussians 1280x720 SH3; Mpix/s; % HBM roofline"
+HBM_PEAK_GBS = 8000.0
+F32 = 4
+
+
+def _parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=1, choices=[0, 1, 2, 3, 4])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-tile-stride", type=int, default=0,
+                    help="rasterize every k-th tile in the CPU baseline (0: auto)")
+    ap.add_argument("--stages-only", action="store_true",
+                    help="print the per-stage breakdown and exit")
+    return ap.parse_args()
+
+
+def _algorithmic_bytes(name, ctx):
+    """Algorithmic HBM bytes of one launch of an entry point (each input read
+    once, each output written once) -- the roofline numerator."""
+    n_isects, nnz, N = ctx["n_isects"], ctx["nnz"], ctx["N"]
+    pix, D, tiles = ctx["pixels"], ctx["D"], ctx["tiles"]
+    K = ctx["K"]
+    gauss2d = 8 + 12 + 4 + F32 * D  # means2d, conic, opacity, colour
+    if name == "gsplat_rasterize_fwd":
+        return n_isects * (4 + gauss2d) + tiles * 4 + pix * (F32 * D + 4 + 4)
+    if name == "gsplat_rasterize_bwd":
+        return (n_isects * (4 + gauss2d) + tiles * 4 + pix * (4 + 4 + F32 * D + 4)
+                + nnz * (8 + 12 + F32 * D + 4))
+    if name == "gsplat_projection_packed_fwd":
+        return N * 44 + nnz * (24 + 8 + 8 + 4 + 12)
+    if name == "gsplat_projection_packed_bwd":
+        return N * 44 + nnz * (24 + 12 + 8 + 4 + 12) + N * 40
+    if name == "gsplat_sh_fwd":
+        return nnz * (12 + 12 * K + 1 + 12)
+    if name == "gsplat_sh_bwd":
+        return nnz * (12 + 12 * K + 1 + 12) + nnz * (12 * K + 12)
+    if name == "gsplat_adam_multi":
+        return ctx.get("adam_elems", 0) * 28
+    return None
+
+
+def _gpu_bench(args):
+    import torch
+
+    import gsplat_amd as gs
+    from gsplat_amd import _lib
+    from gsplat_amd._helper import make_scene
+
+    dev = "cuda:0"
+    scene = make_scene(args.config).to(dev)
+    C = scene.viewmats.shape[0]
+    params = {k: getattr(scene, k).clone().requires_grad_()
+              for k in ("means", "quats", "scales", "opacities", "colors")}
+    kw = dict(scene.kwargs)
+
+    def step():
+        for p in params.values():
+            p.grad = None
+        rc, ra, meta = gs.rasterization(
+            params["means"], params["quats"], params["scales"], params["opacities"],
+            params["colors"], scene.viewmats, scene.Ks, scene.width, scene.height,
+            sh_degree=scene.sh_degree, **kw)
+        loss = (rc - scene.target).abs().mean()
+        loss.backward()
+        return meta
+
+    for _ in range(args.warmup):
+        meta = step()
+    torch.cuda.synchronize()
+
+    # per-stage breakdown (separate pass, every entry point bracketed)
+    stage_timer = _lib.EntryTimer()
+    with _lib.timing(stage_timer):
+        for _ in range(3):
+            meta = step()
+    torch.cuda.synchronize()
+    stages = {k: sum(v) / 3.0 for k, v in stage_timer.results().items()}
+    dominant = max(stages, key=stages.get)
+
+    ctx = {
+        "n_isects": int(meta["isect_ids"].numel()),
+        "nnz": int(meta["means2d"].shape[0]) if meta["means2d"].dim() == 2 else
+        int((meta["radii"] > 0).all(-1).sum()),
+        "N": scene.means.shape[0],
+        "pixels": C * scene.width * scene.height,
+        "D": 3 if kw.get("render_mode", "RGB") == "RGB" else 4,
+        "tiles": C * meta["tile_width"] * meta["tile_height"],
+        "K": scene.colors.shape[-2] if scene.sh_degree is not None else 0,
+    }
+
+    # timed region: K steps, HIP events around the dominant entry point
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    dom_timer = _lib.EntryTimer({dominant})
+    t0.record()
+    with _lib.timing(dom_timer):
+        for _ in range(args.steps):
+            step()
+    t1.record()
+    torch.cuda.synchronize()
+    ms_per_step = t0.elapsed_time(t1) / args.steps
+    dom_ms = dom_timer.results()[dominant]
+    dom_avg = sum(dom_ms) / len(dom_ms)
+    abytes = _algorithmic_bytes(dominant, ctx)
+    roofline = None
+    if abytes is not None:
+        achieved = abytes / (dom_avg * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
+                    "traffic": _measured_traffic(dominant),
+                    "kernel": dominant, "avg_ms": round(dom_avg, 4),
+                    "algorithmic_bytes": int(abytes)}
+    stage_report = {}
+    for k, v in sorted(stages.items(), key=lambda kv: -kv[1]):
+        ab = _algorithmic_bytes(k, ctx)
+        e = {"ms": round(v, 4)}
+        if ab is not None and v > 0:
+            e["GBps"] = round(ab / (v * 1e-3) / 1e9, 1)
+        stage_report[k] = e
+    return {
+        "ms_per_step": ms_per_step,
+        "roofline": roofline,
+        "stages": stage_report,
+        "ctx": ctx,
+        "scene": scene,
+    }
+
+
+def _measured_traffic(kernel):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
+    f = ROOT / "profiles" / "pmc_traffic.txt"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        parts = line.split()
+        if len(parts) >= 2 and parts[0] == kernel:
+            try:
+                return int(float(parts[1]))
+            except ValueError:
+                return None
+    return None
+
+
+def _cpu_baseline(config, stride):
+    """Oracle pipeline on the host: full projection / SH / intersection for all
+    Gaussians, rasterization on every `stride`-th tile, fwd+bwd; the raster
+    share is scaled by `stride`."""
+    import torch
+
+    from gsplat_amd._helper import make_scene
+    from oracle import torch_ref
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    scene = make_scene(config)
+    C = scene.viewmats.shape[0]
+    tw = math.ceil(scene.width / 16)
+    th = math.ceil(scene.height / 16)
+    n_tiles = C * tw * th
+
+    def run(subset):
+        leaves = {k: getattr(scene, k).clone().requires_grad_()
+                  for k in ("means", "quats", "scales", "opacities", "colors")}
+        t = time.perf_counter()
+        rc, ra, meta = torch_ref.rasterization_ref(
+            leaves["means"], leaves["quats"], leaves["scales"], leaves["opacities"],
+            leaves["colors"], scene.viewmats, scene.Ks, scene.width, scene.height,
+            sh_degree=scene.sh_degree, dtype=torch.float32, tile_subset=subset,
+            **scene.kwargs)
+        loss = (rc - scene.target).abs().mean()
+        loss.backward()
+        return time.perf_counter() - t
+
+    sample = list(range(0, n_tiles, stride))
+    t_zero = run([])
+    t_sample = run(sample)
+    est = t_zero + (t_sample - t_zero) * (n_tiles / len(sample))
+    return {
+        "value": round(est * 1e3, 1),
+        "unit": "ms/step",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"config {config}: projection+SH+intersection+sort for all "
+                   f"{scene.means.shape[0]} Gaussians, rasterize fwd+bwd on {len(sample)} "
+                   f"of {n_tiles} tiles (every {stride}th), raster time x{n_tiles / len(sample):.1f}; "
+                   f"measured {t_zero:.1f}s + {t_sample:.1f}s"),
+    }
+
+
+def main():
+    args = _parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "bench.py runs on exactly one GPU: this build has no "
+                          "multi-GPU path (one-GPU boxes only); run with --gpus 1"}))
+        sys.exit(2)
+    res = _gpu_bench(args)
+    if args.stages_only:
+        print(json.dumps(res["stages"], indent=1))
+        return
+    scene = res["scene"]
+    C = scene.viewmats.shape[0]
+    mpix = C * scene.width * scene.height / (res["ms_per_step"] * 1e-3) / 1e6
+    cpu = None
+    if not args.no_cpu_baseline:
+        stride = args.cpu_tile_stride or {0: 1, 1: 12, 2: 48, 3: 30, 4: 20}[args.config]
+        cpu = _cpu_baseline(args.config, stride)
+    workload = {
+        0: "cfg0: 10k Gaussians, SH0, 256x256, packed, fwd+bwd L1",
+        1: "cfg1: 1M Gaussians, SH3, 1280x720, packed, fwd+bwd L1",
+        2: "cfg2: 500k Gaussians, SH1, 8x 960x540, packed, RGB+ED, fwd+bwd L1",
+        3: "cfg3: 6M Gaussians, SH3, 1920x1080, fwd+bwd L1",
+        4: "cfg4: 2M Gaussians, SH3, 1600x1040, fwd+bwd L1",
+    }[args.config]
+    out = {
+        "metric": METRIC,
+        "value": round(res["ms_per_step"], 4),
+        "unit": "ms/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms_per_step"], 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded, gsplat_amd._helper.make_scene)",
+        "config": {"workload": workload, "gaussians": int(scene.means.shape[0]),
+                   "width": scene.width, "height": scene.height, "cameras": C,
+                   "n_isects": res["ctx"]["n_isects"], "visible_rows": res["ctx"]["nnz"]},
+        "mpix_per_s": round(mpix, 2),
+        "roofline": res["roofline"],
+        "stages_ms": res["stages"],
+        "cpu_baseline": cpu,
+    }
+    if cpu is not None:
+        out["speedup_vs_cpu"] = round(cpu["value"] / res["ms_per_step"], 1)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,210 @@
+"""ctypes binding of libgsplat_hip.so, the C ABI declared in include/gsplat_hip.h.
+
+This is the only place Python touches the native library.  Every call passes
+raw device pointers, sizes and the current HIP stream; return codes are turned
+into ``RuntimeError`` carrying the library's message.  There is no fallback:
+if the library is missing or a tensor is not on the GPU, the call fails.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_float, c_int32, c_int64, c_size_t, c_void_p
+from pathlib import Path
+from typing import Optional
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libgsplat_hip.so"
+
+_P = c_void_p
+# name -> argtypes (restype int unless listed in _RESTYPES)
+_SIGNATURES = {
+    "gsplat_last_error": [],
+    "gsplat_version": [],
+    "gsplat_projection_fused_fwd": [
+        c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P,
+        c_int32, c_int32, c_float, c_float, c_float, c_float, c_int32,
+        _P, _P, _P, _P, _P, _P],
+    "gsplat_projection_fused_bwd": [
+        c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P,
+        c_int32, c_int32, c_float, c_int32,
+        _P, _P, _P, _P, _P, _P, _P,
+        _P, _P, _P, _P, _P, _P],
+    "gsplat_projection_packed_workspace_size": [c_int64, c_int64, c_int64],
+    "gsplat_projection_packed_fwd": [
+        c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P,
+        c_int32, c_int32, c_float, c_float, c_float, c_float, c_int32,
+        _P, c_size_t,
+        _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+    "gsplat_projection_packed_bwd": [
+        c_int64, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P,
+        c_int32, c_int32, c_float, c_int32,
+        _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int32,
+        _P, _P, _P, _P, _P, _P],
+    "gsplat_sh_fwd": [c_int64, c_int32, c_int32, _P, _P, _P, _P, _P],
+    "gsplat_sh_bwd": [c_int64, c_int32, c_int32, _P, _P, _P, _P, _P, _P, _P],
+    "gsplat_isect_count_workspace_size": [c_int64],
+    "gsplat_isect_count": [
+        c_int64, c_int64, _P, _P, _P, _P, _P, c_int32, c_int32, c_int32,
+        _P, c_size_t, _P, _P, _P],
+    "gsplat_isect_emit": [
+        c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P,
+        c_int32, c_int32, c_int32, _P, _P, _P, _P],
+    "gsplat_sort_pairs_workspace_size": [c_int64],
+    "gsplat_sort_pairs_u64_u32": [
+        c_int64, c_int32, _P, _P, _P, _P, _P, c_size_t, _P],
+    "gsplat_isect_offsets": [c_int64, _P, c_int64, c_int32, c_int32, _P, _P],
+    "gsplat_rasterize_fwd": [
+        c_int64, c_int64, c_int64, c_int32, _P, _P, _P, _P, _P, _P,
+        c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P],
+    "gsplat_rasterize_bwd": [
+        c_int64, c_int64, c_int64, c_int32, _P, _P, _P, _P, _P, _P,
+        c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P,
+        _P, _P, _P, _P, _P, _P],
+    "gsplat_adam_multi": [_P, c_int32, c_float, c_float, c_float, _P],
+    "gsplat_adam": [
+        _P, _P, _P, _P, _P, c_int64, c_int64, c_float, c_float, c_float,
+        c_float, _P],
+}
+_RESTYPES = {
+    "gsplat_last_error": ctypes.c_char_p,
+    "gsplat_version": ctypes.c_char_p,
+    "gsplat_projection_packed_workspace_size": c_size_t,
+    "gsplat_isect_count_workspace_size": c_size_t,
+    "gsplat_sort_pairs_workspace_size": c_size_t,
+}
+
+
+class AdamTensor(ctypes.Structure):
+    """Mirror of ``gsplat_adam_tensor`` (include/gsplat_hip.h)."""
+
+    _fields_ = [
+        ("param", c_void_p),
+        ("grad", c_void_p),
+        ("exp_avg", c_void_p),
+        ("exp_avg_sq", c_void_p),
+        ("valid", c_void_p),
+        ("n_rows", c_int64),
+        ("row_size", c_int64),
+        ("lr", c_float),
+    ]
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libgsplat_hip.so (once) and declare its signatures."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build it with `python -m gsplat_amd.build` "
+            "(the HIP kernels are the only implementation; there is no fallback)"
+        )
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, argtypes in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = _RESTYPES.get(name, ctypes.c_int)
+    _lib = lib
+    return lib
+
+
+class EntryTimer:
+    """Records HIP events on the current stream around chosen entry points.
+
+    ``EntryTimer({"gsplat_rasterize_bwd"})`` installed with ``timing(...)``
+    brackets every call of those entry points; ``results()`` (after a device
+    synchronize) gives the per-entry list of durations in ms.  An empty set
+    times every entry point.
+    """
+
+    def __init__(self, names=None):
+        self.names = set(names or ())
+        self.events = {}
+
+    def wants(self, name: str) -> bool:
+        return not self.names or name in self.names
+
+    def record(self, name: str):
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        return e
+
+    def add(self, name: str, start, end) -> None:
+        self.events.setdefault(name, []).append((start, end))
+
+    def results(self):
+        return {k: [s.elapsed_time(e) for s, e in v] for k, v in self.events.items()}
+
+
+_timer: Optional[EntryTimer] = None
+
+
+class timing:
+    """Context manager installing an EntryTimer."""
+
+    def __init__(self, timer: EntryTimer):
+        self.timer = timer
+
+    def __enter__(self):
+        global _timer
+        self.prev, _timer = _timer, self.timer
+        return self.timer
+
+    def __exit__(self, *exc):
+        global _timer
+        _timer = self.prev
+        return False
+
+
+def call(name: str, *args) -> None:
+    """Invoke an int-returning entry point and raise on failure."""
+    lib = load()
+    t = _timer
+    if t is not None and t.wants(name):
+        start = t.record(name)
+        rc = getattr(lib, name)(*args)
+        t.add(name, start, t.record(name))
+    else:
+        rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.gsplat_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed ({rc}): {msg}")
+
+
+def query(name: str, *args) -> int:
+    """Invoke a size-returning entry point."""
+    return int(getattr(load(), name)(*args))
+
+
+def version() -> str:
+    return load().gsplat_version().decode()
+
+
+def stream() -> int:
+    """Handle of the current HIP stream of the current device."""
+    return torch.cuda.current_stream().cuda_stream
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    """Device address of a tensor (None for None)."""
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def check_input(t: Optional[torch.Tensor], name: str, dtype: Optional[torch.dtype] = None):
+    """Device + contiguity (+ dtype) check, mirroring CHECK_INPUT
+    (gsplat/cuda/include/Common.h:31-36)."""
+    if t is None:
+        return
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a GPU tensor")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+    if dtype is not None and t.dtype != dtype:
+        raise RuntimeError(f"{name} must have dtype {dtype}, got {t.dtype}")

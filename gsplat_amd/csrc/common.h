@@ -1,0 +1,284 @@
+// Shared device and host helpers for the gfx950 kernels of libgsplat_hip.so.
+//
+// Device side: the splatting constants, wave64 reductions built on DPP row
+// operations, saturating float->int conversion, a portable natural log whose
+// result is reproducible bit for bit on the host, and the decoupled look-back
+// prefix used by the single-pass compaction kernels.
+// Host side: per-thread error text and argument / launch checks shared by the
+// extern "C" entry points.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+
+#include "../../include/gsplat_hip.h"
+
+namespace gs {
+
+// Constants of the splatting model (gsplat/cuda/include/Common.h:73-93,
+// gsplat/cuda/_constants.py:16-29).
+constexpr float kAlphaThreshold = 1.f / 255.f;
+constexpr float kGaussianExtend = 3.33f;
+constexpr float kMaxAlpha = 0.99f;
+constexpr float kTransmittanceThreshold = 1e-4f;
+constexpr float kMinCompensation = 0.005f;
+constexpr float kMinOneMinusAlpha = 1e-6f;
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// Host-side error plumbing.
+// ---------------------------------------------------------------------------
+void set_error(const std::string &msg);
+void clear_error();
+int fail(int code, const std::string &msg);
+// Returns GSPLAT_OK or GSPLAT_ERR_LAUNCH after a kernel launch.
+int check_launch(const char *what);
+
+#define GS_REQUIRE(cond, msg)                                                  \
+    do {                                                                       \
+        if (!(cond))                                                           \
+            return ::gs::fail(GSPLAT_ERR_INVALID_ARGUMENT, (msg));             \
+    } while (0)
+
+#define GS_TRY(expr)                                                           \
+    do {                                                                       \
+        int _gs_rc = (expr);                                                   \
+        if (_gs_rc != GSPLAT_OK)                                               \
+            return _gs_rc;                                                     \
+    } while (0)
+
+inline hipStream_t as_stream(gsplat_stream_t s) {
+    return reinterpret_cast<hipStream_t>(s);
+}
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline bool aligned16(const void *p) {
+    return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+// ---------------------------------------------------------------------------
+// Device helpers.
+// ---------------------------------------------------------------------------
+
+// Float -> int32 with defined results for every input: NaN -> 0, values
+// beyond the int32 range saturate, everything else truncates toward zero.
+// The same rule is spelled out in the host oracle.
+__device__ __forceinline__ int32_t sat_f2i(float x) {
+    if (!(x == x))
+        return 0;
+    if (x >= 2147483648.f)
+        return 2147483647;
+    if (x <= -2147483648.f)
+        return (-2147483647 - 1);
+    return (int32_t)x;
+}
+
+// Natural logarithm from its series: x = 2^e * m with m in [sqrt(1/2),
+// sqrt(2)), s = (m-1)/(m+1), ln m = 2s + 2s^3/3 + 2s^5/5 + 2s^7/7 + 2s^9/9.
+// Only IEEE +, -, *, / are used and contraction is disabled, so the host
+// oracle reproduces every bit.  Valid for positive normal x; returns NaN for
+// x <= 0 or NaN, +inf for +inf.  Accuracy is a few ulp, which matches the
+// fast log the reference uses for the opacity-aware extent.
+__device__ __forceinline__ float portable_logf(float x) {
+#pragma clang fp contract(off)
+    if (!(x > 0.f))
+        return __builtin_nanf("");
+    if (x == __builtin_inff())
+        return x;
+    uint32_t bits = __float_as_uint(x);
+    int32_t e = (int32_t)((bits >> 23) & 0xffu) - 127;
+    float m = __uint_as_float((bits & 0x007fffffu) | 0x3f800000u);
+    if (e == -127) {
+        // subnormal input: renormalise by 2^23
+        float xs = x * 8388608.f;
+        bits = __float_as_uint(xs);
+        e = (int32_t)((bits >> 23) & 0xffu) - 127 - 23;
+        m = __uint_as_float((bits & 0x007fffffu) | 0x3f800000u);
+    }
+    if (m > 1.41421356f) {
+        m = m * 0.5f;
+        e = e + 1;
+    }
+    const float f = m - 1.f;
+    const float s = f / (2.f + f);
+    const float z = s * s;
+    const float r =
+        z * (0.666666667f + z * (0.4f + z * (0.285714286f + z * 0.222222222f)));
+    const float lnm = (s + s) + s * r;
+    const float ef = (float)e;
+    // ln 2 split as hi + lo with hi carrying 7 trailing zero bits, so ef*hi
+    // is exact for |e| <= 128.
+    return ef * 0x1.62e3p-1f + (lnm + ef * 0x1.2fefa2p-17f);
+}
+
+// DPP row operations (gfx9 encodings).
+constexpr int kDppQuadXor1 = 0xB1;   // quad_perm:[1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;   // quad_perm:[2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+template <int CTRL> __device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(
+        0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the lanes of a wave; every lane receives the total (in a scalar
+// register).  Must be called in wave-uniform control flow where every 16-lane
+// row is either fully active or fully inactive (true for workgroups whose size
+// is a multiple of 16); inactive rows are excluded through EXEC.  The
+// association order is fixed, so the result is deterministic.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_f32<kDppQuadXor1>(v);
+    v += dpp_f32<kDppQuadXor2>(v);
+    v += dpp_f32<kDppRowHalfMirror>(v);
+    v += dpp_f32<kDppRowMirror>(v);
+    const int iv = __float_as_int(v);
+    const uint64_t ex = __builtin_amdgcn_read_exec();
+    const float r0 = (ex & 0xffffull)
+                         ? __int_as_float(__builtin_amdgcn_readlane(iv, 0))
+                         : 0.f;
+    const float r1 = ((ex >> 16) & 0xffffull)
+                         ? __int_as_float(__builtin_amdgcn_readlane(iv, 16))
+                         : 0.f;
+    const float r2 = ((ex >> 32) & 0xffffull)
+                         ? __int_as_float(__builtin_amdgcn_readlane(iv, 32))
+                         : 0.f;
+    const float r3 = ((ex >> 48) & 0xffffull)
+                         ? __int_as_float(__builtin_amdgcn_readlane(iv, 48))
+                         : 0.f;
+    return (r0 + r1) + (r2 + r3);
+}
+
+// Maximum over the wave.  In a partially populated wave the shuffles may read
+// lanes that never ran; their stale values can only raise the result, so use
+// it only where an over-estimate is harmless (a conservative bound).
+__device__ __forceinline__ int wave_max_i32(int v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1)
+        v = max(v, __shfl_xor(v, off));
+    return v;
+}
+
+__device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+    return (1ull << lane_id()) - 1ull;
+}
+
+// Inclusive scan of a 64-bit value over the wave (Hillis-Steele).
+__device__ __forceinline__ uint64_t wave_inclusive_scan_u64(uint64_t v) {
+    const uint32_t lane = lane_id();
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        uint64_t o = __shfl_up(v, off);
+        if (lane >= (uint32_t)off)
+            v += o;
+    }
+    return v;
+}
+
+__device__ __forceinline__ void atomic_add_f32(float *p, float v) {
+    unsafeAtomicAdd(p, v);
+}
+
+// ---------------------------------------------------------------------------
+// Decoupled look-back prefix (single-pass scan across workgroups).
+//
+// Workgroups take a ticket in launch order so every predecessor of a ticket
+// holder is already resident or finished; each publishes its aggregate, then
+// its inclusive prefix, in a 64-bit status word: flag in bits 62-63, value in
+// bits 0-61.  The status array and the ticket counter must be zero before the
+// launch (see clear_lookback).
+// ---------------------------------------------------------------------------
+constexpr uint64_t kLbFlagAgg = 1ull << 62;
+constexpr uint64_t kLbFlagInc = 2ull << 62;
+constexpr uint64_t kLbValMask = (1ull << 62) - 1ull;
+
+struct Lookback {
+    uint32_t *ticket;  // one counter
+    uint64_t *status;  // one word per workgroup
+};
+
+// Bytes of workspace for n_blocks workgroups (ticket padded to 256 B).
+inline size_t lookback_bytes(int64_t n_blocks) {
+    return 256 + (size_t)n_blocks * sizeof(uint64_t);
+}
+
+inline Lookback lookback_from(void *ws) {
+    Lookback lb;
+    lb.ticket = reinterpret_cast<uint32_t *>(ws);
+    lb.status = reinterpret_cast<uint64_t *>(reinterpret_cast<char *>(ws) + 256);
+    return lb;
+}
+
+// Zero the ticket and status words (a kernel, not a memset, so the sequence
+// stays valid under stream capture).
+int clear_lookback(void *ws, int64_t n_blocks, hipStream_t stream);
+
+__device__ __forceinline__ uint64_t lb_load(const uint64_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void lb_store(uint64_t *p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Workgroup-uniform ticket (call from every thread; contains a barrier).
+__device__ __forceinline__ uint32_t lb_ticket(const Lookback &lb,
+                                              uint32_t *smem_slot) {
+    if (threadIdx.x == 0)
+        *smem_slot = atomicAdd(lb.ticket, 1u);
+    __syncthreads();
+    return *smem_slot;
+}
+
+// Called by all 64 lanes of ONE wave after `aggregate` of workgroup `bid` is
+// known; returns (in every lane) the exclusive prefix of workgroup bid and
+// publishes its inclusive prefix.
+__device__ __forceinline__ uint64_t lb_exclusive_prefix(const Lookback &lb,
+                                                        uint32_t bid,
+                                                        uint64_t aggregate) {
+    const uint32_t lane = lane_id();
+    if (bid == 0) {
+        if (lane == 0)
+            lb_store(lb.status, kLbFlagInc | aggregate);
+        return 0;
+    }
+    if (lane == 0)
+        lb_store(lb.status + bid, kLbFlagAgg | aggregate);
+    uint64_t excl = 0;
+    int64_t base = (int64_t)bid - 1;
+    while (true) {
+        const int64_t idx = base - (int64_t)lane;
+        uint64_t s = (idx >= 0) ? lb_load(lb.status + idx) : kLbFlagInc;
+        // wait until every predecessor in the window has published something
+        while (__ballot((s >> 62) == 0)) {
+            __builtin_amdgcn_s_sleep(1);
+            if ((s >> 62) == 0)
+                s = lb_load(lb.status + idx);
+        }
+        const uint64_t inc = __ballot((s >> 62) == 2);
+        uint64_t v = s & kLbValMask;
+        if (inc) {
+            const uint32_t first = __builtin_ctzll(inc);  // closest inclusive
+            if (lane > first)
+                v = 0;
+            // sum of lanes 0..first
+            for (int off = 32; off >= 1; off >>= 1)
+                v += __shfl_xor(v, off);
+            excl += v;
+            break;
+        }
+        for (int off = 32; off >= 1; off >>= 1)
+            v += __shfl_xor(v, off);
+        excl += v;
+        base -= 64;
+    }
+    if (lane == 0)
+        lb_store(lb.status + bid, kLbFlagInc | (excl + aggregate));
+    return excl;
+}
+
+}  // namespace gs

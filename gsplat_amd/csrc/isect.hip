@@ -1,0 +1,409 @@
+// Tile intersection: per-row tile sets, key emission and tile offsets.
+//
+// Semantics: gsplat/cuda/csrc/IntersectTile.cu
+//   :38-121  ellipse ("AccuTile") column sweep,
+//   :133-288 count / emit kernel (ellipse test when conics+opacities are
+//            given, otherwise the axis-aligned box of the integer radii),
+//   :391-439 tile offsets by key-boundary detection,
+// and the host logic of gsplat/cuda/csrc/Intersect.cpp:33-164 (key layout
+// image | tile | depth-bits, image_n_bits = bit_length(I), tile_n_bits =
+// bit_length(tiles)).
+//
+// MI355X design: the count pass also produces the inclusive int64 prefix of
+// the counts with a decoupled look-back, so the reference's separate cumsum
+// kernel disappears.  Every floating-point step that decides which tiles are
+// emitted runs in a fixed IEEE order with contraction disabled, with a
+// defined float->int conversion (saturating, NaN -> 0) and a portable log, so
+// the C host oracle reproduces the integer outputs bit for bit.  Count and
+// emit call the same device function, so the two passes agree exactly.
+#include "common.h"
+
+namespace gs {
+namespace {
+
+constexpr int kIsectThreads = 256;
+
+struct IsectArgs {
+    int64_t n;      // rows
+    int64_t N;      // Gaussians per image (dense layout)
+    int64_t I;      // images
+    const int64_t *image_ids;  // packed layout: image of each row
+    const float *means2d;
+    const int32_t *radii;
+    const float *depths;
+    const float *conics;
+    const float *opacities;
+    int32_t tile_size, tile_width, tile_height;
+    int32_t tile_n_bits;
+};
+
+struct Emitter {
+    int64_t *isect_ids;
+    int32_t *flatten_ids;
+    int64_t cursor;
+    int64_t end;      // first slot of the next row (writes stay below it)
+    int64_t key_hi;   // (image << (32 + tile_n_bits))
+    int64_t depth_lo; // zero-extended depth bits
+    int32_t flat;
+    __device__ __forceinline__ void put(int64_t tile_id) {
+        if (cursor < end) {
+            isect_ids[cursor] = key_hi | (tile_id << 32) | depth_lo;
+            flatten_ids[cursor] = flat;
+        }
+        ++cursor;
+    }
+};
+
+__device__ __forceinline__ int imin(int a, int b) { return a < b ? a : b; }
+__device__ __forceinline__ int imax(int a, int b) { return a > b ? a : b; }
+
+// Lower / upper root of the conic level set along the line u = coord.
+__device__ __forceinline__ void ellipse_line(float A, float B, float C,
+                                             float disc, float t, float px,
+                                             float py, bool isY, float coord,
+                                             float &lo, float &hi) {
+#pragma clang fp contract(off)
+    const float p_u = isY ? py : px;
+    const float p_v = isY ? px : py;
+    const float coeff = isY ? A : C;
+    const float h = coord - p_u;
+    const float sq = sqrtf((disc * h) * h + t * coeff);
+    const float mbh = (-B) * h;
+    lo = (mbh - sq) / coeff + p_v;
+    hi = (mbh + sq) / coeff + p_v;
+}
+
+// Number of tiles touched by one row; emits them when `em` is non-null.
+template <bool EMIT>
+__device__ __forceinline__ int32_t row_tiles(const IsectArgs &a, int64_t idx,
+                                             Emitter *em) {
+#pragma clang fp contract(off)
+    const int2 r = reinterpret_cast<const int2 *>(a.radii)[idx];
+    const float radius_x = (float)r.x;
+    const float radius_y = (float)r.y;
+    if (radius_x <= 0.f || radius_y <= 0.f)
+        return 0;
+    const float2 mean = reinterpret_cast<const float2 *>(a.means2d)[idx];
+    const int tw = a.tile_width, th = a.tile_height;
+    const float ts = (float)a.tile_size;
+
+    if (a.conics != nullptr && a.opacities != nullptr) {
+        const float A = a.conics[idx * 3 + 0];
+        const float B = a.conics[idx * 3 + 1];
+        const float C = a.conics[idx * 3 + 2];
+        const float disc = B * B - A * C;
+        const float opacity = a.opacities[idx];
+        const float t = fminf(kGaussianExtend * kGaussianExtend,
+                              2.0f * portable_logf(opacity / kAlphaThreshold));
+        // Guard: the level set is empty unless t >= 0 and the conic is
+        // positive definite (disc < 0); the reference reaches 0 tiles in these
+        // cases through NaN extents, here they are made explicit.
+        if (!(t >= 0.f) || !(disc < 0.f))
+            return 0;
+        const float nt = (-t) / disc;
+        const float x_ext = sqrtf(nt * C);
+        const float y_ext = sqrtf(nt * A);
+        float bmin_x = mean.x - x_ext, bmin_y = mean.y - y_ext;
+        float bmax_x = mean.x + x_ext, bmax_y = mean.y + y_ext;
+        const float bx_over_c = (B * x_ext) / C;
+        const float by_over_a = (B * y_ext) / A;
+        // argmin/argmax: (.x = y where x is extreme, .y = x where y is extreme)
+        float amin_x = mean.y + bx_over_c, amin_y = mean.x + by_over_a;
+        float amax_x = mean.y - bx_over_c, amax_y = mean.x - by_over_a;
+        int rmin_x = imax(0, imin(tw, sat_f2i(bmin_x / ts)));
+        int rmin_y = imax(0, imin(th, sat_f2i(bmin_y / ts)));
+        int rmax_x = imax(0, imin(tw, sat_f2i(bmax_x / ts + 1.f)));
+        int rmax_y = imax(0, imin(th, sat_f2i(bmax_y / ts + 1.f)));
+        const int y_span = rmax_y - rmin_y;
+        const int x_span = rmax_x - rmin_x;
+        if (y_span == 0 || x_span == 0)
+            return 0;
+        const bool isY = y_span < x_span;
+        if (isY) {
+            // sweep along y: swap the roles of the axes
+            int ti;
+            float tf;
+            ti = rmin_x; rmin_x = rmin_y; rmin_y = ti;
+            ti = rmax_x; rmax_x = rmax_y; rmax_y = ti;
+            tf = bmin_x; bmin_x = bmin_y; bmin_y = tf;
+            tf = bmax_x; bmax_x = bmax_y; bmax_y = tf;
+            tf = amin_x; amin_x = amin_y; amin_y = tf;
+            tf = amax_x; amax_x = amax_y; amax_y = tf;
+        }
+        int32_t count = 0;
+        // (lo, hi) roots at the previous and current line
+        float max_lo = bmax_y, max_hi = bmin_y;
+        float min_lo, min_hi;
+        float min_line = (float)rmin_x * ts;
+        if (bmin_x <= min_line) {
+            ellipse_line(A, B, C, disc, t, mean.x, mean.y, isY, min_line,
+                         min_lo, min_hi);
+        } else {
+            min_lo = max_lo;
+            min_hi = max_hi;
+        }
+        for (int u = rmin_x; u < rmax_x; ++u) {
+            const float max_line = min_line + ts;
+            if (max_line <= bmax_x)
+                ellipse_line(A, B, C, disc, t, mean.x, mean.y, isY, max_line,
+                             max_lo, max_hi);
+            float e_min, e_max;
+            if (min_line <= amin_y && amin_y < max_line)
+                e_min = bmin_y;
+            else
+                e_min = fminf(min_lo, max_lo);
+            if (min_line <= amax_y && amax_y < max_line)
+                e_max = bmax_y;
+            else
+                e_max = fmaxf(min_hi, max_hi);
+            const int v0 = imax(rmin_y, imin(rmax_y, sat_f2i(e_min / ts)));
+            const int v1 = imin(rmax_y, imax(rmin_y, sat_f2i(e_max / ts + 1.f)));
+            if (v1 > v0) {
+                count += v1 - v0;
+                if (EMIT) {
+                    for (int v = v0; v < v1; ++v) {
+                        const int64_t tile =
+                            isY ? (int64_t)u * tw + v : (int64_t)v * tw + u;
+                        em->put(tile);
+                    }
+                }
+            }
+            min_lo = max_lo;
+            min_hi = max_hi;
+            min_line = max_line;
+        }
+        return count;
+    }
+
+    // axis-aligned box of the integer radii
+    const float trx = radius_x / ts, try_ = radius_y / ts;
+    const float tx = mean.x / ts, ty = mean.y / ts;
+    const int x0 = imin(imax(0, sat_f2i(floorf(tx - trx))), tw);
+    const int y0 = imin(imax(0, sat_f2i(floorf(ty - try_))), th);
+    const int x1 = imin(imax(0, sat_f2i(ceilf(tx + trx))), tw);
+    const int y1 = imin(imax(0, sat_f2i(ceilf(ty + try_))), th);
+    if (EMIT) {
+        for (int y = y0; y < y1; ++y)
+            for (int x = x0; x < x1; ++x)
+                em->put((int64_t)y * tw + x);
+    }
+    return (y1 - y0) * (x1 - x0);
+}
+
+__global__ void __launch_bounds__(kIsectThreads)
+    isect_count_kernel(const IsectArgs a, Lookback lb,
+                       int32_t *__restrict__ tiles_per_gauss,
+                       int64_t *__restrict__ cum_tiles) {
+    __shared__ uint32_t s_ticket;
+    __shared__ uint64_t s_wave_tot[kIsectThreads / kWave];
+    __shared__ uint64_t s_prefix;
+    const uint32_t bid = lb_ticket(lb, &s_ticket);
+    const int64_t idx = (int64_t)bid * kIsectThreads + threadIdx.x;
+    int32_t cnt = 0;
+    if (idx < a.n)
+        cnt = row_tiles<false>(a, idx, nullptr);
+    // block scan of the counts
+    const uint64_t incl = wave_inclusive_scan_u64((uint64_t)cnt);
+    const uint32_t wave = threadIdx.x / kWave;
+    if (lane_id() == kWave - 1)
+        s_wave_tot[wave] = incl;
+    __syncthreads();
+    uint64_t wave_off = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < kIsectThreads / kWave; ++w) {
+        const uint64_t v = s_wave_tot[w];
+        wave_off += (w < (int)wave) ? v : 0ull;
+        total += v;
+    }
+    if (wave == 0) {
+        const uint64_t excl = lb_exclusive_prefix(lb, bid, total);
+        if (lane_id() == 0)
+            s_prefix = excl;
+    }
+    __syncthreads();
+    if (idx < a.n) {
+        tiles_per_gauss[idx] = cnt;
+        cum_tiles[idx] = (int64_t)(s_prefix + wave_off + incl);
+    }
+}
+
+__global__ void __launch_bounds__(kIsectThreads)
+    isect_emit_kernel(const IsectArgs a, const int64_t *__restrict__ cum_tiles,
+                      int64_t *__restrict__ isect_ids,
+                      int32_t *__restrict__ flatten_ids) {
+    const int64_t idx = (int64_t)blockIdx.x * kIsectThreads + threadIdx.x;
+    if (idx >= a.n)
+        return;
+    const int32_t r0 = a.radii[idx * 2], r1 = a.radii[idx * 2 + 1];
+    if (r0 <= 0 || r1 <= 0)
+        return;
+    Emitter em;
+    em.isect_ids = isect_ids;
+    em.flatten_ids = flatten_ids;
+    em.cursor = idx == 0 ? 0 : cum_tiles[idx - 1];
+    em.end = cum_tiles[idx];
+    const int64_t iid = a.image_ids != nullptr ? a.image_ids[idx] : idx / a.N;
+    em.key_hi = iid << (32 + a.tile_n_bits);
+    em.depth_lo = (int64_t)(uint64_t)__float_as_uint(a.depths[idx]);
+    em.flat = (int32_t)idx;
+    row_tiles<true>(a, idx, &em);
+}
+
+__global__ void isect_offsets_kernel(int64_t n_isects,
+                                     const int64_t *__restrict__ isect_ids,
+                                     int64_t n_slots, int32_t tile_n_bits,
+                                     int32_t n_tiles,
+                                     int32_t *__restrict__ offsets) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= n_isects)
+        return;
+    const int64_t mask = (1ll << tile_n_bits) - 1;
+    const int64_t key = isect_ids[idx] >> 32;
+    const int64_t cur = (key >> tile_n_bits) * n_tiles + (key & mask);
+    if (idx == 0) {
+        for (int64_t i = 0; i <= cur && i < n_slots; ++i)
+            offsets[i] = 0;
+    } else {
+        const int64_t pkey = isect_ids[idx - 1] >> 32;
+        if (pkey != key) {
+            const int64_t prev = (pkey >> tile_n_bits) * n_tiles + (pkey & mask);
+            for (int64_t i = prev + 1; i <= cur && i < n_slots; ++i)
+                offsets[i] = (int32_t)idx;
+        }
+    }
+    if (idx == n_isects - 1) {
+        for (int64_t i = cur + 1; i < n_slots; ++i)
+            offsets[i] = (int32_t)n_isects;
+    }
+}
+
+__global__ void fill_i32_kernel(int32_t *p, int64_t n, int32_t v) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n)
+        p[i] = v;
+}
+
+int bit_length(int64_t v) {
+    int b = 0;
+    while (v > 0) {
+        ++b;
+        v >>= 1;
+    }
+    return b;
+}
+
+int make_args(int64_t n, int64_t N, int64_t I, const int64_t *image_ids,
+              const float *means2d, const int32_t *radii, const float *depths,
+              const float *conics, const float *opacities, int32_t tile_size,
+              int32_t tile_width, int32_t tile_height, IsectArgs &a) {
+    GS_REQUIRE(n >= 0, "isect: negative row count");
+    GS_REQUIRE(tile_size > 0 && tile_width > 0 && tile_height > 0,
+               "isect: tile sizes must be positive");
+    GS_REQUIRE(image_ids != nullptr || N > 0 || n == 0,
+               "isect: dense layout needs N > 0");
+    if (n > 0)
+        GS_REQUIRE(means2d && radii, "isect: NULL means2d/radii");
+    const int tb = bit_length((int64_t)tile_width * tile_height);
+    a.n = n;
+    a.N = N;
+    a.I = I;
+    a.image_ids = image_ids;
+    a.means2d = means2d;
+    a.radii = radii;
+    a.depths = depths;
+    a.conics = conics;
+    a.opacities = opacities;
+    a.tile_size = tile_size;
+    a.tile_width = tile_width;
+    a.tile_height = tile_height;
+    a.tile_n_bits = tb;
+    return GSPLAT_OK;
+}
+
+}  // namespace
+}  // namespace gs
+
+using namespace gs;
+
+extern "C" size_t gsplat_isect_count_workspace_size(int64_t n) {
+    return lookback_bytes(ceil_div(n, kIsectThreads));
+}
+
+extern "C" int gsplat_isect_count(int64_t n, int64_t N,
+                                  const int64_t *image_ids,
+                                  const float *means2d, const int32_t *radii,
+                                  const float *conics, const float *opacities,
+                                  int32_t tile_size, int32_t tile_width,
+                                  int32_t tile_height, void *workspace,
+                                  size_t workspace_bytes,
+                                  int32_t *tiles_per_gauss, int64_t *cum_tiles,
+                                  gsplat_stream_t stream) {
+    clear_error();
+    IsectArgs a;
+    GS_TRY(make_args(n, N, 0, image_ids, means2d, radii, nullptr, conics,
+                     opacities, tile_size, tile_width, tile_height, a));
+    if (n == 0)
+        return GSPLAT_OK;
+    GS_REQUIRE(tiles_per_gauss && cum_tiles, "isect_count: NULL output");
+    GS_REQUIRE(n < (1ll << 31), "isect_count: more than 2^31 rows");
+    const int64_t blocks = ceil_div(n, kIsectThreads);
+    GS_REQUIRE(workspace && workspace_bytes >= lookback_bytes(blocks),
+               "isect_count: workspace too small");
+    hipStream_t st = as_stream(stream);
+    GS_TRY(clear_lookback(workspace, blocks, st));
+    isect_count_kernel<<<(unsigned)blocks, kIsectThreads, 0, st>>>(
+        a, lookback_from(workspace), tiles_per_gauss, cum_tiles);
+    return check_launch("isect_count_kernel");
+}
+
+extern "C" int gsplat_isect_emit(int64_t n, int64_t N, int64_t I,
+                                 const int64_t *image_ids,
+                                 const float *means2d, const int32_t *radii,
+                                 const float *depths, const float *conics,
+                                 const float *opacities, int32_t tile_size,
+                                 int32_t tile_width, int32_t tile_height,
+                                 const int64_t *cum_tiles, int64_t *isect_ids,
+                                 int32_t *flatten_ids, gsplat_stream_t stream) {
+    clear_error();
+    IsectArgs a;
+    GS_TRY(make_args(n, N, I, image_ids, means2d, radii, depths, conics,
+                     opacities, tile_size, tile_width, tile_height, a));
+    if (n == 0)
+        return GSPLAT_OK;
+    GS_REQUIRE(depths && cum_tiles && isect_ids && flatten_ids,
+               "isect_emit: NULL buffer");
+    GS_REQUIRE(I > 0, "isect_emit: I must be positive");
+    const int ib = bit_length(I);
+    GS_REQUIRE(ib + a.tile_n_bits <= 32,
+               "isect_emit: image and tile ids need more than 32 bits");
+    isect_emit_kernel<<<(unsigned)ceil_div(n, kIsectThreads), kIsectThreads, 0,
+                        as_stream(stream)>>>(a, cum_tiles, isect_ids,
+                                             flatten_ids);
+    return check_launch("isect_emit_kernel");
+}
+
+extern "C" int gsplat_isect_offsets(int64_t n_isects, const int64_t *isect_ids,
+                                    int64_t I, int32_t tile_width,
+                                    int32_t tile_height, int32_t *offsets,
+                                    gsplat_stream_t stream) {
+    clear_error();
+    GS_REQUIRE(n_isects >= 0 && I >= 0, "isect_offsets: negative size");
+    GS_REQUIRE(tile_width > 0 && tile_height > 0,
+               "isect_offsets: tile sizes must be positive");
+    const int64_t n_tiles = (int64_t)tile_width * tile_height;
+    const int64_t n_slots = I * n_tiles;
+    if (n_slots == 0)
+        return GSPLAT_OK;
+    GS_REQUIRE(offsets != nullptr, "isect_offsets: NULL offsets");
+    hipStream_t st = as_stream(stream);
+    if (n_isects == 0) {
+        fill_i32_kernel<<<(unsigned)ceil_div(n_slots, 256), 256, 0, st>>>(
+            offsets, n_slots, 0);
+        return check_launch("fill_i32_kernel");
+    }
+    GS_REQUIRE(isect_ids != nullptr, "isect_offsets: NULL isect_ids");
+    const int tb = bit_length(n_tiles);
+    isect_offsets_kernel<<<(unsigned)ceil_div(n_isects, 256), 256, 0, st>>>(
+        n_isects, isect_ids, n_slots, tb, (int32_t)n_tiles, offsets);
+    return check_launch("isect_offsets_kernel");
+}

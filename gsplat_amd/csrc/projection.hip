@@ -1,0 +1,1028 @@
+// EWA projection of 3D Gaussians to screen-space conics, forward and
+// backward, dense ("fused") and packed layouts.
+//
+// Semantics follow gsplat/cuda/csrc/ProjectionEWA3DGSFused.cu:38-234 and
+// ProjectionEWA3DGSPacked.cu:39-286 (math in gsplat/cuda/include/Utils.cuh:
+// posW2C :50, covarW2C :83, quat_to_rotmat :174, quat_scale_to_covar :223,
+// add_blur :424, persp_proj :542, persp_proj_vjp :583).
+//
+// MI355X design:
+//   * one thread per (camera, Gaussian) row, consecutive lanes on consecutive
+//     Gaussians so the AoS input rows ([N,3], [N,4]) of a wave form one
+//     contiguous span (768 B / 1 KiB) and every output row stream is written
+//     contiguously;
+//   * the forward is written in a fixed IEEE operation order with contraction
+//     disabled, so the integer outputs (radii, validity, packed order) are
+//     reproducible bit for bit by the C host oracle;
+//   * the packed forward is ONE pass: rows are compacted with wave ballots and
+//     a decoupled look-back prefix, replacing the reference's count pass, host
+//     cumsum/sync and second projection pass;
+//   * the dense backward gives each Gaussian to one thread that loops over
+//     the C cameras, so gradients need no atomics and are deterministic.
+#include "common.h"
+
+namespace gs {
+namespace {
+
+constexpr int kProjThreads = 256;
+
+struct Cam {
+    float R[9];  // row-major world->camera rotation
+    float t[3];
+    float fx, fy, cx, cy;
+};
+
+__device__ __forceinline__ void load_cam(const float *viewmat, const float *K,
+                                         Cam &cam) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+            cam.R[i * 3 + j] = viewmat[i * 4 + j];
+        cam.t[i] = viewmat[i * 4 + 3];
+    }
+    cam.fx = K[0];
+    cam.fy = K[4];
+    cam.cx = K[2];
+    cam.cy = K[5];
+}
+
+// Symmetric 3x3 stored as (00, 01, 02, 11, 12, 22).
+struct Sym3 {
+    float a00, a01, a02, a11, a12, a22;
+};
+
+struct ProjOut {
+    float mx, my, depth;
+    float ca, cb, cc;  // conic (upper triangle of the inverse 2D covariance)
+    float comp;
+    int32_t rx, ry;
+};
+
+// ---------------------------------------------------------------------------
+// Exact forward (fixed op order, no contraction).  Returns false for culled
+// rows.  The host oracle (oracle/exact_ref.c) restates this sequence.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void quat_to_rot_exact(float w, float x, float y,
+                                                  float z, float M[9]) {
+#pragma clang fp contract(off)
+    const float n2 = ((x * x + y * y) + z * z) + w * w;
+    const float inv = 1.0f / sqrtf(n2);
+    x = x * inv;
+    y = y * inv;
+    z = z * inv;
+    w = w * inv;
+    const float x2 = x * x, y2 = y * y, z2 = z * z;
+    const float xy = x * y, xz = x * z, yz = y * z;
+    const float wx = w * x, wy = w * y, wz = w * z;
+    M[0] = 1.f - 2.f * (y2 + z2);
+    M[1] = 2.f * (xy - wz);
+    M[2] = 2.f * (xz + wy);
+    M[3] = 2.f * (xy + wz);
+    M[4] = 1.f - 2.f * (x2 + z2);
+    M[5] = 2.f * (yz - wx);
+    M[6] = 2.f * (xz - wy);
+    M[7] = 2.f * (yz + wx);
+    M[8] = 1.f - 2.f * (x2 + y2);
+}
+
+__device__ __forceinline__ Sym3 covar_from_quat_scale_exact(const float *q,
+                                                            const float *s) {
+#pragma clang fp contract(off)
+    float M[9];
+    quat_to_rot_exact(q[0], q[1], q[2], q[3], M);
+    float A[9];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        A[i * 3 + 0] = M[i * 3 + 0] * s[0];
+        A[i * 3 + 1] = M[i * 3 + 1] * s[1];
+        A[i * 3 + 2] = M[i * 3 + 2] * s[2];
+    }
+#define GS_DOT_ROWS(i, j)                                                      \
+    ((A[(i) * 3 + 0] * A[(j) * 3 + 0] + A[(i) * 3 + 1] * A[(j) * 3 + 1]) +     \
+     A[(i) * 3 + 2] * A[(j) * 3 + 2])
+    Sym3 S;
+    S.a00 = GS_DOT_ROWS(0, 0);
+    S.a01 = GS_DOT_ROWS(0, 1);
+    S.a02 = GS_DOT_ROWS(0, 2);
+    S.a11 = GS_DOT_ROWS(1, 1);
+    S.a12 = GS_DOT_ROWS(1, 2);
+    S.a22 = GS_DOT_ROWS(2, 2);
+#undef GS_DOT_ROWS
+    return S;
+}
+
+__device__ __forceinline__ bool project_exact(
+    const Cam &cam, const float *mean, const float *covar6, const float *quat,
+    const float *scale, bool has_opacity, float opacity, bool calc_comp,
+    int camera_model, float W, float H, float eps2d, float near_plane,
+    float far_plane, float radius_clip, ProjOut &o) {
+#pragma clang fp contract(off)
+    const float *R = cam.R;
+    const float p0 = mean[0], p1 = mean[1], p2 = mean[2];
+    const float mcx = ((R[0] * p0 + R[1] * p1) + R[2] * p2) + cam.t[0];
+    const float mcy = ((R[3] * p0 + R[4] * p1) + R[5] * p2) + cam.t[1];
+    const float mcz = ((R[6] * p0 + R[7] * p1) + R[8] * p2) + cam.t[2];
+    if (mcz < near_plane || mcz > far_plane)
+        return false;
+
+    Sym3 S;
+    if (covar6 != nullptr) {
+        S.a00 = covar6[0];
+        S.a01 = covar6[1];
+        S.a02 = covar6[2];
+        S.a11 = covar6[3];
+        S.a12 = covar6[4];
+        S.a22 = covar6[5];
+    } else {
+        S = covar_from_quat_scale_exact(quat, scale);
+    }
+    // B = R * S
+    const float Sf[9] = {S.a00, S.a01, S.a02, S.a01, S.a11,
+                         S.a12, S.a02, S.a12, S.a22};
+    float Bm[9];
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+            Bm[i * 3 + j] = (R[i * 3 + 0] * Sf[0 * 3 + j] +
+                             R[i * 3 + 1] * Sf[1 * 3 + j]) +
+                            R[i * 3 + 2] * Sf[2 * 3 + j];
+    // Sc = B * R^T (upper triangle)
+#define GS_SC(i, j)                                                            \
+    ((Bm[(i) * 3 + 0] * R[(j) * 3 + 0] + Bm[(i) * 3 + 1] * R[(j) * 3 + 1]) +   \
+     Bm[(i) * 3 + 2] * R[(j) * 3 + 2])
+    const float s00 = GS_SC(0, 0), s01 = GS_SC(0, 1), s02 = GS_SC(0, 2);
+    const float s11 = GS_SC(1, 1), s12 = GS_SC(1, 2), s22 = GS_SC(2, 2);
+#undef GS_SC
+
+    float J00, J02, J11, J12, mx, my;
+    if (camera_model == GSPLAT_CAMERA_ORTHO) {
+        J00 = cam.fx;
+        J11 = cam.fy;
+        J02 = 0.f;
+        J12 = 0.f;
+        mx = cam.fx * mcx + cam.cx;
+        my = cam.fy * mcy + cam.cy;
+    } else {
+        const float tan_fovx = (0.5f * W) / cam.fx;
+        const float tan_fovy = (0.5f * H) / cam.fy;
+        const float lim_x_pos = (W - cam.cx) / cam.fx + 0.3f * tan_fovx;
+        const float lim_x_neg = cam.cx / cam.fx + 0.3f * tan_fovx;
+        const float lim_y_pos = (H - cam.cy) / cam.fy + 0.3f * tan_fovy;
+        const float lim_y_neg = cam.cy / cam.fy + 0.3f * tan_fovy;
+        const float rz = 1.f / mcz;
+        const float rz2 = rz * rz;
+        const float tx = mcz * fminf(lim_x_pos, fmaxf(-lim_x_neg, mcx * rz));
+        const float ty = mcz * fminf(lim_y_pos, fmaxf(-lim_y_neg, mcy * rz));
+        J00 = cam.fx * rz;
+        J11 = cam.fy * rz;
+        J02 = ((-cam.fx) * tx) * rz2;
+        J12 = ((-cam.fy) * ty) * rz2;
+        mx = ((cam.fx * mcx) * rz) + cam.cx;
+        my = ((cam.fy * mcy) * rz) + cam.cy;
+    }
+    // cov2d = J Sc J^T with J = [[J00, 0, J02], [0, J11, J12]]
+    const float u0 = s00 * J00 + s02 * J02;
+    const float u1 = s01 * J00 + s12 * J02;
+    const float u2 = s02 * J00 + s22 * J02;
+    const float w1 = s11 * J11 + s12 * J12;
+    const float w2 = s12 * J11 + s22 * J12;
+    const float c00 = J00 * u0 + J02 * u2;
+    const float c01 = J11 * u1 + J12 * u2;
+    const float c11 = J11 * w1 + J12 * w2;
+
+    // low-pass blur + compensation (add_blur)
+    const float det_orig = c00 * c11 - c01 * c01;
+    const float c00b = c00 + eps2d;
+    const float c11b = c11 + eps2d;
+    const float det = c00b * c11b - c01 * c01;
+    if (!(det > 0.f))
+        return false;
+    const float comp =
+        sqrtf(fmaxf(kMinCompensation * kMinCompensation, det_orig / det));
+    const float inv_det = 1.f / det;
+
+    float extend = kGaussianExtend;
+    if (has_opacity) {
+        float op = opacity;
+        if (calc_comp)
+            op = op * comp;
+        if (op < kAlphaThreshold)
+            return false;
+        extend = fminf(kGaussianExtend,
+                       sqrtf(2.f * portable_logf(op / kAlphaThreshold)));
+    }
+    const float rx = ceilf(extend * sqrtf(c00b));
+    const float ry = ceilf(extend * sqrtf(c11b));
+    if (rx <= radius_clip && ry <= radius_clip)
+        return false;
+    if (mx + rx <= 0.f || mx - rx >= W || my + ry <= 0.f || my - ry >= H)
+        return false;
+
+    o.mx = mx;
+    o.my = my;
+    o.depth = mcz;
+    o.ca = c11b * inv_det;
+    o.cb = (-c01) * inv_det;
+    o.cc = c00b * inv_det;
+    o.comp = comp;
+    o.rx = sat_f2i(rx);
+    o.ry = sat_f2i(ry);
+    return true;
+}
+
+// ---------------------------------------------------------------------------
+// Forward kernels.
+// ---------------------------------------------------------------------------
+struct FwdArgs {
+    int64_t B, C, N;
+    const float *means, *covars, *quats, *scales, *opacities;
+    const float *viewmats, *Ks;
+    float W, H, eps2d, near_plane, far_plane, radius_clip;
+    int camera_model;
+    bool calc_comp;
+};
+
+__device__ __forceinline__ bool project_flat_row(const FwdArgs &a, int64_t row,
+                                                 ProjOut &o) {
+    const int64_t g = row % a.N;
+    const int64_t bc = row / a.N;  // b * C + c
+    const int64_t b = bc / a.C;
+    Cam cam;
+    load_cam(a.viewmats + bc * 16, a.Ks + bc * 9, cam);
+    const int64_t bg = b * a.N + g;
+    return project_exact(
+        cam, a.means + bg * 3, a.covars ? a.covars + bg * 6 : nullptr,
+        a.quats ? a.quats + bg * 4 : nullptr,
+        a.scales ? a.scales + bg * 3 : nullptr, a.opacities != nullptr,
+        a.opacities ? a.opacities[bg] : 0.f, a.calc_comp, a.camera_model, a.W,
+        a.H, a.eps2d, a.near_plane, a.far_plane, a.radius_clip, o);
+}
+
+__global__ void __launch_bounds__(kProjThreads)
+    projection_fused_fwd_kernel(const FwdArgs a, int32_t *__restrict__ radii,
+                                float *__restrict__ means2d,
+                                float *__restrict__ depths,
+                                float *__restrict__ conics,
+                                float *__restrict__ compensations) {
+    const int64_t row = (int64_t)blockIdx.x * kProjThreads + threadIdx.x;
+    if (row >= a.B * a.C * a.N)
+        return;
+    ProjOut o;
+    const bool valid = project_flat_row(a, row, o);
+    if (!valid) {
+        o.mx = o.my = o.depth = o.ca = o.cb = o.cc = o.comp = 0.f;
+        o.rx = o.ry = 0;
+    }
+    reinterpret_cast<int2 *>(radii)[row] = make_int2(o.rx, o.ry);
+    reinterpret_cast<float2 *>(means2d)[row] = make_float2(o.mx, o.my);
+    depths[row] = o.depth;
+    conics[row * 3 + 0] = o.ca;
+    conics[row * 3 + 1] = o.cb;
+    conics[row * 3 + 2] = o.cc;
+    if (compensations != nullptr)
+        compensations[row] = o.comp;
+}
+
+__global__ void __launch_bounds__(kProjThreads) projection_packed_fwd_kernel(
+    const FwdArgs a, Lookback lb, int32_t *__restrict__ indptr,
+    int64_t *__restrict__ batch_ids, int64_t *__restrict__ camera_ids,
+    int64_t *__restrict__ gaussian_ids, int32_t *__restrict__ radii,
+    float *__restrict__ means2d, float *__restrict__ depths,
+    float *__restrict__ conics, float *__restrict__ compensations,
+    int64_t *__restrict__ nnz_out) {
+    __shared__ uint32_t s_ticket;
+    __shared__ uint32_t s_wave_count[kProjThreads / kWave];
+    __shared__ uint64_t s_prefix;
+
+    const int64_t n_rows = a.B * a.C * a.N;
+    const uint32_t bid = lb_ticket(lb, &s_ticket);
+    const int64_t row = (int64_t)bid * kProjThreads + threadIdx.x;
+    ProjOut o;
+    const bool valid = row < n_rows && project_flat_row(a, row, o);
+
+    const uint32_t wave = threadIdx.x / kWave;
+    const uint64_t ballot = __ballot(valid);
+    const uint32_t rank_in_wave = __popcll(ballot & lanemask_lt());
+    if (lane_id() == 0)
+        s_wave_count[wave] = (uint32_t)__popcll(ballot);
+    __syncthreads();
+    uint32_t wave_offset = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < kProjThreads / kWave; ++w) {
+        const uint32_t cnt = s_wave_count[w];
+        wave_offset += (w < (int)wave) ? cnt : 0u;
+        total += cnt;
+    }
+    if (wave == 0) {
+        const uint64_t excl = lb_exclusive_prefix(lb, bid, total);
+        if (lane_id() == 0)
+            s_prefix = excl;
+    }
+    __syncthreads();
+    const int64_t base = (int64_t)s_prefix;
+    const int64_t pos = base + wave_offset + rank_in_wave;
+
+    if (row < n_rows && row % a.N == 0) {
+        // first Gaussian of camera row bc: its exclusive position is indptr
+        indptr[row / a.N] = (int32_t)pos;
+    }
+    if (valid) {
+        const int64_t g = row % a.N;
+        const int64_t bc = row / a.N;
+        batch_ids[pos] = bc / a.C;
+        camera_ids[pos] = bc % a.C;
+        gaussian_ids[pos] = g;
+        reinterpret_cast<int2 *>(radii)[pos] = make_int2(o.rx, o.ry);
+        reinterpret_cast<float2 *>(means2d)[pos] = make_float2(o.mx, o.my);
+        depths[pos] = o.depth;
+        conics[pos * 3 + 0] = o.ca;
+        conics[pos * 3 + 1] = o.cb;
+        conics[pos * 3 + 2] = o.cc;
+        if (compensations != nullptr)
+            compensations[pos] = o.comp;
+    }
+    const int64_t last_bid = (n_rows - 1) / kProjThreads;
+    if ((int64_t)bid == last_bid && threadIdx.x == 0) {
+        const int64_t nnz = base + total;
+        indptr[a.B * a.C] = (int32_t)nnz;
+        *nnz_out = nnz;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Backward math (contraction allowed; validated against autograd).
+// ---------------------------------------------------------------------------
+struct M3 {
+    float m[9];  // row-major
+};
+
+__device__ __forceinline__ M3 mm(const M3 &a, const M3 &b) {
+    M3 r;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+            r.m[i * 3 + j] = a.m[i * 3 + 0] * b.m[0 * 3 + j] +
+                             a.m[i * 3 + 1] * b.m[1 * 3 + j] +
+                             a.m[i * 3 + 2] * b.m[2 * 3 + j];
+    return r;
+}
+__device__ __forceinline__ M3 mtm(const M3 &a, const M3 &b) {  // a^T b
+    M3 r;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+            r.m[i * 3 + j] = a.m[0 * 3 + i] * b.m[0 * 3 + j] +
+                             a.m[1 * 3 + i] * b.m[1 * 3 + j] +
+                             a.m[2 * 3 + i] * b.m[2 * 3 + j];
+    return r;
+}
+__device__ __forceinline__ M3 mmt(const M3 &a, const M3 &b) {  // a b^T
+    M3 r;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+            r.m[i * 3 + j] = a.m[i * 3 + 0] * b.m[j * 3 + 0] +
+                             a.m[i * 3 + 1] * b.m[j * 3 + 1] +
+                             a.m[i * 3 + 2] * b.m[j * 3 + 2];
+    return r;
+}
+
+struct GaussGeom {
+    M3 S;       // world covariance (full symmetric)
+    M3 Rq;      // rotation from the quaternion (quats path only)
+    float q[4]; // raw quaternion
+    float s[3]; // scales
+};
+
+__device__ __forceinline__ void load_geom(const float *covar6, const float *quat,
+                                          const float *scale, GaussGeom &G) {
+    if (covar6 != nullptr) {
+        const float c[6] = {covar6[0], covar6[1], covar6[2],
+                            covar6[3], covar6[4], covar6[5]};
+        G.S.m[0] = c[0]; G.S.m[1] = c[1]; G.S.m[2] = c[2];
+        G.S.m[3] = c[1]; G.S.m[4] = c[3]; G.S.m[5] = c[4];
+        G.S.m[6] = c[2]; G.S.m[7] = c[4]; G.S.m[8] = c[5];
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        G.q[i] = quat[i];
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+        G.s[i] = scale[i];
+    quat_to_rot_exact(G.q[0], G.q[1], G.q[2], G.q[3], G.Rq.m);
+    M3 A;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+            A.m[i * 3 + k] = G.Rq.m[i * 3 + k] * G.s[k];
+    G.S = mmt(A, A);
+}
+
+// Gradient of one (camera, Gaussian) row: accumulates dL/dmean (world),
+// dL/dS (world covariance, full 3x3) and, if wanted, dL/dR, dL/dt.
+__device__ __forceinline__ void project_row_vjp(
+    const Cam &cam, const float *mean, const GaussGeom &G, int camera_model,
+    float W, float H, float eps2d, const float *conic, bool has_comp,
+    float comp, float v_comp, float v_mx, float v_my, float v_depth,
+    const float *v_conic, float v_mean[3], M3 &v_S, bool want_cam, M3 &v_R,
+    float v_t[3]) {
+    M3 R;
+#pragma unroll
+    for (int i = 0; i < 9; ++i)
+        R.m[i] = cam.R[i];
+    const float p[3] = {mean[0], mean[1], mean[2]};
+    float mc[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+        mc[i] = R.m[i * 3 + 0] * p[0] + R.m[i * 3 + 1] * p[1] +
+                R.m[i * 3 + 2] * p[2] + cam.t[i];
+    const M3 Sc = mmt(mm(R, G.S), R);
+
+    // d/d(cov2d): inverse VJP  dL/dC = -Ci * dL/dCi * Ci (symmetric split)
+    const float ia = conic[0], ib = conic[1], ic = conic[2];
+    const float ga = v_conic[0], gb = 0.5f * v_conic[1], gc = v_conic[2];
+    // T = Ci * G
+    const float t00 = ia * ga + ib * gb, t01 = ia * gb + ib * gc;
+    const float t10 = ib * ga + ic * gb, t11 = ib * gb + ic * gc;
+    float vc00 = -(t00 * ia + t01 * ib);
+    float vc01 = -(t00 * ib + t01 * ic);
+    float vc10 = -(t10 * ia + t11 * ib);
+    float vc11 = -(t10 * ib + t11 * ic);
+    if (has_comp) {
+        // comp = sqrt(det(C) / det(C + eps I)); conic is the blurred inverse
+        const float det_conic = ia * ic - ib * ib;
+        const float v_sqr_comp = v_comp * 0.5f / (comp + 1e-6f);
+        const float one_minus = 1.f - comp * comp;
+        vc00 += v_sqr_comp * (one_minus * ia - eps2d * det_conic);
+        vc01 += v_sqr_comp * (one_minus * ib);
+        vc10 += v_sqr_comp * (one_minus * ib);
+        vc11 += v_sqr_comp * (one_minus * ic - eps2d * det_conic);
+    }
+
+    const float fx = cam.fx, fy = cam.fy;
+    const float x = mc[0], y = mc[1], z = mc[2];
+    float J[6];  // row-major 2x3
+    float vmc[3];
+    M3 vSc;
+    if (camera_model == GSPLAT_CAMERA_ORTHO) {
+        J[0] = fx; J[1] = 0.f; J[2] = 0.f;
+        J[3] = 0.f; J[4] = fy; J[5] = 0.f;
+        vmc[0] = fx * v_mx;
+        vmc[1] = fy * v_my;
+        vmc[2] = 0.f;
+    } else {
+        const float tan_fovx = 0.5f * W / fx, tan_fovy = 0.5f * H / fy;
+        const float lim_x_pos = (W - cam.cx) / fx + 0.3f * tan_fovx;
+        const float lim_x_neg = cam.cx / fx + 0.3f * tan_fovx;
+        const float lim_y_pos = (H - cam.cy) / fy + 0.3f * tan_fovy;
+        const float lim_y_neg = cam.cy / fy + 0.3f * tan_fovy;
+        const float rz = 1.f / z, rz2 = rz * rz, rz3 = rz2 * rz;
+        const float tx = z * fminf(lim_x_pos, fmaxf(-lim_x_neg, x * rz));
+        const float ty = z * fminf(lim_y_pos, fmaxf(-lim_y_neg, y * rz));
+        J[0] = fx * rz; J[1] = 0.f; J[2] = -fx * tx * rz2;
+        J[3] = 0.f; J[4] = fy * rz; J[5] = -fy * ty * rz2;
+        vmc[0] = fx * rz * v_mx;
+        vmc[1] = fy * rz * v_my;
+        vmc[2] = -(fx * x * v_mx + fy * y * v_my) * rz2;
+        // dJ = G J Sc^T + G^T J Sc (Sc symmetric): vJ = (G + G^T) J Sc
+        const float g00 = vc00 + vc00, g01 = vc01 + vc10, g11 = vc11 + vc11;
+        float JS[6];
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int c = 0; c < 3; ++c)
+                JS[r * 3 + c] = J[r * 3 + 0] * Sc.m[0 * 3 + c] +
+                                J[r * 3 + 1] * Sc.m[1 * 3 + c] +
+                                J[r * 3 + 2] * Sc.m[2 * 3 + c];
+        float vJ[6];
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            vJ[0 * 3 + c] = g00 * JS[c] + g01 * JS[3 + c];
+            vJ[1 * 3 + c] = g01 * JS[c] + g11 * JS[3 + c];
+        }
+        const float xr = x * rz, yr = y * rz;
+        if (xr <= lim_x_pos && xr >= -lim_x_neg)
+            vmc[0] += -fx * rz2 * vJ[2];
+        else
+            vmc[2] += -fx * rz3 * vJ[2] * tx;
+        if (yr <= lim_y_pos && yr >= -lim_y_neg)
+            vmc[1] += -fy * rz2 * vJ[5];
+        else
+            vmc[2] += -fy * rz3 * vJ[5] * ty;
+        vmc[2] += -fx * rz2 * vJ[0] - fy * rz2 * vJ[4] +
+                  2.f * fx * tx * rz3 * vJ[2] + 2.f * fy * ty * rz3 * vJ[5];
+    }
+    // v_Sc = J^T G J
+    {
+        float GJ[6];  // G (2x2) * J (2x3)
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            GJ[0 * 3 + c] = vc00 * J[c] + vc01 * J[3 + c];
+            GJ[1 * 3 + c] = vc10 * J[c] + vc11 * J[3 + c];
+        }
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+                vSc.m[i * 3 + j] = J[0 * 3 + i] * GJ[0 * 3 + j] +
+                                   J[1 * 3 + i] * GJ[1 * 3 + j];
+    }
+    vmc[2] += v_depth;
+
+    // mean: mc = R p + t
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+        v_mean[j] += R.m[0 * 3 + j] * vmc[0] + R.m[1 * 3 + j] * vmc[1] +
+                     R.m[2 * 3 + j] * vmc[2];
+    // covariance: Sc = R S R^T  ->  dS = R^T dSc R
+    const M3 dS = mm(mtm(R, vSc), R);
+#pragma unroll
+    for (int i = 0; i < 9; ++i)
+        v_S.m[i] += dS.m[i];
+    if (want_cam) {
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+                v_R.m[i * 3 + j] += vmc[i] * p[j];
+            v_t[i] += vmc[i];
+        }
+        // dR = dSc R S^T + dSc^T R S
+        const M3 RS = mm(R, G.S);
+        const M3 a1 = mm(vSc, RS);   // S symmetric: R S^T == R S
+        const M3 a2 = mtm(vSc, RS);
+#pragma unroll
+        for (int i = 0; i < 9; ++i)
+            v_R.m[i] += a1.m[i] + a2.m[i];
+    }
+}
+
+// dL/dS (full) -> dL/dquat, dL/dscale  (quat_scale_to_covar_vjp +
+// quat_to_rotmat_vjp, Utils.cuh:197-296).
+__device__ __forceinline__ void covar_vjp_to_quat_scale(const GaussGeom &G,
+                                                        const M3 &v_S,
+                                                        float v_q[4],
+                                                        float v_s[3]) {
+    // S = M M^T with M = Rq diag(s):  dM = (dS + dS^T) M
+    M3 Mx;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+            Mx.m[i * 3 + k] = G.Rq.m[i * 3 + k] * G.s[k];
+    M3 sym;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+            sym.m[i * 3 + j] = v_S.m[i * 3 + j] + v_S.m[j * 3 + i];
+    const M3 vM = mm(sym, Mx);
+    // dRq = dM diag(s);  ds_k = sum_i Rq[i][k] dM[i][k]
+    M3 g;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+            g.m[i * 3 + k] = vM.m[i * 3 + k] * G.s[k];
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+        v_s[k] = G.Rq.m[0 * 3 + k] * vM.m[0 * 3 + k] +
+                 G.Rq.m[1 * 3 + k] * vM.m[1 * 3 + k] +
+                 G.Rq.m[2 * 3 + k] * vM.m[2 * 3 + k];
+    // rotation-matrix VJP w.r.t. the normalised quaternion (w, x, y, z)
+    const float n2 = G.q[0] * G.q[0] + G.q[1] * G.q[1] + G.q[2] * G.q[2] +
+                     G.q[3] * G.q[3];
+    const float inv = 1.f / sqrtf(n2);
+    const float w = G.q[0] * inv, x = G.q[1] * inv, y = G.q[2] * inv,
+                z = G.q[3] * inv;
+    const float *m = g.m;  // m[r*3+c] = dL/dR[r][c]
+    const float dw = 2.f * (x * (m[7] - m[5]) + y * (m[2] - m[6]) +
+                            z * (m[3] - m[1]));
+    const float dx = 2.f * (-2.f * x * (m[4] + m[8]) + y * (m[1] + m[3]) +
+                            z * (m[2] + m[6]) + w * (m[7] - m[5]));
+    const float dy = 2.f * (x * (m[1] + m[3]) - 2.f * y * (m[0] + m[8]) +
+                            z * (m[5] + m[7]) + w * (m[2] - m[6]));
+    const float dz = 2.f * (x * (m[2] + m[6]) + y * (m[5] + m[7]) -
+                            2.f * z * (m[0] + m[4]) + w * (m[3] - m[1]));
+    const float dot = dw * w + dx * x + dy * y + dz * z;
+    v_q[0] = (dw - dot * w) * inv;
+    v_q[1] = (dx - dot * x) * inv;
+    v_q[2] = (dy - dot * y) * inv;
+    v_q[3] = (dz - dot * z) * inv;
+}
+
+struct BwdArgs {
+    int64_t B, C, N;
+    const float *means, *covars, *quats, *scales, *viewmats, *Ks;
+    float W, H, eps2d;
+    int camera_model;
+    const float *conics, *compensations;
+    const float *v_means2d, *v_depths, *v_conics, *v_compensations;
+    float *v_means, *v_covars, *v_quats, *v_scales, *v_viewmats;
+};
+
+// Reduce v_R (9) and v_t (3) of the workgroup and add them to the camera's
+// viewmat gradient.  Must be reached by every thread of the block.
+__device__ __forceinline__ void flush_viewmat_grad(float *v_viewmat,
+                                                   const M3 &v_R,
+                                                   const float v_t[3],
+                                                   float *s_red) {
+    const uint32_t wave = threadIdx.x / kWave;
+    float vals[12];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+            vals[i * 4 + j] = v_R.m[i * 3 + j];
+        vals[i * 4 + 3] = v_t[i];
+    }
+#pragma unroll
+    for (int k = 0; k < 12; ++k) {
+        const float s = wave_sum(vals[k]);
+        if (lane_id() == 0)
+            s_red[wave * 12 + k] = s;
+    }
+    __syncthreads();
+    if (threadIdx.x < 12) {
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < kProjThreads / kWave; ++w)
+            acc += s_red[w * 12 + threadIdx.x];
+        atomic_add_f32(v_viewmat + threadIdx.x, acc);
+    }
+    __syncthreads();
+}
+
+__global__ void __launch_bounds__(kProjThreads)
+    projection_fused_bwd_kernel(const BwdArgs a, const int32_t *__restrict__ radii) {
+    __shared__ float s_red[(kProjThreads / kWave) * 12];
+    // one thread per (b, g); loops over the C cameras
+    const int64_t bg = (int64_t)blockIdx.x * kProjThreads + threadIdx.x;
+    const bool in_range = bg < a.B * a.N;
+    const int64_t b = in_range ? bg / a.N : 0;
+    const int64_t g = in_range ? bg % a.N : 0;
+
+    GaussGeom G;
+    if (in_range)
+        load_geom(a.covars ? a.covars + bg * 6 : nullptr,
+                  a.quats ? a.quats + bg * 4 : nullptr,
+                  a.scales ? a.scales + bg * 3 : nullptr, G);
+    float v_mean[3] = {0.f, 0.f, 0.f};
+    M3 v_S;
+#pragma unroll
+    for (int i = 0; i < 9; ++i)
+        v_S.m[i] = 0.f;
+    const bool want_cam = a.v_viewmats != nullptr;
+
+    // b is not uniform across the block when N is small; the camera loop is
+    // over C for every thread, and the viewmat flush is done per (b, c) by
+    // the threads that share that b (per-lane atomics when mixed).
+    for (int64_t c = 0; c < a.C; ++c) {
+        M3 v_R;
+        float v_t[3] = {0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 9; ++i)
+            v_R.m[i] = 0.f;
+        bool active = false;
+        int64_t bc = b * a.C + c;
+        if (in_range) {
+            const int64_t row = bc * a.N + g;
+            const int2 r = reinterpret_cast<const int2 *>(radii)[row];
+            if (r.x > 0 && r.y > 0) {
+                active = true;
+                Cam cam;
+                load_cam(a.viewmats + bc * 16, a.Ks + bc * 9, cam);
+                const bool has_comp = a.v_compensations != nullptr;
+                project_row_vjp(
+                    cam, a.means + bg * 3, G, a.camera_model, a.W, a.H, a.eps2d,
+                    a.conics + row * 3, has_comp,
+                    has_comp ? a.compensations[row] : 0.f,
+                    has_comp ? a.v_compensations[row] : 0.f,
+                    a.v_means2d[row * 2], a.v_means2d[row * 2 + 1],
+                    a.v_depths[row], a.v_conics + row * 3, v_mean, v_S,
+                    want_cam, v_R, v_t);
+            }
+        }
+        if (want_cam) {
+            // b is uniform over the block unless the block straddles two
+            // batches (only when N is not a multiple of the block size).
+            const int64_t first = (int64_t)blockIdx.x * kProjThreads;
+            const int64_t last_row = first + kProjThreads - 1 < a.B * a.N - 1
+                                         ? first + kProjThreads - 1
+                                         : a.B * a.N - 1;
+            const int64_t b0 = first / a.N;
+            if (b0 == last_row / a.N) {
+                flush_viewmat_grad(a.v_viewmats + (b0 * a.C + c) * 16, v_R,
+                                   v_t, s_red);
+            } else if (active) {
+                float *dst = a.v_viewmats + bc * 16;
+#pragma unroll
+                for (int i = 0; i < 3; ++i) {
+#pragma unroll
+                    for (int j = 0; j < 3; ++j)
+                        atomic_add_f32(dst + i * 4 + j, v_R.m[i * 3 + j]);
+                    atomic_add_f32(dst + i * 4 + 3, v_t[i]);
+                }
+            }
+        }
+    }
+    if (!in_range)
+        return;
+    a.v_means[bg * 3 + 0] = v_mean[0];
+    a.v_means[bg * 3 + 1] = v_mean[1];
+    a.v_means[bg * 3 + 2] = v_mean[2];
+    if (a.covars != nullptr) {
+        if (a.v_covars != nullptr) {
+            float *d = a.v_covars + bg * 6;
+            d[0] = v_S.m[0];
+            d[1] = v_S.m[1] + v_S.m[3];
+            d[2] = v_S.m[2] + v_S.m[6];
+            d[3] = v_S.m[4];
+            d[4] = v_S.m[5] + v_S.m[7];
+            d[5] = v_S.m[8];
+        }
+    } else {
+        float v_q[4], v_s[3];
+        covar_vjp_to_quat_scale(G, v_S, v_q, v_s);
+        if (a.v_quats != nullptr)
+            reinterpret_cast<float4 *>(a.v_quats)[bg] =
+                make_float4(v_q[0], v_q[1], v_q[2], v_q[3]);
+        if (a.v_scales != nullptr) {
+            a.v_scales[bg * 3 + 0] = v_s[0];
+            a.v_scales[bg * 3 + 1] = v_s[1];
+            a.v_scales[bg * 3 + 2] = v_s[2];
+        }
+    }
+}
+
+__global__ void __launch_bounds__(kProjThreads) projection_packed_bwd_kernel(
+    const BwdArgs a, int64_t nnz, const int64_t *__restrict__ batch_ids,
+    const int64_t *__restrict__ camera_ids,
+    const int64_t *__restrict__ gaussian_ids, int sparse_grad,
+    int single_image) {
+    __shared__ float s_red[(kProjThreads / kWave) * 12];
+    const int64_t i = (int64_t)blockIdx.x * kProjThreads + threadIdx.x;
+    const bool active = i < nnz;
+    const bool want_cam = a.v_viewmats != nullptr;
+    float v_mean[3] = {0.f, 0.f, 0.f};
+    M3 v_S, v_R;
+    float v_t[3] = {0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+        v_S.m[k] = 0.f;
+        v_R.m[k] = 0.f;
+    }
+    int64_t b = 0, c = 0, g = 0;
+    GaussGeom G;
+    if (active) {
+        b = batch_ids[i];
+        c = camera_ids[i];
+        g = gaussian_ids[i];
+        const int64_t bg = b * a.N + g;
+        const int64_t bc = b * a.C + c;
+        load_geom(a.covars ? a.covars + bg * 6 : nullptr,
+                  a.quats ? a.quats + bg * 4 : nullptr,
+                  a.scales ? a.scales + bg * 3 : nullptr, G);
+        Cam cam;
+        load_cam(a.viewmats + bc * 16, a.Ks + bc * 9, cam);
+        const bool has_comp = a.v_compensations != nullptr;
+        project_row_vjp(cam, a.means + bg * 3, G, a.camera_model, a.W, a.H,
+                        a.eps2d, a.conics + i * 3, has_comp,
+                        has_comp ? a.compensations[i] : 0.f,
+                        has_comp ? a.v_compensations[i] : 0.f,
+                        a.v_means2d[i * 2], a.v_means2d[i * 2 + 1],
+                        a.v_depths[i], a.v_conics + i * 3, v_mean, v_S,
+                        want_cam, v_R, v_t);
+    }
+    if (want_cam) {
+        // rows are sorted by (b, c): the block usually sees one camera
+        const int64_t bc = b * a.C + c;
+        const int64_t first = (int64_t)blockIdx.x * kProjThreads;
+        const int64_t bc0 = batch_ids[first] * a.C + camera_ids[first];
+        const bool uniform = __syncthreads_and(!active || bc == bc0);
+        if (uniform) {
+            flush_viewmat_grad(a.v_viewmats + bc0 * 16, v_R, v_t, s_red);
+        } else if (active) {
+            float *dst = a.v_viewmats + bc * 16;
+#pragma unroll
+            for (int r = 0; r < 3; ++r) {
+#pragma unroll
+                for (int k = 0; k < 3; ++k)
+                    atomic_add_f32(dst + r * 4 + k, v_R.m[r * 3 + k]);
+                atomic_add_f32(dst + r * 4 + 3, v_t[r]);
+            }
+        }
+    }
+    if (!active)
+        return;
+    float v_q[4] = {0.f, 0.f, 0.f, 0.f}, v_s[3] = {0.f, 0.f, 0.f};
+    float v_c6[6];
+    if (a.covars != nullptr) {
+        v_c6[0] = v_S.m[0];
+        v_c6[1] = v_S.m[1] + v_S.m[3];
+        v_c6[2] = v_S.m[2] + v_S.m[6];
+        v_c6[3] = v_S.m[4];
+        v_c6[4] = v_S.m[5] + v_S.m[7];
+        v_c6[5] = v_S.m[8];
+    } else {
+        covar_vjp_to_quat_scale(G, v_S, v_q, v_s);
+    }
+    const bool direct = sparse_grad || single_image;
+    const int64_t dst = sparse_grad ? i : b * a.N + g;
+    if (direct) {
+        if (a.v_means) {
+            a.v_means[dst * 3 + 0] = v_mean[0];
+            a.v_means[dst * 3 + 1] = v_mean[1];
+            a.v_means[dst * 3 + 2] = v_mean[2];
+        }
+        if (a.covars != nullptr) {
+            if (a.v_covars)
+                for (int k = 0; k < 6; ++k)
+                    a.v_covars[dst * 6 + k] = v_c6[k];
+        } else {
+            if (a.v_quats)
+                reinterpret_cast<float4 *>(a.v_quats)[dst] =
+                    make_float4(v_q[0], v_q[1], v_q[2], v_q[3]);
+            if (a.v_scales)
+                for (int k = 0; k < 3; ++k)
+                    a.v_scales[dst * 3 + k] = v_s[k];
+        }
+    } else {
+        if (a.v_means)
+            for (int k = 0; k < 3; ++k)
+                atomic_add_f32(a.v_means + dst * 3 + k, v_mean[k]);
+        if (a.covars != nullptr) {
+            if (a.v_covars)
+                for (int k = 0; k < 6; ++k)
+                    atomic_add_f32(a.v_covars + dst * 6 + k, v_c6[k]);
+        } else {
+            if (a.v_quats)
+                for (int k = 0; k < 4; ++k)
+                    atomic_add_f32(a.v_quats + dst * 4 + k, v_q[k]);
+            if (a.v_scales)
+                for (int k = 0; k < 3; ++k)
+                    atomic_add_f32(a.v_scales + dst * 3 + k, v_s[k]);
+        }
+    }
+}
+
+int check_common(int64_t B, int64_t C, int64_t N, const float *means,
+                 const float *covars, const float *quats, const float *scales,
+                 const float *viewmats, const float *Ks, int32_t W, int32_t H,
+                 int32_t camera_model) {
+    GS_REQUIRE(B >= 0 && C >= 0 && N >= 0, "projection: negative size");
+    GS_REQUIRE(camera_model == GSPLAT_CAMERA_PINHOLE ||
+                   camera_model == GSPLAT_CAMERA_ORTHO,
+               "projection: only the pinhole and ortho camera models are "
+               "implemented");
+    GS_REQUIRE(W > 0 && H > 0, "projection: image size must be positive");
+    if (B * C * N > 0) {
+        GS_REQUIRE(means && viewmats && Ks, "projection: NULL input");
+        GS_REQUIRE(covars != nullptr || (quats != nullptr && scales != nullptr),
+                   "projection: covars or (quats, scales) required");
+    }
+    return GSPLAT_OK;
+}
+
+}  // namespace
+}  // namespace gs
+
+using namespace gs;
+
+extern "C" int gsplat_projection_fused_fwd(
+    int64_t B, int64_t C, int64_t N, const float *means, const float *covars,
+    const float *quats, const float *scales, const float *opacities,
+    const float *viewmats, const float *Ks, int32_t image_width,
+    int32_t image_height, float eps2d, float near_plane, float far_plane,
+    float radius_clip, int32_t camera_model, int32_t *radii, float *means2d,
+    float *depths, float *conics, float *compensations,
+    gsplat_stream_t stream) {
+    clear_error();
+    GS_TRY(check_common(B, C, N, means, covars, quats, scales, viewmats, Ks,
+                        image_width, image_height, camera_model));
+    const int64_t rows = B * C * N;
+    if (rows == 0)
+        return GSPLAT_OK;
+    GS_REQUIRE(radii && means2d && depths && conics, "projection: NULL output");
+    FwdArgs a{B, C, N, means, covars, quats, scales, opacities, viewmats, Ks,
+              (float)image_width, (float)image_height, eps2d, near_plane,
+              far_plane, radius_clip, camera_model, compensations != nullptr};
+    projection_fused_fwd_kernel<<<(unsigned)ceil_div(rows, kProjThreads),
+                                  kProjThreads, 0, as_stream(stream)>>>(
+        a, radii, means2d, depths, conics, compensations);
+    return check_launch("projection_fused_fwd_kernel");
+}
+
+extern "C" size_t gsplat_projection_packed_workspace_size(int64_t B, int64_t C,
+                                                          int64_t N) {
+    return lookback_bytes(ceil_div(B * C * N, kProjThreads));
+}
+
+extern "C" int gsplat_projection_packed_fwd(
+    int64_t B, int64_t C, int64_t N, const float *means, const float *covars,
+    const float *quats, const float *scales, const float *opacities,
+    const float *viewmats, const float *Ks, int32_t image_width,
+    int32_t image_height, float eps2d, float near_plane, float far_plane,
+    float radius_clip, int32_t camera_model, void *workspace,
+    size_t workspace_bytes, int32_t *indptr, int64_t *batch_ids,
+    int64_t *camera_ids, int64_t *gaussian_ids, int32_t *radii,
+    float *means2d, float *depths, float *conics, float *compensations,
+    int64_t *nnz_out, gsplat_stream_t stream) {
+    clear_error();
+    GS_TRY(check_common(B, C, N, means, covars, quats, scales, viewmats, Ks,
+                        image_width, image_height, camera_model));
+    const int64_t rows = B * C * N;
+    GS_REQUIRE(indptr && nnz_out, "projection_packed: NULL indptr/nnz_out");
+    if (rows == 0)
+        return fail(GSPLAT_ERR_INVALID_ARGUMENT,
+                    "projection_packed: zero rows must be handled by the caller");
+    GS_REQUIRE(batch_ids && camera_ids && gaussian_ids && radii && means2d &&
+                   depths && conics,
+               "projection_packed: NULL output");
+    GS_REQUIRE(rows < (1ll << 31), "projection_packed: more than 2^31 rows");
+    const int64_t blocks = ceil_div(rows, kProjThreads);
+    GS_REQUIRE(workspace != nullptr && workspace_bytes >= lookback_bytes(blocks),
+               "projection_packed: workspace too small");
+    hipStream_t st = as_stream(stream);
+    GS_TRY(clear_lookback(workspace, blocks, st));
+    FwdArgs a{B, C, N, means, covars, quats, scales, opacities, viewmats, Ks,
+              (float)image_width, (float)image_height, eps2d, near_plane,
+              far_plane, radius_clip, camera_model, compensations != nullptr};
+    projection_packed_fwd_kernel<<<(unsigned)blocks, kProjThreads, 0, st>>>(
+        a, lookback_from(workspace), indptr, batch_ids, camera_ids,
+        gaussian_ids, radii, means2d, depths, conics, compensations, nnz_out);
+    return check_launch("projection_packed_fwd_kernel");
+}
+
+extern "C" int gsplat_projection_fused_bwd(
+    int64_t B, int64_t C, int64_t N, const float *means, const float *covars,
+    const float *quats, const float *scales, const float *viewmats,
+    const float *Ks, int32_t image_width, int32_t image_height, float eps2d,
+    int32_t camera_model, const int32_t *radii, const float *conics,
+    const float *compensations, const float *v_means2d, const float *v_depths,
+    const float *v_conics, const float *v_compensations, float *v_means,
+    float *v_covars, float *v_quats, float *v_scales, float *v_viewmats,
+    gsplat_stream_t stream) {
+    clear_error();
+    GS_TRY(check_common(B, C, N, means, covars, quats, scales, viewmats, Ks,
+                        image_width, image_height, camera_model));
+    if (B * N == 0)
+        return GSPLAT_OK;
+    GS_REQUIRE(radii && conics && v_means2d && v_depths && v_conics && v_means,
+               "projection_fused_bwd: NULL buffer");
+    GS_REQUIRE(v_compensations == nullptr || compensations != nullptr,
+               "projection_fused_bwd: v_compensations needs compensations");
+    if (covars == nullptr)
+        GS_REQUIRE(v_quats && v_scales,
+                   "projection_fused_bwd: v_quats/v_scales required");
+    BwdArgs a{B, C, N, means, covars, quats, scales, viewmats, Ks,
+              (float)image_width, (float)image_height, eps2d, camera_model,
+              conics, compensations, v_means2d, v_depths, v_conics,
+              v_compensations, v_means, v_covars, v_quats, v_scales,
+              v_viewmats};
+    projection_fused_bwd_kernel<<<(unsigned)ceil_div(B * N, kProjThreads),
+                                  kProjThreads, 0, as_stream(stream)>>>(a,
+                                                                        radii);
+    return check_launch("projection_fused_bwd_kernel");
+}
+
+extern "C" int gsplat_projection_packed_bwd(
+    int64_t B, int64_t C, int64_t N, int64_t nnz, const float *means,
+    const float *covars, const float *quats, const float *scales,
+    const float *viewmats, const float *Ks, int32_t image_width,
+    int32_t image_height, float eps2d, int32_t camera_model,
+    const int64_t *batch_ids, const int64_t *camera_ids,
+    const int64_t *gaussian_ids, const float *conics,
+    const float *compensations, const float *v_means2d, const float *v_depths,
+    const float *v_conics, const float *v_compensations, int32_t sparse_grad,
+    float *v_means, float *v_covars, float *v_quats, float *v_scales,
+    float *v_viewmats, gsplat_stream_t stream) {
+    clear_error();
+    GS_TRY(check_common(B, C, N, means, covars, quats, scales, viewmats, Ks,
+                        image_width, image_height, camera_model));
+    GS_REQUIRE(nnz >= 0, "projection_packed_bwd: negative nnz");
+    if (nnz == 0)
+        return GSPLAT_OK;
+    GS_REQUIRE(batch_ids && camera_ids && gaussian_ids && conics && v_means2d &&
+                   v_depths && v_conics,
+               "projection_packed_bwd: NULL buffer");
+    GS_REQUIRE(v_compensations == nullptr || compensations != nullptr,
+               "projection_packed_bwd: v_compensations needs compensations");
+    BwdArgs a{B, C, N, means, covars, quats, scales, viewmats, Ks,
+              (float)image_width, (float)image_height, eps2d, camera_model,
+              conics, compensations, v_means2d, v_depths, v_conics,
+              v_compensations, v_means, v_covars, v_quats, v_scales,
+              v_viewmats};
+    projection_packed_bwd_kernel<<<(unsigned)ceil_div(nnz, kProjThreads),
+                                   kProjThreads, 0, as_stream(stream)>>>(
+        a, nnz, batch_ids, camera_ids, gaussian_ids, sparse_grad,
+        (B * C == 1) ? 1 : 0);
+    return check_launch("projection_packed_bwd_kernel");
+}

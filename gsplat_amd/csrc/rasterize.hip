@@ -1,0 +1,473 @@
+// Tile rasterizer: front-to-back alpha compositing (forward) and its
+// back-to-front replay (backward).
+//
+// Semantics: gsplat/cuda/csrc/RasterizeToPixels3DGSFwd.cu:41-213 and
+// RasterizeToPixels3DGSBwd.cu:39-301.  Per pixel (px, py) = (j + .5, i + .5),
+// for the depth-sorted Gaussians of its tile:
+//   sigma = 0.5 (a dx^2 + c dy^2) + b dx dy,  dx = mean.x - px, dy = mean.y - py
+//   alpha = min(0.99, o exp(-sigma)); skipped if sigma < 0 or alpha < 1/255
+//   stop (exclusive) once T (1 - alpha) <= 1e-4;  C += c alpha T;  T *= 1 - alpha
+//   colors = C + T bg, alphas = 1 - T, last_ids = isect index of the last
+//   Gaussian composited (0 if none).
+//
+// The two discontinuous decisions that depend on exp() are taken on sigma
+// against per-Gaussian thresholds computed once per tile load:
+//   alpha < 1/255     <=>  sigma > ln(o / (1/255))          ("sig_max")
+//   o exp(-sigma) > .99 <=> sigma < ln(o / 0.99)            ("sig_clamp")
+// sigma is evaluated in a fixed IEEE order without contraction and the logs
+// are portable_logf, so the set of composited Gaussians is reproducible bit
+// for bit by the host oracle; exp() itself uses the hardware v_exp_f32.
+//
+// MI355X design: one workgroup per tile (tile_size^2 threads = 4 waves at
+// 16x16, each wave a 16x4 pixel strip), Gaussians staged in LDS in batches of
+// one per thread (float4 geometry, float4 thresholds+conic, CDIM colours).
+// The forward ends a batch early when every pixel of the wave is done (the
+// per-lane loop exits when the wave's exec mask empties) and skips remaining
+// batches once the whole tile is done (__syncthreads_count).
+// The backward reduces each Gaussian's gradient over the wave with DPP row
+// operations, accumulates the 4 waves in LDS (native ds_add_f32) and issues
+// one global atomic per value per Gaussian per TILE, 8x fewer than one per
+// 32-lane warp.
+#include "common.h"
+
+namespace gs {
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct RasterArgs {
+    int64_t I, n_rows, n_isects;
+    const float *means2d, *conics, *colors, *opacities, *backgrounds;
+    const uint8_t *masks;
+    int32_t W, H, tile_size, tile_width, tile_height;
+    const int32_t *tile_offsets, *flatten_ids;
+};
+
+// exact (uncontracted) Mahalanobis term; the host oracle uses this order
+__device__ __forceinline__ float gauss_sigma(float a, float b, float c,
+                                             float dx, float dy) {
+#pragma clang fp contract(off)
+    return 0.5f * ((a * dx) * dx + (c * dy) * dy) + (b * dx) * dy;
+}
+
+// per-Gaussian decision thresholds (see file comment)
+__device__ __forceinline__ void alpha_thresholds(float o, float &sig_max,
+                                                 float &sig_clamp) {
+    if (o > 0.f) {
+        sig_max = portable_logf(o / kAlphaThreshold);
+        sig_clamp = portable_logf(o / kMaxAlpha);
+    } else {
+        sig_max = -__builtin_inff();  // zero or NaN opacity never composites
+        sig_clamp = -__builtin_inff();
+    }
+}
+
+__device__ __forceinline__ void tile_coords(const RasterArgs &a, int64_t &image,
+                                            int32_t &tile, int32_t &ty,
+                                            int32_t &tx) {
+    const int64_t n_tiles = (int64_t)a.tile_width * a.tile_height;
+    const int64_t gid = blockIdx.x;
+    image = gid / n_tiles;
+    tile = (int32_t)(gid - image * n_tiles);
+    ty = tile / a.tile_width;
+    tx = tile - ty * a.tile_width;
+}
+
+constexpr int kMaxTileThreads = 256;
+
+template <int CDIM>
+__global__ void __launch_bounds__(kMaxTileThreads) rasterize_fwd_kernel(const RasterArgs a,
+                                     float *__restrict__ render_colors,
+                                     float *__restrict__ render_alphas,
+                                     int32_t *__restrict__ last_ids) {
+    extern __shared__ float4 s_mem[];
+    const int bs = blockDim.x;  // tile_size^2
+    float4 *s_geo = s_mem;              // (x, y, opacity, sig_max)
+    float4 *s_con = s_mem + bs;         // (a, b, c, sig_clamp)
+    float *s_col = reinterpret_cast<float *>(s_mem + 2 * bs);  // [bs][CDIM]
+
+    int64_t image;
+    int32_t tile, ty, tx;
+    tile_coords(a, image, tile, ty, tx);
+    const int tr = threadIdx.x;
+    const int i = ty * a.tile_size + tr / a.tile_size;
+    const int j = tx * a.tile_size + tr % a.tile_size;
+    const bool inside = i < a.H && j < a.W;
+    const int64_t pix = ((int64_t)image * a.H + i) * a.W + j;
+    const float px = (float)j + 0.5f, py = (float)i + 0.5f;
+    const int64_t n_tiles = (int64_t)a.tile_width * a.tile_height;
+
+    if (a.masks != nullptr && !a.masks[image * n_tiles + tile]) {
+        if (inside) {
+#pragma unroll
+            for (int k = 0; k < CDIM; ++k)
+                render_colors[pix * CDIM + k] =
+                    a.backgrounds ? a.backgrounds[image * CDIM + k] : 0.f;
+            render_alphas[pix] = 0.f;
+            last_ids[pix] = 0;
+        }
+        return;
+    }
+
+    const int32_t *offs = a.tile_offsets + image * n_tiles;
+    const int32_t range_start = offs[tile];
+    const int32_t range_end = (image == a.I - 1 && tile == n_tiles - 1)
+                                  ? (int32_t)a.n_isects
+                                  : offs[tile + 1];
+    const int num_batches = (range_end - range_start + bs - 1) / bs;
+
+    float T = 1.f;
+    int32_t cur_idx = 0;
+    bool done = !inside;
+    float acc[CDIM];
+#pragma unroll
+    for (int k = 0; k < CDIM; ++k)
+        acc[k] = 0.f;
+
+    for (int b = 0; b < num_batches; ++b) {
+        if (__syncthreads_count(done) >= bs)
+            break;
+        const int32_t batch_start = range_start + b * bs;
+        const int32_t idx = batch_start + tr;
+        if (idx < range_end) {
+            const int32_t g = a.flatten_ids[idx];
+            const float2 xy = reinterpret_cast<const float2 *>(a.means2d)[g];
+            const float o = a.opacities[g];
+            float sig_max, sig_clamp;
+            alpha_thresholds(o, sig_max, sig_clamp);
+            s_geo[tr] = make_float4(xy.x, xy.y, o, sig_max);
+            s_con[tr] = make_float4(a.conics[g * 3 + 0], a.conics[g * 3 + 1],
+                                    a.conics[g * 3 + 2], sig_clamp);
+#pragma unroll
+            for (int k = 0; k < CDIM; ++k)
+                s_col[tr * CDIM + k] = a.colors[(int64_t)g * CDIM + k];
+        }
+        __syncthreads();
+        const int batch_size = min(bs, range_end - batch_start);
+        for (int t = 0; t < batch_size && !done; ++t) {
+            const float4 geo = s_geo[t];
+            const float4 con = s_con[t];
+            const float dx = geo.x - px, dy = geo.y - py;
+            const float sigma = gauss_sigma(con.x, con.y, con.z, dx, dy);
+            if (sigma < 0.f || sigma > geo.w)
+                continue;
+            const float vis = __builtin_amdgcn_exp2f(-sigma * kLog2e);
+            const float alpha = sigma < con.w ? kMaxAlpha : geo.z * vis;
+            const float next_T = T * (1.f - alpha);
+            if (next_T <= kTransmittanceThreshold) {
+                done = true;
+                break;
+            }
+            const float w = alpha * T;
+#pragma unroll
+            for (int k = 0; k < CDIM; ++k)
+                acc[k] += s_col[t * CDIM + k] * w;
+            cur_idx = batch_start + t;
+            T = next_T;
+        }
+    }
+    if (inside) {
+        render_alphas[pix] = 1.f - T;
+#pragma unroll
+        for (int k = 0; k < CDIM; ++k)
+            render_colors[pix * CDIM + k] =
+                a.backgrounds ? acc[k] + T * a.backgrounds[image * CDIM + k]
+                              : acc[k];
+        last_ids[pix] = cur_idx;
+    }
+}
+
+template <int CDIM> struct BwdAcc {
+    // per-Gaussian accumulated values: xy(2), conic(3), colour(CDIM),
+    // opacity(1), |xy|(2)
+    static constexpr int N = 2 + 3 + CDIM + 1 + 2;
+};
+
+template <int CDIM>
+__global__ void __launch_bounds__(kMaxTileThreads) rasterize_bwd_kernel(const RasterArgs a,
+                                     const float *__restrict__ render_alphas,
+                                     const int32_t *__restrict__ last_ids,
+                                     const float *__restrict__ v_render_colors,
+                                     const float *__restrict__ v_render_alphas,
+                                     float *__restrict__ v_means2d_abs,
+                                     float *__restrict__ v_means2d,
+                                     float *__restrict__ v_conics,
+                                     float *__restrict__ v_colors,
+                                     float *__restrict__ v_opacities) {
+    constexpr int NACC = BwdAcc<CDIM>::N;
+    extern __shared__ float4 s_mem[];
+    const int bs = blockDim.x;
+    float4 *s_geo = s_mem;
+    float4 *s_con = s_mem + bs;
+    float *s_col = reinterpret_cast<float *>(s_mem + 2 * bs);  // [bs][CDIM]
+    float *s_acc = s_col + bs * CDIM;                          // [NACC][bs]
+    int32_t *s_gid = reinterpret_cast<int32_t *>(s_acc + NACC * bs);
+    int32_t *s_hit = s_gid + bs;
+
+    int64_t image;
+    int32_t tile, ty, tx;
+    tile_coords(a, image, tile, ty, tx);
+    const int64_t n_tiles = (int64_t)a.tile_width * a.tile_height;
+    if (a.masks != nullptr && !a.masks[image * n_tiles + tile])
+        return;
+    const int tr = threadIdx.x;
+    const int i = ty * a.tile_size + tr / a.tile_size;
+    const int j = tx * a.tile_size + tr % a.tile_size;
+    const bool inside = i < a.H && j < a.W;
+    const int64_t pix = ((int64_t)image * a.H + (inside ? i : 0)) * a.W +
+                        (inside ? j : 0);
+    const float px = (float)j + 0.5f, py = (float)i + 0.5f;
+
+    const int32_t *offs = a.tile_offsets + image * n_tiles;
+    const int32_t range_start = offs[tile];
+    const int32_t range_end = (image == a.I - 1 && tile == n_tiles - 1)
+                                  ? (int32_t)a.n_isects
+                                  : offs[tile + 1];
+    const int num_batches = (range_end - range_start + bs - 1) / bs;
+
+    const float T_final = inside ? 1.f - render_alphas[pix] : 1.f;
+    float T = T_final;
+    const int32_t bin_final = inside ? last_ids[pix] : -1;
+    float v_c[CDIM], buffer[CDIM];
+    float bg_dot = 0.f;
+#pragma unroll
+    for (int k = 0; k < CDIM; ++k) {
+        v_c[k] = inside ? v_render_colors[pix * CDIM + k] : 0.f;
+        buffer[k] = 0.f;
+        if (a.backgrounds)
+            bg_dot += a.backgrounds[image * CDIM + k] * v_c[k];
+    }
+    const float v_a = inside ? v_render_alphas[pix] : 0.f;
+    const int32_t wave_bin_final = wave_max_i32(bin_final);
+    const bool want_abs = v_means2d_abs != nullptr;
+
+    for (int b = 0; b < num_batches; ++b) {
+        __syncthreads();
+        const int32_t batch_end = range_end - 1 - b * bs;
+        const int batch_size = min(bs, batch_end + 1 - range_start);
+        const int32_t idx = batch_end - tr;
+        if (idx >= range_start) {
+            const int32_t g = a.flatten_ids[idx];
+            s_gid[tr] = g;
+            const float2 xy = reinterpret_cast<const float2 *>(a.means2d)[g];
+            const float o = a.opacities[g];
+            float sig_max, sig_clamp;
+            alpha_thresholds(o, sig_max, sig_clamp);
+            s_geo[tr] = make_float4(xy.x, xy.y, o, sig_max);
+            s_con[tr] = make_float4(a.conics[g * 3 + 0], a.conics[g * 3 + 1],
+                                    a.conics[g * 3 + 2], sig_clamp);
+#pragma unroll
+            for (int k = 0; k < CDIM; ++k)
+                s_col[tr * CDIM + k] = a.colors[(int64_t)g * CDIM + k];
+        }
+        s_hit[tr] = 0;
+#pragma unroll
+        for (int k = 0; k < NACC; ++k)
+            s_acc[k * bs + tr] = 0.f;
+        __syncthreads();
+
+        // slots t with isect index batch_end - t > wave_bin_final are behind
+        // every pixel of this wave
+        const int t0 = max(0, batch_end - wave_bin_final);
+        for (int t = t0; t < batch_size; ++t) {
+            const int32_t isect = batch_end - t;
+            bool valid = inside && isect <= bin_final;
+            const float4 geo = s_geo[t];
+            const float4 con = s_con[t];
+            const float dx = geo.x - px, dy = geo.y - py;
+            float sigma = 0.f, vis = 0.f, alpha = 0.f;
+            if (valid) {
+                sigma = gauss_sigma(con.x, con.y, con.z, dx, dy);
+                if (sigma < 0.f || sigma > geo.w)
+                    valid = false;
+            }
+            if (!__ballot(valid))
+                continue;
+            float g_acc[NACC];
+#pragma unroll
+            for (int k = 0; k < NACC; ++k)
+                g_acc[k] = 0.f;
+            if (valid) {
+                vis = __builtin_amdgcn_exp2f(-sigma * kLog2e);
+                const bool clamped = sigma < con.w;
+                alpha = clamped ? kMaxAlpha : geo.z * vis;
+                const float ra = 1.f / fmaxf(kMinOneMinusAlpha, 1.f - alpha);
+                T *= ra;
+                const float fac = alpha * T;
+                float v_alpha = 0.f;
+#pragma unroll
+                for (int k = 0; k < CDIM; ++k) {
+                    const float ck = s_col[t * CDIM + k];
+                    g_acc[5 + k] = fac * v_c[k];
+                    v_alpha += (ck * T - buffer[k] * ra) * v_c[k];
+                    buffer[k] += ck * fac;
+                }
+                v_alpha += T_final * ra * v_a;
+                if (a.backgrounds)
+                    v_alpha += -T_final * ra * bg_dot;
+                if (!clamped) {
+                    const float v_sigma = -geo.z * vis * v_alpha;
+                    g_acc[2] = 0.5f * v_sigma * dx * dx;
+                    g_acc[3] = v_sigma * dx * dy;
+                    g_acc[4] = 0.5f * v_sigma * dy * dy;
+                    g_acc[0] = v_sigma * (con.x * dx + con.y * dy);
+                    g_acc[1] = v_sigma * (con.y * dx + con.z * dy);
+                    g_acc[5 + CDIM] = vis * v_alpha;
+                    g_acc[6 + CDIM] = fabsf(g_acc[0]);
+                    g_acc[7 + CDIM] = fabsf(g_acc[1]);
+                }
+            }
+            const int nred = want_abs ? NACC : NACC - 2;
+            for (int k = 0; k < nred; ++k) {
+                const float s = wave_sum(g_acc[k]);
+                if (lane_id() == 0)
+                    atomicAdd(&s_acc[k * bs + t], s);
+            }
+            if (lane_id() == 0)
+                s_hit[t] = 1;
+        }
+        __syncthreads();
+        if (tr < batch_size && s_hit[tr]) {
+            const int32_t g = s_gid[tr];
+            atomic_add_f32(v_means2d + (int64_t)g * 2 + 0, s_acc[0 * bs + tr]);
+            atomic_add_f32(v_means2d + (int64_t)g * 2 + 1, s_acc[1 * bs + tr]);
+            atomic_add_f32(v_conics + (int64_t)g * 3 + 0, s_acc[2 * bs + tr]);
+            atomic_add_f32(v_conics + (int64_t)g * 3 + 1, s_acc[3 * bs + tr]);
+            atomic_add_f32(v_conics + (int64_t)g * 3 + 2, s_acc[4 * bs + tr]);
+#pragma unroll
+            for (int k = 0; k < CDIM; ++k)
+                atomic_add_f32(v_colors + (int64_t)g * CDIM + k,
+                               s_acc[(5 + k) * bs + tr]);
+            atomic_add_f32(v_opacities + g, s_acc[(5 + CDIM) * bs + tr]);
+            if (want_abs) {
+                atomic_add_f32(v_means2d_abs + (int64_t)g * 2 + 0,
+                               s_acc[(6 + CDIM) * bs + tr]);
+                atomic_add_f32(v_means2d_abs + (int64_t)g * 2 + 1,
+                               s_acc[(7 + CDIM) * bs + tr]);
+            }
+        }
+    }
+}
+
+size_t fwd_smem(int bs, int cdim) {
+    return (size_t)bs * (2 * sizeof(float4) + cdim * sizeof(float));
+}
+
+size_t bwd_smem(int bs, int cdim) {
+    const int nacc = 2 + 3 + cdim + 1 + 2;
+    return (size_t)bs * (2 * sizeof(float4) + cdim * sizeof(float) +
+                         nacc * sizeof(float) + 2 * sizeof(int32_t));
+}
+
+int check_raster(const RasterArgs &a, int cdim) {
+    GS_REQUIRE(a.I >= 0 && a.n_rows >= 0 && a.n_isects >= 0,
+               "rasterize: negative size");
+    GS_REQUIRE(a.tile_size == 4 || a.tile_size == 8 || a.tile_size == 16,
+               "rasterize: tile_size must be 4, 8 or 16");
+    GS_REQUIRE(a.W > 0 && a.H > 0, "rasterize: image size must be positive");
+    GS_REQUIRE((int64_t)a.tile_width * a.tile_size >= a.W &&
+                   (int64_t)a.tile_height * a.tile_size >= a.H,
+               "rasterize: tile grid does not cover the image");
+    GS_REQUIRE(a.n_isects < (1ll << 31), "rasterize: more than 2^31 isects");
+    GS_REQUIRE(a.tile_offsets != nullptr, "rasterize: NULL tile_offsets");
+    if (a.n_isects > 0)
+        GS_REQUIRE(a.flatten_ids && a.means2d && a.conics && a.colors &&
+                       a.opacities,
+                   "rasterize: NULL Gaussian buffer");
+    switch (cdim) {
+    case 1: case 2: case 3: case 4: case 5: case 8: case 9: case 16: case 17:
+    case 32: case 33:
+        return GSPLAT_OK;
+    default:
+        return fail(GSPLAT_ERR_UNSUPPORTED,
+                    "rasterize: unsupported channel count " +
+                        std::to_string(cdim) +
+                        " (supported: 1,2,3,4,5,8,9,16,17,32,33)");
+    }
+}
+
+#define GS_CDIM_SWITCH(CDIM_VAR, MACRO)                                        \
+    switch (CDIM_VAR) {                                                        \
+    case 1: MACRO(1); break;                                                   \
+    case 2: MACRO(2); break;                                                   \
+    case 3: MACRO(3); break;                                                   \
+    case 4: MACRO(4); break;                                                   \
+    case 5: MACRO(5); break;                                                   \
+    case 8: MACRO(8); break;                                                   \
+    case 9: MACRO(9); break;                                                   \
+    case 16: MACRO(16); break;                                                 \
+    case 17: MACRO(17); break;                                                 \
+    case 32: MACRO(32); break;                                                 \
+    default: MACRO(33); break;                                                 \
+    }
+
+}  // namespace
+}  // namespace gs
+
+using namespace gs;
+
+extern "C" int gsplat_rasterize_fwd(
+    int64_t I, int64_t n_rows, int64_t n_isects, int32_t cdim,
+    const float *means2d, const float *conics, const float *colors,
+    const float *opacities, const float *backgrounds, const uint8_t *masks,
+    int32_t image_width, int32_t image_height, int32_t tile_size,
+    int32_t tile_width, int32_t tile_height, const int32_t *tile_offsets,
+    const int32_t *flatten_ids, float *render_colors, float *render_alphas,
+    int32_t *last_ids, gsplat_stream_t stream) {
+    clear_error();
+    RasterArgs a{I, n_rows, n_isects, means2d, conics, colors, opacities,
+                 backgrounds, masks, image_width, image_height, tile_size,
+                 tile_width, tile_height, tile_offsets, flatten_ids};
+    GS_TRY(check_raster(a, cdim));
+    if (I == 0)
+        return GSPLAT_OK;
+    GS_REQUIRE(render_colors && render_alphas && last_ids,
+               "rasterize_fwd: NULL output");
+    const int bs = tile_size * tile_size;
+    const int64_t blocks = I * (int64_t)tile_width * tile_height;
+    GS_REQUIRE(blocks < (1ll << 31), "rasterize_fwd: too many tiles");
+    hipStream_t st = as_stream(stream);
+    const size_t smem = fwd_smem(bs, cdim);
+#define GS_FWD(C)                                                              \
+    rasterize_fwd_kernel<C><<<(unsigned)blocks, bs, smem, st>>>(               \
+        a, render_colors, render_alphas, last_ids)
+    GS_CDIM_SWITCH(cdim, GS_FWD)
+#undef GS_FWD
+    return check_launch("rasterize_fwd_kernel");
+}
+
+extern "C" int gsplat_rasterize_bwd(
+    int64_t I, int64_t n_rows, int64_t n_isects, int32_t cdim,
+    const float *means2d, const float *conics, const float *colors,
+    const float *opacities, const float *backgrounds, const uint8_t *masks,
+    int32_t image_width, int32_t image_height, int32_t tile_size,
+    int32_t tile_width, int32_t tile_height, const int32_t *tile_offsets,
+    const int32_t *flatten_ids, const float *render_alphas,
+    const int32_t *last_ids, const float *v_render_colors,
+    const float *v_render_alphas, float *v_means2d_abs, float *v_means2d,
+    float *v_conics, float *v_colors, float *v_opacities,
+    gsplat_stream_t stream) {
+    clear_error();
+    RasterArgs a{I, n_rows, n_isects, means2d, conics, colors, opacities,
+                 backgrounds, masks, image_width, image_height, tile_size,
+                 tile_width, tile_height, tile_offsets, flatten_ids};
+    GS_TRY(check_raster(a, cdim));
+    if (I == 0 || n_isects == 0)
+        return GSPLAT_OK;
+    GS_REQUIRE(render_alphas && last_ids && v_render_colors && v_render_alphas,
+               "rasterize_bwd: NULL input");
+    GS_REQUIRE(v_means2d && v_conics && v_colors && v_opacities,
+               "rasterize_bwd: NULL gradient output");
+    const int bs = tile_size * tile_size;
+    const int64_t blocks = I * (int64_t)tile_width * tile_height;
+    GS_REQUIRE(blocks < (1ll << 31), "rasterize_bwd: too many tiles");
+    hipStream_t st = as_stream(stream);
+    const size_t smem = bwd_smem(bs, cdim);
+#define GS_BWD(C)                                                              \
+    rasterize_bwd_kernel<C><<<(unsigned)blocks, bs, smem, st>>>(               \
+        a, render_alphas, last_ids, v_render_colors, v_render_alphas,          \
+        v_means2d_abs, v_means2d, v_conics, v_colors, v_opacities)
+    GS_CDIM_SWITCH(cdim, GS_BWD)
+#undef GS_BWD
+    return check_launch("rasterize_bwd_kernel");
+}

@@ -1,0 +1,405 @@
+// Real spherical-harmonics colour evaluation, forward and backward.
+//
+// Semantics: gsplat/cuda/csrc/SphericalHarmonicsCUDA.cu:37-388 (the Sloan 2013
+// basis up to degree 4, evaluated at the normalised direction) and the launch
+// wrappers :391-552.  colors[c] = sum_k Y_k(dir/|dir|) * coeffs[k][c].
+//
+// MI355X design: the coefficient rows ([M, K, 3], 192 B per row at K = 16)
+// are the HBM stream.  A 256-row workgroup copies its contiguous coefficient
+// span into LDS with 16-byte loads (1 KiB per wave instruction), then every
+// thread evaluates one row -- all three channels -- from LDS.  Rows are padded
+// to an odd LDS pitch so the per-row reads are bank-conflict free.  The
+// backward writes the full [M, K, 3] gradient (zeros above the used degree and
+// for masked rows) through the same LDS tile with 16-byte stores, so the
+// caller needs no zero fill.  One thread per row also makes the direction
+// gradient a plain store instead of the reference's per-channel atomics.
+#include "common.h"
+
+namespace gs {
+namespace {
+
+constexpr int kShThreads = 256;
+
+constexpr float kY0 = 0.2820947917738781f;
+constexpr float kY1 = 0.48860251190292f;
+constexpr float kY2a = 1.092548430592079f;
+constexpr float kY2b = 0.9461746957575601f;
+constexpr float kY2c = 0.3153915652525201f;
+constexpr float kY2d = 0.5462742152960395f;
+constexpr float kY3a = 2.285228997322329f;
+constexpr float kY3b = 0.4570457994644658f;
+constexpr float kY3c = 1.445305721320277f;
+constexpr float kY3d = 1.865881662950577f;
+constexpr float kY3e = 1.119528997770346f;
+constexpr float kY3f = 0.5900435899266435f;
+constexpr float kY4a = 4.683325804901025f;
+constexpr float kY4b = 2.007139630671868f;
+constexpr float kY4c = 3.31161143515146f;
+constexpr float kY4d = 0.47308734787878f;
+constexpr float kY4e = 1.770130769779931f;
+constexpr float kY4f = 1.984313483298443f;
+constexpr float kY4g = 1.006230589874905f;
+constexpr float kY4h = 0.6258357354491763f;
+
+template <int DEG> struct ShShape {
+    static constexpr int NB = (DEG + 1) * (DEG + 1);
+    static constexpr int ROW = NB * 3;
+    static constexpr int PITCH = (ROW % 2 == 0) ? ROW + 1 : ROW;
+};
+
+// Basis values Y[0..NB) at the unit direction (x, y, z).
+template <int DEG>
+__device__ __forceinline__ void sh_basis(float x, float y, float z, float *Y) {
+    Y[0] = kY0;
+    if (DEG < 1)
+        return;
+    Y[1] = -kY1 * y;
+    Y[2] = kY1 * z;
+    Y[3] = -kY1 * x;
+    if (DEG < 2)
+        return;
+    const float z2 = z * z;
+    const float fTmp0B = -kY2a * z;
+    const float fC1 = x * x - y * y;
+    const float fS1 = 2.f * x * y;
+    Y[4] = kY2d * fS1;
+    Y[5] = fTmp0B * y;
+    Y[6] = kY2b * z2 - kY2c;
+    Y[7] = fTmp0B * x;
+    Y[8] = kY2d * fC1;
+    if (DEG < 3)
+        return;
+    const float fTmp0C = -kY3a * z2 + kY3b;
+    const float fTmp1B = kY3c * z;
+    const float fC2 = x * fC1 - y * fS1;
+    const float fS2 = x * fS1 + y * fC1;
+    Y[9] = -kY3f * fS2;
+    Y[10] = fTmp1B * fS1;
+    Y[11] = fTmp0C * y;
+    Y[12] = z * (kY3d * z2 - kY3e);
+    Y[13] = fTmp0C * x;
+    Y[14] = fTmp1B * fC1;
+    Y[15] = -kY3f * fC2;
+    if (DEG < 4)
+        return;
+    const float fTmp0D = z * (-kY4a * z2 + kY4b);
+    const float fTmp1C = kY4c * z2 - kY4d;
+    const float fTmp2B = -kY4e * z;
+    const float fC3 = x * fC2 - y * fS2;
+    const float fS3 = x * fS2 + y * fC2;
+    Y[16] = kY4h * fS3;
+    Y[17] = fTmp2B * fS2;
+    Y[18] = fTmp1C * fS1;
+    Y[19] = fTmp0D * y;
+    Y[20] = kY4f * z * Y[12] - kY4g * Y[6];
+    Y[21] = fTmp0D * x;
+    Y[22] = fTmp1C * fC1;
+    Y[23] = fTmp2B * fC2;
+    Y[24] = kY4h * fC3;
+}
+
+// Gradient of sum_k G[k] * Y_k w.r.t. the unit direction components
+// (treated as independent; the normalisation VJP is applied by the caller).
+template <int DEG>
+__device__ __forceinline__ void sh_basis_grad(float x, float y, float z,
+                                              const float *G, float &gx,
+                                              float &gy, float &gz) {
+    gx = gy = gz = 0.f;
+    if (DEG < 1)
+        return;
+    gx += -kY1 * G[3];
+    gy += -kY1 * G[1];
+    gz += kY1 * G[2];
+    if (DEG < 2)
+        return;
+    const float z2 = z * z;
+    const float fC1 = x * x - y * y;
+    const float fS1 = 2.f * x * y;
+    // Y4 = b*fS1, Y5 = -a z y, Y6 = d z^2 - e, Y7 = -a z x, Y8 = b*fC1
+    gx += kY2d * 2.f * y * G[4] - kY2a * z * G[7] + kY2d * 2.f * x * G[8];
+    gy += kY2d * 2.f * x * G[4] - kY2a * z * G[5] - kY2d * 2.f * y * G[8];
+    gz += -kY2a * y * G[5] + 2.f * kY2b * z * G[6] - kY2a * x * G[7];
+    if (DEG < 3)
+        return;
+    const float fTmp0C = -kY3a * z2 + kY3b;
+    const float fC2 = x * fC1 - y * fS1;
+    const float fS2 = x * fS1 + y * fC1;
+    // d fC2 = (3 fC1, -3 fS1), d fS2 = (3 fS1, 3 fC1)
+    gx += -kY3f * 3.f * fS1 * G[9] + kY3c * z * 2.f * y * G[10] +
+          fTmp0C * G[13] + kY3c * z * 2.f * x * G[14] -
+          kY3f * 3.f * fC1 * G[15];
+    gy += -kY3f * 3.f * fC1 * G[9] + kY3c * z * 2.f * x * G[10] +
+          fTmp0C * G[11] - kY3c * z * 2.f * y * G[14] +
+          kY3f * 3.f * fS1 * G[15];
+    gz += kY3c * fS1 * G[10] - 2.f * kY3a * z * y * G[11] +
+          (3.f * kY3d * z2 - kY3e) * G[12] - 2.f * kY3a * z * x * G[13] +
+          kY3c * fC1 * G[14];
+    if (DEG < 4)
+        return;
+    const float fTmp0D = z * (-kY4a * z2 + kY4b);
+    const float dTmp0D = -3.f * kY4a * z2 + kY4b;
+    const float fTmp1C = kY4c * z2 - kY4d;
+    // d fC3 = (4 fC2, -4 fS2), d fS3 = (4 fS2, 4 fC2)
+    gx += kY4h * 4.f * fS2 * G[16] - kY4e * z * 3.f * fS1 * G[17] +
+          fTmp1C * 2.f * y * G[18] + fTmp0D * G[21] +
+          fTmp1C * 2.f * x * G[22] - kY4e * z * 3.f * fC1 * G[23] +
+          kY4h * 4.f * fC2 * G[24];
+    gy += kY4h * 4.f * fC2 * G[16] - kY4e * z * 3.f * fC1 * G[17] +
+          fTmp1C * 2.f * x * G[18] + fTmp0D * G[19] -
+          fTmp1C * 2.f * y * G[22] + kY4e * z * 3.f * fS1 * G[23] -
+          kY4h * 4.f * fS2 * G[24];
+    gz += -kY4e * fS2 * G[17] + 2.f * kY4c * z * fS1 * G[18] +
+          y * dTmp0D * G[19] +
+          (kY4f * (4.f * kY3d * z2 * z - 2.f * kY3e * z) -
+           kY4g * 2.f * kY2b * z) * G[20] +
+          x * dTmp0D * G[21] + 2.f * kY4c * z * fC1 * G[22] -
+          kY4e * fC2 * G[23];
+}
+
+// Copy the coefficient prefix (NB bands) of rows [r0, r0 + nrows) into LDS
+// with pitch PITCH floats per row.
+template <int DEG>
+__device__ __forceinline__ void stage_coeffs(const float *__restrict__ coeffs,
+                                             int64_t r0, int nrows, int K,
+                                             bool vec_ok, float *s) {
+    using S = ShShape<DEG>;
+    const int total = nrows * S::ROW;
+    if (vec_ok) {
+        // K == NB and the span is 16-byte aligned: 16-byte loads.
+        const float4 *src =
+            reinterpret_cast<const float4 *>(coeffs + r0 * S::ROW);
+        const int nvec = total >> 2;
+        for (int v = threadIdx.x; v < nvec; v += kShThreads) {
+            const float4 q = src[v];
+            const int e = v << 2;
+            const float vals[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int ek = e + k;
+                const int row = ek / S::ROW;
+                s[row * S::PITCH + (ek - row * S::ROW)] = vals[k];
+            }
+        }
+        for (int e = (nvec << 2) + threadIdx.x; e < total; e += kShThreads) {
+            const int row = e / S::ROW;
+            s[row * S::PITCH + (e - row * S::ROW)] = coeffs[r0 * S::ROW + e];
+        }
+    } else {
+        for (int e = threadIdx.x; e < total; e += kShThreads) {
+            const int row = e / S::ROW;
+            const int col = e - row * S::ROW;
+            s[row * S::PITCH + col] = coeffs[(r0 + row) * (int64_t)K * 3 + col];
+        }
+    }
+}
+
+template <int DEG>
+__global__ void __launch_bounds__(kShThreads)
+    sh_fwd_kernel(int64_t M, int K, const float *__restrict__ dirs,
+                  const float *__restrict__ coeffs,
+                  const uint8_t *__restrict__ masks, float *__restrict__ colors,
+                  bool vec_ok) {
+    using S = ShShape<DEG>;
+    __shared__ float s_coef[kShThreads * S::PITCH];
+    const int64_t r0 = (int64_t)blockIdx.x * kShThreads;
+    const int nrows = (int)((M - r0) < kShThreads ? (M - r0) : kShThreads);
+    stage_coeffs<DEG>(coeffs, r0, nrows, K, vec_ok, s_coef);
+    __syncthreads();
+    const int t = threadIdx.x;
+    if (t >= nrows)
+        return;
+    const int64_t row = r0 + t;
+    float out0 = 0.f, out1 = 0.f, out2 = 0.f;
+    if (masks == nullptr || masks[row]) {
+        float Y[S::NB];
+        if (DEG > 0) {
+            const float dx = dirs[row * 3 + 0], dy = dirs[row * 3 + 1],
+                        dz = dirs[row * 3 + 2];
+            const float inorm = 1.f / sqrtf(dx * dx + dy * dy + dz * dz);
+            sh_basis<DEG>(dx * inorm, dy * inorm, dz * inorm, Y);
+        } else {
+            Y[0] = kY0;
+        }
+        const float *c = s_coef + t * S::PITCH;
+#pragma unroll
+        for (int k = 0; k < S::NB; ++k) {
+            out0 += Y[k] * c[k * 3 + 0];
+            out1 += Y[k] * c[k * 3 + 1];
+            out2 += Y[k] * c[k * 3 + 2];
+        }
+    }
+    colors[row * 3 + 0] = out0;
+    colors[row * 3 + 1] = out1;
+    colors[row * 3 + 2] = out2;
+}
+
+template <int DEG>
+__global__ void __launch_bounds__(kShThreads)
+    sh_bwd_kernel(int64_t M, int K, const float *__restrict__ dirs,
+                  const float *__restrict__ coeffs,
+                  const uint8_t *__restrict__ masks,
+                  const float *__restrict__ v_colors,
+                  float *__restrict__ v_coeffs, float *__restrict__ v_dirs,
+                  bool vec_ok) {
+    using S = ShShape<DEG>;
+    __shared__ float s_buf[kShThreads * S::PITCH];
+    const int64_t r0 = (int64_t)blockIdx.x * kShThreads;
+    const int nrows = (int)((M - r0) < kShThreads ? (M - r0) : kShThreads);
+    const int t = threadIdx.x;
+    const int64_t row = r0 + t;
+    const bool in_range = t < nrows;
+    const bool active = in_range && (masks == nullptr || masks[row]);
+
+    float vc0 = 0.f, vc1 = 0.f, vc2 = 0.f, x = 0.f, y = 0.f, z = 0.f,
+          inorm = 0.f;
+    if (active) {
+        vc0 = v_colors[row * 3 + 0];
+        vc1 = v_colors[row * 3 + 1];
+        vc2 = v_colors[row * 3 + 2];
+        if (DEG > 0) {
+            const float dx = dirs[row * 3 + 0], dy = dirs[row * 3 + 1],
+                        dz = dirs[row * 3 + 2];
+            inorm = 1.f / sqrtf(dx * dx + dy * dy + dz * dz);
+            x = dx * inorm;
+            y = dy * inorm;
+            z = dz * inorm;
+        }
+    }
+    // direction gradient needs the coefficients
+    if (DEG > 0 && v_dirs != nullptr) {
+        stage_coeffs<DEG>(coeffs, r0, nrows, K, vec_ok, s_buf);
+        __syncthreads();
+        if (in_range) {
+            float vdx = 0.f, vdy = 0.f, vdz = 0.f;
+            if (active) {
+                float G[S::NB];
+                const float *c = s_buf + t * S::PITCH;
+#pragma unroll
+                for (int k = 0; k < S::NB; ++k)
+                    G[k] = c[k * 3 + 0] * vc0 + c[k * 3 + 1] * vc1 +
+                           c[k * 3 + 2] * vc2;
+                float gx, gy, gz;
+                sh_basis_grad<DEG>(x, y, z, G, gx, gy, gz);
+                const float dot = gx * x + gy * y + gz * z;
+                vdx = (gx - dot * x) * inorm;
+                vdy = (gy - dot * y) * inorm;
+                vdz = (gz - dot * z) * inorm;
+            }
+            v_dirs[row * 3 + 0] = vdx;
+            v_dirs[row * 3 + 1] = vdy;
+            v_dirs[row * 3 + 2] = vdz;
+        }
+        __syncthreads();
+    } else if (v_dirs != nullptr && in_range) {
+        v_dirs[row * 3 + 0] = 0.f;
+        v_dirs[row * 3 + 1] = 0.f;
+        v_dirs[row * 3 + 2] = 0.f;
+    }
+
+    // v_coeffs[k][c] = Y_k * v_c, staged in LDS then streamed out
+    if (in_range) {
+        float Y[S::NB];
+        if (DEG > 0)
+            sh_basis<DEG>(x, y, z, Y);
+        else
+            Y[0] = kY0;
+        float *o = s_buf + t * S::PITCH;
+#pragma unroll
+        for (int k = 0; k < S::NB; ++k) {
+            o[k * 3 + 0] = active ? Y[k] * vc0 : 0.f;
+            o[k * 3 + 1] = active ? Y[k] * vc1 : 0.f;
+            o[k * 3 + 2] = active ? Y[k] * vc2 : 0.f;
+        }
+    }
+    __syncthreads();
+    const int rowlen = K * 3;
+    const int total = nrows * rowlen;
+    float *dst = v_coeffs + r0 * rowlen;
+    if (vec_ok && K == S::NB) {
+        float4 *dst4 = reinterpret_cast<float4 *>(dst);
+        const int nvec = total >> 2;
+        for (int v = threadIdx.x; v < nvec; v += kShThreads) {
+            const int e = v << 2;
+            float vals[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int ek = e + k;
+                const int r = ek / S::ROW;
+                vals[k] = s_buf[r * S::PITCH + (ek - r * S::ROW)];
+            }
+            dst4[v] = make_float4(vals[0], vals[1], vals[2], vals[3]);
+        }
+        for (int e = (nvec << 2) + threadIdx.x; e < total; e += kShThreads) {
+            const int r = e / S::ROW;
+            dst[e] = s_buf[r * S::PITCH + (e - r * S::ROW)];
+        }
+    } else {
+        for (int e = threadIdx.x; e < total; e += kShThreads) {
+            const int r = e / rowlen;
+            const int col = e - r * rowlen;
+            dst[e] = col < S::ROW ? s_buf[r * S::PITCH + col] : 0.f;
+        }
+    }
+}
+
+}  // namespace
+}  // namespace gs
+
+using namespace gs;
+
+#define GS_SH_LAUNCH(KERNEL, DEG, ...)                                         \
+    KERNEL<DEG><<<grid, kShThreads, 0, st>>>(__VA_ARGS__)
+
+extern "C" int gsplat_sh_fwd(int64_t M, int32_t K, int32_t degree,
+                             const float *dirs, const float *coeffs,
+                             const uint8_t *masks, float *colors,
+                             gsplat_stream_t stream) {
+    clear_error();
+    GS_REQUIRE(M >= 0, "sh_fwd: negative M");
+    GS_REQUIRE(degree >= 0 && degree <= 4, "sh_fwd: degree must be in [0, 4]");
+    GS_REQUIRE((degree + 1) * (degree + 1) <= K,
+               "sh_fwd: K must be >= (degree + 1)^2");
+    if (M == 0)
+        return GSPLAT_OK;
+    GS_REQUIRE(coeffs && colors && (degree == 0 || dirs), "sh_fwd: NULL buffer");
+    const int nb = (degree + 1) * (degree + 1);
+    const bool vec_ok = (K == nb) && aligned16(coeffs);
+    const dim3 grid((unsigned)ceil_div(M, kShThreads));
+    hipStream_t st = as_stream(stream);
+    switch (degree) {
+    case 0: GS_SH_LAUNCH(sh_fwd_kernel, 0, M, K, dirs, coeffs, masks, colors, vec_ok); break;
+    case 1: GS_SH_LAUNCH(sh_fwd_kernel, 1, M, K, dirs, coeffs, masks, colors, vec_ok); break;
+    case 2: GS_SH_LAUNCH(sh_fwd_kernel, 2, M, K, dirs, coeffs, masks, colors, vec_ok); break;
+    case 3: GS_SH_LAUNCH(sh_fwd_kernel, 3, M, K, dirs, coeffs, masks, colors, vec_ok); break;
+    default: GS_SH_LAUNCH(sh_fwd_kernel, 4, M, K, dirs, coeffs, masks, colors, vec_ok); break;
+    }
+    return check_launch("sh_fwd_kernel");
+}
+
+extern "C" int gsplat_sh_bwd(int64_t M, int32_t K, int32_t degree,
+                             const float *dirs, const float *coeffs,
+                             const uint8_t *masks, const float *v_colors,
+                             float *v_coeffs, float *v_dirs,
+                             gsplat_stream_t stream) {
+    clear_error();
+    GS_REQUIRE(M >= 0, "sh_bwd: negative M");
+    GS_REQUIRE(degree >= 0 && degree <= 4, "sh_bwd: degree must be in [0, 4]");
+    GS_REQUIRE((degree + 1) * (degree + 1) <= K,
+               "sh_bwd: K must be >= (degree + 1)^2");
+    if (M == 0)
+        return GSPLAT_OK;
+    GS_REQUIRE(coeffs && v_colors && v_coeffs && (degree == 0 || dirs),
+               "sh_bwd: NULL buffer");
+    const int nb = (degree + 1) * (degree + 1);
+    const bool vec_ok = (K == nb) && aligned16(coeffs) && aligned16(v_coeffs);
+    const dim3 grid((unsigned)ceil_div(M, kShThreads));
+    hipStream_t st = as_stream(stream);
+    switch (degree) {
+    case 0: GS_SH_LAUNCH(sh_bwd_kernel, 0, M, K, dirs, coeffs, masks, v_colors, v_coeffs, v_dirs, vec_ok); break;
+    case 1: GS_SH_LAUNCH(sh_bwd_kernel, 1, M, K, dirs, coeffs, masks, v_colors, v_coeffs, v_dirs, vec_ok); break;
+    case 2: GS_SH_LAUNCH(sh_bwd_kernel, 2, M, K, dirs, coeffs, masks, v_colors, v_coeffs, v_dirs, vec_ok); break;
+    case 3: GS_SH_LAUNCH(sh_bwd_kernel, 3, M, K, dirs, coeffs, masks, v_colors, v_coeffs, v_dirs, vec_ok); break;
+    default: GS_SH_LAUNCH(sh_bwd_kernel, 4, M, K, dirs, coeffs, masks, v_colors, v_coeffs, v_dirs, vec_ok); break;
+    }
+    return check_launch("sh_bwd_kernel");
+}

@@ -1,0 +1,529 @@
+"""Host side of every gsplat op: output allocation + one C-ABI call.
+
+Each function here has the argument list and return convention of the
+reference op of the same name (schemas in gsplat/cuda/ext.cpp:711-754,
+host wrappers in gsplat/cuda/csrc/{Projection,Intersect,Rasterization,
+SphericalHarmonics,Adam}.cpp).  Outputs are allocated through the torch
+caching allocator on the inputs' device; the kernels run on the current
+stream of that device.  Optional outputs that the reference returns as an
+undefined tensor are returned as ``None``.
+
+These functions are what ``torch.ops.gsplat.*`` dispatches to for the CUDA
+(HIP) key (see ``_backend.py``); the autograd wrappers call them directly to
+skip the dispatcher round trip.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+from torch import Tensor
+
+from .._lib import AdamTensor, call, check_input, ptr, query
+
+_F32 = torch.float32
+_I32 = torch.int32
+_I64 = torch.int64
+
+
+def _stream(t: Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _prod(shape) -> int:
+    return int(math.prod(shape))
+
+
+# --------------------------------------------------------------------------
+# Spherical harmonics  (SphericalHarmonics.cpp:33-91)
+# --------------------------------------------------------------------------
+def spherical_harmonics_fwd(
+    degrees_to_use: int, dirs: Tensor, coeffs: Tensor, masks: Optional[Tensor]
+) -> Tensor:
+    check_input(dirs, "dirs", _F32)
+    check_input(coeffs, "coeffs", _F32)
+    check_input(masks, "masks", torch.bool)
+    M = dirs.numel() // 3
+    K = coeffs.shape[-2]
+    colors = torch.empty_like(dirs)
+    call("gsplat_sh_fwd", M, K, degrees_to_use, ptr(dirs), ptr(coeffs),
+         ptr(masks), ptr(colors), _stream(dirs))
+    return colors
+
+
+def spherical_harmonics_bwd(
+    degrees_to_use: int,
+    dirs: Tensor,
+    coeffs: Tensor,
+    masks: Optional[Tensor],
+    v_colors: Tensor,
+    compute_v_dirs: bool,
+) -> Tuple[Tensor, Optional[Tensor]]:
+    check_input(dirs, "dirs", _F32)
+    check_input(coeffs, "coeffs", _F32)
+    check_input(masks, "masks", torch.bool)
+    check_input(v_colors, "v_colors", _F32)
+    M = dirs.numel() // 3
+    K = coeffs.shape[-2]
+    v_coeffs = torch.empty_like(coeffs)
+    v_dirs = torch.empty_like(dirs) if compute_v_dirs else None
+    call("gsplat_sh_bwd", M, K, degrees_to_use, ptr(dirs), ptr(coeffs),
+         ptr(masks), ptr(v_colors), ptr(v_coeffs), ptr(v_dirs), _stream(dirs))
+    return v_coeffs, v_dirs
+
+
+# --------------------------------------------------------------------------
+# Projection  (Projection.cpp:129-576)
+# --------------------------------------------------------------------------
+def _proj_dims(means: Tensor, viewmats: Tensor):
+    batch_dims = tuple(means.shape[:-2])
+    N = means.shape[-2]
+    C = viewmats.shape[-3]
+    B = _prod(batch_dims)
+    return batch_dims, B, C, N
+
+
+def _check_proj_inputs(means, covars, quats, scales, opacities, viewmats, Ks):
+    check_input(means, "means", _F32)
+    if covars is not None:
+        check_input(covars, "covars", _F32)
+    else:
+        if quats is None or scales is None:
+            raise RuntimeError("projection: covars or (quats, scales) required")
+        check_input(quats, "quats", _F32)
+        check_input(scales, "scales", _F32)
+    check_input(opacities, "opacities", _F32)
+    check_input(viewmats, "viewmats", _F32)
+    check_input(Ks, "Ks", _F32)
+
+
+def projection_ewa_3dgs_fused_fwd(
+    means: Tensor,
+    covars: Optional[Tensor],
+    quats: Optional[Tensor],
+    scales: Optional[Tensor],
+    opacities: Optional[Tensor],
+    viewmats: Tensor,
+    Ks: Tensor,
+    image_width: int,
+    image_height: int,
+    eps2d: float,
+    near_plane: float,
+    far_plane: float,
+    radius_clip: float,
+    calc_compensations: bool,
+    camera_model: int,
+) -> Tuple[Tensor, Tensor, Tensor, Tensor, Optional[Tensor]]:
+    _check_proj_inputs(means, covars, quats, scales, opacities, viewmats, Ks)
+    batch_dims, B, C, N = _proj_dims(means, viewmats)
+    dev = means.device
+    radii = torch.empty(batch_dims + (C, N, 2), dtype=_I32, device=dev)
+    means2d = torch.empty(batch_dims + (C, N, 2), dtype=_F32, device=dev)
+    depths = torch.empty(batch_dims + (C, N), dtype=_F32, device=dev)
+    conics = torch.empty(batch_dims + (C, N, 3), dtype=_F32, device=dev)
+    comps = (torch.empty(batch_dims + (C, N), dtype=_F32, device=dev)
+             if calc_compensations else None)
+    call("gsplat_projection_fused_fwd", B, C, N, ptr(means), ptr(covars),
+         ptr(quats), ptr(scales), ptr(opacities), ptr(viewmats), ptr(Ks),
+         int(image_width), int(image_height), float(eps2d), float(near_plane),
+         float(far_plane), float(radius_clip), int(camera_model),
+         ptr(radii), ptr(means2d), ptr(depths), ptr(conics), ptr(comps),
+         _stream(means))
+    return radii, means2d, depths, conics, comps
+
+
+def projection_ewa_3dgs_fused_bwd(
+    means: Tensor,
+    covars: Optional[Tensor],
+    quats: Optional[Tensor],
+    scales: Optional[Tensor],
+    viewmats: Tensor,
+    Ks: Tensor,
+    image_width: int,
+    image_height: int,
+    eps2d: float,
+    camera_model: int,
+    radii: Tensor,
+    conics: Tensor,
+    compensations: Optional[Tensor],
+    v_means2d: Tensor,
+    v_depths: Tensor,
+    v_conics: Tensor,
+    v_compensations: Optional[Tensor],
+    viewmats_requires_grad: bool,
+):
+    _check_proj_inputs(means, covars, quats, scales, None, viewmats, Ks)
+    for t, n in ((radii, "radii"), (conics, "conics"), (v_means2d, "v_means2d"),
+                 (v_depths, "v_depths"), (v_conics, "v_conics"),
+                 (compensations, "compensations"),
+                 (v_compensations, "v_compensations")):
+        check_input(t, n)
+    batch_dims, B, C, N = _proj_dims(means, viewmats)
+    v_means = torch.empty_like(means)
+    v_covars = v_quats = v_scales = None
+    if covars is not None:
+        v_covars = torch.empty_like(covars)
+    else:
+        v_quats = torch.empty_like(quats)
+        v_scales = torch.empty_like(scales)
+    v_viewmats = torch.zeros_like(viewmats) if viewmats_requires_grad else None
+    call("gsplat_projection_fused_bwd", B, C, N, ptr(means), ptr(covars),
+         ptr(quats), ptr(scales), ptr(viewmats), ptr(Ks), int(image_width),
+         int(image_height), float(eps2d), int(camera_model), ptr(radii),
+         ptr(conics), ptr(compensations), ptr(v_means2d), ptr(v_depths),
+         ptr(v_conics), ptr(v_compensations), ptr(v_means), ptr(v_covars),
+         ptr(v_quats), ptr(v_scales), ptr(v_viewmats), _stream(means))
+    return v_means, v_covars, v_quats, v_scales, v_viewmats
+
+
+def projection_ewa_3dgs_packed_fwd(
+    means: Tensor,
+    covars: Optional[Tensor],
+    quats: Optional[Tensor],
+    scales: Optional[Tensor],
+    opacities: Optional[Tensor],
+    viewmats: Tensor,
+    Ks: Tensor,
+    image_width: int,
+    image_height: int,
+    eps2d: float,
+    near_plane: float,
+    far_plane: float,
+    radius_clip: float,
+    calc_compensations: bool,
+    camera_model: int,
+):
+    _check_proj_inputs(means, covars, quats, scales, opacities, viewmats, Ks)
+    batch_dims, B, C, N = _proj_dims(means, viewmats)
+    dev = means.device
+    cap = B * C * N
+    indptr = torch.empty(B * C + 1, dtype=_I32, device=dev)
+    batch_ids = torch.empty(cap, dtype=_I64, device=dev)
+    camera_ids = torch.empty(cap, dtype=_I64, device=dev)
+    gaussian_ids = torch.empty(cap, dtype=_I64, device=dev)
+    radii = torch.empty(cap, 2, dtype=_I32, device=dev)
+    means2d = torch.empty(cap, 2, dtype=_F32, device=dev)
+    depths = torch.empty(cap, dtype=_F32, device=dev)
+    conics = torch.empty(cap, 3, dtype=_F32, device=dev)
+    comps = torch.empty(cap, dtype=_F32, device=dev) if calc_compensations else None
+    if cap == 0:
+        indptr.zero_()
+        nnz = 0
+    else:
+        ws = torch.empty(query("gsplat_projection_packed_workspace_size", B, C, N),
+                         dtype=torch.uint8, device=dev)
+        nnz_dev = torch.empty(1, dtype=_I64, device=dev)
+        call("gsplat_projection_packed_fwd", B, C, N, ptr(means), ptr(covars),
+             ptr(quats), ptr(scales), ptr(opacities), ptr(viewmats), ptr(Ks),
+             int(image_width), int(image_height), float(eps2d),
+             float(near_plane), float(far_plane), float(radius_clip),
+             int(camera_model), ptr(ws), ws.numel(), ptr(indptr),
+             ptr(batch_ids), ptr(camera_ids), ptr(gaussian_ids), ptr(radii),
+             ptr(means2d), ptr(depths), ptr(conics), ptr(comps), ptr(nnz_dev),
+             _stream(means))
+        nnz = int(nnz_dev.item())
+    return (
+        indptr,
+        batch_ids[:nnz],
+        camera_ids[:nnz],
+        gaussian_ids[:nnz],
+        radii[:nnz],
+        means2d[:nnz],
+        depths[:nnz],
+        conics[:nnz],
+        comps[:nnz] if comps is not None else None,
+    )
+
+
+def projection_ewa_3dgs_packed_bwd(
+    means: Tensor,
+    covars: Optional[Tensor],
+    quats: Optional[Tensor],
+    scales: Optional[Tensor],
+    viewmats: Tensor,
+    Ks: Tensor,
+    image_width: int,
+    image_height: int,
+    eps2d: float,
+    camera_model: int,
+    batch_ids: Tensor,
+    camera_ids: Tensor,
+    gaussian_ids: Tensor,
+    conics: Tensor,
+    compensations: Optional[Tensor],
+    v_means2d: Tensor,
+    v_depths: Tensor,
+    v_conics: Tensor,
+    v_compensations: Optional[Tensor],
+    viewmats_requires_grad: bool,
+    sparse_grad: bool,
+):
+    _check_proj_inputs(means, covars, quats, scales, None, viewmats, Ks)
+    for t, n in ((batch_ids, "batch_ids"), (camera_ids, "camera_ids"),
+                 (gaussian_ids, "gaussian_ids"), (conics, "conics"),
+                 (v_means2d, "v_means2d"), (v_depths, "v_depths"),
+                 (v_conics, "v_conics"), (compensations, "compensations"),
+                 (v_compensations, "v_compensations")):
+        check_input(t, n)
+    batch_dims, B, C, N = _proj_dims(means, viewmats)
+    nnz = batch_ids.shape[0]
+    dev = means.device
+    v_covars = v_quats = v_scales = None
+    if sparse_grad:
+        v_means = torch.empty(nnz, 3, dtype=_F32, device=dev)
+        if covars is not None:
+            v_covars = torch.empty(nnz, 6, dtype=_F32, device=dev)
+        else:
+            v_quats = torch.empty(nnz, 4, dtype=_F32, device=dev)
+            v_scales = torch.empty(nnz, 3, dtype=_F32, device=dev)
+    else:
+        v_means = torch.zeros_like(means)
+        if covars is not None:
+            v_covars = torch.zeros_like(covars)
+        else:
+            v_quats = torch.zeros_like(quats)
+            v_scales = torch.zeros_like(scales)
+    v_viewmats = torch.zeros_like(viewmats) if viewmats_requires_grad else None
+    call("gsplat_projection_packed_bwd", B, C, N, nnz, ptr(means), ptr(covars),
+         ptr(quats), ptr(scales), ptr(viewmats), ptr(Ks), int(image_width),
+         int(image_height), float(eps2d), int(camera_model), ptr(batch_ids),
+         ptr(camera_ids), ptr(gaussian_ids), ptr(conics), ptr(compensations),
+         ptr(v_means2d), ptr(v_depths), ptr(v_conics), ptr(v_compensations),
+         int(bool(sparse_grad)), ptr(v_means), ptr(v_covars), ptr(v_quats),
+         ptr(v_scales), ptr(v_viewmats), _stream(means))
+    return v_means, v_covars, v_quats, v_scales, v_viewmats
+
+
+# --------------------------------------------------------------------------
+# Tile intersection  (Intersect.cpp:33-164, 320-337)
+# --------------------------------------------------------------------------
+def intersect_tile(
+    means2d: Tensor,
+    radii: Tensor,
+    depths: Tensor,
+    conics: Optional[Tensor],
+    opacities: Optional[Tensor],
+    image_ids: Optional[Tensor],
+    gaussian_ids: Optional[Tensor],
+    I: int,
+    tile_size: int,
+    tile_width: int,
+    tile_height: int,
+    sort: bool,
+    segmented: bool,
+) -> Tuple[Tensor, Tensor, Tensor]:
+    check_input(means2d, "means2d", _F32)
+    check_input(radii, "radii", _I32)
+    check_input(depths, "depths", _F32)
+    check_input(conics, "conics", _F32)
+    check_input(opacities, "opacities", _F32)
+    packed = means2d.dim() == 2
+    if packed:
+        if image_ids is None or gaussian_ids is None:
+            raise RuntimeError(
+                "When packed is set, image_ids and gaussian_ids must be provided.")
+        check_input(image_ids, "image_ids", _I64)
+        check_input(gaussian_ids, "gaussian_ids", _I64)
+    n = means2d.numel() // 2
+    N = 0 if packed else means2d.shape[-2]
+    n_tiles = int(tile_width) * int(tile_height)
+    tile_n_bits = n_tiles.bit_length()
+    image_n_bits = int(I).bit_length()
+    if image_n_bits + tile_n_bits > 32:
+        raise RuntimeError("intersect_tile: image and tile ids need more than 32 bits")
+    dev = means2d.device
+    tiles_per_gauss = torch.empty(depths.shape, dtype=_I32, device=dev)
+    if n == 0:
+        return (tiles_per_gauss, torch.empty(0, dtype=_I64, device=dev),
+                torch.empty(0, dtype=_I32, device=dev))
+    st = _stream(means2d)
+    img = image_ids if packed else None
+    cum = torch.empty(n, dtype=_I64, device=dev)
+    ws = torch.empty(query("gsplat_isect_count_workspace_size", n),
+                     dtype=torch.uint8, device=dev)
+    call("gsplat_isect_count", n, N, ptr(img), ptr(means2d), ptr(radii),
+         ptr(conics), ptr(opacities), int(tile_size), int(tile_width),
+         int(tile_height), ptr(ws), ws.numel(), ptr(tiles_per_gauss), ptr(cum), st)
+    n_isects = int(cum[-1].item())
+    isect_ids = torch.empty(n_isects, dtype=_I64, device=dev)
+    flatten_ids = torch.empty(n_isects, dtype=_I32, device=dev)
+    if n_isects == 0:
+        return tiles_per_gauss, isect_ids, flatten_ids
+    call("gsplat_isect_emit", n, N, int(I), ptr(img), ptr(means2d), ptr(radii),
+         ptr(depths), ptr(conics), ptr(opacities), int(tile_size),
+         int(tile_width), int(tile_height), ptr(cum), ptr(isect_ids),
+         ptr(flatten_ids), st)
+    if sort:
+        # One global sort on the significant key bits; a per-image segmented
+        # sort (segmented=True) gives the same order because the image id
+        # occupies the top key bits.
+        keys_out = torch.empty_like(isect_ids)
+        vals_out = torch.empty_like(flatten_ids)
+        sws = torch.empty(query("gsplat_sort_pairs_workspace_size", n_isects),
+                          dtype=torch.uint8, device=dev)
+        call("gsplat_sort_pairs_u64_u32", n_isects, 32 + tile_n_bits + image_n_bits,
+             ptr(isect_ids), ptr(flatten_ids), ptr(keys_out), ptr(vals_out),
+             ptr(sws), sws.numel(), st)
+        isect_ids, flatten_ids = keys_out, vals_out
+    return tiles_per_gauss, isect_ids, flatten_ids
+
+
+def intersect_offset(isect_ids: Tensor, I: int, tile_width: int, tile_height: int) -> Tensor:
+    check_input(isect_ids, "isect_ids", _I64)
+    offsets = torch.empty((int(I), int(tile_height), int(tile_width)), dtype=_I32,
+                          device=isect_ids.device)
+    call("gsplat_isect_offsets", isect_ids.numel(), ptr(isect_ids), int(I),
+         int(tile_width), int(tile_height), ptr(offsets), _stream(isect_ids))
+    return offsets
+
+
+# --------------------------------------------------------------------------
+# Rasterizer  (Rasterization.cpp:42-214)
+# --------------------------------------------------------------------------
+def _raster_common(means2d, conics, colors, opacities, backgrounds, masks,
+                   tile_offsets, flatten_ids):
+    check_input(means2d, "means2d", _F32)
+    check_input(conics, "conics", _F32)
+    check_input(colors, "colors", _F32)
+    check_input(opacities, "opacities", _F32)
+    check_input(backgrounds, "backgrounds", _F32)
+    check_input(masks, "masks", torch.bool)
+    check_input(tile_offsets, "tile_offsets", _I32)
+    check_input(flatten_ids, "flatten_ids", _I32)
+    image_dims = tuple(tile_offsets.shape[:-2])
+    tile_height, tile_width = tile_offsets.shape[-2:]
+    I = _prod(image_dims)
+    n_rows = means2d.numel() // 2
+    return image_dims, I, n_rows, tile_width, tile_height
+
+
+def rasterize_to_pixels_3dgs_fwd(
+    means2d: Tensor,
+    conics: Tensor,
+    colors: Tensor,
+    opacities: Tensor,
+    backgrounds: Optional[Tensor],
+    masks: Optional[Tensor],
+    image_width: int,
+    image_height: int,
+    tile_size: int,
+    tile_offsets: Tensor,
+    flatten_ids: Tensor,
+) -> Tuple[Tensor, Tensor, Tensor]:
+    image_dims, I, n_rows, tw, th = _raster_common(
+        means2d, conics, colors, opacities, backgrounds, masks, tile_offsets,
+        flatten_ids)
+    channels = colors.shape[-1]
+    dev = means2d.device
+    H, W = int(image_height), int(image_width)
+    renders = torch.empty(image_dims + (H, W, channels), dtype=_F32, device=dev)
+    alphas = torch.empty(image_dims + (H, W, 1), dtype=_F32, device=dev)
+    last_ids = torch.empty(image_dims + (H, W), dtype=_I32, device=dev)
+    call("gsplat_rasterize_fwd", I, n_rows, flatten_ids.numel(), channels,
+         ptr(means2d), ptr(conics), ptr(colors), ptr(opacities),
+         ptr(backgrounds), ptr(masks), W, H, int(tile_size), tw, th,
+         ptr(tile_offsets), ptr(flatten_ids), ptr(renders), ptr(alphas),
+         ptr(last_ids), _stream(means2d))
+    return renders, alphas, last_ids
+
+
+def rasterize_to_pixels_3dgs_bwd(
+    means2d: Tensor,
+    conics: Tensor,
+    colors: Tensor,
+    opacities: Tensor,
+    backgrounds: Optional[Tensor],
+    masks: Optional[Tensor],
+    image_width: int,
+    image_height: int,
+    tile_size: int,
+    tile_offsets: Tensor,
+    flatten_ids: Tensor,
+    render_alphas: Tensor,
+    last_ids: Tensor,
+    v_render_colors: Tensor,
+    v_render_alphas: Tensor,
+    absgrad: bool,
+):
+    image_dims, I, n_rows, tw, th = _raster_common(
+        means2d, conics, colors, opacities, backgrounds, masks, tile_offsets,
+        flatten_ids)
+    check_input(render_alphas, "render_alphas", _F32)
+    check_input(last_ids, "last_ids", _I32)
+    check_input(v_render_colors, "v_render_colors", _F32)
+    check_input(v_render_alphas, "v_render_alphas", _F32)
+    channels = colors.shape[-1]
+    v_means2d = torch.zeros_like(means2d)
+    v_conics = torch.zeros_like(conics)
+    v_colors = torch.zeros_like(colors)
+    v_opacities = torch.zeros_like(opacities)
+    v_means2d_abs = torch.zeros_like(means2d) if absgrad else None
+    call("gsplat_rasterize_bwd", I, n_rows, flatten_ids.numel(), channels,
+         ptr(means2d), ptr(conics), ptr(colors), ptr(opacities),
+         ptr(backgrounds), ptr(masks), int(image_width), int(image_height),
+         int(tile_size), tw, th, ptr(tile_offsets), ptr(flatten_ids),
+         ptr(render_alphas), ptr(last_ids), ptr(v_render_colors),
+         ptr(v_render_alphas), ptr(v_means2d_abs), ptr(v_means2d),
+         ptr(v_conics), ptr(v_colors), ptr(v_opacities), _stream(means2d))
+    return v_means2d_abs, v_means2d, v_conics, v_colors, v_opacities
+
+
+# --------------------------------------------------------------------------
+# Fused Adam  (Adam.cpp:37-66)
+# --------------------------------------------------------------------------
+def _adam_checks(param, param_grad, exp_avg, exp_avg_sq, valid):
+    for t, n in ((param, "param"), (param_grad, "param_grad"),
+                 (exp_avg, "exp_avg"), (exp_avg_sq, "exp_avg_sq")):
+        check_input(t, n, _F32)
+    if param_grad.shape != param.shape or exp_avg.shape != param.shape \
+            or exp_avg_sq.shape != param.shape:
+        raise RuntimeError("adam: param, grad and moments must have the same shape")
+    if valid is not None:
+        check_input(valid, "valid", torch.bool)
+        if valid.dim() != 1:
+            raise RuntimeError("valid should be 1D tensor")
+        if valid.size(0) != param.size(0):
+            raise RuntimeError("valid first dimension should match param first dimension")
+
+
+def adam(
+    param: Tensor,
+    param_grad: Tensor,
+    exp_avg: Tensor,
+    exp_avg_sq: Tensor,
+    valid: Optional[Tensor],
+    lr: float,
+    b1: float,
+    b2: float,
+    eps: float,
+) -> None:
+    _adam_checks(param, param_grad, exp_avg, exp_avg_sq, valid)
+    n_rows = param.size(0) if param.dim() > 0 else 1
+    row = param.numel() // n_rows if n_rows > 0 else 0
+    call("gsplat_adam", ptr(param), ptr(param_grad), ptr(exp_avg),
+         ptr(exp_avg_sq), ptr(valid), n_rows, row, float(lr), float(b1),
+         float(b2), float(eps), _stream(param))
+
+
+def adam_multi(groups, b1: float, b2: float, eps: float) -> None:
+    """One launch over several tensors.
+
+    ``groups``: iterable of (param, grad, exp_avg, exp_avg_sq, valid, lr).
+    """
+    entries = []
+    dev = None
+    for (p, g, m, v, valid, lr) in groups:
+        _adam_checks(p, g, m, v, valid)
+        n_rows = p.size(0) if p.dim() > 0 else 1
+        row = p.numel() // n_rows if n_rows > 0 else 0
+        entries.append(AdamTensor(ptr(p), ptr(g), ptr(m), ptr(v), ptr(valid),
+                                  n_rows, row, float(lr)))
+        dev = p
+    if not entries:
+        return
+    arr = (AdamTensor * len(entries))(*entries)
+    import ctypes
+    call("gsplat_adam_multi", ctypes.cast(arr, ctypes.c_void_p), len(entries),
+         float(b1), float(b2), float(eps), _stream(dev))

@@ -1,0 +1,572 @@
+"""Python API of the splatting ops, argument-for-argument the reference's
+``gsplat.cuda._wrapper`` for the 3DGS hot path (gsplat/cuda/_wrapper.py):
+
+    fully_fused_projection  (:479-631)   spherical_harmonics (:342-372)
+    isect_tiles             (:635-730)   isect_offset_encode (:807-826)
+    rasterize_to_pixels     (:829-961)   adam                (:326-339)
+
+with the autograd Functions _FullyFusedProjection (:1464-1594),
+_FullyFusedProjectionPacked (:2107-2326), _SphericalHarmonics (:2329-2363)
+and _RasterizeToPixels (:1709-1836).  The kernels behind them are the HIP
+kernels of libgsplat_hip.so, reached through ``_ops``.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Callable, Optional, Tuple
+
+import torch
+from torch import Tensor
+from typing_extensions import Literal
+
+from . import _ops
+from ._backend import CameraModelType, _C  # noqa: F401  (registers torch.ops.gsplat)
+
+CameraModel = Literal["pinhole", "ortho", "fisheye", "ftheta", "lidar"]
+
+# Channel counts with a compiled rasterizer instantiation.
+SUPPORTED_CHANNELS = (1, 2, 3, 4, 5, 8, 9, 16, 17, 32, 33)
+CHANNEL_CHUNK = 32
+
+
+def _make_lazy_cuda_func(name: str) -> Callable:
+    """Direct handle to the op implementation (same arguments as
+    ``torch.ops.gsplat.<name>``, without the dispatcher round trip)."""
+    return getattr(_ops, name)
+
+
+def _make_lazy_cuda_obj(name: str):
+    obj = _C
+    for part in name.split("."):
+        obj = getattr(obj, part)
+    return obj
+
+
+def _camera_model_type(camera_model: str) -> int:
+    if camera_model not in ("pinhole", "ortho"):
+        raise NotImplementedError(
+            f"camera_model={camera_model!r}: only 'pinhole' and 'ortho' are "
+            "implemented by the MI355X kernels")
+    return int(_make_lazy_cuda_obj(f"CameraModelType.{camera_model.upper()}"))
+
+
+def has_3dgs() -> bool:
+    return hasattr(torch.ops.gsplat, "projection_ewa_3dgs_fused_fwd")
+
+
+def has_adam() -> bool:
+    return hasattr(torch.ops.gsplat, "adam")
+
+
+def has_2dgs() -> bool:
+    return False
+
+
+def has_3dgut() -> bool:
+    return False
+
+
+def has_reloc() -> bool:
+    return False
+
+
+def has_camera_wrappers() -> bool:
+    return False
+
+
+def adam(
+    param: Tensor,
+    param_grad: Tensor,
+    exp_avg: Tensor,
+    exp_avg_sq: Tensor,
+    valid: Tensor,
+    lr: float,
+    b1: float,
+    b2: float,
+    eps: float,
+) -> None:
+    _make_lazy_cuda_func("adam")(
+        param, param_grad, exp_avg, exp_avg_sq, valid, lr, b1, b2, eps
+    )
+
+
+def spherical_harmonics(
+    degrees_to_use: int,
+    dirs: Tensor,  # [..., 3]
+    coeffs: Tensor,  # [..., K, 3]
+    masks: Optional[Tensor] = None,  # [...,]
+) -> Tensor:
+    """Computes spherical harmonics colours. [..., 3]"""
+    assert (degrees_to_use + 1) ** 2 <= coeffs.shape[-2], coeffs.shape
+    batch_dims = dirs.shape[:-1]
+    assert dirs.shape == batch_dims + (3,), dirs.shape
+    assert (
+        (len(coeffs.shape) == len(batch_dims) + 2)
+        and coeffs.shape[:-2] == batch_dims
+        and coeffs.shape[-1] == 3
+    ), coeffs.shape
+    if masks is not None:
+        assert masks.shape == batch_dims, masks.shape
+        masks = masks.contiguous()
+    return _SphericalHarmonics.apply(
+        degrees_to_use, dirs.contiguous(), coeffs.contiguous(), masks
+    )
+
+
+def fully_fused_projection(
+    means: Tensor,  # [..., N, 3]
+    covars: Optional[Tensor],  # [..., N, 6] or None
+    quats: Optional[Tensor],  # [..., N, 4] or None
+    scales: Optional[Tensor],  # [..., N, 3] or None
+    viewmats: Tensor,  # [..., C, 4, 4]
+    Ks: Tensor,  # [..., C, 3, 3]
+    width: int,
+    height: int,
+    eps2d: float = 0.3,
+    near_plane: float = 0.01,
+    far_plane: float = 1e10,
+    radius_clip: float = 0.0,
+    packed: bool = False,
+    sparse_grad: bool = False,
+    calc_compensations: bool = False,
+    camera_model: CameraModel = "pinhole",
+    opacities: Optional[Tensor] = None,  # [..., N] or None
+) -> Tuple[Tensor, ...]:
+    """Projects Gaussians to 2D (EWA splatting).
+
+    Returns, if ``packed``: (batch_ids, camera_ids, gaussian_ids, indptr, radii,
+    means2d, depths, conics, compensations) over the nnz visible rows; else
+    (radii, means2d, depths, conics, compensations) of shape [..., C, N, *].
+    """
+    batch_dims = means.shape[:-2]
+    N = means.shape[-2]
+    C = viewmats.shape[-3]
+    assert means.shape == batch_dims + (N, 3), means.shape
+    assert viewmats.shape == batch_dims + (C, 4, 4), viewmats.shape
+    assert Ks.shape == batch_dims + (C, 3, 3), Ks.shape
+    means = means.contiguous()
+    if covars is not None:
+        assert covars.shape == batch_dims + (N, 6), covars.shape
+        covars = covars.contiguous()
+    else:
+        assert quats is not None, "covars or quats is required"
+        assert scales is not None, "covars or scales is required"
+        assert quats.shape == batch_dims + (N, 4), quats.shape
+        assert scales.shape == batch_dims + (N, 3), scales.shape
+        quats = quats.contiguous()
+        scales = scales.contiguous()
+    if sparse_grad:
+        assert packed, "sparse_grad is only supported when packed is True"
+        assert batch_dims == (), "sparse_grad does not support batch dimensions"
+    if opacities is not None:
+        assert opacities.shape == batch_dims + (N,), opacities.shape
+        opacities = opacities.contiguous()
+    viewmats = viewmats.contiguous()
+    Ks = Ks.contiguous()
+    if packed:
+        return _FullyFusedProjectionPacked.apply(
+            means, covars, quats, scales, viewmats, Ks, width, height, eps2d,
+            near_plane, far_plane, radius_clip, sparse_grad, calc_compensations,
+            camera_model, opacities,
+        )
+    return _FullyFusedProjection.apply(
+        means, covars, quats, scales, viewmats, Ks, width, height, eps2d,
+        near_plane, far_plane, radius_clip, calc_compensations, camera_model,
+        opacities,
+    )
+
+
+@torch.no_grad()
+def isect_tiles(
+    means2d: Tensor,  # [..., N, 2] or [nnz, 2]
+    radii: Tensor,  # [..., N, 2] or [nnz, 2]
+    depths: Tensor,  # [..., N] or [nnz]
+    tile_size: int,
+    tile_width: int,
+    tile_height: int,
+    sort: bool = True,
+    segmented: bool = False,
+    packed: bool = False,
+    n_images: Optional[int] = None,
+    image_ids: Optional[Tensor] = None,
+    gaussian_ids: Optional[Tensor] = None,
+    conics: Optional[Tensor] = None,  # enables the ellipse test with opacities
+    opacities: Optional[Tensor] = None,
+) -> Tuple[Tensor, Tensor, Tensor]:
+    """Maps projected Gaussians to intersecting tiles.
+
+    Returns (tiles_per_gauss int32, isect_ids int64 image|tile|depth-bits,
+    flatten_ids int32 index into [I * N] or [nnz]).
+    """
+    if packed:
+        nnz = means2d.size(0)
+        assert means2d.shape == (nnz, 2), means2d.shape
+        assert radii.shape == (nnz, 2), radii.shape
+        assert depths.shape == (nnz,), depths.shape
+        if conics is not None:
+            assert conics.shape == (nnz, 3), conics.shape
+        if opacities is not None:
+            assert opacities.shape == (nnz,), opacities.shape
+        assert image_ids is not None, "image_ids is required if packed is True"
+        assert gaussian_ids is not None, "gaussian_ids is required if packed is True"
+        assert n_images is not None, "n_images is required if packed is True"
+        image_ids = image_ids.contiguous()
+        gaussian_ids = gaussian_ids.contiguous()
+        I = n_images
+    else:
+        image_dims = means2d.shape[:-2]
+        I = math.prod(image_dims)
+        N = means2d.shape[-2]
+        assert means2d.shape == image_dims + (N, 2), means2d.shape
+        assert radii.shape == image_dims + (N, 2), radii.shape
+        assert depths.shape == image_dims + (N,), depths.shape
+        if conics is not None:
+            assert conics.shape == image_dims + (N, 3), conics.shape
+        if opacities is not None:
+            assert opacities.shape == image_dims + (N,), opacities.shape
+    return _make_lazy_cuda_func("intersect_tile")(
+        means2d.contiguous(),
+        radii.contiguous(),
+        depths.contiguous(),
+        conics.contiguous() if conics is not None else None,
+        opacities.contiguous() if opacities is not None else None,
+        image_ids,
+        gaussian_ids,
+        I,
+        tile_size,
+        tile_width,
+        tile_height,
+        sort,
+        segmented,
+    )
+
+
+@torch.no_grad()
+def isect_offset_encode(
+    isect_ids: Tensor, n_images: int, tile_width: int, tile_height: int
+) -> Tensor:
+    """Encodes intersection ids to tile start offsets. [I, tile_height, tile_width]"""
+    return _make_lazy_cuda_func("intersect_offset")(
+        isect_ids.contiguous(), n_images, tile_width, tile_height
+    )
+
+
+def _pad_channels(channels: int) -> int:
+    for c in SUPPORTED_CHANNELS:
+        if c >= channels:
+            return c
+    raise ValueError(f"Unsupported number of color channels: {channels}")
+
+
+def rasterize_to_pixels(
+    means2d: Tensor,  # [..., N, 2] or [nnz, 2]
+    conics: Tensor,  # [..., N, 3] or [nnz, 3]
+    colors: Tensor,  # [..., N, channels] or [nnz, channels]
+    opacities: Tensor,  # [..., N] or [nnz]
+    image_width: int,
+    image_height: int,
+    tile_size: int,
+    isect_offsets: Tensor,  # [..., tile_height, tile_width]
+    flatten_ids: Tensor,  # [n_isects]
+    backgrounds: Optional[Tensor] = None,  # [..., channels]
+    masks: Optional[Tensor] = None,  # [..., tile_height, tile_width]
+    packed: bool = False,
+    absgrad: bool = False,
+) -> Tuple[Tensor, Tensor]:
+    """Rasterizes Gaussians to pixels.
+
+    Returns (render_colors [..., H, W, channels], render_alphas [..., H, W, 1]).
+    Channel counts without a compiled kernel are zero-padded to the next one;
+    more than 33 channels are rendered in 32-channel chunks (for absgrad, the
+    chunks' |dL/dmean2d| are summed).
+    """
+    image_dims = means2d.shape[:-2]
+    channels = colors.shape[-1]
+    device = means2d.device
+    if packed:
+        nnz = means2d.size(0)
+        assert means2d.shape == (nnz, 2), means2d.shape
+        assert conics.shape == (nnz, 3), conics.shape
+        assert colors.shape[0] == nnz, colors.shape
+        assert opacities.shape == (nnz,), opacities.shape
+    else:
+        N = means2d.size(-2)
+        assert means2d.shape == image_dims + (N, 2), means2d.shape
+        assert conics.shape == image_dims + (N, 3), conics.shape
+        assert colors.shape == image_dims + (N, channels), colors.shape
+        assert opacities.shape == image_dims + (N,), opacities.shape
+    if backgrounds is not None:
+        assert backgrounds.shape == image_dims + (channels,), backgrounds.shape
+        backgrounds = backgrounds.contiguous()
+    if masks is not None:
+        assert masks.shape == isect_offsets.shape, masks.shape
+        masks = masks.contiguous()
+    if channels > 513 or channels == 0:
+        raise ValueError(f"Unsupported number of color channels: {channels}")
+
+    tile_height, tile_width = isect_offsets.shape[-2:]
+    assert (
+        tile_height * tile_size >= image_height
+    ), f"Assert Failed: {tile_height} * {tile_size} >= {image_height}"
+    assert (
+        tile_width * tile_size >= image_width
+    ), f"Assert Failed: {tile_width} * {tile_size} >= {image_width}"
+
+    means2d = means2d.contiguous()
+    conics = conics.contiguous()
+    opacities = opacities.contiguous()
+    isect_offsets = isect_offsets.contiguous()
+    flatten_ids = flatten_ids.contiguous()
+
+    def one(cols: Tensor, bgs: Optional[Tensor]) -> Tuple[Tensor, Tensor]:
+        c = cols.shape[-1]
+        pc = _pad_channels(c)
+        if pc != c:
+            cols = torch.cat(
+                [cols, torch.zeros(*cols.shape[:-1], pc - c, device=device)], dim=-1)
+            if bgs is not None:
+                bgs = torch.cat(
+                    [bgs, torch.zeros(*bgs.shape[:-1], pc - c, device=device)], dim=-1)
+        rc, ra = _RasterizeToPixels.apply(
+            means2d, conics, cols.contiguous(), opacities, bgs, masks,
+            image_width, image_height, tile_size, isect_offsets, flatten_ids,
+            absgrad,
+        )
+        if pc != c:
+            rc = rc[..., :c]
+        return rc, ra
+
+    if channels <= SUPPORTED_CHANNELS[-1]:
+        return one(colors, backgrounds)
+    outs, alphas = [], None
+    for s in range(0, channels, CHANNEL_CHUNK):
+        rc, ra = one(
+            colors[..., s:s + CHANNEL_CHUNK],
+            backgrounds[..., s:s + CHANNEL_CHUNK] if backgrounds is not None else None,
+        )
+        outs.append(rc)
+        if alphas is None:
+            alphas = ra
+    return torch.cat(outs, dim=-1), alphas
+
+
+class _FullyFusedProjection(torch.autograd.Function):
+    """Projects Gaussians to 2D (dense [..., C, N] outputs)."""
+
+    @staticmethod
+    def forward(
+        ctx,
+        means: Tensor,
+        covars: Optional[Tensor],
+        quats: Optional[Tensor],
+        scales: Optional[Tensor],
+        viewmats: Tensor,
+        Ks: Tensor,
+        width: int,
+        height: int,
+        eps2d: float,
+        near_plane: float,
+        far_plane: float,
+        radius_clip: float,
+        calc_compensations: bool,
+        camera_model: CameraModel = "pinhole",
+        opacities: Optional[Tensor] = None,
+    ):
+        cm = _camera_model_type(camera_model)
+        radii, means2d, depths, conics, compensations = _make_lazy_cuda_func(
+            "projection_ewa_3dgs_fused_fwd"
+        )(means, covars, quats, scales, opacities, viewmats, Ks, width, height,
+          eps2d, near_plane, far_plane, radius_clip, calc_compensations, cm)
+        if not calc_compensations:
+            compensations = None
+        ctx.save_for_backward(
+            means, covars, quats, scales, viewmats, Ks, radii, conics, compensations
+        )
+        ctx.width = width
+        ctx.height = height
+        ctx.eps2d = eps2d
+        ctx.camera_model_type = cm
+        ctx.mark_non_differentiable(radii)
+        return radii, means2d, depths, conics, compensations
+
+    @staticmethod
+    def backward(ctx, v_radii, v_means2d, v_depths, v_conics, v_compensations):
+        (means, covars, quats, scales, viewmats, Ks, radii, conics,
+         compensations) = ctx.saved_tensors
+        if compensations is None:
+            v_compensations = None
+        elif v_compensations is not None:
+            v_compensations = v_compensations.contiguous()
+        v_means, v_covars, v_quats, v_scales, v_viewmats = _make_lazy_cuda_func(
+            "projection_ewa_3dgs_fused_bwd"
+        )(means, covars, quats, scales, viewmats, Ks, ctx.width, ctx.height,
+          ctx.eps2d, ctx.camera_model_type, radii, conics, compensations,
+          v_means2d.contiguous(), v_depths.contiguous(), v_conics.contiguous(),
+          v_compensations, ctx.needs_input_grad[4])
+        if not ctx.needs_input_grad[0]:
+            v_means = None
+        if not ctx.needs_input_grad[1]:
+            v_covars = None
+        if not ctx.needs_input_grad[2]:
+            v_quats = None
+        if not ctx.needs_input_grad[3]:
+            v_scales = None
+        if not ctx.needs_input_grad[4]:
+            v_viewmats = None
+        return (v_means, v_covars, v_quats, v_scales, v_viewmats,
+                None, None, None, None, None, None, None, None, None, None)
+
+
+class _FullyFusedProjectionPacked(torch.autograd.Function):
+    """Projects Gaussians to 2D; returns the visible rows packed."""
+
+    @staticmethod
+    def forward(
+        ctx,
+        means: Tensor,
+        covars: Optional[Tensor],
+        quats: Optional[Tensor],
+        scales: Optional[Tensor],
+        viewmats: Tensor,
+        Ks: Tensor,
+        width: int,
+        height: int,
+        eps2d: float,
+        near_plane: float,
+        far_plane: float,
+        radius_clip: float,
+        sparse_grad: bool,
+        calc_compensations: bool,
+        camera_model: CameraModel = "pinhole",
+        opacities: Optional[Tensor] = None,
+    ):
+        cm = _camera_model_type(camera_model)
+        (indptr, batch_ids, camera_ids, gaussian_ids, radii, means2d, depths,
+         conics, compensations) = _make_lazy_cuda_func(
+            "projection_ewa_3dgs_packed_fwd"
+        )(means, covars, quats, scales, opacities, viewmats, Ks, width, height,
+          eps2d, near_plane, far_plane, radius_clip, calc_compensations, cm)
+        if not calc_compensations:
+            compensations = None
+        ctx.save_for_backward(batch_ids, camera_ids, gaussian_ids, means, covars,
+                              quats, scales, viewmats, Ks, conics, compensations)
+        ctx.width = width
+        ctx.height = height
+        ctx.eps2d = eps2d
+        ctx.sparse_grad = sparse_grad
+        ctx.camera_model_type = cm
+        ctx.mark_non_differentiable(batch_ids, camera_ids, gaussian_ids, indptr, radii)
+        return (batch_ids, camera_ids, gaussian_ids, indptr, radii, means2d,
+                depths, conics, compensations)
+
+    @staticmethod
+    def backward(ctx, v_batch_ids, v_camera_ids, v_gaussian_ids, v_indptr,
+                 v_radii, v_means2d, v_depths, v_conics, v_compensations):
+        (batch_ids, camera_ids, gaussian_ids, means, covars, quats, scales,
+         viewmats, Ks, conics, compensations) = ctx.saved_tensors
+        sparse_grad = ctx.sparse_grad
+        if compensations is None:
+            v_compensations = None
+        elif v_compensations is not None:
+            v_compensations = v_compensations.contiguous()
+        v_means, v_covars, v_quats, v_scales, v_viewmats = _make_lazy_cuda_func(
+            "projection_ewa_3dgs_packed_bwd"
+        )(means, covars, quats, scales, viewmats, Ks, ctx.width, ctx.height,
+          ctx.eps2d, ctx.camera_model_type, batch_ids, camera_ids, gaussian_ids,
+          conics, compensations, v_means2d.contiguous(), v_depths.contiguous(),
+          v_conics.contiguous(), v_compensations, ctx.needs_input_grad[4],
+          sparse_grad)
+        coalesced = len(viewmats) == 1
+
+        def sparse(values, like):
+            return torch.sparse_coo_tensor(indices=gaussian_ids[None], values=values,
+                                           size=like.shape, is_coalesced=coalesced)
+
+        if not ctx.needs_input_grad[0]:
+            v_means = None
+        elif sparse_grad:
+            v_means = sparse(v_means, means)
+        if not ctx.needs_input_grad[1]:
+            v_covars = None
+        elif sparse_grad:
+            v_covars = sparse(v_covars, covars)
+        if not ctx.needs_input_grad[2]:
+            v_quats = None
+        elif sparse_grad:
+            v_quats = sparse(v_quats, quats)
+        if not ctx.needs_input_grad[3]:
+            v_scales = None
+        elif sparse_grad:
+            v_scales = sparse(v_scales, scales)
+        if not ctx.needs_input_grad[4]:
+            v_viewmats = None
+        return (v_means, v_covars, v_quats, v_scales, v_viewmats,
+                None, None, None, None, None, None, None, None, None, None, None)
+
+
+class _SphericalHarmonics(torch.autograd.Function):
+    """Spherical harmonics colour evaluation."""
+
+    @staticmethod
+    def forward(ctx, sh_degree: int, dirs: Tensor, coeffs: Tensor, masks: Optional[Tensor]):
+        colors = _make_lazy_cuda_func("spherical_harmonics_fwd")(
+            sh_degree, dirs, coeffs, masks)
+        ctx.save_for_backward(dirs, coeffs, masks)
+        ctx.sh_degree = sh_degree
+        return colors
+
+    @staticmethod
+    def backward(ctx, v_colors: Tensor):
+        dirs, coeffs, masks = ctx.saved_tensors
+        compute_v_dirs = ctx.needs_input_grad[1]
+        v_coeffs, v_dirs = _make_lazy_cuda_func("spherical_harmonics_bwd")(
+            ctx.sh_degree, dirs, coeffs, masks, v_colors.contiguous(), compute_v_dirs)
+        if not compute_v_dirs:
+            v_dirs = None
+        return None, v_dirs, v_coeffs, None
+
+
+class _RasterizeToPixels(torch.autograd.Function):
+    """Tile rasterizer."""
+
+    @staticmethod
+    def forward(ctx, means2d, conics, colors, opacities, backgrounds, masks,
+                width, height, tile_size, isect_offsets, flatten_ids, absgrad):
+        render_colors, render_alphas, last_ids = _make_lazy_cuda_func(
+            "rasterize_to_pixels_3dgs_fwd"
+        )(means2d, conics, colors, opacities, backgrounds, masks, width, height,
+          tile_size, isect_offsets, flatten_ids)
+        ctx.save_for_backward(means2d, conics, colors, opacities, backgrounds,
+                              masks, isect_offsets, flatten_ids, render_alphas,
+                              last_ids)
+        ctx.width = width
+        ctx.height = height
+        ctx.tile_size = tile_size
+        ctx.absgrad = absgrad
+        return render_colors, render_alphas
+
+    @staticmethod
+    def backward(ctx, v_render_colors: Tensor, v_render_alphas: Tensor):
+        (means2d, conics, colors, opacities, backgrounds, masks, isect_offsets,
+         flatten_ids, render_alphas, last_ids) = ctx.saved_tensors
+        (v_means2d_abs, v_means2d, v_conics, v_colors,
+         v_opacities) = _make_lazy_cuda_func("rasterize_to_pixels_3dgs_bwd")(
+            means2d, conics, colors, opacities, backgrounds, masks, ctx.width,
+            ctx.height, ctx.tile_size, isect_offsets, flatten_ids, render_alphas,
+            last_ids, v_render_colors.contiguous(), v_render_alphas.contiguous(),
+            ctx.absgrad)
+        if ctx.absgrad:
+            prev = getattr(means2d, "absgrad", None)
+            if prev is not None and getattr(means2d, "_absgrad_pass", None) is \
+                    torch._C._current_graph_task_id():
+                v_means2d_abs = prev + v_means2d_abs
+            means2d.absgrad = v_means2d_abs
+            means2d._absgrad_pass = torch._C._current_graph_task_id()
+        if ctx.needs_input_grad[4]:
+            v_backgrounds = (v_render_colors * (1.0 - render_alphas).float()).sum(
+                dim=(-3, -2))
+        else:
+            v_backgrounds = None
+        return (v_means2d, v_conics, v_colors, v_opacities, v_backgrounds,
+                None, None, None, None, None, None, None)

@@ -1,0 +1,322 @@
+/*
+ * gsplat_hip.h -- C ABI of libgsplat_hip.so, the MI355X (gfx950) kernels of the
+ * differentiable 3D Gaussian splatting hot path.
+ *
+ * Conventions shared by every entry point:
+ *   - All tensor arguments are raw DEVICE pointers to contiguous, row-major
+ *     buffers; float means IEEE fp32, masks are one byte per element (0/1).
+ *   - Optional inputs/outputs are passed as NULL.
+ *   - The caller owns every allocation (outputs included).  Entry points that
+ *     need scratch memory take a `workspace` pointer whose size is returned by
+ *     the matching *_workspace_size() query; the library clears what it needs
+ *     inside the workspace itself, on `stream`.
+ *   - Work is enqueued on `stream` (a hipStream_t passed as void*; NULL is the
+ *     null stream).  Nothing synchronises the host unless stated.
+ *   - Every entry point returns GSPLAT_OK (0) or a negative error code; the
+ *     message of the last failure on the calling thread is available from
+ *     gsplat_last_error().  Argument errors are detected before anything is
+ *     enqueued.
+ *
+ * Each declaration names the reference interface it replaces (paths relative
+ * to the mc8max/gsplat 1.5.3 source tree).
+ */
+#ifndef GSPLAT_HIP_H
+#define GSPLAT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *gsplat_stream_t;
+
+enum {
+    GSPLAT_OK = 0,
+    GSPLAT_ERR_INVALID_ARGUMENT = -1,
+    GSPLAT_ERR_UNSUPPORTED = -2,
+    GSPLAT_ERR_LAUNCH = -3,
+    GSPLAT_ERR_WORKSPACE = -4,
+};
+
+/* Camera models; values match gsplat::CameraModelType
+ * (gsplat/cuda/include/Common.h:65-71, exposed as _C.CameraModelType,
+ * gsplat/cuda/ext.cpp:38-44).  PINHOLE and ORTHO are implemented. */
+enum {
+    GSPLAT_CAMERA_PINHOLE = 0,
+    GSPLAT_CAMERA_ORTHO = 1,
+    GSPLAT_CAMERA_FISHEYE = 2,
+};
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *gsplat_last_error(void);
+
+/* Library version string, e.g. "gsplat_hip 0.1.0 gfx950". */
+const char *gsplat_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Projection (EWA splatting of 3D Gaussians to 2D conics).                  */
+/* ------------------------------------------------------------------------ */
+
+/* Dense ("fused") projection of B*C*N rows.
+ * Replaces projection_ewa_3dgs_fused_fwd
+ *   (gsplat/cuda/csrc/Projection.cpp:129-200,
+ *    gsplat/cuda/csrc/ProjectionEWA3DGSFused.cu:38-312).
+ * Inputs : means [B,N,3]; either covars [B,N,6] (upper triangle) or
+ *          quats [B,N,4] + scales [B,N,3]; opacities [B,N] (optional, enables
+ *          the opacity-aware radius); viewmats [B,C,4,4]; Ks [B,C,3,3].
+ * Outputs: radii [B,C,N,2] int32 (0,0 for culled rows), means2d [B,C,N,2],
+ *          depths [B,C,N], conics [B,C,N,3], compensations [B,C,N] (optional;
+ *          non-NULL also folds the compensation into the opacity cull).
+ *          Culled rows get radii = 0 and zeros in every float output. */
+int gsplat_projection_fused_fwd(
+    int64_t B, int64_t C, int64_t N,
+    const float *means, const float *covars, const float *quats,
+    const float *scales, const float *opacities,
+    const float *viewmats, const float *Ks,
+    int32_t image_width, int32_t image_height,
+    float eps2d, float near_plane, float far_plane, float radius_clip,
+    int32_t camera_model,
+    int32_t *radii, float *means2d, float *depths, float *conics,
+    float *compensations,
+    gsplat_stream_t stream);
+
+/* Backward of the dense projection.
+ * Replaces projection_ewa_3dgs_fused_bwd
+ *   (gsplat/cuda/csrc/Projection.cpp:202-306,
+ *    gsplat/cuda/csrc/ProjectionEWA3DGSFused.cu:316-650).
+ * Gradients are OVERWRITTEN (not accumulated): v_means [B,N,3]; v_covars
+ * [B,N,6] or v_quats [B,N,4] + v_scales [B,N,3]; v_viewmats [B,C,4,4]
+ * (optional).  Each Gaussian is owned by one thread that loops over the C
+ * cameras, so no atomics are used and results are deterministic. */
+int gsplat_projection_fused_bwd(
+    int64_t B, int64_t C, int64_t N,
+    const float *means, const float *covars, const float *quats,
+    const float *scales, const float *viewmats, const float *Ks,
+    int32_t image_width, int32_t image_height, float eps2d,
+    int32_t camera_model,
+    const int32_t *radii, const float *conics, const float *compensations,
+    const float *v_means2d, const float *v_depths, const float *v_conics,
+    const float *v_compensations,
+    float *v_means, float *v_covars, float *v_quats, float *v_scales,
+    float *v_viewmats,
+    gsplat_stream_t stream);
+
+/* Bytes of workspace gsplat_projection_packed_fwd needs for B*C*N rows. */
+size_t gsplat_projection_packed_workspace_size(int64_t B, int64_t C, int64_t N);
+
+/* Packed projection in ONE pass: rows that survive culling are compacted in
+ * (b, c, g) row-major order with a decoupled look-back scan.
+ * Replaces projection_ewa_3dgs_packed_fwd, whose two passes + host sync this
+ * fuses (gsplat/cuda/csrc/Projection.cpp:308-437,
+ *        gsplat/cuda/csrc/ProjectionEWA3DGSPacked.cu:39-398).
+ * Every per-row output must have capacity for B*C*N rows; the number of rows
+ * written (nnz) is stored to nnz_out (device int64).  indptr [B*C+1] int32;
+ * batch_ids, camera_ids, gaussian_ids int64. */
+int gsplat_projection_packed_fwd(
+    int64_t B, int64_t C, int64_t N,
+    const float *means, const float *covars, const float *quats,
+    const float *scales, const float *opacities,
+    const float *viewmats, const float *Ks,
+    int32_t image_width, int32_t image_height,
+    float eps2d, float near_plane, float far_plane, float radius_clip,
+    int32_t camera_model,
+    void *workspace, size_t workspace_bytes,
+    int32_t *indptr, int64_t *batch_ids, int64_t *camera_ids,
+    int64_t *gaussian_ids, int32_t *radii, float *means2d, float *depths,
+    float *conics, float *compensations, int64_t *nnz_out,
+    gsplat_stream_t stream);
+
+/* Backward of the packed projection over nnz rows.
+ * Replaces projection_ewa_3dgs_packed_bwd
+ *   (gsplat/cuda/csrc/Projection.cpp:439-576,
+ *    gsplat/cuda/csrc/ProjectionEWA3DGSPacked.cu:400-783).
+ * sparse_grad != 0: v_means [nnz,3], v_covars [nnz,6] / v_quats [nnz,4] +
+ *   v_scales [nnz,3] are written row by row (no zero fill needed).
+ * sparse_grad == 0: the per-Gaussian outputs [B,N,*] must be zero-filled by
+ *   the caller; rows are accumulated with atomics unless B*C == 1, in which
+ *   case each Gaussian has at most one row and plain stores are used.
+ * v_viewmats [B,C,4,4] (optional) must be zero-filled by the caller. */
+int gsplat_projection_packed_bwd(
+    int64_t B, int64_t C, int64_t N, int64_t nnz,
+    const float *means, const float *covars, const float *quats,
+    const float *scales, const float *viewmats, const float *Ks,
+    int32_t image_width, int32_t image_height, float eps2d,
+    int32_t camera_model,
+    const int64_t *batch_ids, const int64_t *camera_ids,
+    const int64_t *gaussian_ids, const float *conics,
+    const float *compensations,
+    const float *v_means2d, const float *v_depths, const float *v_conics,
+    const float *v_compensations, int32_t sparse_grad,
+    float *v_means, float *v_covars, float *v_quats, float *v_scales,
+    float *v_viewmats,
+    gsplat_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Spherical harmonics (real SH, Sloan 2013 basis, degree 0..4).             */
+/* ------------------------------------------------------------------------ */
+
+/* Replaces spherical_harmonics_fwd
+ *   (gsplat/cuda/csrc/SphericalHarmonics.cpp:33-55,
+ *    gsplat/cuda/csrc/SphericalHarmonicsCUDA.cu:391-462).
+ * dirs [M,3] (need not be unit length), coeffs [M,K,3], masks [M] (optional),
+ * colors [M,3].  Masked-out rows are written as 0. */
+int gsplat_sh_fwd(
+    int64_t M, int32_t K, int32_t degree,
+    const float *dirs, const float *coeffs, const uint8_t *masks,
+    float *colors, gsplat_stream_t stream);
+
+/* Replaces spherical_harmonics_bwd
+ *   (gsplat/cuda/csrc/SphericalHarmonics.cpp:57-91,
+ *    gsplat/cuda/csrc/SphericalHarmonicsCUDA.cu:465-552).
+ * v_coeffs [M,K,3] is fully written (bands above `degree` and masked rows get
+ * 0, so no zero fill is needed); v_dirs [M,3] optional, fully written. */
+int gsplat_sh_bwd(
+    int64_t M, int32_t K, int32_t degree,
+    const float *dirs, const float *coeffs, const uint8_t *masks,
+    const float *v_colors, float *v_coeffs, float *v_dirs,
+    gsplat_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Tile intersection.                                                        */
+/* ------------------------------------------------------------------------ */
+
+/* Bytes of workspace gsplat_isect_count needs for n rows. */
+size_t gsplat_isect_count_workspace_size(int64_t n);
+
+/* Pass 1 of intersect_tile: tiles touched per row, plus the inclusive prefix
+ * sum of those counts (one pass, decoupled look-back).
+ * Replaces the first launch of intersect_tile_kernel and the at::cumsum in
+ *   gsplat/cuda/csrc/Intersect.cpp:80-104, kernel IntersectTile.cu:133-288.
+ * Rows: n = I*N (dense, image id = row / N) or nnz (packed, image_ids given).
+ * conics [n,3] + opacities [n] both non-NULL select the ellipse ("AccuTile")
+ * test, otherwise the axis-aligned box of `radii` is used.
+ * Outputs tiles_per_gauss [n] int32 and cum_tiles [n] int64 (inclusive). */
+int gsplat_isect_count(
+    int64_t n, int64_t N, const int64_t *image_ids,
+    const float *means2d, const int32_t *radii,
+    const float *conics, const float *opacities,
+    int32_t tile_size, int32_t tile_width, int32_t tile_height,
+    void *workspace, size_t workspace_bytes,
+    int32_t *tiles_per_gauss, int64_t *cum_tiles,
+    gsplat_stream_t stream);
+
+/* Pass 2 of intersect_tile: writes isect_ids [n_isects] (image|tile|depth
+ * bits) and flatten_ids [n_isects] in row order, each row at
+ * cum_tiles[row-1].  Same row/camera arguments as gsplat_isect_count.
+ * Replaces the second launch of intersect_tile_kernel
+ *   (gsplat/cuda/csrc/Intersect.cpp:118-143). */
+int gsplat_isect_emit(
+    int64_t n, int64_t N, int64_t I, const int64_t *image_ids,
+    const float *means2d, const int32_t *radii, const float *depths,
+    const float *conics, const float *opacities,
+    int32_t tile_size, int32_t tile_width, int32_t tile_height,
+    const int64_t *cum_tiles,
+    int64_t *isect_ids, int32_t *flatten_ids,
+    gsplat_stream_t stream);
+
+/* Bytes of workspace gsplat_sort_pairs_u64_u32 needs for n pairs. */
+size_t gsplat_sort_pairs_workspace_size(int64_t n);
+
+/* Stable LSD radix sort of (key, value) pairs on key bits [0, num_bits).
+ * Results land in keys_out/vals_out; the inputs are used as ping-pong
+ * buffers and are clobbered.  Replaces radix_sort_double_buffer
+ *   (gsplat/cuda/csrc/IntersectTile.cu:478-520, cub::DeviceRadixSort). */
+int gsplat_sort_pairs_u64_u32(
+    int64_t n, int32_t num_bits,
+    uint64_t *keys_in, uint32_t *vals_in,
+    uint64_t *keys_out, uint32_t *vals_out,
+    void *workspace, size_t workspace_bytes,
+    gsplat_stream_t stream);
+
+/* Tile start offsets: offsets[i*n_tiles + t] = #{k : isect_ids[k] >> 32 <
+ * (i << tile_n_bits | t)}; all zeros when n_isects == 0.
+ * Replaces intersect_offset (gsplat/cuda/csrc/Intersect.cpp:320-337,
+ *   kernel IntersectTile.cu:391-474). */
+int gsplat_isect_offsets(
+    int64_t n_isects, const int64_t *isect_ids, int64_t I,
+    int32_t tile_width, int32_t tile_height, int32_t *offsets,
+    gsplat_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Tile rasterizer.                                                          */
+/* ------------------------------------------------------------------------ */
+
+/* Front-to-back alpha compositing, one workgroup per tile.
+ * Replaces rasterize_to_pixels_3dgs_fwd
+ *   (gsplat/cuda/csrc/Rasterization.cpp:42-120,
+ *    gsplat/cuda/csrc/RasterizeToPixels3DGSFwd.cu:41-302).
+ * Rows: n_rows = I*N (dense) or nnz (packed); means2d [n,2], conics [n,3],
+ * colors [n,CDIM], opacities [n]; backgrounds [I,CDIM] and masks
+ * [I,tile_height,tile_width] optional; tile_offsets [I,th,tw];
+ * flatten_ids [n_isects].
+ * Outputs: render_colors [I,H,W,CDIM], render_alphas [I,H,W],
+ *          last_ids [I,H,W] int32.
+ * CDIM in {1,2,3,4,5,8,9,16,17,32,33}; tile_size in {4,8,16}. */
+int gsplat_rasterize_fwd(
+    int64_t I, int64_t n_rows, int64_t n_isects, int32_t cdim,
+    const float *means2d, const float *conics, const float *colors,
+    const float *opacities, const float *backgrounds, const uint8_t *masks,
+    int32_t image_width, int32_t image_height, int32_t tile_size,
+    int32_t tile_width, int32_t tile_height,
+    const int32_t *tile_offsets, const int32_t *flatten_ids,
+    float *render_colors, float *render_alphas, int32_t *last_ids,
+    gsplat_stream_t stream);
+
+/* Back-to-front replay of the compositing.
+ * Replaces rasterize_to_pixels_3dgs_bwd
+ *   (gsplat/cuda/csrc/Rasterization.cpp:122-214,
+ *    gsplat/cuda/csrc/RasterizeToPixels3DGSBwd.cu:39-412).
+ * Gradient outputs are ACCUMULATED and must be zero-filled by the caller:
+ * v_means2d [n,2], v_conics [n,3], v_colors [n,CDIM], v_opacities [n],
+ * v_means2d_abs [n,2] (optional; sum over pixels of |dL/dmean2d|). */
+int gsplat_rasterize_bwd(
+    int64_t I, int64_t n_rows, int64_t n_isects, int32_t cdim,
+    const float *means2d, const float *conics, const float *colors,
+    const float *opacities, const float *backgrounds, const uint8_t *masks,
+    int32_t image_width, int32_t image_height, int32_t tile_size,
+    int32_t tile_width, int32_t tile_height,
+    const int32_t *tile_offsets, const int32_t *flatten_ids,
+    const float *render_alphas, const int32_t *last_ids,
+    const float *v_render_colors, const float *v_render_alphas,
+    float *v_means2d_abs, float *v_means2d, float *v_conics,
+    float *v_colors, float *v_opacities,
+    gsplat_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Fused Adam (no bias correction, optional per-row mask).                   */
+/* ------------------------------------------------------------------------ */
+
+typedef struct gsplat_adam_tensor {
+    float *param;           /* [n_rows, row_size], updated in place */
+    const float *grad;      /* [n_rows, row_size] */
+    float *exp_avg;         /* [n_rows, row_size], updated in place */
+    float *exp_avg_sq;      /* [n_rows, row_size], updated in place */
+    const uint8_t *valid;   /* [n_rows] or NULL; rows with 0 are untouched */
+    int64_t n_rows;
+    int64_t row_size;
+    float lr;
+} gsplat_adam_tensor;
+
+/* One launch updating every tensor of the list (a single HBM pass).
+ * Replaces the per-tensor launches of adam_kernel issued by
+ *   gsplat/optimizers/selective_adam.py:63-101
+ *   (gsplat/cuda/csrc/Adam.cpp:37-66, AdamCUDA.cu:35-110).
+ * `tensors` is a HOST array; at most 64 entries. */
+int gsplat_adam_multi(
+    const gsplat_adam_tensor *tensors, int32_t n_tensors,
+    float b1, float b2, float eps, gsplat_stream_t stream);
+
+/* Single-tensor form with the reference op's argument list.
+ * Replaces the `adam` op (gsplat/cuda/ext.cpp:753, Adam.cpp:37-66). */
+int gsplat_adam(
+    float *param, const float *param_grad, float *exp_avg, float *exp_avg_sq,
+    const uint8_t *valid, int64_t n_rows, int64_t row_size,
+    float lr, float b1, float b2, float eps, gsplat_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GSPLAT_HIP_H */

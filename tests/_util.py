@@ -1,0 +1,85 @@
+"""Shared helpers for the parity tests."""
+
+import math
+
+import numpy as np
+import torch
+
+from gsplat_amd._helper import look_at_viewmat
+from oracle import exact
+
+DEV = "cuda:0"
+
+
+def small_scene(seed=0, N=2000, C=2, W=160, H=120, f=150.0, opac_range=(0.05, 1.0),
+                scale_range=(0.01, 0.12), spread=1.2):
+    """Random 3D Gaussians in front of C cameras (CPU float32 tensors)."""
+    g = torch.Generator().manual_seed(seed)
+    means = torch.randn(N, 3, generator=g) * spread
+    quats = torch.randn(N, 4, generator=g)
+    scales = torch.rand(N, 3, generator=g) * (scale_range[1] - scale_range[0]) + scale_range[0]
+    opac = torch.rand(N, generator=g) * (opac_range[1] - opac_range[0]) + opac_range[0]
+    vms = [look_at_viewmat((4 * math.sin(0.5 * k), -0.5, -4 * math.cos(0.5 * k)))
+           for k in range(C)]
+    vm = torch.stack(vms)
+    K = torch.tensor([[f, 0, W / 2], [0, f, H / 2], [0, 0, 1]]).expand(C, 3, 3).contiguous()
+    return means, quats, scales, opac, vm, K, W, H
+
+
+def projected_2d(seed=0, N=2000, C=2, W=160, H=120, tile=16, D=3, packed=False):
+    """Exact-oracle projection + intersection of a random scene: the float32
+    inputs of the rasterizer and its tile lists (numpy/torch CPU)."""
+    means, quats, scales, opac, vm, K, W, H = small_scene(seed, N, C, W, H)
+    ex = exact.projection_fwd(means.numpy(), None, quats.numpy(), scales.numpy(),
+                              opac.numpy(), vm.numpy(), K.numpy(), W, H)
+    g = torch.Generator().manual_seed(seed + 1)
+    colors = torch.rand(C, N, D, generator=g)
+    ops = np.broadcast_to(opac.numpy()[None], (C, N)).copy()
+    tw, th = math.ceil(W / tile), math.ceil(H / tile)
+    if packed:
+        valid = ex["valid"].reshape(-1)
+        rows = np.nonzero(valid)[0]
+        m2 = ex["means2d"].reshape(-1, 2)[rows]
+        con = ex["conics"].reshape(-1, 3)[rows]
+        dep = ex["depths"].reshape(-1)[rows]
+        rad = ex["radii"].reshape(-1, 2)[rows]
+        op = ops.reshape(-1)[rows]
+        col = colors.reshape(-1, D)[rows]
+        image_ids = (rows // N).astype(np.int64)
+        tpg, ids, fl = exact.isect_tiles(m2, rad, dep, tile, tw, th, packed=True,
+                                         n_images=C, image_ids=image_ids,
+                                         conics=con, opacities=op)
+    else:
+        m2, con, dep, rad, op, col = (ex["means2d"], ex["conics"], ex["depths"],
+                                      ex["radii"], ops, colors)
+        tpg, ids, fl = exact.isect_tiles(m2, rad, dep, tile, tw, th, conics=con,
+                                         opacities=op)
+    offs = exact.isect_offset_encode(ids, C, tw, th)
+    return {
+        "means2d": torch.from_numpy(np.ascontiguousarray(m2)),
+        "conics": torch.from_numpy(np.ascontiguousarray(con)),
+        "opacities": torch.from_numpy(np.ascontiguousarray(op)),
+        "colors": col.contiguous(),
+        "offsets": torch.from_numpy(offs),
+        "flatten_ids": torch.from_numpy(fl),
+        "W": W, "H": H, "tile": tile, "C": C,
+    }
+
+
+def report(a, b, name):
+    a = a.detach().double().cpu()
+    b = b.detach().double().cpu()
+    d = (a - b).abs()
+    rel = d / b.abs().clamp(min=1e-12)
+    return (f"{name}: max abs {d.max().item():.3e}, max rel {rel.max().item():.3e}, "
+            f"numel {a.numel()}")
+
+
+def assert_close(a, b, rtol, atol, name):
+    a = a.detach().double().cpu()
+    b = b.detach().double().cpu()
+    ok = (a - b).abs() <= atol + rtol * b.abs()
+    if not bool(ok.all()):
+        bad = (~ok).sum().item()
+        raise AssertionError(f"{report(a, b, name)}; {bad} elements outside "
+                             f"rtol={rtol} atol={atol}")

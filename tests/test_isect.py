@@ -1,0 +1,129 @@
+"""Tile intersection, radix sort and tile offsets on the GPU: bit-exact
+against the host oracle (reference test: tests/test_basic.py:698-736)."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import exact
+from tests._util import DEV
+
+pytestmark = pytest.mark.gpu
+
+
+def _compare(got, want):
+    for name, g, w in zip(("tiles_per_gauss", "isect_ids", "flatten_ids"), got, want):
+        np.testing.assert_array_equal(g.cpu().numpy(), w, err_msg=name)
+
+
+@pytest.mark.parametrize("batch_dims", [(), (2,), (1, 2)])
+def test_isect_box_reference_inputs(batch_dims):
+    """The reference's own test inputs: C=3, N=1000, 40x60 image, random radii."""
+    from gsplat_amd.cuda._wrapper import isect_offset_encode, isect_tiles
+    rng = np.random.default_rng(42)
+    C, N, W, H, ts = 3, 1000, 40, 60, 16
+    means2d = (rng.standard_normal((C, N, 2)) * W).astype(np.float32)
+    radii = rng.integers(0, W, (C, N, 2)).astype(np.int32)
+    depths = rng.random((C, N)).astype(np.float32)
+    if batch_dims:
+        reps = int(np.prod(batch_dims))
+        means2d = np.broadcast_to(means2d, batch_dims + means2d.shape).copy()
+        radii = np.broadcast_to(radii, batch_dims + radii.shape).copy()
+        depths = np.broadcast_to(depths, batch_dims + depths.shape).copy()
+    I = means2d.size // (N * 2)
+    tw, th = math.ceil(W / ts), math.ceil(H / ts)
+    got = isect_tiles(torch.from_numpy(means2d).to(DEV), torch.from_numpy(radii).to(DEV),
+                      torch.from_numpy(depths).to(DEV), ts, tw, th)
+    want = exact.isect_tiles_box_python(means2d, radii, depths, ts, tw, th)
+    _compare(got, want)
+    offs = isect_offset_encode(got[1], I, tw, th)
+    np.testing.assert_array_equal(offs.cpu().numpy(),
+                                  exact.isect_offset_encode(want[1], I, tw, th))
+
+
+@pytest.mark.parametrize("packed", [False, True])
+@pytest.mark.parametrize("accutile", [False, True])
+def test_isect_projected_scene(packed, accutile):
+    from gsplat_amd.cuda._wrapper import isect_offset_encode, isect_tiles
+    from tests._util import small_scene
+    means, quats, scales, opac, vm, K, W, H = small_scene(seed=5, N=20000, C=3, W=320, H=200)
+    ex = exact.projection_fwd(means.numpy(), None, quats.numpy(), scales.numpy(),
+                              opac.numpy(), vm.numpy(), K.numpy(), W, H)
+    C, N = 3, means.shape[0]
+    ts = 16
+    tw, th = math.ceil(W / ts), math.ceil(H / ts)
+    ops = np.broadcast_to(opac.numpy()[None], (C, N)).copy()
+    if packed:
+        rows = np.nonzero(ex["valid"].reshape(-1))[0]
+        m2 = ex["means2d"].reshape(-1, 2)[rows]
+        rad = ex["radii"].reshape(-1, 2)[rows]
+        dep = ex["depths"].reshape(-1)[rows]
+        con = ex["conics"].reshape(-1, 3)[rows]
+        op = ops.reshape(-1)[rows]
+        iid = (rows // N).astype(np.int64)
+        gid = (rows % N).astype(np.int64)
+        kw = dict(conics=con, opacities=op) if accutile else {}
+        want = exact.isect_tiles(m2, rad, dep, ts, tw, th, packed=True, n_images=C,
+                                 image_ids=iid, **kw)
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+        got = isect_tiles(t(m2), t(rad), t(dep), ts, tw, th, packed=True, n_images=C,
+                          image_ids=t(iid), gaussian_ids=t(gid),
+                          conics=t(con) if accutile else None,
+                          opacities=t(op) if accutile else None)
+    else:
+        kw = dict(conics=ex["conics"], opacities=ops) if accutile else {}
+        want = exact.isect_tiles(ex["means2d"], ex["radii"], ex["depths"], ts, tw, th, **kw)
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+        got = isect_tiles(t(ex["means2d"]), t(ex["radii"]), t(ex["depths"]), ts, tw, th,
+                          conics=t(ex["conics"]) if accutile else None,
+                          opacities=t(ops) if accutile else None)
+    assert want[1].shape[0] > 1000
+    _compare(got, want)
+    offs = isect_offset_encode(got[1], C, tw, th)
+    np.testing.assert_array_equal(offs.cpu().numpy(), exact.isect_offset_encode(want[1], C, tw, th))
+
+
+def test_isect_unsorted_emission_order():
+    from gsplat_amd.cuda._wrapper import isect_tiles
+    from tests._util import small_scene
+    means, quats, scales, opac, vm, K, W, H = small_scene(seed=6, N=3000, C=1)
+    ex = exact.projection_fwd(means.numpy(), None, quats.numpy(), scales.numpy(),
+                              opac.numpy(), vm.numpy(), K.numpy(), W, H)
+    want = exact.isect_tiles(ex["means2d"], ex["radii"], ex["depths"], 16, 10, 8, sort=False,
+                             conics=ex["conics"], opacities=opac.numpy()[None])
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    got = isect_tiles(t(ex["means2d"]), t(ex["radii"]), t(ex["depths"]), 16, 10, 8,
+                      sort=False, conics=t(ex["conics"]), opacities=t(opac.numpy()[None]))
+    _compare(got, want)
+
+
+@pytest.mark.parametrize("n", [1, 100, 4096, 4097, 300_001])
+@pytest.mark.parametrize("bits", [8, 13, 37, 45, 47, 64])
+def test_radix_sort_pairs_stable(n, bits):
+    from gsplat_amd import _lib
+    rng = np.random.default_rng(n + bits)
+    hi = np.uint64((1 << bits) - 1) if bits < 64 else np.uint64(0xFFFFFFFFFFFFFFFF)
+    keys = rng.integers(0, 2 ** 63, n, dtype=np.int64).astype(np.uint64) * np.uint64(2) \
+        + rng.integers(0, 2, n).astype(np.uint64)
+    keys &= hi
+    # many duplicates to exercise stability
+    keys[rng.random(n) < 0.3] = keys[0]
+    vals = np.arange(n, dtype=np.uint32)
+    kd = torch.from_numpy(keys.view(np.int64)).to(DEV)
+    vd = torch.from_numpy(vals.view(np.int32)).to(DEV)
+    ko, vo = torch.empty_like(kd), torch.empty_like(vd)
+    ws = torch.empty(_lib.query("gsplat_sort_pairs_workspace_size", n), dtype=torch.uint8,
+                     device=DEV)
+    _lib.call("gsplat_sort_pairs_u64_u32", n, bits, kd.data_ptr(), vd.data_ptr(),
+              ko.data_ptr(), vo.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream())
+    order = np.argsort(keys, kind="stable")
+    np.testing.assert_array_equal(ko.cpu().numpy().view(np.uint64), keys[order])
+    np.testing.assert_array_equal(vo.cpu().numpy().view(np.uint32), vals[order])
+
+
+def test_offsets_empty_and_zero_isects():
+    from gsplat_amd.cuda._wrapper import isect_offset_encode
+    offs = isect_offset_encode(torch.empty(0, dtype=torch.int64, device=DEV), 2, 5, 4)
+    assert offs.shape == (2, 4, 5) and int(offs.abs().sum()) == 0

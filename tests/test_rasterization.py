@@ -1,0 +1,96 @@
+"""End-to-end ``rasterization()`` (gsplat/rendering.py:256-1273) on the GPU
+against the host oracle pipeline, forward and backward, at reduced sizes of
+the benchmark configurations (reference test: tests/test_rasterization.py).
+
+The oracle takes the integer decisions (visible rows, tile lists, sorted
+order, composited pairs) from the bit-exact restatement and the values and
+gradients from the float64 PyTorch restatement; integer outputs must match
+exactly, floats within rtol 1e-4 / atol 1e-5."""
+
+import numpy as np
+import pytest
+import torch
+
+from gsplat_amd._helper import make_scene
+from oracle import torch_ref
+from tests._util import DEV, assert_close
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-4, 1e-5
+
+
+def _check(scene, packed=True, rasterize_mode="classic", render_mode="RGB", bg=False):
+    import gsplat_amd as gs
+    g = torch.Generator().manual_seed(99)
+    C = scene.viewmats.shape[0]
+    backgrounds = torch.rand(C, 3, generator=g) if bg else None
+    leaves = {k: getattr(scene, k).clone() for k in ("means", "quats", "scales", "opacities", "colors")}
+    sh = scene.sh_degree
+    kw = dict(scene.kwargs)
+    kw["render_mode"] = render_mode
+    # oracle
+    ref_leaves = {k: v.double().requires_grad_() for k, v in leaves.items()}
+    rc_r, ra_r, meta_r = torch_ref.rasterization_ref(
+        ref_leaves["means"], ref_leaves["quats"], ref_leaves["scales"],
+        ref_leaves["opacities"], ref_leaves["colors"], scene.viewmats, scene.Ks,
+        scene.width, scene.height, sh_degree=sh, packed=packed,
+        rasterize_mode=rasterize_mode, backgrounds=backgrounds,
+        near_plane=kw.get("near_plane", 0.01), far_plane=kw.get("far_plane", 1e10),
+        render_mode=render_mode)
+    amb = torch.from_numpy(meta_r["ambiguous"])
+    assert amb.float().mean() < 2e-3, int(amb.sum())
+    keep = ~amb
+    D = rc_r.shape[-1]
+    v_rc = torch.randn(rc_r.shape, generator=g) * keep[..., None]
+    v_ra = torch.randn(ra_r.shape, generator=g) * keep[..., None]
+    ((rc_r * v_rc.double()).sum() + (ra_r * v_ra.double()).sum()).backward()
+
+    gl = {k: v.to(DEV).requires_grad_() for k, v in leaves.items()}
+    rc, ra, meta = gs.rasterization(
+        gl["means"], gl["quats"], gl["scales"], gl["opacities"], gl["colors"],
+        scene.viewmats.to(DEV), scene.Ks.to(DEV), scene.width, scene.height,
+        sh_degree=sh, packed=packed, rasterize_mode=rasterize_mode,
+        backgrounds=None if backgrounds is None else backgrounds.to(DEV), **kw)
+    ((rc * v_rc.to(DEV)).sum() + (ra * v_ra.to(DEV)).sum()).backward()
+
+    # integer outputs: bit-exact
+    np.testing.assert_array_equal(meta["isect_ids"].cpu().numpy(), meta_r["isect_ids"])
+    np.testing.assert_array_equal(meta["flatten_ids"].cpu().numpy(), meta_r["flatten_ids"])
+    np.testing.assert_array_equal(meta["isect_offsets"].cpu().numpy().reshape(-1),
+                                  meta_r["offsets"].reshape(-1))
+    # float outputs
+    assert_close(rc.cpu()[keep], rc_r.detach()[keep], RTOL, ATOL, "render_colors")
+    assert_close(ra.cpu()[keep], ra_r.detach()[keep], RTOL, ATOL, "render_alphas")
+    for k in leaves:
+        assert_close(gl[k].grad, ref_leaves[k].grad, RTOL, ATOL, f"d{k}")
+
+
+def test_cfg0_toy_packed():
+    _check(make_scene(0))
+
+
+def test_cfg0_toy_unpacked_antialiased_bg():
+    _check(make_scene(0), packed=False, rasterize_mode="antialiased", bg=True)
+
+
+def _downscale(scene, k):
+    """Same scene at 1/k resolution (focal lengths and principal points
+    scaled), to bound the oracle's run time."""
+    scene.width //= k
+    scene.height //= k
+    scene.Ks = scene.Ks.clone()
+    scene.Ks[:, :2, :] /= k
+    return scene
+
+
+def test_cfg1_reduced_sh3():
+    _check(_downscale(make_scene(1, n=40_000), 2))
+
+
+def test_cfg1_reduced_sh3_unpacked():
+    _check(_downscale(make_scene(1, n=20_000), 4), packed=False)
+
+
+def test_cfg2_reduced_multiview_rgb_ed():
+    _check(_downscale(make_scene(2, n=20_000), 4), render_mode="RGB+ED")
