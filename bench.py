@@ -176,8 +176,12 @@ def _measured_traffic(kernel):
 
 def _cpu_baseline(config, stride):
     """Oracle pipeline on the host: full projection / SH / intersection for all
-    Gaussians, rasterization on every `stride`-th tile, fwd+bwd; the raster
-    share is scaled by `stride`."""
+    Gaussians plus rasterization on a strided sample of the tiles, fwd+bwd.
+
+    Two samples are timed (every `stride`-th and every `2*stride`-th tile);
+    the per-tile raster cost is their difference over the tile-count
+    difference, and the full-image step is the fixed part plus that per-tile
+    cost times the number of tiles."""
     import torch
 
     from gsplat_amd._helper import make_scene
@@ -203,19 +207,23 @@ def _cpu_baseline(config, stride):
         loss.backward()
         return time.perf_counter() - t
 
-    sample = list(range(0, n_tiles, stride))
-    t_zero = run([])
-    t_sample = run(sample)
-    est = t_zero + (t_sample - t_zero) * (n_tiles / len(sample))
+    sample_a = list(range(0, n_tiles, stride))
+    sample_b = list(range(0, n_tiles, 2 * stride))
+    t_b = run(sample_b)
+    t_a = run(sample_a)
+    per_tile = max(0.0, (t_a - t_b) / max(1, len(sample_a) - len(sample_b)))
+    fixed = max(0.0, t_b - per_tile * len(sample_b))
+    est = fixed + per_tile * n_tiles
     return {
         "value": round(est * 1e3, 1),
         "unit": "ms/step",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"config {config}: projection+SH+intersection+sort for all "
-                   f"{scene.means.shape[0]} Gaussians, rasterize fwd+bwd on {len(sample)} "
-                   f"of {n_tiles} tiles (every {stride}th), raster time x{n_tiles / len(sample):.1f}; "
-                   f"measured {t_zero:.1f}s + {t_sample:.1f}s"),
+        "sample": (f"config {config}: oracle fwd+bwd with projection+SH+intersection for all "
+                   f"{scene.means.shape[0]} Gaussians and rasterization on {len(sample_b)} "
+                   f"then {len(sample_a)} of {n_tiles} tiles (strided); took "
+                   f"{t_b:.1f}s / {t_a:.1f}s -> fixed {fixed:.1f}s + "
+                   f"{per_tile * 1e3:.1f} ms/tile x {n_tiles} tiles"),
     }
 
 
