@@ -43,7 +43,26 @@ def _parse():
                     help="rasterize every k-th tile in the CPU baseline (0: auto)")
     ap.add_argument("--stages-only", action="store_true",
                     help="print the per-stage breakdown and exit")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a device-to-device copy of 256 MiB x 10 (the "
+                         "reference kernel for scaling rocprofv3 FETCH_SIZE / "
+                         "WRITE_SIZE counters to bytes)")
     return ap.parse_args()
+
+
+def _copy_calibration():
+    """A plain copy of known size: 256 MiB read + 256 MiB written per launch."""
+    import torch
+
+    n = 64 * 1024 * 1024  # float32 elements = 256 MiB
+    src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration": {"bytes_read_per_launch": n * 4,
+                                           "bytes_written_per_launch": n * 4,
+                                           "launches": 10}}))
 
 
 def _algorithmic_bytes(name, ctx):
@@ -54,7 +73,7 @@ def _algorithmic_bytes(name, ctx):
     K = ctx["K"]
     gauss2d = 8 + 12 + 4 + F32 * D  # means2d, conic, opacity, colour
     if name == "gsplat_rasterize_fwd":
-        return n_isects * (4 + gauss2d) + tiles * 4 + pix * (F32 * D + 4 + 4)
+        return n_isects * (4 + gauss2d) + tiles * 4 + pix * (F32 * D + 4 + 4 + 4)
     if name == "gsplat_rasterize_bwd":
         return (n_isects * (4 + gauss2d) + tiles * 4 + pix * (4 + 4 + F32 * D + 4)
                 + nnz * (8 + 12 + F32 * D + 4))
@@ -140,7 +159,7 @@ def _gpu_bench(args):
         achieved = abytes / (dom_avg * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
-                    "traffic": _measured_traffic(dominant),
+                    "traffic": _measured_traffic(dominant, args.config),
                     "kernel": dominant, "avg_ms": round(dom_avg, 4),
                     "algorithmic_bytes": int(abytes)}
     stage_report = {}
@@ -159,18 +178,18 @@ def _gpu_bench(args):
     }
 
 
-def _measured_traffic(kernel):
-    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
-    f = ROOT / "profiles" / "pmc_traffic.txt"
+def _measured_traffic(kernel, config):
+    """HBM bytes per launch of an entry point's kernel, from the committed
+    rocprofv3 PMC summary of the same workload (FETCH_SIZE and WRITE_SIZE
+    scaled by a plain copy kernel; profiles/cfg1_step_pmc_traffic.txt), or
+    None where no such measurement is committed."""
+    f = ROOT / "profiles" / f"cfg{config}_step_pmc_traffic.txt"
     if not f.exists():
         return None
     for line in f.read_text().splitlines():
         parts = line.split()
-        if len(parts) >= 2 and parts[0] == kernel:
-            try:
-                return int(float(parts[1]))
-            except ValueError:
-                return None
+        if len(parts) == 3 and parts[0] == "traffic" and parts[1] == kernel:
+            return int(parts[2])
     return None
 
 
@@ -234,6 +253,9 @@ def main():
         print(json.dumps({"error": "bench.py runs on exactly one GPU: this build has no "
                           "multi-GPU path (one-GPU boxes only); run with --gpus 1"}))
         sys.exit(2)
+    if args.copy_calibration:
+        _copy_calibration()
+        return
     res = _gpu_bench(args)
     if args.stages_only:
         print(json.dumps(res["stages"], indent=1))

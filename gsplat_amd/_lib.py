@@ -57,11 +57,11 @@ _SIGNATURES = {
     "gsplat_isect_offsets": [c_int64, _P, c_int64, c_int32, c_int32, _P, _P],
     "gsplat_rasterize_fwd": [
         c_int64, c_int64, c_int64, c_int32, _P, _P, _P, _P, _P, _P,
-        c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P],
+        c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P, _P],
     "gsplat_rasterize_bwd": [
         c_int64, c_int64, c_int64, c_int32, _P, _P, _P, _P, _P, _P,
         c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P,
-        _P, _P, _P, _P, _P, _P],
+        _P, _P, _P, _P, _P, _P, _P],
     "gsplat_adam_multi": [_P, c_int32, c_float, c_float, c_float, _P],
     "gsplat_adam": [
         _P, _P, _P, _P, _P, c_int64, c_int64, c_float, c_float, c_float,

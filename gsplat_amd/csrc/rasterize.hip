@@ -24,7 +24,8 @@
 // The forward ends a batch early when every pixel of the wave is done (the
 // per-lane loop exits when the wave's exec mask empties) and skips remaining
 // batches once the whole tile is done (__syncthreads_count).
-// The backward reduces each Gaussian's gradient over the wave with DPP row
+// The backward recovers T with a double-precision division per Gaussian and
+// reduces each Gaussian's gradient over the wave with DPP row
 // operations, accumulates the 4 waves in LDS (native ds_add_f32) and issues
 // one global atomic per value per Gaussian per TILE, 8x fewer than one per
 // 32-lane warp.
@@ -79,7 +80,8 @@ template <int CDIM>
 __global__ void __launch_bounds__(kMaxTileThreads) rasterize_fwd_kernel(const RasterArgs a,
                                      float *__restrict__ render_colors,
                                      float *__restrict__ render_alphas,
-                                     int32_t *__restrict__ last_ids) {
+                                     int32_t *__restrict__ last_ids,
+                                     float *__restrict__ render_T) {
     extern __shared__ float4 s_mem[];
     const int bs = blockDim.x;  // tile_size^2
     float4 *s_geo = s_mem;              // (x, y, opacity, sig_max)
@@ -105,6 +107,8 @@ __global__ void __launch_bounds__(kMaxTileThreads) rasterize_fwd_kernel(const Ra
                     a.backgrounds ? a.backgrounds[image * CDIM + k] : 0.f;
             render_alphas[pix] = 0.f;
             last_ids[pix] = 0;
+            if (render_T != nullptr)
+                render_T[pix] = 1.f;
         }
         return;
     }
@@ -174,6 +178,8 @@ __global__ void __launch_bounds__(kMaxTileThreads) rasterize_fwd_kernel(const Ra
                 a.backgrounds ? acc[k] + T * a.backgrounds[image * CDIM + k]
                               : acc[k];
         last_ids[pix] = cur_idx;
+        if (render_T != nullptr)
+            render_T[pix] = T;
     }
 }
 
@@ -186,6 +192,7 @@ template <int CDIM> struct BwdAcc {
 template <int CDIM>
 __global__ void __launch_bounds__(kMaxTileThreads) rasterize_bwd_kernel(const RasterArgs a,
                                      const float *__restrict__ render_alphas,
+                                     const float *__restrict__ render_T,
                                      const int32_t *__restrict__ last_ids,
                                      const float *__restrict__ v_render_colors,
                                      const float *__restrict__ v_render_alphas,
@@ -225,7 +232,17 @@ __global__ void __launch_bounds__(kMaxTileThreads) rasterize_bwd_kernel(const Ra
                                   : offs[tile + 1];
     const int num_batches = (range_end - range_start + bs - 1) / bs;
 
-    const float T_final = inside ? 1.f - render_alphas[pix] : 1.f;
+    // The transmittance itself when the forward stored it: 1 - (1 - T)
+    // loses most of T's significant bits once T nears the 1e-4 cutoff.
+    const float T_final =
+        inside ? (render_T != nullptr ? render_T[pix] : 1.f - render_alphas[pix])
+               : 1.f;
+    // T before each Gaussian is recovered back to front by undoing the
+    // forward's products.  The division runs in double: each step then undoes
+    // one float32 product (the same float32 1 - alpha the forward used) almost
+    // exactly, so T carries only the forward's own rounding instead of one
+    // extra float32 rounding per Gaussian behind it.
+    double T64 = (double)T_final;
     float T = T_final;
     const int32_t bin_final = inside ? last_ids[pix] : -1;
     float v_c[CDIM], buffer[CDIM];
@@ -291,8 +308,10 @@ __global__ void __launch_bounds__(kMaxTileThreads) rasterize_bwd_kernel(const Ra
                 vis = __builtin_amdgcn_exp2f(-sigma * kLog2e);
                 const bool clamped = sigma < con.w;
                 alpha = clamped ? kMaxAlpha : geo.z * vis;
-                const float ra = 1.f / fmaxf(kMinOneMinusAlpha, 1.f - alpha);
-                T *= ra;
+                const float one_minus = fmaxf(kMinOneMinusAlpha, 1.f - alpha);
+                const float ra = 1.f / one_minus;
+                T64 = T64 / (double)one_minus;
+                T = (float)T64;
                 const float fac = alpha * T;
                 float v_alpha = 0.f;
 #pragma unroll
@@ -413,7 +432,7 @@ extern "C" int gsplat_rasterize_fwd(
     int32_t image_width, int32_t image_height, int32_t tile_size,
     int32_t tile_width, int32_t tile_height, const int32_t *tile_offsets,
     const int32_t *flatten_ids, float *render_colors, float *render_alphas,
-    int32_t *last_ids, gsplat_stream_t stream) {
+    int32_t *last_ids, float *render_transmittance, gsplat_stream_t stream) {
     clear_error();
     RasterArgs a{I, n_rows, n_isects, means2d, conics, colors, opacities,
                  backgrounds, masks, image_width, image_height, tile_size,
@@ -430,7 +449,7 @@ extern "C" int gsplat_rasterize_fwd(
     const size_t smem = fwd_smem(bs, cdim);
 #define GS_FWD(C)                                                              \
     rasterize_fwd_kernel<C><<<(unsigned)blocks, bs, smem, st>>>(               \
-        a, render_colors, render_alphas, last_ids)
+        a, render_colors, render_alphas, last_ids, render_transmittance)
     GS_CDIM_SWITCH(cdim, GS_FWD)
 #undef GS_FWD
     return check_launch("rasterize_fwd_kernel");
@@ -443,7 +462,8 @@ extern "C" int gsplat_rasterize_bwd(
     int32_t image_width, int32_t image_height, int32_t tile_size,
     int32_t tile_width, int32_t tile_height, const int32_t *tile_offsets,
     const int32_t *flatten_ids, const float *render_alphas,
-    const int32_t *last_ids, const float *v_render_colors,
+    const float *render_transmittance, const int32_t *last_ids,
+    const float *v_render_colors,
     const float *v_render_alphas, float *v_means2d_abs, float *v_means2d,
     float *v_conics, float *v_colors, float *v_opacities,
     gsplat_stream_t stream) {
@@ -454,7 +474,8 @@ extern "C" int gsplat_rasterize_bwd(
     GS_TRY(check_raster(a, cdim));
     if (I == 0 || n_isects == 0)
         return GSPLAT_OK;
-    GS_REQUIRE(render_alphas && last_ids && v_render_colors && v_render_alphas,
+    GS_REQUIRE((render_alphas || render_transmittance) && last_ids &&
+                   v_render_colors && v_render_alphas,
                "rasterize_bwd: NULL input");
     GS_REQUIRE(v_means2d && v_conics && v_colors && v_opacities,
                "rasterize_bwd: NULL gradient output");
@@ -465,7 +486,8 @@ extern "C" int gsplat_rasterize_bwd(
     const size_t smem = bwd_smem(bs, cdim);
 #define GS_BWD(C)                                                              \
     rasterize_bwd_kernel<C><<<(unsigned)blocks, bs, smem, st>>>(               \
-        a, render_alphas, last_ids, v_render_colors, v_render_alphas,          \
+        a, render_alphas, render_transmittance, last_ids, v_render_colors,     \
+        v_render_alphas,                                                       \
         v_means2d_abs, v_means2d, v_conics, v_colors, v_opacities)
     GS_CDIM_SWITCH(cdim, GS_BWD)
 #undef GS_BWD

@@ -399,6 +399,40 @@ def _raster_common(means2d, conics, colors, opacities, backgrounds, masks,
     return image_dims, I, n_rows, tile_width, tile_height
 
 
+def rasterize_fwd_with_transmittance(
+    means2d: Tensor,
+    conics: Tensor,
+    colors: Tensor,
+    opacities: Tensor,
+    backgrounds: Optional[Tensor],
+    masks: Optional[Tensor],
+    image_width: int,
+    image_height: int,
+    tile_size: int,
+    tile_offsets: Tensor,
+    flatten_ids: Tensor,
+) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Forward rasterizer that also returns the final transmittance T of every
+    pixel ([..., H, W] float32); the autograd wrapper hands T to the backward
+    instead of re-deriving it as 1 - alpha."""
+    image_dims, I, n_rows, tw, th = _raster_common(
+        means2d, conics, colors, opacities, backgrounds, masks, tile_offsets,
+        flatten_ids)
+    channels = colors.shape[-1]
+    dev = means2d.device
+    H, W = int(image_height), int(image_width)
+    renders = torch.empty(image_dims + (H, W, channels), dtype=_F32, device=dev)
+    alphas = torch.empty(image_dims + (H, W, 1), dtype=_F32, device=dev)
+    last_ids = torch.empty(image_dims + (H, W), dtype=_I32, device=dev)
+    transmittance = torch.empty(image_dims + (H, W), dtype=_F32, device=dev)
+    call("gsplat_rasterize_fwd", I, n_rows, flatten_ids.numel(), channels,
+         ptr(means2d), ptr(conics), ptr(colors), ptr(opacities),
+         ptr(backgrounds), ptr(masks), W, H, int(tile_size), tw, th,
+         ptr(tile_offsets), ptr(flatten_ids), ptr(renders), ptr(alphas),
+         ptr(last_ids), ptr(transmittance), _stream(means2d))
+    return renders, alphas, last_ids, transmittance
+
+
 def rasterize_to_pixels_3dgs_fwd(
     means2d: Tensor,
     conics: Tensor,
@@ -425,7 +459,7 @@ def rasterize_to_pixels_3dgs_fwd(
          ptr(means2d), ptr(conics), ptr(colors), ptr(opacities),
          ptr(backgrounds), ptr(masks), W, H, int(tile_size), tw, th,
          ptr(tile_offsets), ptr(flatten_ids), ptr(renders), ptr(alphas),
-         ptr(last_ids), _stream(means2d))
+         ptr(last_ids), None, _stream(means2d))
     return renders, alphas, last_ids
 
 
@@ -446,7 +480,10 @@ def rasterize_to_pixels_3dgs_bwd(
     v_render_colors: Tensor,
     v_render_alphas: Tensor,
     absgrad: bool,
+    render_transmittance: Optional[Tensor] = None,
 ):
+    """``render_transmittance`` (not part of the reference schema) is the
+    forward's per-pixel T; without it T is taken as 1 - render_alphas."""
     image_dims, I, n_rows, tw, th = _raster_common(
         means2d, conics, colors, opacities, backgrounds, masks, tile_offsets,
         flatten_ids)
@@ -454,6 +491,7 @@ def rasterize_to_pixels_3dgs_bwd(
     check_input(last_ids, "last_ids", _I32)
     check_input(v_render_colors, "v_render_colors", _F32)
     check_input(v_render_alphas, "v_render_alphas", _F32)
+    check_input(render_transmittance, "render_transmittance", _F32)
     channels = colors.shape[-1]
     v_means2d = torch.zeros_like(means2d)
     v_conics = torch.zeros_like(conics)
@@ -464,7 +502,8 @@ def rasterize_to_pixels_3dgs_bwd(
          ptr(means2d), ptr(conics), ptr(colors), ptr(opacities),
          ptr(backgrounds), ptr(masks), int(image_width), int(image_height),
          int(tile_size), tw, th, ptr(tile_offsets), ptr(flatten_ids),
-         ptr(render_alphas), ptr(last_ids), ptr(v_render_colors),
+         ptr(render_alphas), ptr(render_transmittance), ptr(last_ids),
+         ptr(v_render_colors),
          ptr(v_render_alphas), ptr(v_means2d_abs), ptr(v_means2d),
          ptr(v_conics), ptr(v_colors), ptr(v_opacities), _stream(means2d))
     return v_means2d_abs, v_means2d, v_conics, v_colors, v_opacities

@@ -533,12 +533,12 @@ class _RasterizeToPixels(torch.autograd.Function):
     @staticmethod
     def forward(ctx, means2d, conics, colors, opacities, backgrounds, masks,
                 width, height, tile_size, isect_offsets, flatten_ids, absgrad):
-        render_colors, render_alphas, last_ids = _make_lazy_cuda_func(
-            "rasterize_to_pixels_3dgs_fwd"
-        )(means2d, conics, colors, opacities, backgrounds, masks, width, height,
-          tile_size, isect_offsets, flatten_ids)
+        render_colors, render_alphas, last_ids, render_T = \
+            _ops.rasterize_fwd_with_transmittance(
+                means2d, conics, colors, opacities, backgrounds, masks, width,
+                height, tile_size, isect_offsets, flatten_ids)
         ctx.save_for_backward(means2d, conics, colors, opacities, backgrounds,
-                              masks, isect_offsets, flatten_ids, render_alphas,
+                              masks, isect_offsets, flatten_ids, render_T,
                               last_ids)
         ctx.width = width
         ctx.height = height
@@ -549,13 +549,16 @@ class _RasterizeToPixels(torch.autograd.Function):
     @staticmethod
     def backward(ctx, v_render_colors: Tensor, v_render_alphas: Tensor):
         (means2d, conics, colors, opacities, backgrounds, masks, isect_offsets,
-         flatten_ids, render_alphas, last_ids) = ctx.saved_tensors
+         flatten_ids, render_T, last_ids) = ctx.saved_tensors
+        # render_alphas = 1 - T is only needed when T is absent; pass T's
+        # storage as the (unused) alphas argument to satisfy the op's checks.
         (v_means2d_abs, v_means2d, v_conics, v_colors,
-         v_opacities) = _make_lazy_cuda_func("rasterize_to_pixels_3dgs_bwd")(
+         v_opacities) = _ops.rasterize_to_pixels_3dgs_bwd(
             means2d, conics, colors, opacities, backgrounds, masks, ctx.width,
-            ctx.height, ctx.tile_size, isect_offsets, flatten_ids, render_alphas,
-            last_ids, v_render_colors.contiguous(), v_render_alphas.contiguous(),
-            ctx.absgrad)
+            ctx.height, ctx.tile_size, isect_offsets, flatten_ids,
+            render_T, last_ids, v_render_colors.contiguous(),
+            v_render_alphas.contiguous(), ctx.absgrad,
+            render_transmittance=render_T)
         if ctx.absgrad:
             prev = getattr(means2d, "absgrad", None)
             if prev is not None and getattr(means2d, "_absgrad_pass", None) is \
@@ -564,7 +567,7 @@ class _RasterizeToPixels(torch.autograd.Function):
             means2d.absgrad = v_means2d_abs
             means2d._absgrad_pass = torch._C._current_graph_task_id()
         if ctx.needs_input_grad[4]:
-            v_backgrounds = (v_render_colors * (1.0 - render_alphas).float()).sum(
+            v_backgrounds = (v_render_colors * render_T[..., None]).sum(
                 dim=(-3, -2))
         else:
             v_backgrounds = None

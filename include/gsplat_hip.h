@@ -252,7 +252,9 @@ int gsplat_isect_offsets(
  * [I,tile_height,tile_width] optional; tile_offsets [I,th,tw];
  * flatten_ids [n_isects].
  * Outputs: render_colors [I,H,W,CDIM], render_alphas [I,H,W],
- *          last_ids [I,H,W] int32.
+ *          last_ids [I,H,W] int32, render_transmittance [I,H,W] (optional:
+ *          the final transmittance T = 1 - alpha of each pixel, kept at full
+ *          precision for the backward).
  * CDIM in {1,2,3,4,5,8,9,16,17,32,33}; tile_size in {4,8,16}. */
 int gsplat_rasterize_fwd(
     int64_t I, int64_t n_rows, int64_t n_isects, int32_t cdim,
@@ -262,12 +264,15 @@ int gsplat_rasterize_fwd(
     int32_t tile_width, int32_t tile_height,
     const int32_t *tile_offsets, const int32_t *flatten_ids,
     float *render_colors, float *render_alphas, int32_t *last_ids,
-    gsplat_stream_t stream);
+    float *render_transmittance, gsplat_stream_t stream);
 
 /* Back-to-front replay of the compositing.
  * Replaces rasterize_to_pixels_3dgs_bwd
  *   (gsplat/cuda/csrc/Rasterization.cpp:122-214,
  *    gsplat/cuda/csrc/RasterizeToPixels3DGSBwd.cu:39-412).
+ * render_transmittance (optional) is the forward's final T per pixel; when
+ * NULL, T is taken as 1 - render_alphas as the reference does, which loses
+ * relative precision for pixels that end near the 1e-4 cutoff.
  * Gradient outputs are ACCUMULATED and must be zero-filled by the caller:
  * v_means2d [n,2], v_conics [n,3], v_colors [n,CDIM], v_opacities [n],
  * v_means2d_abs [n,2] (optional; sum over pixels of |dL/dmean2d|). */
@@ -278,7 +283,8 @@ int gsplat_rasterize_bwd(
     int32_t image_width, int32_t image_height, int32_t tile_size,
     int32_t tile_width, int32_t tile_height,
     const int32_t *tile_offsets, const int32_t *flatten_ids,
-    const float *render_alphas, const int32_t *last_ids,
+    const float *render_alphas, const float *render_transmittance,
+    const int32_t *last_ids,
     const float *v_render_colors, const float *v_render_alphas,
     float *v_means2d_abs, float *v_means2d, float *v_conics,
     float *v_colors, float *v_opacities,

@@ -61,7 +61,7 @@ def test_argument_errors_are_reported_without_a_gpu(lib_path):
         _lib.call("gsplat_sh_fwd", 10, 16, 7, None, None, None, None, None)
     with pytest.raises(RuntimeError, match="channel"):
         _lib.call("gsplat_rasterize_fwd", 1, 0, 0, 7, None, None, None, None, None, None,
-                  16, 16, 16, 1, 1, 1, None, None, None, None, None)
+                  16, 16, 16, 1, 1, 1, None, None, None, None, None, None)
 
 
 def test_reference_op_schemas_registered():

@@ -3,14 +3,16 @@
 Forward: every output bit-exact against the C restatement (exact_ref.c), for
 the dense and packed layouts, quats/scales and covars inputs, pinhole and
 ortho cameras, batch dims, opacity-aware radii and compensation.
-Backward: against autograd of the float64 PyTorch restatement."""
+Backward: against autograd of the float64 PyTorch restatement, within
+rtol 1e-4 / atol 1e-5 at the float32 floor that the same restatement
+evaluated in float32 measures (tests/_util.py:assert_grad_close)."""
 
 import numpy as np
 import pytest
 import torch
 
 from oracle import exact, torch_ref
-from tests._util import DEV, assert_close, small_scene
+from tests._util import DEV, assert_close, assert_grad_close, small_scene
 
 pytestmark = pytest.mark.gpu
 
@@ -146,11 +148,22 @@ def _grad_check(packed, calc_comp, use_covars=False, viewmat_grad=True, C=2):
     if calc_comp:
         rl = rl + (t["compensations"] * w_p.double())[v].sum()
     rl.backward()
+    # the same restatement in float32: its error measures the fp32 floor
+    l32 = {k: (v.detach().cpu().float().requires_grad_(v.requires_grad))
+           for k, v in leaves.items()}
+    t32 = torch_ref.projection_ref(l32["means"], l32.get("covars"), l32.get("quats"),
+                                   l32.get("scales"), l32["viewmats"], K, W, H,
+                                   calc_compensations=calc_comp)
+    r32 = (t32["means2d"] * w_m)[v].sum() + (t32["conics"] * w_c)[v].sum() + \
+        (t32["depths"] * w_d)[v].sum()
+    if calc_comp:
+        r32 = r32 + (t32["compensations"] * w_p)[v].sum()
+    r32.backward()
     for k in leaves:
         if not leaves[k].requires_grad:
             continue
-        assert_close(leaves[k].grad, ref_leaves[k].grad, rtol=1e-4, atol=1e-5,
-                     name=f"d{k}")
+        assert_grad_close(leaves[k].grad, ref_leaves[k].grad, l32[k].grad,
+                          rtol=1e-4, atol=1e-5, name=f"d{k}")
 
 
 @pytest.mark.parametrize("packed", [False, True])

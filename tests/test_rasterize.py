@@ -6,14 +6,17 @@ Reference test: tests/test_basic.py:1954-2063.
 Pixels whose termination test is ill-conditioned (T (1 - alpha) within 1e-4
 relative of 1e-4 with an exp()-derived alpha) are excluded from the value
 comparison and get zero upstream gradient in both runs; the test asserts
-they are rare."""
+they are rare.  Renders must match the float64 restatement within rtol 1e-4 /
+atol 1e-5; gradients are held to that tolerance at the float32 floor
+(tests/_util.py:assert_grad_close), using the same restatement evaluated in
+float32 as the measure of that floor."""
 
 import numpy as np
 import pytest
 import torch
 
 from oracle import torch_ref
-from tests._util import DEV, assert_close, projected_2d
+from tests._util import DEV, assert_close, assert_grad_close, projected_2d
 
 pytestmark = pytest.mark.gpu
 
@@ -43,6 +46,13 @@ def _run(data, packed, D, backgrounds, masks, absgrad=False):
     v_rc = v_rc * keep[..., None]
     v_ra = v_ra * keep[..., None]
     ((rc_r * v_rc.double()).sum() + (ra_r * v_ra.double()).sum()).backward()
+    # the same restatement in float32 (its error measures the fp32 floor)
+    ins32 = [t.float().clone().requires_grad_() for t in (m2, con, col, op)]
+    bg32 = bg.float().clone().requires_grad_() if bg is not None else None
+    rc32, ra32, _ = torch_ref.rasterize_to_pixels_ref(
+        ins32[0], ins32[1], ins32[2], ins32[3], W, H, ts, offs, fl,
+        backgrounds=bg32, masks=mk, dtype=torch.float32)
+    ((rc32 * v_rc).sum() + (ra32 * v_ra).sum()).backward()
 
     ins = [t.clone().to(DEV).requires_grad_() for t in (m2, con, col, op)]
     bgd = bg.clone().to(DEV).requires_grad_() if bg is not None else None
@@ -55,10 +65,11 @@ def _run(data, packed, D, backgrounds, masks, absgrad=False):
     sel = keep
     assert_close(rc.cpu()[sel], rc_r.detach()[sel], RTOL, ATOL, "render_colors")
     assert_close(ra.cpu()[sel], ra_r.detach()[sel], RTOL, ATOL, "render_alphas")
-    for name, a, b in zip(("v_means2d", "v_conics", "v_colors", "v_opacities"), ins, ins_ref):
-        assert_close(a.grad, b.grad, RTOL, ATOL, name)
+    for name, a, b, b32 in zip(("v_means2d", "v_conics", "v_colors", "v_opacities"),
+                               ins, ins_ref, ins32):
+        assert_grad_close(a.grad, b.grad, b32.grad, RTOL, ATOL, name)
     if bg is not None:
-        assert_close(bgd.grad, bg_ref.grad, RTOL, ATOL, "v_backgrounds")
+        assert_grad_close(bgd.grad, bg_ref.grad, bg32.grad, RTOL, ATOL, "v_backgrounds")
     return ins
 
 
