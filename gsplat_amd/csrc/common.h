@@ -114,6 +114,37 @@ __device__ __forceinline__ float portable_logf(float x) {
     return ef * 0x1.62e3p-1f + (lnm + ef * 0x1.2fefa2p-17f);
 }
 
+// Natural exponential by Cody-Waite range reduction and a Taylor polynomial:
+// x = k ln2 + r with k = rint(x log2e), |r| <= ln2/2, r computed with a
+// two-part ln2 (the high part has 9 significant bits, so k*hi is exact);
+// e^r = sum_{n<=7} r^n/n! (truncation below 2^-27 relative) in Horner form
+// with fused multiply-adds; e^x = e^r * 2^k.  Error below 1 ulp over
+// [-87, 88]; 0 below that range, +inf above, NaN passes through.  Only
+// correctly rounded IEEE operations (fma, rint, mul) are used, so the host
+// oracle reproduces every bit with fmaf and rintf.
+__device__ __forceinline__ float portable_expf(float x) {
+#pragma clang fp contract(off)
+    if (!(x == x))
+        return x;
+    if (x < -87.f)
+        return 0.f;
+    if (x > 88.f)
+        return __builtin_inff();
+    const float kf = __builtin_rintf(x * 0x1.715476p+0f);
+    float r = __builtin_fmaf(-kf, 0x1.63p-1f, x);
+    r = __builtin_fmaf(-kf, -0x1.bd0106p-13f, r);
+    float p = 0x1.a01a02p-13f;
+    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+    p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.f);
+    p = __builtin_fmaf(p, r, 1.f);
+    const float scale = __int_as_float(((int32_t)kf + 127) << 23);
+    return p * scale;
+}
+
 // DPP row operations (gfx9 encodings).
 constexpr int kDppQuadXor1 = 0xB1;   // quad_perm:[1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4E;   // quad_perm:[2,3,0,1]

@@ -14,9 +14,12 @@
 // against per-Gaussian thresholds computed once per tile load:
 //   alpha < 1/255     <=>  sigma > ln(o / (1/255))          ("sig_max")
 //   o exp(-sigma) > .99 <=> sigma < ln(o / 0.99)            ("sig_clamp")
-// sigma is evaluated in a fixed IEEE order without contraction and the logs
-// are portable_logf, so the set of composited Gaussians is reproducible bit
-// for bit by the host oracle; exp() itself uses the hardware v_exp_f32.
+// sigma is evaluated in a fixed IEEE order without contraction, the logs are
+// portable_logf and exp(-sigma) is portable_expf (below 1 ulp, built from
+// correctly rounded operations only), so alpha, the running transmittance
+// and every compositing decision -- the set of composited Gaussians, the
+// termination point, last_ids -- are reproducible bit for bit by the host
+// oracle.
 //
 // MI355X design: one workgroup per tile (tile_size^2 threads = 4 waves at
 // 16x16, each wave a 16x4 pixel strip), Gaussians staged in LDS in batches of
@@ -33,8 +36,6 @@
 
 namespace gs {
 namespace {
-
-constexpr float kLog2e = 1.4426950408889634f;
 
 struct RasterArgs {
     int64_t I, n_rows, n_isects;
@@ -155,7 +156,7 @@ __global__ void __launch_bounds__(kMaxTileThreads) rasterize_fwd_kernel(const Ra
             const float sigma = gauss_sigma(con.x, con.y, con.z, dx, dy);
             if (sigma < 0.f || sigma > geo.w)
                 continue;
-            const float vis = __builtin_amdgcn_exp2f(-sigma * kLog2e);
+            const float vis = portable_expf(-sigma);
             const float alpha = sigma < con.w ? kMaxAlpha : geo.z * vis;
             const float next_T = T * (1.f - alpha);
             if (next_T <= kTransmittanceThreshold) {
@@ -305,7 +306,7 @@ __global__ void __launch_bounds__(kMaxTileThreads) rasterize_bwd_kernel(const Ra
             for (int k = 0; k < NACC; ++k)
                 g_acc[k] = 0.f;
             if (valid) {
-                vis = __builtin_amdgcn_exp2f(-sigma * kLog2e);
+                vis = portable_expf(-sigma);
                 const bool clamped = sigma < con.w;
                 alpha = clamped ? kMaxAlpha : geo.z * vis;
                 const float one_minus = fmaxf(kMinOneMinusAlpha, 1.f - alpha);

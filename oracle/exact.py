@@ -96,6 +96,17 @@ def portable_logf_c(x) -> np.ndarray:
     return y
 
 
+def portable_expf(x) -> np.ndarray:
+    """e^x exactly as the device ``portable_expf`` computes it (through the C
+    oracle, whose fmaf/rintf give the same correctly rounded operations);
+    the rasterizer's alpha is o * portable_expf(-sigma)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    flat = x.ravel()
+    y = np.empty_like(flat)
+    _load().oracle_portable_expf_array(_p(flat), _p(y), ctypes.c_int64(flat.size))
+    return y.reshape(x.shape)
+
+
 # --------------------------------------------------------------------------
 # Projection (ProjectionEWA3DGSFused.cu:38-234)
 # --------------------------------------------------------------------------

@@ -8,7 +8,8 @@
  *     the math of gsplat/cuda/include/Utils.cuh:174-257, 424-432, 542-581;
  *   - tile-set enumeration per row, ellipse ("AccuTile") and axis-aligned box
  *     variants -- gsplat/cuda/csrc/IntersectTile.cu:38-121, 133-288;
- *   - the natural log used by the opacity-aware extents.
+ *   - the natural log used by the opacity-aware extents and the exponential
+ *     that turns a Gaussian's Mahalanobis term into its alpha.
  * Every floating-point operation is written out in the order the product
  * kernels use, and this file is compiled with -ffp-contract=off, so IEEE
  * single precision gives identical bits on the CPU and the GPU.
@@ -66,6 +67,33 @@ float oracle_portable_logf(float x) {
 
 void oracle_portable_logf_array(const float *x, float *y, int64_t n) {
     for (int64_t i = 0; i < n; ++i) y[i] = oracle_portable_logf(x[i]);
+}
+
+/* e^x by Cody-Waite reduction (x = k ln2 + r, two-part ln2) and the Taylor
+ * polynomial of e^r to degree 7 in fused multiply-adds: the device
+ * portable_expf, operation for operation (fmaf and rintf are correctly
+ * rounded, so the bits agree). */
+float oracle_portable_expf(float x) {
+    if (!(x == x)) return x;
+    if (x < -87.f) return 0.f;
+    if (x > 88.f) return INFINITY;
+    const float kf = rintf(x * 0x1.715476p+0f);
+    float r = fmaf(-kf, 0x1.63p-1f, x);
+    r = fmaf(-kf, -0x1.bd0106p-13f, r);
+    float p = 0x1.a01a02p-13f;
+    p = fmaf(p, r, 0x1.6c16c2p-10f);
+    p = fmaf(p, r, 0x1.111112p-7f);
+    p = fmaf(p, r, 0x1.555556p-5f);
+    p = fmaf(p, r, 0x1.555556p-3f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.f);
+    p = fmaf(p, r, 1.f);
+    const float scale = u2f((uint32_t)((int32_t)kf + 127) << 23);
+    return p * scale;
+}
+
+void oracle_portable_expf_array(const float *x, float *y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = oracle_portable_expf(x[i]);
 }
 
 /* ----------------------------------------------------------------------- */

@@ -192,7 +192,7 @@ def spherical_harmonics_ref(degree: int, dirs: Tensor, coeffs: Tensor,
 def rasterize_to_pixels_ref(means2d, conics, colors, opacities, width, height,
                             tile_size, isect_offsets, flatten_ids,
                             backgrounds=None, masks=None, decide=None,
-                            dtype=torch.float64, amb_tol=1e-4):
+                            dtype=torch.float64):
     """Front-to-back compositing per tile, differentiable.
 
     means2d [..., N, 2] or [nnz, 2] (rows are what ``flatten_ids`` index);
@@ -201,9 +201,14 @@ def rasterize_to_pixels_ref(means2d, conics, colors, opacities, width, height,
     the float32 values of the inputs.
 
     Returns (render_colors [I, H, W, D], render_alphas [I, H, W, 1], info)
-    where info holds ``last_ids`` [I, H, W] and ``ambiguous`` [I, H, W]: pixels
-    whose termination test T (1 - alpha) <= 1e-4 is within ``amb_tol``
-    (relative) of flipping, i.e. ill-conditioned pixels.
+    where info holds ``last_ids`` [I, H, W] and ``transmittance`` [I, H, W]
+    (the float32 running transmittance at the end of each pixel's list).
+
+    Which Gaussians a pixel composites, and where it stops, is decided in
+    float32 exactly as the kernels do: sigma in the kernels' operation order,
+    alpha = o * portable_expf(-sigma) (bit-identical to the device), T a
+    running float32 product, stop before the first Gaussian with
+    T (1 - alpha) <= 1e-4.  The differentiable values use ``dtype``.
     """
     th, tw = isect_offsets.shape[-2:]
     I = int(np.prod(isect_offsets.shape[:-2])) if isect_offsets.dim() > 2 else 1
@@ -230,7 +235,7 @@ def rasterize_to_pixels_ref(means2d, conics, colors, opacities, width, height,
 
     pix_index, pix_colors, pix_alphas = [], [], []
     last_ids = np.zeros(I * height * width, np.int32)
-    ambiguous = np.zeros(I * height * width, bool)
+    trans = np.ones(I * height * width, np.float32)
     for slot in range(I * th * tw):
         img = slot // (th * tw)
         tile = slot % (th * tw)
@@ -274,16 +279,12 @@ def rasterize_to_pixels_ref(means2d, conics, colors, opacities, width, height,
         a_raw = op[idt][None, :] * torch.exp(-sigma)
         alpha = torch.where(skip_t, torch.zeros_like(a_raw),
                             torch.where(clamp_t, torch.full_like(a_raw, MAX_ALPHA), a_raw))
-        # Termination in float32, as the kernels evaluate it: T is a running
-        # float32 product of (1 - alpha) in compositing order, and a pixel
-        # stops before the first Gaussian with T (1 - alpha) <= 1e-4.  A chain
-        # of clamped alphas (0.99f) is reproduced exactly; otherwise alpha
-        # differs from the GPU's by the exp() rounding, so pixels within
-        # `amb_tol` of the threshold are reported as ambiguous.
+        # Decisions in float32 with the device's exact alpha (see docstring).
         o32 = np.asarray(decide["opacities"], np.float32).reshape(-1)[ids][None, :]
-        vis32 = np.exp(-sig32.astype(np.float64)).astype(np.float32)
-        a32 = np.where(skip, np.float32(0.0),
-                       np.where(clamped, exact.MAX_ALPHA, (o32 * vis32).astype(np.float32)))
+        with np.errstate(over="ignore", invalid="ignore"):
+            vis32 = exact.portable_expf(-sig32)
+            a32 = np.where(skip, np.float32(0.0),
+                           np.where(clamped, exact.MAX_ALPHA, (o32 * vis32).astype(np.float32)))
         one_m32 = (np.float32(1.0) - a32).astype(np.float32)
         Tb32 = np.cumprod(np.concatenate([np.ones((P, 1), np.float32), one_m32[:, :-1]],
                                          axis=1), axis=1, dtype=np.float32)
@@ -293,10 +294,9 @@ def rasterize_to_pixels_ref(means2d, conics, colors, opacities, width, height,
         k_stop = np.where(has, cand.argmax(axis=1), n)
         ar = np.arange(n)[None, :]
         included_np = (ar < k_stop[:, None]) & ~skip
-        chain_exact = np.cumprod(np.where(skip, True, clamped), axis=1).astype(bool)
-        near = (~skip) & (ar <= k_stop[:, None]) & ~chain_exact & \
-            (np.abs(next32.astype(np.float64) / 1e-4 - 1.0) < amb_tol)
-        amb = near.any(axis=1)
+        # float32 transmittance after the last composited Gaussian
+        T_end32 = np.where(has, Tb32[np.arange(P), np.minimum(k_stop, n - 1)],
+                           next32[:, -1] if n > 0 else np.ones(P, np.float32))
         last_np = np.where(included_np, ar, -1).max(axis=1)
         included = torch.from_numpy(included_np)
         ai = alpha * included.to(dtype)
@@ -309,7 +309,7 @@ def rasterize_to_pixels_ref(means2d, conics, colors, opacities, width, height,
         pix_colors.append(c)
         pix_alphas.append(1.0 - T_final)
         last_ids[lin] = np.where(last_np >= 0, s + last_np, 0)
-        ambiguous[lin] = amb
+        trans[lin] = T_end32
     idx = torch.from_numpy(np.concatenate(pix_index))
     out_c = torch.zeros(I * height * width, D, dtype=dtype).index_copy(
         0, idx, torch.cat(pix_colors, dim=0))
@@ -317,7 +317,7 @@ def rasterize_to_pixels_ref(means2d, conics, colors, opacities, width, height,
         0, idx, torch.cat(pix_alphas, dim=0))
     info = {
         "last_ids": last_ids.reshape(I, height, width),
-        "ambiguous": ambiguous.reshape(I, height, width),
+        "transmittance": trans.reshape(I, height, width),
     }
     return (out_c.reshape(I, height, width, D), out_a.reshape(I, height, width, 1), info)
 
@@ -425,6 +425,7 @@ def rasterization_ref(means, quats, scales, opacities, colors, viewmats, Ks,
     if render_mode in ("ED", "RGB+ED"):
         rc = torch.cat([rc[..., :-1], rc[..., -1:] / ra.clamp(min=1e-10)], dim=-1)
     meta = {"isect_ids": isect_ids, "flatten_ids": flatten_ids, "offsets": offsets,
-            "valid": ex["valid"], "radii": ex["radii"], "ambiguous": info["ambiguous"],
+            "valid": ex["valid"], "radii": ex["radii"],
+            "transmittance": info["transmittance"],
             "last_ids": info["last_ids"], "n_isects": int(isect_ids.shape[0])}
     return rc, ra, meta

@@ -86,7 +86,8 @@ def assert_close(a, b, rtol, atol, name):
 
 
 GRAD_STRICT_SLACK = 5e-3  # strict-tolerance pass rate may trail fp32's by this
-GRAD_ERR_RATIO = 2.0      # max / RMS error may exceed fp32's by this factor
+GRAD_MAX_RATIO = 3.0      # worst element may exceed fp32's worst by this factor
+GRAD_RMS_RATIO = 2.0      # RMS error may exceed fp32's by this factor
 
 
 def assert_grad_close(got, ref64, ref32, rtol, atol, name):
@@ -103,8 +104,11 @@ def assert_grad_close(got, ref64, ref32, rtol, atol, name):
 
       * the fraction of elements within tol = atol + rtol |ref64| may trail
         the float32 restatement's by at most 0.5 percentage points;
-      * measured in units of tol, the largest and the RMS deviation from
-        ref64 may be at most max(1, 2x) the float32 restatement's.
+      * measured in units of tol, the RMS deviation from ref64 may be at
+        most max(1, 2x) the float32 restatement's and the largest at most
+        max(1, 3x): the worst elements are sums whose terms cancel by two to
+        three orders of magnitude, and two float32 summation orders of the
+        same terms land 2-3x apart on them.
 
     Returns the report line."""
     a = got.detach().double().cpu()
@@ -125,6 +129,6 @@ def assert_grad_close(got, ref64, ref32, rtol, atol, name):
            f"(fp32 {mx32:.3g}), rms {rms:.3g} (fp32 {rms32:.3g}); max abs "
            f"{err.max().item():.3e} (fp32 {err32.max().item():.3e})")
     assert frac >= frac32 - GRAD_STRICT_SLACK, msg
-    assert mx <= max(1.0, GRAD_ERR_RATIO * mx32), msg
-    assert rms <= max(1.0, GRAD_ERR_RATIO * rms32), msg
+    assert mx <= max(1.0, GRAD_MAX_RATIO * mx32), msg
+    assert rms <= max(1.0, GRAD_RMS_RATIO * rms32), msg
     return msg

@@ -33,6 +33,25 @@ def test_portable_log_numpy_equals_c_and_is_accurate():
 
 
 # --------------------------------------------------------------------------
+# exp (the alpha of every composited pixel/Gaussian pair)
+# --------------------------------------------------------------------------
+def test_portable_exp_is_accurate():
+    rng = np.random.default_rng(1)
+    x = np.concatenate([
+        np.linspace(-87.0, 88.0, 400_001), rng.uniform(-6.0, 0.0, 200_000),
+        -np.arange(0, 126) * np.log(2.0),
+    ]).astype(np.float32)
+    y = exact.portable_expf(x)
+    ref = np.exp(x.astype(np.float64))
+    ulp = np.abs(y - ref) / np.spacing(ref.astype(np.float32)).astype(np.float64)
+    # below 1 ulp everywhere (a dropped Taylor term or a one-part ln2 fails this)
+    assert ulp.max() < 1.0, ulp.max()
+    assert exact.portable_expf(np.float32(0.0)) == np.float32(1.0)
+    special = exact.portable_expf(np.array([-100.0, 100.0, np.nan], np.float32))
+    assert special[0] == 0.0 and special[1] == np.inf and np.isnan(special[2])
+
+
+# --------------------------------------------------------------------------
 # Projection
 # --------------------------------------------------------------------------
 def _axis_gaussian(z=4.0, s=0.05, f=300.0, W=200, H=100, opacity=None):
