@@ -36,7 +36,7 @@ _SIGNATURES = {
         c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P,
         c_int32, c_int32, c_float, c_float, c_float, c_float, c_int32,
         _P, c_size_t,
-        _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+        _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
     "gsplat_projection_packed_bwd": [
         c_int64, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P,
         c_int32, c_int32, c_float, c_int32,
@@ -44,6 +44,12 @@ _SIGNATURES = {
         _P, _P, _P, _P, _P, _P],
     "gsplat_sh_fwd": [c_int64, c_int32, c_int32, _P, _P, _P, _P, _P],
     "gsplat_sh_bwd": [c_int64, c_int32, c_int32, _P, _P, _P, _P, _P, _P, _P],
+    "gsplat_sh_rows_fwd": [c_int64, c_int64, c_int64, c_int32, c_int32,
+                           _P, _P, _P, _P, _P, _P],
+    "gsplat_sh_rows_bwd": [c_int64, c_int64, c_int64, c_int32, c_int32,
+                           _P, _P, _P, _P, _P, _P, _P, _P],
+    "gsplat_rows_gather": [c_int64, c_int64, c_int64, c_int32, _P, _P, _P, _P],
+    "gsplat_rows_scatter_sum": [c_int64, c_int64, c_int64, c_int32, _P, _P, _P, _P],
     "gsplat_isect_count_workspace_size": [c_int64],
     "gsplat_isect_count": [
         c_int64, c_int64, _P, _P, _P, _P, _P, c_int32, c_int32, c_int32,

@@ -291,7 +291,7 @@ __global__ void __launch_bounds__(kProjThreads) projection_packed_fwd_kernel(
     int64_t *__restrict__ gaussian_ids, int32_t *__restrict__ radii,
     float *__restrict__ means2d, float *__restrict__ depths,
     float *__restrict__ conics, float *__restrict__ compensations,
-    int64_t *__restrict__ nnz_out) {
+    int64_t *__restrict__ nnz_out, int32_t *__restrict__ row_of) {
     __shared__ uint32_t s_ticket;
     __shared__ uint32_t s_wave_count[kProjThreads / kWave];
     __shared__ uint64_t s_prefix;
@@ -328,6 +328,8 @@ __global__ void __launch_bounds__(kProjThreads) projection_packed_fwd_kernel(
         // first Gaussian of camera row bc: its exclusive position is indptr
         indptr[row / a.N] = (int32_t)pos;
     }
+    if (row_of != nullptr && row < n_rows)
+        row_of[row] = valid ? (int32_t)pos : -1;
     if (valid) {
         const int64_t g = row % a.N;
         const int64_t bc = row / a.N;
@@ -934,7 +936,7 @@ extern "C" int gsplat_projection_packed_fwd(
     size_t workspace_bytes, int32_t *indptr, int64_t *batch_ids,
     int64_t *camera_ids, int64_t *gaussian_ids, int32_t *radii,
     float *means2d, float *depths, float *conics, float *compensations,
-    int64_t *nnz_out, gsplat_stream_t stream) {
+    int64_t *nnz_out, int32_t *row_of, gsplat_stream_t stream) {
     clear_error();
     GS_TRY(check_common(B, C, N, means, covars, quats, scales, viewmats, Ks,
                         image_width, image_height, camera_model));
@@ -957,7 +959,8 @@ extern "C" int gsplat_projection_packed_fwd(
               far_plane, radius_clip, camera_model, compensations != nullptr};
     projection_packed_fwd_kernel<<<(unsigned)blocks, kProjThreads, 0, st>>>(
         a, lookback_from(workspace), indptr, batch_ids, camera_ids,
-        gaussian_ids, radii, means2d, depths, conics, compensations, nnz_out);
+        gaussian_ids, radii, means2d, depths, conics, compensations, nnz_out,
+        row_of);
     return check_launch("projection_packed_fwd_kernel");
 }
 

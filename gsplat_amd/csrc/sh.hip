@@ -157,11 +157,13 @@ __device__ __forceinline__ void sh_basis_grad(float x, float y, float z,
 }
 
 // Copy the coefficient prefix (NB bands) of rows [r0, r0 + nrows) into LDS
-// with pitch PITCH floats per row.
+// with pitch PITCH floats per row.  With `vis` (an LDS flag per row), rows
+// whose flag is 0 are not read (their LDS rows are left unset).
 template <int DEG>
 __device__ __forceinline__ void stage_coeffs(const float *__restrict__ coeffs,
                                              int64_t r0, int nrows, int K,
-                                             bool vec_ok, float *s) {
+                                             bool vec_ok, float *s,
+                                             const uint8_t *vis = nullptr) {
     using S = ShShape<DEG>;
     const int total = nrows * S::ROW;
     if (vec_ok) {
@@ -170,8 +172,10 @@ __device__ __forceinline__ void stage_coeffs(const float *__restrict__ coeffs,
             reinterpret_cast<const float4 *>(coeffs + r0 * S::ROW);
         const int nvec = total >> 2;
         for (int v = threadIdx.x; v < nvec; v += kShThreads) {
-            const float4 q = src[v];
             const int e = v << 2;
+            if (vis != nullptr && !vis[e / S::ROW] && !vis[(e + 3) / S::ROW])
+                continue;
+            const float4 q = src[v];
             const float vals[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -182,11 +186,15 @@ __device__ __forceinline__ void stage_coeffs(const float *__restrict__ coeffs,
         }
         for (int e = (nvec << 2) + threadIdx.x; e < total; e += kShThreads) {
             const int row = e / S::ROW;
+            if (vis != nullptr && !vis[row])
+                continue;
             s[row * S::PITCH + (e - row * S::ROW)] = coeffs[r0 * S::ROW + e];
         }
     } else {
         for (int e = threadIdx.x; e < total; e += kShThreads) {
             const int row = e / S::ROW;
+            if (vis != nullptr && !vis[row])
+                continue;
             const int col = e - row * S::ROW;
             s[row * S::PITCH + col] = coeffs[(r0 + row) * (int64_t)K * 3 + col];
         }
@@ -342,6 +350,210 @@ __global__ void __launch_bounds__(kShThreads)
     }
 }
 
+// ---------------------------------------------------------------------------
+// SH over packed rows, driven by Gaussian.
+//
+// The packed layout keeps one row per visible (camera, Gaussian) pair; the
+// reference gathers [nnz, K, 3] coefficients and view directions for them
+// and scatters the gradients back with index_put (rendering.py:227-253,
+// 845-873).  Here each thread owns one Gaussian (b, g): its coefficients are
+// staged once (coalesced, skipped when it is visible in no camera) and it
+// loops over the C cameras through row_of[(b C + c) N + g] (the packed row,
+// or -1).  The forward writes colors[row] = max(SH(dir) + 0.5, 0) with
+// dir = mean - campos (rendering.py:872); the backward accumulates the
+// coefficient and mean gradients over the cameras in registers and writes
+// every Gaussian's gradient row once -- deterministic, no atomics, no
+// zero fill.
+// ---------------------------------------------------------------------------
+struct ShRowsArgs {
+    int64_t B, C, N;
+    int K;
+    const float *means;   // [B, N, 3]
+    const float *campos;  // [B, C, 3]
+    const float *coeffs;  // [B, N, K, 3]
+    const int32_t *row_of;  // [B, C, N]
+    bool vec_ok;
+};
+
+template <int DEG>
+__device__ __forceinline__ bool sh_rows_prologue(const ShRowsArgs &a,
+                                                 int64_t r0, int nrows,
+                                                 float *s_coef, uint8_t *s_vis) {
+    const int t = threadIdx.x;
+    bool vis = false;
+    if (t < nrows) {
+        const int64_t bg = r0 + t;
+        const int64_t b = bg / a.N, g = bg - b * a.N;
+        for (int64_t c = 0; c < a.C; ++c)
+            vis |= a.row_of[(b * a.C + c) * a.N + g] >= 0;
+    }
+    s_vis[t] = vis ? 1 : 0;
+    __syncthreads();
+    stage_coeffs<DEG>(a.coeffs, r0, nrows, a.K, a.vec_ok, s_coef, s_vis);
+    __syncthreads();
+    return vis;
+}
+
+template <int DEG>
+__global__ void __launch_bounds__(kShThreads)
+    sh_rows_fwd_kernel(const ShRowsArgs a, float *__restrict__ colors) {
+    using S = ShShape<DEG>;
+    __shared__ float s_coef[kShThreads * S::PITCH];
+    __shared__ uint8_t s_vis[kShThreads];
+    const int64_t r0 = (int64_t)blockIdx.x * kShThreads;
+    const int64_t BN = a.B * a.N;
+    const int nrows = (int)((BN - r0) < kShThreads ? (BN - r0) : kShThreads);
+    const bool vis = sh_rows_prologue<DEG>(a, r0, nrows, s_coef, s_vis);
+    if (!vis)
+        return;
+    const int t = threadIdx.x;
+    const int64_t bg = r0 + t;
+    const int64_t b = bg / a.N, g = bg - b * a.N;
+    const float mx = a.means[bg * 3 + 0], my = a.means[bg * 3 + 1],
+                mz = a.means[bg * 3 + 2];
+    const float *cf = s_coef + t * S::PITCH;
+    for (int64_t c = 0; c < a.C; ++c) {
+        const int32_t r = a.row_of[(b * a.C + c) * a.N + g];
+        if (r < 0)
+            continue;
+        float Y[S::NB];
+        if (DEG > 0) {
+            const float *cp = a.campos + (b * a.C + c) * 3;
+            const float dx = mx - cp[0], dy = my - cp[1], dz = mz - cp[2];
+            const float inorm = 1.f / sqrtf(dx * dx + dy * dy + dz * dz);
+            sh_basis<DEG>(dx * inorm, dy * inorm, dz * inorm, Y);
+        } else {
+            Y[0] = kY0;
+        }
+        float o0 = 0.f, o1 = 0.f, o2 = 0.f;
+#pragma unroll
+        for (int k = 0; k < S::NB; ++k) {
+            o0 += Y[k] * cf[k * 3 + 0];
+            o1 += Y[k] * cf[k * 3 + 1];
+            o2 += Y[k] * cf[k * 3 + 2];
+        }
+        colors[(int64_t)r * 3 + 0] = fmaxf(o0 + 0.5f, 0.f);
+        colors[(int64_t)r * 3 + 1] = fmaxf(o1 + 0.5f, 0.f);
+        colors[(int64_t)r * 3 + 2] = fmaxf(o2 + 0.5f, 0.f);
+    }
+}
+
+template <int DEG>
+__global__ void __launch_bounds__(kShThreads)
+    sh_rows_bwd_kernel(const ShRowsArgs a, const float *__restrict__ v_colors,
+                       float *__restrict__ v_coeffs,
+                       float *__restrict__ v_means) {
+    using S = ShShape<DEG>;
+    __shared__ float s_buf[kShThreads * S::PITCH];
+    __shared__ uint8_t s_vis[kShThreads];
+    const int64_t r0 = (int64_t)blockIdx.x * kShThreads;
+    const int64_t BN = a.B * a.N;
+    const int nrows = (int)((BN - r0) < kShThreads ? (BN - r0) : kShThreads);
+    const bool vis = sh_rows_prologue<DEG>(a, r0, nrows, s_buf, s_vis);
+    const int t = threadIdx.x;
+    const int64_t bg = r0 + t;
+    float acc[S::ROW];
+#pragma unroll
+    for (int k = 0; k < S::ROW; ++k)
+        acc[k] = 0.f;
+    float vm0 = 0.f, vm1 = 0.f, vm2 = 0.f;
+    if (vis) {
+        const int64_t b = bg / a.N, g = bg - b * a.N;
+        const float mx = a.means[bg * 3 + 0], my = a.means[bg * 3 + 1],
+                    mz = a.means[bg * 3 + 2];
+        const float *cf = s_buf + t * S::PITCH;
+        for (int64_t c = 0; c < a.C; ++c) {
+            const int32_t r = a.row_of[(b * a.C + c) * a.N + g];
+            if (r < 0)
+                continue;
+            float Y[S::NB];
+            float x = 0.f, y = 0.f, z = 0.f, inorm = 0.f;
+            if (DEG > 0) {
+                const float *cp = a.campos + (b * a.C + c) * 3;
+                const float dx = mx - cp[0], dy = my - cp[1], dz = mz - cp[2];
+                inorm = 1.f / sqrtf(dx * dx + dy * dy + dz * dz);
+                x = dx * inorm;
+                y = dy * inorm;
+                z = dz * inorm;
+                sh_basis<DEG>(x, y, z, Y);
+            } else {
+                Y[0] = kY0;
+            }
+            // colour value again for the clamp's gradient mask
+            float o0 = 0.f, o1 = 0.f, o2 = 0.f;
+#pragma unroll
+            for (int k = 0; k < S::NB; ++k) {
+                o0 += Y[k] * cf[k * 3 + 0];
+                o1 += Y[k] * cf[k * 3 + 1];
+                o2 += Y[k] * cf[k * 3 + 2];
+            }
+            const float v0 = o0 + 0.5f >= 0.f ? v_colors[(int64_t)r * 3 + 0] : 0.f;
+            const float v1 = o1 + 0.5f >= 0.f ? v_colors[(int64_t)r * 3 + 1] : 0.f;
+            const float v2 = o2 + 0.5f >= 0.f ? v_colors[(int64_t)r * 3 + 2] : 0.f;
+#pragma unroll
+            for (int k = 0; k < S::NB; ++k) {
+                acc[k * 3 + 0] += Y[k] * v0;
+                acc[k * 3 + 1] += Y[k] * v1;
+                acc[k * 3 + 2] += Y[k] * v2;
+            }
+            if (DEG > 0) {
+                float G[S::NB];
+#pragma unroll
+                for (int k = 0; k < S::NB; ++k)
+                    G[k] = cf[k * 3 + 0] * v0 + cf[k * 3 + 1] * v1 +
+                           cf[k * 3 + 2] * v2;
+                float gx, gy, gz;
+                sh_basis_grad<DEG>(x, y, z, G, gx, gy, gz);
+                const float dot = gx * x + gy * y + gz * z;
+                vm0 += (gx - dot * x) * inorm;
+                vm1 += (gy - dot * y) * inorm;
+                vm2 += (gz - dot * z) * inorm;
+            }
+        }
+    }
+    if (t < nrows) {
+        v_means[bg * 3 + 0] = vm0;
+        v_means[bg * 3 + 1] = vm1;
+        v_means[bg * 3 + 2] = vm2;
+    }
+    __syncthreads();  // every thread is done reading its staged coefficients
+    if (t < nrows) {
+        float *o = s_buf + t * S::PITCH;
+#pragma unroll
+        for (int k = 0; k < S::ROW; ++k)
+            o[k] = acc[k];
+    }
+    __syncthreads();
+    const int rowlen = a.K * 3;
+    const int total = nrows * rowlen;
+    float *dst = v_coeffs + r0 * rowlen;
+    if (a.vec_ok) {
+        float4 *dst4 = reinterpret_cast<float4 *>(dst);
+        const int nvec = total >> 2;
+        for (int v = threadIdx.x; v < nvec; v += kShThreads) {
+            const int e = v << 2;
+            float vals[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int ek = e + k;
+                const int rr = ek / S::ROW;
+                vals[k] = s_buf[rr * S::PITCH + (ek - rr * S::ROW)];
+            }
+            dst4[v] = make_float4(vals[0], vals[1], vals[2], vals[3]);
+        }
+        for (int e = (nvec << 2) + threadIdx.x; e < total; e += kShThreads) {
+            const int rr = e / S::ROW;
+            dst[e] = s_buf[rr * S::PITCH + (e - rr * S::ROW)];
+        }
+    } else {
+        for (int e = threadIdx.x; e < total; e += kShThreads) {
+            const int rr = e / rowlen;
+            const int col = e - rr * rowlen;
+            dst[e] = col < S::ROW ? s_buf[rr * S::PITCH + col] : 0.f;
+        }
+    }
+}
+
 }  // namespace
 }  // namespace gs
 
@@ -402,4 +614,71 @@ extern "C" int gsplat_sh_bwd(int64_t M, int32_t K, int32_t degree,
     default: GS_SH_LAUNCH(sh_bwd_kernel, 4, M, K, dirs, coeffs, masks, v_colors, v_coeffs, v_dirs, vec_ok); break;
     }
     return check_launch("sh_bwd_kernel");
+}
+
+#define GS_SH_ROWS_LAUNCH(KERNEL, DEG, ...)                                    \
+    KERNEL<DEG><<<grid, kShThreads, 0, st>>>(__VA_ARGS__)
+
+static int sh_rows_check(int64_t B, int64_t C, int64_t N, int32_t K,
+                         int32_t degree, const float *means, const float *campos,
+                         const float *coeffs, const int32_t *row_of) {
+    GS_REQUIRE(B >= 0 && C >= 0 && N >= 0, "sh_rows: negative size");
+    GS_REQUIRE(degree >= 0 && degree <= 4, "sh_rows: degree must be in [0, 4]");
+    GS_REQUIRE((degree + 1) * (degree + 1) <= K,
+               "sh_rows: K must be >= (degree + 1)^2");
+    if (B * N > 0)
+        GS_REQUIRE(means && campos && coeffs && row_of, "sh_rows: NULL input");
+    return GSPLAT_OK;
+}
+
+extern "C" int gsplat_sh_rows_fwd(int64_t B, int64_t C, int64_t N, int32_t K,
+                                  int32_t degree, const float *means,
+                                  const float *campos, const float *coeffs,
+                                  const int32_t *row_of, float *colors,
+                                  gsplat_stream_t stream) {
+    clear_error();
+    GS_TRY(sh_rows_check(B, C, N, K, degree, means, campos, coeffs, row_of));
+    if (B * N == 0 || C == 0)
+        return GSPLAT_OK;
+    GS_REQUIRE(colors != nullptr, "sh_rows_fwd: NULL colors");
+    const int nb = (degree + 1) * (degree + 1);
+    ShRowsArgs a{B, C, N, K, means, campos, coeffs, row_of,
+                 (K == nb) && aligned16(coeffs)};
+    const dim3 grid((unsigned)ceil_div(B * N, kShThreads));
+    hipStream_t st = as_stream(stream);
+    switch (degree) {
+    case 0: GS_SH_ROWS_LAUNCH(sh_rows_fwd_kernel, 0, a, colors); break;
+    case 1: GS_SH_ROWS_LAUNCH(sh_rows_fwd_kernel, 1, a, colors); break;
+    case 2: GS_SH_ROWS_LAUNCH(sh_rows_fwd_kernel, 2, a, colors); break;
+    case 3: GS_SH_ROWS_LAUNCH(sh_rows_fwd_kernel, 3, a, colors); break;
+    default: GS_SH_ROWS_LAUNCH(sh_rows_fwd_kernel, 4, a, colors); break;
+    }
+    return check_launch("sh_rows_fwd_kernel");
+}
+
+extern "C" int gsplat_sh_rows_bwd(int64_t B, int64_t C, int64_t N, int32_t K,
+                                  int32_t degree, const float *means,
+                                  const float *campos, const float *coeffs,
+                                  const int32_t *row_of, const float *v_colors,
+                                  float *v_coeffs, float *v_means,
+                                  gsplat_stream_t stream) {
+    clear_error();
+    GS_TRY(sh_rows_check(B, C, N, K, degree, means, campos, coeffs, row_of));
+    if (B * N == 0)
+        return GSPLAT_OK;
+    GS_REQUIRE(v_coeffs && v_means, "sh_rows_bwd: NULL output");
+    GS_REQUIRE(C == 0 || v_colors != nullptr, "sh_rows_bwd: NULL v_colors");
+    const int nb = (degree + 1) * (degree + 1);
+    ShRowsArgs a{B, C, N, K, means, campos, coeffs, row_of,
+                 (K == nb) && aligned16(coeffs) && aligned16(v_coeffs)};
+    const dim3 grid((unsigned)ceil_div(B * N, kShThreads));
+    hipStream_t st = as_stream(stream);
+    switch (degree) {
+    case 0: GS_SH_ROWS_LAUNCH(sh_rows_bwd_kernel, 0, a, v_colors, v_coeffs, v_means); break;
+    case 1: GS_SH_ROWS_LAUNCH(sh_rows_bwd_kernel, 1, a, v_colors, v_coeffs, v_means); break;
+    case 2: GS_SH_ROWS_LAUNCH(sh_rows_bwd_kernel, 2, a, v_colors, v_coeffs, v_means); break;
+    case 3: GS_SH_ROWS_LAUNCH(sh_rows_bwd_kernel, 3, a, v_colors, v_coeffs, v_means); break;
+    default: GS_SH_ROWS_LAUNCH(sh_rows_bwd_kernel, 4, a, v_colors, v_coeffs, v_means); break;
+    }
+    return check_launch("sh_rows_bwd_kernel");
 }

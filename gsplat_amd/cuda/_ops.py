@@ -178,6 +178,70 @@ def projection_ewa_3dgs_fused_bwd(
     return v_means, v_covars, v_quats, v_scales, v_viewmats
 
 
+def projection_packed_fwd_with_row_map(
+    means: Tensor,
+    covars: Optional[Tensor],
+    quats: Optional[Tensor],
+    scales: Optional[Tensor],
+    opacities: Optional[Tensor],
+    viewmats: Tensor,
+    Ks: Tensor,
+    image_width: int,
+    image_height: int,
+    eps2d: float,
+    near_plane: float,
+    far_plane: float,
+    radius_clip: float,
+    calc_compensations: bool,
+    camera_model: int,
+):
+    """The packed projection's nine outputs plus ``row_of`` [B*C*N] int32:
+    the packed row of every (b, c, g), or -1 (the inverse of the id arrays,
+    used by the gathers of the packed rasterization path)."""
+    _check_proj_inputs(means, covars, quats, scales, opacities, viewmats, Ks)
+    batch_dims, B, C, N = _proj_dims(means, viewmats)
+    dev = means.device
+    cap = B * C * N
+    indptr = torch.empty(B * C + 1, dtype=_I32, device=dev)
+    batch_ids = torch.empty(cap, dtype=_I64, device=dev)
+    camera_ids = torch.empty(cap, dtype=_I64, device=dev)
+    gaussian_ids = torch.empty(cap, dtype=_I64, device=dev)
+    radii = torch.empty(cap, 2, dtype=_I32, device=dev)
+    means2d = torch.empty(cap, 2, dtype=_F32, device=dev)
+    depths = torch.empty(cap, dtype=_F32, device=dev)
+    conics = torch.empty(cap, 3, dtype=_F32, device=dev)
+    comps = torch.empty(cap, dtype=_F32, device=dev) if calc_compensations else None
+    row_of = torch.empty(cap, dtype=_I32, device=dev)
+    if cap == 0:
+        indptr.zero_()
+        nnz = 0
+    else:
+        ws = torch.empty(query("gsplat_projection_packed_workspace_size", B, C, N),
+                         dtype=torch.uint8, device=dev)
+        nnz_dev = torch.empty(1, dtype=_I64, device=dev)
+        call("gsplat_projection_packed_fwd", B, C, N, ptr(means), ptr(covars),
+             ptr(quats), ptr(scales), ptr(opacities), ptr(viewmats), ptr(Ks),
+             int(image_width), int(image_height), float(eps2d),
+             float(near_plane), float(far_plane), float(radius_clip),
+             int(camera_model), ptr(ws), ws.numel(), ptr(indptr),
+             ptr(batch_ids), ptr(camera_ids), ptr(gaussian_ids), ptr(radii),
+             ptr(means2d), ptr(depths), ptr(conics), ptr(comps), ptr(nnz_dev),
+             ptr(row_of), _stream(means))
+        nnz = int(nnz_dev.item())
+    return (
+        indptr,
+        batch_ids[:nnz],
+        camera_ids[:nnz],
+        gaussian_ids[:nnz],
+        radii[:nnz],
+        means2d[:nnz],
+        depths[:nnz],
+        conics[:nnz],
+        comps[:nnz] if comps is not None else None,
+        row_of,
+    )
+
+
 def projection_ewa_3dgs_packed_fwd(
     means: Tensor,
     covars: Optional[Tensor],
@@ -195,46 +259,10 @@ def projection_ewa_3dgs_packed_fwd(
     calc_compensations: bool,
     camera_model: int,
 ):
-    _check_proj_inputs(means, covars, quats, scales, opacities, viewmats, Ks)
-    batch_dims, B, C, N = _proj_dims(means, viewmats)
-    dev = means.device
-    cap = B * C * N
-    indptr = torch.empty(B * C + 1, dtype=_I32, device=dev)
-    batch_ids = torch.empty(cap, dtype=_I64, device=dev)
-    camera_ids = torch.empty(cap, dtype=_I64, device=dev)
-    gaussian_ids = torch.empty(cap, dtype=_I64, device=dev)
-    radii = torch.empty(cap, 2, dtype=_I32, device=dev)
-    means2d = torch.empty(cap, 2, dtype=_F32, device=dev)
-    depths = torch.empty(cap, dtype=_F32, device=dev)
-    conics = torch.empty(cap, 3, dtype=_F32, device=dev)
-    comps = torch.empty(cap, dtype=_F32, device=dev) if calc_compensations else None
-    if cap == 0:
-        indptr.zero_()
-        nnz = 0
-    else:
-        ws = torch.empty(query("gsplat_projection_packed_workspace_size", B, C, N),
-                         dtype=torch.uint8, device=dev)
-        nnz_dev = torch.empty(1, dtype=_I64, device=dev)
-        call("gsplat_projection_packed_fwd", B, C, N, ptr(means), ptr(covars),
-             ptr(quats), ptr(scales), ptr(opacities), ptr(viewmats), ptr(Ks),
-             int(image_width), int(image_height), float(eps2d),
-             float(near_plane), float(far_plane), float(radius_clip),
-             int(camera_model), ptr(ws), ws.numel(), ptr(indptr),
-             ptr(batch_ids), ptr(camera_ids), ptr(gaussian_ids), ptr(radii),
-             ptr(means2d), ptr(depths), ptr(conics), ptr(comps), ptr(nnz_dev),
-             _stream(means))
-        nnz = int(nnz_dev.item())
-    return (
-        indptr,
-        batch_ids[:nnz],
-        camera_ids[:nnz],
-        gaussian_ids[:nnz],
-        radii[:nnz],
-        means2d[:nnz],
-        depths[:nnz],
-        conics[:nnz],
-        comps[:nnz] if comps is not None else None,
-    )
+    return projection_packed_fwd_with_row_map(
+        means, covars, quats, scales, opacities, viewmats, Ks, image_width,
+        image_height, eps2d, near_plane, far_plane, radius_clip,
+        calc_compensations, camera_model)[:9]
 
 
 def projection_ewa_3dgs_packed_bwd(
@@ -294,6 +322,61 @@ def projection_ewa_3dgs_packed_bwd(
          int(bool(sparse_grad)), ptr(v_means), ptr(v_covars), ptr(v_quats),
          ptr(v_scales), ptr(v_viewmats), _stream(means))
     return v_means, v_covars, v_quats, v_scales, v_viewmats
+
+
+# --------------------------------------------------------------------------
+# Packed rows driven by Gaussian (replace the gathers / index_put scatters of
+# the packed path, rendering.py:95-213, 782, 845-873)
+# --------------------------------------------------------------------------
+def sh_rows_fwd(degree: int, means: Tensor, campos: Tensor, coeffs: Tensor,
+                row_of: Tensor, nnz: int) -> Tensor:
+    """colors [nnz, 3] = max(SH(normalize(mean - campos)) + 0.5, 0) for every
+    packed row; means [B, N, 3], campos [B, C, 3], coeffs [B, N, K, 3]."""
+    for t, n in ((means, "means"), (campos, "campos"), (coeffs, "coeffs")):
+        check_input(t, n, _F32)
+    check_input(row_of, "row_of", _I32)
+    B, N = means.shape[0], means.shape[1]
+    C = campos.shape[1]
+    K = coeffs.shape[-2]
+    colors = torch.empty(nnz, 3, dtype=_F32, device=means.device)
+    call("gsplat_sh_rows_fwd", B, C, N, K, int(degree), ptr(means), ptr(campos),
+         ptr(coeffs), ptr(row_of), ptr(colors), _stream(means))
+    return colors
+
+
+def sh_rows_bwd(degree: int, means: Tensor, campos: Tensor, coeffs: Tensor,
+                row_of: Tensor, v_colors: Tensor) -> Tuple[Tensor, Tensor]:
+    check_input(v_colors, "v_colors", _F32)
+    B, N = means.shape[0], means.shape[1]
+    C = campos.shape[1]
+    K = coeffs.shape[-2]
+    v_coeffs = torch.empty_like(coeffs)
+    v_means = torch.empty_like(means)
+    call("gsplat_sh_rows_bwd", B, C, N, K, int(degree), ptr(means), ptr(campos),
+         ptr(coeffs), ptr(row_of), ptr(v_colors), ptr(v_coeffs), ptr(v_means),
+         _stream(means))
+    return v_coeffs, v_means
+
+
+def rows_gather(src: Tensor, row_of: Tensor, C: int, nnz: int) -> Tensor:
+    """out [nnz, F] with out[row_of[b, c, g]] = src[b, g]; src [B, N, F]."""
+    check_input(src, "src", _F32)
+    check_input(row_of, "row_of", _I32)
+    B, N, F = src.shape
+    out = torch.empty(nnz, F, dtype=_F32, device=src.device)
+    call("gsplat_rows_gather", B, int(C), N, F, ptr(src), ptr(row_of), ptr(out),
+         _stream(src))
+    return out
+
+
+def rows_scatter_sum(v_out: Tensor, row_of: Tensor, B: int, C: int, N: int) -> Tensor:
+    """v_src [B, N, F]: per Gaussian, the sum of its rows' gradients."""
+    check_input(v_out, "v_out", _F32)
+    F = v_out.shape[-1]
+    v_src = torch.empty(B, N, F, dtype=_F32, device=v_out.device)
+    call("gsplat_rows_scatter_sum", int(B), int(C), int(N), F, ptr(row_of),
+         ptr(v_out), ptr(v_src), _stream(v_out))
+    return v_src
 
 
 # --------------------------------------------------------------------------

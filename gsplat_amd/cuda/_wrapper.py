@@ -139,6 +139,16 @@ def fully_fused_projection(
     means2d, depths, conics, compensations) over the nnz visible rows; else
     (radii, means2d, depths, conics, compensations) of shape [..., C, N, *].
     """
+    out = _project(means, covars, quats, scales, viewmats, Ks, width, height,
+                   eps2d, near_plane, far_plane, radius_clip, packed, sparse_grad,
+                   calc_compensations, camera_model, opacities)
+    return out[:9] if packed else out
+
+
+def _project(means, covars, quats, scales, viewmats, Ks, width, height, eps2d,
+             near_plane, far_plane, radius_clip, packed, sparse_grad,
+             calc_compensations, camera_model, opacities):
+    """fully_fused_projection; the packed form also returns ``row_of``."""
     batch_dims = means.shape[:-2]
     N = means.shape[-2]
     C = viewmats.shape[-3]
@@ -419,7 +429,10 @@ class _FullyFusedProjection(torch.autograd.Function):
 
 
 class _FullyFusedProjectionPacked(torch.autograd.Function):
-    """Projects Gaussians to 2D; returns the visible rows packed."""
+    """Projects Gaussians to 2D; returns the visible rows packed, followed by
+    ``row_of`` [B*C*N] int32 (the packed row of each (b, c, g), or -1), which
+    ``fully_fused_projection`` drops and ``rasterization`` uses for its
+    per-Gaussian gathers."""
 
     @staticmethod
     def forward(
@@ -443,10 +456,9 @@ class _FullyFusedProjectionPacked(torch.autograd.Function):
     ):
         cm = _camera_model_type(camera_model)
         (indptr, batch_ids, camera_ids, gaussian_ids, radii, means2d, depths,
-         conics, compensations) = _make_lazy_cuda_func(
-            "projection_ewa_3dgs_packed_fwd"
-        )(means, covars, quats, scales, opacities, viewmats, Ks, width, height,
-          eps2d, near_plane, far_plane, radius_clip, calc_compensations, cm)
+         conics, compensations, row_of) = _ops.projection_packed_fwd_with_row_map(
+            means, covars, quats, scales, opacities, viewmats, Ks, width, height,
+            eps2d, near_plane, far_plane, radius_clip, calc_compensations, cm)
         if not calc_compensations:
             compensations = None
         ctx.save_for_backward(batch_ids, camera_ids, gaussian_ids, means, covars,
@@ -456,13 +468,14 @@ class _FullyFusedProjectionPacked(torch.autograd.Function):
         ctx.eps2d = eps2d
         ctx.sparse_grad = sparse_grad
         ctx.camera_model_type = cm
-        ctx.mark_non_differentiable(batch_ids, camera_ids, gaussian_ids, indptr, radii)
+        ctx.mark_non_differentiable(batch_ids, camera_ids, gaussian_ids, indptr, radii,
+                                    row_of)
         return (batch_ids, camera_ids, gaussian_ids, indptr, radii, means2d,
-                depths, conics, compensations)
+                depths, conics, compensations, row_of)
 
     @staticmethod
     def backward(ctx, v_batch_ids, v_camera_ids, v_gaussian_ids, v_indptr,
-                 v_radii, v_means2d, v_depths, v_conics, v_compensations):
+                 v_radii, v_means2d, v_depths, v_conics, v_compensations, v_row_of):
         (batch_ids, camera_ids, gaussian_ids, means, covars, quats, scales,
          viewmats, Ks, conics, compensations) = ctx.saved_tensors
         sparse_grad = ctx.sparse_grad
@@ -525,6 +538,53 @@ class _SphericalHarmonics(torch.autograd.Function):
         if not compute_v_dirs:
             v_dirs = None
         return None, v_dirs, v_coeffs, None
+
+
+class _PackedRowsGather(torch.autograd.Function):
+    """out[row_of[b, c, g]] = src[b, g]: a per-Gaussian feature to its packed
+    rows (the reference indexes src[batch_ids, gaussian_ids],
+    rendering.py:782, 170-213).  Backward sums each Gaussian's rows, driven
+    by Gaussian (no index_put)."""
+
+    @staticmethod
+    def forward(ctx, src: Tensor, row_of: Tensor, C: int, nnz: int):
+        ctx.save_for_backward(row_of)
+        ctx.dims = (src.shape[0], C, src.shape[1])
+        return _ops.rows_gather(src.contiguous(), row_of, C, nnz)
+
+    @staticmethod
+    def backward(ctx, v_out: Tensor):
+        (row_of,) = ctx.saved_tensors
+        B, C, N = ctx.dims
+        v_src = None
+        if ctx.needs_input_grad[0]:
+            v_src = _ops.rows_scatter_sum(v_out.contiguous(), row_of, B, C, N)
+        return v_src, None, None, None
+
+
+class _PackedSphericalHarmonics(torch.autograd.Function):
+    """Clamped SH colour of every packed row, max(SH(mean - campos) + 0.5, 0),
+    evaluated per Gaussian (the reference's compute_directions + gathers +
+    spherical_harmonics + clamp_min, rendering.py:227-253, 845-873)."""
+
+    @staticmethod
+    def forward(ctx, degree: int, means: Tensor, coeffs: Tensor, campos: Tensor,
+                row_of: Tensor, nnz: int):
+        means = means.contiguous()
+        coeffs = coeffs.contiguous()
+        campos = campos.contiguous()
+        colors = _ops.sh_rows_fwd(degree, means, campos, coeffs, row_of, nnz)
+        ctx.save_for_backward(means, coeffs, campos, row_of)
+        ctx.degree = degree
+        return colors
+
+    @staticmethod
+    def backward(ctx, v_colors: Tensor):
+        means, coeffs, campos, row_of = ctx.saved_tensors
+        v_coeffs, v_means = _ops.sh_rows_bwd(ctx.degree, means, campos, coeffs,
+                                             row_of, v_colors.contiguous())
+        return (None, v_means if ctx.needs_input_grad[1] else None,
+                v_coeffs if ctx.needs_input_grad[2] else None, None, None, None)
 
 
 class _RasterizeToPixels(torch.autograd.Function):

@@ -21,7 +21,9 @@ from typing_extensions import Literal
 
 from .cuda._wrapper import (
     CameraModel,
-    fully_fused_projection,
+    _PackedRowsGather,
+    _PackedSphericalHarmonics,
+    _project,
     isect_offset_encode,
     isect_tiles,
     rasterize_to_pixels,
@@ -219,17 +221,20 @@ def rasterization(
     if extra_signals is not None:
         check_features(extra_signals, extra_signals_sh_degree, "extra signals")
 
-    proj_results = fully_fused_projection(
-        means, covars, quats, scales, viewmats, Ks, width, height,
-        eps2d=eps2d, packed=packed, near_plane=near_plane, far_plane=far_plane,
-        radius_clip=radius_clip, sparse_grad=sparse_grad,
-        calc_compensations=(rasterize_mode == "antialiased"),
-        camera_model=camera_model, opacities=opacities,
+    proj_results = _project(
+        means, covars, quats, scales, viewmats, Ks, width, height, eps2d,
+        near_plane, far_plane, radius_clip, packed, sparse_grad,
+        rasterize_mode == "antialiased", camera_model, opacities,
     )
+    row_of = None
     if packed:
         (batch_ids, camera_ids, gaussian_ids, indptr, radii, means2d, depths,
-         conics, compensations) = proj_results
-        opacities = opacities.reshape(B, N)[batch_ids, gaussian_ids]
+         conics, compensations, row_of) = proj_results
+        nnz = means2d.shape[0]
+        # per-Gaussian -> packed rows through the inverse map (a gather whose
+        # backward is a per-Gaussian sum, not an index_put)
+        opacities = _PackedRowsGather.apply(
+            opacities.reshape(B, N, 1), row_of, C, nnz).reshape(nnz)
         image_ids = batch_ids * C + camera_ids
     else:
         radii, means2d, depths, conics, compensations = proj_results
@@ -247,7 +252,24 @@ def rasterization(
 
     colors_sh_degree = sh_degree if has_color else None
     proj_features = None
-    if colors_sh_degree is None and extra_signals_sh_degree is None:
+    per_gaussian_colors = has_color and (
+        colors.shape[:num_batch_dims + 1] == batch_dims + (N,)
+        and colors.dim() == num_batch_dims + (2 if colors_sh_degree is None else 3))
+    fused_packed = (packed and extra_signals is None and has_color
+                    and per_gaussian_colors and not viewmats.requires_grad)
+    if fused_packed:
+        # packed rows with per-Gaussian colours: gather (or SH-evaluate) per
+        # Gaussian through row_of instead of indexing [nnz, ...] copies
+        if colors_sh_degree is None:
+            proj_features = _PackedRowsGather.apply(
+                colors.reshape(B, N, D), row_of, C, nnz)
+        else:
+            campos = viewmat_to_camera_position(viewmats).reshape(B, C, 3)
+            K = colors.shape[-2]
+            proj_features = _PackedSphericalHarmonics.apply(
+                colors_sh_degree, means.reshape(B, N, 3), colors.reshape(B, N, K, 3),
+                campos.detach(), row_of, nnz)
+    elif colors_sh_degree is None and extra_signals_sh_degree is None:
         feature_list = []
         if has_color:
             feature_list.append(colors)

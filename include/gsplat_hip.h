@@ -113,7 +113,9 @@ size_t gsplat_projection_packed_workspace_size(int64_t B, int64_t C, int64_t N);
  *        gsplat/cuda/csrc/ProjectionEWA3DGSPacked.cu:39-398).
  * Every per-row output must have capacity for B*C*N rows; the number of rows
  * written (nnz) is stored to nnz_out (device int64).  indptr [B*C+1] int32;
- * batch_ids, camera_ids, gaussian_ids int64. */
+ * batch_ids, camera_ids, gaussian_ids int64.  row_of [B*C*N] int32
+ * (optional) receives, for every (b, c, g), its packed row or -1: the inverse
+ * of (batch_ids, camera_ids, gaussian_ids), used by the gathers below. */
 int gsplat_projection_packed_fwd(
     int64_t B, int64_t C, int64_t N,
     const float *means, const float *covars, const float *quats,
@@ -125,7 +127,7 @@ int gsplat_projection_packed_fwd(
     void *workspace, size_t workspace_bytes,
     int32_t *indptr, int64_t *batch_ids, int64_t *camera_ids,
     int64_t *gaussian_ids, int32_t *radii, float *means2d, float *depths,
-    float *conics, float *compensations, int64_t *nnz_out,
+    float *conics, float *compensations, int64_t *nnz_out, int32_t *row_of,
     gsplat_stream_t stream);
 
 /* Backward of the packed projection over nnz rows.
@@ -177,6 +179,48 @@ int gsplat_sh_bwd(
     const float *dirs, const float *coeffs, const uint8_t *masks,
     const float *v_colors, float *v_coeffs, float *v_dirs,
     gsplat_stream_t stream);
+
+/* SH colour of every packed row, driven by Gaussian (fuses the gathers the
+ * packed path of rasterization() performs before SH).
+ * Replaces, for packed rows, compute_directions + normalize_features_layout
+ * + spherical_harmonics + clamp_min(colors + 0.5, 0)
+ *   (gsplat/rendering.py:227-253, 170-213, 845-873;
+ *    gsplat/cuda/csrc/SphericalHarmonicsCUDA.cu:391-462).
+ * means [B,N,3], campos [B,C,3] (camera centres), coeffs [B,N,K,3],
+ * row_of [B,C,N] (packed row of (b,c,g) or -1, from
+ * gsplat_projection_packed_fwd); writes colors [nnz,3] =
+ * max(SH(normalize(mean - campos)) + 0.5, 0) for every packed row. */
+int gsplat_sh_rows_fwd(
+    int64_t B, int64_t C, int64_t N, int32_t K, int32_t degree,
+    const float *means, const float *campos, const float *coeffs,
+    const int32_t *row_of, float *colors, gsplat_stream_t stream);
+
+/* Backward of gsplat_sh_rows_fwd.  Replaces spherical_harmonics_bwd plus
+ * the index_put scatters of the coefficient and direction gradients
+ *   (gsplat/cuda/csrc/SphericalHarmonicsCUDA.cu:465-552;
+ *    autograd of gsplat/rendering.py:95-213).
+ * v_colors [nnz,3]; v_coeffs [B,N,K,3] and v_means [B,N,3] are fully
+ * written (zeros for Gaussians visible nowhere), summed over cameras in
+ * camera order (deterministic). */
+int gsplat_sh_rows_bwd(
+    int64_t B, int64_t C, int64_t N, int32_t K, int32_t degree,
+    const float *means, const float *campos, const float *coeffs,
+    const int32_t *row_of, const float *v_colors, float *v_coeffs,
+    float *v_means, gsplat_stream_t stream);
+
+/* out[row_of[b,c,g]] = src[b,g] for every packed row: the per-Gaussian
+ * feature gather of the packed path (opacities / colours,
+ * gsplat/rendering.py:782, 170-213).  src [B,N,F], out [nnz,F]. */
+int gsplat_rows_gather(
+    int64_t B, int64_t C, int64_t N, int32_t F, const float *src,
+    const int32_t *row_of, float *out, gsplat_stream_t stream);
+
+/* v_src[b,g] = sum over c of v_out[row_of[b,c,g]] (rows that exist): the
+ * gradient of gsplat_rows_gather, replacing the autograd index_put of the
+ * reference's gathers.  v_src [B,N,F] is fully written. */
+int gsplat_rows_scatter_sum(
+    int64_t B, int64_t C, int64_t N, int32_t F, const int32_t *row_of,
+    const float *v_out, float *v_src, gsplat_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* Tile intersection.                                                        */

@@ -1,0 +1,89 @@
+"""Per-Gaussian gathers of the packed path (rendering.py:95-213, 782,
+845-873) driven by the projection's inverse map ``row_of``: against plain
+indexing (gather: bit-exact), a float64 index_add (scatter), and autograd of
+the float64 SH restatement of gather + normalize + SH + clamp_min(+0.5, 0)
+(fused SH rows)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import torch_ref
+from tests._util import DEV, assert_close, assert_grad_close, small_scene
+
+pytestmark = pytest.mark.gpu
+
+
+def _packed(seed, N, C):
+    from gsplat_amd.cuda import _ops
+    means, quats, scales, opac, vm, K, W, H = small_scene(seed=seed, N=N, C=C)
+    out = _ops.projection_packed_fwd_with_row_map(
+        means.to(DEV), None, quats.to(DEV), scales.to(DEV), opac.to(DEV),
+        vm.to(DEV), K.to(DEV), W, H, 0.3, 0.01, 1e10, 0.0, False, 0)
+    indptr, b, c, g, radii, m2, dep, con, comp, row_of = out
+    return means, vm, b.cpu(), c.cpu(), g.cpu(), row_of, m2.shape[0]
+
+
+@pytest.mark.parametrize("C", [1, 3])
+def test_row_map_is_the_inverse_of_the_ids(C):
+    means, vm, b, c, g, row_of, nnz = _packed(1, 2000, C)
+    ro = row_of.cpu().numpy().reshape(C, -1)
+    N = means.shape[0]
+    expect = np.full((C, N), -1, np.int64)
+    expect[c.numpy(), g.numpy()] = np.arange(nnz)
+    np.testing.assert_array_equal(ro, expect)
+
+
+@pytest.mark.parametrize("C,F", [(1, 1), (3, 1), (3, 3), (2, 5)])
+def test_rows_gather_and_scatter(C, F):
+    from gsplat_amd.cuda import _ops
+    means, vm, b, c, g, row_of, nnz = _packed(2, 3000, C)
+    N = means.shape[0]
+    gen = torch.Generator().manual_seed(5)
+    src = torch.randn(1, N, F, generator=gen)
+    out = _ops.rows_gather(src.to(DEV), row_of, C, nnz)
+    assert torch.equal(out.cpu(), src[0, g])
+    v_out = torch.randn(nnz, F, generator=gen)
+    v_src = _ops.rows_scatter_sum(v_out.to(DEV), row_of, 1, C, N)
+    ref = torch.zeros(N, F, dtype=torch.float64).index_add_(0, g, v_out.double())
+    assert_close(v_src.cpu()[0], ref, 1e-6, 1e-7, "v_src")
+    # Gaussians visible nowhere get an explicit zero row
+    seen = torch.zeros(N, dtype=torch.bool)
+    seen[g] = True
+    assert bool((v_src.cpu()[0][~seen] == 0).all())
+
+
+@pytest.mark.parametrize("degree,C", [(0, 1), (1, 3), (2, 2), (3, 1), (3, 3), (4, 2)])
+def test_sh_rows_fwd_bwd(degree, C):
+    from gsplat_amd.cuda._wrapper import _PackedSphericalHarmonics
+    from gsplat_amd.rendering import viewmat_to_camera_position
+    means, vm, b, c, g, row_of, nnz = _packed(3 + degree, 2500, C)
+    N = means.shape[0]
+    K = (degree + 1) ** 2 + (3 if degree == 2 else 0)  # one case with extra bands
+    gen = torch.Generator().manual_seed(degree)
+    coeffs = torch.randn(N, K, 3, generator=gen) * 0.4
+    campos = viewmat_to_camera_position(vm)
+    v_col = torch.randn(nnz, 3, generator=gen)
+
+    gm = means.clone().to(DEV).requires_grad_()
+    gc = coeffs.clone().to(DEV).requires_grad_()
+    col = _PackedSphericalHarmonics.apply(degree, gm[None], gc[None],
+                                          campos[None].to(DEV), row_of, nnz)
+    (col * v_col.to(DEV)).sum().backward()
+
+    def ref(dtype):
+        m = means.to(dtype).requires_grad_()
+        cf = coeffs.to(dtype).requires_grad_()
+        dirs = m[g] - campos.to(dtype)[c]
+        out = torch.clamp_min(
+            torch_ref.spherical_harmonics_ref(degree, dirs, cf[g]) + 0.5, 0.0)
+        (out * v_col.to(dtype)).sum().backward()
+        # degree 0 does not depend on the direction: no graph to the means
+        mg = m.grad if m.grad is not None else torch.zeros_like(m)
+        return out, mg, cf.grad
+
+    r64, m64, c64 = ref(torch.float64)
+    r32, m32, c32 = ref(torch.float32)
+    assert_close(col.cpu(), r64.detach(), 1e-4, 1e-5, "colors")
+    print(assert_grad_close(gc.grad, c64, c32, 1e-4, 1e-5, "v_coeffs"))
+    print(assert_grad_close(gm.grad, m64, m32, 1e-4, 1e-5, "v_means"))
