@@ -151,6 +151,35 @@ constexpr int kDppQuadXor2 = 0x4E;   // quad_perm:[2,3,0,1]
 constexpr int kDppRowHalfMirror = 0x141;
 constexpr int kDppRowMirror = 0x140;
 
+constexpr int kDppRowBcast15 = 0x142;  // lane 15 of each row -> next row
+constexpr int kDppRowBcast31 = 0x143;  // lane 31 -> rows 2 and 3
+
+// DPP move restricted to the rows set in ROW_MASK; rows outside the mask
+// (and out-of-range sources) read 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f32_rows(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(
+        0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+
+// Sum over the first ROWS (1 or 4) 16-lane rows of a wave, branch free: the
+// row-local butterflies leave every lane with its row's sum, then the two row
+// broadcasts fold rows 0-3 into row 3.  The total is in lane 16 * ROWS - 1
+// (other lanes hold partial sums).  Every lane of those rows must be active.
+template <int ROWS>
+__device__ __forceinline__ float wave_sum_to_last(float v) {
+    static_assert(ROWS == 1 || ROWS == 4, "ROWS must be 1 or 4");
+    v += dpp_f32_rows<0xB1, 0xF>(v);   // quad_perm:[1,0,3,2]
+    v += dpp_f32_rows<0x4E, 0xF>(v);   // quad_perm:[2,3,0,1]
+    v += dpp_f32_rows<0x141, 0xF>(v);  // row_half_mirror
+    v += dpp_f32_rows<0x140, 0xF>(v);  // row_mirror
+    if (ROWS == 4) {
+        v += dpp_f32_rows<kDppRowBcast15, 0xA>(v);
+        v += dpp_f32_rows<kDppRowBcast31, 0xC>(v);
+    }
+    return v;
+}
+
 template <int CTRL> __device__ __forceinline__ float dpp_f32(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(
         0, __float_as_int(v), CTRL, 0xF, 0xF, false));

@@ -27,11 +27,13 @@
 // The forward ends a batch early when every pixel of the wave is done (the
 // per-lane loop exits when the wave's exec mask empties) and skips remaining
 // batches once the whole tile is done (__syncthreads_count).
-// The backward recovers T with a double-precision division per Gaussian and
-// reduces each Gaussian's gradient over the wave with DPP row
-// operations, accumulates the 4 waves in LDS (native ds_add_f32) and issues
+// The backward recovers T back to front in double (one Newton-refined
+// reciprocal per Gaussian), reduces each Gaussian's gradient over the wave
+// with a branch-free DPP reduction (row butterflies + row broadcasts, total
+// in the last lane), accumulates the waves in LDS (ds_add_f32) and issues
 // one global atomic per value per Gaussian per TILE, 8x fewer than one per
-// 32-lane warp.
+// 32-lane warp.  Both kernels are compiled per (CDIM, tile size) so every
+// loop bound and reduction count is a constant.
 #include "common.h"
 
 namespace gs {
@@ -75,26 +77,31 @@ __device__ __forceinline__ void tile_coords(const RasterArgs &a, int64_t &image,
     tx = tile - ty * a.tile_width;
 }
 
-constexpr int kMaxTileThreads = 256;
+// 16-lane rows of a wave that hold pixels: 1 for 4x4 tiles (16 threads),
+// 4 for 8x8 (one full wave) and 16x16 (four full waves).
+template <int TILE> struct TileShape {
+    static constexpr int BS = TILE * TILE;
+    static constexpr int ROWS = BS >= 64 ? 4 : BS / 16;
+    static constexpr int LAST = 16 * ROWS - 1;  // lane holding a wave sum
+    static_assert(BS % 16 == 0, "tile must hold whole 16-lane rows");
+};
 
-template <int CDIM>
-__global__ void __launch_bounds__(kMaxTileThreads) rasterize_fwd_kernel(const RasterArgs a,
-                                     float *__restrict__ render_colors,
-                                     float *__restrict__ render_alphas,
-                                     int32_t *__restrict__ last_ids,
-                                     float *__restrict__ render_T) {
-    extern __shared__ float4 s_mem[];
-    const int bs = blockDim.x;  // tile_size^2
-    float4 *s_geo = s_mem;              // (x, y, opacity, sig_max)
-    float4 *s_con = s_mem + bs;         // (a, b, c, sig_clamp)
-    float *s_col = reinterpret_cast<float *>(s_mem + 2 * bs);  // [bs][CDIM]
+template <int CDIM, int TILE>
+__global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
+    const RasterArgs a, float *__restrict__ render_colors,
+    float *__restrict__ render_alphas, int32_t *__restrict__ last_ids,
+    float *__restrict__ render_T) {
+    constexpr int BS = TileShape<TILE>::BS;
+    __shared__ float4 s_geo[BS];          // (x, y, opacity, sig_max)
+    __shared__ float4 s_con[BS];          // (a, b, c, sig_clamp)
+    __shared__ float s_col[BS * CDIM];
 
     int64_t image;
     int32_t tile, ty, tx;
     tile_coords(a, image, tile, ty, tx);
     const int tr = threadIdx.x;
-    const int i = ty * a.tile_size + tr / a.tile_size;
-    const int j = tx * a.tile_size + tr % a.tile_size;
+    const int i = ty * TILE + tr / TILE;
+    const int j = tx * TILE + tr % TILE;
     const bool inside = i < a.H && j < a.W;
     const int64_t pix = ((int64_t)image * a.H + i) * a.W + j;
     const float px = (float)j + 0.5f, py = (float)i + 0.5f;
@@ -119,7 +126,7 @@ __global__ void __launch_bounds__(kMaxTileThreads) rasterize_fwd_kernel(const Ra
     const int32_t range_end = (image == a.I - 1 && tile == n_tiles - 1)
                                   ? (int32_t)a.n_isects
                                   : offs[tile + 1];
-    const int num_batches = (range_end - range_start + bs - 1) / bs;
+    const int num_batches = (range_end - range_start + BS - 1) / BS;
 
     float T = 1.f;
     int32_t cur_idx = 0;
@@ -130,9 +137,9 @@ __global__ void __launch_bounds__(kMaxTileThreads) rasterize_fwd_kernel(const Ra
         acc[k] = 0.f;
 
     for (int b = 0; b < num_batches; ++b) {
-        if (__syncthreads_count(done) >= bs)
+        if (__syncthreads_count(done) >= BS)
             break;
-        const int32_t batch_start = range_start + b * bs;
+        const int32_t batch_start = range_start + b * BS;
         const int32_t idx = batch_start + tr;
         if (idx < range_end) {
             const int32_t g = a.flatten_ids[idx];
@@ -148,7 +155,7 @@ __global__ void __launch_bounds__(kMaxTileThreads) rasterize_fwd_kernel(const Ra
                 s_col[tr * CDIM + k] = a.colors[(int64_t)g * CDIM + k];
         }
         __syncthreads();
-        const int batch_size = min(bs, range_end - batch_start);
+        const int batch_size = min(BS, range_end - batch_start);
         for (int t = 0; t < batch_size && !done; ++t) {
             const float4 geo = s_geo[t];
             const float4 con = s_con[t];
@@ -184,33 +191,25 @@ __global__ void __launch_bounds__(kMaxTileThreads) rasterize_fwd_kernel(const Ra
     }
 }
 
-template <int CDIM> struct BwdAcc {
-    // per-Gaussian accumulated values: xy(2), conic(3), colour(CDIM),
-    // opacity(1), |xy|(2)
-    static constexpr int N = 2 + 3 + CDIM + 1 + 2;
-};
-
-template <int CDIM>
-__global__ void __launch_bounds__(kMaxTileThreads) rasterize_bwd_kernel(const RasterArgs a,
-                                     const float *__restrict__ render_alphas,
-                                     const float *__restrict__ render_T,
-                                     const int32_t *__restrict__ last_ids,
-                                     const float *__restrict__ v_render_colors,
-                                     const float *__restrict__ v_render_alphas,
-                                     float *__restrict__ v_means2d_abs,
-                                     float *__restrict__ v_means2d,
-                                     float *__restrict__ v_conics,
-                                     float *__restrict__ v_colors,
-                                     float *__restrict__ v_opacities) {
-    constexpr int NACC = BwdAcc<CDIM>::N;
-    extern __shared__ float4 s_mem[];
-    const int bs = blockDim.x;
-    float4 *s_geo = s_mem;
-    float4 *s_con = s_mem + bs;
-    float *s_col = reinterpret_cast<float *>(s_mem + 2 * bs);  // [bs][CDIM]
-    float *s_acc = s_col + bs * CDIM;                          // [NACC][bs]
-    int32_t *s_gid = reinterpret_cast<int32_t *>(s_acc + NACC * bs);
-    int32_t *s_hit = s_gid + bs;
+template <int CDIM, int TILE, bool ABS>
+__global__ void __launch_bounds__(TILE * TILE) rasterize_bwd_kernel(
+    const RasterArgs a, const float *__restrict__ render_alphas,
+    const float *__restrict__ render_T, const int32_t *__restrict__ last_ids,
+    const float *__restrict__ v_render_colors,
+    const float *__restrict__ v_render_alphas,
+    float *__restrict__ v_means2d_abs, float *__restrict__ v_means2d,
+    float *__restrict__ v_conics, float *__restrict__ v_colors,
+    float *__restrict__ v_opacities) {
+    using TS = TileShape<TILE>;
+    constexpr int BS = TS::BS;
+    // per-Gaussian sums: xy(2), conic(3), colour(CDIM), opacity(1) [, |xy|(2)]
+    constexpr int NACC = 2 + 3 + CDIM + 1 + (ABS ? 2 : 0);
+    __shared__ float4 s_geo[BS];
+    __shared__ float4 s_con[BS];
+    __shared__ float s_col[BS * CDIM];
+    __shared__ float s_acc[NACC * BS];
+    __shared__ int32_t s_gid[BS];
+    __shared__ int32_t s_hit[BS];
 
     int64_t image;
     int32_t tile, ty, tx;
@@ -219,19 +218,20 @@ __global__ void __launch_bounds__(kMaxTileThreads) rasterize_bwd_kernel(const Ra
     if (a.masks != nullptr && !a.masks[image * n_tiles + tile])
         return;
     const int tr = threadIdx.x;
-    const int i = ty * a.tile_size + tr / a.tile_size;
-    const int j = tx * a.tile_size + tr % a.tile_size;
+    const int i = ty * TILE + tr / TILE;
+    const int j = tx * TILE + tr % TILE;
     const bool inside = i < a.H && j < a.W;
     const int64_t pix = ((int64_t)image * a.H + (inside ? i : 0)) * a.W +
                         (inside ? j : 0);
     const float px = (float)j + 0.5f, py = (float)i + 0.5f;
+    const bool last_lane = lane_id() == (uint32_t)TS::LAST;
 
     const int32_t *offs = a.tile_offsets + image * n_tiles;
     const int32_t range_start = offs[tile];
     const int32_t range_end = (image == a.I - 1 && tile == n_tiles - 1)
                                   ? (int32_t)a.n_isects
                                   : offs[tile + 1];
-    const int num_batches = (range_end - range_start + bs - 1) / bs;
+    const int num_batches = (range_end - range_start + BS - 1) / BS;
 
     // The transmittance itself when the forward stored it: 1 - (1 - T)
     // loses most of T's significant bits once T nears the 1e-4 cutoff.
@@ -239,9 +239,9 @@ __global__ void __launch_bounds__(kMaxTileThreads) rasterize_bwd_kernel(const Ra
         inside ? (render_T != nullptr ? render_T[pix] : 1.f - render_alphas[pix])
                : 1.f;
     // T before each Gaussian is recovered back to front by undoing the
-    // forward's products.  The division runs in double: each step then undoes
-    // one float32 product (the same float32 1 - alpha the forward used) almost
-    // exactly, so T carries only the forward's own rounding instead of one
+    // forward's products.  It is carried in double and each step multiplies
+    // by 1 / (1 - alpha) refined to ~2^-46 by one Newton step from the fp32
+    // reciprocal, so T keeps only the forward's own rounding instead of one
     // extra float32 rounding per Gaussian behind it.
     double T64 = (double)T_final;
     float T = T_final;
@@ -257,12 +257,11 @@ __global__ void __launch_bounds__(kMaxTileThreads) rasterize_bwd_kernel(const Ra
     }
     const float v_a = inside ? v_render_alphas[pix] : 0.f;
     const int32_t wave_bin_final = wave_max_i32(bin_final);
-    const bool want_abs = v_means2d_abs != nullptr;
 
     for (int b = 0; b < num_batches; ++b) {
         __syncthreads();
-        const int32_t batch_end = range_end - 1 - b * bs;
-        const int batch_size = min(bs, batch_end + 1 - range_start);
+        const int32_t batch_end = range_end - 1 - b * BS;
+        const int batch_size = min(BS, batch_end + 1 - range_start);
         const int32_t idx = batch_end - tr;
         if (idx >= range_start) {
             const int32_t g = a.flatten_ids[idx];
@@ -281,7 +280,7 @@ __global__ void __launch_bounds__(kMaxTileThreads) rasterize_bwd_kernel(const Ra
         s_hit[tr] = 0;
 #pragma unroll
         for (int k = 0; k < NACC; ++k)
-            s_acc[k * bs + tr] = 0.f;
+            s_acc[k * BS + tr] = 0.f;
         __syncthreads();
 
         // slots t with isect index batch_end - t > wave_bin_final are behind
@@ -289,36 +288,37 @@ __global__ void __launch_bounds__(kMaxTileThreads) rasterize_bwd_kernel(const Ra
         const int t0 = max(0, batch_end - wave_bin_final);
         for (int t = t0; t < batch_size; ++t) {
             const int32_t isect = batch_end - t;
-            bool valid = inside && isect <= bin_final;
             const float4 geo = s_geo[t];
             const float4 con = s_con[t];
             const float dx = geo.x - px, dy = geo.y - py;
-            float sigma = 0.f, vis = 0.f, alpha = 0.f;
-            if (valid) {
-                sigma = gauss_sigma(con.x, con.y, con.z, dx, dy);
-                if (sigma < 0.f || sigma > geo.w)
-                    valid = false;
-            }
+            const float sigma = gauss_sigma(con.x, con.y, con.z, dx, dy);
+            const bool valid = inside && isect <= bin_final && sigma >= 0.f &&
+                               sigma <= geo.w;
             if (!__ballot(valid))
                 continue;
-            float g_acc[NACC];
+            float g[NACC];
 #pragma unroll
             for (int k = 0; k < NACC; ++k)
-                g_acc[k] = 0.f;
+                g[k] = 0.f;
             if (valid) {
-                vis = portable_expf(-sigma);
+                const float vis = portable_expf(-sigma);
                 const bool clamped = sigma < con.w;
-                alpha = clamped ? kMaxAlpha : geo.z * vis;
+                const float alpha = clamped ? kMaxAlpha : geo.z * vis;
+                // alpha <= 0.99, so 1 - alpha >= 0.01 (the reference's
+                // 1e-6 floor never binds)
                 const float one_minus = fmaxf(kMinOneMinusAlpha, 1.f - alpha);
-                const float ra = 1.f / one_minus;
-                T64 = T64 / (double)one_minus;
+                const float ra = __builtin_amdgcn_rcpf(one_minus);
+                const double d = (double)one_minus;
+                double r = (double)ra;
+                r = __builtin_fma(r, __builtin_fma(-d, r, 1.0), r);
+                T64 = T64 * r;
                 T = (float)T64;
                 const float fac = alpha * T;
                 float v_alpha = 0.f;
 #pragma unroll
                 for (int k = 0; k < CDIM; ++k) {
                     const float ck = s_col[t * CDIM + k];
-                    g_acc[5 + k] = fac * v_c[k];
+                    g[5 + k] = fac * v_c[k];
                     v_alpha += (ck * T - buffer[k] * ra) * v_c[k];
                     buffer[k] += ck * fac;
                 }
@@ -327,56 +327,49 @@ __global__ void __launch_bounds__(kMaxTileThreads) rasterize_bwd_kernel(const Ra
                     v_alpha += -T_final * ra * bg_dot;
                 if (!clamped) {
                     const float v_sigma = -geo.z * vis * v_alpha;
-                    g_acc[2] = 0.5f * v_sigma * dx * dx;
-                    g_acc[3] = v_sigma * dx * dy;
-                    g_acc[4] = 0.5f * v_sigma * dy * dy;
-                    g_acc[0] = v_sigma * (con.x * dx + con.y * dy);
-                    g_acc[1] = v_sigma * (con.y * dx + con.z * dy);
-                    g_acc[5 + CDIM] = vis * v_alpha;
-                    g_acc[6 + CDIM] = fabsf(g_acc[0]);
-                    g_acc[7 + CDIM] = fabsf(g_acc[1]);
+                    g[2] = 0.5f * v_sigma * dx * dx;
+                    g[3] = v_sigma * dx * dy;
+                    g[4] = 0.5f * v_sigma * dy * dy;
+                    g[0] = v_sigma * (con.x * dx + con.y * dy);
+                    g[1] = v_sigma * (con.y * dx + con.z * dy);
+                    g[5 + CDIM] = vis * v_alpha;
+                    if (ABS) {
+                        g[6 + CDIM] = fabsf(g[0]);
+                        g[7 + CDIM] = fabsf(g[1]);
+                    }
                 }
             }
-            const int nred = want_abs ? NACC : NACC - 2;
-            for (int k = 0; k < nred; ++k) {
-                const float s = wave_sum(g_acc[k]);
-                if (lane_id() == 0)
-                    atomicAdd(&s_acc[k * bs + t], s);
-            }
-            if (lane_id() == 0)
+#pragma unroll
+            for (int k = 0; k < NACC; ++k)
+                g[k] = wave_sum_to_last<TS::ROWS>(g[k]);
+            if (last_lane) {
+#pragma unroll
+                for (int k = 0; k < NACC; ++k)
+                    atomicAdd(&s_acc[k * BS + t], g[k]);
                 s_hit[t] = 1;
+            }
         }
         __syncthreads();
         if (tr < batch_size && s_hit[tr]) {
             const int32_t g = s_gid[tr];
-            atomic_add_f32(v_means2d + (int64_t)g * 2 + 0, s_acc[0 * bs + tr]);
-            atomic_add_f32(v_means2d + (int64_t)g * 2 + 1, s_acc[1 * bs + tr]);
-            atomic_add_f32(v_conics + (int64_t)g * 3 + 0, s_acc[2 * bs + tr]);
-            atomic_add_f32(v_conics + (int64_t)g * 3 + 1, s_acc[3 * bs + tr]);
-            atomic_add_f32(v_conics + (int64_t)g * 3 + 2, s_acc[4 * bs + tr]);
+            atomic_add_f32(v_means2d + (int64_t)g * 2 + 0, s_acc[0 * BS + tr]);
+            atomic_add_f32(v_means2d + (int64_t)g * 2 + 1, s_acc[1 * BS + tr]);
+            atomic_add_f32(v_conics + (int64_t)g * 3 + 0, s_acc[2 * BS + tr]);
+            atomic_add_f32(v_conics + (int64_t)g * 3 + 1, s_acc[3 * BS + tr]);
+            atomic_add_f32(v_conics + (int64_t)g * 3 + 2, s_acc[4 * BS + tr]);
 #pragma unroll
             for (int k = 0; k < CDIM; ++k)
                 atomic_add_f32(v_colors + (int64_t)g * CDIM + k,
-                               s_acc[(5 + k) * bs + tr]);
-            atomic_add_f32(v_opacities + g, s_acc[(5 + CDIM) * bs + tr]);
-            if (want_abs) {
+                               s_acc[(5 + k) * BS + tr]);
+            atomic_add_f32(v_opacities + g, s_acc[(5 + CDIM) * BS + tr]);
+            if (ABS) {
                 atomic_add_f32(v_means2d_abs + (int64_t)g * 2 + 0,
-                               s_acc[(6 + CDIM) * bs + tr]);
+                               s_acc[(6 + CDIM) * BS + tr]);
                 atomic_add_f32(v_means2d_abs + (int64_t)g * 2 + 1,
-                               s_acc[(7 + CDIM) * bs + tr]);
+                               s_acc[(7 + CDIM) * BS + tr]);
             }
         }
     }
-}
-
-size_t fwd_smem(int bs, int cdim) {
-    return (size_t)bs * (2 * sizeof(float4) + cdim * sizeof(float));
-}
-
-size_t bwd_smem(int bs, int cdim) {
-    const int nacc = 2 + 3 + cdim + 1 + 2;
-    return (size_t)bs * (2 * sizeof(float4) + cdim * sizeof(float) +
-                         nacc * sizeof(float) + 2 * sizeof(int32_t));
 }
 
 int check_raster(const RasterArgs &a, int cdim) {
@@ -406,19 +399,19 @@ int check_raster(const RasterArgs &a, int cdim) {
     }
 }
 
-#define GS_CDIM_SWITCH(CDIM_VAR, MACRO)                                        \
+#define GS_CDIM_SWITCH(CDIM_VAR, MACRO, ...)                                   \
     switch (CDIM_VAR) {                                                        \
-    case 1: MACRO(1); break;                                                   \
-    case 2: MACRO(2); break;                                                   \
-    case 3: MACRO(3); break;                                                   \
-    case 4: MACRO(4); break;                                                   \
-    case 5: MACRO(5); break;                                                   \
-    case 8: MACRO(8); break;                                                   \
-    case 9: MACRO(9); break;                                                   \
-    case 16: MACRO(16); break;                                                 \
-    case 17: MACRO(17); break;                                                 \
-    case 32: MACRO(32); break;                                                 \
-    default: MACRO(33); break;                                                 \
+    case 1: MACRO(1, __VA_ARGS__); break;                                      \
+    case 2: MACRO(2, __VA_ARGS__); break;                                      \
+    case 3: MACRO(3, __VA_ARGS__); break;                                      \
+    case 4: MACRO(4, __VA_ARGS__); break;                                      \
+    case 5: MACRO(5, __VA_ARGS__); break;                                      \
+    case 8: MACRO(8, __VA_ARGS__); break;                                      \
+    case 9: MACRO(9, __VA_ARGS__); break;                                      \
+    case 16: MACRO(16, __VA_ARGS__); break;                                    \
+    case 17: MACRO(17, __VA_ARGS__); break;                                    \
+    case 32: MACRO(32, __VA_ARGS__); break;                                    \
+    default: MACRO(33, __VA_ARGS__); break;                                    \
     }
 
 }  // namespace
@@ -443,15 +436,19 @@ extern "C" int gsplat_rasterize_fwd(
         return GSPLAT_OK;
     GS_REQUIRE(render_colors && render_alphas && last_ids,
                "rasterize_fwd: NULL output");
-    const int bs = tile_size * tile_size;
     const int64_t blocks = I * (int64_t)tile_width * tile_height;
     GS_REQUIRE(blocks < (1ll << 31), "rasterize_fwd: too many tiles");
     hipStream_t st = as_stream(stream);
-    const size_t smem = fwd_smem(bs, cdim);
-#define GS_FWD(C)                                                              \
-    rasterize_fwd_kernel<C><<<(unsigned)blocks, bs, smem, st>>>(               \
+#define GS_FWD(C, TILE)                                                        \
+    rasterize_fwd_kernel<C, TILE><<<(unsigned)blocks, TILE * TILE, 0, st>>>(   \
         a, render_colors, render_alphas, last_ids, render_transmittance)
-    GS_CDIM_SWITCH(cdim, GS_FWD)
+    if (tile_size == 16) {
+        GS_CDIM_SWITCH(cdim, GS_FWD, 16)
+    } else if (tile_size == 8) {
+        GS_CDIM_SWITCH(cdim, GS_FWD, 8)
+    } else {
+        GS_CDIM_SWITCH(cdim, GS_FWD, 4)
+    }
 #undef GS_FWD
     return check_launch("rasterize_fwd_kernel");
 }
@@ -480,17 +477,26 @@ extern "C" int gsplat_rasterize_bwd(
                "rasterize_bwd: NULL input");
     GS_REQUIRE(v_means2d && v_conics && v_colors && v_opacities,
                "rasterize_bwd: NULL gradient output");
-    const int bs = tile_size * tile_size;
     const int64_t blocks = I * (int64_t)tile_width * tile_height;
     GS_REQUIRE(blocks < (1ll << 31), "rasterize_bwd: too many tiles");
     hipStream_t st = as_stream(stream);
-    const size_t smem = bwd_smem(bs, cdim);
-#define GS_BWD(C)                                                              \
-    rasterize_bwd_kernel<C><<<(unsigned)blocks, bs, smem, st>>>(               \
+#define GS_BWD(C, TILE, ABS)                                                   \
+    rasterize_bwd_kernel<C, TILE, ABS><<<(unsigned)blocks, TILE * TILE, 0,     \
+                                         st>>>(                                \
         a, render_alphas, render_transmittance, last_ids, v_render_colors,     \
-        v_render_alphas,                                                       \
-        v_means2d_abs, v_means2d, v_conics, v_colors, v_opacities)
-    GS_CDIM_SWITCH(cdim, GS_BWD)
+        v_render_alphas, v_means2d_abs, v_means2d, v_conics, v_colors,         \
+        v_opacities)
+    const bool abs = v_means2d_abs != nullptr;
+    if (tile_size == 16) {
+        if (abs) { GS_CDIM_SWITCH(cdim, GS_BWD, 16, true) }
+        else { GS_CDIM_SWITCH(cdim, GS_BWD, 16, false) }
+    } else if (tile_size == 8) {
+        if (abs) { GS_CDIM_SWITCH(cdim, GS_BWD, 8, true) }
+        else { GS_CDIM_SWITCH(cdim, GS_BWD, 8, false) }
+    } else {
+        if (abs) { GS_CDIM_SWITCH(cdim, GS_BWD, 4, true) }
+        else { GS_CDIM_SWITCH(cdim, GS_BWD, 4, false) }
+    }
 #undef GS_BWD
     return check_launch("rasterize_bwd_kernel");
 }
