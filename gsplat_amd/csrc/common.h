@@ -53,7 +53,7 @@ inline hipStream_t as_stream(gsplat_stream_t s) {
     return reinterpret_cast<hipStream_t>(s);
 }
 
-inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 inline bool aligned16(const void *p) {
     return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
@@ -277,6 +277,23 @@ inline Lookback lookback_from(void *ws) {
 // Zero the ticket and status words (a kernel, not a memset, so the sequence
 // stays valid under stream capture).
 int clear_lookback(void *ws, int64_t n_blocks, hipStream_t stream);
+
+// Stable LSD radix sort of (uint64 key, uint32 value) pairs on key bits
+// [begin_bit, end_bit) (sort.hip).  Passes alternate a -> b -> a ...;
+// *result_in_b tells which pair holds the sorted result (the other pair is
+// clobbered).  radix_sort_passes(bits) is the number of passes it makes.
+int radix_sort_passes(int num_bits);
+size_t radix_sort_workspace_bytes(int64_t n);
+int radix_sort_ping_pong(int64_t n, int begin_bit, int end_bit, uint64_t *keys_a,
+                         uint32_t *vals_a, uint64_t *keys_b, uint32_t *vals_b,
+                         void *workspace, size_t workspace_bytes,
+                         hipStream_t st, bool *result_in_b);
+int copy_pairs(int64_t n, const uint64_t *ks, const uint32_t *vs, uint64_t *kd,
+               uint32_t *vd, hipStream_t st);
+// Exclusive prefix sum of n uint32 values; `ws` holds a look-back workspace
+// of lookback_bytes(ceil(n / 2048)) bytes.
+int scan_u32_exclusive(const uint32_t *in, uint32_t *out, int64_t n, void *ws,
+                       hipStream_t st);
 
 __device__ __forceinline__ uint64_t lb_load(const uint64_t *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -249,6 +249,123 @@ __global__ void __launch_bounds__(kIsectThreads)
     row_tiles<true>(a, idx, &em);
 }
 
+// ---------------------------------------------------------------------------
+// Sorted intersection in two stages.
+//
+// The reference sorts the emitted (key, row) pairs on all 32 + tile_bits +
+// image_bits key bits (IntersectTile.cu:478-520).  Its result is the order by
+// (image|tile, depth bits, row): the sort is stable and rows are emitted in
+// ascending order.  The same order is produced here with far fewer bits
+// moved:
+//   1. rows are sorted stably by their depth bits (32-bit keys, one per
+//      row instead of one per intersection);
+//   2. intersections are emitted row by row in that depth order, each row
+//      at the prefix of the depth-ordered counts;
+//   3. one stable radix sort on the image|tile bits only (usually one or two
+//      passes) groups them by tile, keeping depth order (ties by row) inside.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(kIsectThreads)
+    isect_count_keys_kernel(const IsectArgs a, int32_t *__restrict__ tiles_per_gauss,
+                            uint64_t *__restrict__ depth_keys,
+                            uint32_t *__restrict__ rows) {
+    const int64_t idx = (int64_t)blockIdx.x * kIsectThreads + threadIdx.x;
+    if (idx >= a.n)
+        return;
+    tiles_per_gauss[idx] = row_tiles<false>(a, idx, nullptr);
+    depth_keys[idx] = (uint64_t)__float_as_uint(a.depths[idx]);
+    rows[idx] = (uint32_t)idx;
+}
+
+// Inclusive int64 prefix of tiles_per_gauss[order[i]] (decoupled look-back).
+__global__ void __launch_bounds__(kIsectThreads)
+    gather_count_scan_kernel(int64_t n, const uint32_t *__restrict__ order,
+                             const int32_t *__restrict__ tiles_per_gauss,
+                             Lookback lb, int64_t *__restrict__ cum) {
+    __shared__ uint32_t s_ticket;
+    __shared__ uint64_t s_wave_tot[kIsectThreads / kWave];
+    __shared__ uint64_t s_prefix;
+    const uint32_t bid = lb_ticket(lb, &s_ticket);
+    const int64_t i = (int64_t)bid * kIsectThreads + threadIdx.x;
+    const uint64_t cnt = i < n ? (uint64_t)tiles_per_gauss[order[i]] : 0ull;
+    const uint64_t incl = wave_inclusive_scan_u64(cnt);
+    const uint32_t wave = threadIdx.x / kWave;
+    if (lane_id() == kWave - 1)
+        s_wave_tot[wave] = incl;
+    __syncthreads();
+    uint64_t wave_off = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < kIsectThreads / kWave; ++w) {
+        const uint64_t v = s_wave_tot[w];
+        wave_off += (w < (int)wave) ? v : 0ull;
+        total += v;
+    }
+    if (wave == 0) {
+        const uint64_t excl = lb_exclusive_prefix(lb, bid, total);
+        if (lane_id() == 0)
+            s_prefix = excl;
+    }
+    __syncthreads();
+    if (i < n)
+        cum[i] = (int64_t)(s_prefix + wave_off + incl);
+}
+
+__global__ void __launch_bounds__(kIsectThreads)
+    isect_emit_sorted_kernel(const IsectArgs a, const uint32_t *__restrict__ order,
+                             const int64_t *__restrict__ cum,
+                             uint64_t *__restrict__ isect_ids,
+                             uint32_t *__restrict__ flatten_ids) {
+    const int64_t i = (int64_t)blockIdx.x * kIsectThreads + threadIdx.x;
+    if (i >= a.n)
+        return;
+    const int64_t begin = i == 0 ? 0 : cum[i - 1];
+    const int64_t end = cum[i];
+    if (end == begin)
+        return;
+    const int64_t idx = order[i];
+    Emitter em;
+    em.isect_ids = reinterpret_cast<int64_t *>(isect_ids);
+    em.flatten_ids = reinterpret_cast<int32_t *>(flatten_ids);
+    em.cursor = begin;
+    em.end = end;
+    const int64_t iid = a.image_ids != nullptr ? a.image_ids[idx] : idx / a.N;
+    em.key_hi = iid << (32 + a.tile_n_bits);
+    em.depth_lo = (int64_t)(uint64_t)__float_as_uint(a.depths[idx]);
+    em.flat = (int32_t)idx;
+    row_tiles<true>(a, idx, &em);
+}
+
+struct PrepLayout {
+    size_t keys_a, keys_b, vals_a, vals_b, lookback, sort_ws, total;
+};
+
+inline size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+PrepLayout prep_layout(int64_t n) {
+    PrepLayout L;
+    const size_t k = align256((size_t)n * 8), v = align256((size_t)n * 4);
+    L.keys_a = 0;
+    L.keys_b = k;
+    L.vals_a = 2 * k;
+    L.vals_b = 2 * k;  // one spare row buffer; the caller's `order` is the other
+    L.lookback = 2 * k + v;
+    L.sort_ws = L.lookback + align256(lookback_bytes(ceil_div(n, kIsectThreads)));
+    L.total = L.sort_ws + radix_sort_workspace_bytes(n);
+    return L;
+}
+
+struct EmitLayout {
+    size_t keys, vals, sort_ws, total;
+};
+
+EmitLayout emit_layout(int64_t n_isects) {
+    EmitLayout L;
+    L.keys = 0;
+    L.vals = align256((size_t)n_isects * 8);
+    L.sort_ws = L.vals + align256((size_t)n_isects * 4);
+    L.total = L.sort_ws + radix_sort_workspace_bytes(n_isects);
+    return L;
+}
+
 __global__ void isect_offsets_kernel(int64_t n_isects,
                                      const int64_t *__restrict__ isect_ids,
                                      int64_t n_slots, int32_t tile_n_bits,
@@ -406,4 +523,108 @@ extern "C" int gsplat_isect_offsets(int64_t n_isects, const int64_t *isect_ids,
     isect_offsets_kernel<<<(unsigned)ceil_div(n_isects, 256), 256, 0, st>>>(
         n_isects, isect_ids, n_slots, tb, (int32_t)n_tiles, offsets);
     return check_launch("isect_offsets_kernel");
+}
+
+extern "C" size_t gsplat_isect_prepare_workspace_size(int64_t n) {
+    return prep_layout(n > 0 ? n : 0).total;
+}
+
+extern "C" int gsplat_isect_prepare(int64_t n, int64_t N, const int64_t *image_ids,
+                                    const float *means2d, const int32_t *radii,
+                                    const float *depths, const float *conics,
+                                    const float *opacities, int32_t tile_size,
+                                    int32_t tile_width, int32_t tile_height,
+                                    void *workspace, size_t workspace_bytes,
+                                    int32_t *tiles_per_gauss, uint32_t *order,
+                                    int64_t *cum_sorted, gsplat_stream_t stream) {
+    clear_error();
+    IsectArgs a;
+    GS_TRY(make_args(n, N, 0, image_ids, means2d, radii, depths, conics,
+                     opacities, tile_size, tile_width, tile_height, a));
+    if (n == 0)
+        return GSPLAT_OK;
+    GS_REQUIRE(depths && tiles_per_gauss && order && cum_sorted,
+               "isect_prepare: NULL buffer");
+    GS_REQUIRE(n < (1ll << 31), "isect_prepare: more than 2^31 rows");
+    const PrepLayout L = prep_layout(n);
+    GS_REQUIRE(workspace && workspace_bytes >= L.total,
+               "isect_prepare: workspace too small");
+    char *ws = reinterpret_cast<char *>(workspace);
+    uint64_t *keys_a = reinterpret_cast<uint64_t *>(ws + L.keys_a);
+    uint64_t *keys_b = reinterpret_cast<uint64_t *>(ws + L.keys_b);
+    // the row order must end in `order`: start the passes where they end there
+    uint32_t *spare = reinterpret_cast<uint32_t *>(ws + L.vals_a);
+    const bool odd = radix_sort_passes(32) % 2 == 1;
+    uint32_t *vals_a = odd ? spare : order;
+    uint32_t *vals_b = odd ? order : spare;
+    hipStream_t st = as_stream(stream);
+    const unsigned grid = (unsigned)ceil_div(n, kIsectThreads);
+    isect_count_keys_kernel<<<grid, kIsectThreads, 0, st>>>(a, tiles_per_gauss,
+                                                             keys_a, vals_a);
+    GS_TRY(check_launch("isect_count_keys_kernel"));
+    bool in_b = false;
+    GS_TRY(radix_sort_ping_pong(n, 0, 32, keys_a, vals_a, keys_b, vals_b,
+                                ws + L.sort_ws, workspace_bytes - L.sort_ws, st,
+                                &in_b));
+    const uint32_t *sorted_rows = in_b ? vals_b : vals_a;
+    if (sorted_rows != order)
+        return fail(GSPLAT_ERR_LAUNCH, "isect_prepare: row order in the wrong buffer");
+    GS_TRY(clear_lookback(ws + L.lookback, grid, st));
+    gather_count_scan_kernel<<<grid, kIsectThreads, 0, st>>>(
+        n, sorted_rows, tiles_per_gauss, lookback_from(ws + L.lookback),
+        cum_sorted);
+    return check_launch("gather_count_scan_kernel");
+}
+
+extern "C" size_t gsplat_isect_emit_sorted_workspace_size(int64_t n_isects) {
+    return emit_layout(n_isects > 0 ? n_isects : 0).total;
+}
+
+extern "C" int gsplat_isect_emit_sorted(
+    int64_t n, int64_t N, int64_t I, const int64_t *image_ids,
+    const float *means2d, const int32_t *radii, const float *depths,
+    const float *conics, const float *opacities, int32_t tile_size,
+    int32_t tile_width, int32_t tile_height, const uint32_t *order,
+    const int64_t *cum_sorted, int64_t n_isects, void *workspace,
+    size_t workspace_bytes, int64_t *isect_ids, int32_t *flatten_ids,
+    gsplat_stream_t stream) {
+    clear_error();
+    IsectArgs a;
+    GS_TRY(make_args(n, N, I, image_ids, means2d, radii, depths, conics,
+                     opacities, tile_size, tile_width, tile_height, a));
+    GS_REQUIRE(n_isects >= 0, "isect_emit_sorted: negative n_isects");
+    if (n == 0 || n_isects == 0)
+        return GSPLAT_OK;
+    GS_REQUIRE(depths && order && cum_sorted && isect_ids && flatten_ids,
+               "isect_emit_sorted: NULL buffer");
+    GS_REQUIRE(I > 0, "isect_emit_sorted: I must be positive");
+    const int ib = bit_length(I);
+    GS_REQUIRE(ib + a.tile_n_bits <= 32,
+               "isect_emit_sorted: image and tile ids need more than 32 bits");
+    GS_REQUIRE(n_isects < (1ll << 31), "isect_emit_sorted: more than 2^31 isects");
+    const EmitLayout L = emit_layout(n_isects);
+    GS_REQUIRE(workspace && workspace_bytes >= L.total,
+               "isect_emit_sorted: workspace too small");
+    char *ws = reinterpret_cast<char *>(workspace);
+    uint64_t *tmp_keys = reinterpret_cast<uint64_t *>(ws + L.keys);
+    uint32_t *tmp_vals = reinterpret_cast<uint32_t *>(ws + L.vals);
+    uint64_t *out_keys = reinterpret_cast<uint64_t *>(isect_ids);
+    uint32_t *out_vals = reinterpret_cast<uint32_t *>(flatten_ids);
+    // emit where the tile passes will start so that they end in the outputs
+    const int end_bit = 32 + a.tile_n_bits + ib;
+    const bool odd = radix_sort_passes(end_bit - 32) % 2 == 1;
+    uint64_t *ka = odd ? tmp_keys : out_keys, *kb = odd ? out_keys : tmp_keys;
+    uint32_t *va = odd ? tmp_vals : out_vals, *vb = odd ? out_vals : tmp_vals;
+    hipStream_t st = as_stream(stream);
+    isect_emit_sorted_kernel<<<(unsigned)ceil_div(n, kIsectThreads), kIsectThreads,
+                               0, st>>>(a, order, cum_sorted, ka, va);
+    GS_TRY(check_launch("isect_emit_sorted_kernel"));
+    bool in_b = false;
+    GS_TRY(radix_sort_ping_pong(n_isects, 32, end_bit, ka, va, kb, vb,
+                                ws + L.sort_ws, workspace_bytes - L.sort_ws, st,
+                                &in_b));
+    if ((in_b ? kb : ka) != out_keys)
+        return copy_pairs(n_isects, in_b ? kb : ka, in_b ? vb : va, out_keys,
+                          out_vals, st);
+    return GSPLAT_OK;
 }

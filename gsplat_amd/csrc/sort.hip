@@ -2,20 +2,23 @@
 // exclusive scan, both hand-written for wave64.
 //
 // Replaces cub::DeviceRadixSort::SortPairs as used by radix_sort_double_buffer
-// (gsplat/cuda/csrc/IntersectTile.cu:478-520): keys are sorted on bits
-// [0, num_bits), ties keep their input order.
+// (gsplat/cuda/csrc/IntersectTile.cu:478-520): keys are sorted on a bit range,
+// ties keep their input order.
 //
-// Per pass (digit of up to 10 bits):
-//   1. radix_hist_kernel   each 4096-key tile counts its digits; ranks come
-//                          from wave64 "match" ballots, so no LDS atomics;
-//   2. scan_u32_kernel     one exclusive scan over the digit-major
-//                          [radix][tiles] count table (single pass, decoupled
-//                          look-back);
-//   3. radix_scatter_kernel recomputes the stable rank of every key inside its
-//                          tile (wave-major, item, lane order) and writes it
-//                          to its global slot.
-// The pass count is kept odd where possible (digit width up to 10 bits), so
-// the result lands in the output buffers without a final copy.
+// Per pass (digit of up to 8 bits, 4096-key tiles):
+//   1. radix_hist_kernel    digit counts per tile with LDS atomics, written
+//                           tile-major (coalesced);
+//   2. radix_colscan_kernel one workgroup per digit scans that digit's count
+//                           over the tiles and records the digit total (no
+//                           cross-workgroup waits);
+//   3. radix_scatter_kernel ranks every key stably inside its tile (wave64
+//                           match ballots, order wave, item, lane), reorders
+//                           the tile by digit in LDS, and writes each digit
+//                           run with consecutive threads on consecutive
+//                           addresses.
+// radix_sort_ping_pong alternates between two buffer pairs and reports which
+// one holds the result, so callers that fill the first pair themselves can
+// choose it to make the result land where they want it.
 #include "common.h"
 
 namespace gs {
@@ -25,8 +28,8 @@ constexpr int kSortThreads = 256;
 constexpr int kSortWaves = kSortThreads / kWave;
 constexpr int kSortItems = 16;
 constexpr int kSortTile = kSortThreads * kSortItems;  // keys per workgroup
-constexpr int kMaxDigitBits = 10;
-constexpr int kMaxRadix = 1 << kMaxDigitBits;
+constexpr int kDigitBits = 8;
+constexpr int kRadix = 1 << kDigitBits;
 
 constexpr int kScanThreads = 256;
 constexpr int kScanItems = 8;
@@ -44,60 +47,112 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d, int bits,
     return peers;
 }
 
+// Exclusive prefix over the kSortThreads values v of the workgroup (one per
+// thread); returns the thread's exclusive prefix, *total gets the sum.
+__device__ __forceinline__ uint32_t block_exclusive_u32(uint32_t v,
+                                                        uint32_t *s_wave,
+                                                        uint32_t *total) {
+    const uint32_t incl = (uint32_t)wave_inclusive_scan_u64(v);
+    const int w = threadIdx.x / kWave;
+    if (lane_id() == kWave - 1)
+        s_wave[w] = incl;
+    __syncthreads();
+    uint32_t off = 0, tot = 0;
+#pragma unroll
+    for (int ww = 0; ww < kSortWaves; ++ww) {
+        const uint32_t t = s_wave[ww];
+        off += ww < w ? t : 0u;
+        tot += t;
+    }
+    *total = tot;
+    return off + incl - v;
+}
+
+// Digit counts of one 4096-key tile, block-major: hist[tile * 256 + d].
 __global__ void __launch_bounds__(kSortThreads)
     radix_hist_kernel(const uint64_t *__restrict__ keys, int64_t n, int shift,
-                      int bits, uint32_t *__restrict__ hist, int64_t n_tiles) {
-    __shared__ uint32_t s_cnt[kSortWaves][kMaxRadix];
-    const int radix = 1 << bits;
-    const uint32_t mask = (uint32_t)radix - 1u;
-    for (int i = threadIdx.x; i < kSortWaves * kMaxRadix; i += kSortThreads)
+                      int bits, uint32_t *__restrict__ hist) {
+    __shared__ uint32_t s_cnt[kSortWaves][kRadix];
+    const uint32_t mask = (1u << bits) - 1u;
+    for (int i = threadIdx.x; i < kSortWaves * kRadix; i += kSortThreads)
         (&s_cnt[0][0])[i] = 0u;
     __syncthreads();
     const int w = threadIdx.x / kWave;
-    const uint32_t lane = lane_id();
     const int64_t base = (int64_t)blockIdx.x * kSortTile + (int64_t)w * kWave * kSortItems;
+#pragma unroll 4
     for (int j = 0; j < kSortItems; ++j) {
-        const int64_t i = base + (int64_t)j * kWave + lane;
-        const bool valid = i < n;
-        const uint32_t d = valid ? (uint32_t)(keys[i] >> shift) & mask : 0u;
-        const uint64_t vmask = __ballot(valid);
-        if (vmask == 0)
-            break;
-        const uint64_t peers = match_digit(d, bits, vmask);
-        if (valid && (peers & lanemask_lt()) == 0)
-            s_cnt[w][d] += (uint32_t)__popcll(peers);
-        __builtin_amdgcn_wave_barrier();
+        const int64_t i = base + (int64_t)j * kWave + lane_id();
+        if (i < n)
+            atomicAdd(&s_cnt[w][(uint32_t)(keys[i] >> shift) & mask], 1u);
     }
     __syncthreads();
-    for (int d = threadIdx.x; d < radix; d += kSortThreads) {
-        uint32_t tot = 0;
+    const int d = threadIdx.x;  // kSortThreads == kRadix
+    uint32_t tot = 0;
 #pragma unroll
-        for (int ww = 0; ww < kSortWaves; ++ww)
-            tot += s_cnt[ww][d];
-        hist[(int64_t)d * n_tiles + blockIdx.x] = tot;
-    }
+    for (int ww = 0; ww < kSortWaves; ++ww)
+        tot += s_cnt[ww][d];
+    hist[(int64_t)blockIdx.x * kRadix + d] = tot;
 }
 
+// One workgroup per digit: exclusive prefix of that digit's count over the
+// tiles (prefix[tile * 256 + d]) and the digit's total.
+__global__ void __launch_bounds__(kSortThreads)
+    radix_colscan_kernel(const uint32_t *__restrict__ hist, int64_t n_tiles,
+                         uint32_t *__restrict__ prefix,
+                         uint32_t *__restrict__ totals) {
+    __shared__ uint32_t s_wave[kSortWaves];
+    const int d = blockIdx.x;
+    const int64_t per = ceil_div(n_tiles, kSortThreads);
+    const int64_t t0 = (int64_t)threadIdx.x * per;
+    const int64_t t1 = t0 + per < n_tiles ? t0 + per : n_tiles;
+    uint32_t sum = 0;
+    for (int64_t t = t0; t < t1; ++t)
+        sum += hist[t * kRadix + d];
+    uint32_t total;
+    uint32_t run = block_exclusive_u32(sum, s_wave, &total);
+    for (int64_t t = t0; t < t1; ++t) {
+        const uint32_t c = hist[t * kRadix + d];
+        prefix[t * kRadix + d] = run;
+        run += c;
+    }
+    if (threadIdx.x == 0)
+        totals[d] = total;
+}
+
+// Stable scatter of one 4096-key tile: ranks come from wave64 match ballots
+// (order: wave, item, lane = input order), the tile is reordered by digit in
+// LDS, then every digit run is written out with consecutive threads on
+// consecutive addresses.
 __global__ void __launch_bounds__(kSortThreads)
     radix_scatter_kernel(const uint64_t *__restrict__ keys_in,
                          const uint32_t *__restrict__ vals_in,
                          uint64_t *__restrict__ keys_out,
                          uint32_t *__restrict__ vals_out, int64_t n, int shift,
-                         int bits, const uint32_t *__restrict__ offsets,
-                         int64_t n_tiles) {
-    __shared__ uint32_t s_cnt[kSortWaves][kMaxRadix];
-    __shared__ uint32_t s_goff[kMaxRadix];
-    const int radix = 1 << bits;
-    const uint32_t mask = (uint32_t)radix - 1u;
-    for (int i = threadIdx.x; i < kSortWaves * kMaxRadix; i += kSortThreads)
+                         int bits, const uint32_t *__restrict__ prefix,
+                         const uint32_t *__restrict__ totals) {
+    __shared__ uint64_t s_keys[kSortTile];
+    __shared__ uint32_t s_vals[kSortTile];
+    __shared__ uint32_t s_cnt[kSortWaves][kRadix];
+    __shared__ uint32_t s_lstart[kRadix];  // digit start inside the tile
+    __shared__ uint32_t s_gstart[kRadix];  // digit start of this tile, global
+    __shared__ uint32_t s_wave[kSortWaves];
+    const uint32_t mask = (1u << bits) - 1u;
+    const int tid = threadIdx.x;
+    const int64_t tile_base = (int64_t)blockIdx.x * kSortTile;
+
+    // global start of every digit for this tile: digit base + tile prefix
+    {
+        uint32_t total;
+        const uint32_t base = block_exclusive_u32(totals[tid], s_wave, &total);
+        s_gstart[tid] = base + prefix[(int64_t)blockIdx.x * kRadix + tid];
+    }
+    for (int i = tid; i < kSortWaves * kRadix; i += kSortThreads)
         (&s_cnt[0][0])[i] = 0u;
-    for (int d = threadIdx.x; d < radix; d += kSortThreads)
-        s_goff[d] = offsets[(int64_t)d * n_tiles + blockIdx.x];
     __syncthreads();
 
-    const int w = threadIdx.x / kWave;
+    const int w = tid / kWave;
     const uint32_t lane = lane_id();
-    const int64_t base = (int64_t)blockIdx.x * kSortTile + (int64_t)w * kWave * kSortItems;
+    const int64_t base = tile_base + (int64_t)w * kWave * kSortItems;
     uint64_t k[kSortItems];
     uint32_t v[kSortItems];
     uint32_t rank[kSortItems];
@@ -105,7 +160,7 @@ __global__ void __launch_bounds__(kSortThreads)
     for (int j = 0; j < kSortItems; ++j) {
         const int64_t i = base + (int64_t)j * kWave + lane;
         const bool valid = i < n;
-        k[j] = valid ? keys_in[i] : 0ull;
+        k[j] = valid ? keys_in[i] : ~0ull;
         v[j] = valid ? vals_in[i] : 0u;
     }
 #pragma unroll
@@ -125,14 +180,23 @@ __global__ void __launch_bounds__(kSortThreads)
         __builtin_amdgcn_wave_barrier();
     }
     __syncthreads();
-    // exclusive prefix over the waves for every digit
-    for (int d = threadIdx.x; d < radix; d += kSortThreads) {
-        uint32_t run = 0;
+    // digit starts inside the tile, and each wave's start within its digit
+    {
+        const int d = tid;
+        uint32_t c[kSortWaves], tot = 0;
 #pragma unroll
         for (int ww = 0; ww < kSortWaves; ++ww) {
-            const uint32_t t = s_cnt[ww][d];
+            c[ww] = s_cnt[ww][d];
+            tot += c[ww];
+        }
+        uint32_t count;
+        const uint32_t start = block_exclusive_u32(tot, s_wave, &count);
+        s_lstart[d] = start;
+        uint32_t run = start;
+#pragma unroll
+        for (int ww = 0; ww < kSortWaves; ++ww) {
             s_cnt[ww][d] = run;
-            run += t;
+            run += c[ww];
         }
     }
     __syncthreads();
@@ -141,10 +205,20 @@ __global__ void __launch_bounds__(kSortThreads)
         const int64_t i = base + (int64_t)j * kWave + lane;
         if (i < n) {
             const uint32_t d = (uint32_t)(k[j] >> shift) & mask;
-            const uint64_t pos = (uint64_t)s_goff[d] + s_cnt[w][d] + rank[j];
-            keys_out[pos] = k[j];
-            vals_out[pos] = v[j];
+            const uint32_t pos = s_cnt[w][d] + rank[j];
+            s_keys[pos] = k[j];
+            s_vals[pos] = v[j];
         }
+    }
+    __syncthreads();
+    const int64_t rem = n - tile_base;
+    const int count = rem < kSortTile ? (int)rem : kSortTile;
+    for (int i = tid; i < count; i += kSortThreads) {
+        const uint64_t key = s_keys[i];
+        const uint32_t d = (uint32_t)(key >> shift) & mask;
+        const uint64_t g = (uint64_t)s_gstart[d] + (uint32_t)(i - s_lstart[d]);
+        keys_out[g] = key;
+        vals_out[g] = s_vals[i];
     }
 }
 
@@ -206,25 +280,78 @@ __global__ void copy_pairs_kernel(const uint64_t *__restrict__ ks,
 
 struct SortLayout {
     int64_t n_tiles;
-    int64_t table;          // entries of the [radix][tiles] count table
-    int64_t scan_blocks;
-    size_t hist_off, scanned_off, lb_off, total;
+    size_t hist_off, prefix_off, totals_off, total;
 };
 
 SortLayout sort_layout(int64_t n) {
     SortLayout L;
     L.n_tiles = ceil_div(n > 0 ? n : 1, kSortTile);
-    L.table = (int64_t)kMaxRadix * L.n_tiles;
-    L.scan_blocks = ceil_div(L.table, kScanTile);
-    const size_t tbytes = ((size_t)L.table * 4 + 255) / 256 * 256;
+    const size_t tbytes = ((size_t)L.n_tiles * kRadix * 4 + 255) / 256 * 256;
     L.hist_off = 0;
-    L.scanned_off = tbytes;
-    L.lb_off = 2 * tbytes;
-    L.total = L.lb_off + lookback_bytes(L.scan_blocks);
+    L.prefix_off = tbytes;
+    L.totals_off = 2 * tbytes;
+    L.total = L.totals_off + kRadix * 4;
     return L;
 }
 
 }  // namespace
+
+int radix_sort_passes(int num_bits) {
+    if (num_bits <= 0)
+        return 0;
+    // as few passes as digits of at most kDigitBits allow
+    return (num_bits + kDigitBits - 1) / kDigitBits;
+}
+
+size_t radix_sort_workspace_bytes(int64_t n) { return sort_layout(n).total; }
+
+int radix_sort_ping_pong(int64_t n, int begin_bit, int end_bit, uint64_t *keys_a,
+                         uint32_t *vals_a, uint64_t *keys_b, uint32_t *vals_b,
+                         void *workspace, size_t workspace_bytes,
+                         hipStream_t st, bool *result_in_b) {
+    *result_in_b = false;
+    const int num_bits = end_bit - begin_bit;
+    if (n == 0 || num_bits <= 0)
+        return GSPLAT_OK;
+    GS_REQUIRE(n < (1ll << 32), "radix sort: n must be below 2^32");
+    const SortLayout L = sort_layout(n);
+    GS_REQUIRE(workspace != nullptr && workspace_bytes >= L.total,
+               "radix sort: workspace too small");
+    char *ws = reinterpret_cast<char *>(workspace);
+    uint32_t *hist = reinterpret_cast<uint32_t *>(ws + L.hist_off);
+    uint32_t *prefix = reinterpret_cast<uint32_t *>(ws + L.prefix_off);
+    uint32_t *totals = reinterpret_cast<uint32_t *>(ws + L.totals_off);
+    const int passes = radix_sort_passes(num_bits);
+    int shift = begin_bit;
+    uint64_t *ksrc = keys_a, *kdst = keys_b;
+    uint32_t *vsrc = vals_a, *vdst = vals_b;
+    for (int p = 0; p < passes; ++p) {
+        const int remaining = end_bit - shift;
+        const int bits = (remaining + (passes - p) - 1) / (passes - p);
+        radix_hist_kernel<<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
+            ksrc, n, shift, bits, hist);
+        GS_TRY(check_launch("radix_hist_kernel"));
+        radix_colscan_kernel<<<kRadix, kSortThreads, 0, st>>>(hist, L.n_tiles,
+                                                              prefix, totals);
+        GS_TRY(check_launch("radix_colscan_kernel"));
+        radix_scatter_kernel<<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
+            ksrc, vsrc, kdst, vdst, n, shift, bits, prefix, totals);
+        GS_TRY(check_launch("radix_scatter_kernel"));
+        shift += bits;
+        uint64_t *tk = ksrc; ksrc = kdst; kdst = tk;
+        uint32_t *tv = vsrc; vsrc = vdst; vdst = tv;
+    }
+    *result_in_b = (ksrc == keys_b);
+    return GSPLAT_OK;
+}
+
+int copy_pairs(int64_t n, const uint64_t *ks, const uint32_t *vs, uint64_t *kd,
+               uint32_t *vd, hipStream_t st) {
+    if (n == 0)
+        return GSPLAT_OK;
+    copy_pairs_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(ks, vs, kd, vd, n);
+    return check_launch("copy_pairs_kernel");
+}
 
 // Exclusive scan used by other translation units of the library.
 int scan_u32_exclusive(const uint32_t *in, uint32_t *out, int64_t n, void *ws,
@@ -243,7 +370,7 @@ int scan_u32_exclusive(const uint32_t *in, uint32_t *out, int64_t n, void *ws,
 using namespace gs;
 
 extern "C" size_t gsplat_sort_pairs_workspace_size(int64_t n) {
-    return sort_layout(n).total;
+    return radix_sort_workspace_bytes(n);
 }
 
 extern "C" int gsplat_sort_pairs_u64_u32(int64_t n, int32_t num_bits,
@@ -260,52 +387,14 @@ extern "C" int gsplat_sort_pairs_u64_u32(int64_t n, int32_t num_bits,
     GS_REQUIRE(keys_in && vals_in && keys_out && vals_out,
                "sort_pairs: NULL buffer");
     GS_REQUIRE(n < (1ll << 32), "sort_pairs: n must be below 2^32");
-    const SortLayout L = sort_layout(n);
-    GS_REQUIRE(workspace != nullptr && workspace_bytes >= L.total,
+    GS_REQUIRE(workspace != nullptr &&
+                   workspace_bytes >= radix_sort_workspace_bytes(n),
                "sort_pairs: workspace too small");
     hipStream_t st = as_stream(stream);
-    char *ws = reinterpret_cast<char *>(workspace);
-    uint32_t *hist = reinterpret_cast<uint32_t *>(ws + L.hist_off);
-    uint32_t *scanned = reinterpret_cast<uint32_t *>(ws + L.scanned_off);
-    void *lbws = ws + L.lb_off;
-
-    if (num_bits == 0) {
-        copy_pairs_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(
-            keys_in, vals_in, keys_out, vals_out, n);
-        return check_launch("copy_pairs_kernel");
-    }
-    // choose an odd number of passes with digits of at most 10 bits
-    int passes = (num_bits + 7) / 8;
-    if (passes % 2 == 0) {
-        if ((num_bits + passes - 2) / (passes - 1) <= kMaxDigitBits && passes > 1)
-            passes -= 1;
-        else
-            passes += 1;
-    }
-    int shift = 0;
-    uint64_t *ksrc = keys_in, *kdst = keys_out;
-    uint32_t *vsrc = vals_in, *vdst = vals_out;
-    for (int p = 0; p < passes; ++p) {
-        const int remaining = num_bits - shift;
-        const int bits = (remaining + (passes - p) - 1) / (passes - p);
-        if (bits <= 0)
-            break;
-        const int64_t table = ((int64_t)1 << bits) * L.n_tiles;
-        radix_hist_kernel<<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
-            ksrc, n, shift, bits, hist, L.n_tiles);
-        GS_TRY(check_launch("radix_hist_kernel"));
-        GS_TRY(scan_u32_exclusive(hist, scanned, table, lbws, st));
-        radix_scatter_kernel<<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
-            ksrc, vsrc, kdst, vdst, n, shift, bits, scanned, L.n_tiles);
-        GS_TRY(check_launch("radix_scatter_kernel"));
-        shift += bits;
-        uint64_t *tk = ksrc; ksrc = kdst; kdst = tk;
-        uint32_t *tv = vsrc; vsrc = vdst; vdst = tv;
-    }
-    if (ksrc != keys_out) {
-        copy_pairs_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(
-            ksrc, vsrc, keys_out, vals_out, n);
-        return check_launch("copy_pairs_kernel");
-    }
+    bool in_b = false;
+    GS_TRY(radix_sort_ping_pong(n, 0, num_bits, keys_in, vals_in, keys_out,
+                                vals_out, workspace, workspace_bytes, st, &in_b));
+    if (!in_b)
+        return copy_pairs(n, keys_in, vals_in, keys_out, vals_out, st);
     return GSPLAT_OK;
 }

@@ -423,6 +423,31 @@ def intersect_tile(
                 torch.empty(0, dtype=_I32, device=dev))
     st = _stream(means2d)
     img = image_ids if packed else None
+    if sort:
+        # Rows sorted by depth, intersections emitted in that order, then a
+        # stable sort on the image|tile bits only: the reference's full-key
+        # order (a per-image segmented sort, segmented=True, is the same order
+        # because the image id occupies the top key bits).
+        order = torch.empty(n, dtype=_I32, device=dev)
+        cum = torch.empty(n, dtype=_I64, device=dev)
+        ws = torch.empty(query("gsplat_isect_prepare_workspace_size", n),
+                         dtype=torch.uint8, device=dev)
+        call("gsplat_isect_prepare", n, N, ptr(img), ptr(means2d), ptr(radii),
+             ptr(depths), ptr(conics), ptr(opacities), int(tile_size),
+             int(tile_width), int(tile_height), ptr(ws), ws.numel(),
+             ptr(tiles_per_gauss), ptr(order), ptr(cum), st)
+        n_isects = int(cum[-1].item())
+        isect_ids = torch.empty(n_isects, dtype=_I64, device=dev)
+        flatten_ids = torch.empty(n_isects, dtype=_I32, device=dev)
+        if n_isects == 0:
+            return tiles_per_gauss, isect_ids, flatten_ids
+        ews = torch.empty(query("gsplat_isect_emit_sorted_workspace_size", n_isects),
+                          dtype=torch.uint8, device=dev)
+        call("gsplat_isect_emit_sorted", n, N, int(I), ptr(img), ptr(means2d),
+             ptr(radii), ptr(depths), ptr(conics), ptr(opacities), int(tile_size),
+             int(tile_width), int(tile_height), ptr(order), ptr(cum), n_isects,
+             ptr(ews), ews.numel(), ptr(isect_ids), ptr(flatten_ids), st)
+        return tiles_per_gauss, isect_ids, flatten_ids
     cum = torch.empty(n, dtype=_I64, device=dev)
     ws = torch.empty(query("gsplat_isect_count_workspace_size", n),
                      dtype=torch.uint8, device=dev)
@@ -438,18 +463,6 @@ def intersect_tile(
          ptr(depths), ptr(conics), ptr(opacities), int(tile_size),
          int(tile_width), int(tile_height), ptr(cum), ptr(isect_ids),
          ptr(flatten_ids), st)
-    if sort:
-        # One global sort on the significant key bits; a per-image segmented
-        # sort (segmented=True) gives the same order because the image id
-        # occupies the top key bits.
-        keys_out = torch.empty_like(isect_ids)
-        vals_out = torch.empty_like(flatten_ids)
-        sws = torch.empty(query("gsplat_sort_pairs_workspace_size", n_isects),
-                          dtype=torch.uint8, device=dev)
-        call("gsplat_sort_pairs_u64_u32", n_isects, 32 + tile_n_bits + image_n_bits,
-             ptr(isect_ids), ptr(flatten_ids), ptr(keys_out), ptr(vals_out),
-             ptr(sws), sws.numel(), st)
-        isect_ids, flatten_ids = keys_out, vals_out
     return tiles_per_gauss, isect_ids, flatten_ids
 
 

@@ -85,6 +85,27 @@ def test_isect_projected_scene(packed, accutile):
     np.testing.assert_array_equal(offs.cpu().numpy(), exact.isect_offset_encode(want[1], C, tw, th))
 
 
+@pytest.mark.parametrize("W,H,C", [(64, 48, 2), (1024, 1024, 3)])
+def test_isect_sorted_with_depth_ties(W, H, C):
+    """Quantised depths make many (image, tile, depth) keys equal: the sorted
+    order must still be by (key, row).  The 1024x1024 case has a 13-bit tile
+    key (4096 tiles) and a 2-bit image id, so the tile stage takes two
+    radix passes; the small case one."""
+    from gsplat_amd.cuda._wrapper import isect_tiles
+    rng = np.random.default_rng(W)
+    N, ts = 6000, 16
+    tw, th = math.ceil(W / ts), math.ceil(H / ts)
+    means2d = np.stack([rng.uniform(-20, W + 20, (C, N)),
+                        rng.uniform(-20, H + 20, (C, N))], -1).astype(np.float32)
+    radii = rng.integers(0, 40, (C, N, 2)).astype(np.int32)
+    depths = np.round(rng.uniform(1, 3, (C, N)) * 4).astype(np.float32) / 4
+    want = exact.isect_tiles(means2d, radii, depths, ts, tw, th)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    got = isect_tiles(t(means2d), t(radii), t(depths), ts, tw, th)
+    assert want[1].shape[0] > 5000
+    _compare(got, want)
+
+
 def test_isect_unsorted_emission_order():
     from gsplat_amd.cuda._wrapper import isect_tiles
     from tests._util import small_scene
