@@ -259,8 +259,8 @@ __global__ void __launch_bounds__(kIsectThreads)
 // moved:
 //   1. rows are sorted stably by their depth bits (32-bit keys, one per
 //      row instead of one per intersection);
-//   2. intersections are emitted row by row in that depth order, each row
-//      at the prefix of the depth-ordered counts;
+//   2. every row's intersections are written to the slots the row occupies
+//      in the depth-ordered layout (the prefix of the depth-ordered counts);
 //   3. one stable radix sort on the image|tile bits only (usually one or two
 //      passes) groups them by tile, keeping depth order (ties by row) inside.
 // ---------------------------------------------------------------------------
@@ -276,18 +276,35 @@ __global__ void __launch_bounds__(kIsectThreads)
     rows[idx] = (uint32_t)idx;
 }
 
-// Inclusive int64 prefix of tiles_per_gauss[order[i]] (decoupled look-back).
+constexpr int kScanItemsPerThread = 16;
+constexpr int kScanBlockRows = kIsectThreads * kScanItemsPerThread;
+
+// For the depth order `order` (rows, depth ascending): each row's first slot
+// in the depth-ordered emission, row_start[order[i]] = sum_{i' < i}
+// tiles_per_gauss[order[i']], and the total (n_isects).  Blocks of 4096
+// entries (16 consecutive per thread) chained by decoupled look-back.
 __global__ void __launch_bounds__(kIsectThreads)
-    gather_count_scan_kernel(int64_t n, const uint32_t *__restrict__ order,
-                             const int32_t *__restrict__ tiles_per_gauss,
-                             Lookback lb, int64_t *__restrict__ cum) {
+    depth_order_starts_kernel(int64_t n, const uint32_t *__restrict__ order,
+                              const int32_t *__restrict__ tiles_per_gauss,
+                              Lookback lb, int64_t *__restrict__ row_start,
+                              int64_t *__restrict__ n_isects_out) {
     __shared__ uint32_t s_ticket;
     __shared__ uint64_t s_wave_tot[kIsectThreads / kWave];
     __shared__ uint64_t s_prefix;
     const uint32_t bid = lb_ticket(lb, &s_ticket);
-    const int64_t i = (int64_t)bid * kIsectThreads + threadIdx.x;
-    const uint64_t cnt = i < n ? (uint64_t)tiles_per_gauss[order[i]] : 0ull;
-    const uint64_t incl = wave_inclusive_scan_u64(cnt);
+    const int64_t i0 = (int64_t)bid * kScanBlockRows +
+                       (int64_t)threadIdx.x * kScanItemsPerThread;
+    uint32_t rows[kScanItemsPerThread];
+    uint32_t cnt[kScanItemsPerThread];
+    uint64_t sum = 0;
+#pragma unroll
+    for (int k = 0; k < kScanItemsPerThread; ++k) {
+        const int64_t i = i0 + k;
+        rows[k] = i < n ? order[i] : 0u;
+        cnt[k] = i < n ? (uint32_t)tiles_per_gauss[rows[k]] : 0u;
+        sum += cnt[k];
+    }
+    const uint64_t incl = wave_inclusive_scan_u64(sum);
     const uint32_t wave = threadIdx.x / kWave;
     if (lane_id() == kWave - 1)
         s_wave_tot[wave] = incl;
@@ -305,28 +322,36 @@ __global__ void __launch_bounds__(kIsectThreads)
             s_prefix = excl;
     }
     __syncthreads();
-    if (i < n)
-        cum[i] = (int64_t)(s_prefix + wave_off + incl);
+    uint64_t run = s_prefix + wave_off + (incl - sum);
+#pragma unroll
+    for (int k = 0; k < kScanItemsPerThread; ++k) {
+        if (i0 + k < n)
+            row_start[rows[k]] = (int64_t)run;
+        run += cnt[k];
+    }
+    if (i0 < n && i0 + kScanItemsPerThread >= n)
+        *n_isects_out = (int64_t)run;  // the thread holding the last entry
 }
 
+// Row-order emission (the rows' own order spreads the rows with many tiles
+// over the launch), each row written at its slots of the depth-ordered
+// layout.
 __global__ void __launch_bounds__(kIsectThreads)
-    isect_emit_sorted_kernel(const IsectArgs a, const uint32_t *__restrict__ order,
-                             const int64_t *__restrict__ cum,
-                             uint64_t *__restrict__ isect_ids,
-                             uint32_t *__restrict__ flatten_ids) {
-    const int64_t i = (int64_t)blockIdx.x * kIsectThreads + threadIdx.x;
-    if (i >= a.n)
+    isect_emit_at_kernel(const IsectArgs a, const int32_t *__restrict__ tiles_per_gauss,
+                         const int64_t *__restrict__ row_start,
+                         uint64_t *__restrict__ isect_ids,
+                         uint32_t *__restrict__ flatten_ids) {
+    const int64_t idx = (int64_t)blockIdx.x * kIsectThreads + threadIdx.x;
+    if (idx >= a.n)
         return;
-    const int64_t begin = i == 0 ? 0 : cum[i - 1];
-    const int64_t end = cum[i];
-    if (end == begin)
+    const int32_t count = tiles_per_gauss[idx];
+    if (count == 0)
         return;
-    const int64_t idx = order[i];
     Emitter em;
     em.isect_ids = reinterpret_cast<int64_t *>(isect_ids);
     em.flatten_ids = reinterpret_cast<int32_t *>(flatten_ids);
-    em.cursor = begin;
-    em.end = end;
+    em.cursor = row_start[idx];
+    em.end = em.cursor + count;
     const int64_t iid = a.image_ids != nullptr ? a.image_ids[idx] : idx / a.N;
     em.key_hi = iid << (32 + a.tile_n_bits);
     em.depth_lo = (int64_t)(uint64_t)__float_as_uint(a.depths[idx]);
@@ -346,9 +371,9 @@ PrepLayout prep_layout(int64_t n) {
     L.keys_a = 0;
     L.keys_b = k;
     L.vals_a = 2 * k;
-    L.vals_b = 2 * k;  // one spare row buffer; the caller's `order` is the other
-    L.lookback = 2 * k + v;
-    L.sort_ws = L.lookback + align256(lookback_bytes(ceil_div(n, kIsectThreads)));
+    L.vals_b = 2 * k + v;
+    L.lookback = 2 * k + 2 * v;
+    L.sort_ws = L.lookback + align256(lookback_bytes(ceil_div(n, kScanBlockRows)));
     L.total = L.sort_ws + radix_sort_workspace_bytes(n);
     return L;
 }
@@ -535,15 +560,15 @@ extern "C" int gsplat_isect_prepare(int64_t n, int64_t N, const int64_t *image_i
                                     const float *opacities, int32_t tile_size,
                                     int32_t tile_width, int32_t tile_height,
                                     void *workspace, size_t workspace_bytes,
-                                    int32_t *tiles_per_gauss, uint32_t *order,
-                                    int64_t *cum_sorted, gsplat_stream_t stream) {
+                                    int32_t *tiles_per_gauss, int64_t *row_start,
+                                    int64_t *n_isects_out, gsplat_stream_t stream) {
     clear_error();
     IsectArgs a;
     GS_TRY(make_args(n, N, 0, image_ids, means2d, radii, depths, conics,
                      opacities, tile_size, tile_width, tile_height, a));
     if (n == 0)
         return GSPLAT_OK;
-    GS_REQUIRE(depths && tiles_per_gauss && order && cum_sorted,
+    GS_REQUIRE(depths && tiles_per_gauss && row_start && n_isects_out,
                "isect_prepare: NULL buffer");
     GS_REQUIRE(n < (1ll << 31), "isect_prepare: more than 2^31 rows");
     const PrepLayout L = prep_layout(n);
@@ -552,11 +577,8 @@ extern "C" int gsplat_isect_prepare(int64_t n, int64_t N, const int64_t *image_i
     char *ws = reinterpret_cast<char *>(workspace);
     uint64_t *keys_a = reinterpret_cast<uint64_t *>(ws + L.keys_a);
     uint64_t *keys_b = reinterpret_cast<uint64_t *>(ws + L.keys_b);
-    // the row order must end in `order`: start the passes where they end there
-    uint32_t *spare = reinterpret_cast<uint32_t *>(ws + L.vals_a);
-    const bool odd = radix_sort_passes(32) % 2 == 1;
-    uint32_t *vals_a = odd ? spare : order;
-    uint32_t *vals_b = odd ? order : spare;
+    uint32_t *vals_a = reinterpret_cast<uint32_t *>(ws + L.vals_a);
+    uint32_t *vals_b = reinterpret_cast<uint32_t *>(ws + L.vals_b);
     hipStream_t st = as_stream(stream);
     const unsigned grid = (unsigned)ceil_div(n, kIsectThreads);
     isect_count_keys_kernel<<<grid, kIsectThreads, 0, st>>>(a, tiles_per_gauss,
@@ -566,14 +588,13 @@ extern "C" int gsplat_isect_prepare(int64_t n, int64_t N, const int64_t *image_i
     GS_TRY(radix_sort_ping_pong(n, 0, 32, keys_a, vals_a, keys_b, vals_b,
                                 ws + L.sort_ws, workspace_bytes - L.sort_ws, st,
                                 &in_b));
-    const uint32_t *sorted_rows = in_b ? vals_b : vals_a;
-    if (sorted_rows != order)
-        return fail(GSPLAT_ERR_LAUNCH, "isect_prepare: row order in the wrong buffer");
-    GS_TRY(clear_lookback(ws + L.lookback, grid, st));
-    gather_count_scan_kernel<<<grid, kIsectThreads, 0, st>>>(
-        n, sorted_rows, tiles_per_gauss, lookback_from(ws + L.lookback),
-        cum_sorted);
-    return check_launch("gather_count_scan_kernel");
+    const uint32_t *order = in_b ? vals_b : vals_a;
+    const int64_t scan_blocks = ceil_div(n, kScanBlockRows);
+    GS_TRY(clear_lookback(ws + L.lookback, scan_blocks, st));
+    depth_order_starts_kernel<<<(unsigned)scan_blocks, kIsectThreads, 0, st>>>(
+        n, order, tiles_per_gauss, lookback_from(ws + L.lookback), row_start,
+        n_isects_out);
+    return check_launch("depth_order_starts_kernel");
 }
 
 extern "C" size_t gsplat_isect_emit_sorted_workspace_size(int64_t n_isects) {
@@ -584,8 +605,8 @@ extern "C" int gsplat_isect_emit_sorted(
     int64_t n, int64_t N, int64_t I, const int64_t *image_ids,
     const float *means2d, const int32_t *radii, const float *depths,
     const float *conics, const float *opacities, int32_t tile_size,
-    int32_t tile_width, int32_t tile_height, const uint32_t *order,
-    const int64_t *cum_sorted, int64_t n_isects, void *workspace,
+    int32_t tile_width, int32_t tile_height, const int32_t *tiles_per_gauss,
+    const int64_t *row_start, int64_t n_isects, void *workspace,
     size_t workspace_bytes, int64_t *isect_ids, int32_t *flatten_ids,
     gsplat_stream_t stream) {
     clear_error();
@@ -595,7 +616,7 @@ extern "C" int gsplat_isect_emit_sorted(
     GS_REQUIRE(n_isects >= 0, "isect_emit_sorted: negative n_isects");
     if (n == 0 || n_isects == 0)
         return GSPLAT_OK;
-    GS_REQUIRE(depths && order && cum_sorted && isect_ids && flatten_ids,
+    GS_REQUIRE(depths && tiles_per_gauss && row_start && isect_ids && flatten_ids,
                "isect_emit_sorted: NULL buffer");
     GS_REQUIRE(I > 0, "isect_emit_sorted: I must be positive");
     const int ib = bit_length(I);
@@ -616,9 +637,9 @@ extern "C" int gsplat_isect_emit_sorted(
     uint64_t *ka = odd ? tmp_keys : out_keys, *kb = odd ? out_keys : tmp_keys;
     uint32_t *va = odd ? tmp_vals : out_vals, *vb = odd ? out_vals : tmp_vals;
     hipStream_t st = as_stream(stream);
-    isect_emit_sorted_kernel<<<(unsigned)ceil_div(n, kIsectThreads), kIsectThreads,
-                               0, st>>>(a, order, cum_sorted, ka, va);
-    GS_TRY(check_launch("isect_emit_sorted_kernel"));
+    isect_emit_at_kernel<<<(unsigned)ceil_div(n, kIsectThreads), kIsectThreads,
+                           0, st>>>(a, tiles_per_gauss, row_start, ka, va);
+    GS_TRY(check_launch("isect_emit_at_kernel"));
     bool in_b = false;
     GS_TRY(radix_sort_ping_pong(n_isects, 32, end_bit, ka, va, kb, vb,
                                 ws + L.sort_ws, workspace_bytes - L.sort_ws, st,

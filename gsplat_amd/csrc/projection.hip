@@ -14,9 +14,11 @@
 //   * the forward is written in a fixed IEEE operation order with contraction
 //     disabled, so the integer outputs (radii, validity, packed order) are
 //     reproducible bit for bit by the C host oracle;
-//   * the packed forward is ONE pass: rows are compacted with wave ballots and
-//     a decoupled look-back prefix, replacing the reference's count pass, host
-//     cumsum/sync and second projection pass;
+//   * the packed forward is ONE launch: each workgroup takes 4096 rows, finds
+//     the survivors with wave ballots, gets its output offset from a
+//     decoupled look-back prefix, then recomputes and writes the survivors
+//     (replacing the reference's count pass, host cumsum/sync and second
+//     launch);
 //   * the dense backward gives each Gaussian to one thread that loops over
 //     the C cameras, so gradients need no atomics and are deterministic.
 #include "common.h"
@@ -285,6 +287,12 @@ __global__ void __launch_bounds__(kProjThreads)
         compensations[row] = o.comp;
 }
 
+// Rows per packed-projection workgroup: 16 slices of 256 consecutive rows, so
+// the look-back chain that orders the workgroups is 16x shorter than with
+// one row per thread.
+constexpr int kPackItems = 16;
+constexpr int kPackRows = kProjThreads * kPackItems;
+
 __global__ void __launch_bounds__(kProjThreads) projection_packed_fwd_kernel(
     const FwdArgs a, Lookback lb, int32_t *__restrict__ indptr,
     int64_t *__restrict__ batch_ids, int64_t *__restrict__ camera_ids,
@@ -293,44 +301,70 @@ __global__ void __launch_bounds__(kProjThreads) projection_packed_fwd_kernel(
     float *__restrict__ conics, float *__restrict__ compensations,
     int64_t *__restrict__ nnz_out, int32_t *__restrict__ row_of) {
     __shared__ uint32_t s_ticket;
-    __shared__ uint32_t s_wave_count[kProjThreads / kWave];
+    __shared__ uint64_t s_ballot[kPackItems][kProjThreads / kWave];
+    __shared__ uint32_t s_slice_off[kPackItems + 1];
     __shared__ uint64_t s_prefix;
 
     const int64_t n_rows = a.B * a.C * a.N;
     const uint32_t bid = lb_ticket(lb, &s_ticket);
-    const int64_t row = (int64_t)bid * kProjThreads + threadIdx.x;
-    ProjOut o;
-    const bool valid = row < n_rows && project_flat_row(a, row, o);
-
+    const int64_t base = (int64_t)bid * kPackRows;
     const uint32_t wave = threadIdx.x / kWave;
-    const uint64_t ballot = __ballot(valid);
-    const uint32_t rank_in_wave = __popcll(ballot & lanemask_lt());
-    if (lane_id() == 0)
-        s_wave_count[wave] = (uint32_t)__popcll(ballot);
-    __syncthreads();
-    uint32_t wave_offset = 0, total = 0;
-#pragma unroll
-    for (int w = 0; w < kProjThreads / kWave; ++w) {
-        const uint32_t cnt = s_wave_count[w];
-        wave_offset += (w < (int)wave) ? cnt : 0u;
-        total += cnt;
+    const uint32_t lane = lane_id();
+
+    // phase 1: which rows of the 16 slices survive culling
+#pragma unroll 1
+    for (int j = 0; j < kPackItems; ++j) {
+        const int64_t row = base + (int64_t)j * kProjThreads + threadIdx.x;
+        ProjOut o;
+        const bool valid = row < n_rows && project_flat_row(a, row, o);
+        const uint64_t b = __ballot(valid);
+        if (lane == 0)
+            s_ballot[j][wave] = b;
     }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t run = 0;
+        for (int j = 0; j < kPackItems; ++j) {
+            s_slice_off[j] = run;
+            for (int w = 0; w < kProjThreads / kWave; ++w)
+                run += (uint32_t)__popcll(s_ballot[j][w]);
+        }
+        s_slice_off[kPackItems] = run;
+    }
+    __syncthreads();
+    const uint32_t total = s_slice_off[kPackItems];
     if (wave == 0) {
         const uint64_t excl = lb_exclusive_prefix(lb, bid, total);
-        if (lane_id() == 0)
+        if (lane == 0)
             s_prefix = excl;
     }
     __syncthreads();
-    const int64_t base = (int64_t)s_prefix;
-    const int64_t pos = base + wave_offset + rank_in_wave;
+    const int64_t block_out = (int64_t)s_prefix;
 
-    if (row < n_rows && row % a.N == 0) {
-        // first Gaussian of camera row bc: its exclusive position is indptr
-        indptr[row / a.N] = (int32_t)pos;
-    }
-    if (row_of != nullptr && row < n_rows)
-        row_of[row] = valid ? (int32_t)pos : -1;
-    if (valid) {
+    // phase 2: recompute the surviving rows (inputs are hot in L2) and write
+    // them at their packed positions
+#pragma unroll 1
+    for (int j = 0; j < kPackItems; ++j) {
+        const int64_t row = base + (int64_t)j * kProjThreads + threadIdx.x;
+        if (row >= n_rows)
+            break;
+        uint32_t wave_off = 0;
+        for (uint32_t w = 0; w < wave; ++w)
+            wave_off += (uint32_t)__popcll(s_ballot[j][w]);
+        const uint64_t bal = s_ballot[j][wave];
+        const bool valid = (bal >> lane) & 1ull;
+        const int64_t pos = block_out + s_slice_off[j] + wave_off +
+                            (uint32_t)__popcll(bal & lanemask_lt());
+        if (row % a.N == 0) {
+            // first Gaussian of camera row bc: its exclusive position is indptr
+            indptr[row / a.N] = (int32_t)pos;
+        }
+        if (row_of != nullptr)
+            row_of[row] = valid ? (int32_t)pos : -1;
+        if (!valid)
+            continue;
+        ProjOut o;
+        project_flat_row(a, row, o);
         const int64_t g = row % a.N;
         const int64_t bc = row / a.N;
         batch_ids[pos] = bc / a.C;
@@ -345,9 +379,9 @@ __global__ void __launch_bounds__(kProjThreads) projection_packed_fwd_kernel(
         if (compensations != nullptr)
             compensations[pos] = o.comp;
     }
-    const int64_t last_bid = (n_rows - 1) / kProjThreads;
+    const int64_t last_bid = (n_rows - 1) / kPackRows;
     if ((int64_t)bid == last_bid && threadIdx.x == 0) {
-        const int64_t nnz = base + total;
+        const int64_t nnz = block_out + total;
         indptr[a.B * a.C] = (int32_t)nnz;
         *nnz_out = nnz;
     }
@@ -924,7 +958,7 @@ extern "C" int gsplat_projection_fused_fwd(
 
 extern "C" size_t gsplat_projection_packed_workspace_size(int64_t B, int64_t C,
                                                           int64_t N) {
-    return lookback_bytes(ceil_div(B * C * N, kProjThreads));
+    return lookback_bytes(ceil_div(B * C * N, kPackRows));
 }
 
 extern "C" int gsplat_projection_packed_fwd(
@@ -949,7 +983,7 @@ extern "C" int gsplat_projection_packed_fwd(
                    depths && conics,
                "projection_packed: NULL output");
     GS_REQUIRE(rows < (1ll << 31), "projection_packed: more than 2^31 rows");
-    const int64_t blocks = ceil_div(rows, kProjThreads);
+    const int64_t blocks = ceil_div(rows, kPackRows);
     GS_REQUIRE(workspace != nullptr && workspace_bytes >= lookback_bytes(blocks),
                "projection_packed: workspace too small");
     hipStream_t st = as_stream(stream);

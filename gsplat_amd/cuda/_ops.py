@@ -428,15 +428,15 @@ def intersect_tile(
         # stable sort on the image|tile bits only: the reference's full-key
         # order (a per-image segmented sort, segmented=True, is the same order
         # because the image id occupies the top key bits).
-        order = torch.empty(n, dtype=_I32, device=dev)
-        cum = torch.empty(n, dtype=_I64, device=dev)
+        row_start = torch.empty(n, dtype=_I64, device=dev)
+        total = torch.empty(1, dtype=_I64, device=dev)
         ws = torch.empty(query("gsplat_isect_prepare_workspace_size", n),
                          dtype=torch.uint8, device=dev)
         call("gsplat_isect_prepare", n, N, ptr(img), ptr(means2d), ptr(radii),
              ptr(depths), ptr(conics), ptr(opacities), int(tile_size),
              int(tile_width), int(tile_height), ptr(ws), ws.numel(),
-             ptr(tiles_per_gauss), ptr(order), ptr(cum), st)
-        n_isects = int(cum[-1].item())
+             ptr(tiles_per_gauss), ptr(row_start), ptr(total), st)
+        n_isects = int(total.item())
         isect_ids = torch.empty(n_isects, dtype=_I64, device=dev)
         flatten_ids = torch.empty(n_isects, dtype=_I32, device=dev)
         if n_isects == 0:
@@ -445,8 +445,8 @@ def intersect_tile(
                           dtype=torch.uint8, device=dev)
         call("gsplat_isect_emit_sorted", n, N, int(I), ptr(img), ptr(means2d),
              ptr(radii), ptr(depths), ptr(conics), ptr(opacities), int(tile_size),
-             int(tile_width), int(tile_height), ptr(order), ptr(cum), n_isects,
-             ptr(ews), ews.numel(), ptr(isect_ids), ptr(flatten_ids), st)
+             int(tile_width), int(tile_height), ptr(tiles_per_gauss), ptr(row_start),
+             n_isects, ptr(ews), ews.numel(), ptr(isect_ids), ptr(flatten_ids), st)
         return tiles_per_gauss, isect_ids, flatten_ids
     cum = torch.empty(n, dtype=_I64, device=dev)
     ws = torch.empty(query("gsplat_isect_count_workspace_size", n),

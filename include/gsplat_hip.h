@@ -261,10 +261,11 @@ int gsplat_isect_emit(
     gsplat_stream_t stream);
 
 /* Sorted intersection, stage 1 of 2.  Counts the tiles of every row
- * (tiles_per_gauss [n], row order), sorts the rows stably by their depth
- * bits (order [n]: row indices, depth ascending, ties by row) and writes the
- * inclusive prefix of the counts in that order (cum_sorted [n] int64; its
- * last entry is n_isects).  Same row/camera arguments as gsplat_isect_count.
+ * (tiles_per_gauss [n]), orders the rows stably by their depth bits (ties by
+ * row) and gives every row its first slot in that order: row_start [n]
+ * int64 = the tile count of all rows before it in depth order.  The total
+ * (n_isects) goes to n_isects_out (device int64).  Same row/camera arguments
+ * as gsplat_isect_count.
  * Together with stage 2 this replaces intersect_tile with sort=True
  *   (gsplat/cuda/csrc/Intersect.cpp:33-164: count, cumsum, emit, and the
  *    full-key radix sort of IntersectTile.cu:478-520). */
@@ -275,12 +276,12 @@ int gsplat_isect_prepare(
     const float *conics, const float *opacities,
     int32_t tile_size, int32_t tile_width, int32_t tile_height,
     void *workspace, size_t workspace_bytes,
-    int32_t *tiles_per_gauss, uint32_t *order, int64_t *cum_sorted,
+    int32_t *tiles_per_gauss, int64_t *row_start, int64_t *n_isects_out,
     gsplat_stream_t stream);
 
-/* Sorted intersection, stage 2 of 2.  Emits every row's intersections in the
- * depth order of stage 1 and sorts them stably on the image|tile key bits
- * only.  The result equals the reference's full-key stable sort of the
+/* Sorted intersection, stage 2 of 2.  Writes every row's intersections at
+ * its row_start (stage 1), which lays them out in depth order, then sorts
+ * them stably on the image|tile key bits only.  The result equals the reference's full-key stable sort of the
  * row-order emission bit for bit: isect_ids [n_isects] ascending, ties (same
  * image, tile and depth bits) by row; flatten_ids [n_isects] the rows. */
 size_t gsplat_isect_emit_sorted_workspace_size(int64_t n_isects);
@@ -289,7 +290,7 @@ int gsplat_isect_emit_sorted(
     const float *means2d, const int32_t *radii, const float *depths,
     const float *conics, const float *opacities,
     int32_t tile_size, int32_t tile_width, int32_t tile_height,
-    const uint32_t *order, const int64_t *cum_sorted, int64_t n_isects,
+    const int32_t *tiles_per_gauss, const int64_t *row_start, int64_t n_isects,
     void *workspace, size_t workspace_bytes,
     int64_t *isect_ids, int32_t *flatten_ids, gsplat_stream_t stream);
 
