@@ -145,14 +145,34 @@ __device__ __forceinline__ float portable_expf(float x) {
     return p * scale;
 }
 
+// portable_expf without its range checks, for x that the caller knows to be
+// a non-NaN value <= 0 (the rasterizer's -sigma with 0 <= sigma <= ln(255 o)).
+// x is clamped to -87, so for every x >= -87 the result is bit-identical to
+// portable_expf(x); below -87 it returns e^-87 instead of 0, which can only
+// matter for an opacity above 255 e^87 (beyond the float range).
+__device__ __forceinline__ float portable_expf_nonpos(float x) {
+#pragma clang fp contract(off)
+    x = fmaxf(x, -87.f);
+    const float kf = __builtin_rintf(x * 0x1.715476p+0f);
+    float r = __builtin_fmaf(-kf, 0x1.63p-1f, x);
+    r = __builtin_fmaf(-kf, -0x1.bd0106p-13f, r);
+    float p = 0x1.a01a02p-13f;
+    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+    p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.f);
+    p = __builtin_fmaf(p, r, 1.f);
+    const float scale = __int_as_float(((int32_t)kf + 127) << 23);
+    return p * scale;
+}
+
 // DPP row operations (gfx9 encodings).
 constexpr int kDppQuadXor1 = 0xB1;   // quad_perm:[1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4E;   // quad_perm:[2,3,0,1]
 constexpr int kDppRowHalfMirror = 0x141;
 constexpr int kDppRowMirror = 0x140;
-
-constexpr int kDppRowBcast15 = 0x142;  // lane 15 of each row -> next row
-constexpr int kDppRowBcast31 = 0x143;  // lane 31 -> rows 2 and 3
 
 // DPP move restricted to the rows set in ROW_MASK; rows outside the mask
 // (and out-of-range sources) read 0.
@@ -162,20 +182,27 @@ __device__ __forceinline__ float dpp_f32_rows(float v) {
         0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
 }
 
-// Sum over the first ROWS (1 or 4) 16-lane rows of a wave, branch free: the
-// row-local butterflies leave every lane with its row's sum, then the two row
-// broadcasts fold rows 0-3 into row 3.  The total is in lane 16 * ROWS - 1
-// (other lanes hold partial sums).  Every lane of those rows must be active.
-template <int ROWS>
-__device__ __forceinline__ float wave_sum_to_last(float v) {
-    static_assert(ROWS == 1 || ROWS == 4, "ROWS must be 1 or 4");
+// Sum over each 16-lane row of the wave, branch free: every lane ends with
+// its row's sum.  Every lane of the row must be active.
+__device__ __forceinline__ float row_sum16(float v) {
     v += dpp_f32_rows<0xB1, 0xF>(v);   // quad_perm:[1,0,3,2]
     v += dpp_f32_rows<0x4E, 0xF>(v);   // quad_perm:[2,3,0,1]
     v += dpp_f32_rows<0x141, 0xF>(v);  // row_half_mirror
     v += dpp_f32_rows<0x140, 0xF>(v);  // row_mirror
+    return v;
+}
+
+// Sum over the first ROWS (1 or 4) 16-lane rows of a wave, branch free: row
+// sums, then the row broadcasts 15 (rows 1, 3 += rows 0, 2) and 31 (rows 2,
+// 3 += row 1) fold everything into row 3.  The total is in lane
+// 16 * ROWS - 1.  Every lane of those rows must be active.
+template <int ROWS>
+__device__ __forceinline__ float wave_sum_to_last(float v) {
+    static_assert(ROWS == 1 || ROWS == 4, "ROWS must be 1 or 4");
+    v = row_sum16(v);
     if (ROWS == 4) {
-        v += dpp_f32_rows<kDppRowBcast15, 0xA>(v);
-        v += dpp_f32_rows<kDppRowBcast31, 0xC>(v);
+        v += dpp_f32_rows<0x142, 0xA>(v);  // row_bcast:15
+        v += dpp_f32_rows<0x143, 0xC>(v);  // row_bcast:31
     }
     return v;
 }

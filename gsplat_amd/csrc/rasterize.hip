@@ -27,12 +27,12 @@
 // The forward ends a batch early when every pixel of the wave is done (the
 // per-lane loop exits when the wave's exec mask empties) and skips remaining
 // batches once the whole tile is done (__syncthreads_count).
-// The backward recovers T back to front in double (one Newton-refined
-// reciprocal per Gaussian), reduces each Gaussian's gradient over the wave
-// with a branch-free DPP reduction (row butterflies + row broadcasts, total
-// in the last lane), accumulates the waves in LDS (ds_add_f32) and issues
-// one global atomic per value per Gaussian per TILE, 8x fewer than one per
-// 32-lane warp.  Both kernels are compiled per (CDIM, tile size) so every
+// The backward runs 16x16 tiles with 128 threads of two pixels each,
+// recovers T back to front in double (one Newton-refined reciprocal per
+// Gaussian), sums a lane's two pixels, reduces each Gaussian's gradient over
+// the wave with branch-free DPP (row butterflies + row broadcasts), adds the
+// two wave sums in LDS and issues one global atomic per value per Gaussian
+// per TILE, 8x fewer than one per 32-lane warp.  Both kernels are compiled per (CDIM, tile size) so every
 // loop bound and reduction count is a constant.
 #include "common.h"
 
@@ -66,6 +66,29 @@ __device__ __forceinline__ void alpha_thresholds(float o, float &sig_max,
     }
 }
 
+// Conservative pixel-centre box of {sigma <= sig_max}: for a positive
+// definite conic Q = [[a, b], [b, c]], sigma = 1/2 d^T Q d <= s holds only
+// for |dx| <= sqrt(2 s c / det) and |dy| <= sqrt(2 s a / det).  The extents
+// are widened (x1.001 + 1 px) so float rounding in sigma can never put a
+// composited pixel outside; degenerate conics get an unbounded box and
+// Gaussians that never composite (sig_max < 0 or NaN) an empty one.  Used
+// only to skip work: a pixel outside the box fails the exact test anyway.
+__device__ __forceinline__ float4 alpha_support_box(float mx, float my, float a,
+                                                    float b, float c,
+                                                    float sig_max) {
+    if (!(sig_max >= 0.f))
+        return make_float4(__builtin_inff(), __builtin_inff(),
+                           -__builtin_inff(), -__builtin_inff());
+    const float det = a * c - b * b;
+    const float ex = sqrtf(2.f * sig_max * c / det) * 1.001f + 1.f;
+    const float ey = sqrtf(2.f * sig_max * a / det) * 1.001f + 1.f;
+    if (!(det > 0.f) || !(a > 0.f) || !(c > 0.f) || !(ex < 1e30f) ||
+        !(ey < 1e30f))
+        return make_float4(-__builtin_inff(), -__builtin_inff(),
+                           __builtin_inff(), __builtin_inff());
+    return make_float4(mx - ex, my - ey, mx + ex, my + ey);  // x0, y0, x1, y1
+}
+
 __device__ __forceinline__ void tile_coords(const RasterArgs &a, int64_t &image,
                                             int32_t &tile, int32_t &ty,
                                             int32_t &tx) {
@@ -82,7 +105,6 @@ __device__ __forceinline__ void tile_coords(const RasterArgs &a, int64_t &image,
 template <int TILE> struct TileShape {
     static constexpr int BS = TILE * TILE;
     static constexpr int ROWS = BS >= 64 ? 4 : BS / 16;
-    static constexpr int LAST = 16 * ROWS - 1;  // lane holding a wave sum
     static_assert(BS % 16 == 0, "tile must hold whole 16-lane rows");
 };
 
@@ -156,26 +178,33 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
         }
         __syncthreads();
         const int batch_size = min(BS, range_end - batch_start);
-        for (int t = 0; t < batch_size && !done; ++t) {
+        // wave-uniform loop; a lane that is done (or skips a Gaussian) is
+        // carried by selects, not branches
+        for (int t = 0; t < batch_size; ++t) {
+            if (!__ballot(!done))
+                break;
             const float4 geo = s_geo[t];
             const float4 con = s_con[t];
             const float dx = geo.x - px, dy = geo.y - py;
             const float sigma = gauss_sigma(con.x, con.y, con.z, dx, dy);
-            if (sigma < 0.f || sigma > geo.w)
+            const bool take = !done && sigma >= 0.f && sigma <= geo.w;
+            if (!__ballot(take))
                 continue;
-            const float vis = portable_expf(-sigma);
-            const float alpha = sigma < con.w ? kMaxAlpha : geo.z * vis;
-            const float next_T = T * (1.f - alpha);
-            if (next_T <= kTransmittanceThreshold) {
-                done = true;
-                break;
-            }
-            const float w = alpha * T;
+            if (take) {
+                const float vis = portable_expf_nonpos(-sigma);
+                const float alpha = sigma < con.w ? kMaxAlpha : geo.z * vis;
+                const float next_T = T * (1.f - alpha);
+                const bool stop = next_T <= kTransmittanceThreshold;
+                const float w = alpha * T;
 #pragma unroll
-            for (int k = 0; k < CDIM; ++k)
-                acc[k] += s_col[t * CDIM + k] * w;
-            cur_idx = batch_start + t;
-            T = next_T;
+                for (int k = 0; k < CDIM; ++k) {
+                    const float c = acc[k] + s_col[t * CDIM + k] * w;
+                    acc[k] = stop ? acc[k] : c;
+                }
+                cur_idx = stop ? cur_idx : batch_start + t;
+                T = stop ? T : next_T;
+                done = stop;
+            }
         }
     }
     if (inside) {
@@ -191,8 +220,21 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
     }
 }
 
+// Backward launch shape: at 16x16 every thread takes PX = 2 pixels (two
+// vertically adjacent rows), so each broadcast LDS read of a staged Gaussian
+// serves twice the pixels and a lane sums its two pixels before the wave
+// reduction (half the reductions and LDS atomics per tile).
+template <int TILE> struct BwdShape {
+    static constexpr int BS = TILE * TILE;       // pixels = staged Gaussians
+    static constexpr int PX = TILE == 16 ? 2 : 1;
+    static constexpr int THREADS = BS / PX;
+    static constexpr int ROWS = THREADS >= 64 ? 4 : THREADS / 16;
+    static constexpr int LAST = 16 * ROWS - 1;   // lane holding a wave sum
+    static_assert(THREADS % 16 == 0, "whole 16-lane rows");
+};
+
 template <int CDIM, int TILE, bool ABS>
-__global__ void __launch_bounds__(TILE * TILE) rasterize_bwd_kernel(
+__global__ void __launch_bounds__(BwdShape<TILE>::THREADS) rasterize_bwd_kernel(
     const RasterArgs a, const float *__restrict__ render_alphas,
     const float *__restrict__ render_T, const int32_t *__restrict__ last_ids,
     const float *__restrict__ v_render_colors,
@@ -200,8 +242,10 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_bwd_kernel(
     float *__restrict__ v_means2d_abs, float *__restrict__ v_means2d,
     float *__restrict__ v_conics, float *__restrict__ v_colors,
     float *__restrict__ v_opacities) {
-    using TS = TileShape<TILE>;
-    constexpr int BS = TS::BS;
+    using SH = BwdShape<TILE>;
+    constexpr int BS = SH::BS;
+    constexpr int PX = SH::PX;
+    constexpr int NT = SH::THREADS;
     // per-Gaussian sums: xy(2), conic(3), colour(CDIM), opacity(1) [, |xy|(2)]
     constexpr int NACC = 2 + 3 + CDIM + 1 + (ABS ? 2 : 0);
     __shared__ float4 s_geo[BS];
@@ -210,6 +254,9 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_bwd_kernel(
     __shared__ float s_acc[NACC * BS];
     __shared__ int32_t s_gid[BS];
     __shared__ int32_t s_hit[BS];
+    constexpr int NW = (NT + kWave - 1) / kWave;  // waves per tile
+    __shared__ uint8_t s_wmask[BS];               // waves a Gaussian can reach
+    __shared__ uint16_t s_list[NW][BS];           // per-wave work list
 
     int64_t image;
     int32_t tile, ty, tx;
@@ -218,13 +265,8 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_bwd_kernel(
     if (a.masks != nullptr && !a.masks[image * n_tiles + tile])
         return;
     const int tr = threadIdx.x;
-    const int i = ty * TILE + tr / TILE;
-    const int j = tx * TILE + tr % TILE;
-    const bool inside = i < a.H && j < a.W;
-    const int64_t pix = ((int64_t)image * a.H + (inside ? i : 0)) * a.W +
-                        (inside ? j : 0);
-    const float px = (float)j + 0.5f, py = (float)i + 0.5f;
-    const bool last_lane = lane_id() == (uint32_t)TS::LAST;
+    const bool last_lane = lane_id() == (uint32_t)SH::LAST;
+    const int wave = tr / kWave;
 
     const int32_t *offs = a.tile_offsets + image * n_tiles;
     const int32_t range_start = offs[tile];
@@ -233,115 +275,184 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_bwd_kernel(
                                   : offs[tile + 1];
     const int num_batches = (range_end - range_start + BS - 1) / BS;
 
-    // The transmittance itself when the forward stored it: 1 - (1 - T)
-    // loses most of T's significant bits once T nears the 1e-4 cutoff.
-    const float T_final =
-        inside ? (render_T != nullptr ? render_T[pix] : 1.f - render_alphas[pix])
-               : 1.f;
-    // T before each Gaussian is recovered back to front by undoing the
-    // forward's products.  It is carried in double and each step multiplies
-    // by 1 / (1 - alpha) refined to ~2^-46 by one Newton step from the fp32
-    // reciprocal, so T keeps only the forward's own rounding instead of one
-    // extra float32 rounding per Gaussian behind it.
-    double T64 = (double)T_final;
-    float T = T_final;
-    const int32_t bin_final = inside ? last_ids[pix] : -1;
-    float v_c[CDIM], buffer[CDIM];
-    float bg_dot = 0.f;
+    // per-pixel state; pixel p of thread tr is (row PX * (tr / TILE) + p,
+    // column tr % TILE) of the tile
+    bool inside[PX];
+    float px[PX], py[PX], T_final[PX], T[PX], v_a[PX], bg_dot[PX];
+    double T64[PX];
+    int32_t bin_final[PX];
+    float v_c[PX][CDIM], buffer[PX][CDIM];
+    int32_t wave_bin = -1;
 #pragma unroll
-    for (int k = 0; k < CDIM; ++k) {
-        v_c[k] = inside ? v_render_colors[pix * CDIM + k] : 0.f;
-        buffer[k] = 0.f;
-        if (a.backgrounds)
-            bg_dot += a.backgrounds[image * CDIM + k] * v_c[k];
+    for (int p = 0; p < PX; ++p) {
+        const int i = ty * TILE + PX * (tr / TILE) + p;
+        const int j = tx * TILE + tr % TILE;
+        inside[p] = i < a.H && j < a.W;
+        const int64_t pix = ((int64_t)image * a.H + (inside[p] ? i : 0)) * a.W +
+                            (inside[p] ? j : 0);
+        px[p] = (float)j + 0.5f;
+        py[p] = (float)i + 0.5f;
+        // The transmittance itself when the forward stored it: 1 - (1 - T)
+        // loses most of T's significant bits once T nears the 1e-4 cutoff.
+        T_final[p] = inside[p] ? (render_T != nullptr ? render_T[pix]
+                                                      : 1.f - render_alphas[pix])
+                               : 1.f;
+        // T before each Gaussian is recovered back to front by undoing the
+        // forward's products.  It is carried in double and each step
+        // multiplies by 1 / (1 - alpha) refined to ~2^-46 by one Newton step
+        // from the fp32 reciprocal, so T keeps only the forward's own rounding
+        // instead of one extra float32 rounding per Gaussian behind it.
+        T64[p] = (double)T_final[p];
+        T[p] = T_final[p];
+        bin_final[p] = inside[p] ? last_ids[pix] : -1;
+        wave_bin = max(wave_bin, bin_final[p]);
+        bg_dot[p] = 0.f;
+#pragma unroll
+        for (int k = 0; k < CDIM; ++k) {
+            v_c[p][k] = inside[p] ? v_render_colors[pix * CDIM + k] : 0.f;
+            buffer[p][k] = 0.f;
+            if (a.backgrounds)
+                bg_dot[p] += a.backgrounds[image * CDIM + k] * v_c[p][k];
+        }
+        v_a[p] = inside[p] ? v_render_alphas[pix] : 0.f;
     }
-    const float v_a = inside ? v_render_alphas[pix] : 0.f;
-    const int32_t wave_bin_final = wave_max_i32(bin_final);
+    const int32_t wave_bin_final = wave_max_i32(wave_bin);
 
     for (int b = 0; b < num_batches; ++b) {
         __syncthreads();
         const int32_t batch_end = range_end - 1 - b * BS;
         const int batch_size = min(BS, batch_end + 1 - range_start);
-        const int32_t idx = batch_end - tr;
-        if (idx >= range_start) {
-            const int32_t g = a.flatten_ids[idx];
-            s_gid[tr] = g;
-            const float2 xy = reinterpret_cast<const float2 *>(a.means2d)[g];
-            const float o = a.opacities[g];
-            float sig_max, sig_clamp;
-            alpha_thresholds(o, sig_max, sig_clamp);
-            s_geo[tr] = make_float4(xy.x, xy.y, o, sig_max);
-            s_con[tr] = make_float4(a.conics[g * 3 + 0], a.conics[g * 3 + 1],
-                                    a.conics[g * 3 + 2], sig_clamp);
 #pragma unroll
-            for (int k = 0; k < CDIM; ++k)
-                s_col[tr * CDIM + k] = a.colors[(int64_t)g * CDIM + k];
+        for (int q = 0; q < PX; ++q) {
+            const int slot = tr + q * NT;
+            const int32_t idx = batch_end - slot;
+            if (idx >= range_start) {
+                const int32_t g = a.flatten_ids[idx];
+                s_gid[slot] = g;
+                const float2 xy = reinterpret_cast<const float2 *>(a.means2d)[g];
+                const float o = a.opacities[g];
+                float sig_max, sig_clamp;
+                alpha_thresholds(o, sig_max, sig_clamp);
+                const float ca = a.conics[g * 3 + 0], cb = a.conics[g * 3 + 1],
+                            cc = a.conics[g * 3 + 2];
+                s_geo[slot] = make_float4(xy.x, xy.y, o, sig_max);
+                s_con[slot] = make_float4(ca, cb, cc, sig_clamp);
+#pragma unroll
+                for (int k = 0; k < CDIM; ++k)
+                    s_col[slot * CDIM + k] = a.colors[(int64_t)g * CDIM + k];
+                // which waves' pixel strips the Gaussian's alpha support can
+                // reach (wave w holds rows w * WROWS .. of the tile)
+                const float4 box = alpha_support_box(xy.x, xy.y, ca, cb, cc, sig_max);
+                const float cx0 = (float)(tx * TILE) + 0.5f;
+                const float cx1 = cx0 + (float)(TILE - 1);
+                uint32_t m = 0;
+                if (box.x <= cx1 && box.z >= cx0) {
+#pragma unroll
+                    for (int w = 0; w < NW; ++w) {
+                        constexpr int WROWS = (kWave < NT ? kWave : NT) * PX / TILE;
+                        const float cy0 = (float)(ty * TILE + w * WROWS) + 0.5f;
+                        const float cy1 = cy0 + (float)(WROWS - 1);
+                        if (box.y <= cy1 && box.w >= cy0)
+                            m |= 1u << w;
+                    }
+                }
+                s_wmask[slot] = (uint8_t)m;
+            } else {
+                s_wmask[slot] = 0;
+            }
+            s_hit[slot] = 0;
+#pragma unroll
+            for (int k = 0; k < NACC; ++k)
+                s_acc[k * BS + slot] = 0.f;
         }
-        s_hit[tr] = 0;
-#pragma unroll
-        for (int k = 0; k < NACC; ++k)
-            s_acc[k * BS + tr] = 0.f;
         __syncthreads();
 
-        // slots t with isect index batch_end - t > wave_bin_final are behind
-        // every pixel of this wave
+        // this wave's work list, in slot order: Gaussians in front of the
+        // wave's last contributor (slots t with isect index batch_end - t >
+        // wave_bin_final are behind every pixel of the wave) whose alpha
+        // support reaches the wave's pixels
         const int t0 = max(0, batch_end - wave_bin_final);
-        for (int t = t0; t < batch_size; ++t) {
+        int n_work = 0;
+        for (int c0 = 0; c0 < batch_size; c0 += kWave) {
+            const int slot = c0 + (int)lane_id();
+            const bool take = slot < batch_size && slot >= t0 &&
+                              ((s_wmask[slot] >> wave) & 1u);
+            const uint64_t bal = __ballot(take);
+            if (take)
+                s_list[wave][n_work + __popcll(bal & lanemask_lt())] = (uint16_t)slot;
+            n_work += __popcll(bal);
+        }
+        __builtin_amdgcn_wave_barrier();
+        for (int n = 0; n < n_work; ++n) {
+            const int t = s_list[wave][n];
             const int32_t isect = batch_end - t;
             const float4 geo = s_geo[t];
             const float4 con = s_con[t];
-            const float dx = geo.x - px, dy = geo.y - py;
-            const float sigma = gauss_sigma(con.x, con.y, con.z, dx, dy);
-            const bool valid = inside && isect <= bin_final && sigma >= 0.f &&
-                               sigma <= geo.w;
-            if (!__ballot(valid))
+            float dx[PX], dy[PX], sigma[PX];
+            bool valid[PX];
+            bool any = false;
+#pragma unroll
+            for (int p = 0; p < PX; ++p) {
+                dx[p] = geo.x - px[p];
+                dy[p] = geo.y - py[p];
+                sigma[p] = gauss_sigma(con.x, con.y, con.z, dx[p], dy[p]);
+                valid[p] = inside[p] && isect <= bin_final[p] &&
+                           sigma[p] >= 0.f && sigma[p] <= geo.w;
+                any |= valid[p];
+            }
+            if (!__ballot(any))
                 continue;
             float g[NACC];
 #pragma unroll
             for (int k = 0; k < NACC; ++k)
                 g[k] = 0.f;
-            if (valid) {
-                const float vis = portable_expf(-sigma);
-                const bool clamped = sigma < con.w;
+#pragma unroll
+            for (int p = 0; p < PX; ++p) {
+                if (!valid[p])
+                    continue;
+                const float vis = portable_expf_nonpos(-sigma[p]);
+                const bool clamped = sigma[p] < con.w;
                 const float alpha = clamped ? kMaxAlpha : geo.z * vis;
-                // alpha <= 0.99, so 1 - alpha >= 0.01 (the reference's
-                // 1e-6 floor never binds)
+                // alpha <= 0.99, so 1 - alpha >= 0.01 (the reference's 1e-6
+                // floor never binds)
                 const float one_minus = fmaxf(kMinOneMinusAlpha, 1.f - alpha);
                 const float ra = __builtin_amdgcn_rcpf(one_minus);
                 const double d = (double)one_minus;
                 double r = (double)ra;
                 r = __builtin_fma(r, __builtin_fma(-d, r, 1.0), r);
-                T64 = T64 * r;
-                T = (float)T64;
-                const float fac = alpha * T;
+                T64[p] = T64[p] * r;
+                T[p] = (float)T64[p];
+                const float fac = alpha * T[p];
                 float v_alpha = 0.f;
 #pragma unroll
                 for (int k = 0; k < CDIM; ++k) {
                     const float ck = s_col[t * CDIM + k];
-                    g[5 + k] = fac * v_c[k];
-                    v_alpha += (ck * T - buffer[k] * ra) * v_c[k];
-                    buffer[k] += ck * fac;
+                    g[5 + k] += fac * v_c[p][k];
+                    v_alpha += (ck * T[p] - buffer[p][k] * ra) * v_c[p][k];
+                    buffer[p][k] += ck * fac;
                 }
-                v_alpha += T_final * ra * v_a;
+                v_alpha += T_final[p] * ra * v_a[p];
                 if (a.backgrounds)
-                    v_alpha += -T_final * ra * bg_dot;
+                    v_alpha += -T_final[p] * ra * bg_dot[p];
                 if (!clamped) {
                     const float v_sigma = -geo.z * vis * v_alpha;
-                    g[2] = 0.5f * v_sigma * dx * dx;
-                    g[3] = v_sigma * dx * dy;
-                    g[4] = 0.5f * v_sigma * dy * dy;
-                    g[0] = v_sigma * (con.x * dx + con.y * dy);
-                    g[1] = v_sigma * (con.y * dx + con.z * dy);
-                    g[5 + CDIM] = vis * v_alpha;
+                    const float gx = v_sigma * (con.x * dx[p] + con.y * dy[p]);
+                    const float gy = v_sigma * (con.y * dx[p] + con.z * dy[p]);
+                    g[0] += gx;
+                    g[1] += gy;
+                    g[2] += 0.5f * v_sigma * dx[p] * dx[p];
+                    g[3] += v_sigma * dx[p] * dy[p];
+                    g[4] += 0.5f * v_sigma * dy[p] * dy[p];
+                    g[5 + CDIM] += vis * v_alpha;
                     if (ABS) {
-                        g[6 + CDIM] = fabsf(g[0]);
-                        g[7 + CDIM] = fabsf(g[1]);
+                        g[6 + CDIM] += fabsf(gx);
+                        g[7 + CDIM] += fabsf(gy);
                     }
                 }
             }
 #pragma unroll
             for (int k = 0; k < NACC; ++k)
-                g[k] = wave_sum_to_last<TS::ROWS>(g[k]);
+                g[k] = wave_sum_to_last<SH::ROWS>(g[k]);
             if (last_lane) {
 #pragma unroll
                 for (int k = 0; k < NACC; ++k)
@@ -350,23 +461,27 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_bwd_kernel(
             }
         }
         __syncthreads();
-        if (tr < batch_size && s_hit[tr]) {
-            const int32_t g = s_gid[tr];
-            atomic_add_f32(v_means2d + (int64_t)g * 2 + 0, s_acc[0 * BS + tr]);
-            atomic_add_f32(v_means2d + (int64_t)g * 2 + 1, s_acc[1 * BS + tr]);
-            atomic_add_f32(v_conics + (int64_t)g * 3 + 0, s_acc[2 * BS + tr]);
-            atomic_add_f32(v_conics + (int64_t)g * 3 + 1, s_acc[3 * BS + tr]);
-            atomic_add_f32(v_conics + (int64_t)g * 3 + 2, s_acc[4 * BS + tr]);
 #pragma unroll
-            for (int k = 0; k < CDIM; ++k)
-                atomic_add_f32(v_colors + (int64_t)g * CDIM + k,
-                               s_acc[(5 + k) * BS + tr]);
-            atomic_add_f32(v_opacities + g, s_acc[(5 + CDIM) * BS + tr]);
-            if (ABS) {
-                atomic_add_f32(v_means2d_abs + (int64_t)g * 2 + 0,
-                               s_acc[(6 + CDIM) * BS + tr]);
-                atomic_add_f32(v_means2d_abs + (int64_t)g * 2 + 1,
-                               s_acc[(7 + CDIM) * BS + tr]);
+        for (int q = 0; q < PX; ++q) {
+            const int slot = tr + q * NT;
+            if (slot < batch_size && s_hit[slot]) {
+                const int32_t g = s_gid[slot];
+                atomic_add_f32(v_means2d + (int64_t)g * 2 + 0, s_acc[0 * BS + slot]);
+                atomic_add_f32(v_means2d + (int64_t)g * 2 + 1, s_acc[1 * BS + slot]);
+                atomic_add_f32(v_conics + (int64_t)g * 3 + 0, s_acc[2 * BS + slot]);
+                atomic_add_f32(v_conics + (int64_t)g * 3 + 1, s_acc[3 * BS + slot]);
+                atomic_add_f32(v_conics + (int64_t)g * 3 + 2, s_acc[4 * BS + slot]);
+#pragma unroll
+                for (int k = 0; k < CDIM; ++k)
+                    atomic_add_f32(v_colors + (int64_t)g * CDIM + k,
+                                   s_acc[(5 + k) * BS + slot]);
+                atomic_add_f32(v_opacities + g, s_acc[(5 + CDIM) * BS + slot]);
+                if (ABS) {
+                    atomic_add_f32(v_means2d_abs + (int64_t)g * 2 + 0,
+                                   s_acc[(6 + CDIM) * BS + slot]);
+                    atomic_add_f32(v_means2d_abs + (int64_t)g * 2 + 1,
+                                   s_acc[(7 + CDIM) * BS + slot]);
+                }
             }
         }
     }
@@ -481,8 +596,8 @@ extern "C" int gsplat_rasterize_bwd(
     GS_REQUIRE(blocks < (1ll << 31), "rasterize_bwd: too many tiles");
     hipStream_t st = as_stream(stream);
 #define GS_BWD(C, TILE, ABS)                                                   \
-    rasterize_bwd_kernel<C, TILE, ABS><<<(unsigned)blocks, TILE * TILE, 0,     \
-                                         st>>>(                                \
+    rasterize_bwd_kernel<C, TILE, ABS><<<(unsigned)blocks,                     \
+                                         BwdShape<TILE>::THREADS, 0, st>>>(    \
         a, render_alphas, render_transmittance, last_ids, v_render_colors,     \
         v_render_alphas, v_means2d_abs, v_means2d, v_conics, v_colors,         \
         v_opacities)
