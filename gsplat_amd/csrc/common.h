@@ -338,6 +338,12 @@ __device__ __forceinline__ uint32_t lb_ticket(const Lookback &lb,
     return *smem_slot;
 }
 
+// Predecessor status words each lane examines per look-back step: one step
+// covers 64 * kLbWords workgroups, so the inclusive prefix crosses that many
+// workgroups per round trip through the device-coherent level of the
+// memory hierarchy.
+constexpr int kLbWords = 4;
+
 // Called by all 64 lanes of ONE wave after `aggregate` of workgroup `bid` is
 // known; returns (in every lane) the exclusive prefix of workgroup bid and
 // publishes its inclusive prefix.
@@ -355,30 +361,50 @@ __device__ __forceinline__ uint64_t lb_exclusive_prefix(const Lookback &lb,
     uint64_t excl = 0;
     int64_t base = (int64_t)bid - 1;
     while (true) {
-        const int64_t idx = base - (int64_t)lane;
-        uint64_t s = (idx >= 0) ? lb_load(lb.status + idx) : kLbFlagInc;
-        // wait until every predecessor in the window has published something
-        while (__ballot((s >> 62) == 0)) {
-            __builtin_amdgcn_s_sleep(1);
-            if ((s >> 62) == 0)
-                s = lb_load(lb.status + idx);
+        // lane l holds predecessors base - l * kLbWords - k, nearest first;
+        // indices below 0 read as an inclusive prefix of 0
+        uint64_t s[kLbWords];
+#pragma unroll
+        for (int k = 0; k < kLbWords; ++k) {
+            const int64_t idx = base - (int64_t)lane * kLbWords - k;
+            s[k] = idx >= 0 ? lb_load(lb.status + idx) : kLbFlagInc;
         }
-        const uint64_t inc = __ballot((s >> 62) == 2);
-        uint64_t v = s & kLbValMask;
+        // wait until every predecessor in the window has published something
+        while (true) {
+            bool pending = false;
+#pragma unroll
+            for (int k = 0; k < kLbWords; ++k)
+                pending |= (s[k] >> 62) == 0;
+            if (!__ballot(pending))
+                break;
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int k = 0; k < kLbWords; ++k)
+                if ((s[k] >> 62) == 0)
+                    s[k] = lb_load(lb.status + (base - (int64_t)lane * kLbWords - k));
+        }
+        int kf = kLbWords;  // this lane's nearest inclusive word
+#pragma unroll
+        for (int k = kLbWords - 1; k >= 0; --k)
+            if ((s[k] >> 62) == 2)
+                kf = k;
+        uint64_t v = 0;
+#pragma unroll
+        for (int k = 0; k < kLbWords; ++k)
+            if (k <= kf)
+                v += s[k] & kLbValMask;
+        const uint64_t inc = __ballot(kf < kLbWords);
         if (inc) {
             const uint32_t first = __builtin_ctzll(inc);  // closest inclusive
             if (lane > first)
                 v = 0;
-            // sum of lanes 0..first
-            for (int off = 32; off >= 1; off >>= 1)
-                v += __shfl_xor(v, off);
-            excl += v;
-            break;
         }
         for (int off = 32; off >= 1; off >>= 1)
             v += __shfl_xor(v, off);
         excl += v;
-        base -= 64;
+        if (inc)
+            break;
+        base -= 64 * kLbWords;
     }
     if (lane == 0)
         lb_store(lb.status + bid, kLbFlagInc | (excl + aggregate));

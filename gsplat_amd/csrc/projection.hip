@@ -14,11 +14,11 @@
 //   * the forward is written in a fixed IEEE operation order with contraction
 //     disabled, so the integer outputs (radii, validity, packed order) are
 //     reproducible bit for bit by the C host oracle;
-//   * the packed forward is ONE launch: each workgroup takes 4096 rows, finds
-//     the survivors with wave ballots, gets its output offset from a
-//     decoupled look-back prefix, then recomputes and writes the survivors
-//     (replacing the reference's count pass, host cumsum/sync and second
-//     launch);
+//   * the packed forward is ONE launch: each workgroup projects 4096 rows
+//     into registers, counts the survivors with wave ballots, gets its
+//     output offset from a decoupled look-back prefix and writes the
+//     survivors (replacing the reference's count pass, host cumsum/sync and
+//     second launch, which projects every row twice);
 //   * the dense backward gives each Gaussian to one thread that loops over
 //     the C cameras, so gradients need no atomics and are deterministic.
 #include "common.h"
@@ -32,6 +32,8 @@ struct Cam {
     float R[9];  // row-major world->camera rotation
     float t[3];
     float fx, fy, cx, cy;
+    // forward perspective clamp limits (set_fwd_limits)
+    float lim_x_pos, lim_x_neg, lim_y_pos, lim_y_neg;
 };
 
 __device__ __forceinline__ void load_cam(const float *viewmat, const float *K,
@@ -47,6 +49,19 @@ __device__ __forceinline__ void load_cam(const float *viewmat, const float *K,
     cam.fy = K[4];
     cam.cx = K[2];
     cam.cy = K[5];
+}
+
+// Camera constants of the forward's perspective Jacobian clamp (persp_proj,
+// Utils.cuh:542): computed once per camera load instead of per row; the
+// values are the same IEEE results the per-row formula gives.
+__device__ __forceinline__ void set_fwd_limits(Cam &cam, float W, float H) {
+#pragma clang fp contract(off)
+    const float tan_fovx = (0.5f * W) / cam.fx;
+    const float tan_fovy = (0.5f * H) / cam.fy;
+    cam.lim_x_pos = (W - cam.cx) / cam.fx + 0.3f * tan_fovx;
+    cam.lim_x_neg = cam.cx / cam.fx + 0.3f * tan_fovx;
+    cam.lim_y_pos = (H - cam.cy) / cam.fy + 0.3f * tan_fovy;
+    cam.lim_y_neg = cam.cy / cam.fy + 0.3f * tan_fovy;
 }
 
 // Symmetric 3x3 stored as (00, 01, 02, 11, 12, 22).
@@ -167,16 +182,12 @@ __device__ __forceinline__ bool project_exact(
         mx = cam.fx * mcx + cam.cx;
         my = cam.fy * mcy + cam.cy;
     } else {
-        const float tan_fovx = (0.5f * W) / cam.fx;
-        const float tan_fovy = (0.5f * H) / cam.fy;
-        const float lim_x_pos = (W - cam.cx) / cam.fx + 0.3f * tan_fovx;
-        const float lim_x_neg = cam.cx / cam.fx + 0.3f * tan_fovx;
-        const float lim_y_pos = (H - cam.cy) / cam.fy + 0.3f * tan_fovy;
-        const float lim_y_neg = cam.cy / cam.fy + 0.3f * tan_fovy;
         const float rz = 1.f / mcz;
         const float rz2 = rz * rz;
-        const float tx = mcz * fminf(lim_x_pos, fmaxf(-lim_x_neg, mcx * rz));
-        const float ty = mcz * fminf(lim_y_pos, fmaxf(-lim_y_neg, mcy * rz));
+        const float tx =
+            mcz * fminf(cam.lim_x_pos, fmaxf(-cam.lim_x_neg, mcx * rz));
+        const float ty =
+            mcz * fminf(cam.lim_y_pos, fmaxf(-cam.lim_y_neg, mcy * rz));
         J00 = cam.fx * rz;
         J11 = cam.fy * rz;
         J02 = ((-cam.fx) * tx) * rz2;
@@ -244,16 +255,46 @@ struct FwdArgs {
     float W, H, eps2d, near_plane, far_plane, radius_clip;
     int camera_model;
     bool calc_comp;
+    bool idx32;  // B * C * N < 2^31: row index arithmetic in 32 bits
 };
+
+// row = (b * C + c) * N + g  ->  bc = b * C + c, g, and the Gaussian's input
+// row b * N + g
+__device__ __forceinline__ void split_row(const FwdArgs &a, int64_t row,
+                                          int64_t &bc, int64_t &g,
+                                          int64_t &bg) {
+    if (a.idx32) {
+        const uint32_t r = (uint32_t)row, n = (uint32_t)a.N;
+        const uint32_t q = r / n;
+        bc = q;
+        g = r - q * n;
+        bg = (int64_t)(q / (uint32_t)a.C) * a.N + g;
+    } else {
+        bc = row / a.N;
+        g = row - bc * a.N;
+        bg = (bc / a.C) * a.N + g;
+    }
+}
+
+// Camera of (batch, camera) row bc: loaded once per wave (scalar loads) when
+// all the wave's rows belong to one camera row, per lane otherwise.
+__device__ __forceinline__ void load_row_cam(const FwdArgs &a, int64_t bc,
+                                             Cam &cam) {
+    const int64_t bc0 = ((int64_t)__builtin_amdgcn_readfirstlane((int)(bc >> 32)) << 32) |
+                        (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)bc);
+    if (!__ballot(bc != bc0))
+        load_cam(a.viewmats + bc0 * 16, a.Ks + bc0 * 9, cam);
+    else
+        load_cam(a.viewmats + bc * 16, a.Ks + bc * 9, cam);
+    set_fwd_limits(cam, a.W, a.H);
+}
 
 __device__ __forceinline__ bool project_flat_row(const FwdArgs &a, int64_t row,
                                                  ProjOut &o) {
-    const int64_t g = row % a.N;
-    const int64_t bc = row / a.N;  // b * C + c
-    const int64_t b = bc / a.C;
+    int64_t bc, g, bg;
+    split_row(a, row, bc, g, bg);
     Cam cam;
-    load_cam(a.viewmats + bc * 16, a.Ks + bc * 9, cam);
-    const int64_t bg = b * a.N + g;
+    load_row_cam(a, bc, cam);
     return project_exact(
         cam, a.means + bg * 3, a.covars ? a.covars + bg * 6 : nullptr,
         a.quats ? a.quats + bg * 4 : nullptr,
@@ -287,23 +328,32 @@ __global__ void __launch_bounds__(kProjThreads)
         compensations[row] = o.comp;
 }
 
-// Rows per packed-projection workgroup: 16 slices of 256 consecutive rows, so
-// the look-back chain that orders the workgroups is 16x shorter than with
-// one row per thread.
-constexpr int kPackItems = 16;
-constexpr int kPackRows = kProjThreads * kPackItems;
+// Packed forward workgroup: 1024 threads x kPackItems rows = 4096 rows in
+// kPackItems slices of 1024 consecutive rows (one wave reads 64 consecutive
+// Gaussians per slice).  Every input of a thread's rows is loaded before any
+// of them is projected, so a wave waits for memory once; the projected rows
+// stay in registers between the survivor count and the write (inputs are
+// read once).  Few, large workgroups keep the look-back chain that orders
+// them short (245 links per million rows).
+constexpr int kPackThreads = 1024;
+constexpr int kPackItems = 4;
+constexpr int kPackRows = kPackThreads * kPackItems;
 
-__global__ void __launch_bounds__(kProjThreads) projection_packed_fwd_kernel(
+template <bool COVARS>
+__global__ void __launch_bounds__(kPackThreads) projection_packed_fwd_kernel(
     const FwdArgs a, Lookback lb, int32_t *__restrict__ indptr,
     int64_t *__restrict__ batch_ids, int64_t *__restrict__ camera_ids,
     int64_t *__restrict__ gaussian_ids, int32_t *__restrict__ radii,
     float *__restrict__ means2d, float *__restrict__ depths,
     float *__restrict__ conics, float *__restrict__ compensations,
     int64_t *__restrict__ nnz_out, int32_t *__restrict__ row_of) {
+    constexpr int NW = kPackThreads / kWave;
+    static_assert(kPackItems * NW == kWave, "one wave scans the wave counts");
     __shared__ uint32_t s_ticket;
-    __shared__ uint64_t s_ballot[kPackItems][kProjThreads / kWave];
-    __shared__ uint32_t s_slice_off[kPackItems + 1];
+    __shared__ uint32_t s_cnt[kPackItems * NW];  // survivors per (slice, wave)
+    __shared__ uint32_t s_off[kPackItems * NW];  // their exclusive prefix
     __shared__ uint64_t s_prefix;
+    __shared__ uint32_t s_total;
 
     const int64_t n_rows = a.B * a.C * a.N;
     const uint32_t bid = lb_ticket(lb, &s_ticket);
@@ -311,77 +361,122 @@ __global__ void __launch_bounds__(kProjThreads) projection_packed_fwd_kernel(
     const uint32_t wave = threadIdx.x / kWave;
     const uint32_t lane = lane_id();
 
-    // phase 1: which rows of the 16 slices survive culling
-#pragma unroll 1
+    // phase 0: row indices and every input of the thread's rows (rows past
+    // the end read the last row and are dropped)
+    int64_t bc[kPackItems], g[kPackItems];
+    float mean[kPackItems][3], quat[kPackItems][4], scale[kPackItems][3];
+    float cov[kPackItems][6], opac[kPackItems];
+#pragma unroll
     for (int j = 0; j < kPackItems; ++j) {
-        const int64_t row = base + (int64_t)j * kProjThreads + threadIdx.x;
-        ProjOut o;
-        const bool valid = row < n_rows && project_flat_row(a, row, o);
-        const uint64_t b = __ballot(valid);
-        if (lane == 0)
-            s_ballot[j][wave] = b;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t run = 0;
-        for (int j = 0; j < kPackItems; ++j) {
-            s_slice_off[j] = run;
-            for (int w = 0; w < kProjThreads / kWave; ++w)
-                run += (uint32_t)__popcll(s_ballot[j][w]);
+        const int64_t row = base + (int64_t)j * kPackThreads + threadIdx.x;
+        int64_t bg;
+        split_row(a, row < n_rows ? row : n_rows - 1, bc[j], g[j], bg);
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+            mean[j][k] = a.means[bg * 3 + k];
+        if constexpr (COVARS) {
+#pragma unroll
+            for (int k = 0; k < 6; ++k)
+                cov[j][k] = a.covars[bg * 6 + k];
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                quat[j][k] = a.quats[bg * 4 + k];
+#pragma unroll
+            for (int k = 0; k < 3; ++k)
+                scale[j][k] = a.scales[bg * 3 + k];
         }
-        s_slice_off[kPackItems] = run;
+        opac[j] = a.opacities ? a.opacities[bg] : 0.f;
+    }
+
+    // phase 1: project; the camera is loaded once (scalar loads) when all
+    // rows of the wave belong to one camera row
+    const int64_t bc0 =
+        ((int64_t)__builtin_amdgcn_readfirstlane((int)(bc[0] >> 32)) << 32) |
+        (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)bc[0]);
+    bool mixed = false;
+#pragma unroll
+    for (int j = 0; j < kPackItems; ++j)
+        mixed |= bc[j] != bc0;
+    const bool one_cam = !__ballot(mixed);
+    Cam cam0;
+    if (one_cam) {
+        load_cam(a.viewmats + bc0 * 16, a.Ks + bc0 * 9, cam0);
+        set_fwd_limits(cam0, a.W, a.H);
+    }
+    ProjOut o[kPackItems];
+    uint64_t bal[kPackItems];
+#pragma unroll
+    for (int j = 0; j < kPackItems; ++j) {
+        const int64_t row = base + (int64_t)j * kPackThreads + threadIdx.x;
+        Cam cam;
+        if (one_cam) {
+            cam = cam0;
+        } else {
+            load_cam(a.viewmats + bc[j] * 16, a.Ks + bc[j] * 9, cam);
+            set_fwd_limits(cam, a.W, a.H);
+        }
+        const bool valid =
+            project_exact(cam, mean[j], COVARS ? cov[j] : nullptr,
+                          COVARS ? nullptr : quat[j],
+                          COVARS ? nullptr : scale[j], a.opacities != nullptr,
+                          opac[j], a.calc_comp, a.camera_model, a.W, a.H,
+                          a.eps2d, a.near_plane, a.far_plane, a.radius_clip,
+                          o[j]) &&
+            row < n_rows;
+        bal[j] = __ballot(valid);
+        if (lane == 0)
+            s_cnt[j * NW + wave] = (uint32_t)__popcll(bal[j]);
     }
     __syncthreads();
-    const uint32_t total = s_slice_off[kPackItems];
+    // survivors before each (slice, wave) in row order, and the block's
+    // output offset
     if (wave == 0) {
+        const uint32_t c = s_cnt[lane];
+        const uint32_t inc = (uint32_t)wave_inclusive_scan_u64(c);
+        s_off[lane] = inc - c;
+        const uint32_t total = __shfl(inc, kWave - 1);
         const uint64_t excl = lb_exclusive_prefix(lb, bid, total);
-        if (lane == 0)
+        if (lane == 0) {
             s_prefix = excl;
+            s_total = total;
+        }
     }
     __syncthreads();
     const int64_t block_out = (int64_t)s_prefix;
 
-    // phase 2: recompute the surviving rows (inputs are hot in L2) and write
-    // them at their packed positions
-#pragma unroll 1
+    // phase 2: write the survivors at their packed positions
+#pragma unroll
     for (int j = 0; j < kPackItems; ++j) {
-        const int64_t row = base + (int64_t)j * kProjThreads + threadIdx.x;
+        const int64_t row = base + (int64_t)j * kPackThreads + threadIdx.x;
         if (row >= n_rows)
             break;
-        uint32_t wave_off = 0;
-        for (uint32_t w = 0; w < wave; ++w)
-            wave_off += (uint32_t)__popcll(s_ballot[j][w]);
-        const uint64_t bal = s_ballot[j][wave];
-        const bool valid = (bal >> lane) & 1ull;
-        const int64_t pos = block_out + s_slice_off[j] + wave_off +
-                            (uint32_t)__popcll(bal & lanemask_lt());
-        if (row % a.N == 0) {
+        const bool valid = (bal[j] >> lane) & 1ull;
+        const int64_t pos = block_out + s_off[j * NW + wave] +
+                            (uint32_t)__popcll(bal[j] & lanemask_lt());
+        if (g[j] == 0) {
             // first Gaussian of camera row bc: its exclusive position is indptr
-            indptr[row / a.N] = (int32_t)pos;
+            indptr[bc[j]] = (int32_t)pos;
         }
         if (row_of != nullptr)
             row_of[row] = valid ? (int32_t)pos : -1;
         if (!valid)
             continue;
-        ProjOut o;
-        project_flat_row(a, row, o);
-        const int64_t g = row % a.N;
-        const int64_t bc = row / a.N;
-        batch_ids[pos] = bc / a.C;
-        camera_ids[pos] = bc % a.C;
-        gaussian_ids[pos] = g;
-        reinterpret_cast<int2 *>(radii)[pos] = make_int2(o.rx, o.ry);
-        reinterpret_cast<float2 *>(means2d)[pos] = make_float2(o.mx, o.my);
-        depths[pos] = o.depth;
-        conics[pos * 3 + 0] = o.ca;
-        conics[pos * 3 + 1] = o.cb;
-        conics[pos * 3 + 2] = o.cc;
+        batch_ids[pos] = bc[j] / a.C;
+        camera_ids[pos] = bc[j] % a.C;
+        gaussian_ids[pos] = g[j];
+        reinterpret_cast<int2 *>(radii)[pos] = make_int2(o[j].rx, o[j].ry);
+        reinterpret_cast<float2 *>(means2d)[pos] = make_float2(o[j].mx, o[j].my);
+        depths[pos] = o[j].depth;
+        conics[pos * 3 + 0] = o[j].ca;
+        conics[pos * 3 + 1] = o[j].cb;
+        conics[pos * 3 + 2] = o[j].cc;
         if (compensations != nullptr)
-            compensations[pos] = o.comp;
+            compensations[pos] = o[j].comp;
     }
     const int64_t last_bid = (n_rows - 1) / kPackRows;
     if ((int64_t)bid == last_bid && threadIdx.x == 0) {
-        const int64_t nnz = block_out + total;
+        const int64_t nnz = block_out + s_total;
         indptr[a.B * a.C] = (int32_t)nnz;
         *nnz_out = nnz;
     }
@@ -949,7 +1044,8 @@ extern "C" int gsplat_projection_fused_fwd(
     GS_REQUIRE(radii && means2d && depths && conics, "projection: NULL output");
     FwdArgs a{B, C, N, means, covars, quats, scales, opacities, viewmats, Ks,
               (float)image_width, (float)image_height, eps2d, near_plane,
-              far_plane, radius_clip, camera_model, compensations != nullptr};
+              far_plane, radius_clip, camera_model, compensations != nullptr,
+              rows < (int64_t(1) << 31)};
     projection_fused_fwd_kernel<<<(unsigned)ceil_div(rows, kProjThreads),
                                   kProjThreads, 0, as_stream(stream)>>>(
         a, radii, means2d, depths, conics, compensations);
@@ -990,11 +1086,18 @@ extern "C" int gsplat_projection_packed_fwd(
     GS_TRY(clear_lookback(workspace, blocks, st));
     FwdArgs a{B, C, N, means, covars, quats, scales, opacities, viewmats, Ks,
               (float)image_width, (float)image_height, eps2d, near_plane,
-              far_plane, radius_clip, camera_model, compensations != nullptr};
-    projection_packed_fwd_kernel<<<(unsigned)blocks, kProjThreads, 0, st>>>(
-        a, lookback_from(workspace), indptr, batch_ids, camera_ids,
-        gaussian_ids, radii, means2d, depths, conics, compensations, nnz_out,
-        row_of);
+              far_plane, radius_clip, camera_model, compensations != nullptr,
+              rows < (int64_t(1) << 31)};
+    if (covars != nullptr)
+        projection_packed_fwd_kernel<true><<<(unsigned)blocks, kPackThreads, 0, st>>>(
+            a, lookback_from(workspace), indptr, batch_ids, camera_ids,
+            gaussian_ids, radii, means2d, depths, conics, compensations,
+            nnz_out, row_of);
+    else
+        projection_packed_fwd_kernel<false><<<(unsigned)blocks, kPackThreads, 0, st>>>(
+            a, lookback_from(workspace), indptr, batch_ids, camera_ids,
+            gaussian_ids, radii, means2d, depths, conics, compensations,
+            nnz_out, row_of);
     return check_launch("projection_packed_fwd_kernel");
 }
 

@@ -29,10 +29,10 @@
 // batches once the whole tile is done (__syncthreads_count).
 // The backward runs 16x16 tiles with 128 threads of two pixels each,
 // recovers T back to front in double (one Newton-refined reciprocal per
-// Gaussian), sums a lane's two pixels, reduces each Gaussian's gradient over
-// the wave with branch-free DPP (row butterflies + row broadcasts), adds the
-// two wave sums in LDS and issues one global atomic per value per Gaussian
-// per TILE, 8x fewer than one per 32-lane warp.  Both kernels are compiled per (CDIM, tile size) so every
+// Gaussian), sums a lane's two pixels branch-free, reduces each Gaussian's
+// gradient over every 16-lane row with four DPP butterflies, adds the eight
+// row sums of the tile in LDS (one lane per row) and issues one global atomic
+// per value per Gaussian per TILE, 8x fewer than one per 32-lane warp.  Both kernels are compiled per (CDIM, tile size) so every
 // loop bound and reduction count is a constant.
 #include "common.h"
 
@@ -273,7 +273,9 @@ __global__ void __launch_bounds__(BwdShape<TILE>::THREADS) rasterize_bwd_kernel(
     const int32_t range_end = (image == a.I - 1 && tile == n_tiles - 1)
                                   ? (int32_t)a.n_isects
                                   : offs[tile + 1];
-    const int num_batches = (range_end - range_start + BS - 1) / BS;
+    __shared__ int32_t s_tile_bin;
+    if (tr == 0)
+        s_tile_bin = -1;
 
     // per-pixel state; pixel p of thread tr is (row PX * (tr / TILE) + p,
     // column tr % TILE) of the tile
@@ -317,10 +319,19 @@ __global__ void __launch_bounds__(BwdShape<TILE>::THREADS) rasterize_bwd_kernel(
         v_a[p] = inside[p] ? v_render_alphas[pix] : 0.f;
     }
     const int32_t wave_bin_final = wave_max_i32(wave_bin);
+    // The forward saturates most pixels long before the end of the tile's
+    // range (on dense scenes after a small fraction of it); every Gaussian
+    // behind the tile's last contributor has a zero gradient, so the replay
+    // starts there instead of at the end of the range.
+    __syncthreads();
+    atomicMax(&s_tile_bin, wave_bin);
+    __syncthreads();
+    const int32_t replay_end = min(range_end, s_tile_bin + 1);
+    const int num_batches = max(0, replay_end - range_start + BS - 1) / BS;
 
     for (int b = 0; b < num_batches; ++b) {
         __syncthreads();
-        const int32_t batch_end = range_end - 1 - b * BS;
+        const int32_t batch_end = replay_end - 1 - b * BS;
         const int batch_size = min(BS, batch_end + 1 - range_start);
 #pragma unroll
         for (int q = 0; q < PX; ++q) {
@@ -402,16 +413,19 @@ __global__ void __launch_bounds__(BwdShape<TILE>::THREADS) rasterize_bwd_kernel(
             }
             if (!__ballot(any))
                 continue;
+            // Branch-free over the lane's pixels: an invalid pixel runs the
+            // same arithmetic on sigma = 0 and its contributions are zeroed
+            // through fac and v_sigma, so nothing is carried through
+            // divergent control flow.
             float g[NACC];
 #pragma unroll
             for (int k = 0; k < NACC; ++k)
                 g[k] = 0.f;
 #pragma unroll
             for (int p = 0; p < PX; ++p) {
-                if (!valid[p])
-                    continue;
-                const float vis = portable_expf_nonpos(-sigma[p]);
-                const bool clamped = sigma[p] < con.w;
+                const float sg = valid[p] ? sigma[p] : 0.f;
+                const float vis = portable_expf_nonpos(-sg);
+                const bool clamped = sg < con.w;
                 const float alpha = clamped ? kMaxAlpha : geo.z * vis;
                 // alpha <= 0.99, so 1 - alpha >= 0.01 (the reference's 1e-6
                 // floor never binds)
@@ -420,9 +434,9 @@ __global__ void __launch_bounds__(BwdShape<TILE>::THREADS) rasterize_bwd_kernel(
                 const double d = (double)one_minus;
                 double r = (double)ra;
                 r = __builtin_fma(r, __builtin_fma(-d, r, 1.0), r);
-                T64[p] = T64[p] * r;
+                T64[p] = valid[p] ? T64[p] * r : T64[p];
                 T[p] = (float)T64[p];
-                const float fac = alpha * T[p];
+                const float fac = valid[p] ? alpha * T[p] : 0.f;
                 float v_alpha = 0.f;
 #pragma unroll
                 for (int k = 0; k < CDIM; ++k) {
@@ -434,31 +448,35 @@ __global__ void __launch_bounds__(BwdShape<TILE>::THREADS) rasterize_bwd_kernel(
                 v_alpha += T_final[p] * ra * v_a[p];
                 if (a.backgrounds)
                     v_alpha += -T_final[p] * ra * bg_dot[p];
-                if (!clamped) {
-                    const float v_sigma = -geo.z * vis * v_alpha;
-                    const float gx = v_sigma * (con.x * dx[p] + con.y * dy[p]);
-                    const float gy = v_sigma * (con.y * dx[p] + con.z * dy[p]);
-                    g[0] += gx;
-                    g[1] += gy;
-                    g[2] += 0.5f * v_sigma * dx[p] * dx[p];
-                    g[3] += v_sigma * dx[p] * dy[p];
-                    g[4] += 0.5f * v_sigma * dy[p] * dy[p];
-                    g[5 + CDIM] += vis * v_alpha;
-                    if (ABS) {
-                        g[6 + CDIM] += fabsf(gx);
-                        g[7 + CDIM] += fabsf(gy);
-                    }
+                // a clamped alpha does not depend on the Gaussian's geometry
+                // or opacity
+                const float vv = (valid[p] && !clamped) ? v_alpha : 0.f;
+                const float v_sigma = -geo.z * vis * vv;
+                const float gx = v_sigma * (con.x * dx[p] + con.y * dy[p]);
+                const float gy = v_sigma * (con.y * dx[p] + con.z * dy[p]);
+                g[0] += gx;
+                g[1] += gy;
+                g[2] += 0.5f * v_sigma * dx[p] * dx[p];
+                g[3] += v_sigma * dx[p] * dy[p];
+                g[4] += 0.5f * v_sigma * dy[p] * dy[p];
+                g[5 + CDIM] += vis * vv;
+                if (ABS) {
+                    g[6 + CDIM] += fabsf(gx);
+                    g[7 + CDIM] += fabsf(gy);
                 }
             }
+            // sum over each 16-lane row (every lane of the row ends with the
+            // row's sum); one lane per row adds it to the tile's LDS sums
 #pragma unroll
             for (int k = 0; k < NACC; ++k)
-                g[k] = wave_sum_to_last<SH::ROWS>(g[k]);
-            if (last_lane) {
+                g[k] = row_sum16(g[k]);
+            if ((lane_id() & 15u) == 15u) {
 #pragma unroll
                 for (int k = 0; k < NACC; ++k)
                     atomicAdd(&s_acc[k * BS + t], g[k]);
-                s_hit[t] = 1;
             }
+            if (last_lane)
+                s_hit[t] = 1;
         }
         __syncthreads();
 #pragma unroll
