@@ -158,7 +158,9 @@ __device__ __forceinline__ void sh_basis_grad(float x, float y, float z,
 
 // Copy the coefficient prefix (NB bands) of rows [r0, r0 + nrows) into LDS
 // with pitch PITCH floats per row.  With `vis` (an LDS flag per row), rows
-// whose flag is 0 are not read (their LDS rows are left unset).
+// whose flag is 0 are not read (their LDS rows hold zeros).  Every load
+// of a thread is issued before the first LDS write, so a wave waits for
+// memory once per tile instead of once per 16-byte chunk.
 template <int DEG>
 __device__ __forceinline__ void stage_coeffs(const float *__restrict__ coeffs,
                                              int64_t r0, int nrows, int K,
@@ -171,12 +173,23 @@ __device__ __forceinline__ void stage_coeffs(const float *__restrict__ coeffs,
         const float4 *src =
             reinterpret_cast<const float4 *>(coeffs + r0 * S::ROW);
         const int nvec = total >> 2;
-        for (int v = threadIdx.x; v < nvec; v += kShThreads) {
+        constexpr int NI = (kShThreads * S::ROW / 4 + kShThreads - 1) / kShThreads;
+        // chunks of rows that are not read leave zeros in LDS (never used)
+        float4 q[NI];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int v = (int)threadIdx.x + i * kShThreads;
             const int e = v << 2;
-            if (vis != nullptr && !vis[e / S::ROW] && !vis[(e + 3) / S::ROW])
-                continue;
-            const float4 q = src[v];
-            const float vals[4] = {q.x, q.y, q.z, q.w};
+            const bool take = v < nvec && (vis == nullptr || vis[e / S::ROW] ||
+                                           vis[(e + 3) / S::ROW]);
+            q[i] = take ? src[v] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            if ((int)threadIdx.x + i * kShThreads >= nvec)
+                break;
+            const int e = ((int)threadIdx.x + i * kShThreads) << 2;
+            const float vals[4] = {q[i].x, q[i].y, q[i].z, q[i].w};
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const int ek = e + k;
@@ -191,12 +204,23 @@ __device__ __forceinline__ void stage_coeffs(const float *__restrict__ coeffs,
             s[row * S::PITCH + (e - row * S::ROW)] = coeffs[r0 * S::ROW + e];
         }
     } else {
-        for (int e = threadIdx.x; e < total; e += kShThreads) {
+        constexpr int NI = S::ROW;  // ceil(kShThreads * ROW / kShThreads)
+        float q[NI];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int e = (int)threadIdx.x + i * kShThreads;
             const int row = e / S::ROW;
-            if (vis != nullptr && !vis[row])
-                continue;
-            const int col = e - row * S::ROW;
-            s[row * S::PITCH + col] = coeffs[(r0 + row) * (int64_t)K * 3 + col];
+            const bool take = e < total && (vis == nullptr || vis[row]);
+            q[i] = take ? coeffs[(r0 + row) * (int64_t)K * 3 + (e - row * S::ROW)]
+                        : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            if ((int)threadIdx.x + i * kShThreads >= total)
+                break;
+            const int e = (int)threadIdx.x + i * kShThreads;
+            const int row = e / S::ROW;
+            s[row * S::PITCH + (e - row * S::ROW)] = q[i];
         }
     }
 }
@@ -375,16 +399,28 @@ struct ShRowsArgs {
     bool vec_ok;
 };
 
+// Visibility of the thread's Gaussian (its packed row in camera 0 is
+// returned in *row0), its mean (loaded before the barrier so the load
+// overlaps the visibility round trip), and the workgroup's coefficient tile
+// staged in LDS.
 template <int DEG>
 __device__ __forceinline__ bool sh_rows_prologue(const ShRowsArgs &a,
                                                  int64_t r0, int nrows,
-                                                 float *s_coef, uint8_t *s_vis) {
+                                                 float *s_coef, uint8_t *s_vis,
+                                                 int32_t *row0, float *mean) {
     const int t = threadIdx.x;
     bool vis = false;
+    *row0 = -1;
+    mean[0] = mean[1] = mean[2] = 0.f;
     if (t < nrows) {
         const int64_t bg = r0 + t;
         const int64_t b = bg / a.N, g = bg - b * a.N;
-        for (int64_t c = 0; c < a.C; ++c)
+        mean[0] = a.means[bg * 3 + 0];
+        mean[1] = a.means[bg * 3 + 1];
+        mean[2] = a.means[bg * 3 + 2];
+        *row0 = a.row_of[b * a.C * a.N + g];
+        vis = *row0 >= 0;
+        for (int64_t c = 1; c < a.C; ++c)
             vis |= a.row_of[(b * a.C + c) * a.N + g] >= 0;
     }
     s_vis[t] = vis ? 1 : 0;
@@ -403,17 +439,19 @@ __global__ void __launch_bounds__(kShThreads)
     const int64_t r0 = (int64_t)blockIdx.x * kShThreads;
     const int64_t BN = a.B * a.N;
     const int nrows = (int)((BN - r0) < kShThreads ? (BN - r0) : kShThreads);
-    const bool vis = sh_rows_prologue<DEG>(a, r0, nrows, s_coef, s_vis);
+    int32_t row0;
+    float mean[3];
+    const bool vis =
+        sh_rows_prologue<DEG>(a, r0, nrows, s_coef, s_vis, &row0, mean);
     if (!vis)
         return;
     const int t = threadIdx.x;
     const int64_t bg = r0 + t;
     const int64_t b = bg / a.N, g = bg - b * a.N;
-    const float mx = a.means[bg * 3 + 0], my = a.means[bg * 3 + 1],
-                mz = a.means[bg * 3 + 2];
+    const float mx = mean[0], my = mean[1], mz = mean[2];
     const float *cf = s_coef + t * S::PITCH;
     for (int64_t c = 0; c < a.C; ++c) {
-        const int32_t r = a.row_of[(b * a.C + c) * a.N + g];
+        const int32_t r = c == 0 ? row0 : a.row_of[(b * a.C + c) * a.N + g];
         if (r < 0)
             continue;
         float Y[S::NB];
@@ -449,7 +487,10 @@ __global__ void __launch_bounds__(kShThreads)
     const int64_t r0 = (int64_t)blockIdx.x * kShThreads;
     const int64_t BN = a.B * a.N;
     const int nrows = (int)((BN - r0) < kShThreads ? (BN - r0) : kShThreads);
-    const bool vis = sh_rows_prologue<DEG>(a, r0, nrows, s_buf, s_vis);
+    int32_t row0;
+    float mean[3];
+    const bool vis =
+        sh_rows_prologue<DEG>(a, r0, nrows, s_buf, s_vis, &row0, mean);
     const int t = threadIdx.x;
     const int64_t bg = r0 + t;
     float acc[S::ROW];
@@ -459,11 +500,10 @@ __global__ void __launch_bounds__(kShThreads)
     float vm0 = 0.f, vm1 = 0.f, vm2 = 0.f;
     if (vis) {
         const int64_t b = bg / a.N, g = bg - b * a.N;
-        const float mx = a.means[bg * 3 + 0], my = a.means[bg * 3 + 1],
-                    mz = a.means[bg * 3 + 2];
+        const float mx = mean[0], my = mean[1], mz = mean[2];
         const float *cf = s_buf + t * S::PITCH;
         for (int64_t c = 0; c < a.C; ++c) {
-            const int32_t r = a.row_of[(b * a.C + c) * a.N + g];
+            const int32_t r = c == 0 ? row0 : a.row_of[(b * a.C + c) * a.N + g];
             if (r < 0)
                 continue;
             float Y[S::NB];
@@ -487,9 +527,12 @@ __global__ void __launch_bounds__(kShThreads)
                 o1 += Y[k] * cf[k * 3 + 1];
                 o2 += Y[k] * cf[k * 3 + 2];
             }
-            const float v0 = o0 + 0.5f >= 0.f ? v_colors[(int64_t)r * 3 + 0] : 0.f;
-            const float v1 = o1 + 0.5f >= 0.f ? v_colors[(int64_t)r * 3 + 1] : 0.f;
-            const float v2 = o2 + 0.5f >= 0.f ? v_colors[(int64_t)r * 3 + 2] : 0.f;
+            const float w0 = v_colors[(int64_t)r * 3 + 0];
+            const float w1 = v_colors[(int64_t)r * 3 + 1];
+            const float w2 = v_colors[(int64_t)r * 3 + 2];
+            const float v0 = o0 + 0.5f >= 0.f ? w0 : 0.f;
+            const float v1 = o1 + 0.5f >= 0.f ? w1 : 0.f;
+            const float v2 = o2 + 0.5f >= 0.f ? w2 : 0.f;
 #pragma unroll
             for (int k = 0; k < S::NB; ++k) {
                 acc[k * 3 + 0] += Y[k] * v0;
