@@ -207,6 +207,31 @@ __device__ __forceinline__ float wave_sum_to_last(float v) {
     return v;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave (all lanes active):
+// Kogge-Stone within each 16-lane row (row_shr 1, 2, 4, 8; sources outside
+// the row read 0), then row broadcasts 15 and 31 carry the row totals.
+__device__ __forceinline__ uint32_t wave_inclusive_scan_u32(uint32_t v) {
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, false);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, false);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, false);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false);
+    return v;
+}
+
+// Inclusive running maximum over the 64 lanes of a wave (all lanes active)
+// for values >= -1 (-1 is the identity), same pattern as the sum scan.
+__device__ __forceinline__ int wave_inclusive_max_i32(int v) {
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x111, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x112, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x114, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x118, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x142, 0xA, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x143, 0xC, 0xF, false));
+    return v;
+}
+
 template <int CTRL> __device__ __forceinline__ float dpp_f32(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(
         0, __float_as_int(v), CTRL, 0xF, 0xF, false));
@@ -315,6 +340,7 @@ int radix_sort_ping_pong(int64_t n, int begin_bit, int end_bit, uint64_t *keys_a
                          uint32_t *vals_a, uint64_t *keys_b, uint32_t *vals_b,
                          void *workspace, size_t workspace_bytes,
                          hipStream_t st, bool *result_in_b);
+int copy_u32(int64_t n, const uint32_t *src, uint32_t *dst, hipStream_t st);
 int copy_pairs(int64_t n, const uint64_t *ks, const uint32_t *vs, uint64_t *kd,
                uint32_t *vd, hipStream_t st);
 // Exclusive prefix sum of n uint32 values; `ws` holds a look-back workspace

@@ -73,33 +73,59 @@ __device__ __forceinline__ void ellipse_line(float A, float B, float C,
     hi = (mbh + sq) / coeff + p_v;
 }
 
-// Number of tiles touched by one row; emits them when `em` is non-null.
-template <bool EMIT>
-__device__ __forceinline__ int32_t row_tiles(const IsectArgs &a, int64_t idx,
-                                             Emitter *em) {
+// Per-row state of the ellipse ("AccuTile") column sweep, or of the
+// axis-aligned box when no conics/opacities are given.  After the axis swap
+// (isY), columns u in [rmin_x, rmax_x) are swept along x and each column
+// covers rows v in [v0, v1) of tiles.
+struct Sweep {
+    bool accu, isY;
+    bool pow2;     // tile size is a power of two: x / ts == x * inv_ts exactly
+    float A, B, C, disc, t, mx, my, ts, inv_ts;
+    float bmin_x, bmax_x, bmin_y, bmax_y, amin_y, amax_y;
+    int rmin_x, rmax_x, rmin_y, rmax_y;
+};
+
+// x / ts, as a multiplication when ts is a power of two (both give the
+// correctly rounded x / ts).
+__device__ __forceinline__ float div_ts(const Sweep &sw, float x) {
+    return sw.pow2 ? x * sw.inv_ts : x / sw.ts;
+}
+
+// Opacity-derived squared extent of the ellipse level set (the sweep's t).
+__device__ __forceinline__ float sweep_extent(float opacity) {
 #pragma clang fp contract(off)
-    const int2 r = reinterpret_cast<const int2 *>(a.radii)[idx];
-    const float radius_x = (float)r.x;
-    const float radius_y = (float)r.y;
+    return fminf(kGaussianExtend * kGaussianExtend,
+                 2.0f * portable_logf(opacity / kAlphaThreshold));
+}
+
+// Fills *sw from one row's values (mean, conic A B C and extent t for the
+// ellipse sweep, integer radii for both); returns false when the row
+// touches no tile.
+__device__ __forceinline__ bool sweep_setup_vals(const IsectArgs &a, float mx,
+                                                 float my, float A, float B,
+                                                 float C, float t,
+                                                 float radius_x, float radius_y,
+                                                 Sweep *sw) {
+#pragma clang fp contract(off)
     if (radius_x <= 0.f || radius_y <= 0.f)
-        return 0;
-    const float2 mean = reinterpret_cast<const float2 *>(a.means2d)[idx];
+        return false;
+    const float2 mean = make_float2(mx, my);
     const int tw = a.tile_width, th = a.tile_height;
     const float ts = (float)a.tile_size;
+    sw->ts = ts;
+    sw->pow2 = (a.tile_size & (a.tile_size - 1)) == 0;
+    sw->inv_ts = 1.f / ts;
+    sw->mx = mean.x;
+    sw->my = mean.y;
 
     if (a.conics != nullptr && a.opacities != nullptr) {
-        const float A = a.conics[idx * 3 + 0];
-        const float B = a.conics[idx * 3 + 1];
-        const float C = a.conics[idx * 3 + 2];
+        sw->accu = true;
         const float disc = B * B - A * C;
-        const float opacity = a.opacities[idx];
-        const float t = fminf(kGaussianExtend * kGaussianExtend,
-                              2.0f * portable_logf(opacity / kAlphaThreshold));
         // Guard: the level set is empty unless t >= 0 and the conic is
         // positive definite (disc < 0); the reference reaches 0 tiles in these
         // cases through NaN extents, here they are made explicit.
         if (!(t >= 0.f) || !(disc < 0.f))
-            return 0;
+            return false;
         const float nt = (-t) / disc;
         const float x_ext = sqrtf(nt * C);
         const float y_ext = sqrtf(nt * A);
@@ -110,14 +136,14 @@ __device__ __forceinline__ int32_t row_tiles(const IsectArgs &a, int64_t idx,
         // argmin/argmax: (.x = y where x is extreme, .y = x where y is extreme)
         float amin_x = mean.y + bx_over_c, amin_y = mean.x + by_over_a;
         float amax_x = mean.y - bx_over_c, amax_y = mean.x - by_over_a;
-        int rmin_x = imax(0, imin(tw, sat_f2i(bmin_x / ts)));
-        int rmin_y = imax(0, imin(th, sat_f2i(bmin_y / ts)));
-        int rmax_x = imax(0, imin(tw, sat_f2i(bmax_x / ts + 1.f)));
-        int rmax_y = imax(0, imin(th, sat_f2i(bmax_y / ts + 1.f)));
+        int rmin_x = imax(0, imin(tw, sat_f2i(div_ts(*sw, bmin_x))));
+        int rmin_y = imax(0, imin(th, sat_f2i(div_ts(*sw, bmin_y))));
+        int rmax_x = imax(0, imin(tw, sat_f2i(div_ts(*sw, bmax_x) + 1.f)));
+        int rmax_y = imax(0, imin(th, sat_f2i(div_ts(*sw, bmax_y) + 1.f)));
         const int y_span = rmax_y - rmin_y;
         const int x_span = rmax_x - rmin_x;
         if (y_span == 0 || x_span == 0)
-            return 0;
+            return false;
         const bool isY = y_span < x_span;
         if (isY) {
             // sweep along y: swap the roles of the axes
@@ -130,64 +156,239 @@ __device__ __forceinline__ int32_t row_tiles(const IsectArgs &a, int64_t idx,
             tf = amin_x; amin_x = amin_y; amin_y = tf;
             tf = amax_x; amax_x = amax_y; amax_y = tf;
         }
-        int32_t count = 0;
-        // (lo, hi) roots at the previous and current line
-        float max_lo = bmax_y, max_hi = bmin_y;
-        float min_lo, min_hi;
-        float min_line = (float)rmin_x * ts;
-        if (bmin_x <= min_line) {
-            ellipse_line(A, B, C, disc, t, mean.x, mean.y, isY, min_line,
-                         min_lo, min_hi);
-        } else {
-            min_lo = max_lo;
-            min_hi = max_hi;
-        }
-        for (int u = rmin_x; u < rmax_x; ++u) {
-            const float max_line = min_line + ts;
-            if (max_line <= bmax_x)
-                ellipse_line(A, B, C, disc, t, mean.x, mean.y, isY, max_line,
-                             max_lo, max_hi);
-            float e_min, e_max;
-            if (min_line <= amin_y && amin_y < max_line)
-                e_min = bmin_y;
-            else
-                e_min = fminf(min_lo, max_lo);
-            if (min_line <= amax_y && amax_y < max_line)
-                e_max = bmax_y;
-            else
-                e_max = fmaxf(min_hi, max_hi);
-            const int v0 = imax(rmin_y, imin(rmax_y, sat_f2i(e_min / ts)));
-            const int v1 = imin(rmax_y, imax(rmin_y, sat_f2i(e_max / ts + 1.f)));
-            if (v1 > v0) {
-                count += v1 - v0;
-                if (EMIT) {
-                    for (int v = v0; v < v1; ++v) {
-                        const int64_t tile =
-                            isY ? (int64_t)u * tw + v : (int64_t)v * tw + u;
-                        em->put(tile);
-                    }
-                }
-            }
-            min_lo = max_lo;
-            min_hi = max_hi;
-            min_line = max_line;
-        }
-        return count;
+        sw->isY = isY;
+        sw->A = A;
+        sw->B = B;
+        sw->C = C;
+        sw->disc = disc;
+        sw->t = t;
+        sw->bmin_x = bmin_x;
+        sw->bmax_x = bmax_x;
+        sw->bmin_y = bmin_y;
+        sw->bmax_y = bmax_y;
+        sw->amin_y = amin_y;
+        sw->amax_y = amax_y;
+        sw->rmin_x = rmin_x;
+        sw->rmax_x = rmax_x;
+        sw->rmin_y = rmin_y;
+        sw->rmax_y = rmax_y;
+        return true;
     }
 
-    // axis-aligned box of the integer radii
-    const float trx = radius_x / ts, try_ = radius_y / ts;
-    const float tx = mean.x / ts, ty = mean.y / ts;
-    const int x0 = imin(imax(0, sat_f2i(floorf(tx - trx))), tw);
-    const int y0 = imin(imax(0, sat_f2i(floorf(ty - try_))), th);
-    const int x1 = imin(imax(0, sat_f2i(ceilf(tx + trx))), tw);
-    const int y1 = imin(imax(0, sat_f2i(ceilf(ty + try_))), th);
-    if (EMIT) {
-        for (int y = y0; y < y1; ++y)
-            for (int x = x0; x < x1; ++x)
-                em->put((int64_t)y * tw + x);
+    // axis-aligned box of the integer radii; "columns" are tile rows y, each
+    // covering tiles x in [x0, x1)
+    sw->accu = false;
+    sw->isY = true;
+    const float trx = div_ts(*sw, radius_x), try_ = div_ts(*sw, radius_y);
+    const float tx = div_ts(*sw, mean.x), ty = div_ts(*sw, mean.y);
+    sw->rmin_y = imin(imax(0, sat_f2i(floorf(tx - trx))), tw);
+    sw->rmin_x = imin(imax(0, sat_f2i(floorf(ty - try_))), th);
+    sw->rmax_y = imin(imax(0, sat_f2i(ceilf(tx + trx))), tw);
+    sw->rmax_x = imin(imax(0, sat_f2i(ceilf(ty + try_))), th);
+    return sw->rmax_y > sw->rmin_y && sw->rmax_x > sw->rmin_x;
+}
+
+// The row's values from the row arrays.
+__device__ __forceinline__ bool sweep_setup(const IsectArgs &a, int64_t idx,
+                                            Sweep *sw) {
+    const int2 r = reinterpret_cast<const int2 *>(a.radii)[idx];
+    const float2 mean = reinterpret_cast<const float2 *>(a.means2d)[idx];
+    float A = 0.f, B = 0.f, C = 0.f, t = 0.f;
+    if (a.conics != nullptr && a.opacities != nullptr) {
+        A = a.conics[idx * 3 + 0];
+        B = a.conics[idx * 3 + 1];
+        C = a.conics[idx * 3 + 2];
+        t = sweep_extent(a.opacities[idx]);
     }
-    return (y1 - y0) * (x1 - x0);
+    return sweep_setup_vals(a, mean.x, mean.y, A, B, C, t, (float)r.x,
+                            (float)r.y, sw);
+}
+
+// One row packed in 32 bytes for the depth-ordered emission: (mean, A, B),
+// (C, t, depth bits, image id) -- t < 0 when a radius is not positive, so the
+// sweep sees no tile -- or, for the box, (mean, radii), (0, 0, depth bits,
+// image id).
+struct alignas(16) RowRec {
+    float4 p, q;
+};
+
+__device__ __forceinline__ RowRec row_record(const IsectArgs &a, int64_t idx) {
+    const int2 r = reinterpret_cast<const int2 *>(a.radii)[idx];
+    const float2 mean = reinterpret_cast<const float2 *>(a.means2d)[idx];
+    const int64_t iid = a.image_ids != nullptr ? a.image_ids[idx] : idx / a.N;
+    const float dbits = a.depths[idx];
+    RowRec rec;
+    if (a.conics != nullptr && a.opacities != nullptr) {
+        const float t = (r.x > 0 && r.y > 0) ? sweep_extent(a.opacities[idx]) : -1.f;
+        rec.p = make_float4(mean.x, mean.y, a.conics[idx * 3 + 0], a.conics[idx * 3 + 1]);
+        rec.q = make_float4(a.conics[idx * 3 + 2], t, dbits, __int_as_float((int)iid));
+    } else {
+        rec.p = make_float4(mean.x, mean.y, (float)r.x, (float)r.y);
+        rec.q = make_float4(0.f, 0.f, dbits, __int_as_float((int)iid));
+    }
+    return rec;
+}
+
+__device__ __forceinline__ bool sweep_setup_rec(const IsectArgs &a,
+                                                const RowRec &rec, Sweep *sw) {
+    if (a.conics != nullptr && a.opacities != nullptr)
+        return sweep_setup_vals(a, rec.p.x, rec.p.y, rec.p.z, rec.p.w, rec.q.x,
+                                rec.q.y, 1.f, 1.f, sw);
+    return sweep_setup_vals(a, rec.p.x, rec.p.y, 0.f, 0.f, 0.f, 0.f, rec.p.z,
+                            rec.p.w, sw);
+}
+
+// Tile rows [v0, v1) of column u from the roots at its two lines.
+__device__ __forceinline__ void sweep_span(const Sweep &sw, float min_line,
+                                           float max_line, float min_lo,
+                                           float min_hi, float max_lo,
+                                           float max_hi, int &v0, int &v1) {
+#pragma clang fp contract(off)
+    float e_min, e_max;
+    if (min_line <= sw.amin_y && sw.amin_y < max_line)
+        e_min = sw.bmin_y;
+    else
+        e_min = fminf(min_lo, max_lo);
+    if (min_line <= sw.amax_y && sw.amax_y < max_line)
+        e_max = sw.bmax_y;
+    else
+        e_max = fmaxf(min_hi, max_hi);
+    v0 = imax(sw.rmin_y, imin(sw.rmax_y, sat_f2i(div_ts(sw, e_min))));
+    v1 = imin(sw.rmax_y, imax(sw.rmin_y, sat_f2i(div_ts(sw, e_max) + 1.f)));
+}
+
+__device__ __forceinline__ void sweep_roots(const Sweep &sw, float line,
+                                            float &lo, float &hi) {
+    ellipse_line(sw.A, sw.B, sw.C, sw.disc, sw.t, sw.mx, sw.my, sw.isY, line,
+                 lo, hi);
+}
+
+// Tile id of (column u, row v) of the sweep.
+__device__ __forceinline__ int64_t sweep_tile(const Sweep &sw, int tw, int u,
+                                              int v) {
+    return sw.isY ? (int64_t)u * tw + v : (int64_t)v * tw + u;
+}
+
+// Number of tiles touched by one row; emits them (column by column, rows v
+// ascending) when EMIT.  The sweep carries the roots of the previous line
+// from column to column (IntersectTile.cu:38-121).
+template <bool EMIT>
+__device__ __forceinline__ int32_t sweep_tiles(const IsectArgs &a,
+                                               const Sweep &sw, Emitter *em) {
+#pragma clang fp contract(off)
+    const int tw = a.tile_width;
+    if (!sw.accu) {
+        if (EMIT) {
+            for (int y = sw.rmin_x; y < sw.rmax_x; ++y)
+                for (int x = sw.rmin_y; x < sw.rmax_y; ++x)
+                    em->put((int64_t)y * tw + x);
+        }
+        return (sw.rmax_x - sw.rmin_x) * (sw.rmax_y - sw.rmin_y);
+    }
+    const float ts = sw.ts;
+    int32_t count = 0;
+    // (lo, hi) roots at the previous and current line
+    float max_lo = sw.bmax_y, max_hi = sw.bmin_y;
+    float min_lo, min_hi;
+    float min_line = (float)sw.rmin_x * ts;
+    if (sw.bmin_x <= min_line) {
+        sweep_roots(sw, min_line, min_lo, min_hi);
+    } else {
+        min_lo = max_lo;
+        min_hi = max_hi;
+    }
+    for (int u = sw.rmin_x; u < sw.rmax_x; ++u) {
+        const float max_line = min_line + ts;
+        if (max_line <= sw.bmax_x)
+            sweep_roots(sw, max_line, max_lo, max_hi);
+        int v0, v1;
+        sweep_span(sw, min_line, max_line, min_lo, min_hi, max_lo, max_hi, v0, v1);
+        if (v1 > v0) {
+            count += v1 - v0;
+            if (EMIT) {
+                for (int v = v0; v < v1; ++v)
+                    em->put(sweep_tile(sw, tw, u, v));
+            }
+        }
+        min_lo = max_lo;
+        min_hi = max_hi;
+        min_line = max_line;
+    }
+    return count;
+}
+
+template <bool EMIT>
+__device__ __forceinline__ int32_t row_tiles(const IsectArgs &a, int64_t idx,
+                                             Emitter *em) {
+    Sweep sw;
+    if (!sweep_setup(a, idx, &sw))
+        return 0;
+    return sweep_tiles<EMIT>(a, sw, em);
+}
+
+// The last column j in [rmin_x - 1, rmax_x - 1] whose right line
+// (j + 1) * ts lies at or left of bmax_x (rmin_x - 1: none).  Lines are
+// exact integers in float, so they equal the sweep's running sums.
+__device__ __forceinline__ int sweep_last_line(const Sweep &sw) {
+#pragma clang fp contract(off)
+    int lo = sw.rmin_x - 1, hi = sw.rmax_x - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if ((float)(mid + 1) * sw.ts <= sw.bmax_x)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    return lo;
+}
+
+// Column u of the sweep evaluated on its own, with the sweep's carried state
+// in closed form: the roots a column ends with are those of the last line
+// j + 1 <= min(u, J) + 1 evaluated so far (J = sweep_last_line), or the
+// initial (bmax_y, bmin_y) when none was; a column starts with the previous
+// column's, and the first column with its own left line when bmin_x lies at
+// or left of it.  Gives exactly the [v0, v1) of row_tiles.
+__device__ __forceinline__ void sweep_column(const Sweep &sw, int J, int u,
+                                             int &v0, int &v1) {
+#pragma clang fp contract(off)
+    const float ts = sw.ts;
+    if (!sw.accu) {
+        v0 = sw.rmin_y;
+        v1 = sw.rmax_y;
+        return;
+    }
+    const float min_line = (float)u * ts;
+    const float max_line = (float)(u + 1) * ts;
+    float min_lo, min_hi, max_lo, max_hi;
+    // roots the column ends with
+    const int je = u < J ? u : J;
+    if (je >= sw.rmin_x) {
+        sweep_roots(sw, (float)(je + 1) * ts, max_lo, max_hi);
+    } else {
+        max_lo = sw.bmax_y;
+        max_hi = sw.bmin_y;
+    }
+    // roots the column starts with
+    if (u == sw.rmin_x) {
+        if (sw.bmin_x <= min_line) {
+            sweep_roots(sw, min_line, min_lo, min_hi);
+        } else {
+            min_lo = sw.bmax_y;
+            min_hi = sw.bmin_y;
+        }
+    } else {
+        const int js = (u - 1) < J ? (u - 1) : J;
+        if (js == je) {
+            min_lo = max_lo;
+            min_hi = max_hi;
+        } else if (js >= sw.rmin_x) {
+            sweep_roots(sw, (float)(js + 1) * ts, min_lo, min_hi);
+        } else {
+            min_lo = sw.bmax_y;
+            min_hi = sw.bmin_y;
+        }
+    }
+    sweep_span(sw, min_line, max_line, min_lo, min_hi, max_lo, max_hi, v0, v1);
 }
 
 __global__ void __launch_bounds__(kIsectThreads)
@@ -267,26 +468,32 @@ __global__ void __launch_bounds__(kIsectThreads)
 __global__ void __launch_bounds__(kIsectThreads)
     isect_count_keys_kernel(const IsectArgs a, int32_t *__restrict__ tiles_per_gauss,
                             uint64_t *__restrict__ depth_keys,
-                            uint32_t *__restrict__ rows) {
+                            uint32_t *__restrict__ rows,
+                            RowRec *__restrict__ recs) {
     const int64_t idx = (int64_t)blockIdx.x * kIsectThreads + threadIdx.x;
     if (idx >= a.n)
         return;
-    tiles_per_gauss[idx] = row_tiles<false>(a, idx, nullptr);
-    depth_keys[idx] = (uint64_t)__float_as_uint(a.depths[idx]);
+    const RowRec rec = row_record(a, idx);
+    recs[idx] = rec;
+    Sweep sw;
+    tiles_per_gauss[idx] =
+        sweep_setup_rec(a, rec, &sw) ? sweep_tiles<false>(a, sw, nullptr) : 0;
+    depth_keys[idx] = (uint64_t)__float_as_uint(rec.q.z);
     rows[idx] = (uint32_t)idx;
 }
 
 constexpr int kScanItemsPerThread = 16;
 constexpr int kScanBlockRows = kIsectThreads * kScanItemsPerThread;
 
-// For the depth order `order` (rows, depth ascending): each row's first slot
-// in the depth-ordered emission, row_start[order[i]] = sum_{i' < i}
-// tiles_per_gauss[order[i']], and the total (n_isects).  Blocks of 4096
-// entries (16 consecutive per thread) chained by decoupled look-back.
+// For the depth order `order` (rows, depth ascending): the first slot of
+// every depth position in the depth-ordered emission, dstart[i] =
+// sum_{i' < i} tiles_per_gauss[order[i']], dstart[n] = n_isects (also
+// written to *n_isects_out).  Blocks of 4096 entries (16 consecutive per
+// thread) chained by decoupled look-back.
 __global__ void __launch_bounds__(kIsectThreads)
     depth_order_starts_kernel(int64_t n, const uint32_t *__restrict__ order,
                               const int32_t *__restrict__ tiles_per_gauss,
-                              Lookback lb, int64_t *__restrict__ row_start,
+                              Lookback lb, int64_t *__restrict__ dstart,
                               int64_t *__restrict__ n_isects_out) {
     __shared__ uint32_t s_ticket;
     __shared__ uint64_t s_wave_tot[kIsectThreads / kWave];
@@ -326,41 +533,248 @@ __global__ void __launch_bounds__(kIsectThreads)
 #pragma unroll
     for (int k = 0; k < kScanItemsPerThread; ++k) {
         if (i0 + k < n)
-            row_start[rows[k]] = (int64_t)run;
+            dstart[i0 + k] = (int64_t)run;
         run += cnt[k];
     }
-    if (i0 < n && i0 + kScanItemsPerThread >= n)
-        *n_isects_out = (int64_t)run;  // the thread holding the last entry
+    if (i0 < n && i0 + kScanItemsPerThread >= n) {
+        // the thread holding the last entry
+        dstart[n] = (int64_t)run;
+        *n_isects_out = (int64_t)run;
+    }
 }
 
-// Row-order emission (the rows' own order spreads the rows with many tiles
-// over the launch), each row written at its slots of the depth-ordered
-// layout.
+// Depth-ordered emission.  The rows in depth order own consecutive slot
+// ranges (the depth-ordered prefix dstart of their counts); the slots are cut
+// into chunks of kEmitSlots and each wave writes one chunk, front to back,
+// with consecutive lanes on consecutive slots:
+//   1. the rows that overlap the chunk (from chunk_first, 64 per batch) set
+//      up their sweeps (kept in LDS);
+//   2. their columns, in (row, column) order, are evaluated one per lane
+//      (sweep_column), giving one segment -- an arithmetic run of tile ids --
+//      per column, kEmitCols columns at a time; a column finds its row the
+//      same way (rows mark their first column, running maximum);
+//   3. the chunk's slots are expanded tile by tile: every segment reaching
+//      into the chunk marks its first slot there and a running maximum over
+//      the slots (DPP scan) gives each slot its segment.
+// Every wave writes the same number of slots whatever the rows' tile counts
+// (1 to thousands: a large row is shared by the waves of its chunks), and
+// every store is coalesced.  The layout equals that of row_tiles<true>
+// (column by column, rows v ascending) at each row's depth-ordered slots.
+constexpr int kEmitWaves = kIsectThreads / kWave;
+constexpr int kEmitCols = 4 * kWave;   // segments per batch (4 per lane)
+constexpr int kEmitSlots = 4 * kWave;  // slots per wave
+enum { kRowA, kRowB, kRowC, kRowDisc, kRowT, kRowMx, kRowMy, kRowBminX,
+       kRowBmaxX, kRowBminY, kRowBmaxY, kRowAminY, kRowAmaxY, kRowFloats };
+enum { kRowRminX, kRowRmaxX, kRowRminY, kRowRmaxY, kRowJ, kRowFlags,
+       kRowFlat, kRowInts };
+
+// chunk_first[c] = the depth position whose slot range holds slot
+// c * kEmitSlots (rows without tiles own no slot).
 __global__ void __launch_bounds__(kIsectThreads)
-    isect_emit_at_kernel(const IsectArgs a, const int32_t *__restrict__ tiles_per_gauss,
-                         const int64_t *__restrict__ row_start,
-                         uint64_t *__restrict__ isect_ids,
-                         uint32_t *__restrict__ flatten_ids) {
-    const int64_t idx = (int64_t)blockIdx.x * kIsectThreads + threadIdx.x;
-    if (idx >= a.n)
+    emit_chunk_first_kernel(int64_t n, const int64_t *__restrict__ dstart,
+                            int32_t *__restrict__ chunk_first) {
+    const int64_t i = (int64_t)blockIdx.x * kIsectThreads + threadIdx.x;
+    if (i >= n)
         return;
-    const int32_t count = tiles_per_gauss[idx];
-    if (count == 0)
+    const int64_t lo = dstart[i], hi = dstart[i + 1];
+    for (int64_t c = (lo + kEmitSlots - 1) / kEmitSlots; c * kEmitSlots < hi; ++c)
+        chunk_first[c] = (int32_t)i;
+}
+
+__global__ void __launch_bounds__(kIsectThreads)
+    isect_emit_depth_kernel(const IsectArgs a,
+                            const uint32_t *__restrict__ order,
+                            const int64_t *__restrict__ dstart,
+                            const RowRec *__restrict__ recs,
+                            const int32_t *__restrict__ chunk_first,
+                            int64_t n_isects, uint64_t *__restrict__ isect_ids,
+                            uint32_t *__restrict__ flatten_ids) {
+    __shared__ float s_f[kEmitWaves][kRowFloats][kWave];
+    __shared__ int32_t s_i[kEmitWaves][kRowInts][kWave];
+    __shared__ uint64_t s_key[kEmitWaves][kWave];
+    __shared__ int32_t s_colpre[kEmitWaves][kWave + 1];
+    __shared__ int32_t s_first[kEmitWaves][kEmitCols];
+    __shared__ int32_t s_meta[kEmitWaves][kEmitCols];
+    __shared__ int32_t s_start[kEmitWaves][kEmitCols];
+    __shared__ int32_t s_own[kEmitWaves][kEmitCols > kEmitSlots ? kEmitCols : kEmitSlots];
+
+    const int wave = threadIdx.x / kWave;
+    const int lane = (int)lane_id();
+    const int64_t chunk = (int64_t)blockIdx.x * kEmitWaves + wave;
+    const int64_t S = chunk * kEmitSlots;
+    if (S >= n_isects)
         return;
-    Emitter em;
-    em.isect_ids = reinterpret_cast<int64_t *>(isect_ids);
-    em.flatten_ids = reinterpret_cast<int32_t *>(flatten_ids);
-    em.cursor = row_start[idx];
-    em.end = em.cursor + count;
-    const int64_t iid = a.image_ids != nullptr ? a.image_ids[idx] : idx / a.N;
-    em.key_hi = iid << (32 + a.tile_n_bits);
-    em.depth_lo = (int64_t)(uint64_t)__float_as_uint(a.depths[idx]);
-    em.flat = (int32_t)idx;
-    row_tiles<true>(a, idx, &em);
+    const int64_t E = n_isects < S + kEmitSlots ? n_isects : S + kEmitSlots;
+    const int tw = a.tile_width;
+    const float ts = (float)a.tile_size;
+    const float inv_ts = 1.f / ts;
+    const bool pow2 = (a.tile_size & (a.tile_size - 1)) == 0;
+
+    for (int64_t pb = chunk_first[chunk]; pb < a.n; pb += kWave) {
+        const int64_t base = dstart[pb];  // first slot of the batch
+        if (base >= E)
+            break;
+        // 1. rows of the batch that start before the chunk's end
+        const int64_t p = pb + lane;
+        Sweep sw;
+        bool has = false;
+        if (p < a.n && dstart[p] < E) {
+            const int64_t row = order[p];
+            const RowRec rec = recs[row];
+            has = sweep_setup_rec(a, rec, &sw);
+            if (has) {
+                float *f = &s_f[wave][0][lane];
+                f[kRowA * kWave] = sw.A;
+                f[kRowB * kWave] = sw.B;
+                f[kRowC * kWave] = sw.C;
+                f[kRowDisc * kWave] = sw.disc;
+                f[kRowT * kWave] = sw.t;
+                f[kRowMx * kWave] = sw.mx;
+                f[kRowMy * kWave] = sw.my;
+                f[kRowBminX * kWave] = sw.bmin_x;
+                f[kRowBmaxX * kWave] = sw.bmax_x;
+                f[kRowBminY * kWave] = sw.bmin_y;
+                f[kRowBmaxY * kWave] = sw.bmax_y;
+                f[kRowAminY * kWave] = sw.amin_y;
+                f[kRowAmaxY * kWave] = sw.amax_y;
+                int32_t *q = &s_i[wave][0][lane];
+                q[kRowRminX * kWave] = sw.rmin_x;
+                q[kRowRmaxX * kWave] = sw.rmax_x;
+                q[kRowRminY * kWave] = sw.rmin_y;
+                q[kRowRmaxY * kWave] = sw.rmax_y;
+                q[kRowJ * kWave] = sw.accu ? sweep_last_line(sw) : 0;
+                q[kRowFlags * kWave] = (sw.accu ? 1 : 0) | (sw.isY ? 2 : 0);
+                q[kRowFlat * kWave] = (int32_t)row;
+                const uint64_t iid = (uint32_t)__float_as_int(rec.q.w);
+                s_key[wave][lane] = (iid << (32 + a.tile_n_bits)) |
+                                    (uint64_t)__float_as_uint(rec.q.z);
+            }
+        }
+        const int ncols = has ? sw.rmax_x - sw.rmin_x : 0;
+        const int col_incl = (int)wave_inclusive_scan_u32((uint32_t)ncols);
+        s_colpre[wave][lane + 1] = col_incl;
+        if (lane == 0)
+            s_colpre[wave][0] = 0;
+        const int total_cols = __shfl(col_incl, kWave - 1);
+        __builtin_amdgcn_wave_barrier();
+
+        int64_t seg_base = base;  // first slot of the current column batch
+        for (int cb = 0; cb < total_cols && seg_base < E; cb += kEmitCols) {
+            const int nseg =
+                total_cols - cb < kEmitCols ? total_cols - cb : kEmitCols;
+            // owner row of every column of the batch: each row marks its
+            // first column in the batch, a running maximum fills the rest
+#pragma unroll
+            for (int q = 0; q < kEmitCols / kWave; ++q)
+                s_own[wave][q * kWave + lane] = -1;
+            __builtin_amdgcn_wave_barrier();
+            if (ncols > 0) {
+                const int lo = col_incl - ncols, hi = col_incl;
+                if (lo < cb + nseg && hi > cb)
+                    s_own[wave][(lo > cb ? lo : cb) - cb] = lane;
+            }
+            __builtin_amdgcn_wave_barrier();
+            // 2. segments: column cb + 64 q + lane, slice by slice
+            int batch_total = 0;
+            int row_carry = -1;
+            int starts[kEmitCols / kWave], lens[kEmitCols / kWave];
+#pragma unroll
+            for (int q = 0; q < kEmitCols / kWave; ++q) {
+                const int k = q * kWave + lane;  // segment index in the batch
+                starts[q] = 0;
+                lens[q] = 0;
+                if (q * kWave >= nseg)
+                    continue;
+                const int r = max(wave_inclusive_max_i32(s_own[wave][k]), row_carry);
+                row_carry = __shfl(r, kWave - 1);
+                int len = 0;
+                if (k < nseg) {
+                    const int c = cb + k;
+                    Sweep cs;
+                    const float *f = &s_f[wave][0][r];
+                    cs.A = f[kRowA * kWave];
+                    cs.B = f[kRowB * kWave];
+                    cs.C = f[kRowC * kWave];
+                    cs.disc = f[kRowDisc * kWave];
+                    cs.t = f[kRowT * kWave];
+                    cs.mx = f[kRowMx * kWave];
+                    cs.my = f[kRowMy * kWave];
+                    cs.bmin_x = f[kRowBminX * kWave];
+                    cs.bmax_x = f[kRowBmaxX * kWave];
+                    cs.bmin_y = f[kRowBminY * kWave];
+                    cs.bmax_y = f[kRowBmaxY * kWave];
+                    cs.amin_y = f[kRowAminY * kWave];
+                    cs.amax_y = f[kRowAmaxY * kWave];
+                    cs.ts = ts;
+                    cs.inv_ts = inv_ts;
+                    cs.pow2 = pow2;
+                    const int32_t *qi = &s_i[wave][0][r];
+                    cs.rmin_x = qi[kRowRminX * kWave];
+                    cs.rmax_x = qi[kRowRmaxX * kWave];
+                    cs.rmin_y = qi[kRowRminY * kWave];
+                    cs.rmax_y = qi[kRowRmaxY * kWave];
+                    const int flags = qi[kRowFlags * kWave];
+                    cs.accu = flags & 1;
+                    cs.isY = (flags >> 1) & 1;
+                    const int u = cs.rmin_x + (c - s_colpre[wave][r]);
+                    int v0, v1;
+                    sweep_column(cs, qi[kRowJ * kWave], u, v0, v1);
+                    len = v1 > v0 ? v1 - v0 : 0;
+                    s_first[wave][k] = (int32_t)sweep_tile(cs, tw, u, v0);
+                    s_meta[wave][k] = r | (cs.isY ? 0x100 : 0);
+                }
+                const int incl = (int)wave_inclusive_scan_u32((uint32_t)len);
+                starts[q] = batch_total + incl - len;
+                lens[q] = len;
+                if (k < nseg)
+                    s_start[wave][k] = starts[q];
+                batch_total += __shfl(incl, kWave - 1);
+            }
+            // 3. the chunk's slots: owner segment of every slot of [S, E)
+            // (each segment that reaches into the chunk marks its first slot
+            // there, a running maximum fills the rest)
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int q = 0; q < kEmitSlots / kWave; ++q)
+                s_own[wave][q * kWave + lane] = -1;
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int q = 0; q < kEmitCols / kWave; ++q) {
+                if (lens[q] > 0) {
+                    const int64_t lo = seg_base + starts[q];
+                    const int64_t hi = lo + lens[q];
+                    if (lo < E && hi > S)
+                        s_own[wave][(int)((lo > S ? lo : S) - S)] = q * kWave + lane;
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+            const int64_t seg_end = seg_base + batch_total;
+            int seg_carry = -1;
+#pragma unroll
+            for (int q = 0; q < kEmitSlots / kWave; ++q) {
+                const int i = q * kWave + lane;
+                const int sk = max(wave_inclusive_max_i32(s_own[wave][i]), seg_carry);
+                seg_carry = __shfl(sk, kWave - 1);
+                const int64_t slot = S + i;
+                if (sk >= 0 && slot < E && slot < seg_end) {
+                    const int meta = s_meta[wave][sk];
+                    const int r = meta & 0xFF;
+                    const int off = (int)(slot - seg_base) - s_start[wave][sk];
+                    const uint32_t tile =
+                        (uint32_t)s_first[wave][sk] +
+                        (uint32_t)off * ((meta & 0x100) ? 1u : (uint32_t)tw);
+                    isect_ids[slot] = s_key[wave][r] | ((uint64_t)tile << 32);
+                    flatten_ids[slot] = (uint32_t)s_i[wave][kRowFlat][r];
+                }
+            }
+            seg_base += batch_total;
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
 }
 
 struct PrepLayout {
-    size_t keys_a, keys_b, vals_a, vals_b, lookback, sort_ws, total;
+    size_t keys_a, keys_b, vals_b, lookback, sort_ws, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) / 256 * 256; }
@@ -370,23 +784,23 @@ PrepLayout prep_layout(int64_t n) {
     const size_t k = align256((size_t)n * 8), v = align256((size_t)n * 4);
     L.keys_a = 0;
     L.keys_b = k;
-    L.vals_a = 2 * k;
-    L.vals_b = 2 * k + v;
-    L.lookback = 2 * k + 2 * v;
+    L.vals_b = 2 * k;
+    L.lookback = 2 * k + v;
     L.sort_ws = L.lookback + align256(lookback_bytes(ceil_div(n, kScanBlockRows)));
     L.total = L.sort_ws + radix_sort_workspace_bytes(n);
     return L;
 }
 
 struct EmitLayout {
-    size_t keys, vals, sort_ws, total;
+    size_t keys, vals, chunks, sort_ws, total;
 };
 
 EmitLayout emit_layout(int64_t n_isects) {
     EmitLayout L;
     L.keys = 0;
     L.vals = align256((size_t)n_isects * 8);
-    L.sort_ws = L.vals + align256((size_t)n_isects * 4);
+    L.chunks = L.vals + align256((size_t)n_isects * 4);
+    L.sort_ws = L.chunks + align256((size_t)ceil_div(n_isects, kEmitSlots) * 4);
     L.total = L.sort_ws + radix_sort_workspace_bytes(n_isects);
     return L;
 }
@@ -560,7 +974,8 @@ extern "C" int gsplat_isect_prepare(int64_t n, int64_t N, const int64_t *image_i
                                     const float *opacities, int32_t tile_size,
                                     int32_t tile_width, int32_t tile_height,
                                     void *workspace, size_t workspace_bytes,
-                                    int32_t *tiles_per_gauss, int64_t *row_start,
+                                    int32_t *tiles_per_gauss, int32_t *depth_order,
+                                    int64_t *depth_starts, float *row_records,
                                     int64_t *n_isects_out, gsplat_stream_t stream) {
     clear_error();
     IsectArgs a;
@@ -568,8 +983,11 @@ extern "C" int gsplat_isect_prepare(int64_t n, int64_t N, const int64_t *image_i
                      opacities, tile_size, tile_width, tile_height, a));
     if (n == 0)
         return GSPLAT_OK;
-    GS_REQUIRE(depths && tiles_per_gauss && row_start && n_isects_out,
+    GS_REQUIRE(depths && tiles_per_gauss && depth_order && depth_starts &&
+                   row_records && n_isects_out,
                "isect_prepare: NULL buffer");
+    GS_REQUIRE(reinterpret_cast<uintptr_t>(row_records) % 16 == 0,
+               "isect_prepare: row_records must be 16-byte aligned");
     GS_REQUIRE(n < (1ll << 31), "isect_prepare: more than 2^31 rows");
     const PrepLayout L = prep_layout(n);
     GS_REQUIRE(workspace && workspace_bytes >= L.total,
@@ -577,22 +995,23 @@ extern "C" int gsplat_isect_prepare(int64_t n, int64_t N, const int64_t *image_i
     char *ws = reinterpret_cast<char *>(workspace);
     uint64_t *keys_a = reinterpret_cast<uint64_t *>(ws + L.keys_a);
     uint64_t *keys_b = reinterpret_cast<uint64_t *>(ws + L.keys_b);
-    uint32_t *vals_a = reinterpret_cast<uint32_t *>(ws + L.vals_a);
+    uint32_t *vals_a = reinterpret_cast<uint32_t *>(depth_order);
     uint32_t *vals_b = reinterpret_cast<uint32_t *>(ws + L.vals_b);
     hipStream_t st = as_stream(stream);
     const unsigned grid = (unsigned)ceil_div(n, kIsectThreads);
-    isect_count_keys_kernel<<<grid, kIsectThreads, 0, st>>>(a, tiles_per_gauss,
-                                                             keys_a, vals_a);
+    isect_count_keys_kernel<<<grid, kIsectThreads, 0, st>>>(
+        a, tiles_per_gauss, keys_a, vals_a, reinterpret_cast<RowRec *>(row_records));
     GS_TRY(check_launch("isect_count_keys_kernel"));
     bool in_b = false;
     GS_TRY(radix_sort_ping_pong(n, 0, 32, keys_a, vals_a, keys_b, vals_b,
                                 ws + L.sort_ws, workspace_bytes - L.sort_ws, st,
                                 &in_b));
-    const uint32_t *order = in_b ? vals_b : vals_a;
+    if (in_b)
+        GS_TRY(copy_u32(n, vals_b, vals_a, st));
     const int64_t scan_blocks = ceil_div(n, kScanBlockRows);
     GS_TRY(clear_lookback(ws + L.lookback, scan_blocks, st));
     depth_order_starts_kernel<<<(unsigned)scan_blocks, kIsectThreads, 0, st>>>(
-        n, order, tiles_per_gauss, lookback_from(ws + L.lookback), row_start,
+        n, vals_a, tiles_per_gauss, lookback_from(ws + L.lookback), depth_starts,
         n_isects_out);
     return check_launch("depth_order_starts_kernel");
 }
@@ -605,8 +1024,9 @@ extern "C" int gsplat_isect_emit_sorted(
     int64_t n, int64_t N, int64_t I, const int64_t *image_ids,
     const float *means2d, const int32_t *radii, const float *depths,
     const float *conics, const float *opacities, int32_t tile_size,
-    int32_t tile_width, int32_t tile_height, const int32_t *tiles_per_gauss,
-    const int64_t *row_start, int64_t n_isects, void *workspace,
+    int32_t tile_width, int32_t tile_height, const int32_t *depth_order,
+    const int64_t *depth_starts, const float *row_records, int64_t n_isects,
+    void *workspace,
     size_t workspace_bytes, int64_t *isect_ids, int32_t *flatten_ids,
     gsplat_stream_t stream) {
     clear_error();
@@ -616,8 +1036,11 @@ extern "C" int gsplat_isect_emit_sorted(
     GS_REQUIRE(n_isects >= 0, "isect_emit_sorted: negative n_isects");
     if (n == 0 || n_isects == 0)
         return GSPLAT_OK;
-    GS_REQUIRE(depths && tiles_per_gauss && row_start && isect_ids && flatten_ids,
+    GS_REQUIRE(depths && depth_order && depth_starts && row_records && isect_ids &&
+                   flatten_ids,
                "isect_emit_sorted: NULL buffer");
+    GS_REQUIRE(reinterpret_cast<uintptr_t>(row_records) % 16 == 0,
+               "isect_emit_sorted: row_records must be 16-byte aligned");
     GS_REQUIRE(I > 0, "isect_emit_sorted: I must be positive");
     const int ib = bit_length(I);
     GS_REQUIRE(ib + a.tile_n_bits <= 32,
@@ -637,9 +1060,17 @@ extern "C" int gsplat_isect_emit_sorted(
     uint64_t *ka = odd ? tmp_keys : out_keys, *kb = odd ? out_keys : tmp_keys;
     uint32_t *va = odd ? tmp_vals : out_vals, *vb = odd ? out_vals : tmp_vals;
     hipStream_t st = as_stream(stream);
-    isect_emit_at_kernel<<<(unsigned)ceil_div(n, kIsectThreads), kIsectThreads,
-                           0, st>>>(a, tiles_per_gauss, row_start, ka, va);
-    GS_TRY(check_launch("isect_emit_at_kernel"));
+    int32_t *chunk_first = reinterpret_cast<int32_t *>(ws + L.chunks);
+    emit_chunk_first_kernel<<<(unsigned)ceil_div(n, kIsectThreads), kIsectThreads,
+                              0, st>>>(n, depth_starts, chunk_first);
+    GS_TRY(check_launch("emit_chunk_first_kernel"));
+    const int64_t chunks = ceil_div(n_isects, kEmitSlots);
+    isect_emit_depth_kernel<<<(unsigned)ceil_div(chunks, kEmitWaves),
+                              kIsectThreads, 0, st>>>(
+        a, reinterpret_cast<const uint32_t *>(depth_order), depth_starts,
+        reinterpret_cast<const RowRec *>(row_records), chunk_first, n_isects, ka,
+        va);
+    GS_TRY(check_launch("isect_emit_depth_kernel"));
     bool in_b = false;
     GS_TRY(radix_sort_ping_pong(n_isects, 32, end_bit, ka, va, kb, vb,
                                 ws + L.sort_ws, workspace_bytes - L.sort_ws, st,

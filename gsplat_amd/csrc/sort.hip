@@ -5,7 +5,8 @@
 // (gsplat/cuda/csrc/IntersectTile.cu:478-520): keys are sorted on a bit range,
 // ties keep their input order.
 //
-// Per pass (digit of up to 8 bits, 4096-key tiles):
+// Per pass (digit of up to 8 bits, 1024-key tiles up to 2M keys, 2048-key
+// tiles above):
 //   1. radix_hist_kernel    digit counts per tile with LDS atomics, written
 //                           tile-major (coalesced);
 //   2. radix_colscan_kernel one workgroup per digit scans that digit's count
@@ -26,8 +27,14 @@ namespace {
 
 constexpr int kSortThreads = 256;
 constexpr int kSortWaves = kSortThreads / kWave;
-constexpr int kSortItems = 16;
-constexpr int kSortTile = kSortThreads * kSortItems;  // keys per workgroup
+// Keys per thread of a tile: short tiles (more workgroups, shorter serial
+// ranking chains) for small sorts, longer ones for large sorts.
+constexpr int kSortItemsSmall = 4;   // 1024-key tiles
+constexpr int kSortItemsLarge = 8;   // 2048-key tiles
+constexpr int64_t kSortSmallMax = 1ll << 21;
+inline int sort_items(int64_t n) {
+    return n <= kSortSmallMax ? kSortItemsSmall : kSortItemsLarge;
+}
 constexpr int kDigitBits = 8;
 constexpr int kRadix = 1 << kDigitBits;
 
@@ -52,7 +59,7 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d, int bits,
 __device__ __forceinline__ uint32_t block_exclusive_u32(uint32_t v,
                                                         uint32_t *s_wave,
                                                         uint32_t *total) {
-    const uint32_t incl = (uint32_t)wave_inclusive_scan_u64(v);
+    const uint32_t incl = wave_inclusive_scan_u32(v);
     const int w = threadIdx.x / kWave;
     if (lane_id() == kWave - 1)
         s_wave[w] = incl;
@@ -68,10 +75,13 @@ __device__ __forceinline__ uint32_t block_exclusive_u32(uint32_t v,
     return off + incl - v;
 }
 
-// Digit counts of one 4096-key tile, block-major: hist[tile * 256 + d].
+// Digit counts of one tile, block-major: hist[tile * 256 + d].
+template <int ITEMS>
 __global__ void __launch_bounds__(kSortThreads)
     radix_hist_kernel(const uint64_t *__restrict__ keys, int64_t n, int shift,
                       int bits, uint32_t *__restrict__ hist) {
+    constexpr int kSortItems = ITEMS;
+    constexpr int kSortTile = kSortThreads * ITEMS;
     __shared__ uint32_t s_cnt[kSortWaves][kRadix];
     const uint32_t mask = (1u << bits) - 1u;
     for (int i = threadIdx.x; i < kSortWaves * kRadix; i += kSortThreads)
@@ -79,11 +89,17 @@ __global__ void __launch_bounds__(kSortThreads)
     __syncthreads();
     const int w = threadIdx.x / kWave;
     const int64_t base = (int64_t)blockIdx.x * kSortTile + (int64_t)w * kWave * kSortItems;
-#pragma unroll 4
+    uint64_t kk[kSortItems];
+#pragma unroll
+    for (int j = 0; j < kSortItems; ++j) {
+        const int64_t i = base + (int64_t)j * kWave + lane_id();
+        kk[j] = i < n ? keys[i] : 0ull;
+    }
+#pragma unroll
     for (int j = 0; j < kSortItems; ++j) {
         const int64_t i = base + (int64_t)j * kWave + lane_id();
         if (i < n)
-            atomicAdd(&s_cnt[w][(uint32_t)(keys[i] >> shift) & mask], 1u);
+            atomicAdd(&s_cnt[w][(uint32_t)(kk[j] >> shift) & mask], 1u);
     }
     __syncthreads();
     const int d = threadIdx.x;  // kSortThreads == kRadix
@@ -119,10 +135,11 @@ __global__ void __launch_bounds__(kSortThreads)
         totals[d] = total;
 }
 
-// Stable scatter of one 4096-key tile: ranks come from wave64 match ballots
+// Stable scatter of one tile: ranks come from wave64 match ballots
 // (order: wave, item, lane = input order), the tile is reordered by digit in
 // LDS, then every digit run is written out with consecutive threads on
 // consecutive addresses.
+template <int ITEMS>
 __global__ void __launch_bounds__(kSortThreads)
     radix_scatter_kernel(const uint64_t *__restrict__ keys_in,
                          const uint32_t *__restrict__ vals_in,
@@ -130,6 +147,8 @@ __global__ void __launch_bounds__(kSortThreads)
                          uint32_t *__restrict__ vals_out, int64_t n, int shift,
                          int bits, const uint32_t *__restrict__ prefix,
                          const uint32_t *__restrict__ totals) {
+    constexpr int kSortItems = ITEMS;
+    constexpr int kSortTile = kSortThreads * ITEMS;
     __shared__ uint64_t s_keys[kSortTile];
     __shared__ uint32_t s_vals[kSortTile];
     __shared__ uint32_t s_cnt[kSortWaves][kRadix];
@@ -278,6 +297,13 @@ __global__ void copy_pairs_kernel(const uint64_t *__restrict__ ks,
     }
 }
 
+__global__ void copy_u32_kernel(const uint32_t *__restrict__ src,
+                                uint32_t *__restrict__ dst, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n)
+        dst[i] = src[i];
+}
+
 struct SortLayout {
     int64_t n_tiles;
     size_t hist_off, prefix_off, totals_off, total;
@@ -285,7 +311,7 @@ struct SortLayout {
 
 SortLayout sort_layout(int64_t n) {
     SortLayout L;
-    L.n_tiles = ceil_div(n > 0 ? n : 1, kSortTile);
+    L.n_tiles = ceil_div(n > 0 ? n : 1, (int64_t)kSortThreads * sort_items(n));
     const size_t tbytes = ((size_t)L.n_tiles * kRadix * 4 + 255) / 256 * 256;
     L.hist_off = 0;
     L.prefix_off = tbytes;
@@ -328,14 +354,23 @@ int radix_sort_ping_pong(int64_t n, int begin_bit, int end_bit, uint64_t *keys_a
     for (int p = 0; p < passes; ++p) {
         const int remaining = end_bit - shift;
         const int bits = (remaining + (passes - p) - 1) / (passes - p);
-        radix_hist_kernel<<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
-            ksrc, n, shift, bits, hist);
+        const bool small = sort_items(n) == kSortItemsSmall;
+        if (small)
+            radix_hist_kernel<kSortItemsSmall><<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
+                ksrc, n, shift, bits, hist);
+        else
+            radix_hist_kernel<kSortItemsLarge><<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
+                ksrc, n, shift, bits, hist);
         GS_TRY(check_launch("radix_hist_kernel"));
         radix_colscan_kernel<<<kRadix, kSortThreads, 0, st>>>(hist, L.n_tiles,
                                                               prefix, totals);
         GS_TRY(check_launch("radix_colscan_kernel"));
-        radix_scatter_kernel<<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
-            ksrc, vsrc, kdst, vdst, n, shift, bits, prefix, totals);
+        if (small)
+            radix_scatter_kernel<kSortItemsSmall><<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
+                ksrc, vsrc, kdst, vdst, n, shift, bits, prefix, totals);
+        else
+            radix_scatter_kernel<kSortItemsLarge><<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
+                ksrc, vsrc, kdst, vdst, n, shift, bits, prefix, totals);
         GS_TRY(check_launch("radix_scatter_kernel"));
         shift += bits;
         uint64_t *tk = ksrc; ksrc = kdst; kdst = tk;
@@ -351,6 +386,13 @@ int copy_pairs(int64_t n, const uint64_t *ks, const uint32_t *vs, uint64_t *kd,
         return GSPLAT_OK;
     copy_pairs_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(ks, vs, kd, vd, n);
     return check_launch("copy_pairs_kernel");
+}
+
+int copy_u32(int64_t n, const uint32_t *src, uint32_t *dst, hipStream_t st) {
+    if (n == 0)
+        return GSPLAT_OK;
+    copy_u32_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(src, dst, n);
+    return check_launch("copy_u32_kernel");
 }
 
 // Exclusive scan used by other translation units of the library.

@@ -428,14 +428,17 @@ def intersect_tile(
         # stable sort on the image|tile bits only: the reference's full-key
         # order (a per-image segmented sort, segmented=True, is the same order
         # because the image id occupies the top key bits).
-        row_start = torch.empty(n, dtype=_I64, device=dev)
+        depth_order = torch.empty(n, dtype=_I32, device=dev)
+        depth_starts = torch.empty(n + 1, dtype=_I64, device=dev)
+        records = torch.empty(n, 8, dtype=_F32, device=dev)
         total = torch.empty(1, dtype=_I64, device=dev)
         ws = torch.empty(query("gsplat_isect_prepare_workspace_size", n),
                          dtype=torch.uint8, device=dev)
         call("gsplat_isect_prepare", n, N, ptr(img), ptr(means2d), ptr(radii),
              ptr(depths), ptr(conics), ptr(opacities), int(tile_size),
              int(tile_width), int(tile_height), ptr(ws), ws.numel(),
-             ptr(tiles_per_gauss), ptr(row_start), ptr(total), st)
+             ptr(tiles_per_gauss), ptr(depth_order), ptr(depth_starts), ptr(records),
+             ptr(total), st)
         n_isects = int(total.item())
         isect_ids = torch.empty(n_isects, dtype=_I64, device=dev)
         flatten_ids = torch.empty(n_isects, dtype=_I32, device=dev)
@@ -445,8 +448,8 @@ def intersect_tile(
                           dtype=torch.uint8, device=dev)
         call("gsplat_isect_emit_sorted", n, N, int(I), ptr(img), ptr(means2d),
              ptr(radii), ptr(depths), ptr(conics), ptr(opacities), int(tile_size),
-             int(tile_width), int(tile_height), ptr(tiles_per_gauss), ptr(row_start),
-             n_isects, ptr(ews), ews.numel(), ptr(isect_ids), ptr(flatten_ids), st)
+             int(tile_width), int(tile_height), ptr(depth_order), ptr(depth_starts),
+             ptr(records), n_isects, ptr(ews), ews.numel(), ptr(isect_ids), ptr(flatten_ids), st)
         return tiles_per_gauss, isect_ids, flatten_ids
     cum = torch.empty(n, dtype=_I64, device=dev)
     ws = torch.empty(query("gsplat_isect_count_workspace_size", n),

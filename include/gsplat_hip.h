@@ -262,10 +262,13 @@ int gsplat_isect_emit(
 
 /* Sorted intersection, stage 1 of 2.  Counts the tiles of every row
  * (tiles_per_gauss [n]), orders the rows stably by their depth bits (ties by
- * row) and gives every row its first slot in that order: row_start [n]
- * int64 = the tile count of all rows before it in depth order.  The total
- * (n_isects) goes to n_isects_out (device int64).  Same row/camera arguments
- * as gsplat_isect_count.
+ * row) -- depth_order [n] int32,
+ * the rows in that order -- and gives every depth position its first slot:
+ * depth_starts [n + 1] int64, the tile count of all rows before it in depth
+ * order (depth_starts[n] = n_isects, also written to n_isects_out, device
+ * int64) -- and packs every row's sweep inputs into row_records [n, 8] float
+ * (16-byte aligned) for stage 2.  Same row/camera arguments as
+ * gsplat_isect_count.
  * Together with stage 2 this replaces intersect_tile with sort=True
  *   (gsplat/cuda/csrc/Intersect.cpp:33-164: count, cumsum, emit, and the
  *    full-key radix sort of IntersectTile.cu:478-520). */
@@ -275,22 +278,26 @@ int gsplat_isect_prepare(
     const float *means2d, const int32_t *radii, const float *depths,
     const float *conics, const float *opacities,
     int32_t tile_size, int32_t tile_width, int32_t tile_height,
-    void *workspace, size_t workspace_bytes,
-    int32_t *tiles_per_gauss, int64_t *row_start, int64_t *n_isects_out,
-    gsplat_stream_t stream);
+    void *workspace, size_t workspace_bytes, int32_t *tiles_per_gauss,
+    int32_t *depth_order, int64_t *depth_starts, float *row_records,
+    int64_t *n_isects_out, gsplat_stream_t stream);
 
-/* Sorted intersection, stage 2 of 2.  Writes every row's intersections at
- * its row_start (stage 1), which lays them out in depth order, then sorts
- * them stably on the image|tile key bits only.  The result equals the reference's full-key stable sort of the
- * row-order emission bit for bit: isect_ids [n_isects] ascending, ties (same
- * image, tile and depth bits) by row; flatten_ids [n_isects] the rows. */
+/* Sorted intersection, stage 2 of 2.  Writes the intersections of the rows
+ * in depth order (depth_order, depth_starts, row_records from stage 1) --
+ * every row's
+ * tiles at its depth-ordered slots -- then sorts them stably on the
+ * image|tile key bits only.  The result equals the reference's full-key
+ * stable sort of the row-order emission bit for bit: isect_ids [n_isects]
+ * ascending, ties (same image, tile and depth bits) by row; flatten_ids
+ * [n_isects] the rows. */
 size_t gsplat_isect_emit_sorted_workspace_size(int64_t n_isects);
 int gsplat_isect_emit_sorted(
     int64_t n, int64_t N, int64_t I, const int64_t *image_ids,
     const float *means2d, const int32_t *radii, const float *depths,
     const float *conics, const float *opacities,
     int32_t tile_size, int32_t tile_width, int32_t tile_height,
-    const int32_t *tiles_per_gauss, const int64_t *row_start, int64_t n_isects,
+    const int32_t *depth_order, const int64_t *depth_starts,
+    const float *row_records, int64_t n_isects,
     void *workspace, size_t workspace_bytes,
     int64_t *isect_ids, int32_t *flatten_ids, gsplat_stream_t stream);
 
