@@ -792,16 +792,32 @@ __device__ __forceinline__ void flush_viewmat_grad(float *v_viewmat,
 }
 
 __global__ void __launch_bounds__(kProjThreads)
-    projection_fused_bwd_kernel(const BwdArgs a, const int32_t *__restrict__ radii) {
+    projection_fused_bwd_kernel(const BwdArgs a, const int32_t *__restrict__ radii,
+                                const int32_t *__restrict__ row_of) {
     __shared__ float s_red[(kProjThreads / kWave) * 12];
-    // one thread per (b, g); loops over the C cameras
+    // one thread per (b, g); loops over the C cameras.  The rows are the
+    // dense (b, c, g) rows (visible when both radii are positive) or, with
+    // row_of, the packed rows row_of[(b C + c) N + g] (visible when >= 0).
     const int64_t bg = (int64_t)blockIdx.x * kProjThreads + threadIdx.x;
     const bool in_range = bg < a.B * a.N;
     const int64_t b = in_range ? bg / a.N : 0;
     const int64_t g = in_range ? bg % a.N : 0;
 
+    // the geometry is only read for Gaussians visible in some camera
+    bool seen = false;
+    if (in_range) {
+        for (int64_t c = 0; c < a.C && !seen; ++c) {
+            const int64_t row = (b * a.C + c) * a.N + g;
+            if (row_of != nullptr) {
+                seen = row_of[row] >= 0;
+            } else {
+                const int2 r = reinterpret_cast<const int2 *>(radii)[row];
+                seen = r.x > 0 && r.y > 0;
+            }
+        }
+    }
     GaussGeom G;
-    if (in_range)
+    if (seen)
         load_geom(a.covars ? a.covars + bg * 6 : nullptr,
                   a.quats ? a.quats + bg * 4 : nullptr,
                   a.scales ? a.scales + bg * 3 : nullptr, G);
@@ -823,11 +839,16 @@ __global__ void __launch_bounds__(kProjThreads)
             v_R.m[i] = 0.f;
         bool active = false;
         int64_t bc = b * a.C + c;
-        if (in_range) {
-            const int64_t row = bc * a.N + g;
-            const int2 r = reinterpret_cast<const int2 *>(radii)[row];
-            if (r.x > 0 && r.y > 0) {
-                active = true;
+        if (seen) {
+            int64_t row = bc * a.N + g;
+            if (row_of != nullptr) {
+                row = row_of[row];
+                active = row >= 0;
+            } else {
+                const int2 r = reinterpret_cast<const int2 *>(radii)[row];
+                active = r.x > 0 && r.y > 0;
+            }
+            if (active) {
                 Cam cam;
                 load_cam(a.viewmats + bc * 16, a.Ks + bc * 9, cam);
                 const bool has_comp = a.v_compensations != nullptr;
@@ -837,8 +858,8 @@ __global__ void __launch_bounds__(kProjThreads)
                     has_comp ? a.compensations[row] : 0.f,
                     has_comp ? a.v_compensations[row] : 0.f,
                     a.v_means2d[row * 2], a.v_means2d[row * 2 + 1],
-                    a.v_depths[row], a.v_conics + row * 3, v_mean, v_S,
-                    want_cam, v_R, v_t);
+                    a.v_depths != nullptr ? a.v_depths[row] : 0.f,
+                    a.v_conics + row * 3, v_mean, v_S, want_cam, v_R, v_t);
             }
         }
         if (want_cam) {
@@ -866,9 +887,26 @@ __global__ void __launch_bounds__(kProjThreads)
     }
     if (!in_range)
         return;
-    a.v_means[bg * 3 + 0] = v_mean[0];
-    a.v_means[bg * 3 + 1] = v_mean[1];
-    a.v_means[bg * 3 + 2] = v_mean[2];
+    if (a.v_means != nullptr) {
+        a.v_means[bg * 3 + 0] = v_mean[0];
+        a.v_means[bg * 3 + 1] = v_mean[1];
+        a.v_means[bg * 3 + 2] = v_mean[2];
+    }
+    if (!seen) {
+        // visible in no camera: zero gradient rows
+        if (a.covars != nullptr) {
+            if (a.v_covars != nullptr)
+                for (int k = 0; k < 6; ++k)
+                    a.v_covars[bg * 6 + k] = 0.f;
+        } else {
+            if (a.v_quats != nullptr)
+                reinterpret_cast<float4 *>(a.v_quats)[bg] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (a.v_scales != nullptr)
+                for (int k = 0; k < 3; ++k)
+                    a.v_scales[bg * 3 + k] = 0.f;
+        }
+        return;
+    }
     if (a.covars != nullptr) {
         if (a.v_covars != nullptr) {
             float *d = a.v_covars + bg * 6;
@@ -1128,8 +1166,37 @@ extern "C" int gsplat_projection_fused_bwd(
               v_compensations, v_means, v_covars, v_quats, v_scales,
               v_viewmats};
     projection_fused_bwd_kernel<<<(unsigned)ceil_div(B * N, kProjThreads),
-                                  kProjThreads, 0, as_stream(stream)>>>(a,
-                                                                        radii);
+                                  kProjThreads, 0, as_stream(stream)>>>(
+        a, radii, nullptr);
+    return check_launch("projection_fused_bwd_kernel");
+}
+
+extern "C" int gsplat_projection_packed_bwd_rows(
+    int64_t B, int64_t C, int64_t N, const float *means, const float *covars,
+    const float *quats, const float *scales, const float *viewmats,
+    const float *Ks, int32_t image_width, int32_t image_height, float eps2d,
+    int32_t camera_model, const int32_t *row_of, const float *conics,
+    const float *compensations, const float *v_means2d, const float *v_depths,
+    const float *v_conics, const float *v_compensations, float *v_means,
+    float *v_covars, float *v_quats, float *v_scales, float *v_viewmats,
+    gsplat_stream_t stream) {
+    clear_error();
+    GS_TRY(check_common(B, C, N, means, covars, quats, scales, viewmats, Ks,
+                        image_width, image_height, camera_model));
+    if (B * N == 0)
+        return GSPLAT_OK;
+    GS_REQUIRE(row_of && conics && v_means2d && v_conics,
+               "projection_packed_bwd_rows: NULL buffer");
+    GS_REQUIRE(v_compensations == nullptr || compensations != nullptr,
+               "projection_packed_bwd_rows: v_compensations needs compensations");
+    BwdArgs a{B, C, N, means, covars, quats, scales, viewmats, Ks,
+              (float)image_width, (float)image_height, eps2d, camera_model,
+              conics, compensations, v_means2d, v_depths, v_conics,
+              v_compensations, v_means, v_covars, v_quats, v_scales,
+              v_viewmats};
+    projection_fused_bwd_kernel<<<(unsigned)ceil_div(B * N, kProjThreads),
+                                  kProjThreads, 0, as_stream(stream)>>>(
+        a, nullptr, row_of);
     return check_launch("projection_fused_bwd_kernel");
 }
 

@@ -316,7 +316,8 @@ __global__ void __launch_bounds__(BwdShape<TILE>::THREADS) rasterize_bwd_kernel(
             if (a.backgrounds)
                 bg_dot[p] += a.backgrounds[image * CDIM + k] * v_c[p][k];
         }
-        v_a[p] = inside[p] ? v_render_alphas[pix] : 0.f;
+        v_a[p] = (inside[p] && v_render_alphas != nullptr) ? v_render_alphas[pix]
+                                                           : 0.f;
     }
     const int32_t wave_bin_final = wave_max_i32(wave_bin);
     // The forward saturates most pixels long before the end of the tile's
@@ -606,7 +607,7 @@ extern "C" int gsplat_rasterize_bwd(
     if (I == 0 || n_isects == 0)
         return GSPLAT_OK;
     GS_REQUIRE((render_alphas || render_transmittance) && last_ids &&
-                   v_render_colors && v_render_alphas,
+                   v_render_colors,
                "rasterize_bwd: NULL input");
     GS_REQUIRE(v_means2d && v_conics && v_colors && v_opacities,
                "rasterize_bwd: NULL gradient output");

@@ -324,6 +324,50 @@ def projection_ewa_3dgs_packed_bwd(
     return v_means, v_covars, v_quats, v_scales, v_viewmats
 
 
+def projection_packed_bwd_rows(
+    means: Tensor,
+    covars: Optional[Tensor],
+    quats: Optional[Tensor],
+    scales: Optional[Tensor],
+    viewmats: Tensor,
+    Ks: Tensor,
+    image_width: int,
+    image_height: int,
+    eps2d: float,
+    camera_model: int,
+    row_of: Tensor,
+    conics: Tensor,
+    compensations: Optional[Tensor],
+    v_means2d: Tensor,
+    v_depths: Optional[Tensor],
+    v_conics: Tensor,
+    v_compensations: Optional[Tensor],
+    viewmats_requires_grad: bool,
+):
+    """Dense gradients of the packed projection from its row map ``row_of``
+    (one pass driven by Gaussian; no zero fill, no atomics).  ``v_depths``
+    may be None (zero gradient)."""
+    _check_proj_inputs(means, covars, quats, scales, None, viewmats, Ks)
+    check_input(row_of, "row_of", _I32)
+    for t, n in ((conics, "conics"), (v_means2d, "v_means2d"), (v_depths, "v_depths"),
+                 (v_conics, "v_conics"), (compensations, "compensations"),
+                 (v_compensations, "v_compensations")):
+        check_input(t, n)
+    batch_dims, B, C, N = _proj_dims(means, viewmats)
+    v_means = torch.empty_like(means)
+    v_covars = torch.empty_like(covars) if covars is not None else None
+    v_quats = torch.empty_like(quats) if covars is None else None
+    v_scales = torch.empty_like(scales) if covars is None else None
+    v_viewmats = torch.zeros_like(viewmats) if viewmats_requires_grad else None
+    call("gsplat_projection_packed_bwd_rows", B, C, N, ptr(means), ptr(covars),
+         ptr(quats), ptr(scales), ptr(viewmats), ptr(Ks), int(image_width),
+         int(image_height), float(eps2d), int(camera_model), ptr(row_of),
+         ptr(conics), ptr(compensations), ptr(v_means2d), ptr(v_depths),
+         ptr(v_conics), ptr(v_compensations), ptr(v_means), ptr(v_covars),
+         ptr(v_quats), ptr(v_scales), ptr(v_viewmats), _stream(means))
+    return v_means, v_covars, v_quats, v_scales, v_viewmats
+
+
 # --------------------------------------------------------------------------
 # Packed rows driven by Gaussian (replace the gathers / index_put scatters of
 # the packed path, rendering.py:95-213, 782, 845-873)
@@ -577,12 +621,13 @@ def rasterize_to_pixels_3dgs_bwd(
     render_alphas: Tensor,
     last_ids: Tensor,
     v_render_colors: Tensor,
-    v_render_alphas: Tensor,
+    v_render_alphas: Optional[Tensor],
     absgrad: bool,
     render_transmittance: Optional[Tensor] = None,
 ):
     """``render_transmittance`` (not part of the reference schema) is the
-    forward's per-pixel T; without it T is taken as 1 - render_alphas."""
+    forward's per-pixel T; without it T is taken as 1 - render_alphas.
+    ``v_render_alphas`` may be None (zero)."""
     image_dims, I, n_rows, tw, th = _raster_common(
         means2d, conics, colors, opacities, backgrounds, masks, tile_offsets,
         flatten_ids)
@@ -592,11 +637,14 @@ def rasterize_to_pixels_3dgs_bwd(
     check_input(v_render_alphas, "v_render_alphas", _F32)
     check_input(render_transmittance, "render_transmittance", _F32)
     channels = colors.shape[-1]
-    v_means2d = torch.zeros_like(means2d)
-    v_conics = torch.zeros_like(conics)
-    v_colors = torch.zeros_like(colors)
-    v_opacities = torch.zeros_like(opacities)
-    v_means2d_abs = torch.zeros_like(means2d) if absgrad else None
+    # the kernel accumulates with atomics: one zero fill for every
+    # accumulator, handed out as disjoint views
+    likes = [means2d, conics, colors, opacities] + ([means2d] if absgrad else [])
+    sizes = [t.numel() for t in likes]
+    parts = torch.zeros(sum(sizes), dtype=_F32, device=means2d.device).split(sizes)
+    v_means2d, v_conics, v_colors, v_opacities = (
+        parts[k].view(likes[k].shape) for k in range(4))
+    v_means2d_abs = parts[4].view(means2d.shape) if absgrad else None
     call("gsplat_rasterize_bwd", I, n_rows, flatten_ids.numel(), channels,
          ptr(means2d), ptr(conics), ptr(colors), ptr(opacities),
          ptr(backgrounds), ptr(masks), int(image_width), int(image_height),

@@ -462,7 +462,10 @@ class _FullyFusedProjectionPacked(torch.autograd.Function):
         if not calc_compensations:
             compensations = None
         ctx.save_for_backward(batch_ids, camera_ids, gaussian_ids, means, covars,
-                              quats, scales, viewmats, Ks, conics, compensations)
+                              quats, scales, viewmats, Ks, conics, compensations,
+                              row_of)
+        # unused outputs (depths, often) reach backward as None, not zeros
+        ctx.set_materialize_grads(False)
         ctx.width = width
         ctx.height = height
         ctx.eps2d = eps2d
@@ -477,19 +480,31 @@ class _FullyFusedProjectionPacked(torch.autograd.Function):
     def backward(ctx, v_batch_ids, v_camera_ids, v_gaussian_ids, v_indptr,
                  v_radii, v_means2d, v_depths, v_conics, v_compensations, v_row_of):
         (batch_ids, camera_ids, gaussian_ids, means, covars, quats, scales,
-         viewmats, Ks, conics, compensations) = ctx.saved_tensors
+         viewmats, Ks, conics, compensations, row_of) = ctx.saved_tensors
         sparse_grad = ctx.sparse_grad
         if compensations is None:
             v_compensations = None
         elif v_compensations is not None:
             v_compensations = v_compensations.contiguous()
-        v_means, v_covars, v_quats, v_scales, v_viewmats = _make_lazy_cuda_func(
-            "projection_ewa_3dgs_packed_bwd"
-        )(means, covars, quats, scales, viewmats, Ks, ctx.width, ctx.height,
-          ctx.eps2d, ctx.camera_model_type, batch_ids, camera_ids, gaussian_ids,
-          conics, compensations, v_means2d.contiguous(), v_depths.contiguous(),
-          v_conics.contiguous(), v_compensations, ctx.needs_input_grad[4],
-          sparse_grad)
+        v_means2d = (torch.zeros_like(conics[:, :2]) if v_means2d is None
+                     else v_means2d.contiguous())
+        v_conics = torch.zeros_like(conics) if v_conics is None else v_conics.contiguous()
+        if sparse_grad:
+            if v_depths is None:
+                v_depths = torch.zeros_like(conics[:, 0])
+            v_means, v_covars, v_quats, v_scales, v_viewmats = _make_lazy_cuda_func(
+                "projection_ewa_3dgs_packed_bwd"
+            )(means, covars, quats, scales, viewmats, Ks, ctx.width, ctx.height,
+              ctx.eps2d, ctx.camera_model_type, batch_ids, camera_ids, gaussian_ids,
+              conics, compensations, v_means2d, v_depths.contiguous(),
+              v_conics, v_compensations, ctx.needs_input_grad[4], sparse_grad)
+        else:
+            # dense gradients straight from the row map: one pass, no fill
+            v_means, v_covars, v_quats, v_scales, v_viewmats = _ops.projection_packed_bwd_rows(
+                means, covars, quats, scales, viewmats, Ks, ctx.width, ctx.height,
+                ctx.eps2d, ctx.camera_model_type, row_of, conics, compensations,
+                v_means2d, None if v_depths is None else v_depths.contiguous(),
+                v_conics, v_compensations, ctx.needs_input_grad[4])
         coalesced = len(viewmats) == 1
 
         def sparse(values, like):
@@ -604,12 +619,19 @@ class _RasterizeToPixels(torch.autograd.Function):
         ctx.height = height
         ctx.tile_size = tile_size
         ctx.absgrad = absgrad
+        # an unused alpha (or colour) output reaches backward as None
+        ctx.set_materialize_grads(False)
         return render_colors, render_alphas
 
     @staticmethod
-    def backward(ctx, v_render_colors: Tensor, v_render_alphas: Tensor):
+    def backward(ctx, v_render_colors: Optional[Tensor],
+                 v_render_alphas: Optional[Tensor]):
         (means2d, conics, colors, opacities, backgrounds, masks, isect_offsets,
          flatten_ids, render_T, last_ids) = ctx.saved_tensors
+        if v_render_colors is None and v_render_alphas is None:
+            return (None,) * 12
+        if v_render_colors is None:
+            v_render_colors = render_T.new_zeros((*render_T.shape, colors.shape[-1]))
         # render_alphas = 1 - T is only needed when T is absent; pass T's
         # storage as the (unused) alphas argument to satisfy the op's checks.
         (v_means2d_abs, v_means2d, v_conics, v_colors,
@@ -617,8 +639,8 @@ class _RasterizeToPixels(torch.autograd.Function):
             means2d, conics, colors, opacities, backgrounds, masks, ctx.width,
             ctx.height, ctx.tile_size, isect_offsets, flatten_ids,
             render_T, last_ids, v_render_colors.contiguous(),
-            v_render_alphas.contiguous(), ctx.absgrad,
-            render_transmittance=render_T)
+            None if v_render_alphas is None else v_render_alphas.contiguous(),
+            ctx.absgrad, render_transmittance=render_T)
         if ctx.absgrad:
             prev = getattr(means2d, "absgrad", None)
             if prev is not None and getattr(means2d, "_absgrad_pass", None) is \

@@ -155,6 +155,30 @@ int gsplat_projection_packed_bwd(
     float *v_viewmats,
     gsplat_stream_t stream);
 
+/* Backward of the packed projection driven by Gaussian: one thread per
+ * (b, g) sums the gradients of its packed rows row_of[(b C + c) N + g]
+ * (>= 0; the map written by gsplat_projection_packed_fwd) over the C
+ * cameras and writes every dense gradient row once -- v_means [B,N,3],
+ * v_covars [B,N,6] or v_quats [B,N,4] + v_scales [B,N,3], zeros for
+ * Gaussians visible nowhere -- so the caller needs no zero fill and no
+ * atomics are used.  v_depths and v_means may be NULL (zero gradient / not
+ * wanted).  v_viewmats [B,C,4,4] (optional) must be zero-filled.
+ * Same result as gsplat_projection_packed_bwd with sparse_grad == 0
+ * (gsplat/cuda/csrc/Projection.cpp:439-576); used by rasterization() where
+ * the row map is at hand. */
+int gsplat_projection_packed_bwd_rows(
+    int64_t B, int64_t C, int64_t N,
+    const float *means, const float *covars, const float *quats,
+    const float *scales, const float *viewmats, const float *Ks,
+    int32_t image_width, int32_t image_height, float eps2d,
+    int32_t camera_model, const int32_t *row_of,
+    const float *conics, const float *compensations,
+    const float *v_means2d, const float *v_depths, const float *v_conics,
+    const float *v_compensations,
+    float *v_means, float *v_covars, float *v_quats, float *v_scales,
+    float *v_viewmats,
+    gsplat_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Spherical harmonics (real SH, Sloan 2013 basis, degree 0..4).             */
 /* ------------------------------------------------------------------------ */
@@ -358,6 +382,7 @@ int gsplat_rasterize_fwd(
  * render_transmittance (optional) is the forward's final T per pixel; when
  * NULL, T is taken as 1 - render_alphas as the reference does, which loses
  * relative precision for pixels that end near the 1e-4 cutoff.
+ * v_render_alphas may be NULL (a zero alpha gradient).
  * Gradient outputs are ACCUMULATED and must be zero-filled by the caller:
  * v_means2d [n,2], v_conics [n,3], v_colors [n,CDIM], v_opacities [n],
  * v_means2d_abs [n,2] (optional; sum over pixels of |dL/dmean2d|). */

@@ -134,3 +134,30 @@ def test_rasterize_last_ids_match_oracle():
     np.testing.assert_array_equal(last.cpu().numpy(), info["last_ids"])
     np.testing.assert_array_equal(ra.cpu().numpy()[..., 0],
                                   (np.float32(1.0) - info["transmittance"]).astype(np.float32))
+
+
+def test_rasterize_unused_alpha_gradient():
+    """A loss on the colours only: the alpha gradient reaches the backward as
+    None (no zero tensor) and gives the same gradients as an explicit zero
+    alpha gradient."""
+    from gsplat_amd.cuda._wrapper import rasterize_to_pixels
+    data = projected_2d(seed=60, N=2000, C=1, D=3)
+    W, H, ts = data["W"], data["H"], data["tile"]
+    grads = []
+    for with_alpha in (False, True):
+        ins = [data[k].clone().to(DEV).requires_grad_()
+               for k in ("means2d", "conics", "colors", "opacities")]
+        rc, ra = rasterize_to_pixels(ins[0], ins[1], ins[2], ins[3], W, H, ts,
+                                     data["offsets"].to(DEV),
+                                     data["flatten_ids"].to(DEV))
+        g = torch.Generator().manual_seed(3)
+        loss = (rc * torch.randn(rc.shape, generator=g).to(DEV)).sum()
+        if with_alpha:
+            loss = loss + (ra * 0.0).sum()
+        loss.backward()
+        grads.append([t.grad for t in ins])
+    # tiles add their sums with float atomics in no fixed order: equal to
+    # float32 rounding, not bit for bit
+    for name, a, b in zip(("v_means2d", "v_conics", "v_colors", "v_opacities"),
+                          *grads):
+        assert_close(a.cpu(), b.cpu(), RTOL, ATOL, name)
