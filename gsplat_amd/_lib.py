@@ -79,7 +79,7 @@ _SIGNATURES = {
     "gsplat_rasterize_bwd": [
         c_int64, c_int64, c_int64, c_int32, _P, _P, _P, _P, _P, _P,
         c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P,
-        _P, _P, _P, _P, _P, _P, _P],
+        _P, _P, _P, _P, _P, _P, _P, _P],
     "gsplat_adam_multi": [_P, c_int32, c_float, c_float, c_float, _P],
     "gsplat_adam": [
         _P, _P, _P, _P, _P, c_int64, c_int64, c_float, c_float, c_float,

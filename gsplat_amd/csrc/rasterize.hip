@@ -89,11 +89,10 @@ __device__ __forceinline__ float4 alpha_support_box(float mx, float my, float a,
     return make_float4(mx - ex, my - ey, mx + ex, my + ey);  // x0, y0, x1, y1
 }
 
-__device__ __forceinline__ void tile_coords(const RasterArgs &a, int64_t &image,
-                                            int32_t &tile, int32_t &ty,
-                                            int32_t &tx) {
+__device__ __forceinline__ void tile_coords(const RasterArgs &a, int64_t gid,
+                                            int64_t &image, int32_t &tile,
+                                            int32_t &ty, int32_t &tx) {
     const int64_t n_tiles = (int64_t)a.tile_width * a.tile_height;
-    const int64_t gid = blockIdx.x;
     image = gid / n_tiles;
     tile = (int32_t)(gid - image * n_tiles);
     ty = tile / a.tile_width;
@@ -120,7 +119,7 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
 
     int64_t image;
     int32_t tile, ty, tx;
-    tile_coords(a, image, tile, ty, tx);
+    tile_coords(a, blockIdx.x, image, tile, ty, tx);
     const int tr = threadIdx.x;
     const int i = ty * TILE + tr / TILE;
     const int j = tx * TILE + tr % TILE;
@@ -233,34 +232,53 @@ template <int TILE> struct BwdShape {
     static_assert(THREADS % 16 == 0, "whole 16-lane rows");
 };
 
+// LDS of one backward workgroup (reused tile after tile).
+template <int CDIM, int TILE, bool ABS> struct BwdSmem {
+    using SH = BwdShape<TILE>;
+    static constexpr int BS = SH::BS;
+    static constexpr int NACC = 2 + 3 + CDIM + 1 + (ABS ? 2 : 0);
+    static constexpr int NW = (SH::THREADS + kWave - 1) / kWave;
+    float4 geo[BS];
+    float4 con[BS];
+    float col[BS * CDIM];
+    float acc[NACC * BS];
+    int32_t gid[BS];
+    int32_t hit[BS];
+    uint8_t wmask[BS];        // waves a Gaussian can reach
+    uint16_t list[NW][BS];    // per-wave work list
+    int32_t tile_bin;
+    int64_t next_tile;
+};
+
 template <int CDIM, int TILE, bool ABS>
-__global__ void __launch_bounds__(BwdShape<TILE>::THREADS) rasterize_bwd_kernel(
-    const RasterArgs a, const float *__restrict__ render_alphas,
+__device__ __forceinline__ void rasterize_bwd_tile(
+    const RasterArgs &a, int64_t tile_gid, const float *__restrict__ render_alphas,
     const float *__restrict__ render_T, const int32_t *__restrict__ last_ids,
     const float *__restrict__ v_render_colors,
     const float *__restrict__ v_render_alphas,
     float *__restrict__ v_means2d_abs, float *__restrict__ v_means2d,
     float *__restrict__ v_conics, float *__restrict__ v_colors,
-    float *__restrict__ v_opacities) {
+    float *__restrict__ v_opacities, BwdSmem<CDIM, TILE, ABS> &sm) {
     using SH = BwdShape<TILE>;
     constexpr int BS = SH::BS;
     constexpr int PX = SH::PX;
     constexpr int NT = SH::THREADS;
     // per-Gaussian sums: xy(2), conic(3), colour(CDIM), opacity(1) [, |xy|(2)]
     constexpr int NACC = 2 + 3 + CDIM + 1 + (ABS ? 2 : 0);
-    __shared__ float4 s_geo[BS];
-    __shared__ float4 s_con[BS];
-    __shared__ float s_col[BS * CDIM];
-    __shared__ float s_acc[NACC * BS];
-    __shared__ int32_t s_gid[BS];
-    __shared__ int32_t s_hit[BS];
     constexpr int NW = (NT + kWave - 1) / kWave;  // waves per tile
-    __shared__ uint8_t s_wmask[BS];               // waves a Gaussian can reach
-    __shared__ uint16_t s_list[NW][BS];           // per-wave work list
+    float4 *s_geo = sm.geo;
+    float4 *s_con = sm.con;
+    float *s_col = sm.col;
+    float *s_acc = sm.acc;
+    int32_t *s_gid = sm.gid;
+    int32_t *s_hit = sm.hit;
+    uint8_t *s_wmask = sm.wmask;
+    auto &s_list = sm.list;
+    int32_t &s_tile_bin = sm.tile_bin;
 
     int64_t image;
     int32_t tile, ty, tx;
-    tile_coords(a, image, tile, ty, tx);
+    tile_coords(a, tile_gid, image, tile, ty, tx);
     const int64_t n_tiles = (int64_t)a.tile_width * a.tile_height;
     if (a.masks != nullptr && !a.masks[image * n_tiles + tile])
         return;
@@ -273,7 +291,6 @@ __global__ void __launch_bounds__(BwdShape<TILE>::THREADS) rasterize_bwd_kernel(
     const int32_t range_end = (image == a.I - 1 && tile == n_tiles - 1)
                                   ? (int32_t)a.n_isects
                                   : offs[tile + 1];
-    __shared__ int32_t s_tile_bin;
     if (tr == 0)
         s_tile_bin = -1;
 
@@ -461,7 +478,7 @@ __global__ void __launch_bounds__(BwdShape<TILE>::THREADS) rasterize_bwd_kernel(
                 g[3] += v_sigma * dx[p] * dy[p];
                 g[4] += 0.5f * v_sigma * dy[p] * dy[p];
                 g[5 + CDIM] += vis * vv;
-                if (ABS) {
+                if constexpr (ABS) {
                     g[6 + CDIM] += fabsf(gx);
                     g[7 + CDIM] += fabsf(gy);
                 }
@@ -495,7 +512,7 @@ __global__ void __launch_bounds__(BwdShape<TILE>::THREADS) rasterize_bwd_kernel(
                     atomic_add_f32(v_colors + (int64_t)g * CDIM + k,
                                    s_acc[(5 + k) * BS + slot]);
                 atomic_add_f32(v_opacities + g, s_acc[(5 + CDIM) * BS + slot]);
-                if (ABS) {
+                if constexpr (ABS) {
                     atomic_add_f32(v_means2d_abs + (int64_t)g * 2 + 0,
                                    s_acc[(6 + CDIM) * BS + slot]);
                     atomic_add_f32(v_means2d_abs + (int64_t)g * 2 + 1,
@@ -504,6 +521,59 @@ __global__ void __launch_bounds__(BwdShape<TILE>::THREADS) rasterize_bwd_kernel(
             }
         }
     }
+}
+
+
+// One tile per workgroup, or (tile_counter != NULL, a zeroed counter) a
+// grid sized to the resident workgroups in which every workgroup takes tile
+// after tile from the counter until none is left: no partial last round of
+// workgroups, and a heavy tile never waits behind a full round.
+template <int CDIM, int TILE, bool ABS>
+__global__ void __launch_bounds__(BwdShape<TILE>::THREADS) rasterize_bwd_kernel(
+    const RasterArgs a, const float *__restrict__ render_alphas,
+    const float *__restrict__ render_T, const int32_t *__restrict__ last_ids,
+    const float *__restrict__ v_render_colors,
+    const float *__restrict__ v_render_alphas,
+    float *__restrict__ v_means2d_abs, float *__restrict__ v_means2d,
+    float *__restrict__ v_conics, float *__restrict__ v_colors,
+    float *__restrict__ v_opacities, uint32_t *__restrict__ tile_counter,
+    int64_t n_tiles_total) {
+    __shared__ BwdSmem<CDIM, TILE, ABS> sm;
+    const bool queue = tile_counter != nullptr;
+    int64_t gid = blockIdx.x;
+    while (true) {
+        if (queue) {
+            __syncthreads();  // the previous tile is finished with the LDS
+            if (threadIdx.x == 0)
+                sm.next_tile = atomicAdd(tile_counter, 1u);
+            __syncthreads();
+            gid = sm.next_tile;
+        }
+        if (gid >= n_tiles_total)
+            break;
+        rasterize_bwd_tile<CDIM, TILE, ABS>(
+            a, gid, render_alphas, render_T, last_ids, v_render_colors,
+            v_render_alphas, v_means2d_abs, v_means2d, v_conics, v_colors,
+            v_opacities, sm);
+        if (!queue)
+            break;
+    }
+}
+
+// Workgroups of `kernel` (block threads, static LDS) that fit on the device
+// at once, capped at `work`.
+int resident_grid(const void *kernel, int block, int64_t work, int64_t *grid) {
+    int dev = 0, per_cu = 0, cus = 0;
+    GS_REQUIRE(hipGetDevice(&dev) == hipSuccess, "hipGetDevice failed");
+    GS_REQUIRE(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel,
+                                                           block, 0) == hipSuccess,
+               "hipOccupancyMaxActiveBlocksPerMultiprocessor failed");
+    GS_REQUIRE(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount,
+                                     dev) == hipSuccess,
+               "hipDeviceGetAttribute failed");
+    const int64_t g = (int64_t)(per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+    *grid = g < work ? g : work;
+    return GSPLAT_OK;
 }
 
 int check_raster(const RasterArgs &a, int cdim) {
@@ -598,7 +668,7 @@ extern "C" int gsplat_rasterize_bwd(
     const float *v_render_colors,
     const float *v_render_alphas, float *v_means2d_abs, float *v_means2d,
     float *v_conics, float *v_colors, float *v_opacities,
-    gsplat_stream_t stream) {
+    uint32_t *tile_counter, gsplat_stream_t stream) {
     clear_error();
     RasterArgs a{I, n_rows, n_isects, means2d, conics, colors, opacities,
                  backgrounds, masks, image_width, image_height, tile_size,
@@ -615,11 +685,17 @@ extern "C" int gsplat_rasterize_bwd(
     GS_REQUIRE(blocks < (1ll << 31), "rasterize_bwd: too many tiles");
     hipStream_t st = as_stream(stream);
 #define GS_BWD(C, TILE, ABS)                                                   \
-    rasterize_bwd_kernel<C, TILE, ABS><<<(unsigned)blocks,                     \
-                                         BwdShape<TILE>::THREADS, 0, st>>>(    \
-        a, render_alphas, render_transmittance, last_ids, v_render_colors,     \
-        v_render_alphas, v_means2d_abs, v_means2d, v_conics, v_colors,         \
-        v_opacities)
+    {                                                                          \
+        auto kern = rasterize_bwd_kernel<C, TILE, ABS>;                        \
+        int64_t grid = blocks;                                                 \
+        if (tile_counter != nullptr)                                           \
+            GS_TRY(resident_grid((const void *)kern, BwdShape<TILE>::THREADS,  \
+                                 blocks, &grid));                              \
+        kern<<<(unsigned)grid, BwdShape<TILE>::THREADS, 0, st>>>(              \
+            a, render_alphas, render_transmittance, last_ids, v_render_colors, \
+            v_render_alphas, v_means2d_abs, v_means2d, v_conics, v_colors,     \
+            v_opacities, tile_counter, blocks);                                \
+    }
     const bool abs = v_means2d_abs != nullptr;
     if (tile_size == 16) {
         if (abs) { GS_CDIM_SWITCH(cdim, GS_BWD, 16, true) }

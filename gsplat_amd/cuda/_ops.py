@@ -638,13 +638,15 @@ def rasterize_to_pixels_3dgs_bwd(
     check_input(render_transmittance, "render_transmittance", _F32)
     channels = colors.shape[-1]
     # the kernel accumulates with atomics: one zero fill for every
-    # accumulator, handed out as disjoint views
+    # accumulator, handed out as disjoint views, plus the zeroed tile counter
+    # its workgroups take their tiles from
     likes = [means2d, conics, colors, opacities] + ([means2d] if absgrad else [])
-    sizes = [t.numel() for t in likes]
+    sizes = [t.numel() for t in likes] + [1]
     parts = torch.zeros(sum(sizes), dtype=_F32, device=means2d.device).split(sizes)
     v_means2d, v_conics, v_colors, v_opacities = (
         parts[k].view(likes[k].shape) for k in range(4))
     v_means2d_abs = parts[4].view(means2d.shape) if absgrad else None
+    tile_counter = parts[-1]
     call("gsplat_rasterize_bwd", I, n_rows, flatten_ids.numel(), channels,
          ptr(means2d), ptr(conics), ptr(colors), ptr(opacities),
          ptr(backgrounds), ptr(masks), int(image_width), int(image_height),
@@ -652,7 +654,8 @@ def rasterize_to_pixels_3dgs_bwd(
          ptr(render_alphas), ptr(render_transmittance), ptr(last_ids),
          ptr(v_render_colors),
          ptr(v_render_alphas), ptr(v_means2d_abs), ptr(v_means2d),
-         ptr(v_conics), ptr(v_colors), ptr(v_opacities), _stream(means2d))
+         ptr(v_conics), ptr(v_colors), ptr(v_opacities), ptr(tile_counter),
+         _stream(means2d))
     return v_means2d_abs, v_means2d, v_conics, v_colors, v_opacities
 
 

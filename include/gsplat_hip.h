@@ -385,7 +385,10 @@ int gsplat_rasterize_fwd(
  * v_render_alphas may be NULL (a zero alpha gradient).
  * Gradient outputs are ACCUMULATED and must be zero-filled by the caller:
  * v_means2d [n,2], v_conics [n,3], v_colors [n,CDIM], v_opacities [n],
- * v_means2d_abs [n,2] (optional; sum over pixels of |dL/dmean2d|). */
+ * v_means2d_abs [n,2] (optional; sum over pixels of |dL/dmean2d|).
+ * tile_counter (optional, one uint32, zero on entry): when given, a grid of
+ * the workgroups that fit on the device takes the tiles one after another
+ * from it (no partial last round); NULL launches one workgroup per tile. */
 int gsplat_rasterize_bwd(
     int64_t I, int64_t n_rows, int64_t n_isects, int32_t cdim,
     const float *means2d, const float *conics, const float *colors,
@@ -397,7 +400,7 @@ int gsplat_rasterize_bwd(
     const int32_t *last_ids,
     const float *v_render_colors, const float *v_render_alphas,
     float *v_means2d_abs, float *v_means2d, float *v_conics,
-    float *v_colors, float *v_opacities,
+    float *v_colors, float *v_opacities, uint32_t *tile_counter,
     gsplat_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
