@@ -85,6 +85,17 @@ def _algorithmic_bytes(name, ctx):
         return nnz * (12 + 12 * K + 1 + 12)
     if name == "gsplat_sh_bwd":
         return nnz * (12 + 12 * K + 1 + 12) + nnz * (12 * K + 12)
+    if name == "gsplat_projection_packed_bwd_rows":
+        # row map, geometry of the visible Gaussians, the rows' conics and
+        # gradients in; dense v_means / v_quats / v_scales out
+        return N * 4 * ctx["C"] + nnz * (44 + 12 + 8 + 4 + 12) + N * 40
+    if name == "gsplat_sh_rows_fwd":
+        # row map, mean + used coefficients of the visible Gaussians in,
+        # one colour row per packed row out
+        return N * 4 * ctx["C"] + nnz * (12 + 12 * K) + nnz * 12
+    if name == "gsplat_sh_rows_bwd":
+        return (N * 4 * ctx["C"] + nnz * (12 + 12 * K + 12)
+                + N * (12 * K + 12))
     if name == "gsplat_adam_multi":
         return ctx.get("adam_elems", 0) * 28
     return None
@@ -100,20 +111,69 @@ def _gpu_bench(args):
     dev = "cuda:0"
     scene = make_scene(args.config).to(dev)
     C = scene.viewmats.shape[0]
-    params = {k: getattr(scene, k).clone().requires_grad_()
-              for k in ("means", "quats", "scales", "opacities", "colors")}
     kw = dict(scene.kwargs)
 
-    def step():
-        for p in params.values():
-            p.grad = None
-        rc, ra, meta = gs.rasterization(
-            params["means"], params["quats"], params["scales"], params["opacities"],
-            params["colors"], scene.viewmats, scene.Ks, scene.width, scene.height,
-            sh_degree=scene.sh_degree, **kw)
-        loss = (rc - scene.target).abs().mean()
-        loss.backward()
-        return meta
+    if args.config == 4:
+        # full optimizer step: raw parameters, absgrad
+        # densification statistics, one fused Adam launch over six tensors
+        from gsplat_amd.cuda import _ops
+        from gsplat_amd.strategy.stats import accumulate_grad2d_stats
+        raw = {
+            "means": scene.means, "log_scales": scene.log_scales,
+            "quats": scene.quats, "opacity_logits": scene.opacity_logits,
+            "sh0": scene.colors[:, :1], "shN": scene.colors[:, 1:],
+        }
+        params = {k: v.clone().contiguous().requires_grad_() for k, v in raw.items()}
+        lrs = {"means": 1.6e-4, "log_scales": 5e-3, "quats": 1e-3,
+               "opacity_logits": 5e-2, "sh0": 2.5e-3, "shN": 1.25e-4}
+        moments = {k: (torch.zeros_like(v), torch.zeros_like(v)) for k, v in params.items()}
+        stats = {"grad2d": None, "count": None}
+        kw["absgrad"] = True
+
+        def step():
+            for p in params.values():
+                p.grad = None
+            rc, ra, meta = gs.rasterization(
+                params["means"], params["quats"], params["log_scales"].exp(),
+                torch.sigmoid(params["opacity_logits"]),
+                torch.cat([params["sh0"], params["shN"]], dim=1), scene.viewmats,
+                scene.Ks, scene.width, scene.height, sh_degree=scene.sh_degree, **kw)
+            loss = (rc - scene.target).abs().mean()
+            loss.backward()
+            stats["grad2d"], stats["count"] = accumulate_grad2d_stats(
+                meta, stats["grad2d"], stats["count"], scene.means.shape[0],
+                packed=True, absgrad=True)
+            with torch.no_grad():
+                _ops.adam_multi(
+                    [(params[k], params[k].grad, moments[k][0], moments[k][1], None,
+                      lrs[k]) for k in params], 0.9, 0.999, 1e-15)
+            return meta
+    elif args.config == 3:
+        # large-scene inference render: forward only
+        params = {k: getattr(scene, k).contiguous()
+                  for k in ("means", "quats", "scales", "opacities", "colors")}
+
+        def step():
+            with torch.no_grad():
+                rc, ra, meta = gs.rasterization(
+                    params["means"], params["quats"], params["scales"],
+                    params["opacities"], params["colors"], scene.viewmats, scene.Ks,
+                    scene.width, scene.height, sh_degree=scene.sh_degree, **kw)
+            return meta
+    else:
+        params = {k: getattr(scene, k).clone().requires_grad_()
+                  for k in ("means", "quats", "scales", "opacities", "colors")}
+
+        def step():
+            for p in params.values():
+                p.grad = None
+            rc, ra, meta = gs.rasterization(
+                params["means"], params["quats"], params["scales"], params["opacities"],
+                params["colors"], scene.viewmats, scene.Ks, scene.width, scene.height,
+                sh_degree=scene.sh_degree, **kw)
+            loss = (rc - scene.target).abs().mean()
+            loss.backward()
+            return meta
 
     for _ in range(args.warmup):
         meta = step()
@@ -137,6 +197,8 @@ def _gpu_bench(args):
         "D": 3 if kw.get("render_mode", "RGB") == "RGB" else 4,
         "tiles": C * meta["tile_width"] * meta["tile_height"],
         "K": scene.colors.shape[-2] if scene.sh_degree is not None else 0,
+        "adam_elems": sum(p.numel() for p in params.values()) if args.config == 4 else 0,
+        "C": C,
     }
 
     # timed region: K steps, HIP events around the dominant entry point
@@ -213,17 +275,32 @@ def _cpu_baseline(config, stride):
     th = math.ceil(scene.height / 16)
     n_tiles = C * tw * th
 
+    fwd_only = config == 3
+    moments = {}
+
     def run(subset):
-        leaves = {k: getattr(scene, k).clone().requires_grad_()
+        leaves = {k: getattr(scene, k).clone().requires_grad_(not fwd_only)
                   for k in ("means", "quats", "scales", "opacities", "colors")}
         t = time.perf_counter()
-        rc, ra, meta = torch_ref.rasterization_ref(
-            leaves["means"], leaves["quats"], leaves["scales"], leaves["opacities"],
-            leaves["colors"], scene.viewmats, scene.Ks, scene.width, scene.height,
-            sh_degree=scene.sh_degree, dtype=torch.float32, tile_subset=subset,
-            **scene.kwargs)
+        with torch.set_grad_enabled(not fwd_only):
+            rc, ra, meta = torch_ref.rasterization_ref(
+                leaves["means"], leaves["quats"], leaves["scales"], leaves["opacities"],
+                leaves["colors"], scene.viewmats, scene.Ks, scene.width, scene.height,
+                sh_degree=scene.sh_degree, dtype=torch.float32, tile_subset=subset,
+                **scene.kwargs)
+        if fwd_only:
+            return time.perf_counter() - t
         loss = (rc - scene.target).abs().mean()
         loss.backward()
+        if config == 4:
+            # the Adam update over the same parameter elements (118M), in torch
+            with torch.no_grad():
+                for k, p in leaves.items():
+                    m, v = moments.setdefault(k, (torch.zeros_like(p), torch.zeros_like(p)))
+                    g = p.grad
+                    m.mul_(0.9).add_(g, alpha=0.1)
+                    v.mul_(0.999).addcmul_(g, g, value=0.001)
+                    p.sub_(1e-3 * m / (v.sqrt() + 1e-15))
         return time.perf_counter() - t
 
     sample_a = list(range(0, n_tiles, stride))
@@ -238,7 +315,8 @@ def _cpu_baseline(config, stride):
         "unit": "ms/step",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"config {config}: oracle fwd+bwd with projection+SH+intersection for all "
+        "sample": (f"config {config}: oracle {'fwd' if fwd_only else 'fwd+bwd'}"
+                   f"{' + Adam' if config == 4 else ''} with projection+SH+intersection for all "
                    f"{scene.means.shape[0]} Gaussians and rasterization on {len(sample_b)} "
                    f"then {len(sample_a)} of {n_tiles} tiles (strided); took "
                    f"{t_b:.1f}s / {t_a:.1f}s -> fixed {fixed:.1f}s + "
@@ -271,8 +349,9 @@ def main():
         0: "cfg0: 10k Gaussians, SH0, 256x256, packed, fwd+bwd L1",
         1: "cfg1: 1M Gaussians, SH3, 1280x720, packed, fwd+bwd L1",
         2: "cfg2: 500k Gaussians, SH1, 8x 960x540, packed, RGB+ED, fwd+bwd L1",
-        3: "cfg3: 6M Gaussians, SH3, 1920x1080, fwd+bwd L1",
-        4: "cfg4: 2M Gaussians, SH3, 1600x1040, fwd+bwd L1",
+        3: "cfg3: 6M Gaussians, SH3, 1920x1080, forward only",
+        4: ("cfg4: 2M Gaussians, SH3, 1600x1040, fwd+bwd L1 with absgrad stats and "
+            "fused Adam over 6 tensors"),
     }[args.config]
     out = {
         "metric": METRIC,

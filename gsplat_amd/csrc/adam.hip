@@ -7,7 +7,8 @@
 // write p, m, v).  Every workgroup owns a 4096-element chunk of exactly one
 // tensor, so one launch covers all tensors without per-element tensor lookup;
 // each thread moves 16-byte vectors (4 per chunk pass) so a wave issues
-// 1 KiB-wide coalesced loads.  The arithmetic is done in the order written
+// 1 KiB-wide coalesced loads; all of a thread's loads are issued before its
+// first update, and the accesses are non-temporal (streamed once).  The arithmetic is done in the order written
 // above with contraction disabled, which makes the result bit-for-bit
 // reproducible by a float32 host restatement.
 #include "common.h"
@@ -19,6 +20,18 @@ constexpr int kAdamThreads = 256;
 constexpr int kAdamVecPerThread = 4;
 constexpr int64_t kAdamChunk = (int64_t)kAdamThreads * kAdamVecPerThread * 4;
 constexpr int kAdamMaxTensors = 24;
+
+// Streaming (non-temporal) 16-byte accesses: every byte is touched once, so
+// the lines are not worth keeping in the caches.
+typedef float gs_v4f __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 stream_load(const float4 *p) {
+    const gs_v4f v = __builtin_nontemporal_load(reinterpret_cast<const gs_v4f *>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void stream_store(float4 *p, float4 x) {
+    const gs_v4f v = {x.x, x.y, x.z, x.w};
+    __builtin_nontemporal_store(v, reinterpret_cast<gs_v4f *>(p));
+}
 
 struct AdamDesc {
     float *p;
@@ -79,16 +92,30 @@ __global__ void __launch_bounds__(kAdamThreads)
         float4 *m4 = reinterpret_cast<float4 *>(d.m);
         float4 *v4 = reinterpret_cast<float4 *>(d.v);
         const int64_t vbase = chunk_begin >> 2;
+        // every load of the thread is issued before the first update, so a
+        // wave waits for memory once per chunk
+        float4 P[kAdamVecPerThread], G[kAdamVecPerThread], M[kAdamVecPerThread],
+            V[kAdamVecPerThread];
+        bool ok[kAdamVecPerThread];
 #pragma unroll
         for (int it = 0; it < kAdamVecPerThread; ++it) {
             const int64_t q = vbase + (int64_t)it * kAdamThreads + threadIdx.x;
-            if (q >= nvec_total || (q << 2) >= chunk_end)
-                break;
-            float4 p = p4[q];
-            const float4 g = g4[q];
-            float4 m = m4[q];
-            float4 v = v4[q];
+            ok[it] = q < nvec_total && (q << 2) < chunk_end;
+            if (ok[it]) {
+                P[it] = stream_load(&p4[q]);
+                G[it] = stream_load(&g4[q]);
+                M[it] = stream_load(&m4[q]);
+                V[it] = stream_load(&v4[q]);
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < kAdamVecPerThread; ++it) {
+            if (!ok[it])
+                continue;
+            const int64_t q = vbase + (int64_t)it * kAdamThreads + threadIdx.x;
             const int64_t e0 = q << 2;
+            float4 &p = P[it], &m = M[it], &v = V[it];
+            const float4 g = G[it];
             if (d.valid == nullptr) {
                 adam_update(p.x, g.x, m.x, v.x, d.lr, b1, b2, eps);
                 adam_update(p.y, g.y, m.y, v.y, d.lr, b1, b2, eps);
@@ -104,9 +131,9 @@ __global__ void __launch_bounds__(kAdamThreads)
                 if (row_valid(d, e0 + 3))
                     adam_update(p.w, g.w, m.w, v.w, d.lr, b1, b2, eps);
             }
-            p4[q] = p;
-            m4[q] = m;
-            v4[q] = v;
+            stream_store(&p4[q], p);
+            stream_store(&m4[q], m);
+            stream_store(&v4[q], v);
         }
         // scalar tail (numel not a multiple of 4) handled by the last chunk
         const int64_t tail_begin = nvec_total << 2;
