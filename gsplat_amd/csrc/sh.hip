@@ -384,16 +384,25 @@ __global__ void __launch_bounds__(kShThreads)
 // staged once (coalesced, skipped when it is visible in no camera) and it
 // loops over the C cameras through row_of[(b C + c) N + g] (the packed row,
 // or -1).  The forward writes colors[row] = max(SH(dir) + 0.5, 0) with
-// dir = mean - campos (rendering.py:872); the backward accumulates the
+// dir = mean - campos, campos = -R^T t of the camera (rendering.py:872,
+// taken from the view matrix in the kernel); the backward accumulates the
 // coefficient and mean gradients over the cameras in registers and writes
 // every Gaussian's gradient row once -- deterministic, no atomics, no
 // zero fill.
 // ---------------------------------------------------------------------------
+// Camera centre -R^T t of a row-major world->camera matrix (the camera
+// position of rendering.py:216-224).
+__device__ __forceinline__ void camera_centre(const float *vm, float *cp) {
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+        cp[j] = -(vm[0 * 4 + j] * vm[3] + vm[1 * 4 + j] * vm[7] + vm[2 * 4 + j] * vm[11]);
+}
+
 struct ShRowsArgs {
     int64_t B, C, N;
     int K;
     const float *means;   // [B, N, 3]
-    const float *campos;  // [B, C, 3]
+    const float *viewmats;  // [B, C, 4, 4] world->camera
     const float *coeffs;  // [B, N, K, 3]
     const int32_t *row_of;  // [B, C, N]
     bool vec_ok;
@@ -456,7 +465,8 @@ __global__ void __launch_bounds__(kShThreads)
             continue;
         float Y[S::NB];
         if (DEG > 0) {
-            const float *cp = a.campos + (b * a.C + c) * 3;
+            float cp[3];
+            camera_centre(a.viewmats + (b * a.C + c) * 16, cp);
             const float dx = mx - cp[0], dy = my - cp[1], dz = mz - cp[2];
             const float inorm = 1.f / sqrtf(dx * dx + dy * dy + dz * dz);
             sh_basis<DEG>(dx * inorm, dy * inorm, dz * inorm, Y);
@@ -509,7 +519,8 @@ __global__ void __launch_bounds__(kShThreads)
             float Y[S::NB];
             float x = 0.f, y = 0.f, z = 0.f, inorm = 0.f;
             if (DEG > 0) {
-                const float *cp = a.campos + (b * a.C + c) * 3;
+                float cp[3];
+                camera_centre(a.viewmats + (b * a.C + c) * 16, cp);
                 const float dx = mx - cp[0], dy = my - cp[1], dz = mz - cp[2];
                 inorm = 1.f / sqrtf(dx * dx + dy * dy + dz * dz);
                 x = dx * inorm;
@@ -663,29 +674,29 @@ extern "C" int gsplat_sh_bwd(int64_t M, int32_t K, int32_t degree,
     KERNEL<DEG><<<grid, kShThreads, 0, st>>>(__VA_ARGS__)
 
 static int sh_rows_check(int64_t B, int64_t C, int64_t N, int32_t K,
-                         int32_t degree, const float *means, const float *campos,
+                         int32_t degree, const float *means, const float *viewmats,
                          const float *coeffs, const int32_t *row_of) {
     GS_REQUIRE(B >= 0 && C >= 0 && N >= 0, "sh_rows: negative size");
     GS_REQUIRE(degree >= 0 && degree <= 4, "sh_rows: degree must be in [0, 4]");
     GS_REQUIRE((degree + 1) * (degree + 1) <= K,
                "sh_rows: K must be >= (degree + 1)^2");
     if (B * N > 0)
-        GS_REQUIRE(means && campos && coeffs && row_of, "sh_rows: NULL input");
+        GS_REQUIRE(means && viewmats && coeffs && row_of, "sh_rows: NULL input");
     return GSPLAT_OK;
 }
 
 extern "C" int gsplat_sh_rows_fwd(int64_t B, int64_t C, int64_t N, int32_t K,
                                   int32_t degree, const float *means,
-                                  const float *campos, const float *coeffs,
+                                  const float *viewmats, const float *coeffs,
                                   const int32_t *row_of, float *colors,
                                   gsplat_stream_t stream) {
     clear_error();
-    GS_TRY(sh_rows_check(B, C, N, K, degree, means, campos, coeffs, row_of));
+    GS_TRY(sh_rows_check(B, C, N, K, degree, means, viewmats, coeffs, row_of));
     if (B * N == 0 || C == 0)
         return GSPLAT_OK;
     GS_REQUIRE(colors != nullptr, "sh_rows_fwd: NULL colors");
     const int nb = (degree + 1) * (degree + 1);
-    ShRowsArgs a{B, C, N, K, means, campos, coeffs, row_of,
+    ShRowsArgs a{B, C, N, K, means, viewmats, coeffs, row_of,
                  (K == nb) && aligned16(coeffs)};
     const dim3 grid((unsigned)ceil_div(B * N, kShThreads));
     hipStream_t st = as_stream(stream);
@@ -701,18 +712,18 @@ extern "C" int gsplat_sh_rows_fwd(int64_t B, int64_t C, int64_t N, int32_t K,
 
 extern "C" int gsplat_sh_rows_bwd(int64_t B, int64_t C, int64_t N, int32_t K,
                                   int32_t degree, const float *means,
-                                  const float *campos, const float *coeffs,
+                                  const float *viewmats, const float *coeffs,
                                   const int32_t *row_of, const float *v_colors,
                                   float *v_coeffs, float *v_means,
                                   gsplat_stream_t stream) {
     clear_error();
-    GS_TRY(sh_rows_check(B, C, N, K, degree, means, campos, coeffs, row_of));
+    GS_TRY(sh_rows_check(B, C, N, K, degree, means, viewmats, coeffs, row_of));
     if (B * N == 0)
         return GSPLAT_OK;
     GS_REQUIRE(v_coeffs && v_means, "sh_rows_bwd: NULL output");
     GS_REQUIRE(C == 0 || v_colors != nullptr, "sh_rows_bwd: NULL v_colors");
     const int nb = (degree + 1) * (degree + 1);
-    ShRowsArgs a{B, C, N, K, means, campos, coeffs, row_of,
+    ShRowsArgs a{B, C, N, K, means, viewmats, coeffs, row_of,
                  (K == nb) && aligned16(coeffs) && aligned16(v_coeffs)};
     const dim3 grid((unsigned)ceil_div(B * N, kShThreads));
     hipStream_t st = as_stream(stream);

@@ -372,31 +372,32 @@ def projection_packed_bwd_rows(
 # Packed rows driven by Gaussian (replace the gathers / index_put scatters of
 # the packed path, rendering.py:95-213, 782, 845-873)
 # --------------------------------------------------------------------------
-def sh_rows_fwd(degree: int, means: Tensor, campos: Tensor, coeffs: Tensor,
+def sh_rows_fwd(degree: int, means: Tensor, viewmats: Tensor, coeffs: Tensor,
                 row_of: Tensor, nnz: int) -> Tensor:
-    """colors [nnz, 3] = max(SH(normalize(mean - campos)) + 0.5, 0) for every
-    packed row; means [B, N, 3], campos [B, C, 3], coeffs [B, N, K, 3]."""
-    for t, n in ((means, "means"), (campos, "campos"), (coeffs, "coeffs")):
+    """colors [nnz, 3] = max(SH(normalize(mean - centre)) + 0.5, 0) for every
+    packed row, centre = -R^T t of the camera; means [B, N, 3], viewmats
+    [B, C, 4, 4], coeffs [B, N, K, 3]."""
+    for t, n in ((means, "means"), (viewmats, "viewmats"), (coeffs, "coeffs")):
         check_input(t, n, _F32)
     check_input(row_of, "row_of", _I32)
     B, N = means.shape[0], means.shape[1]
-    C = campos.shape[1]
+    C = viewmats.shape[1]
     K = coeffs.shape[-2]
     colors = torch.empty(nnz, 3, dtype=_F32, device=means.device)
-    call("gsplat_sh_rows_fwd", B, C, N, K, int(degree), ptr(means), ptr(campos),
+    call("gsplat_sh_rows_fwd", B, C, N, K, int(degree), ptr(means), ptr(viewmats),
          ptr(coeffs), ptr(row_of), ptr(colors), _stream(means))
     return colors
 
 
-def sh_rows_bwd(degree: int, means: Tensor, campos: Tensor, coeffs: Tensor,
+def sh_rows_bwd(degree: int, means: Tensor, viewmats: Tensor, coeffs: Tensor,
                 row_of: Tensor, v_colors: Tensor) -> Tuple[Tensor, Tensor]:
     check_input(v_colors, "v_colors", _F32)
     B, N = means.shape[0], means.shape[1]
-    C = campos.shape[1]
+    C = viewmats.shape[1]
     K = coeffs.shape[-2]
     v_coeffs = torch.empty_like(coeffs)
     v_means = torch.empty_like(means)
-    call("gsplat_sh_rows_bwd", B, C, N, K, int(degree), ptr(means), ptr(campos),
+    call("gsplat_sh_rows_bwd", B, C, N, K, int(degree), ptr(means), ptr(viewmats),
          ptr(coeffs), ptr(row_of), ptr(v_colors), ptr(v_coeffs), ptr(v_means),
          _stream(means))
     return v_coeffs, v_means
@@ -467,6 +468,10 @@ def intersect_tile(
                 torch.empty(0, dtype=_I32, device=dev))
     st = _stream(means2d)
     img = image_ids if packed else None
+    if packed and int(I) == 1:
+        # one image: every row's image id is 0, which the dense layout with
+        # N = n gives (row // n) without reading the ids
+        img, N = None, n
     if sort:
         # Rows sorted by depth, intersections emitted in that order, then a
         # stable sort on the image|tile bits only: the reference's full-key

@@ -578,25 +578,27 @@ class _PackedRowsGather(torch.autograd.Function):
 
 
 class _PackedSphericalHarmonics(torch.autograd.Function):
-    """Clamped SH colour of every packed row, max(SH(mean - campos) + 0.5, 0),
+    """Clamped SH colour of every packed row, max(SH(mean - campos) + 0.5, 0)
+    with campos = -R^T t taken from the view matrices in the kernel,
     evaluated per Gaussian (the reference's compute_directions + gathers +
-    spherical_harmonics + clamp_min, rendering.py:227-253, 845-873)."""
+    spherical_harmonics + clamp_min, rendering.py:227-253, 845-873).  The
+    view matrices get no gradient (the caller detaches them)."""
 
     @staticmethod
-    def forward(ctx, degree: int, means: Tensor, coeffs: Tensor, campos: Tensor,
+    def forward(ctx, degree: int, means: Tensor, coeffs: Tensor, viewmats: Tensor,
                 row_of: Tensor, nnz: int):
         means = means.contiguous()
         coeffs = coeffs.contiguous()
-        campos = campos.contiguous()
-        colors = _ops.sh_rows_fwd(degree, means, campos, coeffs, row_of, nnz)
-        ctx.save_for_backward(means, coeffs, campos, row_of)
+        viewmats = viewmats.contiguous()
+        colors = _ops.sh_rows_fwd(degree, means, viewmats, coeffs, row_of, nnz)
+        ctx.save_for_backward(means, coeffs, viewmats, row_of)
         ctx.degree = degree
         return colors
 
     @staticmethod
     def backward(ctx, v_colors: Tensor):
-        means, coeffs, campos, row_of = ctx.saved_tensors
-        v_coeffs, v_means = _ops.sh_rows_bwd(ctx.degree, means, campos, coeffs,
+        means, coeffs, viewmats, row_of = ctx.saved_tensors
+        v_coeffs, v_means = _ops.sh_rows_bwd(ctx.degree, means, viewmats, coeffs,
                                              row_of, v_colors.contiguous())
         return (None, v_means if ctx.needs_input_grad[1] else None,
                 v_coeffs if ctx.needs_input_grad[2] else None, None, None, None)

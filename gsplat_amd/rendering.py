@@ -235,7 +235,8 @@ def rasterization(
         # backward is a per-Gaussian sum, not an index_put)
         opacities = _PackedRowsGather.apply(
             opacities.reshape(B, N, 1), row_of, C, nnz).reshape(nnz)
-        image_ids = batch_ids * C + camera_ids
+        # with one image every row's image id is 0 (= camera_ids)
+        image_ids = camera_ids if B * C == 1 else batch_ids * C + camera_ids
     else:
         radii, means2d, depths, conics, compensations = proj_results
         opacities = torch.broadcast_to(opacities[..., None, :], batch_dims + (C, N))
@@ -243,7 +244,6 @@ def rasterization(
         image_ids = None
     if compensations is not None:
         opacities = opacities * compensations
-    valid_gaussians = (radii > 0).all(dim=-1)
     meta.update({
         "batch_ids": batch_ids, "camera_ids": camera_ids,
         "gaussian_ids": gaussian_ids, "radii": radii, "means2d": means2d,
@@ -264,11 +264,10 @@ def rasterization(
             proj_features = _PackedRowsGather.apply(
                 colors.reshape(B, N, D), row_of, C, nnz)
         else:
-            campos = viewmat_to_camera_position(viewmats).reshape(B, C, 3)
             K = colors.shape[-2]
             proj_features = _PackedSphericalHarmonics.apply(
                 colors_sh_degree, means.reshape(B, N, 3), colors.reshape(B, N, K, 3),
-                campos.detach(), row_of, nnz)
+                viewmats.reshape(B, C, 4, 4).detach(), row_of, nnz)
     elif colors_sh_degree is None and extra_signals_sh_degree is None:
         feature_list = []
         if has_color:
@@ -291,7 +290,7 @@ def rasterization(
                                                batch_ids, camera_ids, gaussian_ids)
             if colors_sh_degree is not None:
                 colors = spherical_harmonics(colors_sh_degree, dirs, colors,
-                                             masks=valid_gaussians)
+                                             masks=(radii > 0).all(dim=-1))
                 colors = torch.clamp_min(colors + 0.5, 0.0)
             feature_list.append(colors)
         if extra_signals is not None:
@@ -301,7 +300,7 @@ def rasterization(
                                            batch_ids, camera_ids, gaussian_ids)
             if extra_signals_sh_degree is not None:
                 es = spherical_harmonics(extra_signals_sh_degree, dirs, es,
-                                         masks=valid_gaussians) + 0.5
+                                         masks=(radii > 0).all(dim=-1)) + 0.5
             feature_list.append(es)
         if feature_list:
             proj_features = (torch.cat(feature_list, dim=-1)

@@ -210,13 +210,14 @@ int gsplat_sh_bwd(
  * + spherical_harmonics + clamp_min(colors + 0.5, 0)
  *   (gsplat/rendering.py:227-253, 170-213, 845-873;
  *    gsplat/cuda/csrc/SphericalHarmonicsCUDA.cu:391-462).
- * means [B,N,3], campos [B,C,3] (camera centres), coeffs [B,N,K,3],
+ * means [B,N,3], viewmats [B,C,4,4] (world->camera; the camera centre
+ * -R^T t is taken from them), coeffs [B,N,K,3],
  * row_of [B,C,N] (packed row of (b,c,g) or -1, from
  * gsplat_projection_packed_fwd); writes colors [nnz,3] =
- * max(SH(normalize(mean - campos)) + 0.5, 0) for every packed row. */
+ * max(SH(normalize(mean - centre)) + 0.5, 0) for every packed row. */
 int gsplat_sh_rows_fwd(
     int64_t B, int64_t C, int64_t N, int32_t K, int32_t degree,
-    const float *means, const float *campos, const float *coeffs,
+    const float *means, const float *viewmats, const float *coeffs,
     const int32_t *row_of, float *colors, gsplat_stream_t stream);
 
 /* Backward of gsplat_sh_rows_fwd.  Replaces spherical_harmonics_bwd plus
@@ -228,7 +229,7 @@ int gsplat_sh_rows_fwd(
  * camera order (deterministic). */
 int gsplat_sh_rows_bwd(
     int64_t B, int64_t C, int64_t N, int32_t K, int32_t degree,
-    const float *means, const float *campos, const float *coeffs,
+    const float *means, const float *viewmats, const float *coeffs,
     const int32_t *row_of, const float *v_colors, float *v_coeffs,
     float *v_means, gsplat_stream_t stream);
 

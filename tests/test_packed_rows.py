@@ -68,7 +68,7 @@ def test_sh_rows_fwd_bwd(degree, C):
     gm = means.clone().to(DEV).requires_grad_()
     gc = coeffs.clone().to(DEV).requires_grad_()
     col = _PackedSphericalHarmonics.apply(degree, gm[None], gc[None],
-                                          campos[None].to(DEV), row_of, nnz)
+                                          vm[None].to(DEV), row_of, nnz)
     (col * v_col.to(DEV)).sum().backward()
 
     def ref(dtype):
