@@ -9,9 +9,9 @@
 // tiles above):
 //   1. radix_hist_kernel    digit counts per tile with LDS atomics, written
 //                           tile-major (coalesced);
-//   2. radix_colscan_kernel one workgroup per digit scans that digit's count
-//                           over the tiles and records the digit total (no
-//                           cross-workgroup waits);
+//   2. radix_colscan_kernel one workgroup per 4 digits scans those digits'
+//                           counts over the tiles and records the digit
+//                           totals (no cross-workgroup waits);
 //   3. radix_scatter_kernel ranks every key stably inside its tile (wave64
 //                           match ballots, order wave, item, lane), reorders
 //                           the tile by digit in LDS, and writes each digit
@@ -110,29 +110,50 @@ __global__ void __launch_bounds__(kSortThreads)
     hist[(int64_t)blockIdx.x * kRadix + d] = tot;
 }
 
-// One workgroup per digit: exclusive prefix of that digit's count over the
-// tiles (prefix[tile * 256 + d]) and the digit's total.
+// kColDigits consecutive digits per workgroup: exclusive prefix of each
+// digit's count over the tiles (prefix[tile * 256 + d]) and the digit's
+// total.  A thread reads the digits' counts of one tile as one 16-byte load
+// (the tile-major rows are 1 KiB), so the workgroups touch every row line
+// once per kColDigits digits instead of once per digit.
+constexpr int kColDigits = 4;
+
 __global__ void __launch_bounds__(kSortThreads)
     radix_colscan_kernel(const uint32_t *__restrict__ hist, int64_t n_tiles,
                          uint32_t *__restrict__ prefix,
                          uint32_t *__restrict__ totals) {
     __shared__ uint32_t s_wave[kSortWaves];
-    const int d = blockIdx.x;
+    const int d0 = blockIdx.x * kColDigits;
     const int64_t per = ceil_div(n_tiles, kSortThreads);
     const int64_t t0 = (int64_t)threadIdx.x * per;
     const int64_t t1 = t0 + per < n_tiles ? t0 + per : n_tiles;
-    uint32_t sum = 0;
-    for (int64_t t = t0; t < t1; ++t)
-        sum += hist[t * kRadix + d];
-    uint32_t total;
-    uint32_t run = block_exclusive_u32(sum, s_wave, &total);
+    uint32_t sum[kColDigits] = {0u, 0u, 0u, 0u};
+#pragma unroll 8
     for (int64_t t = t0; t < t1; ++t) {
-        const uint32_t c = hist[t * kRadix + d];
-        prefix[t * kRadix + d] = run;
-        run += c;
+        const uint4 c = *reinterpret_cast<const uint4 *>(hist + t * kRadix + d0);
+        sum[0] += c.x;
+        sum[1] += c.y;
+        sum[2] += c.z;
+        sum[3] += c.w;
     }
-    if (threadIdx.x == 0)
-        totals[d] = total;
+    uint32_t run[kColDigits];
+#pragma unroll
+    for (int k = 0; k < kColDigits; ++k) {
+        uint32_t total;
+        run[k] = block_exclusive_u32(sum[k], s_wave, &total);
+        if (threadIdx.x == 0)
+            totals[d0 + k] = total;
+        __syncthreads();  // s_wave is reused by the next digit's scan
+    }
+#pragma unroll 8
+    for (int64_t t = t0; t < t1; ++t) {
+        const uint4 c = *reinterpret_cast<const uint4 *>(hist + t * kRadix + d0);
+        *reinterpret_cast<uint4 *>(prefix + t * kRadix + d0) =
+            make_uint4(run[0], run[1], run[2], run[3]);
+        run[0] += c.x;
+        run[1] += c.y;
+        run[2] += c.z;
+        run[3] += c.w;
+    }
 }
 
 // Stable scatter of one tile: ranks come from wave64 match ballots
@@ -362,8 +383,8 @@ int radix_sort_ping_pong(int64_t n, int begin_bit, int end_bit, uint64_t *keys_a
             radix_hist_kernel<kSortItemsLarge><<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
                 ksrc, n, shift, bits, hist);
         GS_TRY(check_launch("radix_hist_kernel"));
-        radix_colscan_kernel<<<kRadix, kSortThreads, 0, st>>>(hist, L.n_tiles,
-                                                              prefix, totals);
+        radix_colscan_kernel<<<kRadix / kColDigits, kSortThreads, 0, st>>>(
+            hist, L.n_tiles, prefix, totals);
         GS_TRY(check_launch("radix_colscan_kernel"));
         if (small)
             radix_scatter_kernel<kSortItemsSmall><<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
