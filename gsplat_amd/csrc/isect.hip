@@ -467,7 +467,7 @@ __global__ void __launch_bounds__(kIsectThreads)
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(kIsectThreads)
     isect_count_keys_kernel(const IsectArgs a, int32_t *__restrict__ tiles_per_gauss,
-                            uint64_t *__restrict__ depth_keys,
+                            uint32_t *__restrict__ depth_keys,
                             uint32_t *__restrict__ rows,
                             RowRec *__restrict__ recs) {
     const int64_t idx = (int64_t)blockIdx.x * kIsectThreads + threadIdx.x;
@@ -478,7 +478,7 @@ __global__ void __launch_bounds__(kIsectThreads)
     Sweep sw;
     tiles_per_gauss[idx] =
         sweep_setup_rec(a, rec, &sw) ? sweep_tiles<false>(a, sw, nullptr) : 0;
-    depth_keys[idx] = (uint64_t)__float_as_uint(rec.q.z);
+    depth_keys[idx] = __float_as_uint(rec.q.z);
     rows[idx] = (uint32_t)idx;
 }
 
@@ -587,11 +587,11 @@ __global__ void __launch_bounds__(kIsectThreads)
                             const int64_t *__restrict__ dstart,
                             const RowRec *__restrict__ recs,
                             const int32_t *__restrict__ chunk_first,
-                            int64_t n_isects, uint64_t *__restrict__ isect_ids,
+                            int64_t n_isects, uint32_t *__restrict__ isect_keys,
                             uint32_t *__restrict__ flatten_ids) {
     __shared__ float s_f[kEmitWaves][kRowFloats][kWave];
     __shared__ int32_t s_i[kEmitWaves][kRowInts][kWave];
-    __shared__ uint64_t s_key[kEmitWaves][kWave];
+    __shared__ uint32_t s_key[kEmitWaves][kWave];
     __shared__ int32_t s_colpre[kEmitWaves][kWave + 1];
     __shared__ int32_t s_first[kEmitWaves][kEmitCols];
     __shared__ int32_t s_meta[kEmitWaves][kEmitCols];
@@ -645,9 +645,7 @@ __global__ void __launch_bounds__(kIsectThreads)
                 q[kRowJ * kWave] = sw.accu ? sweep_last_line(sw) : 0;
                 q[kRowFlags * kWave] = (sw.accu ? 1 : 0) | (sw.isY ? 2 : 0);
                 q[kRowFlat * kWave] = (int32_t)row;
-                const uint64_t iid = (uint32_t)__float_as_int(rec.q.w);
-                s_key[wave][lane] = (iid << (32 + a.tile_n_bits)) |
-                                    (uint64_t)__float_as_uint(rec.q.z);
+                s_key[wave][lane] = (uint32_t)__float_as_int(rec.q.w) << a.tile_n_bits;
             }
         }
         const int ncols = has ? sw.rmax_x - sw.rmin_x : 0;
@@ -763,7 +761,7 @@ __global__ void __launch_bounds__(kIsectThreads)
                     const uint32_t tile =
                         (uint32_t)s_first[wave][sk] +
                         (uint32_t)off * ((meta & 0x100) ? 1u : (uint32_t)tw);
-                    isect_ids[slot] = s_key[wave][r] | ((uint64_t)tile << 32);
+                    isect_keys[slot] = s_key[wave][r] | tile;
                     flatten_ids[slot] = (uint32_t)s_i[wave][kRowFlat][r];
                 }
             }
@@ -777,29 +775,35 @@ struct PrepLayout {
     size_t keys_a, keys_b, vals_b, lookback, sort_ws, total;
 };
 
+// Depth keys are the float bits of positive depths (every row with tiles
+// has depth > near_plane > 0), so bit 31 never orders two such rows.
+constexpr int kDepthKeyBits = 31;
+
 inline size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
 PrepLayout prep_layout(int64_t n) {
     PrepLayout L;
-    const size_t k = align256((size_t)n * 8), v = align256((size_t)n * 4);
+    const size_t v = align256((size_t)n * 4);
     L.keys_a = 0;
-    L.keys_b = k;
-    L.vals_b = 2 * k;
-    L.lookback = 2 * k + v;
+    L.keys_b = v;
+    L.vals_b = 2 * v;
+    L.lookback = 3 * v;
     L.sort_ws = L.lookback + align256(lookback_bytes(ceil_div(n, kScanBlockRows)));
     L.total = L.sort_ws + radix_sort_workspace_bytes(n);
     return L;
 }
 
 struct EmitLayout {
-    size_t keys, vals, chunks, sort_ws, total;
+    size_t keys_a, keys_b, vals, chunks, sort_ws, total;
 };
 
 EmitLayout emit_layout(int64_t n_isects) {
     EmitLayout L;
-    L.keys = 0;
-    L.vals = align256((size_t)n_isects * 8);
-    L.chunks = L.vals + align256((size_t)n_isects * 4);
+    const size_t v = align256((size_t)n_isects * 4);
+    L.keys_a = 0;
+    L.keys_b = v;
+    L.vals = 2 * v;
+    L.chunks = 3 * v;
     L.sort_ws = L.chunks + align256((size_t)ceil_div(n_isects, kEmitSlots) * 4);
     L.total = L.sort_ws + radix_sort_workspace_bytes(n_isects);
     return L;
@@ -993,8 +997,8 @@ extern "C" int gsplat_isect_prepare(int64_t n, int64_t N, const int64_t *image_i
     GS_REQUIRE(workspace && workspace_bytes >= L.total,
                "isect_prepare: workspace too small");
     char *ws = reinterpret_cast<char *>(workspace);
-    uint64_t *keys_a = reinterpret_cast<uint64_t *>(ws + L.keys_a);
-    uint64_t *keys_b = reinterpret_cast<uint64_t *>(ws + L.keys_b);
+    uint32_t *keys_a = reinterpret_cast<uint32_t *>(ws + L.keys_a);
+    uint32_t *keys_b = reinterpret_cast<uint32_t *>(ws + L.keys_b);
     uint32_t *vals_a = reinterpret_cast<uint32_t *>(depth_order);
     uint32_t *vals_b = reinterpret_cast<uint32_t *>(ws + L.vals_b);
     hipStream_t st = as_stream(stream);
@@ -1003,9 +1007,9 @@ extern "C" int gsplat_isect_prepare(int64_t n, int64_t N, const int64_t *image_i
         a, tiles_per_gauss, keys_a, vals_a, reinterpret_cast<RowRec *>(row_records));
     GS_TRY(check_launch("isect_count_keys_kernel"));
     bool in_b = false;
-    GS_TRY(radix_sort_ping_pong(n, 0, 32, keys_a, vals_a, keys_b, vals_b,
-                                ws + L.sort_ws, workspace_bytes - L.sort_ws, st,
-                                &in_b));
+    GS_TRY(radix_sort_u32(n, kDepthKeyBits, keys_a, vals_a, keys_b, vals_b,
+                          ws + L.sort_ws, workspace_bytes - L.sort_ws, st, &in_b,
+                          nullptr, nullptr));
     if (in_b)
         GS_TRY(copy_u32(n, vals_b, vals_a, st));
     const int64_t scan_blocks = ceil_div(n, kScanBlockRows);
@@ -1050,15 +1054,20 @@ extern "C" int gsplat_isect_emit_sorted(
     GS_REQUIRE(workspace && workspace_bytes >= L.total,
                "isect_emit_sorted: workspace too small");
     char *ws = reinterpret_cast<char *>(workspace);
-    uint64_t *tmp_keys = reinterpret_cast<uint64_t *>(ws + L.keys);
+    // The emission writes 32-bit (image | tile) keys in depth order; a
+    // stable sort on those bits alone then gives the reference's order, and
+    // its last pass writes the 64-bit isect ids (key << 32 | depth bits of
+    // the row) and the rows straight into the outputs.
+    const int key_bits = a.tile_n_bits + ib;
+    const int passes = radix_sort_passes(key_bits);
+    uint32_t *ka = reinterpret_cast<uint32_t *>(ws + L.keys_a);
+    uint32_t *kb = reinterpret_cast<uint32_t *>(ws + L.keys_b);
     uint32_t *tmp_vals = reinterpret_cast<uint32_t *>(ws + L.vals);
-    uint64_t *out_keys = reinterpret_cast<uint64_t *>(isect_ids);
     uint32_t *out_vals = reinterpret_cast<uint32_t *>(flatten_ids);
-    // emit where the tile passes will start so that they end in the outputs
-    const int end_bit = 32 + a.tile_n_bits + ib;
-    const bool odd = radix_sort_passes(end_bit - 32) % 2 == 1;
-    uint64_t *ka = odd ? tmp_keys : out_keys, *kb = odd ? out_keys : tmp_keys;
-    uint32_t *va = odd ? tmp_vals : out_vals, *vb = odd ? out_vals : tmp_vals;
+    // the passes alternate a -> b -> a ...: emit into the pair whose
+    // partner (odd pass count) or itself (even) receives the last pass
+    uint32_t *va = passes % 2 == 1 ? tmp_vals : out_vals;
+    uint32_t *vb = passes % 2 == 1 ? out_vals : tmp_vals;
     hipStream_t st = as_stream(stream);
     int32_t *chunk_first = reinterpret_cast<int32_t *>(ws + L.chunks);
     emit_chunk_first_kernel<<<(unsigned)ceil_div(n, kIsectThreads), kIsectThreads,
@@ -1072,11 +1081,10 @@ extern "C" int gsplat_isect_emit_sorted(
         va);
     GS_TRY(check_launch("isect_emit_depth_kernel"));
     bool in_b = false;
-    GS_TRY(radix_sort_ping_pong(n_isects, 32, end_bit, ka, va, kb, vb,
-                                ws + L.sort_ws, workspace_bytes - L.sort_ws, st,
-                                &in_b));
-    if ((in_b ? kb : ka) != out_keys)
-        return copy_pairs(n_isects, in_b ? kb : ka, in_b ? vb : va, out_keys,
-                          out_vals, st);
+    GS_TRY(radix_sort_u32(n_isects, key_bits, ka, va, kb, vb, ws + L.sort_ws,
+                          workspace_bytes - L.sort_ws, st, &in_b,
+                          reinterpret_cast<const uint32_t *>(depths),
+                          reinterpret_cast<uint64_t *>(isect_ids)));
+    GS_REQUIRE((in_b ? vb : va) == out_vals, "isect_emit_sorted: pass parity");
     return GSPLAT_OK;
 }

@@ -68,11 +68,15 @@ __device__ __forceinline__ void alpha_thresholds(float o, float &sig_max,
 
 // Conservative pixel-centre box of {sigma <= sig_max}: for a positive
 // definite conic Q = [[a, b], [b, c]], sigma = 1/2 d^T Q d <= s holds only
-// for |dx| <= sqrt(2 s c / det) and |dy| <= sqrt(2 s a / det).  The extents
-// are widened (x1.001 + 1 px) so float rounding in sigma can never put a
-// composited pixel outside; degenerate conics get an unbounded box and
-// Gaussians that never composite (sig_max < 0 or NaN) an empty one.  Used
-// only to skip work: a pixel outside the box fails the exact test anyway.
+// for |dx| <= sqrt(2 s c / det) and |dy| <= sqrt(2 s a / det).  The float
+// sigma of gauss_sigma can undershoot the exact one by a few ulp of
+// 1/2 (a dx^2 + c dy^2) + |b dx dy|, which is at most 4 ac/det times sigma,
+// and det = ac - b^2 itself carries a relative error of order eps ac/det; the
+// extents are therefore widened by (1 + 1e-3 + 1e-6 ac/det), more than 4x
+// the worst of both, plus 1 px, so rounding can never put a composited pixel
+// outside.  Degenerate conics get an unbounded box and Gaussians that never
+// composite (sig_max < 0 or NaN) an empty one.  Used only to skip work: a
+// pixel outside the box fails the exact test anyway.
 __device__ __forceinline__ float4 alpha_support_box(float mx, float my, float a,
                                                     float b, float c,
                                                     float sig_max) {
@@ -80,13 +84,53 @@ __device__ __forceinline__ float4 alpha_support_box(float mx, float my, float a,
         return make_float4(__builtin_inff(), __builtin_inff(),
                            -__builtin_inff(), -__builtin_inff());
     const float det = a * c - b * b;
-    const float ex = sqrtf(2.f * sig_max * c / det) * 1.001f + 1.f;
-    const float ey = sqrtf(2.f * sig_max * a / det) * 1.001f + 1.f;
+    const float widen = 1.001f + 1e-6f * (a * c / det);
+    const float ex = sqrtf(2.f * sig_max * c / det) * widen + 1.f;
+    const float ey = sqrtf(2.f * sig_max * a / det) * widen + 1.f;
     if (!(det > 0.f) || !(a > 0.f) || !(c > 0.f) || !(ex < 1e30f) ||
         !(ey < 1e30f))
         return make_float4(-__builtin_inff(), -__builtin_inff(),
                            __builtin_inff(), __builtin_inff());
     return make_float4(mx - ex, my - ey, mx + ex, my + ey);  // x0, y0, x1, y1
+}
+
+// Bit w set when the box reaches a pixel centre of wave w's strip of tile
+// (tx, ty): the strips are WROWS whole tile rows each, NW of them.
+template <int TILE, int NW, int WROWS>
+__device__ __forceinline__ uint32_t strip_mask(float4 box, int32_t tx,
+                                               int32_t ty) {
+    static_assert(NW <= 8, "strip masks are kept in 8 bits");
+    const float cx0 = (float)(tx * TILE) + 0.5f;
+    const float cx1 = cx0 + (float)(TILE - 1);
+    uint32_t m = 0;
+    if (box.x <= cx1 && box.z >= cx0) {
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const float cy0 = (float)(ty * TILE + w * WROWS) + 0.5f;
+            const float cy1 = cy0 + (float)(WROWS - 1);
+            if (box.y <= cy1 && box.w >= cy0)
+                m |= 1u << w;
+        }
+    }
+    return m;
+}
+
+// Appends, in slot order, the slots s < n whose strip mask holds this wave's
+// bit to list; returns the count (uniform over the wave).
+template <typename SlotT>
+__device__ __forceinline__ int wave_work_list(const uint8_t *wmask, int t0,
+                                              int n, int wave, SlotT *list) {
+    int n_work = 0;
+    for (int c0 = 0; c0 < n; c0 += kWave) {
+        const int slot = c0 + (int)lane_id();
+        const bool take = slot < n && slot >= t0 && ((wmask[slot] >> wave) & 1u);
+        const uint64_t bal = __ballot(take);
+        if (take)
+            list[n_work + __popcll(bal & lanemask_lt())] = (SlotT)slot;
+        n_work += __popcll(bal);
+    }
+    __builtin_amdgcn_wave_barrier();
+    return n_work;
 }
 
 __device__ __forceinline__ void tile_coords(const RasterArgs &a, int64_t gid,
@@ -113,9 +157,13 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
     float *__restrict__ render_alphas, int32_t *__restrict__ last_ids,
     float *__restrict__ render_T) {
     constexpr int BS = TileShape<TILE>::BS;
+    constexpr int NW = (BS + kWave - 1) / kWave;       // waves per tile
+    constexpr int WROWS = (kWave < BS ? kWave : BS) / TILE;  // rows per wave
     __shared__ float4 s_geo[BS];          // (x, y, opacity, sig_max)
     __shared__ float4 s_con[BS];          // (a, b, c, sig_clamp)
     __shared__ float s_col[BS * CDIM];
+    __shared__ uint8_t s_wmask[BS];       // waves a Gaussian can reach
+    __shared__ uint8_t s_list[NW][BS];    // per-wave work list
 
     int64_t image;
     int32_t tile, ty, tx;
@@ -168,20 +216,28 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
             const float o = a.opacities[g];
             float sig_max, sig_clamp;
             alpha_thresholds(o, sig_max, sig_clamp);
+            const float ca = a.conics[g * 3 + 0], cb = a.conics[g * 3 + 1],
+                        cc = a.conics[g * 3 + 2];
             s_geo[tr] = make_float4(xy.x, xy.y, o, sig_max);
-            s_con[tr] = make_float4(a.conics[g * 3 + 0], a.conics[g * 3 + 1],
-                                    a.conics[g * 3 + 2], sig_clamp);
+            s_con[tr] = make_float4(ca, cb, cc, sig_clamp);
 #pragma unroll
             for (int k = 0; k < CDIM; ++k)
                 s_col[tr * CDIM + k] = a.colors[(int64_t)g * CDIM + k];
+            s_wmask[tr] = (uint8_t)strip_mask<TILE, NW, WROWS>(
+                alpha_support_box(xy.x, xy.y, ca, cb, cc, sig_max), tx, ty);
         }
         __syncthreads();
         const int batch_size = min(BS, range_end - batch_start);
+        // the staged Gaussians whose alpha support reaches this wave's strip
+        // (no other can composite on its pixels), in depth order
+        const int wave = tr / kWave;
+        const int n_work = wave_work_list(s_wmask, 0, batch_size, wave, s_list[wave]);
         // wave-uniform loop; a lane that is done (or skips a Gaussian) is
         // carried by selects, not branches
-        for (int t = 0; t < batch_size; ++t) {
+        for (int n = 0; n < n_work; ++n) {
             if (!__ballot(!done))
                 break;
+            const int t = s_list[wave][n];
             const float4 geo = s_geo[t];
             const float4 con = s_con[t];
             const float dx = geo.x - px, dy = geo.y - py;
@@ -371,21 +427,9 @@ __device__ __forceinline__ void rasterize_bwd_tile(
                     s_col[slot * CDIM + k] = a.colors[(int64_t)g * CDIM + k];
                 // which waves' pixel strips the Gaussian's alpha support can
                 // reach (wave w holds rows w * WROWS .. of the tile)
-                const float4 box = alpha_support_box(xy.x, xy.y, ca, cb, cc, sig_max);
-                const float cx0 = (float)(tx * TILE) + 0.5f;
-                const float cx1 = cx0 + (float)(TILE - 1);
-                uint32_t m = 0;
-                if (box.x <= cx1 && box.z >= cx0) {
-#pragma unroll
-                    for (int w = 0; w < NW; ++w) {
-                        constexpr int WROWS = (kWave < NT ? kWave : NT) * PX / TILE;
-                        const float cy0 = (float)(ty * TILE + w * WROWS) + 0.5f;
-                        const float cy1 = cy0 + (float)(WROWS - 1);
-                        if (box.y <= cy1 && box.w >= cy0)
-                            m |= 1u << w;
-                    }
-                }
-                s_wmask[slot] = (uint8_t)m;
+                constexpr int WROWS = (kWave < NT ? kWave : NT) * PX / TILE;
+                s_wmask[slot] = (uint8_t)strip_mask<TILE, NW, WROWS>(
+                    alpha_support_box(xy.x, xy.y, ca, cb, cc, sig_max), tx, ty);
             } else {
                 s_wmask[slot] = 0;
             }
@@ -401,17 +445,7 @@ __device__ __forceinline__ void rasterize_bwd_tile(
         // wave_bin_final are behind every pixel of the wave) whose alpha
         // support reaches the wave's pixels
         const int t0 = max(0, batch_end - wave_bin_final);
-        int n_work = 0;
-        for (int c0 = 0; c0 < batch_size; c0 += kWave) {
-            const int slot = c0 + (int)lane_id();
-            const bool take = slot < batch_size && slot >= t0 &&
-                              ((s_wmask[slot] >> wave) & 1u);
-            const uint64_t bal = __ballot(take);
-            if (take)
-                s_list[wave][n_work + __popcll(bal & lanemask_lt())] = (uint16_t)slot;
-            n_work += __popcll(bal);
-        }
-        __builtin_amdgcn_wave_barrier();
+        const int n_work = wave_work_list(s_wmask, t0, batch_size, wave, s_list[wave]);
         for (int n = 0; n < n_work; ++n) {
             const int t = s_list[wave][n];
             const int32_t isect = batch_end - t;

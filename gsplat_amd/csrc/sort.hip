@@ -1,12 +1,13 @@
-// Stable LSD radix sort of (uint64 key, uint32 value) pairs and a device-wide
-// exclusive scan, both hand-written for wave64.
+// Stable LSD radix sort of (uint64 or uint32 key, uint32 value) pairs and a
+// device-wide exclusive scan, both hand-written for wave64.
 //
 // Replaces cub::DeviceRadixSort::SortPairs as used by radix_sort_double_buffer
 // (gsplat/cuda/csrc/IntersectTile.cu:478-520): keys are sorted on a bit range,
 // ties keep their input order.
 //
-// Per pass (digit of up to 8 bits, 1024-key tiles up to 2M keys, 2048-key
-// tiles above):
+// Per pass (digit of up to 8 bits, 1024-key tiles up to 2M keys, 4096-key
+// tiles above, so that a large sort's scatter fits one round of resident
+// workgroups):
 //   1. radix_hist_kernel    digit counts per tile with LDS atomics, written
 //                           tile-major (coalesced);
 //   2. radix_colscan_kernel one workgroup per 4 digits scans those digits'
@@ -17,6 +18,10 @@
 //                           the tile by digit in LDS, and writes each digit
 //                           run with consecutive threads on consecutive
 //                           addresses.
+// Three launches per digit, and no single-pass (decoupled look-back) sort:
+// on this GPU a look-back step is a cross-XCD round trip and a workgroup
+// ticket a serialized device atomic, which cost more at these sizes than the
+// two extra launch boundaries.
 // radix_sort_ping_pong alternates between two buffer pairs and reports which
 // one holds the result, so callers that fill the first pair themselves can
 // choose it to make the result land where they want it.
@@ -30,7 +35,7 @@ constexpr int kSortWaves = kSortThreads / kWave;
 // Keys per thread of a tile: short tiles (more workgroups, shorter serial
 // ranking chains) for small sorts, longer ones for large sorts.
 constexpr int kSortItemsSmall = 4;   // 1024-key tiles
-constexpr int kSortItemsLarge = 8;   // 2048-key tiles
+constexpr int kSortItemsLarge = 16;  // 4096-key tiles
 constexpr int64_t kSortSmallMax = 1ll << 21;
 inline int sort_items(int64_t n) {
     return n <= kSortSmallMax ? kSortItemsSmall : kSortItemsLarge;
@@ -52,6 +57,36 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d, int bits,
         peers &= bit ? m : ~m;
     }
     return peers;
+}
+
+// Stable ranks of a wave's span of ITEMS * 64 keys (key j of a lane at
+// base + 64 j + lane; order item, lane = input order): rank[j] is the number
+// of earlier keys of the span with the same digit plus cnt[digit] on entry,
+// and cnt[d] is advanced by the span's count of digit d.  Keys at or past n
+// are ignored.
+template <int ITEMS, typename K>
+__device__ __forceinline__ void rank_wave_span(const K (&k)[ITEMS], int64_t base,
+                                               int64_t n, int shift, int bits,
+                                               uint32_t *cnt,
+                                               uint32_t (&rank)[ITEMS]) {
+    const uint32_t mask = (1u << bits) - 1u;
+    const uint32_t lane = lane_id();
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+        const int64_t i = base + (int64_t)j * kWave + lane;
+        const bool valid = i < n;
+        const uint32_t d = (uint32_t)(k[j] >> shift) & mask;
+        const uint64_t vmask = __ballot(valid);
+        const uint64_t peers = match_digit(d, bits, vmask);
+        uint32_t r = 0;
+        if (valid)
+            r = cnt[d] + (uint32_t)__popcll(peers & lanemask_lt());
+        rank[j] = r;
+        __builtin_amdgcn_wave_barrier();
+        if (valid && (peers & lanemask_lt()) == 0)
+            cnt[d] += (uint32_t)__popcll(peers);
+        __builtin_amdgcn_wave_barrier();
+    }
 }
 
 // Exclusive prefix over the kSortThreads values v of the workgroup (one per
@@ -76,9 +111,9 @@ __device__ __forceinline__ uint32_t block_exclusive_u32(uint32_t v,
 }
 
 // Digit counts of one tile, block-major: hist[tile * 256 + d].
-template <int ITEMS>
+template <int ITEMS, typename K>
 __global__ void __launch_bounds__(kSortThreads)
-    radix_hist_kernel(const uint64_t *__restrict__ keys, int64_t n, int shift,
+    radix_hist_kernel(const K *__restrict__ keys, int64_t n, int shift,
                       int bits, uint32_t *__restrict__ hist) {
     constexpr int kSortItems = ITEMS;
     constexpr int kSortTile = kSortThreads * ITEMS;
@@ -89,11 +124,11 @@ __global__ void __launch_bounds__(kSortThreads)
     __syncthreads();
     const int w = threadIdx.x / kWave;
     const int64_t base = (int64_t)blockIdx.x * kSortTile + (int64_t)w * kWave * kSortItems;
-    uint64_t kk[kSortItems];
+    K kk[kSortItems];
 #pragma unroll
     for (int j = 0; j < kSortItems; ++j) {
         const int64_t i = base + (int64_t)j * kWave + lane_id();
-        kk[j] = i < n ? keys[i] : 0ull;
+        kk[j] = i < n ? keys[i] : (K)0;
     }
 #pragma unroll
     for (int j = 0; j < kSortItems; ++j) {
@@ -117,6 +152,10 @@ __global__ void __launch_bounds__(kSortThreads)
 // once per kColDigits digits instead of once per digit.
 constexpr int kColDigits = 4;
 
+// The counts of up to kColCache tiles per thread stay in registers between
+// the summing and the writing loop (one memory round trip instead of two).
+constexpr int kColCache = 8;
+
 __global__ void __launch_bounds__(kSortThreads)
     radix_colscan_kernel(const uint32_t *__restrict__ hist, int64_t n_tiles,
                          uint32_t *__restrict__ prefix,
@@ -126,9 +165,21 @@ __global__ void __launch_bounds__(kSortThreads)
     const int64_t per = ceil_div(n_tiles, kSortThreads);
     const int64_t t0 = (int64_t)threadIdx.x * per;
     const int64_t t1 = t0 + per < n_tiles ? t0 + per : n_tiles;
+    uint4 cache[kColCache];
+#pragma unroll
+    for (int j = 0; j < kColCache; ++j)
+        cache[j] = t0 + j < t1
+                       ? *reinterpret_cast<const uint4 *>(hist + (t0 + j) * kRadix + d0)
+                       : make_uint4(0u, 0u, 0u, 0u);
     uint32_t sum[kColDigits] = {0u, 0u, 0u, 0u};
-#pragma unroll 8
-    for (int64_t t = t0; t < t1; ++t) {
+#pragma unroll
+    for (int j = 0; j < kColCache; ++j) {
+        sum[0] += cache[j].x;
+        sum[1] += cache[j].y;
+        sum[2] += cache[j].z;
+        sum[3] += cache[j].w;
+    }
+    for (int64_t t = t0 + kColCache; t < t1; ++t) {
         const uint4 c = *reinterpret_cast<const uint4 *>(hist + t * kRadix + d0);
         sum[0] += c.x;
         sum[1] += c.y;
@@ -144,8 +195,18 @@ __global__ void __launch_bounds__(kSortThreads)
             totals[d0 + k] = total;
         __syncthreads();  // s_wave is reused by the next digit's scan
     }
-#pragma unroll 8
-    for (int64_t t = t0; t < t1; ++t) {
+#pragma unroll
+    for (int j = 0; j < kColCache; ++j) {
+        if (t0 + j < t1) {
+            *reinterpret_cast<uint4 *>(prefix + (t0 + j) * kRadix + d0) =
+                make_uint4(run[0], run[1], run[2], run[3]);
+            run[0] += cache[j].x;
+            run[1] += cache[j].y;
+            run[2] += cache[j].z;
+            run[3] += cache[j].w;
+        }
+    }
+    for (int64_t t = t0 + kColCache; t < t1; ++t) {
         const uint4 c = *reinterpret_cast<const uint4 *>(hist + t * kRadix + d0);
         *reinterpret_cast<uint4 *>(prefix + t * kRadix + d0) =
             make_uint4(run[0], run[1], run[2], run[3]);
@@ -159,18 +220,21 @@ __global__ void __launch_bounds__(kSortThreads)
 // Stable scatter of one tile: ranks come from wave64 match ballots
 // (order: wave, item, lane = input order), the tile is reordered by digit in
 // LDS, then every digit run is written out with consecutive threads on
-// consecutive addresses.
-template <int ITEMS>
+// consecutive addresses.  With keys64_out (32-bit keys only) the keys are
+// written there as (key << 32 | low_bits[value]) instead of to keys_out.
+template <int ITEMS, typename K>
 __global__ void __launch_bounds__(kSortThreads)
-    radix_scatter_kernel(const uint64_t *__restrict__ keys_in,
+    radix_scatter_kernel(const K *__restrict__ keys_in,
                          const uint32_t *__restrict__ vals_in,
-                         uint64_t *__restrict__ keys_out,
+                         K *__restrict__ keys_out,
                          uint32_t *__restrict__ vals_out, int64_t n, int shift,
                          int bits, const uint32_t *__restrict__ prefix,
-                         const uint32_t *__restrict__ totals) {
+                         const uint32_t *__restrict__ totals,
+                         const uint32_t *__restrict__ low_bits,
+                         uint64_t *__restrict__ keys64_out) {
     constexpr int kSortItems = ITEMS;
     constexpr int kSortTile = kSortThreads * ITEMS;
-    __shared__ uint64_t s_keys[kSortTile];
+    __shared__ K s_keys[kSortTile];
     __shared__ uint32_t s_vals[kSortTile];
     __shared__ uint32_t s_cnt[kSortWaves][kRadix];
     __shared__ uint32_t s_lstart[kRadix];  // digit start inside the tile
@@ -180,45 +244,33 @@ __global__ void __launch_bounds__(kSortThreads)
     const int tid = threadIdx.x;
     const int64_t tile_base = (int64_t)blockIdx.x * kSortTile;
 
-    // global start of every digit for this tile: digit base + tile prefix
-    {
-        uint32_t total;
-        const uint32_t base = block_exclusive_u32(totals[tid], s_wave, &total);
-        s_gstart[tid] = base + prefix[(int64_t)blockIdx.x * kRadix + tid];
-    }
-    for (int i = tid; i < kSortWaves * kRadix; i += kSortThreads)
-        (&s_cnt[0][0])[i] = 0u;
-    __syncthreads();
-
+    // the tile's keys first, so their round trip overlaps the one of the
+    // digit totals and prefixes below
     const int w = tid / kWave;
     const uint32_t lane = lane_id();
     const int64_t base = tile_base + (int64_t)w * kWave * kSortItems;
-    uint64_t k[kSortItems];
+    K k[kSortItems];
     uint32_t v[kSortItems];
     uint32_t rank[kSortItems];
 #pragma unroll
     for (int j = 0; j < kSortItems; ++j) {
         const int64_t i = base + (int64_t)j * kWave + lane;
         const bool valid = i < n;
-        k[j] = valid ? keys_in[i] : ~0ull;
+        k[j] = valid ? keys_in[i] : ~(K)0;
         v[j] = valid ? vals_in[i] : 0u;
     }
-#pragma unroll
-    for (int j = 0; j < kSortItems; ++j) {
-        const int64_t i = base + (int64_t)j * kWave + lane;
-        const bool valid = i < n;
-        const uint32_t d = (uint32_t)(k[j] >> shift) & mask;
-        const uint64_t vmask = __ballot(valid);
-        const uint64_t peers = match_digit(d, bits, vmask);
-        uint32_t r = 0;
-        if (valid)
-            r = s_cnt[w][d] + (uint32_t)__popcll(peers & lanemask_lt());
-        rank[j] = r;
-        __builtin_amdgcn_wave_barrier();
-        if (valid && (peers & lanemask_lt()) == 0)
-            s_cnt[w][d] += (uint32_t)__popcll(peers);
-        __builtin_amdgcn_wave_barrier();
+    // global start of every digit for this tile: digit base + tile prefix
+    {
+        const uint32_t tile_prefix = prefix[(int64_t)blockIdx.x * kRadix + tid];
+        uint32_t total;
+        const uint32_t dbase = block_exclusive_u32(totals[tid], s_wave, &total);
+        s_gstart[tid] = dbase + tile_prefix;
     }
+    for (int i = tid; i < kSortWaves * kRadix; i += kSortThreads)
+        (&s_cnt[0][0])[i] = 0u;
+    __syncthreads();
+
+    rank_wave_span<ITEMS>(k, base, n, shift, bits, s_cnt[w], rank);
     __syncthreads();
     // digit starts inside the tile, and each wave's start within its digit
     {
@@ -253,12 +305,25 @@ __global__ void __launch_bounds__(kSortThreads)
     __syncthreads();
     const int64_t rem = n - tile_base;
     const int count = rem < kSortTile ? (int)rem : kSortTile;
-    for (int i = tid; i < count; i += kSortThreads) {
-        const uint64_t key = s_keys[i];
-        const uint32_t d = (uint32_t)(key >> shift) & mask;
-        const uint64_t g = (uint64_t)s_gstart[d] + (uint32_t)(i - s_lstart[d]);
-        keys_out[g] = key;
-        vals_out[g] = s_vals[i];
+    // unrolled so that a thread's gathers of low bits are in flight together
+#pragma unroll
+    for (int j = 0; j < kSortItems; ++j) {
+        const int i = tid + j * kSortThreads;
+        if (i < count) {
+            const K key = s_keys[i];
+            const uint32_t val = s_vals[i];
+            const uint32_t d = (uint32_t)(key >> shift) & mask;
+            const uint64_t g = (uint64_t)s_gstart[d] + (uint32_t)(i - s_lstart[d]);
+            if constexpr (sizeof(K) == 4) {
+                if (keys64_out != nullptr)
+                    keys64_out[g] = ((uint64_t)key << 32) | low_bits[val];
+                else
+                    keys_out[g] = key;
+            } else {
+                keys_out[g] = key;
+            }
+            vals_out[g] = val;
+        }
     }
 }
 
@@ -325,6 +390,7 @@ __global__ void copy_u32_kernel(const uint32_t *__restrict__ src,
         dst[i] = src[i];
 }
 
+
 struct SortLayout {
     int64_t n_tiles;
     size_t hist_off, prefix_off, totals_off, total;
@@ -352,10 +418,11 @@ int radix_sort_passes(int num_bits) {
 
 size_t radix_sort_workspace_bytes(int64_t n) { return sort_layout(n).total; }
 
-int radix_sort_ping_pong(int64_t n, int begin_bit, int end_bit, uint64_t *keys_a,
-                         uint32_t *vals_a, uint64_t *keys_b, uint32_t *vals_b,
-                         void *workspace, size_t workspace_bytes,
-                         hipStream_t st, bool *result_in_b) {
+template <typename K>
+int radix_sort_impl(int64_t n, int begin_bit, int end_bit, K *keys_a,
+                    uint32_t *vals_a, K *keys_b, uint32_t *vals_b, void *workspace,
+                    size_t workspace_bytes, hipStream_t st, bool *result_in_b,
+                    const uint32_t *low_bits, uint64_t *keys64_out) {
     *result_in_b = false;
     const int num_bits = end_bit - begin_bit;
     if (n == 0 || num_bits <= 0)
@@ -370,35 +437,57 @@ int radix_sort_ping_pong(int64_t n, int begin_bit, int end_bit, uint64_t *keys_a
     uint32_t *totals = reinterpret_cast<uint32_t *>(ws + L.totals_off);
     const int passes = radix_sort_passes(num_bits);
     int shift = begin_bit;
-    uint64_t *ksrc = keys_a, *kdst = keys_b;
+    K *ksrc = keys_a, *kdst = keys_b;
     uint32_t *vsrc = vals_a, *vdst = vals_b;
+    const bool small = sort_items(n) == kSortItemsSmall;
     for (int p = 0; p < passes; ++p) {
         const int remaining = end_bit - shift;
         const int bits = (remaining + (passes - p) - 1) / (passes - p);
-        const bool small = sort_items(n) == kSortItemsSmall;
+        uint64_t *k64 = p == passes - 1 ? keys64_out : nullptr;
         if (small)
-            radix_hist_kernel<kSortItemsSmall><<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
+            radix_hist_kernel<kSortItemsSmall, K><<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
                 ksrc, n, shift, bits, hist);
         else
-            radix_hist_kernel<kSortItemsLarge><<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
+            radix_hist_kernel<kSortItemsLarge, K><<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
                 ksrc, n, shift, bits, hist);
         GS_TRY(check_launch("radix_hist_kernel"));
         radix_colscan_kernel<<<kRadix / kColDigits, kSortThreads, 0, st>>>(
             hist, L.n_tiles, prefix, totals);
         GS_TRY(check_launch("radix_colscan_kernel"));
         if (small)
-            radix_scatter_kernel<kSortItemsSmall><<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
-                ksrc, vsrc, kdst, vdst, n, shift, bits, prefix, totals);
+            radix_scatter_kernel<kSortItemsSmall, K><<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
+                ksrc, vsrc, kdst, vdst, n, shift, bits, prefix, totals, low_bits, k64);
         else
-            radix_scatter_kernel<kSortItemsLarge><<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
-                ksrc, vsrc, kdst, vdst, n, shift, bits, prefix, totals);
+            radix_scatter_kernel<kSortItemsLarge, K><<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
+                ksrc, vsrc, kdst, vdst, n, shift, bits, prefix, totals, low_bits, k64);
         GS_TRY(check_launch("radix_scatter_kernel"));
         shift += bits;
-        uint64_t *tk = ksrc; ksrc = kdst; kdst = tk;
+        K *tk = ksrc; ksrc = kdst; kdst = tk;
         uint32_t *tv = vsrc; vsrc = vdst; vdst = tv;
     }
-    *result_in_b = (ksrc == keys_b);
+    *result_in_b = (vsrc == vals_b);
     return GSPLAT_OK;
+}
+
+int radix_sort_ping_pong(int64_t n, int begin_bit, int end_bit, uint64_t *keys_a,
+                         uint32_t *vals_a, uint64_t *keys_b, uint32_t *vals_b,
+                         void *workspace, size_t workspace_bytes,
+                         hipStream_t st, bool *result_in_b) {
+    return radix_sort_impl<uint64_t>(n, begin_bit, end_bit, keys_a, vals_a, keys_b,
+                                     vals_b, workspace, workspace_bytes, st,
+                                     result_in_b, nullptr, nullptr);
+}
+
+int radix_sort_u32(int64_t n, int num_bits, uint32_t *keys_a, uint32_t *vals_a,
+                   uint32_t *keys_b, uint32_t *vals_b, void *workspace,
+                   size_t workspace_bytes, hipStream_t st, bool *result_in_b,
+                   const uint32_t *low_bits, uint64_t *keys64_out) {
+    GS_REQUIRE(num_bits >= 0 && num_bits <= 32, "radix sort: num_bits in [0, 32]");
+    GS_REQUIRE(keys64_out == nullptr || (low_bits != nullptr && num_bits > 0),
+               "radix sort: 64-bit output needs low bits and at least one pass");
+    return radix_sort_impl<uint32_t>(n, 0, num_bits, keys_a, vals_a, keys_b, vals_b,
+                                     workspace, workspace_bytes, st, result_in_b,
+                                     low_bits, keys64_out);
 }
 
 int copy_pairs(int64_t n, const uint64_t *ks, const uint32_t *vs, uint64_t *kd,
