@@ -147,12 +147,14 @@ __device__ __forceinline__ float portable_expf(float x) {
 
 // portable_expf without its range checks, for x that the caller knows to be
 // a non-NaN value <= 0 (the rasterizer's -sigma with 0 <= sigma <= ln(255 o)).
-// x is clamped to -87, so for every x >= -87 the result is bit-identical to
-// portable_expf(x); below -87 it returns e^-87 instead of 0, which can only
-// matter for an opacity above 255 e^87 (beyond the float range).
+// x is clamped to [-87, 0] (one med3), so for every x >= -87 the result is
+// bit-identical to portable_expf(x); below -87 it returns e^-87 instead of
+// 0, which can only matter for an opacity above e^87 / 255 (about 2.4e35).
+// The scaling by 2^k (k in [-126, 0]) is one ldexp, exactly the product
+// p * 2^k that portable_expf forms.
 __device__ __forceinline__ float portable_expf_nonpos(float x) {
 #pragma clang fp contract(off)
-    x = fmaxf(x, -87.f);
+    x = __builtin_amdgcn_fmed3f(x, -87.f, 0.f);
     const float kf = __builtin_rintf(x * 0x1.715476p+0f);
     float r = __builtin_fmaf(-kf, 0x1.63p-1f, x);
     r = __builtin_fmaf(-kf, -0x1.bd0106p-13f, r);
@@ -164,8 +166,7 @@ __device__ __forceinline__ float portable_expf_nonpos(float x) {
     p = __builtin_fmaf(p, r, 0.5f);
     p = __builtin_fmaf(p, r, 1.f);
     p = __builtin_fmaf(p, r, 1.f);
-    const float scale = __int_as_float(((int32_t)kf + 127) << 23);
-    return p * scale;
+    return __builtin_ldexpf(p, (int32_t)kf);
 }
 
 // DPP row operations (gfx9 encodings).

@@ -245,21 +245,23 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
             const bool take = !done && sigma >= 0.f && sigma <= geo.w;
             if (!__ballot(take))
                 continue;
-            if (take) {
-                const float vis = portable_expf_nonpos(-sigma);
-                const float alpha = sigma < con.w ? kMaxAlpha : geo.z * vis;
-                const float next_T = T * (1.f - alpha);
-                const bool stop = next_T <= kTransmittanceThreshold;
-                const float w = alpha * T;
+            // every lane runs the arithmetic (the exp clamps any sigma into
+            // range); lanes that do not take the Gaussian keep their state
+            // through selects
+            const float vis = portable_expf_nonpos(-sigma);
+            const float alpha = sigma < con.w ? kMaxAlpha : geo.z * vis;
+            const float next_T = T * (1.f - alpha);
+            const bool stop = next_T <= kTransmittanceThreshold;
+            const bool upd = take && !stop;
+            const float w = alpha * T;
 #pragma unroll
-                for (int k = 0; k < CDIM; ++k) {
-                    const float c = acc[k] + s_col[t * CDIM + k] * w;
-                    acc[k] = stop ? acc[k] : c;
-                }
-                cur_idx = stop ? cur_idx : batch_start + t;
-                T = stop ? T : next_T;
-                done = stop;
+            for (int k = 0; k < CDIM; ++k) {
+                const float c = acc[k] + s_col[t * CDIM + k] * w;
+                acc[k] = upd ? c : acc[k];
             }
+            cur_idx = upd ? batch_start + t : cur_idx;
+            T = upd ? next_T : T;
+            done = done || (take && stop);
         }
     }
     if (inside) {
@@ -273,6 +275,78 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
         if (render_T != nullptr)
             render_T[pix] = T;
     }
+}
+
+// Transposed row reduction of N values.  Four DPP steps, each pairing every
+// lane with the lane whose in-row index differs in one bit (row_mirror: bit
+// 3, row_half_mirror: bit 2, quad_perm [2,3,0,1]: bit 1, quad_perm [1,0,3,2]:
+// bit 0; in that order every partner agrees with the lane on the bits of the
+// earlier steps): two registers A, B become one, lanes with the bit clear
+// keeping A's sum and lanes with it set B's, so each step halves the
+// registers in flight (3 instructions per pair instead of 2 per value).  A
+// register left unpaired is summed on both sides.  Afterwards register f of
+// lane l (in-row index) holds the 16-lane row sum of value
+// RowReduce<N>::value(f, l).
+template <int N> struct RowReduce {
+    static constexpr int N1 = (N + 1) / 2, N2 = (N1 + 1) / 2;
+    static constexpr int N3 = (N2 + 1) / 2, N4 = (N3 + 1) / 2;
+    // input register of a step's output register r for a lane whose step bit
+    // is `hi`, the step having n inputs
+    static constexpr int src(int r, int n, bool hi) {
+        return (2 * r + 1 < n && hi) ? 2 * r + 1 : 2 * r;
+    }
+    static constexpr int value(int f, int l) {
+        const int r3 = src(f, N3, (l & 1) != 0);
+        const int r2 = src(r3, N2, (l & 2) != 0);
+        const int r1 = src(r2, N1, (l & 4) != 0);
+        return src(r1, N, (l & 8) != 0);
+    }
+    // the first (register, lane) holding a value adds it; later copies skip
+    static constexpr bool owner(int f, int l) {
+        for (int g = 0; g <= f; ++g)
+            for (int m = 0; m < 16; ++m) {
+                if (g == f && m == l)
+                    return true;
+                if (value(g, m) == value(f, l))
+                    return false;
+            }
+        return true;
+    }
+    // value index this lane adds from register f, or -1
+    __device__ static int lane_value(int f, int l) {
+        int v = -1;
+#pragma unroll
+        for (int m = 0; m < 16; ++m)
+            if (m == l)
+                v = owner(f, m) ? value(f, m) : -1;
+        return v;
+    }
+};
+
+template <int CTRL, int N>
+__device__ __forceinline__ void row_reduce_step(const float (&in)[N],
+                                                float (&out)[(N + 1) / 2],
+                                                bool hi) {
+#pragma unroll
+    for (int j = 0; j < N / 2; ++j) {
+        const float send = hi ? in[2 * j] : in[2 * j + 1];
+        const float keep = hi ? in[2 * j + 1] : in[2 * j];
+        out[j] = keep + dpp_f32<CTRL>(send);
+    }
+    if constexpr (N % 2 == 1)
+        out[N / 2] = in[N - 1] + dpp_f32<CTRL>(in[N - 1]);
+}
+
+template <int N>
+__device__ __forceinline__ void row_reduce(const float (&v)[N],
+                                           float (&out)[RowReduce<N>::N4]) {
+    using R = RowReduce<N>;
+    const uint32_t l = lane_id() & 15u;
+    float a[R::N1], b[R::N2], c[R::N3];
+    row_reduce_step<kDppRowMirror>(v, a, (l & 8u) != 0);
+    row_reduce_step<kDppRowHalfMirror>(a, b, (l & 4u) != 0);
+    row_reduce_step<kDppQuadXor2>(b, c, (l & 2u) != 0);
+    row_reduce_step<kDppQuadXor1>(c, out, (l & 1u) != 0);
 }
 
 // Backward launch shape: at 16x16 every thread takes PX = 2 pixels (two
@@ -351,46 +425,51 @@ __device__ __forceinline__ void rasterize_bwd_tile(
         s_tile_bin = -1;
 
     // per-pixel state; pixel p of thread tr is (row PX * (tr / TILE) + p,
-    // column tr % TILE) of the tile
-    bool inside[PX];
-    float px[PX], py[PX], T_final[PX], T[PX], v_a[PX], bg_dot[PX];
+    // column tr % TILE) of the tile, so a thread's pixels share one column
+    // (one dx per Gaussian)
+    const float px = (float)(tx * TILE + tr % TILE) + 0.5f;
+    float py[PX], T[PX], Bv[PX], Kv[PX];
     double T64[PX];
     int32_t bin_final[PX];
-    float v_c[PX][CDIM], buffer[PX][CDIM];
+    float v_c[PX][CDIM];
     int32_t wave_bin = -1;
 #pragma unroll
     for (int p = 0; p < PX; ++p) {
         const int i = ty * TILE + PX * (tr / TILE) + p;
         const int j = tx * TILE + tr % TILE;
-        inside[p] = i < a.H && j < a.W;
-        const int64_t pix = ((int64_t)image * a.H + (inside[p] ? i : 0)) * a.W +
-                            (inside[p] ? j : 0);
-        px[p] = (float)j + 0.5f;
+        const bool inside = i < a.H && j < a.W;
+        const int64_t pix = ((int64_t)image * a.H + (inside ? i : 0)) * a.W +
+                            (inside ? j : 0);
         py[p] = (float)i + 0.5f;
         // The transmittance itself when the forward stored it: 1 - (1 - T)
         // loses most of T's significant bits once T nears the 1e-4 cutoff.
-        T_final[p] = inside[p] ? (render_T != nullptr ? render_T[pix]
-                                                      : 1.f - render_alphas[pix])
-                               : 1.f;
+        const float T_final = inside ? (render_T != nullptr ? render_T[pix]
+                                                            : 1.f - render_alphas[pix])
+                                     : 1.f;
         // T before each Gaussian is recovered back to front by undoing the
         // forward's products.  It is carried in double and each step
         // multiplies by 1 / (1 - alpha) refined to ~2^-46 by one Newton step
         // from the fp32 reciprocal, so T keeps only the forward's own rounding
         // instead of one extra float32 rounding per Gaussian behind it.
-        T64[p] = (double)T_final[p];
-        T[p] = T_final[p];
-        bin_final[p] = inside[p] ? last_ids[pix] : -1;
+        T64[p] = (double)T_final;
+        T[p] = T_final;
+        bin_final[p] = inside ? last_ids[pix] : -1;
         wave_bin = max(wave_bin, bin_final[p]);
-        bg_dot[p] = 0.f;
+        float bg_dot = 0.f;
 #pragma unroll
         for (int k = 0; k < CDIM; ++k) {
-            v_c[p][k] = inside[p] ? v_render_colors[pix * CDIM + k] : 0.f;
-            buffer[p][k] = 0.f;
+            v_c[p][k] = inside ? v_render_colors[pix * CDIM + k] : 0.f;
             if (a.backgrounds)
-                bg_dot[p] += a.backgrounds[image * CDIM + k] * v_c[p][k];
+                bg_dot += a.backgrounds[image * CDIM + k] * v_c[p][k];
         }
-        v_a[p] = (inside[p] && v_render_alphas != nullptr) ? v_render_alphas[pix]
-                                                           : 0.f;
+        const float v_a = (inside && v_render_alphas != nullptr) ? v_render_alphas[pix]
+                                                                 : 0.f;
+        // d loss / d alpha_g = T_g (c_g . v_c) - (B_g - K) / (1 - alpha_g)
+        // with B_g = sum over the Gaussians behind g (already replayed) of
+        // (c . v_c) alpha T, and K = T_final (v_alpha - bg . v_c): the
+        // reference's per-channel colour buffer folded into one running sum.
+        Bv[p] = 0.f;
+        Kv[p] = T_final * (v_a - bg_dot);
     }
     const int32_t wave_bin_final = wave_max_i32(wave_bin);
     // The forward saturates most pixels long before the end of the tile's
@@ -402,6 +481,13 @@ __device__ __forceinline__ void rasterize_bwd_tile(
     __syncthreads();
     const int32_t replay_end = min(range_end, s_tile_bin + 1);
     const int num_batches = max(0, replay_end - range_start + BS - 1) / BS;
+
+    // the tile-sum slot this lane adds from every reduced register
+    using RR = RowReduce<NACC>;
+    int red_slot[RR::N4];
+#pragma unroll
+    for (int f = 0; f < RR::N4; ++f)
+        red_slot[f] = RR::lane_value(f, (int)(lane_id() & 15u));
 
     for (int b = 0; b < num_batches; ++b) {
         __syncthreads();
@@ -436,7 +522,7 @@ __device__ __forceinline__ void rasterize_bwd_tile(
             s_hit[slot] = 0;
 #pragma unroll
             for (int k = 0; k < NACC; ++k)
-                s_acc[k * BS + slot] = 0.f;
+                s_acc[slot * NACC + k] = 0.f;
         }
         __syncthreads();
 
@@ -451,33 +537,38 @@ __device__ __forceinline__ void rasterize_bwd_tile(
             const int32_t isect = batch_end - t;
             const float4 geo = s_geo[t];
             const float4 con = s_con[t];
-            float dx[PX], dy[PX], sigma[PX];
+            const float dx = geo.x - px;
+            float dy[PX], sigma[PX];
             bool valid[PX];
             bool any = false;
 #pragma unroll
             for (int p = 0; p < PX; ++p) {
-                dx[p] = geo.x - px[p];
                 dy[p] = geo.y - py[p];
-                sigma[p] = gauss_sigma(con.x, con.y, con.z, dx[p], dy[p]);
-                valid[p] = inside[p] && isect <= bin_final[p] &&
-                           sigma[p] >= 0.f && sigma[p] <= geo.w;
+                sigma[p] = gauss_sigma(con.x, con.y, con.z, dx, dy[p]);
+                valid[p] = isect <= bin_final[p] && sigma[p] >= 0.f &&
+                           sigma[p] <= geo.w;
                 any |= valid[p];
             }
             if (!__ballot(any))
                 continue;
             // Branch-free over the lane's pixels: an invalid pixel runs the
-            // same arithmetic on sigma = 0 and its contributions are zeroed
-            // through fac and v_sigma, so nothing is carried through
-            // divergent control flow.
-            float g[NACC];
+            // same arithmetic and its contributions are zeroed through
+            // selects (fac, w, T64), so nothing is carried through divergent
+            // control flow.  Per lane it accumulates the sums over its
+            // pixels that the gradient needs:
+            //   V = sum vs, Vy = sum vs dy, Vyy = sum vs dy^2 (vs = dL/dsigma),
+            //   Vo = sum e^-sigma dL/dalpha, colour sums of alpha T v_c.
+            float V = 0.f, Vy = 0.f, Vyy = 0.f, Vo = 0.f, ax = 0.f, ay = 0.f;
+            float cg[CDIM];
 #pragma unroll
-            for (int k = 0; k < NACC; ++k)
-                g[k] = 0.f;
+            for (int k = 0; k < CDIM; ++k)
+                cg[k] = 0.f;
 #pragma unroll
             for (int p = 0; p < PX; ++p) {
-                const float sg = valid[p] ? sigma[p] : 0.f;
-                const float vis = portable_expf_nonpos(-sg);
-                const bool clamped = sg < con.w;
+                // invalid pixels run on their own sigma (the exp clamps it);
+                // every contribution of theirs is selected away below
+                const float vis = portable_expf_nonpos(-sigma[p]);
+                const bool clamped = sigma[p] < con.w;
                 const float alpha = clamped ? kMaxAlpha : geo.z * vis;
                 // alpha <= 0.99, so 1 - alpha >= 0.01 (the reference's 1e-6
                 // floor never binds)
@@ -489,44 +580,53 @@ __device__ __forceinline__ void rasterize_bwd_tile(
                 T64[p] = valid[p] ? T64[p] * r : T64[p];
                 T[p] = (float)T64[p];
                 const float fac = valid[p] ? alpha * T[p] : 0.f;
-                float v_alpha = 0.f;
+                float scv = 0.f;
 #pragma unroll
                 for (int k = 0; k < CDIM; ++k) {
-                    const float ck = s_col[t * CDIM + k];
-                    g[5 + k] += fac * v_c[p][k];
-                    v_alpha += (ck * T[p] - buffer[p][k] * ra) * v_c[p][k];
-                    buffer[p][k] += ck * fac;
+                    scv += s_col[t * CDIM + k] * v_c[p][k];
+                    cg[k] += fac * v_c[p][k];
                 }
-                v_alpha += T_final[p] * ra * v_a[p];
-                if (a.backgrounds)
-                    v_alpha += -T_final[p] * ra * bg_dot[p];
+                const float v_alpha = T[p] * scv - (Bv[p] - Kv[p]) * ra;
+                Bv[p] += fac * scv;
                 // a clamped alpha does not depend on the Gaussian's geometry
                 // or opacity
-                const float vv = (valid[p] && !clamped) ? v_alpha : 0.f;
-                const float v_sigma = -geo.z * vis * vv;
-                const float gx = v_sigma * (con.x * dx[p] + con.y * dy[p]);
-                const float gy = v_sigma * (con.y * dx[p] + con.z * dy[p]);
-                g[0] += gx;
-                g[1] += gy;
-                g[2] += 0.5f * v_sigma * dx[p] * dx[p];
-                g[3] += v_sigma * dx[p] * dy[p];
-                g[4] += 0.5f * v_sigma * dy[p] * dy[p];
-                g[5 + CDIM] += vis * vv;
+                const float w = (valid[p] && !clamped) ? vis * v_alpha : 0.f;
+                Vo += w;
+                const float vs = -geo.z * w;
+                V += vs;
+                const float vy = vs * dy[p];
+                Vy += vy;
+                Vyy += vy * dy[p];
                 if constexpr (ABS) {
-                    g[6 + CDIM] += fabsf(gx);
-                    g[7 + CDIM] += fabsf(gy);
+                    ax += fabsf(vs * (con.x * dx + con.y * dy[p]));
+                    ay += fabsf(vs * (con.y * dx + con.z * dy[p]));
                 }
             }
-            // sum over each 16-lane row (every lane of the row ends with the
-            // row's sum); one lane per row adds it to the tile's LDS sums
+            // the lane's gradient terms: d/dmean = sum vs (Q d), d/dconic =
+            // sum vs (dx^2 / 2, dx dy, dy^2 / 2), with dx shared by the
+            // lane's pixels
+            float gv[NACC];
+            gv[0] = con.x * (dx * V) + con.y * Vy;
+            gv[1] = con.y * (dx * V) + con.z * Vy;
+            gv[2] = 0.5f * (dx * dx) * V;
+            gv[3] = dx * Vy;
+            gv[4] = 0.5f * Vyy;
 #pragma unroll
-            for (int k = 0; k < NACC; ++k)
-                g[k] = row_sum16(g[k]);
-            if ((lane_id() & 15u) == 15u) {
-#pragma unroll
-                for (int k = 0; k < NACC; ++k)
-                    atomicAdd(&s_acc[k * BS + t], g[k]);
+            for (int k = 0; k < CDIM; ++k)
+                gv[5 + k] = cg[k];
+            gv[5 + CDIM] = Vo;
+            if constexpr (ABS) {
+                gv[6 + CDIM] = ax;
+                gv[7 + CDIM] = ay;
             }
+            // sums over each 16-lane row, one value per lane, added to the
+            // tile's LDS sums (rows of a wave add to the same slots)
+            float red[RR::N4];
+            row_reduce<NACC>(gv, red);
+#pragma unroll
+            for (int f = 0; f < RR::N4; ++f)
+                if (red_slot[f] >= 0)
+                    atomicAdd(&s_acc[t * NACC + red_slot[f]], red[f]);
             if (last_lane)
                 s_hit[t] = 1;
         }
@@ -536,21 +636,19 @@ __device__ __forceinline__ void rasterize_bwd_tile(
             const int slot = tr + q * NT;
             if (slot < batch_size && s_hit[slot]) {
                 const int32_t g = s_gid[slot];
-                atomic_add_f32(v_means2d + (int64_t)g * 2 + 0, s_acc[0 * BS + slot]);
-                atomic_add_f32(v_means2d + (int64_t)g * 2 + 1, s_acc[1 * BS + slot]);
-                atomic_add_f32(v_conics + (int64_t)g * 3 + 0, s_acc[2 * BS + slot]);
-                atomic_add_f32(v_conics + (int64_t)g * 3 + 1, s_acc[3 * BS + slot]);
-                atomic_add_f32(v_conics + (int64_t)g * 3 + 2, s_acc[4 * BS + slot]);
+                const float *acc = s_acc + slot * NACC;
+                atomic_add_f32(v_means2d + (int64_t)g * 2 + 0, acc[0]);
+                atomic_add_f32(v_means2d + (int64_t)g * 2 + 1, acc[1]);
+                atomic_add_f32(v_conics + (int64_t)g * 3 + 0, acc[2]);
+                atomic_add_f32(v_conics + (int64_t)g * 3 + 1, acc[3]);
+                atomic_add_f32(v_conics + (int64_t)g * 3 + 2, acc[4]);
 #pragma unroll
                 for (int k = 0; k < CDIM; ++k)
-                    atomic_add_f32(v_colors + (int64_t)g * CDIM + k,
-                                   s_acc[(5 + k) * BS + slot]);
-                atomic_add_f32(v_opacities + g, s_acc[(5 + CDIM) * BS + slot]);
+                    atomic_add_f32(v_colors + (int64_t)g * CDIM + k, acc[5 + k]);
+                atomic_add_f32(v_opacities + g, acc[5 + CDIM]);
                 if constexpr (ABS) {
-                    atomic_add_f32(v_means2d_abs + (int64_t)g * 2 + 0,
-                                   s_acc[(6 + CDIM) * BS + slot]);
-                    atomic_add_f32(v_means2d_abs + (int64_t)g * 2 + 1,
-                                   s_acc[(7 + CDIM) * BS + slot]);
+                    atomic_add_f32(v_means2d_abs + (int64_t)g * 2 + 0, acc[6 + CDIM]);
+                    atomic_add_f32(v_means2d_abs + (int64_t)g * 2 + 1, acc[7 + CDIM]);
                 }
             }
         }
