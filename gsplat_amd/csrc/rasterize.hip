@@ -354,9 +354,14 @@ __device__ __forceinline__ void row_reduce(const float (&v)[N],
 // serves twice the pixels and a lane sums its two pixels before the wave
 // reduction (half the reductions and LDS atomics per tile).
 template <int TILE> struct BwdShape {
-    static constexpr int BS = TILE * TILE;       // pixels = staged Gaussians
+    static constexpr int BS = TILE * TILE;       // pixels of a tile
     static constexpr int PX = TILE == 16 ? 2 : 1;
     static constexpr int THREADS = BS / PX;
+    // Gaussians staged per batch (PX per thread).  Half as many would halve
+    // the LDS per workgroup (about 90 B per staged Gaussian) and allow more
+    // resident waves, but measured slower: the per-batch staging and
+    // barriers then cost more than the latency the extra waves hide.
+    static constexpr int BATCH = BS;
     static constexpr int ROWS = THREADS >= 64 ? 4 : THREADS / 16;
     static constexpr int LAST = 16 * ROWS - 1;   // lane holding a wave sum
     static_assert(THREADS % 16 == 0, "whole 16-lane rows");
@@ -365,17 +370,17 @@ template <int TILE> struct BwdShape {
 // LDS of one backward workgroup (reused tile after tile).
 template <int CDIM, int TILE, bool ABS> struct BwdSmem {
     using SH = BwdShape<TILE>;
-    static constexpr int BS = SH::BS;
+    static constexpr int NB = SH::BATCH;
     static constexpr int NACC = 2 + 3 + CDIM + 1 + (ABS ? 2 : 0);
     static constexpr int NW = (SH::THREADS + kWave - 1) / kWave;
-    float4 geo[BS];
-    float4 con[BS];
-    float col[BS * CDIM];
-    float acc[NACC * BS];
-    int32_t gid[BS];
-    int32_t hit[BS];
-    uint8_t wmask[BS];        // waves a Gaussian can reach
-    uint16_t list[NW][BS];    // per-wave work list
+    float4 geo[NB];
+    float4 con[NB];
+    float col[NB * CDIM];
+    float acc[NACC * NB];
+    int32_t gid[NB];
+    int32_t hit[NB];
+    uint8_t wmask[NB];        // waves a Gaussian can reach
+    uint16_t list[NW][NB];    // per-wave work list
     int32_t tile_bin;
     int64_t next_tile;
 };
@@ -390,9 +395,10 @@ __device__ __forceinline__ void rasterize_bwd_tile(
     float *__restrict__ v_conics, float *__restrict__ v_colors,
     float *__restrict__ v_opacities, BwdSmem<CDIM, TILE, ABS> &sm) {
     using SH = BwdShape<TILE>;
-    constexpr int BS = SH::BS;
+    constexpr int NB = SH::BATCH;
     constexpr int PX = SH::PX;
     constexpr int NT = SH::THREADS;
+    constexpr int SLOTS = NB / NT;  // staged Gaussians per thread
     // per-Gaussian sums: xy(2), conic(3), colour(CDIM), opacity(1) [, |xy|(2)]
     constexpr int NACC = 2 + 3 + CDIM + 1 + (ABS ? 2 : 0);
     constexpr int NW = (NT + kWave - 1) / kWave;  // waves per tile
@@ -480,7 +486,7 @@ __device__ __forceinline__ void rasterize_bwd_tile(
     atomicMax(&s_tile_bin, wave_bin);
     __syncthreads();
     const int32_t replay_end = min(range_end, s_tile_bin + 1);
-    const int num_batches = max(0, replay_end - range_start + BS - 1) / BS;
+    const int num_batches = max(0, replay_end - range_start + NB - 1) / NB;
 
     // the tile-sum slot this lane adds from every reduced register
     using RR = RowReduce<NACC>;
@@ -491,10 +497,10 @@ __device__ __forceinline__ void rasterize_bwd_tile(
 
     for (int b = 0; b < num_batches; ++b) {
         __syncthreads();
-        const int32_t batch_end = replay_end - 1 - b * BS;
-        const int batch_size = min(BS, batch_end + 1 - range_start);
+        const int32_t batch_end = replay_end - 1 - b * NB;
+        const int batch_size = min(NB, batch_end + 1 - range_start);
 #pragma unroll
-        for (int q = 0; q < PX; ++q) {
+        for (int q = 0; q < SLOTS; ++q) {
             const int slot = tr + q * NT;
             const int32_t idx = batch_end - slot;
             if (idx >= range_start) {
@@ -632,7 +638,7 @@ __device__ __forceinline__ void rasterize_bwd_tile(
         }
         __syncthreads();
 #pragma unroll
-        for (int q = 0; q < PX; ++q) {
+        for (int q = 0; q < SLOTS; ++q) {
             const int slot = tr + q * NT;
             if (slot < batch_size && s_hit[slot]) {
                 const int32_t g = s_gid[slot];
