@@ -80,6 +80,8 @@ _SIGNATURES = {
         c_int64, c_int64, c_int64, c_int32, _P, _P, _P, _P, _P, _P,
         c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P,
         _P, _P, _P, _P, _P, _P, _P, _P],
+    "gsplat_grad2d_stats": [
+        c_int64, c_int64, _P, _P, _P, c_float, c_float, _P, _P, _P],
     "gsplat_adam_multi": [_P, c_int32, c_float, c_float, c_float, _P],
     "gsplat_adam": [
         _P, _P, _P, _P, _P, c_int64, c_int64, c_float, c_float, c_float,

@@ -665,6 +665,34 @@ def rasterize_to_pixels_3dgs_bwd(
 
 
 # --------------------------------------------------------------------------
+# Densification statistics  (strategy/default.py:218-268)
+# --------------------------------------------------------------------------
+def grad2d_stats(grads: Tensor, gaussian_ids: Optional[Tensor],
+                 radii: Optional[Tensor], n_gaussians: int, scale_x: float,
+                 scale_y: float, grad2d: Tensor, count: Tensor) -> None:
+    """grad2d[g] += ||grads[r] * (scale_x, scale_y)||, count[g] += 1 for every
+    visible row r: packed rows (``gaussian_ids``) or dense rows [..., N]
+    counted where both ``radii`` are > 0."""
+    check_input(grads, "grads", _F32)
+    check_input(gaussian_ids, "gaussian_ids", torch.int64)
+    check_input(radii, "radii", _I32)
+    check_input(grad2d, "grad2d", _F32)
+    check_input(count, "count", _F32)
+    if grads.shape[-1] != 2:
+        raise RuntimeError("grads must end in a dimension of 2")
+    n_rows = grads.numel() // 2
+    if grad2d.numel() != n_gaussians or count.numel() != n_gaussians:
+        raise RuntimeError("grad2d and count must hold one value per Gaussian")
+    if gaussian_ids is not None and gaussian_ids.numel() != n_rows:
+        raise RuntimeError("gaussian_ids must hold one id per row")
+    if gaussian_ids is None and (radii is None or radii.numel() != 2 * n_rows):
+        raise RuntimeError("dense rows need radii of the same shape as grads")
+    call("gsplat_grad2d_stats", n_rows, int(n_gaussians), ptr(grads),
+         ptr(gaussian_ids), ptr(radii), float(scale_x), float(scale_y),
+         ptr(grad2d), ptr(count), _stream(grads))
+
+
+# --------------------------------------------------------------------------
 # Fused Adam  (Adam.cpp:37-66)
 # --------------------------------------------------------------------------
 def _adam_checks(param, param_grad, exp_avg, exp_avg_sq, valid):

@@ -4,7 +4,9 @@
 gsplat/strategy/default.py:218-268 (``DefaultStrategy._update_state``):
 the per-row 2D mean gradient (``absgrad`` or ``grad``) is scaled to the
 [-1, 1] screen range, and its norm plus a visit count are added to per-
-Gaussian accumulators.
+Gaussian accumulators.  One HIP launch (``gsplat_grad2d_stats``) reads the
+row gradients once, where the reference runs a clone, two column scales, a
+norm and two ``index_add_``.
 """
 
 from __future__ import annotations
@@ -13,6 +15,8 @@ from typing import Dict, Optional
 
 import torch
 from torch import Tensor
+
+from ..cuda import _ops
 
 
 @torch.no_grad()
@@ -31,19 +35,16 @@ def accumulate_grad2d_stats(
     """
     means2d = info["means2d"]
     grads = means2d.absgrad if absgrad else means2d.grad
-    grads = grads.clone()
-    grads[..., 0] *= info["width"] / 2.0 * info["n_cameras"]
-    grads[..., 1] *= info["height"] / 2.0 * info["n_cameras"]
     if grad2d is None:
         grad2d = torch.zeros(n_gaussians, device=grads.device)
     if count is None:
         count = torch.zeros(n_gaussians, device=grads.device)
+    sx = info["width"] / 2.0 * info["n_cameras"]
+    sy = info["height"] / 2.0 * info["n_cameras"]
     if packed:
-        gs_ids = info["gaussian_ids"]
+        _ops.grad2d_stats(grads.contiguous(), info["gaussian_ids"].contiguous(), None,
+                          n_gaussians, sx, sy, grad2d, count)
     else:
-        sel = (info["radii"] > 0.0).all(dim=-1)
-        gs_ids = torch.where(sel)[-1]
-        grads = grads[sel]
-    grad2d.index_add_(0, gs_ids, grads.norm(dim=-1))
-    count.index_add_(0, gs_ids, torch.ones_like(gs_ids, dtype=torch.float32))
+        _ops.grad2d_stats(grads.contiguous(), None, info["radii"].contiguous(),
+                          n_gaussians, sx, sy, grad2d, count)
     return grad2d, count

@@ -405,6 +405,24 @@ int gsplat_rasterize_bwd(
     gsplat_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
+/* Densification statistics.                                                 */
+/* ------------------------------------------------------------------------ */
+
+/* Running-state update of DefaultStrategy._update_state
+ *   (gsplat/strategy/default.py:218-268): for every visible row,
+ *   grad2d[g] += ||(grads[r,0] * scale_x, grads[r,1] * scale_y)|| and
+ *   count[g] += 1 (scale_x = W/2 * n_cameras, scale_y = H/2 * n_cameras).
+ * grads [n_rows,2] (the 2D mean gradient or absgrad); packed rows give
+ * gaussian_ids [n_rows] (int64, ids outside [0, N) are skipped); dense rows
+ * [C,N] give radii [n_rows,2] instead and count where both radii are > 0.
+ * grad2d [N] and count [N] are ACCUMULATED (float atomics, as the
+ * reference's index_add_). */
+int gsplat_grad2d_stats(
+    int64_t n_rows, int64_t N, const float *grads, const int64_t *gaussian_ids,
+    const int32_t *radii, float scale_x, float scale_y, float *grad2d,
+    float *count, gsplat_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
 /* Fused Adam (no bias correction, optional per-row mask).                   */
 /* ------------------------------------------------------------------------ */
 

@@ -429,3 +429,30 @@ def rasterization_ref(means, quats, scales, opacities, colors, viewmats, Ks,
             "transmittance": info["transmittance"],
             "last_ids": info["last_ids"], "n_isects": int(isect_ids.shape[0])}
     return rc, ra, meta
+
+
+def grad2d_stats_ref(grads, gaussian_ids, radii, n_gaussians, width, height,
+                     n_cameras, grad2d=None, count=None):
+    """Densification statistics of DefaultStrategy._update_state
+    (gsplat/strategy/default.py:235-268), in float64 on the host.
+
+    grads [nnz, 2] with ``gaussian_ids`` [nnz] (packed), or grads [..., N, 2]
+    with ``radii`` [..., N, 2] (dense; rows count where both radii are > 0).
+    Adds ||grads * (W/2 * C, H/2 * C)|| and 1 per visible row to the
+    Gaussian's accumulators; returns (grad2d, count)."""
+    g = grads.detach().double().clone()
+    g[..., 0] *= width / 2.0 * n_cameras
+    g[..., 1] *= height / 2.0 * n_cameras
+    if gaussian_ids is None:
+        sel = (radii > 0).all(dim=-1)
+        ids = torch.where(sel)[-1]
+        g = g[sel]
+    else:
+        ids = gaussian_ids
+    out_g = torch.zeros(n_gaussians, dtype=torch.float64) if grad2d is None \
+        else grad2d.double().clone()
+    out_c = torch.zeros(n_gaussians, dtype=torch.float64) if count is None \
+        else count.double().clone()
+    out_g.index_add_(0, ids, g.norm(dim=-1))
+    out_c.index_add_(0, ids, torch.ones(ids.shape[0], dtype=torch.float64))
+    return out_g, out_c

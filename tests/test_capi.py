@@ -35,7 +35,8 @@ def test_header_declares_the_survey_export_list():
                      "gsplat_sh_fwd", "gsplat_sh_bwd", "gsplat_isect_count",
                      "gsplat_isect_emit", "gsplat_sort_pairs_u64_u32",
                      "gsplat_isect_offsets", "gsplat_rasterize_fwd",
-                     "gsplat_rasterize_bwd", "gsplat_adam_multi", "gsplat_adam"]:
+                     "gsplat_rasterize_bwd", "gsplat_grad2d_stats", "gsplat_adam_multi",
+                     "gsplat_adam"]:
         assert required in names, required
 
 

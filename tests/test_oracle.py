@@ -386,3 +386,22 @@ def test_adam_first_step_closed_form_and_mask():
     np.testing.assert_array_equal(pn[~valid], p[~valid])
     np.testing.assert_array_equal(mn[~valid], 0)
     np.testing.assert_allclose(mn[valid], (1 - b1) * g[valid], rtol=1e-6)
+
+
+def test_grad2d_stats_closed_form():
+    # gradient (3/640, 4/360) on a 1280x720 image, one camera: the screen-space
+    # vector is (3, 4), norm 5; a second camera's row of the same Gaussian
+    # (2 cameras: scale doubles) adds 10; culled dense rows add nothing
+    grads = torch.tensor([[3 / 640, 4 / 360], [0.0, 0.0], [3 / 640, 4 / 360]])
+    g, c = torch_ref.grad2d_stats_ref(grads, torch.tensor([1, 0, 1]), None, 3,
+                                      1280, 720, 1)
+    assert torch.allclose(g, torch.tensor([0.0, 10.0, 0.0], dtype=torch.float64))
+    assert torch.equal(c, torch.tensor([1.0, 2.0, 0.0], dtype=torch.float64))
+    g, c = torch_ref.grad2d_stats_ref(grads[:2], torch.tensor([2, 2]), None, 3,
+                                      1280, 720, 2)
+    assert torch.allclose(g, torch.tensor([0.0, 0.0, 10.0], dtype=torch.float64))
+    dense = torch.tensor([[[3 / 640, 4 / 360], [1.0, 1.0]]])
+    radii = torch.tensor([[[2, 3], [0, 5]]], dtype=torch.int32)
+    g, c = torch_ref.grad2d_stats_ref(dense, None, radii, 2, 1280, 720, 1)
+    assert torch.allclose(g, torch.tensor([5.0, 0.0], dtype=torch.float64))
+    assert torch.equal(c, torch.tensor([1.0, 0.0], dtype=torch.float64))
