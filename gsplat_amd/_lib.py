@@ -80,6 +80,16 @@ _SIGNATURES = {
         c_int64, c_int64, c_int64, c_int32, _P, _P, _P, _P, _P, _P,
         c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P,
         _P, _P, _P, _P, _P, _P, _P, _P],
+    "gsplat_quat_scale_to_covar_preci_fwd": [c_int64, _P, _P, c_int32, _P, _P, _P],
+    "gsplat_quat_scale_to_covar_preci_bwd": [
+        c_int64, _P, _P, c_int32, _P, _P, _P, _P, _P],
+    "gsplat_rasterize_to_indices_workspace_size": [c_int64],
+    "gsplat_rasterize_to_indices_count": [
+        c_int64, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, _P, c_int32,
+        c_int32, c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P, c_size_t, _P],
+    "gsplat_rasterize_to_indices_write": [
+        c_int64, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, _P, c_int32,
+        c_int32, c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P],
     "gsplat_grad2d_stats": [
         c_int64, c_int64, _P, _P, _P, c_float, c_float, _P, _P, _P],
     "gsplat_adam_multi": [_P, c_int32, c_float, c_float, c_float, _P],
@@ -95,6 +105,7 @@ _RESTYPES = {
     "gsplat_sort_pairs_workspace_size": c_size_t,
     "gsplat_isect_prepare_workspace_size": c_size_t,
     "gsplat_isect_emit_sorted_workspace_size": c_size_t,
+    "gsplat_rasterize_to_indices_workspace_size": c_size_t,
 }
 
 

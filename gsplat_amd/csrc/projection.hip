@@ -1060,6 +1060,126 @@ int check_common(int64_t B, int64_t C, int64_t N, const float *means,
     return GSPLAT_OK;
 }
 
+
+// ---------------------------------------------------------------------------
+// Covariance / precision from quaternion and scale
+//   (quat_scale_to_covar_preci_fwd/bwd, QuatScaleToCovarCUDA.cu:37-236,
+//    Utils.cuh:223-340).  Covariance R diag(s)^2 R^T, precision
+//   R diag(1/s)^2 R^T; triu layout (xx, xy, xz, yy, yz, zz), else row-major
+//   3x3.  One thread per Gaussian.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void write_sym(const M3 &S, bool triu, float *out) {
+    if (triu) {
+        out[0] = S.m[0]; out[1] = S.m[1]; out[2] = S.m[2];
+        out[3] = S.m[4]; out[4] = S.m[5]; out[5] = S.m[8];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 9; ++i)
+            out[i] = S.m[i];
+    }
+}
+
+// dL/dS as a full matrix: triu entries cover both off-diagonal places, so
+// each place gets half of the entry's gradient.
+__device__ __forceinline__ M3 read_sym_grad(const float *g, bool triu) {
+    M3 v;
+    if (triu) {
+        v.m[0] = g[0];        v.m[1] = 0.5f * g[1]; v.m[2] = 0.5f * g[2];
+        v.m[3] = 0.5f * g[1]; v.m[4] = g[3];        v.m[5] = 0.5f * g[4];
+        v.m[6] = 0.5f * g[2]; v.m[7] = 0.5f * g[4]; v.m[8] = g[5];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 9; ++i)
+            v.m[i] = g[i];
+    }
+    return v;
+}
+
+__global__ void __launch_bounds__(kProjThreads)
+    covar_preci_fwd_kernel(int64_t N, const float *__restrict__ quats,
+                           const float *__restrict__ scales, bool triu,
+                           float *__restrict__ covars, float *__restrict__ precis) {
+    const int64_t i = (int64_t)blockIdx.x * kProjThreads + threadIdx.x;
+    if (i >= N)
+        return;
+    const int osz = triu ? 6 : 9;
+    M3 R;
+    quat_to_rot_exact(quats[i * 4 + 0], quats[i * 4 + 1], quats[i * 4 + 2],
+                      quats[i * 4 + 3], R.m);
+    const float s[3] = {scales[i * 3 + 0], scales[i * 3 + 1], scales[i * 3 + 2]};
+    if (covars != nullptr) {
+        M3 A;
+#pragma unroll
+        for (int r = 0; r < 3; ++r)
+#pragma unroll
+            for (int k = 0; k < 3; ++k)
+                A.m[r * 3 + k] = R.m[r * 3 + k] * s[k];
+        write_sym(mmt(A, A), triu, covars + i * osz);
+    }
+    if (precis != nullptr) {
+        M3 A;
+#pragma unroll
+        for (int r = 0; r < 3; ++r)
+#pragma unroll
+            for (int k = 0; k < 3; ++k)
+                A.m[r * 3 + k] = R.m[r * 3 + k] * (1.f / s[k]);
+        write_sym(mmt(A, A), triu, precis + i * osz);
+    }
+}
+
+__global__ void __launch_bounds__(kProjThreads)
+    covar_preci_bwd_kernel(int64_t N, const float *__restrict__ quats,
+                           const float *__restrict__ scales, bool triu,
+                           const float *__restrict__ v_covars,
+                           const float *__restrict__ v_precis,
+                           float *__restrict__ v_quats, float *__restrict__ v_scales) {
+    const int64_t i = (int64_t)blockIdx.x * kProjThreads + threadIdx.x;
+    if (i >= N)
+        return;
+    const int osz = triu ? 6 : 9;
+    GaussGeom G;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        G.q[k] = quats[i * 4 + k];
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+        G.s[k] = scales[i * 3 + k];
+    quat_to_rot_exact(G.q[0], G.q[1], G.q[2], G.q[3], G.Rq.m);
+    float vq[4] = {0.f, 0.f, 0.f, 0.f}, vs[3] = {0.f, 0.f, 0.f};
+    if (v_covars != nullptr) {
+        float q[4], s3[3];
+        covar_vjp_to_quat_scale(G, read_sym_grad(v_covars + i * osz, triu), q, s3);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            vq[k] += q[k];
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+            vs[k] += s3[k];
+    }
+    if (v_precis != nullptr) {
+        // the precision is the covariance of scales 1/s: chain through
+        // d(1/s)/ds = -1/s^2
+        GaussGeom P = G;
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+            P.s[k] = 1.f / G.s[k];
+        float q[4], s3[3];
+        covar_vjp_to_quat_scale(P, read_sym_grad(v_precis + i * osz, triu), q, s3);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            vq[k] += q[k];
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+            vs[k] += -(P.s[k] * P.s[k]) * s3[k];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        v_quats[i * 4 + k] = vq[k];
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+        v_scales[i * 3 + k] = vs[k];
+}
+
 }  // namespace
 }  // namespace gs
 
@@ -1232,4 +1352,37 @@ extern "C" int gsplat_projection_packed_bwd(
         a, nnz, batch_ids, camera_ids, gaussian_ids, sparse_grad,
         (B * C == 1) ? 1 : 0);
     return check_launch("projection_packed_bwd_kernel");
+}
+
+extern "C" int gsplat_quat_scale_to_covar_preci_fwd(int64_t N, const float *quats,
+                                                    const float *scales,
+                                                    int32_t triu, float *covars,
+                                                    float *precis,
+                                                    gsplat_stream_t stream) {
+    clear_error();
+    GS_REQUIRE(N >= 0, "quat_scale_to_covar_preci_fwd: negative N");
+    if (N == 0 || (covars == nullptr && precis == nullptr))
+        return GSPLAT_OK;
+    GS_REQUIRE(quats && scales, "quat_scale_to_covar_preci_fwd: NULL input");
+    covar_preci_fwd_kernel<<<(unsigned)ceil_div(N, kProjThreads), kProjThreads, 0,
+                             as_stream(stream)>>>(N, quats, scales, triu != 0,
+                                                  covars, precis);
+    return check_launch("covar_preci_fwd_kernel");
+}
+
+extern "C" int gsplat_quat_scale_to_covar_preci_bwd(
+    int64_t N, const float *quats, const float *scales, int32_t triu,
+    const float *v_covars, const float *v_precis, float *v_quats, float *v_scales,
+    gsplat_stream_t stream) {
+    clear_error();
+    GS_REQUIRE(N >= 0, "quat_scale_to_covar_preci_bwd: negative N");
+    if (N == 0)
+        return GSPLAT_OK;
+    GS_REQUIRE(quats && scales && v_quats && v_scales,
+               "quat_scale_to_covar_preci_bwd: NULL buffer");
+    covar_preci_bwd_kernel<<<(unsigned)ceil_div(N, kProjThreads), kProjThreads, 0,
+                             as_stream(stream)>>>(N, quats, scales, triu != 0,
+                                                  v_covars, v_precis, v_quats,
+                                                  v_scales);
+    return check_launch("covar_preci_bwd_kernel");
 }

@@ -698,6 +698,99 @@ __global__ void __launch_bounds__(BwdShape<TILE>::THREADS) rasterize_bwd_kernel(
     }
 }
 
+// Rasterize to indices (rasterize_to_indices_3dgs, RasterizeToIndices3DGS.cu
+// :36-196): the (Gaussian, pixel) pairs each pixel composites over the isect
+// batches [range_start, range_end) of its tile (batches of tile_size^2),
+// starting from the pixel's given transmittance.  The compositing decisions
+// are the forward kernel's (exact sigma order, thresholds on sigma,
+// portable_expf), so the pairs agree with rasterize_fwd bit for bit.  COUNT
+// writes the per-pixel counts; otherwise the pairs go to the per-pixel
+// starts from the scan of those counts.  One workgroup per tile.
+template <int TILE, bool COUNT>
+__global__ void __launch_bounds__(TILE * TILE) rasterize_indices_kernel(
+    const RasterArgs a, int64_t N, int64_t range_start, int64_t range_end,
+    const float *__restrict__ trans_in, const uint32_t *__restrict__ starts,
+    uint32_t *__restrict__ counts, int64_t *__restrict__ gaussian_ids,
+    int64_t *__restrict__ pixel_ids) {
+    constexpr int BS = TileShape<TILE>::BS;
+    __shared__ float4 s_geo[BS];   // (x, y, opacity, sig_max)
+    __shared__ float4 s_con[BS];   // (a, b, c, sig_clamp)
+    __shared__ int32_t s_id[BS];
+
+    int64_t image;
+    int32_t tile, ty, tx;
+    tile_coords(a, blockIdx.x, image, tile, ty, tx);
+    const int tr = threadIdx.x;
+    const int i = ty * TILE + tr / TILE;
+    const int j = tx * TILE + tr % TILE;
+    const bool inside = i < a.H && j < a.W;
+    const int64_t pix = ((int64_t)image * a.H + i) * a.W + j;
+    const float px = (float)j + 0.5f, py = (float)i + 0.5f;
+    const int64_t n_tiles = (int64_t)a.tile_width * a.tile_height;
+
+    const int32_t *offs = a.tile_offsets + image * n_tiles;
+    const int32_t range_lo = offs[tile];
+    const int32_t range_hi = (image == a.I - 1 && tile == n_tiles - 1)
+                                 ? (int32_t)a.n_isects
+                                 : offs[tile + 1];
+    const int64_t num_batches = (range_hi - range_lo + BS - 1) / BS;
+    const int64_t b_end = range_end < num_batches ? range_end : num_batches;
+
+    float T = inside ? trans_in[pix] : 1.f;
+    bool done = !inside;
+    uint32_t cnt = 0;
+    const uint32_t base = (!COUNT && inside) ? starts[pix] : 0u;
+    for (int64_t b = range_start; b < b_end; ++b) {
+        if (__syncthreads_count(done) >= BS)
+            break;
+        const int32_t batch_start = range_lo + (int32_t)b * BS;
+        const int32_t idx = batch_start + tr;
+        if (idx < range_hi) {
+            const int32_t g = a.flatten_ids[idx];
+            s_id[tr] = g;
+            const float2 xy = reinterpret_cast<const float2 *>(a.means2d)[g];
+            const float o = a.opacities[g];
+            float sig_max, sig_clamp;
+            alpha_thresholds(o, sig_max, sig_clamp);
+            s_geo[tr] = make_float4(xy.x, xy.y, o, sig_max);
+            s_con[tr] = make_float4(a.conics[g * 3 + 0], a.conics[g * 3 + 1],
+                                    a.conics[g * 3 + 2], sig_clamp);
+        }
+        __syncthreads();
+        const int batch_size = min(BS, range_hi - batch_start);
+        for (int t = 0; t < batch_size; ++t) {
+            if (!__ballot(!done))
+                break;
+            const float4 geo = s_geo[t];
+            const float4 con = s_con[t];
+            const float sigma = gauss_sigma(con.x, con.y, con.z, geo.x - px, geo.y - py);
+            const bool take = !done && sigma >= 0.f && sigma <= geo.w;
+            if (!__ballot(take))
+                continue;
+            const float vis = portable_expf_nonpos(-sigma);
+            const float alpha = sigma < con.w ? kMaxAlpha : geo.z * vis;
+            const float next_T = T * (1.f - alpha);
+            const bool stop = next_T <= kTransmittanceThreshold;
+            const bool emit = take && !stop;
+            if (!COUNT && emit) {
+                gaussian_ids[base + cnt] = s_id[t] % N;
+                pixel_ids[base + cnt] = pix;
+            }
+            cnt += emit ? 1u : 0u;
+            T = emit ? next_T : T;
+            done = done || (take && stop);
+        }
+    }
+    if (COUNT && inside)
+        counts[pix] = cnt;
+}
+
+__global__ void indices_total_kernel(const uint32_t *__restrict__ starts,
+                                     const uint32_t *__restrict__ counts, int64_t n,
+                                     int64_t *__restrict__ total) {
+    total[0] = (int64_t)starts[n - 1] + (int64_t)counts[n - 1];
+}
+
 // Workgroups of `kernel` (block threads, static LDS) that fit on the device
 // at once, capped at `work`.
 int resident_grid(const void *kernel, int block, int64_t work, int64_t *grid) {
@@ -847,4 +940,102 @@ extern "C" int gsplat_rasterize_bwd(
     }
 #undef GS_BWD
     return check_launch("rasterize_bwd_kernel");
+}
+
+// Shared argument handling of the two indices entry points.  The op has no
+// colours; the shared raster checks get means2d as a stand-in pointer (never
+// read).
+static int indices_args(int64_t I, int64_t N, int64_t n_isects,
+                        const float *means2d, const float *conics,
+                        const float *opacities, int32_t image_width,
+                        int32_t image_height, int32_t tile_size, int32_t tile_width,
+                        int32_t tile_height, const int32_t *tile_offsets,
+                        const int32_t *flatten_ids, const float *transmittances,
+                        int64_t range_start, RasterArgs *a) {
+    *a = RasterArgs{I, I * N, n_isects, means2d, conics, means2d, opacities,
+                    nullptr, nullptr, image_width, image_height, tile_size,
+                    tile_width, tile_height, tile_offsets, flatten_ids};
+    GS_TRY(check_raster(*a, 1));
+    GS_REQUIRE(N > 0, "rasterize_to_indices: N must be positive");
+    GS_REQUIRE(range_start >= 0, "rasterize_to_indices: negative range_start");
+    GS_REQUIRE(transmittances != nullptr, "rasterize_to_indices: NULL transmittances");
+    GS_REQUIRE(I * (int64_t)image_width * image_height < (1ll << 32),
+               "rasterize_to_indices: too many pixels");
+    return GSPLAT_OK;
+}
+
+extern "C" size_t gsplat_rasterize_to_indices_workspace_size(int64_t n_pixels) {
+    return lookback_bytes(ceil_div(n_pixels > 0 ? n_pixels : 1, 2048));
+}
+
+extern "C" int gsplat_rasterize_to_indices_count(
+    int64_t range_start, int64_t range_end, int64_t I, int64_t N, int64_t n_isects,
+    const float *transmittances, const float *means2d, const float *conics,
+    const float *opacities, int32_t image_width, int32_t image_height,
+    int32_t tile_size, int32_t tile_width, int32_t tile_height,
+    const int32_t *tile_offsets, const int32_t *flatten_ids, int32_t *chunk_cnts,
+    int32_t *chunk_starts, int64_t *n_elems, void *workspace,
+    size_t workspace_bytes, gsplat_stream_t stream) {
+    clear_error();
+    RasterArgs a;
+    GS_TRY(indices_args(I, N, n_isects, means2d, conics, opacities, image_width,
+                        image_height, tile_size, tile_width, tile_height,
+                        tile_offsets, flatten_ids, transmittances, range_start, &a));
+    if (I == 0)
+        return GSPLAT_OK;
+    GS_REQUIRE(chunk_cnts && chunk_starts && n_elems,
+               "rasterize_to_indices_count: NULL output");
+    const int64_t n_pix = I * (int64_t)image_width * image_height;
+    GS_REQUIRE(workspace != nullptr &&
+                   workspace_bytes >= gsplat_rasterize_to_indices_workspace_size(n_pix),
+               "rasterize_to_indices_count: workspace too small");
+    const int64_t blocks = I * (int64_t)tile_width * tile_height;
+    GS_REQUIRE(blocks < (1ll << 31), "rasterize_to_indices: too many tiles");
+    hipStream_t st = as_stream(stream);
+    uint32_t *cnt = reinterpret_cast<uint32_t *>(chunk_cnts);
+    uint32_t *start = reinterpret_cast<uint32_t *>(chunk_starts);
+#define GS_IDX(TILE)                                                           \
+    rasterize_indices_kernel<TILE, true><<<(unsigned)blocks, TILE * TILE, 0, st>>>( \
+        a, N, range_start, range_end, transmittances, nullptr, cnt, nullptr,   \
+        nullptr)
+    if (tile_size == 16) GS_IDX(16);
+    else if (tile_size == 8) GS_IDX(8);
+    else GS_IDX(4);
+#undef GS_IDX
+    GS_TRY(check_launch("rasterize_indices_kernel"));
+    GS_TRY(scan_u32_exclusive(cnt, start, n_pix, workspace, st));
+    indices_total_kernel<<<1, 1, 0, st>>>(start, cnt, n_pix, n_elems);
+    return check_launch("indices_total_kernel");
+}
+
+extern "C" int gsplat_rasterize_to_indices_write(
+    int64_t range_start, int64_t range_end, int64_t I, int64_t N, int64_t n_isects,
+    const float *transmittances, const float *means2d, const float *conics,
+    const float *opacities, int32_t image_width, int32_t image_height,
+    int32_t tile_size, int32_t tile_width, int32_t tile_height,
+    const int32_t *tile_offsets, const int32_t *flatten_ids,
+    const int32_t *chunk_starts, int64_t *gaussian_ids, int64_t *pixel_ids,
+    gsplat_stream_t stream) {
+    clear_error();
+    RasterArgs a;
+    GS_TRY(indices_args(I, N, n_isects, means2d, conics, opacities, image_width,
+                        image_height, tile_size, tile_width, tile_height,
+                        tile_offsets, flatten_ids, transmittances, range_start, &a));
+    if (I == 0)
+        return GSPLAT_OK;
+    GS_REQUIRE(chunk_starts && gaussian_ids && pixel_ids,
+               "rasterize_to_indices_write: NULL buffer");
+    const int64_t blocks = I * (int64_t)tile_width * tile_height;
+    GS_REQUIRE(blocks < (1ll << 31), "rasterize_to_indices: too many tiles");
+    hipStream_t st = as_stream(stream);
+    const uint32_t *start = reinterpret_cast<const uint32_t *>(chunk_starts);
+#define GS_IDX(TILE)                                                           \
+    rasterize_indices_kernel<TILE, false><<<(unsigned)blocks, TILE * TILE, 0, st>>>( \
+        a, N, range_start, range_end, transmittances, start, nullptr,          \
+        gaussian_ids, pixel_ids)
+    if (tile_size == 16) GS_IDX(16);
+    else if (tile_size == 8) GS_IDX(8);
+    else GS_IDX(4);
+#undef GS_IDX
+    return check_launch("rasterize_indices_kernel");
 }

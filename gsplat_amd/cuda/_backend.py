@@ -140,6 +140,32 @@ _IMPLS = {
     "adam": _ops.adam,
 }
 
+_SCHEMAS.update({
+    "quat_scale_to_covar_preci_fwd":
+        "quat_scale_to_covar_preci_fwd(Tensor quats, Tensor scales, bool compute_covar, "
+        "bool compute_preci, bool triu) -> (Tensor, Tensor)",
+    "quat_scale_to_covar_preci_bwd":
+        "quat_scale_to_covar_preci_bwd(Tensor quats, Tensor scales, bool triu, "
+        "Tensor? v_covars, Tensor? v_precis) -> (Tensor, Tensor)",
+    "rasterize_to_indices_3dgs":
+        "rasterize_to_indices_3dgs(int range_start, int range_end, Tensor transmittances, "
+        "Tensor means2d, Tensor conics, Tensor opacities, int image_width, "
+        "int image_height, int tile_size, Tensor tile_offsets, Tensor flatten_ids) "
+        "-> (Tensor, Tensor)",
+})
+
+
+def _impl_covar_fwd(quats, scales, compute_covar, compute_preci, triu):
+    return _fill(_ops.quat_scale_to_covar_preci_fwd(quats, scales, compute_covar,
+                                                    compute_preci, triu), quats)
+
+
+_IMPLS.update({
+    "quat_scale_to_covar_preci_fwd": _impl_covar_fwd,
+    "quat_scale_to_covar_preci_bwd": _ops.quat_scale_to_covar_preci_bwd,
+    "rasterize_to_indices_3dgs": _ops.rasterize_to_indices_3dgs,
+})
+
 _LIBRARY = None
 
 

@@ -665,6 +665,91 @@ def rasterize_to_pixels_3dgs_bwd(
 
 
 # --------------------------------------------------------------------------
+# Covariance / precision  (QuatScaleToCovar.cpp:37-110)
+# --------------------------------------------------------------------------
+def quat_scale_to_covar_preci_fwd(quats: Tensor, scales: Tensor, compute_covar: bool,
+                                  compute_preci: bool, triu: bool):
+    check_input(quats, "quats", _F32)
+    check_input(scales, "scales", _F32)
+    if quats.shape[-1] != 4 or scales.shape[:-1] != quats.shape[:-1] \
+            or scales.shape[-1] != 3:
+        raise RuntimeError("quats must be [..., 4] and scales [..., 3]")
+    N = quats.numel() // 4
+    out_shape = tuple(quats.shape[:-1]) + ((6,) if triu else (3, 3))
+    covars = torch.empty(out_shape, dtype=_F32, device=quats.device) \
+        if compute_covar else None
+    precis = torch.empty(out_shape, dtype=_F32, device=quats.device) \
+        if compute_preci else None
+    call("gsplat_quat_scale_to_covar_preci_fwd", N, ptr(quats), ptr(scales),
+         1 if triu else 0, ptr(covars), ptr(precis), _stream(quats))
+    return covars, precis
+
+
+def quat_scale_to_covar_preci_bwd(quats: Tensor, scales: Tensor, triu: bool,
+                                  v_covars: Optional[Tensor],
+                                  v_precis: Optional[Tensor]):
+    check_input(quats, "quats", _F32)
+    check_input(scales, "scales", _F32)
+    check_input(v_covars, "v_covars", _F32)
+    check_input(v_precis, "v_precis", _F32)
+    N = quats.numel() // 4
+    per = 6 if triu else 9
+    for t, name in ((v_covars, "v_covars"), (v_precis, "v_precis")):
+        if t is not None and t.numel() != N * per:
+            raise RuntimeError(f"{name} must hold {per} values per Gaussian")
+    v_quats = torch.empty_like(quats)
+    v_scales = torch.empty_like(scales)
+    call("gsplat_quat_scale_to_covar_preci_bwd", N, ptr(quats), ptr(scales),
+         1 if triu else 0, ptr(v_covars), ptr(v_precis), ptr(v_quats),
+         ptr(v_scales), _stream(quats))
+    return v_quats, v_scales
+
+
+# --------------------------------------------------------------------------
+# Rasterize to indices  (Rasterization.cpp:216-308)
+# --------------------------------------------------------------------------
+def rasterize_to_indices_3dgs(range_start: int, range_end: int, transmittances: Tensor,
+                              means2d: Tensor, conics: Tensor, opacities: Tensor,
+                              image_width: int, image_height: int, tile_size: int,
+                              tile_offsets: Tensor, flatten_ids: Tensor):
+    for t, n, dt in ((transmittances, "transmittances", _F32), (means2d, "means2d", _F32),
+                     (conics, "conics", _F32), (opacities, "opacities", _F32),
+                     (tile_offsets, "tile_offsets", _I32),
+                     (flatten_ids, "flatten_ids", _I32)):
+        check_input(t, n, dt)
+    N = means2d.shape[-2]
+    I = means2d.numel() // (2 * N) if N > 0 else 0
+    tile_height, tile_width = tile_offsets.shape[-2:]
+    H, W = int(image_height), int(image_width)
+    n_isects = flatten_ids.numel()
+    dev = means2d.device
+    if n_isects == 0 or I == 0:
+        empty = torch.empty(0, dtype=torch.int64, device=dev)
+        return empty, empty.clone()
+    if transmittances.numel() != I * H * W:
+        raise RuntimeError("transmittances must be [..., image_height, image_width]")
+    n_pix = I * H * W
+    cnts = torch.empty(n_pix, dtype=_I32, device=dev)
+    starts = torch.empty(n_pix, dtype=_I32, device=dev)
+    total = torch.empty(1, dtype=torch.int64, device=dev)
+    ws = torch.empty(query("gsplat_rasterize_to_indices_workspace_size", n_pix),
+                     dtype=torch.uint8, device=dev)
+    args = (int(range_start), int(min(range_end, 2 ** 62)), I, N, n_isects,
+            ptr(transmittances), ptr(means2d), ptr(conics), ptr(opacities), W, H,
+            int(tile_size), int(tile_width), int(tile_height), ptr(tile_offsets),
+            ptr(flatten_ids))
+    call("gsplat_rasterize_to_indices_count", *args, ptr(cnts), ptr(starts),
+         ptr(total), ptr(ws), ws.numel(), _stream(means2d))
+    n_elems = int(total.item())
+    gaussian_ids = torch.empty(n_elems, dtype=torch.int64, device=dev)
+    pixel_ids = torch.empty(n_elems, dtype=torch.int64, device=dev)
+    if n_elems:
+        call("gsplat_rasterize_to_indices_write", *args, ptr(starts),
+             ptr(gaussian_ids), ptr(pixel_ids), _stream(means2d))
+    return gaussian_ids, pixel_ids
+
+
+# --------------------------------------------------------------------------
 # Densification statistics  (strategy/default.py:218-268)
 # --------------------------------------------------------------------------
 def grad2d_stats(grads: Tensor, gaussian_ids: Optional[Tensor],

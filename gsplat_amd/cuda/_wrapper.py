@@ -361,6 +361,89 @@ def rasterize_to_pixels(
     return torch.cat(outs, dim=-1), alphas
 
 
+def quat_scale_to_covar_preci(
+    quats: Tensor,
+    scales: Tensor,
+    compute_covar: bool = True,
+    compute_preci: bool = True,
+    triu: bool = False,
+) -> Tuple[Optional[Tensor], Optional[Tensor]]:
+    """Covariance R S^2 R^T and precision R S^-2 R^T matrices from (unnormalized)
+    quaternions [..., 4] and scales [..., 3]; [..., 6] upper triangles when
+    ``triu``, else [..., 3, 3].  Signature of gsplat/cuda/_wrapper.py:375-414."""
+    batch_dims = quats.shape[:-1]
+    assert quats.shape == batch_dims + (4,), quats.shape
+    assert scales.shape == batch_dims + (3,), scales.shape
+    covars, precis = _QuatScaleToCovarPreci.apply(
+        quats.contiguous(), scales.contiguous(), compute_covar, compute_preci, triu)
+    return covars if compute_covar else None, precis if compute_preci else None
+
+
+class _QuatScaleToCovarPreci(torch.autograd.Function):
+    """gsplat/cuda/_wrapper.py:1355-1400."""
+
+    @staticmethod
+    def forward(ctx, quats, scales, compute_covar, compute_preci, triu):
+        covars, precis = _make_lazy_cuda_func("quat_scale_to_covar_preci_fwd")(
+            quats, scales, compute_covar, compute_preci, triu)
+        ctx.save_for_backward(quats, scales)
+        ctx.compute_covar = compute_covar
+        ctx.compute_preci = compute_preci
+        ctx.triu = triu
+        return covars, precis
+
+    @staticmethod
+    def backward(ctx, v_covars, v_precis):
+        quats, scales = ctx.saved_tensors
+        if ctx.compute_covar and v_covars is not None and v_covars.is_sparse:
+            v_covars = v_covars.to_dense()
+        if ctx.compute_preci and v_precis is not None and v_precis.is_sparse:
+            v_precis = v_precis.to_dense()
+        v_quats, v_scales = _make_lazy_cuda_func("quat_scale_to_covar_preci_bwd")(
+            quats, scales, ctx.triu,
+            v_covars.contiguous() if ctx.compute_covar and v_covars is not None else None,
+            v_precis.contiguous() if ctx.compute_preci and v_precis is not None else None)
+        return v_quats, v_scales, None, None, None
+
+
+def rasterize_to_indices_in_range(
+    range_start: int,
+    range_end: int,
+    transmittances: Tensor,
+    means2d: Tensor,
+    conics: Tensor,
+    opacities: Tensor,
+    image_width: int,
+    image_height: int,
+    tile_size: int,
+    isect_offsets: Tensor,
+    flatten_ids: Tensor,
+) -> Tuple[Tensor, Tensor, Tensor]:
+    """The (Gaussian id, pixel id, image id) of every pixel-Gaussian pair
+    composited over the isect batches [range_start, range_end) from the given
+    transmittances [..., H, W]; means2d [..., N, 2].  Signature and results of
+    gsplat/cuda/_wrapper.py:1274-1352."""
+    image_dims = means2d.shape[:-2]
+    tile_height, tile_width = isect_offsets.shape[-2:]
+    N = means2d.shape[-2]
+    assert transmittances.shape == image_dims + (image_height, image_width), \
+        transmittances.shape
+    assert means2d.shape == image_dims + (N, 2), means2d.shape
+    assert conics.shape == image_dims + (N, 3), conics.shape
+    assert opacities.shape == image_dims + (N,), opacities.shape
+    assert isect_offsets.shape == image_dims + (tile_height, tile_width), \
+        isect_offsets.shape
+    assert tile_height * tile_size >= image_height
+    assert tile_width * tile_size >= image_width
+    out_gauss_ids, out_indices = _make_lazy_cuda_func("rasterize_to_indices_3dgs")(
+        range_start, range_end, transmittances.contiguous(), means2d.contiguous(),
+        conics.contiguous(), opacities.contiguous(), image_width, image_height,
+        tile_size, isect_offsets.contiguous(), flatten_ids.contiguous())
+    out_pixel_ids = out_indices % (image_width * image_height)
+    out_image_ids = out_indices // (image_width * image_height)
+    return out_gauss_ids, out_pixel_ids, out_image_ids
+
+
 class _FullyFusedProjection(torch.autograd.Function):
     """Projects Gaussians to 2D (dense [..., C, N] outputs)."""
 

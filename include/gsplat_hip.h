@@ -179,6 +179,26 @@ int gsplat_projection_packed_bwd_rows(
     float *v_viewmats,
     gsplat_stream_t stream);
 
+/* Covariance and/or precision matrices from quaternions and scales.
+ * Replaces quat_scale_to_covar_preci_fwd
+ *   (gsplat/cuda/csrc/QuatScaleToCovar.cpp:37-72,
+ *    QuatScaleToCovarCUDA.cu:37-146).
+ * quats [N,4] (w,x,y,z, any norm), scales [N,3]; covars = R S^2 R^T and
+ * precis = R S^-2 R^T, each optional (NULL: not computed), [N,6] upper
+ * triangle (xx, xy, xz, yy, yz, zz) when triu != 0, else [N,3,3]. */
+int gsplat_quat_scale_to_covar_preci_fwd(
+    int64_t N, const float *quats, const float *scales, int32_t triu,
+    float *covars, float *precis, gsplat_stream_t stream);
+
+/* Backward of the above.  Replaces quat_scale_to_covar_preci_bwd
+ *   (QuatScaleToCovar.cpp:74-110, QuatScaleToCovarCUDA.cu:150-287).
+ * v_covars / v_precis optional (NULL: zero gradient), same layout as the
+ * forward's outputs; v_quats [N,4] and v_scales [N,3] are fully written. */
+int gsplat_quat_scale_to_covar_preci_bwd(
+    int64_t N, const float *quats, const float *scales, int32_t triu,
+    const float *v_covars, const float *v_precis, float *v_quats,
+    float *v_scales, gsplat_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Spherical harmonics (real SH, Sloan 2013 basis, degree 0..4).             */
 /* ------------------------------------------------------------------------ */
@@ -402,6 +422,38 @@ int gsplat_rasterize_bwd(
     const float *v_render_colors, const float *v_render_alphas,
     float *v_means2d_abs, float *v_means2d, float *v_conics,
     float *v_colors, float *v_opacities, uint32_t *tile_counter,
+    gsplat_stream_t stream);
+
+/* Rasterize to indices: the (Gaussian, pixel) pairs each pixel composites
+ * over the isect batches [range_start, range_end) of its tile (batches of
+ * tile_size^2, front to back), starting from the pixel's transmittance
+ * transmittances [I,H,W].  Replaces rasterize_to_indices_3dgs
+ *   (gsplat/cuda/csrc/Rasterization.cpp:216-308,
+ *    RasterizeToIndices3DGS.cu:36-271) in two steps around the one host
+ * read of the pair count, as the reference:
+ *  1. ..._count writes chunk_cnts [I*H*W] (pairs per pixel), chunk_starts
+ *     [I*H*W] (exclusive prefix) and n_elems (device int64, the total);
+ *     workspace of gsplat_rasterize_to_indices_workspace_size(I*H*W) bytes.
+ *  2. ..._write writes gaussian_ids [n_elems] (row % N) and pixel_ids
+ *     [n_elems] (image * H * W + i * W + j), pixel-major, front to back.
+ * Rows: means2d [I*N,2], conics [I*N,3], opacities [I*N] (or packed rows with
+ * I = 1, N = nnz).  Decisions are those of gsplat_rasterize_fwd. */
+size_t gsplat_rasterize_to_indices_workspace_size(int64_t n_pixels);
+int gsplat_rasterize_to_indices_count(
+    int64_t range_start, int64_t range_end, int64_t I, int64_t N,
+    int64_t n_isects, const float *transmittances, const float *means2d,
+    const float *conics, const float *opacities, int32_t image_width,
+    int32_t image_height, int32_t tile_size, int32_t tile_width,
+    int32_t tile_height, const int32_t *tile_offsets, const int32_t *flatten_ids,
+    int32_t *chunk_cnts, int32_t *chunk_starts, int64_t *n_elems,
+    void *workspace, size_t workspace_bytes, gsplat_stream_t stream);
+int gsplat_rasterize_to_indices_write(
+    int64_t range_start, int64_t range_end, int64_t I, int64_t N,
+    int64_t n_isects, const float *transmittances, const float *means2d,
+    const float *conics, const float *opacities, int32_t image_width,
+    int32_t image_height, int32_t tile_size, int32_t tile_width,
+    int32_t tile_height, const int32_t *tile_offsets, const int32_t *flatten_ids,
+    const int32_t *chunk_starts, int64_t *gaussian_ids, int64_t *pixel_ids,
     gsplat_stream_t stream);
 
 /* ------------------------------------------------------------------------ */

@@ -327,3 +327,66 @@ def alpha_thresholds(opacity) -> Tuple[np.ndarray, np.ndarray]:
         sig_clamp = np.where(pos, portable_logf(o / MAX_ALPHA).reshape(o.shape),
                              np.float32(-np.inf))
     return sig_max.astype(np.float32), sig_clamp.astype(np.float32)
+
+
+# --------------------------------------------------------------------------
+# Rasterize to indices (RasterizeToIndices3DGS.cu:36-196, both passes;
+# Rasterization.cpp:216-308)
+# --------------------------------------------------------------------------
+def rasterize_to_indices(range_start, range_end, transmittances, means2d, conics,
+                         opacities, width, height, tile_size, tile_offsets,
+                         flatten_ids, N):
+    """The (gaussian, pixel) pairs a pixel composites over the isect batches
+    [range_start, range_end) of its tile (batches of tile_size^2), starting
+    from its given transmittance; pixel-major order, depth order within a
+    pixel.  Decisions are the device's: float32 sigma in the kernels' order,
+    thresholds from ``alpha_thresholds``, alpha = o * portable_expf(-sigma)
+    clamped at 0.99, stop (exclusive) once T (1 - alpha) <= 1e-4.  A plain
+    per-pixel loop: for small inputs only.  Returns int64 arrays
+    (gaussian_ids = row % N, pixel_ids = image * H * W + i * W + j)."""
+    offs = np.asarray(tile_offsets, np.int64)
+    th, tw = offs.shape[-2:]
+    offs = offs.reshape(-1)
+    I = offs.size // (th * tw)
+    fids = np.asarray(flatten_ids, np.int64)
+    n_isects = fids.size
+    xy = np.asarray(means2d, np.float32).reshape(-1, 2)
+    con = np.asarray(conics, np.float32).reshape(-1, 3)
+    op = np.asarray(opacities, np.float32).reshape(-1)
+    sig_max, sig_clamp = alpha_thresholds(op)
+    T0 = np.asarray(transmittances, np.float32).reshape(-1)
+    bs = tile_size * tile_size
+    out_g, out_p = [], []
+    for img in range(I):
+        for i in range(height):
+            for j in range(width):
+                tile = (i // tile_size) * tw + j // tile_size
+                slot = img * th * tw + tile
+                s = offs[slot]
+                e = n_isects if slot == I * th * tw - 1 else offs[slot + 1]
+                n_batches = (e - s + bs - 1) // bs
+                pix = (img * height + i) * width + j
+                T = np.float32(T0[pix])
+                px, py = np.float32(j + 0.5), np.float32(i + 0.5)
+                stop = False
+                for b in range(range_start, min(range_end, n_batches)):
+                    for k in range(s + b * bs, min(s + (b + 1) * bs, e)):
+                        g = fids[k]
+                        sig = gauss_sigma_f32(con[g, 0], con[g, 1], con[g, 2],
+                                              xy[g, 0] - px, xy[g, 1] - py)
+                        if sig < 0 or not (sig <= sig_max[g]):
+                            continue
+                        if sig < sig_clamp[g]:
+                            alpha = MAX_ALPHA
+                        else:
+                            alpha = np.float32(op[g] * portable_expf(-sig).reshape(()))
+                        nxt = np.float32(T * np.float32(np.float32(1.0) - alpha))
+                        if nxt <= TRANSMITTANCE_THRESHOLD:
+                            stop = True
+                            break
+                        out_g.append(g % N)
+                        out_p.append(pix)
+                        T = nxt
+                    if stop:
+                        break
+    return np.asarray(out_g, np.int64), np.asarray(out_p, np.int64)

@@ -36,7 +36,10 @@ def test_header_declares_the_survey_export_list():
                      "gsplat_isect_emit", "gsplat_sort_pairs_u64_u32",
                      "gsplat_isect_offsets", "gsplat_rasterize_fwd",
                      "gsplat_rasterize_bwd", "gsplat_grad2d_stats", "gsplat_adam_multi",
-                     "gsplat_adam"]:
+                     "gsplat_adam", "gsplat_quat_scale_to_covar_preci_fwd",
+                     "gsplat_quat_scale_to_covar_preci_bwd",
+                     "gsplat_rasterize_to_indices_count",
+                     "gsplat_rasterize_to_indices_write"]:
         assert required in names, required
 
 
@@ -71,7 +74,8 @@ def test_reference_op_schemas_registered():
                "intersect_offset", "projection_ewa_3dgs_fused_fwd",
                "projection_ewa_3dgs_fused_bwd", "projection_ewa_3dgs_packed_fwd",
                "projection_ewa_3dgs_packed_bwd", "rasterize_to_pixels_3dgs_fwd",
-               "rasterize_to_pixels_3dgs_bwd", "adam"]:
+               "rasterize_to_pixels_3dgs_bwd", "adam", "quat_scale_to_covar_preci_fwd",
+               "quat_scale_to_covar_preci_bwd", "rasterize_to_indices_3dgs"]:
         assert hasattr(torch.ops.gsplat, op), op
     s = str(torch.ops.gsplat.adam.default._schema)
     assert "Tensor(a!) param" in s and "Tensor? valid" in s

@@ -405,3 +405,70 @@ def test_grad2d_stats_closed_form():
     g, c = torch_ref.grad2d_stats_ref(dense, None, radii, 2, 1280, 720, 1)
     assert torch.allclose(g, torch.tensor([5.0, 0.0], dtype=torch.float64))
     assert torch.equal(c, torch.tensor([1.0, 0.0], dtype=torch.float64))
+
+
+def test_rasterize_to_indices_oracle_single_gaussian_closed_form():
+    # one isotropic Gaussian (conic 1/s^2 I) centred in a 16x16 tile, opacity
+    # 0.8, full transmittance: the pairs are exactly the pixels with
+    # sigma = |d|^2 / (2 s^2) <= ln(255 * 0.8), in pixel order
+    s2 = 9.0
+    m2 = np.array([[8.0, 8.0]], np.float32)
+    con = np.array([[1 / s2, 0.0, 1 / s2]], np.float32)
+    op = np.array([0.8], np.float32)
+    offs = np.zeros((1, 1, 1), np.int32)
+    gids, pids = exact.rasterize_to_indices(0, 10 ** 9, np.ones((1, 16, 16), np.float32),
+                                            m2, con, op, 16, 16, 16, offs,
+                                            np.zeros(1, np.int32), 1)
+    yy, xx = np.mgrid[0:16, 0:16]
+    d2 = (xx + 0.5 - 8.0) ** 2 + (yy + 0.5 - 8.0) ** 2
+    expect = np.nonzero((d2 / (2 * s2) <= math.log(255 * 0.8)).ravel())[0]
+    np.testing.assert_array_equal(pids, expect)
+    assert (gids == 0).all()
+    # a pixel whose transmittance is already at the cutoff takes nothing
+    T = np.ones((1, 16, 16), np.float32)
+    T[0, 8, 8] = 1e-4
+    _, pids2 = exact.rasterize_to_indices(0, 10 ** 9, T, m2, con, op, 16, 16, 16, offs,
+                                          np.zeros(1, np.int32), 1)
+    assert 8 * 16 + 8 not in set(pids2.tolist())
+    assert len(pids2) == len(pids) - 1
+    # batches past the tile's range leave every pixel empty
+    g3, _ = exact.rasterize_to_indices(1, 10 ** 9, np.ones((1, 16, 16), np.float32),
+                                       m2, con, op, 16, 16, 16, offs,
+                                       np.zeros(1, np.int32), 1)
+    assert g3.size == 0
+
+
+def test_rasterize_to_indices_oracle_agrees_with_compositing_oracle():
+    # full range from T = 1: every pixel's last pair is the forward oracle's
+    # last composited Gaussian, and pixels with no pair have alpha 0
+    from tests._util import projected_2d
+    d = projected_2d(seed=5, N=400, C=1, W=48, H=40)
+    N = d["means2d"].shape[-2]
+    gids, pids = exact.rasterize_to_indices(
+        0, 10 ** 9, np.ones((1, d["H"], d["W"]), np.float32), d["means2d"].numpy(),
+        d["conics"].numpy(), d["opacities"].numpy(), d["W"], d["H"], d["tile"],
+        d["offsets"].numpy(), d["flatten_ids"].numpy(), N)
+    _, ra, info = torch_ref.rasterize_to_pixels_ref(
+        d["means2d"].double(), d["conics"].double(), d["colors"].double(),
+        d["opacities"].double(), d["W"], d["H"], d["tile"], d["offsets"],
+        d["flatten_ids"])
+    fl = d["flatten_ids"].numpy()
+    last = info["last_ids"].reshape(-1)
+    alpha = ra.detach().numpy().reshape(-1)
+    has = np.zeros(alpha.size, bool)
+    has[pids] = True
+    np.testing.assert_array_equal(has, alpha > 0)
+    assert pids.size > 1000
+    ends = np.r_[np.nonzero(np.diff(pids))[0], pids.size - 1]
+    np.testing.assert_array_equal(gids[ends], fl[last[pids[ends]]] % N)
+    assert (np.diff(pids) >= 0).all()
+
+
+def test_precision_oracle_is_the_covariance_inverse():
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(64, 4, generator=g, dtype=torch.float64)
+    s = torch.rand(64, 3, generator=g, dtype=torch.float64) + 0.2
+    C = torch_ref.quat_scale_to_covar(q, s)
+    R = torch_ref.quat_to_rotmat(q)
+    P = R @ torch.diag_embed(1.0 / s ** 2) @ R.transpose(-1, -2)
+    torch.testing.assert_close(C @ P, torch.eye(3, dtype=torch.float64).expand(64, 3, 3))
