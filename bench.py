@@ -235,9 +235,71 @@ def _gpu_bench(args):
         "ms_per_step": ms_per_step,
         "roofline": roofline,
         "stages": stage_report,
+        "extra_ops": _extra_ops(scene, meta, ctx),
         "ctx": ctx,
         "scene": scene,
     }
+
+
+def _extra_ops(scene, meta, ctx):
+    """Timing of the ops outside the training step, on the same workload
+    (after the timed region; not part of the metric): covariance/precision
+    fwd+bwd for every Gaussian, rasterize-to-indices over the full range of
+    the step's intersections, and the densification statistics over its
+    rows.  HIP events around each entry point; average of 10 calls."""
+    import torch
+
+    from gsplat_amd import _lib
+    from gsplat_amd.cuda import _ops
+
+    if meta["means2d"].dim() != 2:  # packed rows only
+        return None
+    dev = scene.means.device
+    N, nnz = ctx["N"], ctx["nnz"]
+    quats, scales = scene.quats.contiguous(), scene.scales.contiguous()
+    v_c = torch.randn(N, 3, 3, device=dev)
+    v_p = torch.randn(N, 3, 3, device=dev)
+    m2 = meta["means2d"].detach()[None].contiguous()
+    con = meta["conics"].detach()[None].contiguous()
+    op = meta["opacities"].detach()[None].contiguous()
+    T = torch.ones(1, scene.height, scene.width, device=dev)
+    offs = meta["isect_offsets"].reshape(1, meta["tile_height"], meta["tile_width"])
+    grads = torch.randn(nnz, 2, device=dev) * 1e-3
+    ids = meta["gaussian_ids"]
+    g2d = torch.zeros(N, device=dev)
+    cnt = torch.zeros(N, device=dev)
+    n_pairs = [0]
+
+    def run():
+        _ops.quat_scale_to_covar_preci_fwd(quats, scales, True, True, False)
+        _ops.quat_scale_to_covar_preci_bwd(quats, scales, False, v_c, v_p)
+        gi, _ = _ops.rasterize_to_indices_3dgs(0, 1 << 40, T, m2, con, op, scene.width,
+                                               scene.height, 16, offs,
+                                               meta["flatten_ids"])
+        n_pairs[0] = int(gi.numel())
+        _ops.grad2d_stats(grads, ids, None, N, 640.0, 360.0, g2d, cnt)
+
+    run()
+    torch.cuda.synchronize()
+    timer = _lib.EntryTimer()
+    with _lib.timing(timer):
+        for _ in range(10):
+            run()
+    torch.cuda.synchronize()
+    ms = {k: sum(v) / len(v) for k, v in timer.results().items()}
+    algorithmic = {
+        "gsplat_quat_scale_to_covar_preci_fwd": N * (16 + 12 + 36 + 36),
+        "gsplat_quat_scale_to_covar_preci_bwd": N * (16 + 12 + 36 + 36 + 16 + 12),
+        "gsplat_grad2d_stats": nnz * (8 + 8 + 8),
+    }
+    out = {}
+    for k, v in ms.items():
+        e = {"ms": round(v, 4)}
+        if k in algorithmic and v > 0:
+            e["GBps"] = round(algorithmic[k] / (v * 1e-3) / 1e9, 1)
+        out[k] = e
+    out["rasterize_to_indices_pairs"] = n_pairs[0]
+    return out
 
 
 def _measured_traffic(kernel, config):
@@ -372,6 +434,7 @@ def main():
         "mpix_per_s": round(mpix, 2),
         "roofline": res["roofline"],
         "stages_ms": res["stages"],
+        "extra_ops_ms": res["extra_ops"],
         "cpu_baseline": cpu,
     }
     if cpu is not None:
