@@ -439,26 +439,41 @@ __device__ __forceinline__ bool sh_rows_prologue(const ShRowsArgs &a,
     return vis;
 }
 
+// One thread per Gaussian; its coefficients go straight to registers (16-byte
+// loads when a row is a whole number of float4), which leaves occupancy to
+// the registers instead of the ~12.5 KB per wave an LDS staging takes.
 template <int DEG>
 __global__ void __launch_bounds__(kShThreads)
     sh_rows_fwd_kernel(const ShRowsArgs a, float *__restrict__ colors) {
     using S = ShShape<DEG>;
-    __shared__ float s_coef[kShThreads * S::PITCH];
-    __shared__ uint8_t s_vis[kShThreads];
-    const int64_t r0 = (int64_t)blockIdx.x * kShThreads;
-    const int64_t BN = a.B * a.N;
-    const int nrows = (int)((BN - r0) < kShThreads ? (BN - r0) : kShThreads);
-    int32_t row0;
-    float mean[3];
-    const bool vis =
-        sh_rows_prologue<DEG>(a, r0, nrows, s_coef, s_vis, &row0, mean);
+    const int64_t bg = (int64_t)blockIdx.x * kShThreads + threadIdx.x;
+    if (bg >= a.B * a.N)
+        return;
+    const int64_t b = bg / a.N, g = bg - b * a.N;
+    const int32_t row0 = a.row_of[b * a.C * a.N + g];
+    bool vis = row0 >= 0;
+    for (int64_t c = 1; c < a.C; ++c)
+        vis |= a.row_of[(b * a.C + c) * a.N + g] >= 0;
     if (!vis)
         return;
-    const int t = threadIdx.x;
-    const int64_t bg = r0 + t;
-    const int64_t b = bg / a.N, g = bg - b * a.N;
-    const float mx = mean[0], my = mean[1], mz = mean[2];
-    const float *cf = s_coef + t * S::PITCH;
+    const float mx = a.means[bg * 3 + 0], my = a.means[bg * 3 + 1],
+                mz = a.means[bg * 3 + 2];
+    float cf[S::ROW];
+    if (S::ROW % 4 == 0 && a.vec_ok) {
+        const float4 *src = reinterpret_cast<const float4 *>(a.coeffs + bg * S::ROW);
+#pragma unroll
+        for (int i = 0; i < S::ROW / 4; ++i) {
+            const float4 v = src[i];
+            cf[4 * i + 0] = v.x;
+            cf[4 * i + 1] = v.y;
+            cf[4 * i + 2] = v.z;
+            cf[4 * i + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < S::ROW; ++i)
+            cf[i] = a.coeffs[bg * (int64_t)a.K * 3 + i];
+    }
     for (int64_t c = 0; c < a.C; ++c) {
         const int32_t r = c == 0 ? row0 : a.row_of[(b * a.C + c) * a.N + g];
         if (r < 0)
