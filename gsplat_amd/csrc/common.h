@@ -277,6 +277,13 @@ __device__ __forceinline__ int wave_max_i32(int v) {
 
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
 
+// Mask of the active lanes where p holds.  The builtin takes the predicate
+// as a lane mask, where __ballot(int) first materialises it in a VGPR and
+// compares it again (two VALU instructions per vote).
+__device__ __forceinline__ uint64_t wave_ballot(bool p) {
+    return __builtin_amdgcn_ballot_w64(p);
+}
+
 __device__ __forceinline__ uint64_t lanemask_lt() {
     return (1ull << lane_id()) - 1ull;
 }
@@ -410,7 +417,7 @@ __device__ __forceinline__ uint64_t lb_exclusive_prefix(const Lookback &lb,
 #pragma unroll
             for (int k = 0; k < kLbWords; ++k)
                 pending |= (s[k] >> 62) == 0;
-            if (!__ballot(pending))
+            if (!wave_ballot(pending))
                 break;
             __builtin_amdgcn_s_sleep(1);
 #pragma unroll
@@ -428,7 +435,7 @@ __device__ __forceinline__ uint64_t lb_exclusive_prefix(const Lookback &lb,
         for (int k = 0; k < kLbWords; ++k)
             if (k <= kf)
                 v += s[k] & kLbValMask;
-        const uint64_t inc = __ballot(kf < kLbWords);
+        const uint64_t inc = wave_ballot(kf < kLbWords);
         if (inc) {
             const uint32_t first = __builtin_ctzll(inc);  // closest inclusive
             if (lane > first)

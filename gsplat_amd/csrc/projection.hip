@@ -282,7 +282,7 @@ __device__ __forceinline__ void load_row_cam(const FwdArgs &a, int64_t bc,
                                              Cam &cam) {
     const int64_t bc0 = ((int64_t)__builtin_amdgcn_readfirstlane((int)(bc >> 32)) << 32) |
                         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)bc);
-    if (!__ballot(bc != bc0))
+    if (!wave_ballot(bc != bc0))
         load_cam(a.viewmats + bc0 * 16, a.Ks + bc0 * 9, cam);
     else
         load_cam(a.viewmats + bc * 16, a.Ks + bc * 9, cam);
@@ -398,7 +398,7 @@ __global__ void __launch_bounds__(kPackThreads) projection_packed_fwd_kernel(
 #pragma unroll
     for (int j = 0; j < kPackItems; ++j)
         mixed |= bc[j] != bc0;
-    const bool one_cam = !__ballot(mixed);
+    const bool one_cam = !wave_ballot(mixed);
     Cam cam0;
     if (one_cam) {
         load_cam(a.viewmats + bc0 * 16, a.Ks + bc0 * 9, cam0);
@@ -424,7 +424,7 @@ __global__ void __launch_bounds__(kPackThreads) projection_packed_fwd_kernel(
                           a.eps2d, a.near_plane, a.far_plane, a.radius_clip,
                           o[j]) &&
             row < n_rows;
-        bal[j] = __ballot(valid);
+        bal[j] = wave_ballot(valid);
         if (lane == 0)
             s_cnt[j * NW + wave] = (uint32_t)__popcll(bal[j]);
     }

@@ -124,7 +124,7 @@ __device__ __forceinline__ int wave_work_list(const uint8_t *wmask, int t0,
     for (int c0 = 0; c0 < n; c0 += kWave) {
         const int slot = c0 + (int)lane_id();
         const bool take = slot < n && slot >= t0 && ((wmask[slot] >> wave) & 1u);
-        const uint64_t bal = __ballot(take);
+        const uint64_t bal = wave_ballot(take);
         if (take)
             list[n_work + __popcll(bal & lanemask_lt())] = (SlotT)slot;
         n_work += __popcll(bal);
@@ -199,14 +199,17 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
 
     float T = 1.f;
     int32_t cur_idx = 0;
-    bool done = !inside;
+    // per-lane state as wave masks: votes come straight from the compares and
+    // combine in scalar registers, and the selects read the mask directly
+    const uint64_t lanes_m = wave_ballot(true);
+    uint64_t done_m = wave_ballot(!inside);
     float acc[CDIM];
 #pragma unroll
     for (int k = 0; k < CDIM; ++k)
         acc[k] = 0.f;
 
     for (int b = 0; b < num_batches; ++b) {
-        if (__syncthreads_count(done) >= BS)
+        if (__syncthreads_count(__builtin_amdgcn_inverse_ballot_w64(done_m)) >= BS)
             break;
         const int32_t batch_start = range_start + b * BS;
         const int32_t idx = batch_start + tr;
@@ -235,15 +238,16 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
         // wave-uniform loop; a lane that is done (or skips a Gaussian) is
         // carried by selects, not branches
         for (int n = 0; n < n_work; ++n) {
-            if (!__ballot(!done))
+            if (done_m == lanes_m)
                 break;
             const int t = s_list[wave][n];
             const float4 geo = s_geo[t];
             const float4 con = s_con[t];
             const float dx = geo.x - px, dy = geo.y - py;
             const float sigma = gauss_sigma(con.x, con.y, con.z, dx, dy);
-            const bool take = !done && sigma >= 0.f && sigma <= geo.w;
-            if (!__ballot(take))
+            const uint64_t take_m =
+                wave_ballot(sigma >= 0.f) & wave_ballot(sigma <= geo.w) & ~done_m;
+            if (take_m == 0)
                 continue;
             // every lane runs the arithmetic (the exp clamps any sigma into
             // range); lanes that do not take the Gaussian keep their state
@@ -251,17 +255,18 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
             const float vis = portable_expf_nonpos(-sigma);
             const float alpha = sigma < con.w ? kMaxAlpha : geo.z * vis;
             const float next_T = T * (1.f - alpha);
-            const bool stop = next_T <= kTransmittanceThreshold;
-            const bool upd = take && !stop;
-            const float w = alpha * T;
+            const uint64_t stop_m = wave_ballot(next_T <= kTransmittanceThreshold);
+            const bool upd = __builtin_amdgcn_inverse_ballot_w64(take_m & ~stop_m);
+            // a lane that keeps its state adds c * 0 (= +0, exact): the colour
+            // loads stay unconditional instead of each turning into its own
+            // exec-masked branch and LDS round trip
+            const float w = upd ? alpha * T : 0.f;
 #pragma unroll
-            for (int k = 0; k < CDIM; ++k) {
-                const float c = acc[k] + s_col[t * CDIM + k] * w;
-                acc[k] = upd ? c : acc[k];
-            }
+            for (int k = 0; k < CDIM; ++k)
+                acc[k] = fmaf(s_col[t * CDIM + k], w, acc[k]);
             cur_idx = upd ? batch_start + t : cur_idx;
             T = upd ? next_T : T;
-            done = done || (take && stop);
+            done_m |= take_m & stop_m;
         }
     }
     if (inside) {
@@ -495,6 +500,10 @@ __device__ __forceinline__ void rasterize_bwd_tile(
     for (int f = 0; f < RR::N4; ++f)
         red_slot[f] = RR::lane_value(f, (int)(lane_id() & 15u));
 
+    // No barrier before restaging: each thread stages exactly the slots it
+    // flushed at the end of the previous batch (slot = tr + q * NT in both),
+    // and every other read of the staged data ended at the barrier before
+    // that flush.
     for (int b = 0; b < num_batches; ++b) {
         __syncthreads();
         const int32_t batch_end = replay_end - 1 - b * NB;
@@ -538,24 +547,36 @@ __device__ __forceinline__ void rasterize_bwd_tile(
         // support reaches the wave's pixels
         const int t0 = max(0, batch_end - wave_bin_final);
         const int n_work = wave_work_list(s_wmask, t0, batch_size, wave, s_list[wave]);
+        // software pipeline: the next work item's slot and geometry are read
+        // one iteration ahead, so the two dependent LDS round trips overlap
+        // the current Gaussian's arithmetic
+        int t_nx = n_work > 0 ? (int)s_list[wave][0] : 0;
+        float4 geo_nx = s_geo[t_nx], con_nx = s_con[t_nx];
         for (int n = 0; n < n_work; ++n) {
-            const int t = s_list[wave][n];
+            const int t = t_nx;
             const int32_t isect = batch_end - t;
-            const float4 geo = s_geo[t];
-            const float4 con = s_con[t];
+            const float4 geo = geo_nx;
+            const float4 con = con_nx;
+            t_nx = s_list[wave][min(n + 1, n_work - 1)];
+            geo_nx = s_geo[t_nx];
+            con_nx = s_con[t_nx];
             const float dx = geo.x - px;
             float dy[PX], sigma[PX];
             bool valid[PX];
-            bool any = false;
+            uint64_t any_m = 0;
 #pragma unroll
             for (int p = 0; p < PX; ++p) {
                 dy[p] = geo.y - py[p];
                 sigma[p] = gauss_sigma(con.x, con.y, con.z, dx, dy[p]);
-                valid[p] = isect <= bin_final[p] && sigma[p] >= 0.f &&
-                           sigma[p] <= geo.w;
-                any |= valid[p];
+                // votes straight from the compares, combined in scalar
+                // registers; the selects below read the mask
+                const uint64_t valid_m = wave_ballot(isect <= bin_final[p]) &
+                                         wave_ballot(sigma[p] >= 0.f) &
+                                         wave_ballot(sigma[p] <= geo.w);
+                valid[p] = __builtin_amdgcn_inverse_ballot_w64(valid_m);
+                any_m |= valid_m;
             }
-            if (!__ballot(any))
+            if (any_m == 0)
                 continue;
             // Branch-free over the lane's pixels: an invalid pixel runs the
             // same arithmetic and its contributions are zeroed through
@@ -759,13 +780,13 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_indices_kernel(
         __syncthreads();
         const int batch_size = min(BS, range_hi - batch_start);
         for (int t = 0; t < batch_size; ++t) {
-            if (!__ballot(!done))
+            if (!wave_ballot(!done))
                 break;
             const float4 geo = s_geo[t];
             const float4 con = s_con[t];
             const float sigma = gauss_sigma(con.x, con.y, con.z, geo.x - px, geo.y - py);
             const bool take = !done && sigma >= 0.f && sigma <= geo.w;
-            if (!__ballot(take))
+            if (!wave_ballot(take))
                 continue;
             const float vis = portable_expf_nonpos(-sigma);
             const float alpha = sigma < con.w ? kMaxAlpha : geo.z * vis;

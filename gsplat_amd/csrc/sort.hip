@@ -53,7 +53,7 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d, int bits,
     uint64_t peers = valid;
     for (int b = 0; b < bits; ++b) {
         const bool bit = (d >> b) & 1u;
-        const uint64_t m = __ballot(bit);
+        const uint64_t m = wave_ballot(bit);
         peers &= bit ? m : ~m;
     }
     return peers;
@@ -76,7 +76,7 @@ __device__ __forceinline__ void rank_wave_span(const K (&k)[ITEMS], int64_t base
         const int64_t i = base + (int64_t)j * kWave + lane;
         const bool valid = i < n;
         const uint32_t d = (uint32_t)(k[j] >> shift) & mask;
-        const uint64_t vmask = __ballot(valid);
+        const uint64_t vmask = wave_ballot(valid);
         const uint64_t peers = match_digit(d, bits, vmask);
         uint32_t r = 0;
         if (valid)
