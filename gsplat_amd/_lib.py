@@ -36,7 +36,7 @@ _SIGNATURES = {
         c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P,
         c_int32, c_int32, c_float, c_float, c_float, c_float, c_int32,
         _P, c_size_t,
-        _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+        _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
     "gsplat_projection_packed_bwd": [
         c_int64, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P,
         c_int32, c_int32, c_float, c_int32,
@@ -45,7 +45,7 @@ _SIGNATURES = {
     "gsplat_projection_packed_bwd_rows": [
         c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P,
         c_int32, c_int32, c_float, c_int32,
-        _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+        _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
     "gsplat_sh_fwd": [c_int64, c_int32, c_int32, _P, _P, _P, _P, _P],
     "gsplat_sh_bwd": [c_int64, c_int32, c_int32, _P, _P, _P, _P, _P, _P, _P],
     "gsplat_sh_rows_fwd": [c_int64, c_int64, c_int64, c_int32, c_int32,

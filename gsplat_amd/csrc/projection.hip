@@ -346,7 +346,8 @@ __global__ void __launch_bounds__(kPackThreads) projection_packed_fwd_kernel(
     int64_t *__restrict__ gaussian_ids, int32_t *__restrict__ radii,
     float *__restrict__ means2d, float *__restrict__ depths,
     float *__restrict__ conics, float *__restrict__ compensations,
-    int64_t *__restrict__ nnz_out, int32_t *__restrict__ row_of) {
+    int64_t *__restrict__ nnz_out, int32_t *__restrict__ row_of,
+    float *__restrict__ row_opacities) {
     constexpr int NW = kPackThreads / kWave;
     static_assert(kPackItems * NW == kWave, "one wave scans the wave counts");
     __shared__ uint32_t s_ticket;
@@ -473,6 +474,9 @@ __global__ void __launch_bounds__(kPackThreads) projection_packed_fwd_kernel(
         conics[pos * 3 + 2] = o[j].cc;
         if (compensations != nullptr)
             compensations[pos] = o[j].comp;
+        // the row's opacity, opacities[b, g] (read above for the culling)
+        if (row_opacities != nullptr)
+            row_opacities[pos] = opac[j];
     }
     const int64_t last_bid = (n_rows - 1) / kPackRows;
     if ((int64_t)bid == last_bid && threadIdx.x == 0) {
@@ -757,6 +761,11 @@ struct BwdArgs {
     const float *conics, *compensations;
     const float *v_means2d, *v_depths, *v_conics, *v_compensations;
     float *v_means, *v_covars, *v_quats, *v_scales, *v_viewmats;
+    // packed rows only (all nullable): per-row opacity gradients summed into
+    // v_opacities[b, g], and a dense [B, N, 3] term added to v_means
+    const float *v_row_opacities;
+    float *v_opacities;
+    const float *v_means_add;
 };
 
 // Reduce v_R (9) and v_t (3) of the workgroup and add them to the camera's
@@ -822,6 +831,7 @@ __global__ void __launch_bounds__(kProjThreads)
                   a.quats ? a.quats + bg * 4 : nullptr,
                   a.scales ? a.scales + bg * 3 : nullptr, G);
     float v_mean[3] = {0.f, 0.f, 0.f};
+    float v_op = 0.f;
     M3 v_S;
 #pragma unroll
     for (int i = 0; i < 9; ++i)
@@ -849,6 +859,8 @@ __global__ void __launch_bounds__(kProjThreads)
                 active = r.x > 0 && r.y > 0;
             }
             if (active) {
+                if (a.v_row_opacities != nullptr)
+                    v_op += a.v_row_opacities[row];
                 Cam cam;
                 load_cam(a.viewmats + bc * 16, a.Ks + bc * 9, cam);
                 const bool has_comp = a.v_compensations != nullptr;
@@ -888,10 +900,17 @@ __global__ void __launch_bounds__(kProjThreads)
     if (!in_range)
         return;
     if (a.v_means != nullptr) {
+        if (a.v_means_add != nullptr) {
+#pragma unroll
+            for (int k = 0; k < 3; ++k)
+                v_mean[k] += a.v_means_add[bg * 3 + k];
+        }
         a.v_means[bg * 3 + 0] = v_mean[0];
         a.v_means[bg * 3 + 1] = v_mean[1];
         a.v_means[bg * 3 + 2] = v_mean[2];
     }
+    if (a.v_opacities != nullptr)
+        a.v_opacities[bg] = v_op;
     if (!seen) {
         // visible in no camera: zero gradient rows
         if (a.covars != nullptr) {
@@ -1224,7 +1243,8 @@ extern "C" int gsplat_projection_packed_fwd(
     size_t workspace_bytes, int32_t *indptr, int64_t *batch_ids,
     int64_t *camera_ids, int64_t *gaussian_ids, int32_t *radii,
     float *means2d, float *depths, float *conics, float *compensations,
-    int64_t *nnz_out, int32_t *row_of, gsplat_stream_t stream) {
+    int64_t *nnz_out, int32_t *row_of, float *row_opacities,
+    gsplat_stream_t stream) {
     clear_error();
     GS_TRY(check_common(B, C, N, means, covars, quats, scales, viewmats, Ks,
                         image_width, image_height, camera_model));
@@ -1237,6 +1257,8 @@ extern "C" int gsplat_projection_packed_fwd(
                    depths && conics,
                "projection_packed: NULL output");
     GS_REQUIRE(rows < (1ll << 31), "projection_packed: more than 2^31 rows");
+    GS_REQUIRE(row_opacities == nullptr || opacities != nullptr,
+               "projection_packed: row opacities need opacities");
     const int64_t blocks = ceil_div(rows, kPackRows);
     GS_REQUIRE(workspace != nullptr && workspace_bytes >= lookback_bytes(blocks),
                "projection_packed: workspace too small");
@@ -1250,12 +1272,12 @@ extern "C" int gsplat_projection_packed_fwd(
         projection_packed_fwd_kernel<true><<<(unsigned)blocks, kPackThreads, 0, st>>>(
             a, lookback_from(workspace), indptr, batch_ids, camera_ids,
             gaussian_ids, radii, means2d, depths, conics, compensations,
-            nnz_out, row_of);
+            nnz_out, row_of, row_opacities);
     else
         projection_packed_fwd_kernel<false><<<(unsigned)blocks, kPackThreads, 0, st>>>(
             a, lookback_from(workspace), indptr, batch_ids, camera_ids,
             gaussian_ids, radii, means2d, depths, conics, compensations,
-            nnz_out, row_of);
+            nnz_out, row_of, row_opacities);
     return check_launch("projection_packed_fwd_kernel");
 }
 
@@ -1299,12 +1321,17 @@ extern "C" int gsplat_projection_packed_bwd_rows(
     const float *compensations, const float *v_means2d, const float *v_depths,
     const float *v_conics, const float *v_compensations, float *v_means,
     float *v_covars, float *v_quats, float *v_scales, float *v_viewmats,
+    const float *v_row_opacities, float *v_opacities, const float *v_means_add,
     gsplat_stream_t stream) {
     clear_error();
     GS_TRY(check_common(B, C, N, means, covars, quats, scales, viewmats, Ks,
                         image_width, image_height, camera_model));
     if (B * N == 0)
         return GSPLAT_OK;
+    GS_REQUIRE((v_row_opacities == nullptr) == (v_opacities == nullptr),
+               "projection_packed_bwd_rows: v_row_opacities and v_opacities go together");
+    GS_REQUIRE(v_means_add == nullptr || v_means != nullptr,
+               "projection_packed_bwd_rows: v_means_add needs v_means");
     GS_REQUIRE(row_of && conics && v_means2d && v_conics,
                "projection_packed_bwd_rows: NULL buffer");
     GS_REQUIRE(v_compensations == nullptr || compensations != nullptr,
@@ -1313,7 +1340,7 @@ extern "C" int gsplat_projection_packed_bwd_rows(
               (float)image_width, (float)image_height, eps2d, camera_model,
               conics, compensations, v_means2d, v_depths, v_conics,
               v_compensations, v_means, v_covars, v_quats, v_scales,
-              v_viewmats};
+              v_viewmats, v_row_opacities, v_opacities, v_means_add};
     projection_fused_bwd_kernel<<<(unsigned)ceil_div(B * N, kProjThreads),
                                   kProjThreads, 0, as_stream(stream)>>>(
         a, nullptr, row_of);

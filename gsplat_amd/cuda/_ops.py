@@ -226,7 +226,7 @@ def projection_packed_fwd_with_row_map(
              int(camera_model), ptr(ws), ws.numel(), ptr(indptr),
              ptr(batch_ids), ptr(camera_ids), ptr(gaussian_ids), ptr(radii),
              ptr(means2d), ptr(depths), ptr(conics), ptr(comps), ptr(nnz_dev),
-             ptr(row_of), _stream(means))
+             ptr(row_of), None, _stream(means))
         nnz = int(nnz_dev.item())
     return (
         indptr,
@@ -239,6 +239,131 @@ def projection_packed_fwd_with_row_map(
         conics[:nnz],
         comps[:nnz] if comps is not None else None,
         row_of,
+    )
+
+
+def packed_front_fwd(
+    means: Tensor,
+    covars: Optional[Tensor],
+    quats: Optional[Tensor],
+    scales: Optional[Tensor],
+    opacities: Tensor,
+    features: Tensor,
+    viewmats: Tensor,
+    Ks: Tensor,
+    image_width: int,
+    image_height: int,
+    eps2d: float,
+    near_plane: float,
+    far_plane: float,
+    radius_clip: float,
+    calc_compensations: bool,
+    camera_model: int,
+    sh_degree: Optional[int],
+    isect: Optional[dict] = None,
+):
+    """rasterization()'s packed front end: the packed projection plus every
+    row's opacity (opacities[b, g]) and colour, either the clamped SH colour
+    of per-Gaussian coefficients ``features`` [..., N, K, 3] (``sh_degree``
+    given) or a gather of per-Gaussian features [..., N, D].
+
+    The colour kernel is driven by Gaussian through ``row_of`` and writes
+    into capacity-sized rows, so it is queued right behind the projection;
+    the visible count travels to a pinned host word in between, and the host
+    waits for that copy only, while the colour kernel runs.  Returns the
+    outputs of ``projection_packed_fwd_with_row_map`` followed by
+    ``row_opacities`` [nnz] and ``row_colors`` [nnz, D].
+
+    With ``isect`` = {"tile_size", "tile_width", "tile_height"} (for row
+    opacities that are used as they are, i.e. without compensations), the
+    first half of the sorted tile intersection of the rows is queued right
+    after the wait, before the host slices the outputs, and its state is
+    left in ``isect["state"]`` for ``isect_emit_sorted``."""
+    _check_proj_inputs(means, covars, quats, scales, opacities, viewmats, Ks)
+    if opacities is None:
+        raise RuntimeError("packed_front_fwd: opacities are required")
+    check_input(features, "features", _F32)
+    batch_dims, B, C, N = _proj_dims(means, viewmats)
+    dev = means.device
+    if sh_degree is None:
+        D = features.shape[-1]
+        if tuple(features.shape) != batch_dims + (N, D):
+            raise RuntimeError(f"packed_front_fwd: features {tuple(features.shape)} "
+                               f"must be [..., N, D]")
+    else:
+        D = 3
+        K = features.shape[-2]
+        if (tuple(features.shape) != batch_dims + (N, K, 3)
+                or (int(sh_degree) + 1) ** 2 > K):
+            raise RuntimeError(f"packed_front_fwd: coefficients {tuple(features.shape)} "
+                               f"do not hold degree {sh_degree}")
+    cap = B * C * N
+    indptr = torch.empty(B * C + 1, dtype=_I32, device=dev)
+    batch_ids = torch.empty(cap, dtype=_I64, device=dev)
+    camera_ids = torch.empty(cap, dtype=_I64, device=dev)
+    gaussian_ids = torch.empty(cap, dtype=_I64, device=dev)
+    radii = torch.empty(cap, 2, dtype=_I32, device=dev)
+    means2d = torch.empty(cap, 2, dtype=_F32, device=dev)
+    depths = torch.empty(cap, dtype=_F32, device=dev)
+    conics = torch.empty(cap, 3, dtype=_F32, device=dev)
+    comps = torch.empty(cap, dtype=_F32, device=dev) if calc_compensations else None
+    row_of = torch.empty(cap, dtype=_I32, device=dev)
+    row_opac = torch.empty(cap, dtype=_F32, device=dev)
+    row_colors = torch.empty(cap, D, dtype=_F32, device=dev)
+    if cap == 0:
+        indptr.zero_()
+        nnz = 0
+    else:
+        st = _stream(means)
+        ws = torch.empty(query("gsplat_projection_packed_workspace_size", B, C, N),
+                         dtype=torch.uint8, device=dev)
+        nnz_dev = torch.empty(1, dtype=_I64, device=dev)
+        call("gsplat_projection_packed_fwd", B, C, N, ptr(means), ptr(covars),
+             ptr(quats), ptr(scales), ptr(opacities), ptr(viewmats), ptr(Ks),
+             int(image_width), int(image_height), float(eps2d),
+             float(near_plane), float(far_plane), float(radius_clip),
+             int(camera_model), ptr(ws), ws.numel(), ptr(indptr),
+             ptr(batch_ids), ptr(camera_ids), ptr(gaussian_ids), ptr(radii),
+             ptr(means2d), ptr(depths), ptr(conics), ptr(comps), ptr(nnz_dev),
+             ptr(row_of), ptr(row_opac), st)
+        nnz_host = torch.empty(1, dtype=_I64, pin_memory=True)
+        nnz_host.copy_(nnz_dev, non_blocking=True)
+        copied = torch.cuda.Event()
+        copied.record()
+        if sh_degree is None:
+            call("gsplat_rows_gather", B, C, N, D, ptr(features), ptr(row_of),
+                 ptr(row_colors), st)
+        else:
+            call("gsplat_sh_rows_fwd", B, C, N, K, int(sh_degree), ptr(means),
+                 ptr(viewmats), ptr(features), ptr(row_of), ptr(row_colors), st)
+        copied.synchronize()
+        nnz = int(nnz_host[0])
+        if isect is not None and nnz > 0:
+            ts, tw, th = isect["tile_size"], isect["tile_width"], isect["tile_height"]
+            I = B * C
+            if (int(I).bit_length() + (int(tw) * int(th)).bit_length()) <= 32:
+                if I == 1:
+                    img = None
+                else:
+                    img = (camera_ids[:nnz] if B == 1
+                           else batch_ids[:nnz] * C + camera_ids[:nnz])
+                isect["state"] = isect_prepare_sorted(
+                    means2d[:nnz], radii[:nnz], depths[:nnz], conics[:nnz],
+                    row_opac[:nnz], img, nnz if I == 1 else 0, I, ts, tw, th,
+                    torch.empty(nnz, dtype=_I32, device=dev))
+    return (
+        indptr,
+        batch_ids[:nnz],
+        camera_ids[:nnz],
+        gaussian_ids[:nnz],
+        radii[:nnz],
+        means2d[:nnz],
+        depths[:nnz],
+        conics[:nnz],
+        comps[:nnz] if comps is not None else None,
+        row_of,
+        row_opac[:nnz],
+        row_colors[:nnz],
     )
 
 
@@ -343,10 +468,15 @@ def projection_packed_bwd_rows(
     v_conics: Tensor,
     v_compensations: Optional[Tensor],
     viewmats_requires_grad: bool,
+    v_row_opacities: Optional[Tensor] = None,
+    v_means_add: Optional[Tensor] = None,
 ):
     """Dense gradients of the packed projection from its row map ``row_of``
     (one pass driven by Gaussian; no zero fill, no atomics).  ``v_depths``
-    may be None (zero gradient)."""
+    may be None (zero gradient).  With ``v_row_opacities`` [nnz] it also
+    returns v_opacities (each Gaussian's sum over its rows, shaped like
+    ``means[..., 0]``); ``v_means_add`` (like ``means``) is added to v_means.
+    Returns (v_means, v_covars, v_quats, v_scales, v_viewmats[, v_opacities])."""
     _check_proj_inputs(means, covars, quats, scales, None, viewmats, Ks)
     check_input(row_of, "row_of", _I32)
     for t, n in ((conics, "conics"), (v_means2d, "v_means2d"), (v_depths, "v_depths"),
@@ -359,12 +489,21 @@ def projection_packed_bwd_rows(
     v_quats = torch.empty_like(quats) if covars is None else None
     v_scales = torch.empty_like(scales) if covars is None else None
     v_viewmats = torch.zeros_like(viewmats) if viewmats_requires_grad else None
+    check_input(v_row_opacities, "v_row_opacities", _F32)
+    check_input(v_means_add, "v_means_add", _F32)
+    if v_means_add is not None and v_means_add.shape != means.shape:
+        raise RuntimeError("projection_packed_bwd_rows: v_means_add must be shaped like means")
+    v_opacities = (torch.empty(means.shape[:-1], dtype=_F32, device=means.device)
+                   if v_row_opacities is not None else None)
     call("gsplat_projection_packed_bwd_rows", B, C, N, ptr(means), ptr(covars),
          ptr(quats), ptr(scales), ptr(viewmats), ptr(Ks), int(image_width),
          int(image_height), float(eps2d), int(camera_model), ptr(row_of),
          ptr(conics), ptr(compensations), ptr(v_means2d), ptr(v_depths),
          ptr(v_conics), ptr(v_compensations), ptr(v_means), ptr(v_covars),
-         ptr(v_quats), ptr(v_scales), ptr(v_viewmats), _stream(means))
+         ptr(v_quats), ptr(v_scales), ptr(v_viewmats), ptr(v_row_opacities),
+         ptr(v_opacities), ptr(v_means_add), _stream(means))
+    if v_row_opacities is not None:
+        return v_means, v_covars, v_quats, v_scales, v_viewmats, v_opacities
     return v_means, v_covars, v_quats, v_scales, v_viewmats
 
 
@@ -477,29 +616,10 @@ def intersect_tile(
         # stable sort on the image|tile bits only: the reference's full-key
         # order (a per-image segmented sort, segmented=True, is the same order
         # because the image id occupies the top key bits).
-        depth_order = torch.empty(n, dtype=_I32, device=dev)
-        depth_starts = torch.empty(n + 1, dtype=_I64, device=dev)
-        records = torch.empty(n, 8, dtype=_F32, device=dev)
-        total = torch.empty(1, dtype=_I64, device=dev)
-        ws = torch.empty(query("gsplat_isect_prepare_workspace_size", n),
-                         dtype=torch.uint8, device=dev)
-        call("gsplat_isect_prepare", n, N, ptr(img), ptr(means2d), ptr(radii),
-             ptr(depths), ptr(conics), ptr(opacities), int(tile_size),
-             int(tile_width), int(tile_height), ptr(ws), ws.numel(),
-             ptr(tiles_per_gauss), ptr(depth_order), ptr(depth_starts), ptr(records),
-             ptr(total), st)
-        n_isects = int(total.item())
-        isect_ids = torch.empty(n_isects, dtype=_I64, device=dev)
-        flatten_ids = torch.empty(n_isects, dtype=_I32, device=dev)
-        if n_isects == 0:
-            return tiles_per_gauss, isect_ids, flatten_ids
-        ews = torch.empty(query("gsplat_isect_emit_sorted_workspace_size", n_isects),
-                          dtype=torch.uint8, device=dev)
-        call("gsplat_isect_emit_sorted", n, N, int(I), ptr(img), ptr(means2d),
-             ptr(radii), ptr(depths), ptr(conics), ptr(opacities), int(tile_size),
-             int(tile_width), int(tile_height), ptr(depth_order), ptr(depth_starts),
-             ptr(records), n_isects, ptr(ews), ews.numel(), ptr(isect_ids), ptr(flatten_ids), st)
-        return tiles_per_gauss, isect_ids, flatten_ids
+        state = isect_prepare_sorted(means2d, radii, depths, conics, opacities, img,
+                                     N, I, tile_size, tile_width, tile_height,
+                                     tiles_per_gauss)
+        return isect_emit_sorted(state)
     cum = torch.empty(n, dtype=_I64, device=dev)
     ws = torch.empty(query("gsplat_isect_count_workspace_size", n),
                      dtype=torch.uint8, device=dev)
@@ -516,6 +636,66 @@ def intersect_tile(
          int(tile_width), int(tile_height), ptr(cum), ptr(isect_ids),
          ptr(flatten_ids), st)
     return tiles_per_gauss, isect_ids, flatten_ids
+
+
+def isect_prepare_sorted(means2d, radii, depths, conics, opacities, img, N, I,
+                         tile_size, tile_width, tile_height, tiles_per_gauss):
+    """First half of the sorted intersection of n > 0 rows (inputs checked by
+    the caller): the tile counts, the depth order of the rows and their first
+    slots (gsplat_isect_prepare).  The intersection count goes to a pinned
+    host word behind an event, so the caller can queue or do other work
+    before ``isect_emit_sorted`` waits for it."""
+    n = means2d.numel() // 2
+    dev = means2d.device
+    st = _stream(means2d)
+    state = {
+        "n": n, "N": N, "I": int(I), "img": img, "means2d": means2d, "radii": radii,
+        "depths": depths, "conics": conics, "opacities": opacities,
+        "tile": (int(tile_size), int(tile_width), int(tile_height)),
+        "tiles_per_gauss": tiles_per_gauss,
+        "depth_order": torch.empty(n, dtype=_I32, device=dev),
+        "depth_starts": torch.empty(n + 1, dtype=_I64, device=dev),
+        "records": torch.empty(n, 8, dtype=_F32, device=dev),
+    }
+    total = torch.empty(1, dtype=_I64, device=dev)
+    ws = torch.empty(query("gsplat_isect_prepare_workspace_size", n),
+                     dtype=torch.uint8, device=dev)
+    call("gsplat_isect_prepare", n, N, ptr(img), ptr(means2d), ptr(radii),
+         ptr(depths), ptr(conics), ptr(opacities), int(tile_size),
+         int(tile_width), int(tile_height), ptr(ws), ws.numel(),
+         ptr(tiles_per_gauss), ptr(state["depth_order"]), ptr(state["depth_starts"]),
+         ptr(state["records"]), ptr(total), st)
+    host = torch.empty(1, dtype=_I64, pin_memory=True)
+    host.copy_(total, non_blocking=True)
+    ev = torch.cuda.Event()
+    ev.record()
+    state["total"] = (host, ev)
+    return state
+
+
+def isect_emit_sorted(state):
+    """Second half: waits for the intersection count, then emits the
+    intersections in depth order and sorts them on the image|tile bits
+    (gsplat_isect_emit_sorted).  Returns (tiles_per_gauss, isect_ids,
+    flatten_ids)."""
+    host, ev = state["total"]
+    ev.synchronize()
+    n_isects = int(host[0])
+    dev = state["means2d"].device
+    isect_ids = torch.empty(n_isects, dtype=_I64, device=dev)
+    flatten_ids = torch.empty(n_isects, dtype=_I32, device=dev)
+    if n_isects == 0:
+        return state["tiles_per_gauss"], isect_ids, flatten_ids
+    ts, tw, th = state["tile"]
+    ews = torch.empty(query("gsplat_isect_emit_sorted_workspace_size", n_isects),
+                      dtype=torch.uint8, device=dev)
+    call("gsplat_isect_emit_sorted", state["n"], state["N"], state["I"],
+         ptr(state["img"]), ptr(state["means2d"]), ptr(state["radii"]),
+         ptr(state["depths"]), ptr(state["conics"]), ptr(state["opacities"]), ts, tw,
+         th, ptr(state["depth_order"]), ptr(state["depth_starts"]),
+         ptr(state["records"]), n_isects, ptr(ews), ews.numel(), ptr(isect_ids),
+         ptr(flatten_ids), _stream(state["means2d"]))
+    return state["tiles_per_gauss"], isect_ids, flatten_ids
 
 
 def intersect_offset(isect_ids: Tensor, I: int, tile_width: int, tile_height: int) -> Tensor:

@@ -687,6 +687,97 @@ class _PackedSphericalHarmonics(torch.autograd.Function):
                 v_coeffs if ctx.needs_input_grad[2] else None, None, None, None)
 
 
+class _PackedFrontEnd(torch.autograd.Function):
+    """rasterization()'s packed front end as one node: the packed projection
+    (``_FullyFusedProjectionPacked``), the per-row opacities
+    opacities[batch_ids, gaussian_ids] and the per-row colours (clamped SH of
+    per-Gaussian coefficients, or a gather of per-Gaussian features) -- the
+    reference's fully_fused_projection + index + compute_directions +
+    spherical_harmonics + clamp_min (rendering.py:256-873).  The colour
+    kernel runs while the host waits for the visible count
+    (``_ops.packed_front_fwd``).  Backward: the colour VJP first, then one
+    pass per Gaussian that writes the projection's gradients together with
+    v_opacities and the colour term of v_means.  The view matrices get no
+    gradient (the caller uses this node only when they need none)."""
+
+    @staticmethod
+    def forward(ctx, means, covars, quats, scales, opacities, features, viewmats,
+                Ks, width, height, eps2d, near_plane, far_plane, radius_clip,
+                calc_compensations, camera_model, sh_degree, isect=None):
+        cm = _camera_model_type(camera_model)
+        (indptr, batch_ids, camera_ids, gaussian_ids, radii, means2d, depths,
+         conics, compensations, row_of, row_opac, row_colors) = _ops.packed_front_fwd(
+            means, covars, quats, scales, opacities, features, viewmats, Ks, width,
+            height, eps2d, near_plane, far_plane, radius_clip, calc_compensations,
+            cm, sh_degree, isect)
+        if not calc_compensations:
+            compensations = None
+        ctx.save_for_backward(means, covars, quats, scales, viewmats, Ks, conics,
+                              compensations, row_of, features)
+        ctx.set_materialize_grads(False)
+        ctx.width = width
+        ctx.height = height
+        ctx.eps2d = eps2d
+        ctx.camera_model_type = cm
+        ctx.sh_degree = sh_degree
+        ctx.mark_non_differentiable(batch_ids, camera_ids, gaussian_ids, indptr, radii,
+                                    row_of)
+        return (batch_ids, camera_ids, gaussian_ids, indptr, radii, means2d,
+                depths, conics, compensations, row_of, row_opac, row_colors)
+
+    @staticmethod
+    def backward(ctx, v_batch_ids, v_camera_ids, v_gaussian_ids, v_indptr,
+                 v_radii, v_means2d, v_depths, v_conics, v_compensations, v_row_of,
+                 v_row_opac, v_row_colors):
+        (means, covars, quats, scales, viewmats, Ks, conics, compensations, row_of,
+         features) = ctx.saved_tensors
+        batch_dims = means.shape[:-2]
+        N = means.shape[-2]
+        C = viewmats.shape[-3]
+        B = math.prod(batch_dims)
+        need = ctx.needs_input_grad
+        # colour VJP first: its direction term is added to v_means below
+        v_features = None
+        v_means_sh = None
+        if v_row_colors is not None and (need[5] or need[0]):
+            v_row_colors = v_row_colors.contiguous()
+            if ctx.sh_degree is None:
+                if need[5]:
+                    v_features = _ops.rows_scatter_sum(
+                        v_row_colors, row_of, B, C, N).reshape(features.shape)
+            else:
+                K = features.shape[-2]
+                v_coeffs, v_means_sh = _ops.sh_rows_bwd(
+                    ctx.sh_degree, means.reshape(B, N, 3),
+                    viewmats.reshape(B, C, 4, 4), features.reshape(B, N, K, 3),
+                    row_of, v_row_colors)
+                v_features = v_coeffs.reshape(features.shape) if need[5] else None
+                v_means_sh = v_means_sh.reshape(means.shape)
+        if compensations is None:
+            v_compensations = None
+        elif v_compensations is not None:
+            v_compensations = v_compensations.contiguous()
+        v_means2d = (torch.zeros_like(conics[:, :2]) if v_means2d is None
+                     else v_means2d.contiguous())
+        v_conics = torch.zeros_like(conics) if v_conics is None else v_conics.contiguous()
+        v_row_opac = (v_row_opac.contiguous() if v_row_opac is not None and need[4]
+                      else None)
+        res = _ops.projection_packed_bwd_rows(
+            means, covars, quats, scales, viewmats, Ks, ctx.width, ctx.height,
+            ctx.eps2d, ctx.camera_model_type, row_of, conics, compensations,
+            v_means2d, None if v_depths is None else v_depths.contiguous(),
+            v_conics, v_compensations, False, v_row_opacities=v_row_opac,
+            v_means_add=v_means_sh)
+        v_means, v_covars, v_quats, v_scales = res[:4]
+        v_opacities = res[5] if v_row_opac is not None else None
+        return (v_means if need[0] else None,
+                v_covars if need[1] else None,
+                v_quats if need[2] else None,
+                v_scales if need[3] else None,
+                v_opacities, v_features,
+                None, None, None, None, None, None, None, None, None, None, None, None)
+
+
 class _RasterizeToPixels(torch.autograd.Function):
     """Tile rasterizer."""
 

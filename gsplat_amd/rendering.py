@@ -19,8 +19,10 @@ import torch.nn.functional as F
 from torch import Tensor
 from typing_extensions import Literal
 
+from .cuda import _ops
 from .cuda._wrapper import (
     CameraModel,
+    _PackedFrontEnd,
     _PackedRowsGather,
     _PackedSphericalHarmonics,
     _project,
@@ -221,13 +223,42 @@ def rasterization(
     if extra_signals is not None:
         check_features(extra_signals, extra_signals_sh_degree, "extra signals")
 
-    proj_results = _project(
-        means, covars, quats, scales, viewmats, Ks, width, height, eps2d,
-        near_plane, far_plane, radius_clip, packed, sparse_grad,
-        rasterize_mode == "antialiased", camera_model, opacities,
-    )
+    colors_sh_degree = sh_degree if has_color else None
+    proj_features = None
+    per_gaussian_colors = has_color and (
+        colors.shape[:num_batch_dims + 1] == batch_dims + (N,)
+        and colors.dim() == num_batch_dims + (2 if colors_sh_degree is None else 3))
+    fused_packed = (packed and extra_signals is None and has_color
+                    and per_gaussian_colors and not viewmats.requires_grad)
+    # projection, row opacities and row colours in one node (sparse_grad
+    # keeps the reference's separate projection with its sparse gradients)
+    front_end = fused_packed and not sparse_grad
+    tile_width = math.ceil(width / float(tile_size))
+    tile_height = math.ceil(height / float(tile_size))
+    # the sorted tile intersection is started inside the front end when the
+    # row opacities are final (no compensation factor)
+    isect_req = ({"tile_size": tile_size, "tile_width": tile_width,
+                  "tile_height": tile_height}
+                 if front_end and rasterize_mode != "antialiased" else None)
     row_of = None
-    if packed:
+    if front_end:
+        (batch_ids, camera_ids, gaussian_ids, indptr, radii, means2d, depths,
+         conics, compensations, row_of, opacities, proj_features) = _PackedFrontEnd.apply(
+            means.contiguous(), None if covars is None else covars.contiguous(),
+            None if quats is None else quats.contiguous(),
+            None if scales is None else scales.contiguous(),
+            opacities.contiguous(), colors.contiguous(), viewmats.contiguous(),
+            Ks.contiguous(), width, height, eps2d, near_plane, far_plane,
+            radius_clip, rasterize_mode == "antialiased", camera_model,
+            colors_sh_degree, isect_req)
+        nnz = means2d.shape[0]
+        image_ids = camera_ids if B * C == 1 else batch_ids * C + camera_ids
+    elif packed:
+        proj_results = _project(
+            means, covars, quats, scales, viewmats, Ks, width, height, eps2d,
+            near_plane, far_plane, radius_clip, packed, sparse_grad,
+            rasterize_mode == "antialiased", camera_model, opacities,
+        )
         (batch_ids, camera_ids, gaussian_ids, indptr, radii, means2d, depths,
          conics, compensations, row_of) = proj_results
         nnz = means2d.shape[0]
@@ -238,7 +269,11 @@ def rasterization(
         # with one image every row's image id is 0 (= camera_ids)
         image_ids = camera_ids if B * C == 1 else batch_ids * C + camera_ids
     else:
-        radii, means2d, depths, conics, compensations = proj_results
+        radii, means2d, depths, conics, compensations = _project(
+            means, covars, quats, scales, viewmats, Ks, width, height, eps2d,
+            near_plane, far_plane, radius_clip, packed, sparse_grad,
+            rasterize_mode == "antialiased", camera_model, opacities,
+        )
         opacities = torch.broadcast_to(opacities[..., None, :], batch_dims + (C, N))
         batch_ids = camera_ids = gaussian_ids = indptr = None
         image_ids = None
@@ -250,14 +285,9 @@ def rasterization(
         "depths": depths, "conics": conics, "opacities": opacities,
     })
 
-    colors_sh_degree = sh_degree if has_color else None
-    proj_features = None
-    per_gaussian_colors = has_color and (
-        colors.shape[:num_batch_dims + 1] == batch_dims + (N,)
-        and colors.dim() == num_batch_dims + (2 if colors_sh_degree is None else 3))
-    fused_packed = (packed and extra_signals is None and has_color
-                    and per_gaussian_colors and not viewmats.requires_grad)
-    if fused_packed:
+    if front_end:
+        pass  # row colours came with the projection
+    elif fused_packed:
         # packed rows with per-Gaussian colours: gather (or SH-evaluate) per
         # Gaussian through row_of instead of indexing [nnz, ...] copies
         if colors_sh_degree is None:
@@ -321,13 +351,15 @@ def rasterization(
                 backgrounds = torch.zeros((*batch_dims, C, 1), device=backgrounds.device)
     assert proj_features is not None
 
-    tile_width = math.ceil(width / float(tile_size))
-    tile_height = math.ceil(height / float(tile_size))
-    tiles_per_gauss, isect_ids, flatten_ids = isect_tiles(
-        means2d, radii, depths, tile_size, tile_width, tile_height,
-        segmented=segmented, packed=packed, n_images=I, image_ids=image_ids,
-        gaussian_ids=gaussian_ids, conics=conics, opacities=opacities,
-    )
+    if isect_req is not None and "state" in isect_req:
+        tiles_per_gauss, isect_ids, flatten_ids = _ops.isect_emit_sorted(
+            isect_req.pop("state"))
+    else:
+        tiles_per_gauss, isect_ids, flatten_ids = isect_tiles(
+            means2d, radii, depths, tile_size, tile_width, tile_height,
+            segmented=segmented, packed=packed, n_images=I, image_ids=image_ids,
+            gaussian_ids=gaussian_ids, conics=conics, opacities=opacities,
+        )
     isect_offsets = isect_offset_encode(isect_ids, I, tile_width, tile_height)
     isect_offsets = isect_offsets.reshape(batch_dims + (C, tile_height, tile_width))
     meta.update({

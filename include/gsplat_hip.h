@@ -115,7 +115,10 @@ size_t gsplat_projection_packed_workspace_size(int64_t B, int64_t C, int64_t N);
  * written (nnz) is stored to nnz_out (device int64).  indptr [B*C+1] int32;
  * batch_ids, camera_ids, gaussian_ids int64.  row_of [B*C*N] int32
  * (optional) receives, for every (b, c, g), its packed row or -1: the inverse
- * of (batch_ids, camera_ids, gaussian_ids), used by the gathers below. */
+ * of (batch_ids, camera_ids, gaussian_ids), used by the gathers below.
+ * row_opacities [B*C*N] (optional, needs opacities) receives each row's
+ * opacities[b, g], the reference's opacities[batch_ids, gaussian_ids]
+ * (gsplat/rendering.py:782). */
 int gsplat_projection_packed_fwd(
     int64_t B, int64_t C, int64_t N,
     const float *means, const float *covars, const float *quats,
@@ -128,7 +131,7 @@ int gsplat_projection_packed_fwd(
     int32_t *indptr, int64_t *batch_ids, int64_t *camera_ids,
     int64_t *gaussian_ids, int32_t *radii, float *means2d, float *depths,
     float *conics, float *compensations, int64_t *nnz_out, int32_t *row_of,
-    gsplat_stream_t stream);
+    float *row_opacities, gsplat_stream_t stream);
 
 /* Backward of the packed projection over nnz rows.
  * Replaces projection_ewa_3dgs_packed_bwd
@@ -165,7 +168,10 @@ int gsplat_projection_packed_bwd(
  * wanted).  v_viewmats [B,C,4,4] (optional) must be zero-filled.
  * Same result as gsplat_projection_packed_bwd with sparse_grad == 0
  * (gsplat/cuda/csrc/Projection.cpp:439-576); used by rasterization() where
- * the row map is at hand. */
+ * the row map is at hand.  Optional: v_row_opacities [nnz] with v_opacities
+ * [B,N] receives each Gaussian's sum over its rows (the backward of the
+ * row opacity gather), and v_means_add [B,N,3] is added to v_means (e.g.
+ * the SH direction term); both are written densely. */
 int gsplat_projection_packed_bwd_rows(
     int64_t B, int64_t C, int64_t N,
     const float *means, const float *covars, const float *quats,
@@ -176,7 +182,8 @@ int gsplat_projection_packed_bwd_rows(
     const float *v_means2d, const float *v_depths, const float *v_conics,
     const float *v_compensations,
     float *v_means, float *v_covars, float *v_quats, float *v_scales,
-    float *v_viewmats,
+    float *v_viewmats, const float *v_row_opacities, float *v_opacities,
+    const float *v_means_add,
     gsplat_stream_t stream);
 
 /* Covariance and/or precision matrices from quaternions and scales.
