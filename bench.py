@@ -39,6 +39,8 @@ def _parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=1, choices=[0, 1, 2, 3, 4])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra-ops", action="store_true",
+                    help="skip the timing of the ops outside the step (profiling runs)")
     ap.add_argument("--cpu-tile-stride", type=int, default=0,
                     help="rasterize every k-th tile in the CPU baseline (0: auto)")
     ap.add_argument("--stages-only", action="store_true",
@@ -235,7 +237,7 @@ def _gpu_bench(args):
         "ms_per_step": ms_per_step,
         "roofline": roofline,
         "stages": stage_report,
-        "extra_ops": _extra_ops(scene, meta, ctx),
+        "extra_ops": None if args.no_extra_ops else _extra_ops(scene, meta, ctx),
         "ctx": ctx,
         "scene": scene,
     }

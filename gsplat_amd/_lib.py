@@ -69,6 +69,9 @@ _SIGNATURES = {
     "gsplat_isect_emit_sorted": [
         c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int32, c_int32,
         c_int32, _P, _P, _P, c_int64, _P, c_size_t, _P, _P, _P],
+    "gsplat_isect_emit_sorted_dev": [
+        c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int32, c_int32,
+        c_int32, _P, _P, _P, c_int64, _P, c_size_t, _P, _P, _P],
     "gsplat_sort_pairs_workspace_size": [c_int64],
     "gsplat_sort_pairs_u64_u32": [
         c_int64, c_int32, _P, _P, _P, _P, _P, c_size_t, _P],

@@ -351,11 +351,13 @@ int radix_sort_ping_pong(int64_t n, int begin_bit, int end_bit, uint64_t *keys_a
 // The same sort on (uint32 key, uint32 value) pairs, key bits [0, num_bits),
 // num_bits <= 32.  With keys64_out (and low_bits) the last pass writes the
 // keys as (key << 32 | low_bits[value]) into keys64_out instead of the key
-// buffer.
+// buffer.  With n_dev the number of keys is min(n, *n_dev), read on the
+// device: n is then a capacity that sizes the launches and the workspace.
 int radix_sort_u32(int64_t n, int num_bits, uint32_t *keys_a, uint32_t *vals_a,
                    uint32_t *keys_b, uint32_t *vals_b, void *workspace,
                    size_t workspace_bytes, hipStream_t st, bool *result_in_b,
-                   const uint32_t *low_bits, uint64_t *keys64_out);
+                   const uint32_t *low_bits, uint64_t *keys64_out,
+                   const int64_t *n_dev = nullptr);
 int copy_u32(int64_t n, const uint32_t *src, uint32_t *dst, hipStream_t st);
 int copy_pairs(int64_t n, const uint64_t *ks, const uint32_t *vs, uint64_t *kd,
                uint32_t *vd, hipStream_t st);

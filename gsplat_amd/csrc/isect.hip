@@ -572,11 +572,13 @@ enum { kRowRminX, kRowRmaxX, kRowRminY, kRowRmaxY, kRowJ, kRowFlags,
 // c * kEmitSlots (rows without tiles own no slot).
 __global__ void __launch_bounds__(kIsectThreads)
     emit_chunk_first_kernel(int64_t n, const int64_t *__restrict__ dstart,
-                            int32_t *__restrict__ chunk_first) {
+                            int64_t cap, int32_t *__restrict__ chunk_first) {
     const int64_t i = (int64_t)blockIdx.x * kIsectThreads + threadIdx.x;
     if (i >= n)
         return;
-    const int64_t lo = dstart[i], hi = dstart[i + 1];
+    // slots at or past the capacity are not emitted (cap >= dstart[n] on
+    // the exact path)
+    const int64_t lo = dstart[i], hi = min(dstart[i + 1], cap);
     for (int64_t c = (lo + kEmitSlots - 1) / kEmitSlots; c * kEmitSlots < hi; ++c)
         chunk_first[c] = (int32_t)i;
 }
@@ -587,7 +589,8 @@ __global__ void __launch_bounds__(kIsectThreads)
                             const int64_t *__restrict__ dstart,
                             const RowRec *__restrict__ recs,
                             const int32_t *__restrict__ chunk_first,
-                            int64_t n_isects, uint32_t *__restrict__ isect_keys,
+                            int64_t n_isects, const int64_t *__restrict__ n_dev,
+                            uint32_t *__restrict__ isect_keys,
                             uint32_t *__restrict__ flatten_ids) {
     __shared__ float s_f[kEmitWaves][kRowFloats][kWave];
     __shared__ int32_t s_i[kEmitWaves][kRowInts][kWave];
@@ -602,6 +605,8 @@ __global__ void __launch_bounds__(kIsectThreads)
     const int lane = (int)lane_id();
     const int64_t chunk = (int64_t)blockIdx.x * kEmitWaves + wave;
     const int64_t S = chunk * kEmitSlots;
+    if (n_dev != nullptr)  // count on the device, n_isects the capacity
+        n_isects = min(n_isects, *n_dev);
     if (S >= n_isects)
         return;
     const int64_t E = n_isects < S + kEmitSlots ? n_isects : S + kEmitSlots;
@@ -1024,16 +1029,15 @@ extern "C" size_t gsplat_isect_emit_sorted_workspace_size(int64_t n_isects) {
     return emit_layout(n_isects > 0 ? n_isects : 0).total;
 }
 
-extern "C" int gsplat_isect_emit_sorted(
+static int emit_sorted_impl(
     int64_t n, int64_t N, int64_t I, const int64_t *image_ids,
     const float *means2d, const int32_t *radii, const float *depths,
     const float *conics, const float *opacities, int32_t tile_size,
     int32_t tile_width, int32_t tile_height, const int32_t *depth_order,
     const int64_t *depth_starts, const float *row_records, int64_t n_isects,
-    void *workspace,
+    const int64_t *n_dev, void *workspace,
     size_t workspace_bytes, int64_t *isect_ids, int32_t *flatten_ids,
     gsplat_stream_t stream) {
-    clear_error();
     IsectArgs a;
     GS_TRY(make_args(n, N, I, image_ids, means2d, radii, depths, conics,
                      opacities, tile_size, tile_width, tile_height, a));
@@ -1071,20 +1075,56 @@ extern "C" int gsplat_isect_emit_sorted(
     hipStream_t st = as_stream(stream);
     int32_t *chunk_first = reinterpret_cast<int32_t *>(ws + L.chunks);
     emit_chunk_first_kernel<<<(unsigned)ceil_div(n, kIsectThreads), kIsectThreads,
-                              0, st>>>(n, depth_starts, chunk_first);
+                              0, st>>>(n, depth_starts, n_isects, chunk_first);
     GS_TRY(check_launch("emit_chunk_first_kernel"));
     const int64_t chunks = ceil_div(n_isects, kEmitSlots);
     isect_emit_depth_kernel<<<(unsigned)ceil_div(chunks, kEmitWaves),
                               kIsectThreads, 0, st>>>(
         a, reinterpret_cast<const uint32_t *>(depth_order), depth_starts,
-        reinterpret_cast<const RowRec *>(row_records), chunk_first, n_isects, ka,
-        va);
+        reinterpret_cast<const RowRec *>(row_records), chunk_first, n_isects,
+        n_dev, ka, va);
     GS_TRY(check_launch("isect_emit_depth_kernel"));
     bool in_b = false;
     GS_TRY(radix_sort_u32(n_isects, key_bits, ka, va, kb, vb, ws + L.sort_ws,
                           workspace_bytes - L.sort_ws, st, &in_b,
                           reinterpret_cast<const uint32_t *>(depths),
-                          reinterpret_cast<uint64_t *>(isect_ids)));
+                          reinterpret_cast<uint64_t *>(isect_ids), n_dev));
     GS_REQUIRE((in_b ? vb : va) == out_vals, "isect_emit_sorted: pass parity");
     return GSPLAT_OK;
+}
+
+extern "C" int gsplat_isect_emit_sorted(
+    int64_t n, int64_t N, int64_t I, const int64_t *image_ids,
+    const float *means2d, const int32_t *radii, const float *depths,
+    const float *conics, const float *opacities, int32_t tile_size,
+    int32_t tile_width, int32_t tile_height, const int32_t *depth_order,
+    const int64_t *depth_starts, const float *row_records, int64_t n_isects,
+    void *workspace,
+    size_t workspace_bytes, int64_t *isect_ids, int32_t *flatten_ids,
+    gsplat_stream_t stream) {
+    clear_error();
+    return emit_sorted_impl(n, N, I, image_ids, means2d, radii, depths, conics,
+                            opacities, tile_size, tile_width, tile_height,
+                            depth_order, depth_starts, row_records, n_isects,
+                            nullptr, workspace, workspace_bytes, isect_ids,
+                            flatten_ids, stream);
+}
+
+extern "C" int gsplat_isect_emit_sorted_dev(
+    int64_t n, int64_t N, int64_t I, const int64_t *image_ids,
+    const float *means2d, const int32_t *radii, const float *depths,
+    const float *conics, const float *opacities, int32_t tile_size,
+    int32_t tile_width, int32_t tile_height, const int32_t *depth_order,
+    const int64_t *depth_starts, const float *row_records, int64_t capacity,
+    void *workspace,
+    size_t workspace_bytes, int64_t *isect_ids, int32_t *flatten_ids,
+    gsplat_stream_t stream) {
+    clear_error();
+    GS_REQUIRE(depth_starts != nullptr, "isect_emit_sorted_dev: NULL depth_starts");
+    // the intersection count is depth_starts[n], read by the kernels
+    return emit_sorted_impl(n, N, I, image_ids, means2d, radii, depths, conics,
+                            opacities, tile_size, tile_width, tile_height,
+                            depth_order, depth_starts, row_records, capacity,
+                            depth_starts + n, workspace, workspace_bytes,
+                            isect_ids, flatten_ids, stream);
 }

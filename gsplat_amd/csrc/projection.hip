@@ -349,7 +349,7 @@ __global__ void __launch_bounds__(kPackThreads) projection_packed_fwd_kernel(
     int64_t *__restrict__ nnz_out, int32_t *__restrict__ row_of,
     float *__restrict__ row_opacities) {
     constexpr int NW = kPackThreads / kWave;
-    static_assert(kPackItems * NW == kWave, "one wave scans the wave counts");
+    static_assert(kPackItems * NW <= kWave, "one wave scans the wave counts");
     __shared__ uint32_t s_ticket;
     __shared__ uint32_t s_cnt[kPackItems * NW];  // survivors per (slice, wave)
     __shared__ uint32_t s_off[kPackItems * NW];  // their exclusive prefix
@@ -433,9 +433,10 @@ __global__ void __launch_bounds__(kPackThreads) projection_packed_fwd_kernel(
     // survivors before each (slice, wave) in row order, and the block's
     // output offset
     if (wave == 0) {
-        const uint32_t c = s_cnt[lane];
+        const uint32_t c = lane < (uint32_t)(kPackItems * NW) ? s_cnt[lane] : 0u;
         const uint32_t inc = (uint32_t)wave_inclusive_scan_u64(c);
-        s_off[lane] = inc - c;
+        if (lane < (uint32_t)(kPackItems * NW))
+            s_off[lane] = inc - c;
         const uint32_t total = __shfl(inc, kWave - 1);
         const uint64_t excl = lb_exclusive_prefix(lb, bid, total);
         if (lane == 0) {

@@ -114,10 +114,13 @@ __device__ __forceinline__ uint32_t block_exclusive_u32(uint32_t v,
 template <int ITEMS, typename K>
 __global__ void __launch_bounds__(kSortThreads)
     radix_hist_kernel(const K *__restrict__ keys, int64_t n, int shift,
-                      int bits, uint32_t *__restrict__ hist) {
+                      int bits, uint32_t *__restrict__ hist,
+                      const int64_t *__restrict__ n_dev) {
     constexpr int kSortItems = ITEMS;
     constexpr int kSortTile = kSortThreads * ITEMS;
     __shared__ uint32_t s_cnt[kSortWaves][kRadix];
+    if (n_dev != nullptr)  // key count on the device, n the capacity
+        n = min(n, *n_dev);
     const uint32_t mask = (1u << bits) - 1u;
     for (int i = threadIdx.x; i < kSortWaves * kRadix; i += kSortThreads)
         (&s_cnt[0][0])[i] = 0u;
@@ -231,8 +234,11 @@ __global__ void __launch_bounds__(kSortThreads)
                          int bits, const uint32_t *__restrict__ prefix,
                          const uint32_t *__restrict__ totals,
                          const uint32_t *__restrict__ low_bits,
-                         uint64_t *__restrict__ keys64_out) {
+                         uint64_t *__restrict__ keys64_out,
+                         const int64_t *__restrict__ n_dev) {
     constexpr int kSortItems = ITEMS;
+    if (n_dev != nullptr)  // key count on the device, n the capacity
+        n = min(n, *n_dev);
     constexpr int kSortTile = kSortThreads * ITEMS;
     __shared__ K s_keys[kSortTile];
     __shared__ uint32_t s_vals[kSortTile];
@@ -422,7 +428,8 @@ template <typename K>
 int radix_sort_impl(int64_t n, int begin_bit, int end_bit, K *keys_a,
                     uint32_t *vals_a, K *keys_b, uint32_t *vals_b, void *workspace,
                     size_t workspace_bytes, hipStream_t st, bool *result_in_b,
-                    const uint32_t *low_bits, uint64_t *keys64_out) {
+                    const uint32_t *low_bits, uint64_t *keys64_out,
+                    const int64_t *n_dev) {
     *result_in_b = false;
     const int num_bits = end_bit - begin_bit;
     if (n == 0 || num_bits <= 0)
@@ -446,20 +453,22 @@ int radix_sort_impl(int64_t n, int begin_bit, int end_bit, K *keys_a,
         uint64_t *k64 = p == passes - 1 ? keys64_out : nullptr;
         if (small)
             radix_hist_kernel<kSortItemsSmall, K><<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
-                ksrc, n, shift, bits, hist);
+                ksrc, n, shift, bits, hist, n_dev);
         else
             radix_hist_kernel<kSortItemsLarge, K><<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
-                ksrc, n, shift, bits, hist);
+                ksrc, n, shift, bits, hist, n_dev);
         GS_TRY(check_launch("radix_hist_kernel"));
         radix_colscan_kernel<<<kRadix / kColDigits, kSortThreads, 0, st>>>(
             hist, L.n_tiles, prefix, totals);
         GS_TRY(check_launch("radix_colscan_kernel"));
         if (small)
             radix_scatter_kernel<kSortItemsSmall, K><<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
-                ksrc, vsrc, kdst, vdst, n, shift, bits, prefix, totals, low_bits, k64);
+                ksrc, vsrc, kdst, vdst, n, shift, bits, prefix, totals, low_bits, k64,
+                n_dev);
         else
             radix_scatter_kernel<kSortItemsLarge, K><<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
-                ksrc, vsrc, kdst, vdst, n, shift, bits, prefix, totals, low_bits, k64);
+                ksrc, vsrc, kdst, vdst, n, shift, bits, prefix, totals, low_bits, k64,
+                n_dev);
         GS_TRY(check_launch("radix_scatter_kernel"));
         shift += bits;
         K *tk = ksrc; ksrc = kdst; kdst = tk;
@@ -475,19 +484,20 @@ int radix_sort_ping_pong(int64_t n, int begin_bit, int end_bit, uint64_t *keys_a
                          hipStream_t st, bool *result_in_b) {
     return radix_sort_impl<uint64_t>(n, begin_bit, end_bit, keys_a, vals_a, keys_b,
                                      vals_b, workspace, workspace_bytes, st,
-                                     result_in_b, nullptr, nullptr);
+                                     result_in_b, nullptr, nullptr, nullptr);
 }
 
 int radix_sort_u32(int64_t n, int num_bits, uint32_t *keys_a, uint32_t *vals_a,
                    uint32_t *keys_b, uint32_t *vals_b, void *workspace,
                    size_t workspace_bytes, hipStream_t st, bool *result_in_b,
-                   const uint32_t *low_bits, uint64_t *keys64_out) {
+                   const uint32_t *low_bits, uint64_t *keys64_out,
+                   const int64_t *n_dev) {
     GS_REQUIRE(num_bits >= 0 && num_bits <= 32, "radix sort: num_bits in [0, 32]");
     GS_REQUIRE(keys64_out == nullptr || (low_bits != nullptr && num_bits > 0),
                "radix sort: 64-bit output needs low bits and at least one pass");
     return radix_sort_impl<uint32_t>(n, 0, num_bits, keys_a, vals_a, keys_b, vals_b,
                                      workspace, workspace_bytes, st, result_in_b,
-                                     low_bits, keys64_out);
+                                     low_bits, keys64_out, n_dev);
 }
 
 int copy_pairs(int64_t n, const uint64_t *ks, const uint32_t *vs, uint64_t *kd,

@@ -347,10 +347,14 @@ def packed_front_fwd(
                 else:
                     img = (camera_ids[:nnz] if B == 1
                            else batch_ids[:nnz] * C + camera_ids[:nnz])
-                isect["state"] = isect_prepare_sorted(
+                state = isect_prepare_sorted(
                     means2d[:nnz], radii[:nnz], depths[:nnz], conics[:nnz],
                     row_opac[:nnz], img, nnz if I == 1 else 0, I, ts, tw, th,
                     torch.empty(nnz, dtype=_I32, device=dev))
+                cap = isect_capacity(dev)
+                if cap is not None:
+                    isect_emit_sorted_queue(state, cap)
+                isect["state"] = state
     return (
         indptr,
         batch_ids[:nnz],
@@ -638,6 +642,38 @@ def intersect_tile(
     return tiles_per_gauss, isect_ids, flatten_ids
 
 
+# Intersection count of the last sorted intersection per device: the next
+# call queues its emission for this many plus 1/16 (and 4096) before the
+# host knows its own count.
+_ISECT_LAST = {}
+
+
+def isect_capacity(device: torch.device) -> Optional[int]:
+    """Capacity for a device-counted emission (None before the first count)."""
+    last = _ISECT_LAST.get(device.index)
+    return None if last is None else last + last // 16 + 4096
+
+
+def isect_emit_sorted_queue(state, capacity: int) -> None:
+    """Queues the second half of the sorted intersection behind the first
+    with the count read on the device (gsplat_isect_emit_sorted_dev), into
+    buffers of ``capacity`` entries; ``isect_emit_sorted`` then only checks
+    the count against the capacity."""
+    dev = state["means2d"].device
+    isect_ids = torch.empty(capacity, dtype=_I64, device=dev)
+    flatten_ids = torch.empty(capacity, dtype=_I32, device=dev)
+    ts, tw, th = state["tile"]
+    ews = torch.empty(query("gsplat_isect_emit_sorted_workspace_size", capacity),
+                      dtype=torch.uint8, device=dev)
+    call("gsplat_isect_emit_sorted_dev", state["n"], state["N"], state["I"],
+         ptr(state["img"]), ptr(state["means2d"]), ptr(state["radii"]),
+         ptr(state["depths"]), ptr(state["conics"]), ptr(state["opacities"]), ts, tw,
+         th, ptr(state["depth_order"]), ptr(state["depth_starts"]),
+         ptr(state["records"]), int(capacity), ptr(ews), ews.numel(), ptr(isect_ids),
+         ptr(flatten_ids), _stream(state["means2d"]))
+    state["queued"] = (int(capacity), isect_ids, flatten_ids)
+
+
 def isect_prepare_sorted(means2d, radii, depths, conics, opacities, img, N, I,
                          tile_size, tile_width, tile_height, tiles_per_gauss):
     """First half of the sorted intersection of n > 0 rows (inputs checked by
@@ -682,6 +718,12 @@ def isect_emit_sorted(state):
     ev.synchronize()
     n_isects = int(host[0])
     dev = state["means2d"].device
+    _ISECT_LAST[dev.index] = n_isects
+    queued = state.get("queued")
+    if queued is not None and n_isects <= queued[0]:
+        return state["tiles_per_gauss"], queued[1][:n_isects], queued[2][:n_isects]
+    # no queued emission, or more intersections than it had room for (its
+    # output is dropped): emit with the exact count
     isect_ids = torch.empty(n_isects, dtype=_I64, device=dev)
     flatten_ids = torch.empty(n_isects, dtype=_I32, device=dev)
     if n_isects == 0:

@@ -353,6 +353,27 @@ int gsplat_isect_emit_sorted(
     void *workspace, size_t workspace_bytes,
     int64_t *isect_ids, int32_t *flatten_ids, gsplat_stream_t stream);
 
+/* Stage 2 with the intersection count read on the device
+ * (depth_starts[n], written by stage 1), so the caller can queue it right
+ * behind stage 1 without waiting for the count on the host.  Same inputs
+ * as gsplat_isect_emit_sorted, with `capacity` in place of n_isects:
+ * isect_ids and flatten_ids hold capacity entries, the workspace is
+ * gsplat_isect_emit_sorted_workspace_size(capacity), and the first
+ * min(n_isects, capacity) entries are written.  When n_isects <= capacity
+ * they equal gsplat_isect_emit_sorted's output; otherwise the caller must
+ * run gsplat_isect_emit_sorted with room for n_isects.  No reference
+ * counterpart: the reference reads the count on the host between the two
+ * stages (gsplat/cuda/csrc/Intersect.cpp:104-122). */
+int gsplat_isect_emit_sorted_dev(
+    int64_t n, int64_t N, int64_t I, const int64_t *image_ids,
+    const float *means2d, const int32_t *radii, const float *depths,
+    const float *conics, const float *opacities,
+    int32_t tile_size, int32_t tile_width, int32_t tile_height,
+    const int32_t *depth_order, const int64_t *depth_starts,
+    const float *row_records, int64_t capacity,
+    void *workspace, size_t workspace_bytes,
+    int64_t *isect_ids, int32_t *flatten_ids, gsplat_stream_t stream);
+
 /* Bytes of workspace gsplat_sort_pairs_u64_u32 needs for n pairs. */
 size_t gsplat_sort_pairs_workspace_size(int64_t n);
 

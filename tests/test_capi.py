@@ -39,7 +39,7 @@ def test_header_declares_the_survey_export_list():
                      "gsplat_adam", "gsplat_quat_scale_to_covar_preci_fwd",
                      "gsplat_quat_scale_to_covar_preci_bwd",
                      "gsplat_rasterize_to_indices_count",
-                     "gsplat_rasterize_to_indices_write"]:
+                     "gsplat_rasterize_to_indices_write", "gsplat_isect_emit_sorted_dev"]:
         assert required in names, required
 
 

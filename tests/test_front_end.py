@@ -127,3 +127,56 @@ def test_front_end_matches_separate_nodes(case):
     for k in gf:
         assert gf[k] is not None and gs_[k] is not None, k
         assert torch.equal(gf[k], gs_[k]), (k, (gf[k] - gs_[k]).abs().max().item())
+
+
+def test_queued_emission_matches_exact_and_falls_back():
+    """rasterization() three times on one scene: the first call emits the
+    intersections with the count read on the host, the second queues the
+    emission with the count read on the device (capacity from the first
+    count), the third is given a capacity below the count and must fall back
+    to the exact emission.  All three give the same intersections and
+    renders."""
+    import gsplat_amd as gs
+    from gsplat_amd.cuda import _ops
+
+    means, quats, scales, opac, vm, K, W, H = small_scene(seed=5, N=6000, C=1, W=320,
+                                                          H=240)
+    g = torch.Generator().manual_seed(9)
+    coeffs = (torch.randn(6000, 16, 3, generator=g) * 0.3).to(DEV)
+    args = [t.to(DEV) for t in (means, quats, scales, opac)]
+    names = []
+    real_call = _ops.call
+
+    def spy(name, *a):
+        names.append(name)
+        return real_call(name, *a)
+
+    def render():
+        names.clear()
+        rc, ra, meta = gs.rasterization(*args, coeffs, vm.to(DEV), K.to(DEV), W, H,
+                                        sh_degree=3, packed=True)
+        return rc, ra, meta, list(names)
+
+    dev = torch.device(DEV)
+    _ops._ISECT_LAST.pop(dev.index if dev.index is not None else 0, None)
+    _ops._ISECT_LAST.pop(torch.cuda.current_device(), None)
+    _ops.call = spy
+    try:
+        out = [render()]
+        n = out[0][2]["isect_ids"].numel()
+        assert n > 5000
+        out.append(render())
+        _ops._ISECT_LAST[torch.cuda.current_device()] = 10  # capacity 4107 < n
+        out.append(render())
+    finally:
+        _ops.call = real_call
+    assert "gsplat_isect_emit_sorted_dev" not in out[0][3]
+    assert "gsplat_isect_emit_sorted_dev" in out[1][3]
+    assert "gsplat_isect_emit_sorted" not in out[1][3]
+    assert "gsplat_isect_emit_sorted_dev" in out[2][3]
+    assert "gsplat_isect_emit_sorted" in out[2][3]
+    for rc, ra, meta, _ in out[1:]:
+        for k in ("isect_ids", "flatten_ids", "isect_offsets"):
+            assert torch.equal(meta[k], out[0][2][k]), k
+        assert torch.equal(rc, out[0][0])
+        assert torch.equal(ra, out[0][1])
