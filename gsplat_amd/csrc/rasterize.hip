@@ -383,9 +383,8 @@ template <int CDIM, int TILE, bool ABS> struct BwdSmem {
     float col[NB * CDIM];
     float acc[NACC * NB];
     int32_t gid[NB];
-    int32_t hit[NB];
     uint8_t wmask[NB];        // waves a Gaussian can reach
-    uint16_t list[NW][NB];    // per-wave work list
+    uint8_t list[NW][NB];     // per-wave work list (slots < 256)
     int32_t tile_bin;
     int64_t next_tile;
 };
@@ -412,7 +411,6 @@ __device__ __forceinline__ void rasterize_bwd_tile(
     float *s_col = sm.col;
     float *s_acc = sm.acc;
     int32_t *s_gid = sm.gid;
-    int32_t *s_hit = sm.hit;
     uint8_t *s_wmask = sm.wmask;
     auto &s_list = sm.list;
     int32_t &s_tile_bin = sm.tile_bin;
@@ -424,7 +422,6 @@ __device__ __forceinline__ void rasterize_bwd_tile(
     if (a.masks != nullptr && !a.masks[image * n_tiles + tile])
         return;
     const int tr = threadIdx.x;
-    const bool last_lane = lane_id() == (uint32_t)SH::LAST;
     const int wave = tr / kWave;
 
     const int32_t *offs = a.tile_offsets + image * n_tiles;
@@ -534,7 +531,6 @@ __device__ __forceinline__ void rasterize_bwd_tile(
             } else {
                 s_wmask[slot] = 0;
             }
-            s_hit[slot] = 0;
 #pragma unroll
             for (int k = 0; k < NACC; ++k)
                 s_acc[slot * NACC + k] = 0.f;
@@ -654,28 +650,35 @@ __device__ __forceinline__ void rasterize_bwd_tile(
             for (int f = 0; f < RR::N4; ++f)
                 if (red_slot[f] >= 0)
                     atomicAdd(&s_acc[t * NACC + red_slot[f]], red[f]);
-            if (last_lane)
-                s_hit[t] = 1;
         }
         __syncthreads();
 #pragma unroll
         for (int q = 0; q < SLOTS; ++q) {
             const int slot = tr + q * NT;
-            if (slot < batch_size && s_hit[slot]) {
+            // a sum that is zero (a Gaussian no pixel took, or a term that
+            // vanished) adds nothing and is skipped
+            if (slot < batch_size) {
                 const int32_t g = s_gid[slot];
-                const float *acc = s_acc + slot * NACC;
-                atomic_add_f32(v_means2d + (int64_t)g * 2 + 0, acc[0]);
-                atomic_add_f32(v_means2d + (int64_t)g * 2 + 1, acc[1]);
-                atomic_add_f32(v_conics + (int64_t)g * 3 + 0, acc[2]);
-                atomic_add_f32(v_conics + (int64_t)g * 3 + 1, acc[3]);
-                atomic_add_f32(v_conics + (int64_t)g * 3 + 2, acc[4]);
+                float acc[NACC];
+#pragma unroll
+                for (int k = 0; k < NACC; ++k)
+                    acc[k] = s_acc[slot * NACC + k];
+                auto add = [](float *p, float v) {
+                    if (v != 0.f)
+                        atomic_add_f32(p, v);
+                };
+                add(v_means2d + (int64_t)g * 2 + 0, acc[0]);
+                add(v_means2d + (int64_t)g * 2 + 1, acc[1]);
+                add(v_conics + (int64_t)g * 3 + 0, acc[2]);
+                add(v_conics + (int64_t)g * 3 + 1, acc[3]);
+                add(v_conics + (int64_t)g * 3 + 2, acc[4]);
 #pragma unroll
                 for (int k = 0; k < CDIM; ++k)
-                    atomic_add_f32(v_colors + (int64_t)g * CDIM + k, acc[5 + k]);
-                atomic_add_f32(v_opacities + g, acc[5 + CDIM]);
+                    add(v_colors + (int64_t)g * CDIM + k, acc[5 + k]);
+                add(v_opacities + g, acc[5 + CDIM]);
                 if constexpr (ABS) {
-                    atomic_add_f32(v_means2d_abs + (int64_t)g * 2 + 0, acc[6 + CDIM]);
-                    atomic_add_f32(v_means2d_abs + (int64_t)g * 2 + 1, acc[7 + CDIM]);
+                    add(v_means2d_abs + (int64_t)g * 2 + 0, acc[6 + CDIM]);
+                    add(v_means2d_abs + (int64_t)g * 2 + 1, acc[7 + CDIM]);
                 }
             }
         }
