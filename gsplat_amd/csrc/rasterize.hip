@@ -151,6 +151,15 @@ template <int TILE> struct TileShape {
     static_assert(BS % 16 == 0, "tile must hold whole 16-lane rows");
 };
 
+// One staged Gaussian of the forward: every field at a constant offset from
+// one slot address, and the intersection index in the word after the
+// colours (the last_ids candidate, read with the colours).
+template <int CDIM> struct FwdSlot {
+    float4 geo;                           // (x, y, opacity, sig_max)
+    float4 con;                           // (a, b, c, sig_clamp)
+    float col[(CDIM + 1 + 3) / 4 * 4];    // CDIM colours, isect index bits, pad
+};
+
 template <int CDIM, int TILE>
 __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
     const RasterArgs a, float *__restrict__ render_colors,
@@ -159,9 +168,7 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
     constexpr int BS = TileShape<TILE>::BS;
     constexpr int NW = (BS + kWave - 1) / kWave;       // waves per tile
     constexpr int WROWS = (kWave < BS ? kWave : BS) / TILE;  // rows per wave
-    __shared__ float4 s_geo[BS];          // (x, y, opacity, sig_max)
-    __shared__ float4 s_con[BS];          // (a, b, c, sig_clamp)
-    __shared__ float s_col[BS * CDIM];
+    __shared__ FwdSlot<CDIM> s_slot[BS];
     __shared__ uint8_t s_wmask[BS];       // waves a Gaussian can reach
     __shared__ uint8_t s_list[NW][BS];    // per-wave work list
 
@@ -221,11 +228,13 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
             alpha_thresholds(o, sig_max, sig_clamp);
             const float ca = a.conics[g * 3 + 0], cb = a.conics[g * 3 + 1],
                         cc = a.conics[g * 3 + 2];
-            s_geo[tr] = make_float4(xy.x, xy.y, o, sig_max);
-            s_con[tr] = make_float4(ca, cb, cc, sig_clamp);
+            FwdSlot<CDIM> &sl = s_slot[tr];
+            sl.geo = make_float4(xy.x, xy.y, o, sig_max);
+            sl.con = make_float4(ca, cb, cc, sig_clamp);
 #pragma unroll
             for (int k = 0; k < CDIM; ++k)
-                s_col[tr * CDIM + k] = a.colors[(int64_t)g * CDIM + k];
+                sl.col[k] = a.colors[(int64_t)g * CDIM + k];
+            sl.col[CDIM] = __int_as_float(idx);
             s_wmask[tr] = (uint8_t)strip_mask<TILE, NW, WROWS>(
                 alpha_support_box(xy.x, xy.y, ca, cb, cc, sig_max), tx, ty);
         }
@@ -241,8 +250,9 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
             if (done_m == lanes_m)
                 break;
             const int t = s_list[wave][n];
-            const float4 geo = s_geo[t];
-            const float4 con = s_con[t];
+            const FwdSlot<CDIM> &sl = s_slot[t];
+            const float4 geo = sl.geo;
+            const float4 con = sl.con;
             const float dx = geo.x - px, dy = geo.y - py;
             const float sigma = gauss_sigma(con.x, con.y, con.z, dx, dy);
             const uint64_t take_m =
@@ -263,8 +273,12 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
             const float w = upd ? alpha * T : 0.f;
 #pragma unroll
             for (int k = 0; k < CDIM; ++k)
-                acc[k] = fmaf(s_col[t * CDIM + k], w, acc[k]);
-            cur_idx = upd ? batch_start + t : cur_idx;
+                acc[k] = fmaf(sl.col[k], w, acc[k]);
+            // read unconditionally: a conditional read becomes another
+            // exec-masked branch around one LDS load
+            int32_t slot_idx = __float_as_int(sl.col[CDIM]);
+            asm volatile("" : "+v"(slot_idx));
+            cur_idx = upd ? slot_idx : cur_idx;
             T = upd ? next_T : T;
             done_m |= take_m & stop_m;
         }
