@@ -499,6 +499,17 @@ def projection_packed_bwd_rows(
         raise RuntimeError("projection_packed_bwd_rows: v_means_add must be shaped like means")
     v_opacities = (torch.empty(means.shape[:-1], dtype=_F32, device=means.device)
                    if v_row_opacities is not None else None)
+    if conics.shape[0] == 0:
+        # no visible row: every gradient is zero (plus the added term); the
+        # empty row buffers have no storage to hand to the kernel
+        for t in (v_means, v_covars, v_quats, v_scales, v_opacities):
+            if t is not None:
+                t.zero_()
+        if v_means_add is not None:
+            v_means.copy_(v_means_add)
+        if v_row_opacities is not None:
+            return v_means, v_covars, v_quats, v_scales, v_viewmats, v_opacities
+        return v_means, v_covars, v_quats, v_scales, v_viewmats
     call("gsplat_projection_packed_bwd_rows", B, C, N, ptr(means), ptr(covars),
          ptr(quats), ptr(scales), ptr(viewmats), ptr(Ks), int(image_width),
          int(image_height), float(eps2d), int(camera_model), ptr(row_of),
@@ -527,6 +538,8 @@ def sh_rows_fwd(degree: int, means: Tensor, viewmats: Tensor, coeffs: Tensor,
     C = viewmats.shape[1]
     K = coeffs.shape[-2]
     colors = torch.empty(nnz, 3, dtype=_F32, device=means.device)
+    if nnz == 0:
+        return colors
     call("gsplat_sh_rows_fwd", B, C, N, K, int(degree), ptr(means), ptr(viewmats),
          ptr(coeffs), ptr(row_of), ptr(colors), _stream(means))
     return colors
@@ -540,6 +553,8 @@ def sh_rows_bwd(degree: int, means: Tensor, viewmats: Tensor, coeffs: Tensor,
     K = coeffs.shape[-2]
     v_coeffs = torch.empty_like(coeffs)
     v_means = torch.empty_like(means)
+    if v_colors.shape[0] == 0:  # no visible row: zero gradients
+        return v_coeffs.zero_(), v_means.zero_()
     call("gsplat_sh_rows_bwd", B, C, N, K, int(degree), ptr(means), ptr(viewmats),
          ptr(coeffs), ptr(row_of), ptr(v_colors), ptr(v_coeffs), ptr(v_means),
          _stream(means))
@@ -552,6 +567,8 @@ def rows_gather(src: Tensor, row_of: Tensor, C: int, nnz: int) -> Tensor:
     check_input(row_of, "row_of", _I32)
     B, N, F = src.shape
     out = torch.empty(nnz, F, dtype=_F32, device=src.device)
+    if nnz == 0:
+        return out
     call("gsplat_rows_gather", B, int(C), N, F, ptr(src), ptr(row_of), ptr(out),
          _stream(src))
     return out
@@ -562,6 +579,8 @@ def rows_scatter_sum(v_out: Tensor, row_of: Tensor, B: int, C: int, N: int) -> T
     check_input(v_out, "v_out", _F32)
     F = v_out.shape[-1]
     v_src = torch.empty(B, N, F, dtype=_F32, device=v_out.device)
+    if v_out.shape[0] == 0:  # no visible row: zero gradients
+        return v_src.zero_()
     call("gsplat_rows_scatter_sum", int(B), int(C), int(N), F, ptr(row_of),
          ptr(v_out), ptr(v_src), _stream(v_out))
     return v_src

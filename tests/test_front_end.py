@@ -180,3 +180,38 @@ def test_queued_emission_matches_exact_and_falls_back():
             assert torch.equal(meta[k], out[0][2][k]), k
         assert torch.equal(rc, out[0][0])
         assert torch.equal(ra, out[0][1])
+
+
+@pytest.mark.parametrize("packed", [True, False])
+def test_rasterization_with_every_gaussian_culled(packed):
+    """Every Gaussian behind the camera: no visible rows and no intersections
+    (the front end's count is 0, the intersection stages are skipped).  The
+    image is the background, alpha 0, and every gradient is zero (the
+    reference's behaviour: nothing composites)."""
+    import gsplat_amd as gs
+    from gsplat_amd.cuda import _ops
+
+    means, quats, scales, opac, vm, K, W, H = small_scene(seed=2, N=500, C=1)
+    means = means.clone()
+    means[:, 2] = means[:, 2] - 100.0  # z of every mean behind the camera
+    g = torch.Generator().manual_seed(3)
+    coeffs = (torch.randn(500, 4, 3, generator=g) * 0.3).to(DEV).requires_grad_()
+    leaves = [t.to(DEV).requires_grad_() for t in (means, quats, scales, opac)]
+    # backgrounds [C, D] only on the dense path: packed rasterize_to_pixels
+    # takes [D] (its image dims are empty), as in the reference
+    # (_wrapper.py:868-885)
+    bg = None if packed else torch.tensor([[0.2, 0.4, 0.6]], device=DEV)
+    for _ in range(2):  # the second call also sees the previous intersection count
+        rc, ra, meta = gs.rasterization(*leaves, coeffs, vm.to(DEV), K.to(DEV), W, H,
+                                        sh_degree=1, packed=packed, backgrounds=bg)
+        if packed:
+            assert meta["means2d"].shape[0] == 0
+        assert meta["isect_ids"].numel() == 0
+        expect = torch.zeros(3, device=DEV) if bg is None else bg.reshape(3)
+        assert torch.equal(rc, expect.expand_as(rc))
+        assert torch.equal(ra, torch.zeros_like(ra))
+        (rc.sum() + ra.sum()).backward()
+        for t in leaves + [coeffs]:
+            assert t.grad is not None and torch.count_nonzero(t.grad) == 0
+            t.grad = None
+    _ops._ISECT_LAST.clear()
