@@ -239,6 +239,10 @@ __global__ void __launch_bounds__(kSortThreads)
     constexpr int kSortItems = ITEMS;
     if (n_dev != nullptr)  // key count on the device, n the capacity
         n = min(n, *n_dev);
+    // workgroups past the device count have no key to move (the whole
+    // workgroup sees the same count, so the return is uniform)
+    if ((int64_t)blockIdx.x * (kSortThreads * ITEMS) >= n)
+        return;
     constexpr int kSortTile = kSortThreads * ITEMS;
     __shared__ K s_keys[kSortTile];
     __shared__ uint32_t s_vals[kSortTile];
