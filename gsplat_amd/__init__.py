@@ -17,6 +17,9 @@ from .cuda._wrapper import (
     has_reloc,
     isect_offset_encode,
     isect_tiles,
+    proj,
+    quat_scale_to_covar_preci,
+    rasterize_to_indices_in_range,
     rasterize_to_pixels,
     spherical_harmonics,
 )
@@ -38,7 +41,10 @@ __all__ = [
     "has_reloc",
     "isect_offset_encode",
     "isect_tiles",
+    "proj",
+    "quat_scale_to_covar_preci",
     "rasterization",
+    "rasterize_to_indices_in_range",
     "rasterize_to_pixels",
     "spherical_harmonics",
     "SelectiveAdam",

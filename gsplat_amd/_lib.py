@@ -22,6 +22,11 @@ _P = c_void_p
 _SIGNATURES = {
     "gsplat_last_error": [],
     "gsplat_version": [],
+    "gsplat_projection_simple_fwd": [
+        c_int64, c_int64, c_int64, _P, _P, _P, c_int32, c_int32, c_int32, _P, _P, _P],
+    "gsplat_projection_simple_bwd": [
+        c_int64, c_int64, c_int64, _P, _P, _P, c_int32, c_int32, c_int32, _P, _P, _P,
+        _P, _P],
     "gsplat_projection_fused_fwd": [
         c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P,
         c_int32, c_int32, c_float, c_float, c_float, c_float, c_int32,

@@ -141,6 +141,20 @@ _IMPLS = {
 }
 
 _SCHEMAS.update({
+    "projection_ewa_simple_fwd":
+        "projection_ewa_simple_fwd(Tensor means, Tensor covars, Tensor Ks, int width, "
+        "int height, int camera_model) -> (Tensor, Tensor)",
+    "projection_ewa_simple_bwd":
+        "projection_ewa_simple_bwd(Tensor means, Tensor covars, Tensor Ks, int width, "
+        "int height, int camera_model, Tensor v_means2d, Tensor v_covars2d) "
+        "-> (Tensor, Tensor)",
+})
+_IMPLS.update({
+    "projection_ewa_simple_fwd": _ops.projection_ewa_simple_fwd,
+    "projection_ewa_simple_bwd": _ops.projection_ewa_simple_bwd,
+})
+
+_SCHEMAS.update({
     "quat_scale_to_covar_preci_fwd":
         "quat_scale_to_covar_preci_fwd(Tensor quats, Tensor scales, bool compute_covar, "
         "bool compute_preci, bool triu) -> (Tensor, Tensor)",

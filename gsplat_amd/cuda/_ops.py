@@ -99,6 +99,43 @@ def _check_proj_inputs(means, covars, quats, scales, opacities, viewmats, Ks):
     check_input(Ks, "Ks", _F32)
 
 
+def projection_ewa_simple_fwd(means: Tensor, covars: Tensor, Ks: Tensor, width: int,
+                              height: int, camera_model: int) -> Tuple[Tensor, Tensor]:
+    """means [..., C, N, 3], covars [..., C, N, 3, 3], Ks [..., C, 3, 3] ->
+    means2d [..., C, N, 2], covars2d [..., C, N, 2, 2] (Projection.cpp:41-80)."""
+    check_input(means, "means", _F32)
+    check_input(covars, "covars", _F32)
+    check_input(Ks, "Ks", _F32)
+    C, N = means.shape[-3], means.shape[-2]
+    B = _prod(means.shape[:-3])
+    lead = tuple(means.shape[:-1])
+    means2d = torch.empty(lead + (2,), dtype=_F32, device=means.device)
+    covars2d = torch.empty(lead + (2, 2), dtype=_F32, device=means.device)
+    call("gsplat_projection_simple_fwd", B, C, N, ptr(means), ptr(covars), ptr(Ks),
+         int(width), int(height), int(camera_model), ptr(means2d), ptr(covars2d),
+         _stream(means))
+    return means2d, covars2d
+
+
+def projection_ewa_simple_bwd(means: Tensor, covars: Tensor, Ks: Tensor, width: int,
+                              height: int, camera_model: int, v_means2d: Tensor,
+                              v_covars2d: Tensor) -> Tuple[Tensor, Tensor]:
+    """Gradients of ``projection_ewa_simple_fwd`` (Projection.cpp:82-127)."""
+    check_input(means, "means", _F32)
+    check_input(covars, "covars", _F32)
+    check_input(Ks, "Ks", _F32)
+    check_input(v_means2d, "v_means2d", _F32)
+    check_input(v_covars2d, "v_covars2d", _F32)
+    C, N = means.shape[-3], means.shape[-2]
+    B = _prod(means.shape[:-3])
+    v_means = torch.empty_like(means)
+    v_covars = torch.empty_like(covars)
+    call("gsplat_projection_simple_bwd", B, C, N, ptr(means), ptr(covars), ptr(Ks),
+         int(width), int(height), int(camera_model), ptr(v_means2d), ptr(v_covars2d),
+         ptr(v_means), ptr(v_covars), _stream(means))
+    return v_means, v_covars
+
+
 def projection_ewa_3dgs_fused_fwd(
     means: Tensor,
     covars: Optional[Tensor],

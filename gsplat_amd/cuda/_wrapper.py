@@ -52,7 +52,8 @@ def _camera_model_type(camera_model: str) -> int:
 
 
 def has_3dgs() -> bool:
-    return hasattr(torch.ops.gsplat, "projection_ewa_3dgs_fused_fwd")
+    # the reference's probe (_wrapper.py:181-184)
+    return hasattr(torch.ops.gsplat, "projection_ewa_simple_fwd")
 
 
 def has_adam() -> bool:
@@ -112,6 +113,28 @@ def spherical_harmonics(
     return _SphericalHarmonics.apply(
         degrees_to_use, dirs.contiguous(), coeffs.contiguous(), masks
     )
+
+
+def proj(
+    means: Tensor,  # [..., C, N, 3]
+    covars: Tensor,  # [..., C, N, 3, 3]
+    Ks: Tensor,  # [..., C, 3, 3]
+    width: int,
+    height: int,
+    camera_model: CameraModel = "pinhole",
+) -> Tuple[Tensor, Tensor]:
+    """Projection of camera-space Gaussians (perspective or orthographic):
+    (means2d [..., C, N, 2], covars2d [..., C, N, 2, 2])."""
+    assert (
+        camera_model != "ftheta"
+    ), "ftheta camera is only supported via UT, please set with_ut=True in the rasterization()"
+    batch_dims = means.shape[:-3]
+    C, N = means.shape[-3:-1]
+    assert means.shape == batch_dims + (C, N, 3), means.shape
+    assert covars.shape == batch_dims + (C, N, 3, 3), covars.shape
+    assert Ks.shape == batch_dims + (C, 3, 3), Ks.shape
+    return _Proj.apply(means.contiguous(), covars.contiguous(), Ks.contiguous(), width,
+                       height, camera_model)
 
 
 def fully_fused_projection(
@@ -442,6 +465,35 @@ def rasterize_to_indices_in_range(
     out_pixel_ids = out_indices % (image_width * image_height)
     out_image_ids = out_indices // (image_width * image_height)
     return out_gauss_ids, out_pixel_ids, out_image_ids
+
+
+class _Proj(torch.autograd.Function):
+    """Autograd node of ``proj`` (reference _wrapper.py:1403-1460)."""
+
+    @staticmethod
+    def forward(ctx, means, covars, Ks, width, height, camera_model="pinhole"):
+        camera_model_type = _camera_model_type(camera_model)
+        means2d, covars2d = _make_lazy_cuda_func("projection_ewa_simple_fwd")(
+            means, covars, Ks, width, height, camera_model_type)
+        ctx.save_for_backward(means, covars, Ks)
+        ctx.width = width
+        ctx.height = height
+        ctx.camera_model_type = camera_model_type
+        return means2d, covars2d
+
+    @staticmethod
+    def backward(ctx, v_means2d, v_covars2d):
+        means, covars, Ks = ctx.saved_tensors
+        if v_means2d is None:
+            v_means2d = torch.zeros(means.shape[:-1] + (2,), dtype=means.dtype,
+                                    device=means.device)
+        if v_covars2d is None:
+            v_covars2d = torch.zeros(means.shape[:-1] + (2, 2), dtype=means.dtype,
+                                     device=means.device)
+        v_means, v_covars = _make_lazy_cuda_func("projection_ewa_simple_bwd")(
+            means, covars, Ks, ctx.width, ctx.height, ctx.camera_model_type,
+            v_means2d.contiguous(), v_covars2d.contiguous())
+        return v_means, v_covars, None, None, None, None
 
 
 class _FullyFusedProjection(torch.autograd.Function):

@@ -59,6 +59,35 @@ const char *gsplat_version(void);
 /* Projection (EWA splatting of 3D Gaussians to 2D conics).                  */
 /* ------------------------------------------------------------------------ */
 
+/* Camera-space projection of B*C*N Gaussians given by mean and full 3x3
+ * covariance (no culling, no eps2d): means2d = the pinhole (or orthographic)
+ * projection of the mean, covars2d = J S J^T with the projection's Jacobian
+ * J, the pinhole one evaluated with x/z and y/z clamped to 1.3x the field of
+ * view.  camera_model: PINHOLE or ORTHO (others return
+ * GSPLAT_ERR_UNSUPPORTED).
+ * Replaces projection_ewa_simple_fwd
+ *   (gsplat/cuda/csrc/Projection.cpp:41-80,
+ *    gsplat/cuda/csrc/ProjectionEWASimple.cu:37-138; the probe of has_3dgs(),
+ *    gsplat/cuda/_wrapper.py:181-184).
+ * Inputs : means [B,C,N,3], covars [B,C,N,3,3], Ks [B,C,3,3].
+ * Outputs: means2d [B,C,N,2], covars2d [B,C,N,2,2]. */
+int gsplat_projection_simple_fwd(
+    int64_t B, int64_t C, int64_t N, const float *means, const float *covars,
+    const float *Ks, int32_t image_width, int32_t image_height, int32_t camera_model,
+    float *means2d, float *covars2d, gsplat_stream_t stream);
+
+/* Vector-Jacobian product of gsplat_projection_simple_fwd.
+ * Replaces projection_ewa_simple_bwd
+ *   (gsplat/cuda/csrc/Projection.cpp:82-127,
+ *    gsplat/cuda/csrc/ProjectionEWASimple.cu:140-262).
+ * Inputs : the forward's inputs, v_means2d [B,C,N,2], v_covars2d [B,C,N,2,2].
+ * Outputs: v_means [B,C,N,3], v_covars [B,C,N,3,3] (every element written). */
+int gsplat_projection_simple_bwd(
+    int64_t B, int64_t C, int64_t N, const float *means, const float *covars,
+    const float *Ks, int32_t image_width, int32_t image_height, int32_t camera_model,
+    const float *v_means2d, const float *v_covars2d, float *v_means, float *v_covars,
+    gsplat_stream_t stream);
+
 /* Dense ("fused") projection of B*C*N rows.
  * Replaces projection_ewa_3dgs_fused_fwd
  *   (gsplat/cuda/csrc/Projection.cpp:129-200,

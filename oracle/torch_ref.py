@@ -60,6 +60,36 @@ def covar6_to_mat(c6: Tensor) -> Tensor:
     return torch.stack([a, b, c, b, d, e, c, e, f], dim=-1).reshape(c6.shape[:-1] + (3, 3))
 
 
+def proj_ref(means, covars, Ks, width, height, camera_model="pinhole"):
+    """Camera-space projection of Gaussians, differentiable: means [..., C, N, 3],
+    covars [..., C, N, 3, 3] -> means2d [..., C, N, 2], cov2d = J S J^T
+    [..., C, N, 2, 2] (gsplat/cuda/_torch_impl.py:42-97 pinhole with the
+    1.3x field-of-view clamp of the Jacobian, :169-211 orthographic)."""
+    x, y, z = torch.unbind(means, dim=-1)
+    fx = Ks[..., 0, 0, None]
+    fy = Ks[..., 1, 1, None]
+    cx = Ks[..., 0, 2, None]
+    cy = Ks[..., 1, 2, None]
+    zero = torch.zeros_like(z)
+    if camera_model == "ortho":
+        J = torch.stack([fx + zero, zero, zero, zero, fy + zero, zero], dim=-1)
+        means2d = torch.stack([fx * x + cx, fy * y + cy], dim=-1)
+    else:
+        tan_fovx = 0.5 * width / fx
+        tan_fovy = 0.5 * height / fy
+        lim_x_pos = (width - cx) / fx + 0.3 * tan_fovx
+        lim_x_neg = cx / fx + 0.3 * tan_fovx
+        lim_y_pos = (height - cy) / fy + 0.3 * tan_fovy
+        lim_y_neg = cy / fy + 0.3 * tan_fovy
+        tx = z * torch.minimum(lim_x_pos, torch.maximum(-lim_x_neg, x / z))
+        ty = z * torch.minimum(lim_y_pos, torch.maximum(-lim_y_neg, y / z))
+        J = torch.stack([fx / z, zero, -fx * tx / z ** 2,
+                         zero, fy / z, -fy * ty / z ** 2], dim=-1)
+        means2d = torch.stack([fx * x / z + cx, fy * y / z + cy], dim=-1)
+    J = J.reshape(J.shape[:-1] + (2, 3))
+    return means2d, J @ covars @ J.transpose(-1, -2)
+
+
 def projection_ref(means, covars, quats, scales, viewmats, Ks, width, height,
                    eps2d=0.3, near_plane=0.01, far_plane=1e10, radius_clip=0.0,
                    calc_compensations=False, camera_model="pinhole",
@@ -330,15 +360,17 @@ def rasterization_ref(means, quats, scales, opacities, colors, viewmats, Ks,
                       radius_clip=0.0, eps2d=0.3, sh_degree=None, packed=True,
                       tile_size=16, backgrounds=None, render_mode="RGB",
                       rasterize_mode="classic", camera_model="pinhole",
-                      dtype=torch.float64, tile_subset=None):
+                      dtype=torch.float64, tile_subset=None, restrict_rows=False):
     """CPU restatement of ``rasterization()`` for one batch (no batch dims).
 
     Inputs are CPU tensors (float32 values; gradients flow to them).  The
     visible rows, their tile lists and sorted order come from the bit-exact
     oracle run on the float32 inputs; the differentiable values from
     ``projection_ref`` in ``dtype``.  ``tile_subset`` (optional iterable of
-    tile slots) restricts the rasterizer to a sample of tiles (used to bound
-    the CPU baseline); other tiles are left empty.
+    tile slots) restricts the rasterizer to a sample of tiles; other tiles are
+    left empty.  With ``restrict_rows`` the float restatement (projection,
+    SH) is evaluated only on the rows those tiles reference, which bounds the
+    cost of checking full-size scenes; the values are the same either way.
     Returns (render_colors, render_alphas, meta).
     """
     N = means.shape[-2]
@@ -349,20 +381,7 @@ def rasterization_ref(means, quats, scales, opacities, colors, viewmats, Ks,
     ex = exact.projection_fwd(f32(means), None, f32(quats), f32(scales), f32(opacities),
                               f32(viewmats), f32(Ks), width, height, eps2d, near_plane,
                               far_plane, radius_clip, calc_comp, cm)
-    proj = projection_ref(means.to(dtype), None, quats.to(dtype), scales.to(dtype),
-                          viewmats.to(dtype), Ks.to(dtype), width, height, eps2d,
-                          near_plane, far_plane, radius_clip, calc_comp, camera_model,
-                          opacities.to(dtype))
     valid = ex["valid"].reshape(C * N)
-    rows = torch.from_numpy(np.nonzero(valid)[0]) if packed else None
-    flat = lambda t, k: t.reshape((C * N,) + t.shape[2:])
-    means2d = flat(proj["means2d"], 2)
-    conics = flat(proj["conics"], 3)
-    depths = flat(proj["depths"], 0)
-    op_rows = opacities.to(dtype)[None, :].expand(C, N).reshape(C * N)
-    comp = flat(proj["compensations"], 0) if calc_comp else None
-    if comp is not None:
-        op_rows = op_rows * comp
     # float32 values the GPU sees (bit-exact oracle) for the decisions
     ex_op = np.broadcast_to(f32(opacities)[None, :], (C, N)).reshape(C * N)
     if calc_comp:
@@ -372,55 +391,97 @@ def rasterization_ref(means, quats, scales, opacities, colors, viewmats, Ks,
     ex_dep = ex["depths"].reshape(C * N)
     ex_rad = ex["radii"].reshape(C * N, 2)
 
+    tile_w = math.ceil(width / tile_size)
+    tile_h = math.ceil(height / tile_size)
+    if packed:
+        # rows: the flattened (camera, Gaussian) index of each packed row
+        rows = np.nonzero(valid)[0]
+        image_ids = (rows // N).astype(np.int64)
+        _, isect_ids, flatten_ids = exact.isect_tiles(
+            ex_m2[rows], ex_rad[rows], ex_dep[rows], tile_size, tile_w, tile_h,
+            packed=True, n_images=C, image_ids=image_ids, conics=ex_con[rows],
+            opacities=ex_op[rows])
+    else:
+        rows = np.arange(C * N)
+        _, isect_ids, flatten_ids = exact.isect_tiles(
+            ex_m2.reshape(C, N, 2), ex_rad.reshape(C, N, 2), ex_dep.reshape(C, N),
+            tile_size, tile_w, tile_h, conics=ex_con.reshape(C, N, 3),
+            opacities=ex_op.reshape(C, N))
+    offsets = exact.isect_offset_encode(isect_ids, C, tile_w, tile_h)
+    masks = None
+    fl = flatten_ids
+    if tile_subset is not None:
+        sub = np.unique(np.asarray(list(tile_subset), np.int64))
+        m = np.zeros(C * tile_h * tile_w, bool)
+        m[sub] = True
+        masks = torch.from_numpy(m.reshape(C, tile_h, tile_w))
+    if tile_subset is not None and restrict_rows:
+        offs = offsets.reshape(-1).astype(np.int64)
+        ends = np.append(offs[1:], flatten_ids.shape[0])
+        used = np.unique(np.concatenate(
+            [flatten_ids[offs[t]:ends[t]] for t in sub] + [np.zeros(0, np.int32)]))
+        lookup = np.zeros(rows.shape[0], np.int32)
+        lookup[used] = np.arange(used.shape[0], dtype=np.int32)
+        fl = lookup[flatten_ids]
+        need = used.astype(np.int64)
+    else:
+        need = np.arange(rows.shape[0], dtype=np.int64)
+    # the differentiable values of the needed rows, one camera at a time
+    flat_need = rows[need]
+    cam_need, gid_need = flat_need // N, flat_need % N
+    n_need = need.shape[0]
+    m2_rows = torch.zeros(n_need, 2, dtype=dtype)
+    con_rows = torch.zeros(n_need, 3, dtype=dtype)
+    dep_rows = torch.zeros(n_need, dtype=dtype)
+    comp_rows = torch.zeros(n_need, dtype=dtype) if calc_comp else None
+    feat_parts = []
     if sh_degree is not None:
         campos = -(viewmats[:, :3, :3].transpose(-1, -2).to(dtype)
                    @ viewmats[:, :3, 3:].to(dtype))[..., 0]
-        dirs = means.to(dtype)[None, :, :] - campos[:, None, :]
-        dirs = dirs.reshape(C * N, 3)
-        coeffs = colors.to(dtype)[None].expand((C,) + colors.shape).reshape(
-            (C * N,) + colors.shape[-2:])
-        feats = spherical_harmonics_ref(sh_degree, dirs, coeffs)
-        feats = torch.clamp_min(feats + 0.5, 0.0)
-    else:
-        feats = colors.to(dtype)[None].expand((C,) + colors.shape).reshape(
-            C * N, colors.shape[-1])
-    D = feats.shape[-1] if render_mode in ("RGB", "RGB+D", "RGB+ED") else 0
+    for c in range(C):
+        sel_c = np.nonzero(cam_need == c)[0]
+        if sel_c.size == 0:
+            continue
+        g = torch.from_numpy(gid_need[sel_c])
+        at = torch.from_numpy(sel_c)
+        proj = projection_ref(means[g].to(dtype), None, quats[g].to(dtype),
+                              scales[g].to(dtype), viewmats[c:c + 1].to(dtype),
+                              Ks[c:c + 1].to(dtype), width, height, eps2d, near_plane,
+                              far_plane, radius_clip, calc_comp, camera_model,
+                              opacities[g].to(dtype))
+        m2_rows = m2_rows.index_copy(0, at, proj["means2d"][0])
+        con_rows = con_rows.index_copy(0, at, proj["conics"][0])
+        dep_rows = dep_rows.index_copy(0, at, proj["depths"][0])
+        if calc_comp:
+            comp_rows = comp_rows.index_copy(0, at, proj["compensations"][0])
+        if sh_degree is not None:
+            dirs = means[g].to(dtype) - campos[c][None, :]
+            f = spherical_harmonics_ref(sh_degree, dirs, colors[g].to(dtype))
+            f = torch.clamp_min(f + 0.5, 0.0)
+        else:
+            f = colors[g].to(dtype)
+        feat_parts.append((at, f))
+    op_rows = opacities.to(dtype)[torch.from_numpy(gid_need)]
+    if calc_comp:
+        op_rows = op_rows * comp_rows
+    Dc = colors.shape[-1]
+    feats = torch.zeros(n_need, Dc, dtype=dtype)
+    for at, f in feat_parts:
+        feats = feats.index_copy(0, at, f)
     if render_mode in ("D", "ED"):
-        feats = depths[:, None]
+        feats = dep_rows[:, None]
     elif render_mode in ("RGB+D", "RGB+ED"):
-        feats = torch.cat([feats, depths[:, None]], dim=-1)
+        feats = torch.cat([feats, dep_rows[:, None]], dim=-1)
     bg = backgrounds.to(dtype) if backgrounds is not None else None
     if bg is not None and render_mode in ("RGB+D", "RGB+ED"):
         bg = torch.cat([bg, torch.zeros(C, 1, dtype=dtype)], dim=-1)
     elif bg is not None and render_mode in ("D", "ED"):
         bg = torch.zeros(C, 1, dtype=dtype)
-
-    tile_w = math.ceil(width / tile_size)
-    tile_h = math.ceil(height / tile_size)
-    if packed:
-        r = rows.numpy()
-        image_ids = (r // N).astype(np.int64)
-        _, isect_ids, flatten_ids = exact.isect_tiles(
-            ex_m2[r], ex_rad[r], ex_dep[r], tile_size, tile_w, tile_h, packed=True,
-            n_images=C, image_ids=image_ids, conics=ex_con[r], opacities=ex_op[r])
-        sel = lambda t: t[rows]
-        dec = {"means2d": ex_m2[r], "conics": ex_con[r], "opacities": ex_op[r]}
-    else:
-        _, isect_ids, flatten_ids = exact.isect_tiles(
-            ex_m2.reshape(C, N, 2), ex_rad.reshape(C, N, 2), ex_dep.reshape(C, N),
-            tile_size, tile_w, tile_h, conics=ex_con.reshape(C, N, 3),
-            opacities=ex_op.reshape(C, N))
-        sel = lambda t: t
-        dec = {"means2d": ex_m2, "conics": ex_con, "opacities": ex_op}
-    offsets = exact.isect_offset_encode(isect_ids, C, tile_w, tile_h)
-    masks = None
-    if tile_subset is not None:
-        m = np.zeros(C * tile_h * tile_w, bool)
-        m[np.asarray(list(tile_subset), np.int64)] = True
-        masks = torch.from_numpy(m.reshape(C, tile_h, tile_w))
+    fr = flat_need
+    dec = {"means2d": ex_m2[fr], "conics": ex_con[fr], "opacities": ex_op[fr]}
     rc, ra, info = rasterize_to_pixels_ref(
-        sel(means2d), sel(conics), sel(feats), sel(op_rows), width, height,
-        tile_size, torch.from_numpy(offsets), torch.from_numpy(flatten_ids),
+        m2_rows, con_rows, feats, op_rows, width, height, tile_size,
+        torch.from_numpy(offsets), torch.from_numpy(np.ascontiguousarray(fl)),
         backgrounds=bg, masks=masks, decide=dec, dtype=dtype)
     if render_mode in ("ED", "RGB+ED"):
         rc = torch.cat([rc[..., :-1], rc[..., -1:] / ra.clamp(min=1e-10)], dim=-1)

@@ -66,6 +66,9 @@ def test_argument_errors_are_reported_without_a_gpu(lib_path):
     with pytest.raises(RuntimeError, match="channel"):
         _lib.call("gsplat_rasterize_fwd", 1, 0, 0, 7, None, None, None, None, None, None,
                   16, 16, 16, 1, 1, 1, None, None, None, None, None, None)
+    with pytest.raises(RuntimeError, match="pinhole"):
+        _lib.call("gsplat_projection_simple_fwd", 1, 1, 1, None, None, None, 16, 16, 2,
+                  None, None, None)
 
 
 def test_reference_op_schemas_registered():
@@ -75,11 +78,15 @@ def test_reference_op_schemas_registered():
                "projection_ewa_3dgs_fused_bwd", "projection_ewa_3dgs_packed_fwd",
                "projection_ewa_3dgs_packed_bwd", "rasterize_to_pixels_3dgs_fwd",
                "rasterize_to_pixels_3dgs_bwd", "adam", "quat_scale_to_covar_preci_fwd",
-               "quat_scale_to_covar_preci_bwd", "rasterize_to_indices_3dgs"]:
+               "quat_scale_to_covar_preci_bwd", "rasterize_to_indices_3dgs",
+               "projection_ewa_simple_fwd", "projection_ewa_simple_bwd"]:
         assert hasattr(torch.ops.gsplat, op), op
     s = str(torch.ops.gsplat.adam.default._schema)
     assert "Tensor(a!) param" in s and "Tensor? valid" in s
     assert gsplat_amd.has_3dgs() and gsplat_amd.has_adam()
+    # the reference's own probes (_wrapper.py:181-196), unchanged
+    assert hasattr(torch.ops.gsplat, "projection_ewa_simple_fwd")
+    assert hasattr(torch.ops.gsplat, "adam")
 
 
 def test_host_tensors_fail_loudly():

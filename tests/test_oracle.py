@@ -136,6 +136,41 @@ def _random_scene(seed=0, N=3000, C=2):
     return means, quats, scales, opac, vm, K, 320, 240
 
 
+def test_proj_ref_closed_forms():
+    """On the optical axis the pinhole Jacobian is diag(f/z) with third column
+    0, so cov2d is the xy block scaled by (f/z)^2 and the mean lands on the
+    principal point; off axis the third column is -f (x, y)/z^2 and means2d is
+    f (x, y)/z + c; outside 1.3x the field of view x/z is clamped in J only."""
+    f, W, H, z = 200.0, 100, 80, 4.0
+    K = torch.tensor([[[f, 0, 50.0], [0, f, 40.0], [0, 0, 1]]], dtype=torch.float64)
+    S = torch.tensor([[1.0, 0.2, 0.3], [0.2, 2.0, -0.1], [0.3, -0.1, 0.5]], dtype=torch.float64)
+    m = torch.tensor([[[0.0, 0.0, z]]], dtype=torch.float64)
+    m2, c2 = torch_ref.proj_ref(m, S[None, None], K, W, H)
+    torch.testing.assert_close(m2[0, 0], torch.tensor([50.0, 40.0], dtype=torch.float64))
+    torch.testing.assert_close(c2[0, 0], (f / z) ** 2 * S[:2, :2])
+    x, y = 0.3, -0.2
+    m = torch.tensor([[[x, y, z]]], dtype=torch.float64)
+    m2, c2 = torch_ref.proj_ref(m, S[None, None], K, W, H)
+    J = torch.tensor([[f / z, 0, -f * x / z ** 2], [0, f / z, -f * y / z ** 2]],
+                     dtype=torch.float64)
+    torch.testing.assert_close(m2[0, 0], torch.tensor([f * x / z + 50, f * y / z + 40],
+                                                      dtype=torch.float64))
+    torch.testing.assert_close(c2[0, 0], J @ S @ J.T)
+    # far off to the right: tx = z * lim_x_pos in J, the mean itself unclamped
+    xf = 10.0
+    lim = (W - 50.0) / f + 0.3 * 0.5 * W / f
+    m = torch.tensor([[[xf, y, z]]], dtype=torch.float64)
+    m2, c2 = torch_ref.proj_ref(m, S[None, None], K, W, H)
+    Jc = torch.tensor([[f / z, 0, -f * lim / z], [0, f / z, -f * y / z ** 2]],
+                      dtype=torch.float64)
+    torch.testing.assert_close(c2[0, 0], Jc @ S @ Jc.T)
+    assert abs(m2[0, 0, 0].item() - (f * xf / z + 50)) < 1e-9
+    m2, c2 = torch_ref.proj_ref(m, S[None, None], K, W, H, camera_model="ortho")
+    torch.testing.assert_close(c2[0, 0], f * f * S[:2, :2])
+    torch.testing.assert_close(m2[0, 0], torch.tensor([f * xf + 50, f * y + 40],
+                                                      dtype=torch.float64))
+
+
 def test_projection_exact_oracle_matches_float_restatement():
     means, quats, scales, opac, vm, K, W, H = _random_scene()
     ex = exact.projection_fwd(means.numpy(), None, quats.numpy(), scales.numpy(),
@@ -245,6 +280,154 @@ def test_accutile_subset_of_box_and_covers_level_set():
         inside = q < 0.999 * t
         tiles = set(((py[inside] // ts).astype(int) * tw + (px[inside] // ts).astype(int)).tolist())
         assert tiles <= acc_sets[i], (i, tiles - acc_sets[i])
+
+
+def _accutile_rows(seed=7, n=3000, W=200, H=150):
+    """Ellipses of every aspect ratio (1 to 40) and angle, from sub-pixel to
+    larger than a tile row, centred inside and outside the image."""
+    rng = np.random.default_rng(seed)
+    mean = np.stack([rng.uniform(-40, W + 40, n), rng.uniform(-40, H + 40, n)], -1)
+    ang = rng.uniform(0, np.pi, n)
+    s1 = np.exp(rng.uniform(np.log(0.3), np.log(60.0), n))
+    s2 = s1 / np.exp(rng.uniform(0.0, np.log(40.0), n))
+    c, s = np.cos(ang), np.sin(ang)
+    cov = np.empty((n, 2, 2))
+    cov[:, 0, 0] = c * c * s1 ** 2 + s * s * s2 ** 2
+    cov[:, 1, 1] = s * s * s1 ** 2 + c * c * s2 ** 2
+    cov[:, 0, 1] = cov[:, 1, 0] = c * s * (s1 ** 2 - s2 ** 2)
+    inv = np.linalg.inv(cov)
+    conics = np.stack([inv[:, 0, 0], inv[:, 0, 1], inv[:, 1, 1]], -1).astype(np.float32)
+    opac = np.exp(rng.uniform(np.log(0.005), 0.0, n)).astype(np.float32)
+    ext = np.minimum(3.33, np.sqrt(2 * np.log(np.maximum(opac * 255.0, 1.0))))
+    radii = np.ceil(ext[:, None] * np.sqrt(np.stack([cov[:, 0, 0], cov[:, 1, 1]], -1)))
+    radii = np.maximum(radii, 1).astype(np.int32)
+    depths = rng.uniform(1, 10, n).astype(np.float32)
+    return mean.astype(np.float32), radii, depths, conics, opac
+
+
+def _exact_tile_sets(mean, conic, opac, ts, tw, th, tol=2e-3):
+    """The tiles each ellipse {a dx^2 + 2 b dx dy + c dy^2 <= t} touches, in
+    float64, with t = min(3.33^2, 2 ln(255 o)) (IntersectTile.cu:205-214).
+
+    For every column strip of the sweep axis the other axis' extent of the
+    ellipse over that strip is the range [min lower boundary, max upper
+    boundary]; the lower boundary is convex in the sweep coordinate, so its
+    minimum over the strip is at the ellipse's extreme point clamped into the
+    strip (likewise the maximum of the upper boundary).  The tiles are that
+    range's tile rows, clamped to the row's tile rectangle -- the set
+    IntersectTile.cu:38-121 enumerates.  Returns the sets and, per row,
+    whether any edge lies within ``tol`` px of a tile boundary (float32
+    rounding may then decide either way)."""
+    sets, ambiguous = [], []
+    clamp = lambda v, hi: max(0, min(hi, v))
+    for i in range(mean.shape[0]):
+        mx, my = float(mean[i, 0]), float(mean[i, 1])
+        a, b, c = (float(v) for v in conic[i])
+        t = min(3.33 ** 2, 2 * math.log(float(opac[i]) * 255.0))
+        det = a * c - b * b
+        if t < 0 or det <= 0:
+            sets.append(set())
+            ambiguous.append(False)
+            continue
+        near = lambda v: abs(v / ts - round(v / ts)) * ts < tol + 1e-6 * abs(v)
+        xe, ye = math.sqrt(t * c / det), math.sqrt(t * a / det)
+        amb = any(near(v) for v in (mx - xe, mx + xe, my - ye, my + ye))
+        rx0, rx1 = clamp(math.floor((mx - xe) / ts), tw), clamp(math.floor((mx + xe) / ts) + 1, tw)
+        ry0, ry1 = clamp(math.floor((my - ye) / ts), th), clamp(math.floor((my + ye) / ts) + 1, th)
+        tiles = set()
+        if rx1 > rx0 and ry1 > ry0:
+            # sweep along the longer tile span (either axis gives the same set)
+            sweep_y = (ry1 - ry0) < (rx1 - rx0)
+            if sweep_y:
+                mu, mv, ue, quu, qvv, u0, u1, v0, v1 = my, mx, ye, c, a, ry0, ry1, rx0, rx1
+            else:
+                mu, mv, ue, quu, qvv, u0, u1, v0, v1 = mx, my, xe, a, c, rx0, rx1, ry0, ry1
+            ve = math.sqrt(t * quu / det)
+            du_min, du_max = b * ve / quu, -b * ve / quu  # where dv is -ve / +ve
+            root = lambda du: math.sqrt(max(0.0, t * qvv - det * du * du))
+            for u in range(u0, u1):
+                lo = max(u * ts, mu - ue) - mu
+                hi = min((u + 1) * ts, mu + ue) - mu
+                if hi < lo:
+                    continue
+                dlo = min(max(du_min, lo), hi)
+                dhi = min(max(du_max, lo), hi)
+                vmin = mv + (-b * dlo - root(dlo)) / qvv
+                vmax = mv + (-b * dhi + root(dhi)) / qvv
+                amb = amb or near(vmin) or near(vmax)
+                for v in range(max(v0, math.floor(vmin / ts)), min(v1, math.floor(vmax / ts) + 1)):
+                    tiles.add(u * tw + v if sweep_y else v * tw + u)
+        sets.append(tiles)
+        ambiguous.append(amb)
+    return sets, np.array(ambiguous)
+
+
+def _emitted_tile_sets(n, tw, th, isect):
+    tb = (tw * th).bit_length()
+    sets = [set() for _ in range(n)]
+    for k, f in zip(isect[1], isect[2]):
+        sets[f].add(int((k >> 32) & ((1 << tb) - 1)))
+    return sets
+
+
+_ACC_GEOM = dict(W=200, H=150, ts=16)
+
+
+def _accutile_mismatches(lib=None):
+    """Rows (unambiguous ones) whose oracle tile set differs from the exact
+    per-strip extent; ``lib`` substitutes a differently built oracle."""
+    W, H, ts = _ACC_GEOM["W"], _ACC_GEOM["H"], _ACC_GEOM["ts"]
+    tw, th = math.ceil(W / ts), math.ceil(H / ts)
+    mean, radii, depths, conics, opac = _accutile_rows(W=W, H=H)
+    saved = exact._lib
+    try:
+        if lib is not None:
+            exact._lib = lib
+        isect = exact.isect_tiles(mean[None], radii[None], depths[None], ts, tw, th,
+                                  sort=False, conics=conics[None], opacities=opac[None])
+    finally:
+        exact._lib = saved
+    got = _emitted_tile_sets(mean.shape[0], tw, th, isect)
+    want, amb = _exact_tile_sets(mean, conics, opac, ts, tw, th)
+    bad = [i for i in range(mean.shape[0]) if not amb[i] and got[i] != want[i]]
+    return bad, amb, want
+
+
+def test_accutile_equals_exact_extent_per_strip():
+    bad, amb, want = _accutile_mismatches()
+    assert amb.mean() < 0.02, amb.mean()
+    assert sum(len(s) for s in want) > 10_000
+    assert not bad, bad[:10]
+
+
+# Plausible slips in the sweep, each planted in a copy of the C oracle: the
+# extent check above must reject every one of them.
+_ACCUTILE_MUTATIONS = {
+    "no_extreme_point_rule": ("else e_min = fminf(min_lo, max_lo);",
+                              "e_min = fminf(min_lo, max_lo);"),
+    "snug_box_per_row": ("const int v0 = imax(rmin_y, imin(rmax_y, sat_f2i(e_min / ts)));",
+                         "const int v0 = rmin_y; (void)e_min;"),
+    "wrong_sign_cross_term": ("const float mbh = (-B) * h;", "const float mbh = B * h;"),
+    "dropped_factor_two": ("2.0f * oracle_portable_logf(*opacity / ALPHA_THRESHOLD)",
+                           "oracle_portable_logf(*opacity / ALPHA_THRESHOLD)"),
+    "upper_edge_off_by_one": ("sat_f2i(e_max / ts + 1.f)", "sat_f2i(e_max / ts + 2.f)"),
+}
+
+
+@pytest.mark.parametrize("mutation", sorted(_ACCUTILE_MUTATIONS))
+def test_accutile_extent_check_rejects_planted_mistakes(mutation, tmp_path):
+    import ctypes
+    import subprocess
+    src = (exact._HERE / "exact_ref.c").read_text()
+    old, new = _ACCUTILE_MUTATIONS[mutation]
+    assert src.count(old) == 1, (mutation, "pattern not found in the oracle")
+    mutated = tmp_path / "mutated.c"
+    mutated.write_text(src.replace(old, new))
+    so = tmp_path / "libmutated.so"
+    subprocess.run(["gcc", "-O2", "-fPIC", "-shared", "-std=c11", "-ffp-contract=off",
+                    "-o", str(so), str(mutated), "-lm"], check=True)
+    bad, _, _ = _accutile_mismatches(ctypes.CDLL(str(so)))
+    assert len(bad) > 0, mutation
 
 
 def test_isect_sorted_order_is_key_then_row():
@@ -368,6 +551,72 @@ def test_sh_basis_is_orthonormal():
     Y = torch_ref.sh_bases(25, torch.tensor(d)).numpy()
     G = (Y * w[:, None]).T @ Y
     np.testing.assert_allclose(G, np.eye(25), atol=1e-10)
+
+
+def _real_sh_closed_form(l, m, d):
+    """Real spherical harmonic Y_lm at unit directions d, from the associated
+    Legendre function (Condon-Shortley phase, scipy.special.lpmv):
+    Y_l0 = K_l0 P_l0(z); Y_lm = sqrt2 K_lm cos(m phi) P_lm(z) for m > 0 and
+    sqrt2 K_l|m| sin(|m| phi) P_l|m|(z) for m < 0, with
+    K_lm = sqrt((2l+1)/(4 pi) (l-|m|)!/(l+|m|)!).  Column l^2 + l + m of the
+    basis (the ordering of _torch_impl.py:686-768)."""
+    from scipy.special import lpmv
+    z = np.clip(d[:, 2], -1.0, 1.0)
+    phi = np.arctan2(d[:, 1], d[:, 0])
+    am = abs(m)
+    K = math.sqrt((2 * l + 1) / (4 * math.pi) * math.factorial(l - am) / math.factorial(l + am))
+    P = lpmv(am, l, z)
+    if m == 0:
+        return K * P
+    trig = np.cos(am * phi) if m > 0 else np.sin(am * phi)
+    return math.sqrt(2.0) * K * trig * P
+
+
+def _sh_check_dirs():
+    axes = np.array([[1, 0, 0], [-1, 0, 0], [0, 1, 0], [0, -1, 0], [0, 0, 1], [0, 0, -1],
+                     [1, 1, 1], [-1, 2, -3]], np.float64)
+    rng = np.random.default_rng(3)
+    d = np.concatenate([axes, rng.standard_normal((300, 3))])
+    return d / np.linalg.norm(d, axis=1, keepdims=True)
+
+
+def _sh_closed_form_error(Y, d):
+    err = np.zeros(25)
+    for l in range(5):
+        for m in range(-l, l + 1):
+            k = l * l + l + m
+            err[k] = np.abs(Y[:, k] - _real_sh_closed_form(l, m, d)).max()
+    return err
+
+
+def test_sh_basis_matches_closed_forms():
+    d = _sh_check_dirs()
+    Y = torch_ref.sh_bases(25, torch.tensor(d)).numpy()
+    assert _sh_closed_form_error(Y, d).max() < 1e-12
+    # named values: at the poles Y_l0 = (+-1)^l sqrt((2l+1)/4pi); band 1 is
+    # (-y, z, -x) sqrt(3/4pi); at (1,1,1)/sqrt3, Y_2,-2 = sqrt(15/4pi) xy
+    for sgn, row in ((1, 4), (-1, 5)):
+        for l in range(5):
+            np.testing.assert_allclose(Y[row, l * l + l], sgn ** l * math.sqrt((2 * l + 1) / (4 * math.pi)),
+                                       rtol=1e-14)
+    c1 = math.sqrt(3 / (4 * math.pi))
+    np.testing.assert_allclose(Y[:, 1:4], np.stack([-d[:, 1], d[:, 2], -d[:, 0]], -1) * c1,
+                               rtol=1e-13, atol=1e-15)
+    np.testing.assert_allclose(Y[6, 4], math.sqrt(15 / (4 * math.pi)) / 3, rtol=1e-14)
+
+
+@pytest.mark.parametrize("mutation", ["swap_4_8", "swap_10_14", "flip_13", "flip_21",
+                                      "swap_16_24"])
+def test_sh_closed_form_check_rejects_planted_mistakes(mutation):
+    d = _sh_check_dirs()
+    Y = torch_ref.sh_bases(25, torch.tensor(d)).numpy().copy()
+    kind, *idx = mutation.split("_")
+    idx = [int(i) for i in idx]
+    if kind == "swap":
+        Y[:, idx] = Y[:, idx[::-1]]
+    else:
+        Y[:, idx[0]] *= -1
+    assert _sh_closed_form_error(Y, d).max() > 1e-3
 
 
 # --------------------------------------------------------------------------

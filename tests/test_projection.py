@@ -240,3 +240,58 @@ def test_packed_bwd_rows_matches_row_scatter(C, use_covars):
     for x, y in zip(got0, ref0):
         if y is not None:
             assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("calc_comp", [False, True])
+def test_packed_sparse_grad_rows_match_per_row_autograd(calc_comp):
+    """sparse_grad=True (ProjectionEWA3DGSPacked.cu:578-611,
+    _wrapper.py:2258-2305): the op returns one gradient row per packed row,
+    indexed by gaussian_ids and not summed over cameras.  Each row is held to
+    the float64 autograd gradient of that row's own outputs alone: the
+    restatement is run per camera on a copy of the Gaussians of that camera's
+    rows, so every leaf row sees exactly one packed row."""
+    from gsplat_amd.cuda import _ops
+    C = 2
+    means, quats, scales, opac, vm, K, W, H = small_scene(seed=12, N=2500, C=C)
+    d = lambda t: t.to(DEV)
+    out = _ops.projection_ewa_3dgs_packed_fwd(
+        d(means), None, d(quats), d(scales), d(opac), d(vm), d(K), W, H, 0.3, 0.01,
+        1e10, 0.0, calc_comp, 0)
+    indptr, b, cam, gid, radii, m2, dep, con, comp = out
+    nnz = m2.shape[0]
+    g = torch.Generator().manual_seed(13)
+    v_m2 = torch.randn(nnz, 2, generator=g)
+    v_con = torch.randn(nnz, 3, generator=g)
+    v_dep = torch.randn(nnz, generator=g)
+    v_comp = torch.randn(nnz, generator=g) if calc_comp else None
+    v_means, _, v_quats, v_scales, _ = _ops.projection_ewa_3dgs_packed_bwd(
+        d(means), None, d(quats), d(scales), d(vm), d(K), W, H, 0.3, 0, b, cam, gid,
+        con, comp, d(v_m2), d(v_dep), d(v_con),
+        None if v_comp is None else d(v_comp), False, True)
+    assert v_means.shape == (nnz, 3) and v_quats.shape == (nnz, 4)
+
+    cam_np, gid_np = cam.cpu().numpy(), gid.cpu().numpy()
+    got = {"means": v_means.cpu(), "quats": v_quats.cpu(), "scales": v_scales.cpu()}
+    ref = {k: torch.zeros(nnz, t.shape[1], dtype=torch.float64) for k, t in got.items()}
+    ref32 = {k: torch.zeros(nnz, t.shape[1], dtype=torch.float64) for k, t in got.items()}
+    for dtype, dst in ((torch.float64, ref), (torch.float32, ref32)):
+        for c in range(C):
+            rows = np.nonzero(cam_np == c)[0]
+            gi = torch.from_numpy(gid_np[rows])
+            leaves = {k: src[gi].to(dtype).clone().requires_grad_()
+                      for k, src in (("means", means), ("quats", quats), ("scales", scales))}
+            t = torch_ref.projection_ref(leaves["means"], None, leaves["quats"],
+                                         leaves["scales"], vm[c:c + 1].to(dtype),
+                                         K[c:c + 1].to(dtype), W, H,
+                                         calc_compensations=calc_comp)
+            r = torch.from_numpy(rows)
+            loss = (t["means2d"][0] * v_m2[r].to(dtype)).sum() + \
+                (t["conics"][0] * v_con[r].to(dtype)).sum() + \
+                (t["depths"][0] * v_dep[r].to(dtype)).sum()
+            if calc_comp:
+                loss = loss + (t["compensations"][0] * v_comp[r].to(dtype)).sum()
+            loss.backward()
+            for k in dst:
+                dst[k][r] = leaves[k].grad.double()
+    for k in got:
+        print(assert_grad_close(got[k], ref[k], ref32[k], 1e-4, 1e-5, f"sparse d{k}"))

@@ -161,3 +161,62 @@ def test_rasterize_unused_alpha_gradient():
     for name, a, b in zip(("v_means2d", "v_conics", "v_colors", "v_opacities"),
                           *grads):
         assert_close(a.cpu(), b.cpu(), RTOL, ATOL, name)
+
+
+def test_reference_schema_fwd_bwd_without_transmittance():
+    """The reference's own autograd path (_wrapper.py:1709-1836) calls the
+    schema ops: rasterize_to_pixels_3dgs_fwd, then rasterize_to_pixels_3dgs_bwd
+    with render_alphas and last_ids only, so the backward takes the final
+    transmittance as T' = 1 - render_alphas (RasterizeToPixels3DGSBwd.cu:130)
+    instead of the forward's saved T.
+
+    Every term of that backward is linear in the recovered transmittances
+    (T_k = T' / prod_{j>=k} (1 - alpha_j), the colour buffer and T' itself), so
+    its exact result is the exact gradient with each pixel's upstream
+    gradients scaled by s = T' / T.  The oracle is therefore the float64
+    restatement's autograd with v_render_colors and v_render_alphas scaled by
+    s per pixel; the float32 restatement with the same scaling measures the
+    fp32 floor."""
+    data = projected_2d(seed=70, N=3000, C=2, D=3)
+    W, H, ts, C, D = data["W"], data["H"], data["tile"], data["C"], 3
+    m2, con, col, op = data["means2d"], data["conics"], data["colors"], data["opacities"]
+    offs, fl = data["offsets"], data["flatten_ids"]
+    g = torch.Generator().manual_seed(71)
+    bg = torch.rand(C, D, generator=g)
+    v_rc = torch.randn(C, H, W, D, generator=g)
+    v_ra = torch.randn(C, H, W, 1, generator=g)
+
+    ops = torch.ops.gsplat
+    dev = [t.to(DEV) for t in (m2, con, col, op, bg, offs, fl)]
+    rc, ra, last = ops.rasterize_to_pixels_3dgs_fwd(
+        dev[0], dev[1], dev[2], dev[3], dev[4], None, W, H, ts, dev[5], dev[6])
+    v_abs, v_m2, v_con, v_col, v_op = ops.rasterize_to_pixels_3dgs_bwd(
+        dev[0], dev[1], dev[2], dev[3], dev[4], None, W, H, ts, dev[5], dev[6],
+        ra, last, v_rc.to(DEV).contiguous(), v_ra.to(DEV).contiguous(), True)
+
+    ins_ref = [t.double().requires_grad_() for t in (m2, con, col, op)]
+    rc_r, ra_r, info = torch_ref.rasterize_to_pixels_ref(
+        ins_ref[0], ins_ref[1], ins_ref[2], ins_ref[3], W, H, ts, offs, fl,
+        backgrounds=bg.double())
+    # forward outputs: decisions exact, colours within tolerance
+    np.testing.assert_array_equal(last.cpu().numpy(), info["last_ids"])
+    alpha32 = (np.float32(1.0) - info["transmittance"]).astype(np.float32)
+    np.testing.assert_array_equal(ra.cpu().numpy()[..., 0], alpha32)
+    assert_close(rc.cpu(), rc_r.detach(), RTOL, ATOL, "render_colors")
+
+    t_saved = 1.0 - torch.from_numpy(alpha32.astype(np.float64))[..., None]
+    s = (t_saved / (1.0 - ra_r.detach())).detach()
+    ((rc_r * (v_rc.double() * s)).sum() + (ra_r * (v_ra.double() * s)).sum()).backward()
+    ins32 = [t.float().clone().requires_grad_() for t in (m2, con, col, op)]
+    rc32, ra32, _ = torch_ref.rasterize_to_pixels_ref(
+        ins32[0], ins32[1], ins32[2], ins32[3], W, H, ts, offs, fl,
+        backgrounds=bg.float(), dtype=torch.float32)
+    s32 = s.float()
+    ((rc32 * (v_rc * s32)).sum() + (ra32 * (v_ra * s32)).sum()).backward()
+    for name, a, b, b32 in zip(("v_means2d", "v_conics", "v_colors", "v_opacities"),
+                               (v_m2, v_con, v_col, v_op), ins_ref, ins32):
+        print(assert_grad_close(a, b.grad, b32.grad, RTOL, ATOL, name))
+    assert bool(torch.isfinite(v_abs).all())
+    assert bool((v_abs + 1e-6 >= v_m2.abs()).all())
+    # the scaling matters: pixels near the 1e-4 cutoff carry few bits of T'
+    assert float((s - 1).abs().max()) > 1e-5
