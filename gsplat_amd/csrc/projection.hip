@@ -489,13 +489,27 @@ __global__ void __launch_bounds__(kPackThreads) projection_packed_fwd_kernel(
 
 // ---------------------------------------------------------------------------
 // Backward math (contraction allowed; validated against autograd).
+//
+// The vector-Jacobian products run in double precision from the float32
+// inputs.  The covariance chain (2D inverse -> camera covariance -> world
+// covariance -> scaled rotation -> quaternion and scales) multiplies the
+// upstream gradient by J^T ... J, whose entries are ~f/z, and then contracts
+// the result with the Gaussian's axes; for an axis close to the viewing ray
+// the terms cancel by orders of magnitude, and float32 loses that many
+// digits of the scale and quaternion gradients.  On gfx950 a double FMA
+// issues at the rate of an unpacked float32 FMA, and these kernels are bound
+// by memory latency, so the double chain costs no time.
 // ---------------------------------------------------------------------------
-struct M3 {
-    float m[9];  // row-major
+template <typename T>
+struct Mat3 {
+    T m[9];  // row-major
 };
+using M3 = Mat3<float>;
+using M3d = Mat3<double>;
 
-__device__ __forceinline__ M3 mm(const M3 &a, const M3 &b) {
-    M3 r;
+template <typename T>
+__device__ __forceinline__ Mat3<T> mm(const Mat3<T> &a, const Mat3<T> &b) {
+    Mat3<T> r;
 #pragma unroll
     for (int i = 0; i < 3; ++i)
 #pragma unroll
@@ -505,8 +519,9 @@ __device__ __forceinline__ M3 mm(const M3 &a, const M3 &b) {
                              a.m[i * 3 + 2] * b.m[2 * 3 + j];
     return r;
 }
-__device__ __forceinline__ M3 mtm(const M3 &a, const M3 &b) {  // a^T b
-    M3 r;
+template <typename T>
+__device__ __forceinline__ Mat3<T> mtm(const Mat3<T> &a, const Mat3<T> &b) {  // a^T b
+    Mat3<T> r;
 #pragma unroll
     for (int i = 0; i < 3; ++i)
 #pragma unroll
@@ -516,8 +531,9 @@ __device__ __forceinline__ M3 mtm(const M3 &a, const M3 &b) {  // a^T b
                              a.m[2 * 3 + i] * b.m[2 * 3 + j];
     return r;
 }
-__device__ __forceinline__ M3 mmt(const M3 &a, const M3 &b) {  // a b^T
-    M3 r;
+template <typename T>
+__device__ __forceinline__ Mat3<T> mmt(const Mat3<T> &a, const Mat3<T> &b) {  // a b^T
+    Mat3<T> r;
 #pragma unroll
     for (int i = 0; i < 3; ++i)
 #pragma unroll
@@ -528,21 +544,65 @@ __device__ __forceinline__ M3 mmt(const M3 &a, const M3 &b) {  // a b^T
     return r;
 }
 
+// Rotation of the normalised (w, x, y, z) quaternion, in double.
+__device__ __forceinline__ void quat_to_rot_d(const float qf[4], double R[9]) {
+    const double q0 = qf[0], q1 = qf[1], q2 = qf[2], q3 = qf[3];
+    const double inv = 1.0 / sqrt(q0 * q0 + q1 * q1 + q2 * q2 + q3 * q3);
+    const double w = q0 * inv, x = q1 * inv, y = q2 * inv, z = q3 * inv;
+    R[0] = 1.0 - 2.0 * (y * y + z * z);
+    R[1] = 2.0 * (x * y - w * z);
+    R[2] = 2.0 * (x * z + w * y);
+    R[3] = 2.0 * (x * y + w * z);
+    R[4] = 1.0 - 2.0 * (x * x + z * z);
+    R[5] = 2.0 * (y * z - w * x);
+    R[6] = 2.0 * (x * z - w * y);
+    R[7] = 2.0 * (y * z + w * x);
+    R[8] = 1.0 - 2.0 * (x * x + y * y);
+}
+
+// Symmetric 3x3 matrix: (xx, xy, xz, yy, yz, zz).
+struct Sym3d {
+    double v[6];
+    __device__ __forceinline__ double at(int i, int j) const {
+        // index of (i, j) in the upper triangle
+        const int a = i < j ? i : j, b = i < j ? j : i;
+        return v[a == 0 ? b : (a == 1 ? 2 + b : 5)];
+    }
+};
+
+// A S A^T for a general A (given by a functor of (i, j)) and symmetric S.
+template <typename AT>
+__device__ __forceinline__ Sym3d congruence(const AT &A, const Sym3d &S) {
+    double T[9];  // A S
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+            T[i * 3 + j] = A(i, 0) * S.at(0, j) + A(i, 1) * S.at(1, j) + A(i, 2) * S.at(2, j);
+    Sym3d r;
+    int k = 0;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = i; j < 3; ++j)
+            r.v[k++] = T[i * 3 + 0] * A(j, 0) + T[i * 3 + 1] * A(j, 1) + T[i * 3 + 2] * A(j, 2);
+    return r;
+}
+
+// Gaussian geometry for the backward: the raw inputs (float) and the world
+// covariance in double, recomputed from them.
 struct GaussGeom {
-    M3 S;       // world covariance (full symmetric)
-    M3 Rq;      // rotation from the quaternion (quats path only)
-    float q[4]; // raw quaternion
+    Sym3d S;    // world covariance
+    float q[4]; // raw quaternion (quats path only)
     float s[3]; // scales
 };
 
 __device__ __forceinline__ void load_geom(const float *covar6, const float *quat,
                                           const float *scale, GaussGeom &G) {
     if (covar6 != nullptr) {
-        const float c[6] = {covar6[0], covar6[1], covar6[2],
-                            covar6[3], covar6[4], covar6[5]};
-        G.S.m[0] = c[0]; G.S.m[1] = c[1]; G.S.m[2] = c[2];
-        G.S.m[3] = c[1]; G.S.m[4] = c[3]; G.S.m[5] = c[4];
-        G.S.m[6] = c[2]; G.S.m[7] = c[4]; G.S.m[8] = c[5];
+#pragma unroll
+        for (int k = 0; k < 6; ++k)
+            G.S.v[k] = covar6[k];
         return;
     }
 #pragma unroll
@@ -551,137 +611,136 @@ __device__ __forceinline__ void load_geom(const float *covar6, const float *quat
 #pragma unroll
     for (int i = 0; i < 3; ++i)
         G.s[i] = scale[i];
-    quat_to_rot_exact(G.q[0], G.q[1], G.q[2], G.q[3], G.Rq.m);
-    M3 A;
+    double Rq[9];
+    quat_to_rot_d(G.q, Rq);
+    const double s2[3] = {(double)G.s[0] * G.s[0], (double)G.s[1] * G.s[1],
+                          (double)G.s[2] * G.s[2]};
+    int k = 0;
 #pragma unroll
     for (int i = 0; i < 3; ++i)
 #pragma unroll
-        for (int k = 0; k < 3; ++k)
-            A.m[i * 3 + k] = G.Rq.m[i * 3 + k] * G.s[k];
-    G.S = mmt(A, A);
+        for (int j = i; j < 3; ++j)
+            G.S.v[k++] = Rq[i * 3 + 0] * Rq[j * 3 + 0] * s2[0] +
+                         Rq[i * 3 + 1] * Rq[j * 3 + 1] * s2[1] +
+                         Rq[i * 3 + 2] * Rq[j * 3 + 2] * s2[2];
 }
 
 // Gradient of one (camera, Gaussian) row: accumulates dL/dmean (world),
-// dL/dS (world covariance, full 3x3) and, if wanted, dL/dR, dL/dt.
+// dL/dS (world covariance, symmetric) and, if wanted, dL/dR, dL/dt.
 __device__ __forceinline__ void project_row_vjp(
     const Cam &cam, const float *mean, const GaussGeom &G, int camera_model,
     float W, float H, float eps2d, const float *conic, bool has_comp,
-    float comp, float v_comp, float v_mx, float v_my, float v_depth,
-    const float *v_conic, float v_mean[3], M3 &v_S, bool want_cam, M3 &v_R,
-    float v_t[3]) {
-    M3 R;
-#pragma unroll
-    for (int i = 0; i < 9; ++i)
-        R.m[i] = cam.R[i];
-    const float p[3] = {mean[0], mean[1], mean[2]};
-    float mc[3];
+    float comp_f, float v_comp_f, float v_mx_f, float v_my_f, float v_depth_f,
+    const float *v_conic, double v_mean[3], Sym3d &v_S, bool want_cam, M3d &v_R,
+    double v_t[3]) {
+    const float *Rf = cam.R;
+    auto R = [&](int i, int j) -> double { return (double)Rf[i * 3 + j]; };
+    auto Rt = [&](int i, int j) -> double { return (double)Rf[j * 3 + i]; };
+    const double p[3] = {mean[0], mean[1], mean[2]};
+    double mc[3];
 #pragma unroll
     for (int i = 0; i < 3; ++i)
-        mc[i] = R.m[i * 3 + 0] * p[0] + R.m[i * 3 + 1] * p[1] +
-                R.m[i * 3 + 2] * p[2] + cam.t[i];
-    const M3 Sc = mmt(mm(R, G.S), R);
+        mc[i] = R(i, 0) * p[0] + R(i, 1) * p[1] + R(i, 2) * p[2] + (double)cam.t[i];
+    const Sym3d Sc = congruence(R, G.S);
+    const double v_mx = v_mx_f, v_my = v_my_f;
 
-    // d/d(cov2d): inverse VJP  dL/dC = -Ci * dL/dCi * Ci (symmetric split)
-    const float ia = conic[0], ib = conic[1], ic = conic[2];
-    const float ga = v_conic[0], gb = 0.5f * v_conic[1], gc = v_conic[2];
-    // T = Ci * G
-    const float t00 = ia * ga + ib * gb, t01 = ia * gb + ib * gc;
-    const float t10 = ib * ga + ic * gb, t11 = ib * gb + ic * gc;
-    float vc00 = -(t00 * ia + t01 * ib);
-    float vc01 = -(t00 * ib + t01 * ic);
-    float vc10 = -(t10 * ia + t11 * ib);
-    float vc11 = -(t10 * ib + t11 * ic);
+    // d/d(cov2d): inverse VJP  dL/dC = -Ci * dL/dCi * Ci (symmetric)
+    const double ia = conic[0], ib = conic[1], ic = conic[2];
+    const double ga = v_conic[0], gb = 0.5 * (double)v_conic[1], gc = v_conic[2];
+    const double t00 = ia * ga + ib * gb, t01 = ia * gb + ib * gc;
+    const double t11 = ib * gb + ic * gc;
+    double vc00 = -(t00 * ia + t01 * ib);
+    double vc01 = -(t00 * ib + t01 * ic);
+    double vc11 = -((ib * ga + ic * gb) * ib + t11 * ic);
     if (has_comp) {
         // comp = sqrt(det(C) / det(C + eps I)); conic is the blurred inverse
-        const float det_conic = ia * ic - ib * ib;
-        const float v_sqr_comp = v_comp * 0.5f / (comp + 1e-6f);
-        const float one_minus = 1.f - comp * comp;
-        vc00 += v_sqr_comp * (one_minus * ia - eps2d * det_conic);
+        const double comp = comp_f, eps = eps2d;
+        const double det_conic = ia * ic - ib * ib;
+        const double v_sqr_comp = (double)v_comp_f * 0.5 / (comp + 1e-6);
+        const double one_minus = 1.0 - comp * comp;
+        vc00 += v_sqr_comp * (one_minus * ia - eps * det_conic);
         vc01 += v_sqr_comp * (one_minus * ib);
-        vc10 += v_sqr_comp * (one_minus * ib);
-        vc11 += v_sqr_comp * (one_minus * ic - eps2d * det_conic);
+        vc11 += v_sqr_comp * (one_minus * ic - eps * det_conic);
     }
 
-    const float fx = cam.fx, fy = cam.fy;
-    const float x = mc[0], y = mc[1], z = mc[2];
-    float J[6];  // row-major 2x3
-    float vmc[3];
-    M3 vSc;
+    const double fx = cam.fx, fy = cam.fy;
+    const double x = mc[0], y = mc[1], z = mc[2];
+    double J[6];  // row-major 2x3
+    double vmc[3];
     if (camera_model == GSPLAT_CAMERA_ORTHO) {
-        J[0] = fx; J[1] = 0.f; J[2] = 0.f;
-        J[3] = 0.f; J[4] = fy; J[5] = 0.f;
+        J[0] = fx; J[1] = 0.0; J[2] = 0.0;
+        J[3] = 0.0; J[4] = fy; J[5] = 0.0;
         vmc[0] = fx * v_mx;
         vmc[1] = fy * v_my;
-        vmc[2] = 0.f;
+        vmc[2] = 0.0;
     } else {
-        const float tan_fovx = 0.5f * W / fx, tan_fovy = 0.5f * H / fy;
-        const float lim_x_pos = (W - cam.cx) / fx + 0.3f * tan_fovx;
-        const float lim_x_neg = cam.cx / fx + 0.3f * tan_fovx;
-        const float lim_y_pos = (H - cam.cy) / fy + 0.3f * tan_fovy;
-        const float lim_y_neg = cam.cy / fy + 0.3f * tan_fovy;
-        const float rz = 1.f / z, rz2 = rz * rz, rz3 = rz2 * rz;
-        const float tx = z * fminf(lim_x_pos, fmaxf(-lim_x_neg, x * rz));
-        const float ty = z * fminf(lim_y_pos, fmaxf(-lim_y_neg, y * rz));
-        J[0] = fx * rz; J[1] = 0.f; J[2] = -fx * tx * rz2;
-        J[3] = 0.f; J[4] = fy * rz; J[5] = -fy * ty * rz2;
+        // the clamp limits are the forward's float32 values
+        const float tan_fovx = 0.5f * W / cam.fx, tan_fovy = 0.5f * H / cam.fy;
+        const double lim_x_pos = (W - cam.cx) / cam.fx + 0.3f * tan_fovx;
+        const double lim_x_neg = cam.cx / cam.fx + 0.3f * tan_fovx;
+        const double lim_y_pos = (H - cam.cy) / cam.fy + 0.3f * tan_fovy;
+        const double lim_y_neg = cam.cy / cam.fy + 0.3f * tan_fovy;
+        const double rz = 1.0 / z, rz2 = rz * rz, rz3 = rz2 * rz;
+        const double xr = x * rz, yr = y * rz;
+        const double tx = z * fmin(lim_x_pos, fmax(-lim_x_neg, xr));
+        const double ty = z * fmin(lim_y_pos, fmax(-lim_y_neg, yr));
+        J[0] = fx * rz; J[1] = 0.0; J[2] = -fx * tx * rz2;
+        J[3] = 0.0; J[4] = fy * rz; J[5] = -fy * ty * rz2;
         vmc[0] = fx * rz * v_mx;
         vmc[1] = fy * rz * v_my;
         vmc[2] = -(fx * x * v_mx + fy * y * v_my) * rz2;
-        // dJ = G J Sc^T + G^T J Sc (Sc symmetric): vJ = (G + G^T) J Sc
-        const float g00 = vc00 + vc00, g01 = vc01 + vc10, g11 = vc11 + vc11;
-        float JS[6];
+        // dL/dJ = (G + G^T) J Sc with G = dL/dcov2d; only the columns 0 and 2
+        // of row 0 and columns 1 and 2 of row 1 depend on the mean
+        const double g00 = vc00 + vc00, g01 = vc01 + vc01, g11 = vc11 + vc11;
+        double JS[6];
 #pragma unroll
         for (int r = 0; r < 2; ++r)
 #pragma unroll
             for (int c = 0; c < 3; ++c)
-                JS[r * 3 + c] = J[r * 3 + 0] * Sc.m[0 * 3 + c] +
-                                J[r * 3 + 1] * Sc.m[1 * 3 + c] +
-                                J[r * 3 + 2] * Sc.m[2 * 3 + c];
-        float vJ[6];
-#pragma unroll
-        for (int c = 0; c < 3; ++c) {
-            vJ[0 * 3 + c] = g00 * JS[c] + g01 * JS[3 + c];
-            vJ[1 * 3 + c] = g01 * JS[c] + g11 * JS[3 + c];
-        }
-        const float xr = x * rz, yr = y * rz;
+                JS[r * 3 + c] = J[r * 3 + 0] * Sc.at(0, c) + J[r * 3 + 1] * Sc.at(1, c) +
+                                J[r * 3 + 2] * Sc.at(2, c);
+        const double vJ00 = g00 * JS[0] + g01 * JS[3];
+        const double vJ02 = g00 * JS[2] + g01 * JS[5];
+        const double vJ11 = g01 * JS[1] + g11 * JS[4];
+        const double vJ12 = g01 * JS[2] + g11 * JS[5];
         if (xr <= lim_x_pos && xr >= -lim_x_neg)
-            vmc[0] += -fx * rz2 * vJ[2];
+            vmc[0] += -fx * rz2 * vJ02;
         else
-            vmc[2] += -fx * rz3 * vJ[2] * tx;
+            vmc[2] += -fx * rz3 * vJ02 * tx;
         if (yr <= lim_y_pos && yr >= -lim_y_neg)
-            vmc[1] += -fy * rz2 * vJ[5];
+            vmc[1] += -fy * rz2 * vJ12;
         else
-            vmc[2] += -fy * rz3 * vJ[5] * ty;
-        vmc[2] += -fx * rz2 * vJ[0] - fy * rz2 * vJ[4] +
-                  2.f * fx * tx * rz3 * vJ[2] + 2.f * fy * ty * rz3 * vJ[5];
+            vmc[2] += -fy * rz3 * vJ12 * ty;
+        vmc[2] += -fx * rz2 * vJ00 - fy * rz2 * vJ11 +
+                  2.0 * fx * tx * rz3 * vJ02 + 2.0 * fy * ty * rz3 * vJ12;
     }
-    // v_Sc = J^T G J
+    // v_Sc = J^T G J (symmetric)
+    Sym3d vSc;
     {
-        float GJ[6];  // G (2x2) * J (2x3)
+        double GJ[6];  // G (2x2) * J (2x3)
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
             GJ[0 * 3 + c] = vc00 * J[c] + vc01 * J[3 + c];
-            GJ[1 * 3 + c] = vc10 * J[c] + vc11 * J[3 + c];
+            GJ[1 * 3 + c] = vc01 * J[c] + vc11 * J[3 + c];
         }
+        int k = 0;
 #pragma unroll
         for (int i = 0; i < 3; ++i)
 #pragma unroll
-            for (int j = 0; j < 3; ++j)
-                vSc.m[i * 3 + j] = J[0 * 3 + i] * GJ[0 * 3 + j] +
-                                   J[1 * 3 + i] * GJ[1 * 3 + j];
+            for (int j = i; j < 3; ++j)
+                vSc.v[k++] = J[0 * 3 + i] * GJ[0 * 3 + j] + J[1 * 3 + i] * GJ[1 * 3 + j];
     }
-    vmc[2] += v_depth;
+    vmc[2] += (double)v_depth_f;
 
     // mean: mc = R p + t
 #pragma unroll
     for (int j = 0; j < 3; ++j)
-        v_mean[j] += R.m[0 * 3 + j] * vmc[0] + R.m[1 * 3 + j] * vmc[1] +
-                     R.m[2 * 3 + j] * vmc[2];
+        v_mean[j] += R(0, j) * vmc[0] + R(1, j) * vmc[1] + R(2, j) * vmc[2];
     // covariance: Sc = R S R^T  ->  dS = R^T dSc R
-    const M3 dS = mm(mtm(R, vSc), R);
+    const Sym3d dS = congruence(Rt, vSc);
 #pragma unroll
-    for (int i = 0; i < 9; ++i)
-        v_S.m[i] += dS.m[i];
+    for (int k = 0; k < 6; ++k)
+        v_S.v[k] += dS.v[k];
     if (want_cam) {
 #pragma unroll
         for (int i = 0; i < 3; ++i) {
@@ -690,68 +749,81 @@ __device__ __forceinline__ void project_row_vjp(
                 v_R.m[i * 3 + j] += vmc[i] * p[j];
             v_t[i] += vmc[i];
         }
-        // dR = dSc R S^T + dSc^T R S
-        const M3 RS = mm(R, G.S);
-        const M3 a1 = mm(vSc, RS);   // S symmetric: R S^T == R S
-        const M3 a2 = mtm(vSc, RS);
+        // dR = dSc R S^T + dSc^T R S = 2 dSc R S (both symmetric)
+        double RS[9];
 #pragma unroll
-        for (int i = 0; i < 9; ++i)
-            v_R.m[i] += a1.m[i] + a2.m[i];
+        for (int i = 0; i < 3; ++i)
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+                RS[i * 3 + j] = R(i, 0) * G.S.at(0, j) + R(i, 1) * G.S.at(1, j) +
+                                R(i, 2) * G.S.at(2, j);
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+                v_R.m[i * 3 + j] += 2.0 * (vSc.at(i, 0) * RS[0 * 3 + j] +
+                                           vSc.at(i, 1) * RS[1 * 3 + j] +
+                                           vSc.at(i, 2) * RS[2 * 3 + j]);
     }
 }
 
-// dL/dS (full) -> dL/dquat, dL/dscale  (quat_scale_to_covar_vjp +
-// quat_to_rotmat_vjp, Utils.cuh:197-296).
-__device__ __forceinline__ void covar_vjp_to_quat_scale(const GaussGeom &G,
-                                                        const M3 &v_S,
-                                                        float v_q[4],
-                                                        float v_s[3]) {
-    // S = M M^T with M = Rq diag(s):  dM = (dS + dS^T) M
-    M3 Mx;
+// dL/dS (symmetric) -> dL/dquat, dL/dscale  (quat_scale_to_covar_vjp +
+// quat_to_rotmat_vjp, Utils.cuh:197-296), for the Gaussian (q, s).
+__device__ __forceinline__ void covar_vjp_to_quat_scale(const float qf[4],
+                                                        const double s[3],
+                                                        const Sym3d &v_S,
+                                                        double v_q[4],
+                                                        double v_s[3]) {
+    double Rq[9];
+    quat_to_rot_d(qf, Rq);
+    // S = M M^T with M = Rq diag(s):  dM = (dS + dS^T) M = 2 dS M
+    double vM[9];
 #pragma unroll
     for (int i = 0; i < 3; ++i)
 #pragma unroll
         for (int k = 0; k < 3; ++k)
-            Mx.m[i * 3 + k] = G.Rq.m[i * 3 + k] * G.s[k];
-    M3 sym;
-#pragma unroll
-    for (int i = 0; i < 3; ++i)
-#pragma unroll
-        for (int j = 0; j < 3; ++j)
-            sym.m[i * 3 + j] = v_S.m[i * 3 + j] + v_S.m[j * 3 + i];
-    const M3 vM = mm(sym, Mx);
-    // dRq = dM diag(s);  ds_k = sum_i Rq[i][k] dM[i][k]
-    M3 g;
-#pragma unroll
-    for (int i = 0; i < 3; ++i)
-#pragma unroll
-        for (int k = 0; k < 3; ++k)
-            g.m[i * 3 + k] = vM.m[i * 3 + k] * G.s[k];
+            vM[i * 3 + k] = 2.0 * s[k] * (v_S.at(i, 0) * Rq[0 * 3 + k] +
+                                          v_S.at(i, 1) * Rq[1 * 3 + k] +
+                                          v_S.at(i, 2) * Rq[2 * 3 + k]);
+    // ds_k = sum_i Rq[i][k] dM[i][k];  dRq = dM diag(s)
 #pragma unroll
     for (int k = 0; k < 3; ++k)
-        v_s[k] = G.Rq.m[0 * 3 + k] * vM.m[0 * 3 + k] +
-                 G.Rq.m[1 * 3 + k] * vM.m[1 * 3 + k] +
-                 G.Rq.m[2 * 3 + k] * vM.m[2 * 3 + k];
+        v_s[k] = Rq[0 * 3 + k] * vM[0 * 3 + k] + Rq[1 * 3 + k] * vM[1 * 3 + k] +
+                 Rq[2 * 3 + k] * vM[2 * 3 + k];
+    double m[9];  // m[r*3+c] = dL/dRq[r][c]
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+            m[i * 3 + k] = vM[i * 3 + k] * s[k];
     // rotation-matrix VJP w.r.t. the normalised quaternion (w, x, y, z)
-    const float n2 = G.q[0] * G.q[0] + G.q[1] * G.q[1] + G.q[2] * G.q[2] +
-                     G.q[3] * G.q[3];
-    const float inv = 1.f / sqrtf(n2);
-    const float w = G.q[0] * inv, x = G.q[1] * inv, y = G.q[2] * inv,
-                z = G.q[3] * inv;
-    const float *m = g.m;  // m[r*3+c] = dL/dR[r][c]
-    const float dw = 2.f * (x * (m[7] - m[5]) + y * (m[2] - m[6]) +
-                            z * (m[3] - m[1]));
-    const float dx = 2.f * (-2.f * x * (m[4] + m[8]) + y * (m[1] + m[3]) +
-                            z * (m[2] + m[6]) + w * (m[7] - m[5]));
-    const float dy = 2.f * (x * (m[1] + m[3]) - 2.f * y * (m[0] + m[8]) +
-                            z * (m[5] + m[7]) + w * (m[2] - m[6]));
-    const float dz = 2.f * (x * (m[2] + m[6]) + y * (m[5] + m[7]) -
-                            2.f * z * (m[0] + m[4]) + w * (m[3] - m[1]));
-    const float dot = dw * w + dx * x + dy * y + dz * z;
+    const double q0 = qf[0], q1 = qf[1], q2 = qf[2], q3 = qf[3];
+    const double inv = 1.0 / sqrt(q0 * q0 + q1 * q1 + q2 * q2 + q3 * q3);
+    const double w = q0 * inv, x = q1 * inv, y = q2 * inv, z = q3 * inv;
+    const double dw = 2.0 * (x * (m[7] - m[5]) + y * (m[2] - m[6]) +
+                             z * (m[3] - m[1]));
+    const double dx = 2.0 * (-2.0 * x * (m[4] + m[8]) + y * (m[1] + m[3]) +
+                             z * (m[2] + m[6]) + w * (m[7] - m[5]));
+    const double dy = 2.0 * (x * (m[1] + m[3]) - 2.0 * y * (m[0] + m[8]) +
+                             z * (m[5] + m[7]) + w * (m[2] - m[6]));
+    const double dz = 2.0 * (x * (m[2] + m[6]) + y * (m[5] + m[7]) -
+                             2.0 * z * (m[0] + m[4]) + w * (m[3] - m[1]));
+    const double dot = dw * w + dx * x + dy * y + dz * z;
     v_q[0] = (dw - dot * w) * inv;
     v_q[1] = (dx - dot * x) * inv;
     v_q[2] = (dy - dot * y) * inv;
     v_q[3] = (dz - dot * z) * inv;
+}
+
+// dL/dS (symmetric) as the gradient of the triu covars input: each
+// off-diagonal entry stands for both of its places.
+__device__ __forceinline__ void covar6_grad(const Sym3d &v_S, float out[6]) {
+    out[0] = (float)v_S.v[0];
+    out[1] = (float)(2.0 * v_S.v[1]);
+    out[2] = (float)(2.0 * v_S.v[2]);
+    out[3] = (float)v_S.v[3];
+    out[4] = (float)(2.0 * v_S.v[4]);
+    out[5] = (float)v_S.v[5];
 }
 
 struct BwdArgs {
@@ -772,8 +844,8 @@ struct BwdArgs {
 // Reduce v_R (9) and v_t (3) of the workgroup and add them to the camera's
 // viewmat gradient.  Must be reached by every thread of the block.
 __device__ __forceinline__ void flush_viewmat_grad(float *v_viewmat,
-                                                   const M3 &v_R,
-                                                   const float v_t[3],
+                                                   const M3d &v_R,
+                                                   const double v_t[3],
                                                    float *s_red) {
     const uint32_t wave = threadIdx.x / kWave;
     float vals[12];
@@ -781,8 +853,8 @@ __device__ __forceinline__ void flush_viewmat_grad(float *v_viewmat,
     for (int i = 0; i < 3; ++i) {
 #pragma unroll
         for (int j = 0; j < 3; ++j)
-            vals[i * 4 + j] = v_R.m[i * 3 + j];
-        vals[i * 4 + 3] = v_t[i];
+            vals[i * 4 + j] = (float)v_R.m[i * 3 + j];
+        vals[i * 4 + 3] = (float)v_t[i];
     }
 #pragma unroll
     for (int k = 0; k < 12; ++k) {
@@ -801,6 +873,7 @@ __device__ __forceinline__ void flush_viewmat_grad(float *v_viewmat,
     __syncthreads();
 }
 
+template <bool kWantCam>
 __global__ void __launch_bounds__(kProjThreads)
     projection_fused_bwd_kernel(const BwdArgs a, const int32_t *__restrict__ radii,
                                 const int32_t *__restrict__ row_of) {
@@ -831,23 +904,23 @@ __global__ void __launch_bounds__(kProjThreads)
         load_geom(a.covars ? a.covars + bg * 6 : nullptr,
                   a.quats ? a.quats + bg * 4 : nullptr,
                   a.scales ? a.scales + bg * 3 : nullptr, G);
-    float v_mean[3] = {0.f, 0.f, 0.f};
+    double v_mean[3] = {0.0, 0.0, 0.0};
     float v_op = 0.f;
-    M3 v_S;
+    Sym3d v_S;
 #pragma unroll
-    for (int i = 0; i < 9; ++i)
-        v_S.m[i] = 0.f;
-    const bool want_cam = a.v_viewmats != nullptr;
+    for (int i = 0; i < 6; ++i)
+        v_S.v[i] = 0.0;
+    constexpr bool want_cam = kWantCam;
 
     // b is not uniform across the block when N is small; the camera loop is
     // over C for every thread, and the viewmat flush is done per (b, c) by
     // the threads that share that b (per-lane atomics when mixed).
     for (int64_t c = 0; c < a.C; ++c) {
-        M3 v_R;
-        float v_t[3] = {0.f, 0.f, 0.f};
+        M3d v_R;
+        double v_t[3] = {0.0, 0.0, 0.0};
 #pragma unroll
         for (int i = 0; i < 9; ++i)
-            v_R.m[i] = 0.f;
+            v_R.m[i] = 0.0;
         bool active = false;
         int64_t bc = b * a.C + c;
         if (seen) {
@@ -892,8 +965,8 @@ __global__ void __launch_bounds__(kProjThreads)
                 for (int i = 0; i < 3; ++i) {
 #pragma unroll
                     for (int j = 0; j < 3; ++j)
-                        atomic_add_f32(dst + i * 4 + j, v_R.m[i * 3 + j]);
-                    atomic_add_f32(dst + i * 4 + 3, v_t[i]);
+                        atomic_add_f32(dst + i * 4 + j, (float)v_R.m[i * 3 + j]);
+                    atomic_add_f32(dst + i * 4 + 3, (float)v_t[i]);
                 }
             }
         }
@@ -901,14 +974,17 @@ __global__ void __launch_bounds__(kProjThreads)
     if (!in_range)
         return;
     if (a.v_means != nullptr) {
+        // rounded to float32 before the added term: the sum autograd forms
+        // when the two gradients of the means come from separate nodes
+        float vm[3] = {(float)v_mean[0], (float)v_mean[1], (float)v_mean[2]};
         if (a.v_means_add != nullptr) {
 #pragma unroll
             for (int k = 0; k < 3; ++k)
-                v_mean[k] += a.v_means_add[bg * 3 + k];
+                vm[k] += a.v_means_add[bg * 3 + k];
         }
-        a.v_means[bg * 3 + 0] = v_mean[0];
-        a.v_means[bg * 3 + 1] = v_mean[1];
-        a.v_means[bg * 3 + 2] = v_mean[2];
+        a.v_means[bg * 3 + 0] = vm[0];
+        a.v_means[bg * 3 + 1] = vm[1];
+        a.v_means[bg * 3 + 2] = vm[2];
     }
     if (a.v_opacities != nullptr)
         a.v_opacities[bg] = v_op;
@@ -929,24 +1005,19 @@ __global__ void __launch_bounds__(kProjThreads)
     }
     if (a.covars != nullptr) {
         if (a.v_covars != nullptr) {
-            float *d = a.v_covars + bg * 6;
-            d[0] = v_S.m[0];
-            d[1] = v_S.m[1] + v_S.m[3];
-            d[2] = v_S.m[2] + v_S.m[6];
-            d[3] = v_S.m[4];
-            d[4] = v_S.m[5] + v_S.m[7];
-            d[5] = v_S.m[8];
+            covar6_grad(v_S, a.v_covars + bg * 6);
         }
     } else {
-        float v_q[4], v_s[3];
-        covar_vjp_to_quat_scale(G, v_S, v_q, v_s);
+        double v_q[4], v_s[3];
+        const double sd[3] = {G.s[0], G.s[1], G.s[2]};
+        covar_vjp_to_quat_scale(G.q, sd, v_S, v_q, v_s);
         if (a.v_quats != nullptr)
             reinterpret_cast<float4 *>(a.v_quats)[bg] =
-                make_float4(v_q[0], v_q[1], v_q[2], v_q[3]);
+                make_float4((float)v_q[0], (float)v_q[1], (float)v_q[2], (float)v_q[3]);
         if (a.v_scales != nullptr) {
-            a.v_scales[bg * 3 + 0] = v_s[0];
-            a.v_scales[bg * 3 + 1] = v_s[1];
-            a.v_scales[bg * 3 + 2] = v_s[2];
+            a.v_scales[bg * 3 + 0] = (float)v_s[0];
+            a.v_scales[bg * 3 + 1] = (float)v_s[1];
+            a.v_scales[bg * 3 + 2] = (float)v_s[2];
         }
     }
 }
@@ -960,14 +1031,16 @@ __global__ void __launch_bounds__(kProjThreads) projection_packed_bwd_kernel(
     const int64_t i = (int64_t)blockIdx.x * kProjThreads + threadIdx.x;
     const bool active = i < nnz;
     const bool want_cam = a.v_viewmats != nullptr;
-    float v_mean[3] = {0.f, 0.f, 0.f};
-    M3 v_S, v_R;
-    float v_t[3] = {0.f, 0.f, 0.f};
+    double v_mean[3] = {0.0, 0.0, 0.0};
+    Sym3d v_S;
+    M3d v_R;
+    double v_t[3] = {0.0, 0.0, 0.0};
 #pragma unroll
-    for (int k = 0; k < 9; ++k) {
-        v_S.m[k] = 0.f;
-        v_R.m[k] = 0.f;
-    }
+    for (int k = 0; k < 9; ++k)
+        v_R.m[k] = 0.0;
+#pragma unroll
+    for (int k = 0; k < 6; ++k)
+        v_S.v[k] = 0.0;
     int64_t b = 0, c = 0, g = 0;
     GaussGeom G;
     if (active) {
@@ -1004,8 +1077,8 @@ __global__ void __launch_bounds__(kProjThreads) projection_packed_bwd_kernel(
             for (int r = 0; r < 3; ++r) {
 #pragma unroll
                 for (int k = 0; k < 3; ++k)
-                    atomic_add_f32(dst + r * 4 + k, v_R.m[r * 3 + k]);
-                atomic_add_f32(dst + r * 4 + 3, v_t[r]);
+                    atomic_add_f32(dst + r * 4 + k, (float)v_R.m[r * 3 + k]);
+                atomic_add_f32(dst + r * 4 + 3, (float)v_t[r]);
             }
         }
     }
@@ -1014,22 +1087,26 @@ __global__ void __launch_bounds__(kProjThreads) projection_packed_bwd_kernel(
     float v_q[4] = {0.f, 0.f, 0.f, 0.f}, v_s[3] = {0.f, 0.f, 0.f};
     float v_c6[6];
     if (a.covars != nullptr) {
-        v_c6[0] = v_S.m[0];
-        v_c6[1] = v_S.m[1] + v_S.m[3];
-        v_c6[2] = v_S.m[2] + v_S.m[6];
-        v_c6[3] = v_S.m[4];
-        v_c6[4] = v_S.m[5] + v_S.m[7];
-        v_c6[5] = v_S.m[8];
+        covar6_grad(v_S, v_c6);
     } else {
-        covar_vjp_to_quat_scale(G, v_S, v_q, v_s);
+        double q4[4], s3[3];
+        const double sd[3] = {G.s[0], G.s[1], G.s[2]};
+        covar_vjp_to_quat_scale(G.q, sd, v_S, q4, s3);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            v_q[k] = (float)q4[k];
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+            v_s[k] = (float)s3[k];
     }
+    float v_meanf[3] = {(float)v_mean[0], (float)v_mean[1], (float)v_mean[2]};
     const bool direct = sparse_grad || single_image;
     const int64_t dst = sparse_grad ? i : b * a.N + g;
     if (direct) {
         if (a.v_means) {
-            a.v_means[dst * 3 + 0] = v_mean[0];
-            a.v_means[dst * 3 + 1] = v_mean[1];
-            a.v_means[dst * 3 + 2] = v_mean[2];
+            a.v_means[dst * 3 + 0] = v_meanf[0];
+            a.v_means[dst * 3 + 1] = v_meanf[1];
+            a.v_means[dst * 3 + 2] = v_meanf[2];
         }
         if (a.covars != nullptr) {
             if (a.v_covars)
@@ -1046,7 +1123,7 @@ __global__ void __launch_bounds__(kProjThreads) projection_packed_bwd_kernel(
     } else {
         if (a.v_means)
             for (int k = 0; k < 3; ++k)
-                atomic_add_f32(a.v_means + dst * 3 + k, v_mean[k]);
+                atomic_add_f32(a.v_means + dst * 3 + k, v_meanf[k]);
         if (a.covars != nullptr) {
             if (a.v_covars)
                 for (int k = 0; k < 6; ++k)
@@ -1101,16 +1178,20 @@ __device__ __forceinline__ void write_sym(const M3 &S, bool triu, float *out) {
 
 // dL/dS as a full matrix: triu entries cover both off-diagonal places, so
 // each place gets half of the entry's gradient.
-__device__ __forceinline__ M3 read_sym_grad(const float *g, bool triu) {
-    M3 v;
+// (A full 3x3 gradient enters through its symmetric part: the covariance
+// is symmetric.)
+__device__ __forceinline__ Sym3d read_sym_grad(const float *g, bool triu) {
+    Sym3d v;
     if (triu) {
-        v.m[0] = g[0];        v.m[1] = 0.5f * g[1]; v.m[2] = 0.5f * g[2];
-        v.m[3] = 0.5f * g[1]; v.m[4] = g[3];        v.m[5] = 0.5f * g[4];
-        v.m[6] = 0.5f * g[2]; v.m[7] = 0.5f * g[4]; v.m[8] = g[5];
+        v.v[0] = g[0];       v.v[1] = 0.5 * g[1]; v.v[2] = 0.5 * g[2];
+        v.v[3] = g[3];       v.v[4] = 0.5 * g[4]; v.v[5] = g[5];
     } else {
-#pragma unroll
-        for (int i = 0; i < 9; ++i)
-            v.m[i] = g[i];
+        v.v[0] = g[0];
+        v.v[1] = 0.5 * ((double)g[1] + g[3]);
+        v.v[2] = 0.5 * ((double)g[2] + g[6]);
+        v.v[3] = g[4];
+        v.v[4] = 0.5 * ((double)g[5] + g[7]);
+        v.v[5] = g[8];
     }
     return v;
 }
@@ -1157,47 +1238,47 @@ __global__ void __launch_bounds__(kProjThreads)
     if (i >= N)
         return;
     const int osz = triu ? 6 : 9;
-    GaussGeom G;
+    float q[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k)
-        G.q[k] = quats[i * 4 + k];
+        q[k] = quats[i * 4 + k];
+    double sd[3];
 #pragma unroll
     for (int k = 0; k < 3; ++k)
-        G.s[k] = scales[i * 3 + k];
-    quat_to_rot_exact(G.q[0], G.q[1], G.q[2], G.q[3], G.Rq.m);
-    float vq[4] = {0.f, 0.f, 0.f, 0.f}, vs[3] = {0.f, 0.f, 0.f};
+        sd[k] = scales[i * 3 + k];
+    double vq[4] = {0.0, 0.0, 0.0, 0.0}, vs[3] = {0.0, 0.0, 0.0};
     if (v_covars != nullptr) {
-        float q[4], s3[3];
-        covar_vjp_to_quat_scale(G, read_sym_grad(v_covars + i * osz, triu), q, s3);
+        double gq[4], gs3[3];
+        covar_vjp_to_quat_scale(q, sd, read_sym_grad(v_covars + i * osz, triu), gq, gs3);
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-            vq[k] += q[k];
+            vq[k] += gq[k];
 #pragma unroll
         for (int k = 0; k < 3; ++k)
-            vs[k] += s3[k];
+            vs[k] += gs3[k];
     }
     if (v_precis != nullptr) {
         // the precision is the covariance of scales 1/s: chain through
         // d(1/s)/ds = -1/s^2
-        GaussGeom P = G;
+        double inv_s[3];
 #pragma unroll
         for (int k = 0; k < 3; ++k)
-            P.s[k] = 1.f / G.s[k];
-        float q[4], s3[3];
-        covar_vjp_to_quat_scale(P, read_sym_grad(v_precis + i * osz, triu), q, s3);
+            inv_s[k] = 1.0 / sd[k];
+        double gq[4], gs3[3];
+        covar_vjp_to_quat_scale(q, inv_s, read_sym_grad(v_precis + i * osz, triu), gq, gs3);
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-            vq[k] += q[k];
+            vq[k] += gq[k];
 #pragma unroll
         for (int k = 0; k < 3; ++k)
-            vs[k] += -(P.s[k] * P.s[k]) * s3[k];
+            vs[k] += -(inv_s[k] * inv_s[k]) * gs3[k];
     }
 #pragma unroll
     for (int k = 0; k < 4; ++k)
-        v_quats[i * 4 + k] = vq[k];
+        v_quats[i * 4 + k] = (float)vq[k];
 #pragma unroll
     for (int k = 0; k < 3; ++k)
-        v_scales[i * 3 + k] = vs[k];
+        v_scales[i * 3 + k] = (float)vs[k];
 }
 
 }  // namespace
@@ -1308,9 +1389,10 @@ extern "C" int gsplat_projection_fused_bwd(
               conics, compensations, v_means2d, v_depths, v_conics,
               v_compensations, v_means, v_covars, v_quats, v_scales,
               v_viewmats};
-    projection_fused_bwd_kernel<<<(unsigned)ceil_div(B * N, kProjThreads),
-                                  kProjThreads, 0, as_stream(stream)>>>(
-        a, radii, nullptr);
+    auto kernel = v_viewmats != nullptr ? projection_fused_bwd_kernel<true>
+                                        : projection_fused_bwd_kernel<false>;
+    kernel<<<(unsigned)ceil_div(B * N, kProjThreads), kProjThreads, 0,
+             as_stream(stream)>>>(a, radii, nullptr);
     return check_launch("projection_fused_bwd_kernel");
 }
 
@@ -1342,9 +1424,10 @@ extern "C" int gsplat_projection_packed_bwd_rows(
               conics, compensations, v_means2d, v_depths, v_conics,
               v_compensations, v_means, v_covars, v_quats, v_scales,
               v_viewmats, v_row_opacities, v_opacities, v_means_add};
-    projection_fused_bwd_kernel<<<(unsigned)ceil_div(B * N, kProjThreads),
-                                  kProjThreads, 0, as_stream(stream)>>>(
-        a, nullptr, row_of);
+    auto kernel = v_viewmats != nullptr ? projection_fused_bwd_kernel<true>
+                                        : projection_fused_bwd_kernel<false>;
+    kernel<<<(unsigned)ceil_div(B * N, kProjThreads), kProjThreads, 0,
+             as_stream(stream)>>>(a, nullptr, row_of);
     return check_launch("projection_fused_bwd_kernel");
 }
 

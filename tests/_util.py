@@ -86,7 +86,7 @@ def assert_close(a, b, rtol, atol, name):
 
 
 GRAD_STRICT_SLACK = 5e-3  # strict-tolerance pass rate may trail fp32's by this
-GRAD_MAX_RATIO = 3.0      # worst element may exceed fp32's worst by this factor
+GRAD_MAX_RATIO = 2.5      # worst element may exceed fp32's worst by this factor
 GRAD_RMS_RATIO = 2.0      # RMS error may exceed fp32's by this factor
 
 
@@ -106,9 +106,9 @@ def assert_grad_close(got, ref64, ref32, rtol, atol, name):
         the float32 restatement's by at most 0.5 percentage points;
       * measured in units of tol, the RMS deviation from ref64 may be at
         most max(1, 2x) the float32 restatement's and the largest at most
-        max(1, 3x): the worst elements are sums whose terms cancel by two to
-        three orders of magnitude, and two float32 summation orders of the
-        same terms land 2-3x apart on them.
+        max(1, 2.5x): the worst elements are sums whose terms cancel by two
+        to three orders of magnitude, and two float32 summation orders of the
+        same terms land up to ~2x apart on them.
 
     Returns the report line."""
     a = got.detach().double().cpu()
@@ -124,10 +124,13 @@ def assert_grad_close(got, ref64, ref32, rtol, atol, name):
     frac32 = (e32 <= 1).double().mean().item()
     mx, mx32 = e.max().item(), e32.max().item()
     rms, rms32 = e.square().mean().sqrt().item(), e32.square().mean().sqrt().item()
+    worst = int(e.reshape(-1).argmax())
     msg = (f"{name}: numel {err.numel()}; within rtol={rtol} atol={atol}: {frac:.5f} "
            f"(fp32 restatement {frac32:.5f}); in units of tol: max {mx:.3g} "
            f"(fp32 {mx32:.3g}), rms {rms:.3g} (fp32 {rms32:.3g}); max abs "
-           f"{err.max().item():.3e} (fp32 {err32.max().item():.3e})")
+           f"{err.max().item():.3e} (fp32 {err32.max().item():.3e}); worst element "
+           f"{worst}: got {a.reshape(-1)[worst].item():.9g}, float64 "
+           f"{r.reshape(-1)[worst].item():.9g}, float32 {r32.reshape(-1)[worst].item():.9g}")
     assert frac >= frac32 - GRAD_STRICT_SLACK, msg
     assert mx <= max(1.0, GRAD_MAX_RATIO * mx32), msg
     assert rms <= max(1.0, GRAD_RMS_RATIO * rms32), msg
