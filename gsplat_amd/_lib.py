@@ -42,6 +42,11 @@ _SIGNATURES = {
         c_int32, c_int32, c_float, c_float, c_float, c_float, c_int32,
         _P, c_size_t,
         _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+    "gsplat_projection_packed_fwd_noalloc": [
+        c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P,
+        c_int32, c_int32, c_float, c_float, c_float, c_float, c_int32,
+        _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+    "gsplat_projection_packed_fwd_noalloc_max_rows": [],
     "gsplat_projection_packed_bwd": [
         c_int64, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P,
         c_int32, c_int32, c_float, c_int32,
@@ -109,6 +114,7 @@ _RESTYPES = {
     "gsplat_last_error": ctypes.c_char_p,
     "gsplat_version": ctypes.c_char_p,
     "gsplat_projection_packed_workspace_size": c_size_t,
+    "gsplat_projection_packed_fwd_noalloc_max_rows": c_int64,
     "gsplat_isect_count_workspace_size": c_size_t,
     "gsplat_sort_pairs_workspace_size": c_size_t,
     "gsplat_isect_prepare_workspace_size": c_size_t,

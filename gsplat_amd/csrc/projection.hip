@@ -21,6 +21,8 @@
 //     second launch, which projects every row twice);
 //   * the dense backward gives each Gaussian to one thread that loops over
 //     the C cameras, so gradients need no atomics and are deterministic.
+#include <mutex>
+
 #include "common.h"
 
 namespace gs {
@@ -1316,35 +1318,23 @@ extern "C" size_t gsplat_projection_packed_workspace_size(int64_t B, int64_t C,
     return lookback_bytes(ceil_div(B * C * N, kPackRows));
 }
 
-extern "C" int gsplat_projection_packed_fwd(
-    int64_t B, int64_t C, int64_t N, const float *means, const float *covars,
-    const float *quats, const float *scales, const float *opacities,
-    const float *viewmats, const float *Ks, int32_t image_width,
-    int32_t image_height, float eps2d, float near_plane, float far_plane,
-    float radius_clip, int32_t camera_model, void *workspace,
-    size_t workspace_bytes, int32_t *indptr, int64_t *batch_ids,
-    int64_t *camera_ids, int64_t *gaussian_ids, int32_t *radii,
-    float *means2d, float *depths, float *conics, float *compensations,
-    int64_t *nnz_out, int32_t *row_of, float *row_opacities,
-    gsplat_stream_t stream) {
-    clear_error();
-    GS_TRY(check_common(B, C, N, means, covars, quats, scales, viewmats, Ks,
-                        image_width, image_height, camera_model));
+namespace gs {
+namespace {
+
+// The packed forward over a caller-checked look-back workspace of at least
+// lookback_bytes(ceil(B*C*N / kPackRows)) bytes.
+int packed_fwd_launch(int64_t B, int64_t C, int64_t N, const float *means,
+                      const float *covars, const float *quats, const float *scales,
+                      const float *opacities, const float *viewmats, const float *Ks,
+                      int32_t image_width, int32_t image_height, float eps2d,
+                      float near_plane, float far_plane, float radius_clip,
+                      int32_t camera_model, void *workspace, int32_t *indptr,
+                      int64_t *batch_ids, int64_t *camera_ids, int64_t *gaussian_ids,
+                      int32_t *radii, float *means2d, float *depths, float *conics,
+                      float *compensations, int64_t *nnz_out, int32_t *row_of,
+                      float *row_opacities, hipStream_t st) {
     const int64_t rows = B * C * N;
-    GS_REQUIRE(indptr && nnz_out, "projection_packed: NULL indptr/nnz_out");
-    if (rows == 0)
-        return fail(GSPLAT_ERR_INVALID_ARGUMENT,
-                    "projection_packed: zero rows must be handled by the caller");
-    GS_REQUIRE(batch_ids && camera_ids && gaussian_ids && radii && means2d &&
-                   depths && conics,
-               "projection_packed: NULL output");
-    GS_REQUIRE(rows < (1ll << 31), "projection_packed: more than 2^31 rows");
-    GS_REQUIRE(row_opacities == nullptr || opacities != nullptr,
-               "projection_packed: row opacities need opacities");
     const int64_t blocks = ceil_div(rows, kPackRows);
-    GS_REQUIRE(workspace != nullptr && workspace_bytes >= lookback_bytes(blocks),
-               "projection_packed: workspace too small");
-    hipStream_t st = as_stream(stream);
     GS_TRY(clear_lookback(workspace, blocks, st));
     FwdArgs a{B, C, N, means, covars, quats, scales, opacities, viewmats, Ks,
               (float)image_width, (float)image_height, eps2d, near_plane,
@@ -1361,6 +1351,133 @@ extern "C" int gsplat_projection_packed_fwd(
             gaussian_ids, radii, means2d, depths, conics, compensations,
             nnz_out, row_of, row_opacities);
     return check_launch("projection_packed_fwd_kernel");
+}
+
+int check_packed_fwd(int64_t B, int64_t C, int64_t N, const float *means,
+                     const float *covars, const float *quats, const float *scales,
+                     const float *opacities, const float *viewmats, const float *Ks,
+                     int32_t image_width, int32_t image_height, int32_t camera_model,
+                     int32_t *indptr, int64_t *batch_ids, int64_t *camera_ids,
+                     int64_t *gaussian_ids, int32_t *radii, float *means2d,
+                     float *depths, float *conics, int64_t *nnz_out,
+                     float *row_opacities) {
+    GS_TRY(check_common(B, C, N, means, covars, quats, scales, viewmats, Ks,
+                        image_width, image_height, camera_model));
+    const int64_t rows = B * C * N;
+    GS_REQUIRE(indptr && nnz_out, "projection_packed: NULL indptr/nnz_out");
+    if (rows == 0)
+        return fail(GSPLAT_ERR_INVALID_ARGUMENT,
+                    "projection_packed: zero rows must be handled by the caller");
+    GS_REQUIRE(batch_ids && camera_ids && gaussian_ids && radii && means2d &&
+                   depths && conics,
+               "projection_packed: NULL output");
+    GS_REQUIRE(rows < (1ll << 31), "projection_packed: more than 2^31 rows");
+    GS_REQUIRE(row_opacities == nullptr || opacities != nullptr,
+               "projection_packed: row opacities need opacities");
+    return GSPLAT_OK;
+}
+
+// Scratch of the allocation-free packed forward: the look-back ticket and
+// status words of up to kNoAllocMaxBlocks workgroups (kPackRows rows each).
+// Each device holds its own copy for the life of the process; host code
+// reaches it only through the address hipGetSymbolAddress returns on that
+// device (the symbol's name is a host-side stand-in).
+constexpr int64_t kNoAllocMaxBlocks = int64_t(1) << 16;
+constexpr size_t kNoAllocScratchBytes = 256 + size_t(kNoAllocMaxBlocks) * sizeof(uint64_t);
+
+}  // namespace
+
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// The scratch address on the current device, looked up once per device.
+int device_scratch(void **out) {
+    int dev = -1;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess)
+        return fail(GSPLAT_ERR_LAUNCH, std::string("hipGetDevice: ") + hipGetErrorString(err));
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(GSPLAT_ERR_UNSUPPORTED, "projection_packed_fwd_noalloc: device index " +
+                                                std::to_string(dev) + " out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void *p = nullptr;
+        err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || p == nullptr)
+            return fail(GSPLAT_ERR_LAUNCH, std::string("hipGetSymbolAddress(scratch): ") +
+                                               hipGetErrorString(err));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return GSPLAT_OK;
+}
+
+}  // namespace
+}  // namespace gs
+
+extern "C" int gsplat_projection_packed_fwd(
+    int64_t B, int64_t C, int64_t N, const float *means, const float *covars,
+    const float *quats, const float *scales, const float *opacities,
+    const float *viewmats, const float *Ks, int32_t image_width,
+    int32_t image_height, float eps2d, float near_plane, float far_plane,
+    float radius_clip, int32_t camera_model, void *workspace,
+    size_t workspace_bytes, int32_t *indptr, int64_t *batch_ids,
+    int64_t *camera_ids, int64_t *gaussian_ids, int32_t *radii,
+    float *means2d, float *depths, float *conics, float *compensations,
+    int64_t *nnz_out, int32_t *row_of, float *row_opacities,
+    gsplat_stream_t stream) {
+    clear_error();
+    GS_TRY(check_packed_fwd(B, C, N, means, covars, quats, scales, opacities, viewmats,
+                            Ks, image_width, image_height, camera_model, indptr,
+                            batch_ids, camera_ids, gaussian_ids, radii, means2d, depths,
+                            conics, nnz_out, row_opacities));
+    const int64_t blocks = ceil_div(B * C * N, kPackRows);
+    GS_REQUIRE(workspace != nullptr && workspace_bytes >= lookback_bytes(blocks),
+               "projection_packed: workspace too small");
+    return packed_fwd_launch(B, C, N, means, covars, quats, scales, opacities, viewmats,
+                             Ks, image_width, image_height, eps2d, near_plane, far_plane,
+                             radius_clip, camera_model, workspace, indptr, batch_ids,
+                             camera_ids, gaussian_ids, radii, means2d, depths, conics,
+                             compensations, nnz_out, row_of, row_opacities,
+                             as_stream(stream));
+}
+
+extern "C" int64_t gsplat_projection_packed_fwd_noalloc_max_rows(void) {
+    return kNoAllocMaxBlocks * kPackRows;
+}
+
+extern "C" int gsplat_projection_packed_fwd_noalloc(
+    int64_t B, int64_t C, int64_t N, const float *means, const float *covars,
+    const float *quats, const float *scales, const float *opacities,
+    const float *viewmats, const float *Ks, int32_t image_width,
+    int32_t image_height, float eps2d, float near_plane, float far_plane,
+    float radius_clip, int32_t camera_model, int32_t *indptr, int64_t *batch_ids,
+    int64_t *camera_ids, int64_t *gaussian_ids, int32_t *radii, float *means2d,
+    float *depths, float *conics, float *compensations, int64_t *nnz_out,
+    int32_t *row_of, float *row_opacities, gsplat_stream_t stream) {
+    clear_error();
+    GS_TRY(check_packed_fwd(B, C, N, means, covars, quats, scales, opacities, viewmats,
+                            Ks, image_width, image_height, camera_model, indptr,
+                            batch_ids, camera_ids, gaussian_ids, radii, means2d, depths,
+                            conics, nnz_out, row_opacities));
+    const int64_t blocks = ceil_div(B * C * N, kPackRows);
+    if (blocks > kNoAllocMaxBlocks)
+        return fail(GSPLAT_ERR_WORKSPACE,
+                    "projection_packed_fwd_noalloc: " + std::to_string(B * C * N) +
+                        " rows exceed the static scratch's limit of " +
+                        std::to_string(kNoAllocMaxBlocks * kPackRows) + " rows");
+    void *ws = nullptr;
+    GS_TRY(device_scratch(&ws));
+    return packed_fwd_launch(B, C, N, means, covars, quats, scales, opacities, viewmats,
+                             Ks, image_width, image_height, eps2d, near_plane, far_plane,
+                             radius_clip, camera_model, ws, indptr, batch_ids, camera_ids,
+                             gaussian_ids, radii, means2d, depths, conics, compensations,
+                             nnz_out, row_of, row_opacities, as_stream(stream));
 }
 
 extern "C" int gsplat_projection_fused_bwd(

@@ -162,6 +162,33 @@ int gsplat_projection_packed_fwd(
     float *conics, float *compensations, int64_t *nnz_out, int32_t *row_of,
     float *row_opacities, gsplat_stream_t stream);
 
+/* Allocation-free variant of gsplat_projection_packed_fwd, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * Same arguments, outputs and results as gsplat_projection_packed_fwd without
+ * the workspace: the look-back scratch is a static device array of
+ * 256 + 65536 * 8 bytes (512 KiB) per GPU, held until the process ends, so
+ * B*C*N may be at most gsplat_projection_packed_fwd_noalloc_max_rows()
+ * (65536 workgroups of 4096 rows = 268,435,456 rows); larger inputs return
+ * GSPLAT_ERR_WORKSPACE.  Calls no hipMalloc/hipFree.  The scratch is shared
+ * by every call on one GPU and cleared by each call before use: calls that
+ * overlap on one GPU (concurrent streams or host threads) race. */
+int gsplat_projection_packed_fwd_noalloc(
+    int64_t B, int64_t C, int64_t N,
+    const float *means, const float *covars, const float *quats,
+    const float *scales, const float *opacities,
+    const float *viewmats, const float *Ks,
+    int32_t image_width, int32_t image_height,
+    float eps2d, float near_plane, float far_plane, float radius_clip,
+    int32_t camera_model,
+    int32_t *indptr, int64_t *batch_ids, int64_t *camera_ids,
+    int64_t *gaussian_ids, int32_t *radii, float *means2d, float *depths,
+    float *conics, float *compensations, int64_t *nnz_out, int32_t *row_of,
+    float *row_opacities, gsplat_stream_t stream);
+
+/* Largest B*C*N that gsplat_projection_packed_fwd_noalloc accepts. */
+int64_t gsplat_projection_packed_fwd_noalloc_max_rows(void);
+
 /* Backward of the packed projection over nnz rows.
  * Replaces projection_ewa_3dgs_packed_bwd
  *   (gsplat/cuda/csrc/Projection.cpp:439-576,

@@ -69,6 +69,13 @@ def test_argument_errors_are_reported_without_a_gpu(lib_path):
     with pytest.raises(RuntimeError, match="pinhole"):
         _lib.call("gsplat_projection_simple_fwd", 1, 1, 1, None, None, None, 16, 16, 2,
                   None, None, None)
+    # the allocation-free packed projection rejects sizes beyond its static
+    # scratch before touching the device (the pointers are never read)
+    limit = _lib.query("gsplat_projection_packed_fwd_noalloc_max_rows")
+    fake = [8] * 10
+    with pytest.raises(RuntimeError, match="exceed the static scratch"):
+        _lib.call("gsplat_projection_packed_fwd_noalloc", 1, 1, limit + 1, 8, None, 8, 8,
+                  None, 8, 8, 16, 16, 0.3, 0.01, 1e10, 0.0, 0, *fake, None, None, None)
 
 
 def test_reference_op_schemas_registered():
