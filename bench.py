@@ -6,7 +6,9 @@ one 1280x720 pinhole camera, gsplat_amd.rasterization() with the API defaults
 (packed=True, 16x16 tiles), L1 loss against a random target, backward to all
 Gaussian parameters.  Synthetic seeded data (gsplat_amd._helper.make_scene).
 
-Prints ONE JSON line (rank 0).  Besides ms/step it reports Mpix/s, a
+Prints ONE JSON line (rank 0).  The metric is the median of the per-step
+times of the K timed steps (HIP events between consecutive steps).  Besides
+ms/step it reports Mpix/s, a
 per-stage breakdown (HIP events around every C-ABI entry point, measured in a
 separate pass), the roofline of the dominant kernel (HIP events around that
 kernel inside the timed steps) and a CPU baseline: the host oracle pipeline
@@ -27,8 +29,20 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-METRIC = "ms per fwd+bwd step @1M Gaussians 1280x720 SH3; Mpix/s; % HBM roofline"
+# BASELINE.json's metric (config 1) and the same quantity named for the other
+# configurations' workloads
+METRICS = {
+    0: "ms per fwd+bwd step @10k Gaussians 256x256 SH0; Mpix/s; % HBM roofline",
+    1: "ms per fwd+bwd step @1M Gaussians 1280x720 SH3; Mpix/s; % HBM roofline",
+    2: "ms per fwd+bwd step @500k Gaussians 8x 960x540 SH1 RGB+ED; Mpix/s; % HBM roofline",
+    3: "ms per forward render @6M Gaussians 1920x1080 SH3; Mpix/s; % HBM roofline",
+    4: ("ms per optimizer step (fwd+bwd, absgrad stats, fused Adam) @2M Gaussians "
+        "1600x1040 SH3; Mpix/s; % HBM roofline"),
+}
 HBM_PEAK_GBS = 8000.0
+# MI355X: 256 CUs x 128 B/clk of LDS at 2.4 GHz
+LDS_PEAK_GBS = 256 * 128 * 2.4
+SIMDS = 1024
 F32 = 4
 
 
@@ -38,6 +52,8 @@ def _parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=1, choices=[0, 1, 2, 3, 4])
+    ap.add_argument("--unpacked", action="store_true",
+                    help="rasterization(packed=False) (dense [C, N] rows)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra-ops", action="store_true",
                     help="skip the timing of the ops outside the step (profiling runs)")
@@ -114,6 +130,8 @@ def _gpu_bench(args):
     scene = make_scene(args.config).to(dev)
     C = scene.viewmats.shape[0]
     kw = dict(scene.kwargs)
+    if args.unpacked:
+        kw["packed"] = False
 
     if args.config == 4:
         # full optimizer step: raw parameters, absgrad
@@ -203,18 +221,23 @@ def _gpu_bench(args):
         "C": C,
     }
 
-    # timed region: K steps, HIP events around the dominant entry point
+    # timed region: K steps, an event between consecutive steps (per-step
+    # times, their median is the metric) and HIP events around the dominant
+    # entry point
     torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     dom_timer = _lib.EntryTimer({dominant})
-    t0.record()
+    marks[0].record()
     with _lib.timing(dom_timer):
-        for _ in range(args.steps):
+        for k in range(args.steps):
             step()
-    t1.record()
+            marks[k + 1].record()
     torch.cuda.synchronize()
-    ms_per_step = t0.elapsed_time(t1) / args.steps
+    step_ms = sorted(marks[k].elapsed_time(marks[k + 1]) for k in range(args.steps))
+    mean_ms = marks[0].elapsed_time(marks[-1]) / args.steps
+    mid = len(step_ms) // 2
+    ms_per_step = (step_ms[mid] if len(step_ms) % 2 else
+                   0.5 * (step_ms[mid - 1] + step_ms[mid]))
     dom_ms = dom_timer.results()[dominant]
     dom_avg = sum(dom_ms) / len(dom_ms)
     abytes = _algorithmic_bytes(dominant, ctx)
@@ -235,6 +258,8 @@ def _gpu_bench(args):
         stage_report[k] = e
     return {
         "ms_per_step": ms_per_step,
+        "mean_ms_per_step": mean_ms,
+        "step_ms_min_max": (step_ms[0], step_ms[-1]),
         "roofline": roofline,
         "stages": stage_report,
         "extra_ops": None if args.no_extra_ops else _extra_ops(scene, meta, ctx),
@@ -304,6 +329,64 @@ def _extra_ops(scene, meta, ctx):
     return out
 
 
+def _copy_bandwidth():
+    """Measured HBM bandwidth of a plain device copy (256 MiB read + 256 MiB
+    written per launch, 10 launches, HIP events), reported beside the 8 TB/s
+    specification: the practical ceiling of a streaming kernel on this box."""
+    import torch
+
+    n = 64 * 1024 * 1024
+    src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(10):
+        dst.copy_(src)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / 10
+    return {"GBps": round(2 * n * 4 / (ms * 1e-3) / 1e9, 1), "bytes_per_launch": 2 * n * 4,
+            "ms_per_launch": round(ms, 4), "spec_GBps": HBM_PEAK_GBS}
+
+
+def _raster_counters(config):
+    """VALU and LDS figures of the two rasterizer kernels from the committed
+    rocprofv3 SQ-counter summary of the same workload
+    (profiles/cfg<N>_raster_sq_counters.txt), or None.
+
+    valu_busy = SQ_INSTS_VALU x 4 cycles (a wave64 instruction on a 16-lane
+    SIMD) / 1,024 SIMDs / (GRBM_GUI_ACTIVE / 8 XCDs); lds_GBps estimates the
+    LDS bytes as SQ_INSTS_LDS x 64 lanes x 4 B over the kernel's time
+    (GRBM_GUI_ACTIVE / 8 at 2.4 GHz), against 256 CUs x 128 B/clk."""
+    f = ROOT / "profiles" / f"cfg{config}_raster_sq_counters.txt"
+    if not f.exists():
+        return None
+    out, cur = {}, None
+    for line in f.read_text().splitlines():
+        if line.startswith("void gs::rasterize_"):
+            cur = "bwd" if "rasterize_bwd" in line else "fwd"
+            out[cur] = {}
+        elif cur and line.strip() and line.split()[0].isupper():
+            k, v = line.split()[:2]
+            out[cur][k] = float(v)
+    res = {}
+    for k, c in out.items():
+        if "GRBM_GUI_ACTIVE" not in c or "SQ_INSTS_VALU" not in c:
+            continue
+        cycles = c["GRBM_GUI_ACTIVE"] / 8.0
+        secs = cycles / 2.4e9
+        lds_bytes = c.get("SQ_INSTS_LDS", 0.0) * 64 * 4
+        res[k] = {"valu_busy": round(c["SQ_INSTS_VALU"] * 4 / SIMDS / cycles, 3),
+                  "lds_GBps": round(lds_bytes / secs / 1e9, 1),
+                  "lds_peak_GBps": LDS_PEAK_GBS,
+                  "lds_bank_conflicts": int(c.get("SQ_LDS_BANK_CONFLICT", 0)),
+                  "source": f.name}
+    return res or None
+
+
 def _measured_traffic(kernel, config):
     """HBM bytes per launch of an entry point's kernel, from the committed
     rocprofv3 PMC summary of the same workload (FETCH_SIZE and WRITE_SIZE
@@ -319,7 +402,7 @@ def _measured_traffic(kernel, config):
     return None
 
 
-def _cpu_baseline(config, stride):
+def _cpu_baseline(config, stride, packed=True):
     """Oracle pipeline on the host: full projection / SH / intersection for all
     Gaussians plus rasterization on a strided sample of the tiles, fwd+bwd.
 
@@ -351,7 +434,7 @@ def _cpu_baseline(config, stride):
                 leaves["means"], leaves["quats"], leaves["scales"], leaves["opacities"],
                 leaves["colors"], scene.viewmats, scene.Ks, scene.width, scene.height,
                 sh_degree=scene.sh_degree, dtype=torch.float32, tile_subset=subset,
-                **scene.kwargs)
+                packed=packed, **scene.kwargs)
         if fwd_only:
             return time.perf_counter() - t
         loss = (rc - scene.target).abs().mean()
@@ -379,6 +462,8 @@ def _cpu_baseline(config, stride):
         "unit": "ms/step",
         "cores": torch.get_num_threads(),
         "kind": "port",
+        "method": ("extrapolated: fixed part + per-tile rasterization cost x all tiles, "
+                   "from two timed strided tile samples"),
         "sample": (f"config {config}: oracle {'fwd' if fwd_only else 'fwd+bwd'}"
                    f"{' + Adam' if config == 4 else ''} with projection+SH+intersection for all "
                    f"{scene.means.shape[0]} Gaussians and rasterization on {len(sample_b)} "
@@ -399,6 +484,7 @@ def main():
         _copy_calibration()
         return
     res = _gpu_bench(args)
+    copy_bw = _copy_bandwidth()
     if args.stages_only:
         print(json.dumps(res["stages"], indent=1))
         return
@@ -408,7 +494,7 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         stride = args.cpu_tile_stride or {0: 1, 1: 12, 2: 48, 3: 30, 4: 20}[args.config]
-        cpu = _cpu_baseline(args.config, stride)
+        cpu = _cpu_baseline(args.config, stride, packed=not args.unpacked)
     workload = {
         0: "cfg0: 10k Gaussians, SH0, 256x256, packed, fwd+bwd L1",
         1: "cfg1: 1M Gaussians, SH3, 1280x720, packed, fwd+bwd L1",
@@ -417,8 +503,10 @@ def main():
         4: ("cfg4: 2M Gaussians, SH3, 1600x1040, fwd+bwd L1 with absgrad stats and "
             "fused Adam over 6 tensors"),
     }[args.config]
+    if args.unpacked:
+        workload = workload.replace("packed,", "unpacked (packed=False),")
     out = {
-        "metric": METRIC,
+        "metric": METRICS[args.config],
         "value": round(res["ms_per_step"], 4),
         "unit": "ms/step",
         "n_gpus": 1,
@@ -434,7 +522,13 @@ def main():
                    "width": scene.width, "height": scene.height, "cameras": C,
                    "n_isects": res["ctx"]["n_isects"], "visible_rows": res["ctx"]["nnz"]},
         "mpix_per_s": round(mpix, 2),
+        "timing": {"statistic": "median of per-step times (HIP events between steps)",
+                   "mean_ms_per_step": round(res["mean_ms_per_step"], 4),
+                   "min_ms": round(res["step_ms_min_max"][0], 4),
+                   "max_ms": round(res["step_ms_min_max"][1], 4)},
         "roofline": res["roofline"],
+        "hbm_copy": copy_bw,
+        "raster_counters": _raster_counters(args.config),
         "stages_ms": res["stages"],
         "extra_ops_ms": res["extra_ops"],
         "cpu_baseline": cpu,
