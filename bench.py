@@ -137,7 +137,7 @@ def _gpu_bench(args):
         # full optimizer step: raw parameters, absgrad
         # densification statistics, one fused Adam launch over six tensors
         from gsplat_amd.cuda import _ops
-        from gsplat_amd.strategy.stats import accumulate_grad2d_stats
+        from gsplat_amd.strategy.stats import accumulate_grad2d_stats, fuse_grad2d_stats
         raw = {
             "means": scene.means, "log_scales": scene.log_scales,
             "quats": scene.quats, "opacity_logits": scene.opacity_logits,
@@ -158,11 +158,15 @@ def _gpu_bench(args):
                 torch.sigmoid(params["opacity_logits"]),
                 torch.cat([params["sh0"], params["shN"]], dim=1), scene.viewmats,
                 scene.Ks, scene.width, scene.height, sh_degree=scene.sh_degree, **kw)
+            # the densification statistics join the projection's backward pass
+            stats["grad2d"], stats["count"], fused = fuse_grad2d_stats(
+                meta, stats["grad2d"], stats["count"], scene.means.shape[0])
             loss = (rc - scene.target).abs().mean()
             loss.backward()
-            stats["grad2d"], stats["count"] = accumulate_grad2d_stats(
-                meta, stats["grad2d"], stats["count"], scene.means.shape[0],
-                packed=True, absgrad=True)
+            if not fused:
+                stats["grad2d"], stats["count"] = accumulate_grad2d_stats(
+                    meta, stats["grad2d"], stats["count"], scene.means.shape[0],
+                    packed=True, absgrad=True)
             with torch.no_grad():
                 _ops.adam_multi(
                     [(params[k], params[k].grad, moments[k][0], moments[k][1], None,

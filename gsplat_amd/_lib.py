@@ -56,6 +56,11 @@ _SIGNATURES = {
         c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P,
         c_int32, c_int32, c_float, c_int32,
         _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+    "gsplat_projection_packed_bwd_rows_stats": [
+        c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P,
+        c_int32, c_int32, c_float, c_int32,
+        _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+        _P, c_float, c_float, _P, _P, _P],
     "gsplat_sh_fwd": [c_int64, c_int32, c_int32, _P, _P, _P, _P, _P],
     "gsplat_sh_bwd": [c_int64, c_int32, c_int32, _P, _P, _P, _P, _P, _P, _P],
     "gsplat_sh_rows_fwd": [c_int64, c_int64, c_int64, c_int32, c_int32,

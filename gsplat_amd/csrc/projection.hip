@@ -841,6 +841,11 @@ struct BwdArgs {
     const float *v_row_opacities;
     float *v_opacities;
     const float *v_means_add;
+    // densification statistics (B == 1): per packed row,
+    // grad2d[g] += ||(stat_grads[row] * (stat_sx, stat_sy))||, count[g] += 1
+    const float *stat_grads;
+    float stat_sx, stat_sy;
+    float *grad2d, *count;
 };
 
 // Reduce v_R (9) and v_t (3) of the workgroup and add them to the camera's
@@ -908,6 +913,7 @@ __global__ void __launch_bounds__(kProjThreads)
                   a.scales ? a.scales + bg * 3 : nullptr, G);
     double v_mean[3] = {0.0, 0.0, 0.0};
     float v_op = 0.f;
+    float stat_norm = 0.f, stat_rows = 0.f;
     Sym3d v_S;
 #pragma unroll
     for (int i = 0; i < 6; ++i)
@@ -937,6 +943,12 @@ __global__ void __launch_bounds__(kProjThreads)
             if (active) {
                 if (a.v_row_opacities != nullptr)
                     v_op += a.v_row_opacities[row];
+                if (a.stat_grads != nullptr) {
+                    const float sx = a.stat_grads[row * 2] * a.stat_sx;
+                    const float sy = a.stat_grads[row * 2 + 1] * a.stat_sy;
+                    stat_norm += sqrtf(sx * sx + sy * sy);
+                    stat_rows += 1.f;
+                }
                 Cam cam;
                 load_cam(a.viewmats + bc * 16, a.Ks + bc * 9, cam);
                 const bool has_comp = a.v_compensations != nullptr;
@@ -990,6 +1002,10 @@ __global__ void __launch_bounds__(kProjThreads)
     }
     if (a.v_opacities != nullptr)
         a.v_opacities[bg] = v_op;
+    if (a.grad2d != nullptr && stat_rows > 0.f) {
+        a.grad2d[bg] += stat_norm;
+        a.count[bg] += stat_rows;
+    }
     if (!seen) {
         // visible in no camera: zero gradient rows
         if (a.covars != nullptr) {
@@ -1513,6 +1529,28 @@ extern "C" int gsplat_projection_fused_bwd(
     return check_launch("projection_fused_bwd_kernel");
 }
 
+namespace gs {
+namespace {
+
+int packed_bwd_rows_launch(const BwdArgs &a, const int32_t *row_of, hipStream_t st) {
+    GS_REQUIRE((a.v_row_opacities == nullptr) == (a.v_opacities == nullptr),
+               "projection_packed_bwd_rows: v_row_opacities and v_opacities go together");
+    GS_REQUIRE(a.v_means_add == nullptr || a.v_means != nullptr,
+               "projection_packed_bwd_rows: v_means_add needs v_means");
+    GS_REQUIRE(row_of && a.conics && a.v_means2d && a.v_conics,
+               "projection_packed_bwd_rows: NULL buffer");
+    GS_REQUIRE(a.v_compensations == nullptr || a.compensations != nullptr,
+               "projection_packed_bwd_rows: v_compensations needs compensations");
+    auto kernel = a.v_viewmats != nullptr ? projection_fused_bwd_kernel<true>
+                                          : projection_fused_bwd_kernel<false>;
+    kernel<<<(unsigned)ceil_div(a.B * a.N, kProjThreads), kProjThreads, 0, st>>>(
+        a, nullptr, row_of);
+    return check_launch("projection_fused_bwd_kernel");
+}
+
+}  // namespace
+}  // namespace gs
+
 extern "C" int gsplat_projection_packed_bwd_rows(
     int64_t B, int64_t C, int64_t N, const float *means, const float *covars,
     const float *quats, const float *scales, const float *viewmats,
@@ -1528,24 +1566,41 @@ extern "C" int gsplat_projection_packed_bwd_rows(
                         image_width, image_height, camera_model));
     if (B * N == 0)
         return GSPLAT_OK;
-    GS_REQUIRE((v_row_opacities == nullptr) == (v_opacities == nullptr),
-               "projection_packed_bwd_rows: v_row_opacities and v_opacities go together");
-    GS_REQUIRE(v_means_add == nullptr || v_means != nullptr,
-               "projection_packed_bwd_rows: v_means_add needs v_means");
-    GS_REQUIRE(row_of && conics && v_means2d && v_conics,
-               "projection_packed_bwd_rows: NULL buffer");
-    GS_REQUIRE(v_compensations == nullptr || compensations != nullptr,
-               "projection_packed_bwd_rows: v_compensations needs compensations");
     BwdArgs a{B, C, N, means, covars, quats, scales, viewmats, Ks,
               (float)image_width, (float)image_height, eps2d, camera_model,
               conics, compensations, v_means2d, v_depths, v_conics,
               v_compensations, v_means, v_covars, v_quats, v_scales,
-              v_viewmats, v_row_opacities, v_opacities, v_means_add};
-    auto kernel = v_viewmats != nullptr ? projection_fused_bwd_kernel<true>
-                                        : projection_fused_bwd_kernel<false>;
-    kernel<<<(unsigned)ceil_div(B * N, kProjThreads), kProjThreads, 0,
-             as_stream(stream)>>>(a, nullptr, row_of);
-    return check_launch("projection_fused_bwd_kernel");
+              v_viewmats, v_row_opacities, v_opacities, v_means_add,
+              nullptr, 0.f, 0.f, nullptr, nullptr};
+    return packed_bwd_rows_launch(a, row_of, as_stream(stream));
+}
+
+extern "C" int gsplat_projection_packed_bwd_rows_stats(
+    int64_t B, int64_t C, int64_t N, const float *means, const float *covars,
+    const float *quats, const float *scales, const float *viewmats,
+    const float *Ks, int32_t image_width, int32_t image_height, float eps2d,
+    int32_t camera_model, const int32_t *row_of, const float *conics,
+    const float *compensations, const float *v_means2d, const float *v_depths,
+    const float *v_conics, const float *v_compensations, float *v_means,
+    float *v_covars, float *v_quats, float *v_scales, float *v_viewmats,
+    const float *v_row_opacities, float *v_opacities, const float *v_means_add,
+    const float *stat_grads, float stat_scale_x, float stat_scale_y, float *grad2d,
+    float *count, gsplat_stream_t stream) {
+    clear_error();
+    GS_TRY(check_common(B, C, N, means, covars, quats, scales, viewmats, Ks,
+                        image_width, image_height, camera_model));
+    GS_REQUIRE(B == 1, "projection_packed_bwd_rows_stats: one batch only");
+    GS_REQUIRE(stat_grads && grad2d && count,
+               "projection_packed_bwd_rows_stats: NULL statistics buffer");
+    if (B * N == 0)
+        return GSPLAT_OK;
+    BwdArgs a{B, C, N, means, covars, quats, scales, viewmats, Ks,
+              (float)image_width, (float)image_height, eps2d, camera_model,
+              conics, compensations, v_means2d, v_depths, v_conics,
+              v_compensations, v_means, v_covars, v_quats, v_scales,
+              v_viewmats, v_row_opacities, v_opacities, v_means_add,
+              stat_grads, stat_scale_x, stat_scale_y, grad2d, count};
+    return packed_bwd_rows_launch(a, row_of, as_stream(stream));
 }
 
 extern "C" int gsplat_projection_packed_bwd(

@@ -511,12 +511,16 @@ def projection_packed_bwd_rows(
     viewmats_requires_grad: bool,
     v_row_opacities: Optional[Tensor] = None,
     v_means_add: Optional[Tensor] = None,
+    stats: Optional[Tuple[Tensor, float, float, Tensor, Tensor]] = None,
 ):
     """Dense gradients of the packed projection from its row map ``row_of``
     (one pass driven by Gaussian; no zero fill, no atomics).  ``v_depths``
     may be None (zero gradient).  With ``v_row_opacities`` [nnz] it also
     returns v_opacities (each Gaussian's sum over its rows, shaped like
     ``means[..., 0]``); ``v_means_add`` (like ``means``) is added to v_means.
+    ``stats`` = (row gradients [nnz, 2], scale_x, scale_y, grad2d [N],
+    count [N]) also accumulates the densification statistics in the same pass
+    (one batch only).
     Returns (v_means, v_covars, v_quats, v_scales, v_viewmats[, v_opacities])."""
     _check_proj_inputs(means, covars, quats, scales, None, viewmats, Ks)
     check_input(row_of, "row_of", _I32)
@@ -547,13 +551,24 @@ def projection_packed_bwd_rows(
         if v_row_opacities is not None:
             return v_means, v_covars, v_quats, v_scales, v_viewmats, v_opacities
         return v_means, v_covars, v_quats, v_scales, v_viewmats
-    call("gsplat_projection_packed_bwd_rows", B, C, N, ptr(means), ptr(covars),
-         ptr(quats), ptr(scales), ptr(viewmats), ptr(Ks), int(image_width),
-         int(image_height), float(eps2d), int(camera_model), ptr(row_of),
-         ptr(conics), ptr(compensations), ptr(v_means2d), ptr(v_depths),
-         ptr(v_conics), ptr(v_compensations), ptr(v_means), ptr(v_covars),
-         ptr(v_quats), ptr(v_scales), ptr(v_viewmats), ptr(v_row_opacities),
-         ptr(v_opacities), ptr(v_means_add), _stream(means))
+    args = [B, C, N, ptr(means), ptr(covars), ptr(quats), ptr(scales), ptr(viewmats),
+            ptr(Ks), int(image_width), int(image_height), float(eps2d),
+            int(camera_model), ptr(row_of), ptr(conics), ptr(compensations),
+            ptr(v_means2d), ptr(v_depths), ptr(v_conics), ptr(v_compensations),
+            ptr(v_means), ptr(v_covars), ptr(v_quats), ptr(v_scales), ptr(v_viewmats),
+            ptr(v_row_opacities), ptr(v_opacities), ptr(v_means_add)]
+    if stats is None:
+        call("gsplat_projection_packed_bwd_rows", *args, _stream(means))
+    else:
+        grads, sx, sy, grad2d, count = stats
+        check_input(grads, "stat_grads", _F32)
+        check_input(grad2d, "grad2d", _F32)
+        check_input(count, "count", _F32)
+        if grads.shape != conics[:, :2].shape or grad2d.numel() != N or count.numel() != N:
+            raise RuntimeError("projection_packed_bwd_rows: statistics buffers must be "
+                               "[nnz, 2] row gradients and [N] accumulators")
+        call("gsplat_projection_packed_bwd_rows_stats", *args, ptr(grads), float(sx),
+             float(sy), ptr(grad2d), ptr(count), _stream(means))
     if v_row_opacities is not None:
         return v_means, v_covars, v_quats, v_scales, v_viewmats, v_opacities
     return v_means, v_covars, v_quats, v_scales, v_viewmats

@@ -739,6 +739,19 @@ class _PackedSphericalHarmonics(torch.autograd.Function):
                 v_coeffs if ctx.needs_input_grad[2] else None, None, None, None)
 
 
+class Grad2dStatsSlot:
+    """Carries a densification-statistics request from the caller to the
+    packed front end's backward (``gsplat_amd.strategy.stats.fuse_grad2d_stats``
+    fills it between the forward and ``backward()``): the projection backward
+    then accumulates the statistics in its own pass."""
+
+    def __init__(self, width: int, height: int, n_cameras: int):
+        self.scale_x = width / 2.0 * n_cameras
+        self.scale_y = height / 2.0 * n_cameras
+        self.means2d: Optional[Tensor] = None
+        self.request = None  # (grad2d, count, absgrad)
+
+
 class _PackedFrontEnd(torch.autograd.Function):
     """rasterization()'s packed front end as one node: the packed projection
     (``_FullyFusedProjectionPacked``), the per-row opacities
@@ -755,7 +768,8 @@ class _PackedFrontEnd(torch.autograd.Function):
     @staticmethod
     def forward(ctx, means, covars, quats, scales, opacities, features, viewmats,
                 Ks, width, height, eps2d, near_plane, far_plane, radius_clip,
-                calc_compensations, camera_model, sh_degree, isect=None):
+                calc_compensations, camera_model, sh_degree, isect=None,
+                stats_slot=None):
         cm = _camera_model_type(camera_model)
         (indptr, batch_ids, camera_ids, gaussian_ids, radii, means2d, depths,
          conics, compensations, row_of, row_opac, row_colors) = _ops.packed_front_fwd(
@@ -772,6 +786,7 @@ class _PackedFrontEnd(torch.autograd.Function):
         ctx.eps2d = eps2d
         ctx.camera_model_type = cm
         ctx.sh_degree = sh_degree
+        ctx.stats_slot = stats_slot
         ctx.mark_non_differentiable(batch_ids, camera_ids, gaussian_ids, indptr, radii,
                                     row_of)
         return (batch_ids, camera_ids, gaussian_ids, indptr, radii, means2d,
@@ -814,12 +829,21 @@ class _PackedFrontEnd(torch.autograd.Function):
         v_conics = torch.zeros_like(conics) if v_conics is None else v_conics.contiguous()
         v_row_opac = (v_row_opac.contiguous() if v_row_opac is not None and need[4]
                       else None)
+        stats = None
+        slot = ctx.stats_slot
+        if slot is not None and slot.request is not None:
+            grad2d, count, absgrad = slot.request
+            rows = getattr(slot.means2d, "absgrad", None) if absgrad else v_means2d
+            if rows is None:
+                raise RuntimeError("fused densification statistics need absgrad=True "
+                                   "in rasterization()")
+            stats = (rows.contiguous(), slot.scale_x, slot.scale_y, grad2d, count)
         res = _ops.projection_packed_bwd_rows(
             means, covars, quats, scales, viewmats, Ks, ctx.width, ctx.height,
             ctx.eps2d, ctx.camera_model_type, row_of, conics, compensations,
             v_means2d, None if v_depths is None else v_depths.contiguous(),
             v_conics, v_compensations, False, v_row_opacities=v_row_opac,
-            v_means_add=v_means_sh)
+            v_means_add=v_means_sh, stats=stats)
         v_means, v_covars, v_quats, v_scales = res[:4]
         v_opacities = res[5] if v_row_opac is not None else None
         return (v_means if need[0] else None,
@@ -827,7 +851,8 @@ class _PackedFrontEnd(torch.autograd.Function):
                 v_quats if need[2] else None,
                 v_scales if need[3] else None,
                 v_opacities, v_features,
-                None, None, None, None, None, None, None, None, None, None, None, None)
+                None, None, None, None, None, None, None, None, None, None, None, None,
+                None)
 
 
 class _RasterizeToPixels(torch.autograd.Function):

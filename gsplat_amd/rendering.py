@@ -22,6 +22,7 @@ from typing_extensions import Literal
 from .cuda import _ops
 from .cuda._wrapper import (
     CameraModel,
+    Grad2dStatsSlot,
     _PackedFrontEnd,
     _PackedRowsGather,
     _PackedSphericalHarmonics,
@@ -242,6 +243,9 @@ def rasterization(
                  if front_end and rasterize_mode != "antialiased" else None)
     row_of = None
     if front_end:
+        # densification statistics can join the projection backward (one
+        # batch; gsplat_amd.strategy.stats.fuse_grad2d_stats)
+        stats_slot = Grad2dStatsSlot(width, height, C) if B == 1 else None
         (batch_ids, camera_ids, gaussian_ids, indptr, radii, means2d, depths,
          conics, compensations, row_of, opacities, proj_features) = _PackedFrontEnd.apply(
             means.contiguous(), None if covars is None else covars.contiguous(),
@@ -250,7 +254,10 @@ def rasterization(
             opacities.contiguous(), colors.contiguous(), viewmats.contiguous(),
             Ks.contiguous(), width, height, eps2d, near_plane, far_plane,
             radius_clip, rasterize_mode == "antialiased", camera_model,
-            colors_sh_degree, isect_req)
+            colors_sh_degree, isect_req, stats_slot)
+        if stats_slot is not None:
+            stats_slot.means2d = means2d
+            meta["grad2d_stats_slot"] = stats_slot
         nnz = means2d.shape[0]
         image_ids = camera_ids if B * C == 1 else batch_ids * C + camera_ids
     elif packed:

@@ -48,3 +48,30 @@ def accumulate_grad2d_stats(
         _ops.grad2d_stats(grads.contiguous(), None, info["radii"].contiguous(),
                           n_gaussians, sx, sy, grad2d, count)
     return grad2d, count
+
+
+def fuse_grad2d_stats(
+    info: Dict,
+    grad2d: Optional[Tensor],
+    count: Optional[Tensor],
+    n_gaussians: int,
+    absgrad: bool = True,
+):
+    """Requests the same statistics update as ``accumulate_grad2d_stats``,
+    performed inside the backward pass by the packed projection's own
+    gradient kernel instead of a separate pass over the rows afterwards.
+
+    Call it between ``rasterization()`` and ``backward()``.  Available for the
+    packed path with one batch (``info["grad2d_stats_slot"]`` present);
+    returns ``(grad2d, count, fused)``, and when ``fused`` is False the
+    caller runs ``accumulate_grad2d_stats`` after the backward as usual."""
+    slot = info.get("grad2d_stats_slot")
+    means2d = info["means2d"]
+    if grad2d is None:
+        grad2d = torch.zeros(n_gaussians, device=means2d.device)
+    if count is None:
+        count = torch.zeros(n_gaussians, device=means2d.device)
+    if slot is None or grad2d.numel() != n_gaussians or count.numel() != n_gaussians:
+        return grad2d, count, False
+    slot.request = (grad2d, count, absgrad)
+    return grad2d, count, True

@@ -242,6 +242,27 @@ int gsplat_projection_packed_bwd_rows(
     const float *v_means_add,
     gsplat_stream_t stream);
 
+/* gsplat_projection_packed_bwd_rows with the densification statistics of
+ * DefaultStrategy._update_state (gsplat/strategy/default.py:235-268) in the
+ * same pass, for one batch (B == 1): for every packed row r of Gaussian g,
+ *   grad2d[g] += || (stat_grads[r,0] * stat_scale_x, stat_grads[r,1] * stat_scale_y) ||
+ *   count[g]  += 1
+ * stat_grads [nnz,2] are the rows' 2D mean gradients (absgrad or grad),
+ * stat_scale_x/y = W/2 * C and H/2 * C; grad2d [N] and count [N] accumulate
+ * in place.  Replaces the separate statistics pass (gsplat_grad2d_stats)
+ * after the backward. */
+int gsplat_projection_packed_bwd_rows_stats(
+    int64_t B, int64_t C, int64_t N, const float *means, const float *covars,
+    const float *quats, const float *scales, const float *viewmats, const float *Ks,
+    int32_t image_width, int32_t image_height, float eps2d, int32_t camera_model,
+    const int32_t *row_of, const float *conics, const float *compensations,
+    const float *v_means2d, const float *v_depths, const float *v_conics,
+    const float *v_compensations, float *v_means, float *v_covars, float *v_quats,
+    float *v_scales, float *v_viewmats, const float *v_row_opacities,
+    float *v_opacities, const float *v_means_add, const float *stat_grads,
+    float stat_scale_x, float stat_scale_y, float *grad2d, float *count,
+    gsplat_stream_t stream);
+
 /* Covariance and/or precision matrices from quaternions and scales.
  * Replaces quat_scale_to_covar_preci_fwd
  *   (gsplat/cuda/csrc/QuatScaleToCovar.cpp:37-72,

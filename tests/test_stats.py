@@ -83,3 +83,39 @@ def test_grad2d_stats_reads_unaligned_views():
     ref_g, ref_c = torch_ref.grad2d_stats_ref(grads, ids, None, N, 1600, 1040, 1)
     _check(grad2d, ref_g)
     assert torch.equal(count.cpu().double(), ref_c)
+
+
+@pytest.mark.parametrize("C,absgrad", [(1, True), (3, True), (2, False)])
+def test_grad2d_stats_fused_into_projection_backward(C, absgrad):
+    """fuse_grad2d_stats: the statistics accumulated by the packed projection's
+    backward pass equal the separate pass over the same step's row gradients
+    (and the float64 restatement), onto existing state."""
+    import gsplat_amd as gs
+    from gsplat_amd.strategy.stats import accumulate_grad2d_stats, fuse_grad2d_stats
+    from tests._util import small_scene
+    means, quats, scales, opac, vm, K, W, H = small_scene(seed=30 + C, N=20_000, C=C)
+    g = torch.Generator().manual_seed(C)
+    colors = torch.rand(means.shape[0], 3, generator=g)
+    prev_g = torch.rand(means.shape[0], generator=g)
+    prev_c = torch.randint(0, 5, (means.shape[0],), generator=g).float()
+    ins = [t.to(DEV).requires_grad_() for t in (means, quats, scales, opac, colors)]
+    rc, ra, meta = gs.rasterization(*ins, vm.to(DEV), K.to(DEV), W, H, absgrad=absgrad)
+    grad2d, count, fused = fuse_grad2d_stats(meta, prev_g.to(DEV).clone(),
+                                             prev_c.to(DEV).clone(), means.shape[0],
+                                             absgrad=absgrad)
+    assert fused
+    target = torch.rand(rc.shape, generator=g).to(DEV)
+    if not absgrad:
+        meta["means2d"].retain_grad()
+    (rc - target).abs().mean().backward()
+    sep_g, sep_c = accumulate_grad2d_stats(meta, prev_g.to(DEV).clone(),
+                                           prev_c.to(DEV).clone(), means.shape[0],
+                                           packed=True, absgrad=absgrad)
+    rows = meta["means2d"].absgrad if absgrad else meta["means2d"].grad
+    assert float(rows.abs().sum()) > 0
+    ref_g, ref_c = torch_ref.grad2d_stats_ref(rows.cpu(), meta["gaussian_ids"].cpu(), None,
+                                              means.shape[0], W, H, C, prev_g, prev_c)
+    assert torch.equal(count.cpu(), sep_c.cpu())
+    assert torch.equal(count.cpu().double(), ref_c)
+    _check(grad2d, ref_g)
+    torch.testing.assert_close(grad2d, sep_g, rtol=1e-6, atol=1e-9)
