@@ -55,6 +55,8 @@ def _parse():
     ap.add_argument("--unpacked", action="store_true",
                     help="rasterization(packed=False) (dense [C, N] rows)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-copy-bandwidth", action="store_true",
+                    help="skip the device-copy bandwidth measurement (profiling runs)")
     ap.add_argument("--no-extra-ops", action="store_true",
                     help="skip the timing of the ops outside the step (profiling runs)")
     ap.add_argument("--cpu-tile-stride", type=int, default=0,
@@ -283,7 +285,7 @@ def _extra_ops(scene, meta, ctx):
     from gsplat_amd import _lib
     from gsplat_amd.cuda import _ops
 
-    if meta["means2d"].dim() != 2:  # packed rows only
+    if meta["means2d"].dim() != 2 or ctx["C"] != 1:  # packed rows of one image
         return None
     dev = scene.means.device
     N, nnz = ctx["N"], ctx["nnz"]
@@ -488,7 +490,7 @@ def main():
         _copy_calibration()
         return
     res = _gpu_bench(args)
-    copy_bw = _copy_bandwidth()
+    copy_bw = None if args.no_copy_bandwidth else _copy_bandwidth()
     if args.stages_only:
         print(json.dumps(res["stages"], indent=1))
         return
