@@ -87,6 +87,17 @@ _SIGNATURES = {
     "gsplat_isect_emit_sorted_dev": [
         c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int32, c_int32,
         c_int32, _P, _P, _P, c_int64, _P, c_size_t, _P, _P, _P],
+    "gsplat_isect_prepare_rows_workspace_size": [c_int64],
+    "gsplat_isect_prepare_rows": [
+        c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int32, c_int32, c_int32,
+        _P, c_size_t, _P, _P, _P, _P, _P],
+    "gsplat_isect_emit_tiles_workspace_size": [c_int64],
+    "gsplat_isect_emit_tiles": [
+        c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int32, c_int32,
+        c_int32, _P, _P, c_int64, _P, c_size_t, _P, _P, _P, _P],
+    "gsplat_isect_emit_tiles_dev": [
+        c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int32, c_int32,
+        c_int32, _P, _P, c_int64, _P, c_size_t, _P, _P, _P, _P],
     "gsplat_sort_pairs_workspace_size": [c_int64],
     "gsplat_sort_pairs_u64_u32": [
         c_int64, c_int32, _P, _P, _P, _P, _P, c_size_t, _P],
@@ -124,6 +135,8 @@ _RESTYPES = {
     "gsplat_sort_pairs_workspace_size": c_size_t,
     "gsplat_isect_prepare_workspace_size": c_size_t,
     "gsplat_isect_emit_sorted_workspace_size": c_size_t,
+    "gsplat_isect_prepare_rows_workspace_size": c_size_t,
+    "gsplat_isect_emit_tiles_workspace_size": c_size_t,
     "gsplat_rasterize_to_indices_workspace_size": c_size_t,
 }
 

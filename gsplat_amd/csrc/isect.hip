@@ -16,7 +16,7 @@
 // defined float->int conversion (saturating, NaN -> 0) and a portable log, so
 // the C host oracle reproduces the integer outputs bit for bit.  Count and
 // emit call the same device function, so the two passes agree exactly.
-#include "common.h"
+#include "radix.h"
 
 namespace gs {
 namespace {
@@ -543,10 +543,11 @@ __global__ void __launch_bounds__(kIsectThreads)
     }
 }
 
-// Depth-ordered emission.  The rows in depth order own consecutive slot
-// ranges (the depth-ordered prefix dstart of their counts); the slots are cut
-// into chunks of kEmitSlots and each wave writes one chunk, front to back,
-// with consecutive lanes on consecutive slots:
+// Ordered emission.  The rows in the given order (`order`: the depth order,
+// or NULL: row order) own consecutive slot ranges (the prefix dstart of their
+// counts in that order); the slots are cut into chunks of kEmitSlots and
+// each wave writes one chunk, front to back, with consecutive lanes on
+// consecutive slots:
 //   1. the rows that overlap the chunk (from chunk_first, 64 per batch) set
 //      up their sweeps (kept in LDS);
 //   2. their columns, in (row, column) order, are evaluated one per lane
@@ -559,7 +560,7 @@ __global__ void __launch_bounds__(kIsectThreads)
 // Every wave writes the same number of slots whatever the rows' tile counts
 // (1 to thousands: a large row is shared by the waves of its chunks), and
 // every store is coalesced.  The layout equals that of row_tiles<true>
-// (column by column, rows v ascending) at each row's depth-ordered slots.
+// (column by column, rows v ascending) at each row's slots.
 constexpr int kEmitWaves = kIsectThreads / kWave;
 constexpr int kEmitCols = 4 * kWave;   // segments per batch (4 per lane)
 constexpr int kEmitSlots = 4 * kWave;  // slots per wave
@@ -624,7 +625,7 @@ __global__ void __launch_bounds__(kIsectThreads)
         Sweep sw;
         bool has = false;
         if (p < a.n && dstart[p] < E) {
-            const int64_t row = order[p];
+            const int64_t row = order != nullptr ? (int64_t)order[p] : p;
             const RowRec rec = recs[row];
             has = sweep_setup_rec(a, rec, &sw);
             if (has) {
@@ -776,13 +777,520 @@ __global__ void __launch_bounds__(kIsectThreads)
     }
 }
 
+// ---------------------------------------------------------------------------
+// Sorted intersection, tile first (the form rasterization() uses).
+//
+//   1. isect_count_rows_kernel: every row's tile count and sweep record,
+//      and the row-order exclusive prefix of the counts (prefix inside each
+//      workgroup, one workgroup scanning the workgroup totals, a pass adding
+//      them); starts[n] = n_isects.  A decoupled look-back over the ~2,600
+//      workgroups of this VALU-heavy kernel took 71 us at config 1, against
+//      24 us for the counts alone: every waiting workgroup polls its
+//      predecessors' status words through the device-coherent level.
+//   2. emission in row order (isect_emit_depth_kernel with no order): a
+//      32-bit image|tile key and the row per slot.
+//   3. a stable radix sort on the image|tile bits: the slots grouped by
+//      tile, in row order inside each tile.
+//   4. tile_bounds_kernel: the first slot of every tile from the sorted keys
+//      (the reference's isect_offset_encode).
+//   5. tile_depth_sort_kernel: one workgroup per tile sorts the tile's rows
+//      stably on their 32 depth bits -- in LDS up to 4,096 rows, through
+//      global scratch above -- and writes the 64-bit ids and the rows.
+// The reference sorts stably on image|tile|depth over row-order emission,
+// which orders by (image|tile, depth bits, row); steps 3 and 5 produce that
+// order.  The depth order is taken per tile (~1,000 rows at config 1) in LDS
+// instead of over all rows through device memory.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(kIsectThreads)
+    isect_count_rows_kernel(const IsectArgs a, int32_t *__restrict__ tiles_per_gauss,
+                            RowRec *__restrict__ recs,
+                            int64_t *__restrict__ starts,
+                            uint64_t *__restrict__ block_tot) {
+    __shared__ uint64_t s_wave_tot[kIsectThreads / kWave];
+    const int64_t idx = (int64_t)blockIdx.x * kIsectThreads + threadIdx.x;
+    int32_t cnt = 0;
+    if (idx < a.n) {
+        const RowRec rec = row_record(a, idx);
+        recs[idx] = rec;
+        Sweep sw;
+        cnt = sweep_setup_rec(a, rec, &sw) ? sweep_tiles<false>(a, sw, nullptr) : 0;
+    }
+    const uint64_t incl = wave_inclusive_scan_u64((uint64_t)cnt);
+    const uint32_t wave = threadIdx.x / kWave;
+    if (lane_id() == kWave - 1)
+        s_wave_tot[wave] = incl;
+    __syncthreads();
+    uint64_t wave_off = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < kIsectThreads / kWave; ++w) {
+        const uint64_t v = s_wave_tot[w];
+        wave_off += (w < (int)wave) ? v : 0ull;
+        total += v;
+    }
+    if (idx < a.n) {
+        tiles_per_gauss[idx] = cnt;
+        // the prefix inside the workgroup; isect_starts_finalize_kernel adds
+        // the workgroup's own prefix
+        starts[idx] = (int64_t)(wave_off + incl - (uint64_t)cnt);
+    }
+    if (threadIdx.x == 0)
+        block_tot[blockIdx.x] = total;
+}
+
+// Exclusive prefix of the per-workgroup totals of isect_count_rows_kernel,
+// by one workgroup (4 totals per thread per step, a running carry between
+// steps); writes starts[n] and *n_isects_out.
+constexpr int kBlockScanThreads = 1024;
+constexpr int kBlockScanItems = 4;
+
+__global__ void __launch_bounds__(kBlockScanThreads)
+    isect_block_scan_kernel(int64_t n_blocks, const uint64_t *__restrict__ block_tot,
+                            uint64_t *__restrict__ block_pre, int64_t n,
+                            int64_t *__restrict__ starts,
+                            int64_t *__restrict__ n_isects_out) {
+    __shared__ uint64_t s_wave_tot[kBlockScanThreads / kWave];
+    __shared__ uint64_t s_carry;
+    if (threadIdx.x == 0)
+        s_carry = 0;
+    constexpr int kStep = kBlockScanThreads * kBlockScanItems;
+    const uint32_t wave = threadIdx.x / kWave;
+    for (int64_t b0 = 0; b0 < n_blocks; b0 += kStep) {
+        const int64_t i0 = b0 + (int64_t)threadIdx.x * kBlockScanItems;
+        uint64_t v[kBlockScanItems], sum = 0;
+#pragma unroll
+        for (int k = 0; k < kBlockScanItems; ++k) {
+            v[k] = i0 + k < n_blocks ? block_tot[i0 + k] : 0ull;
+            sum += v[k];
+        }
+        const uint64_t incl = wave_inclusive_scan_u64(sum);
+        if (lane_id() == kWave - 1)
+            s_wave_tot[wave] = incl;
+        __syncthreads();
+        uint64_t off = s_carry, step_tot = 0;
+#pragma unroll
+        for (int w = 0; w < kBlockScanThreads / kWave; ++w) {
+            const uint64_t t = s_wave_tot[w];
+            off += (w < (int)wave) ? t : 0ull;
+            step_tot += t;
+        }
+        uint64_t run = off + incl - sum;
+#pragma unroll
+        for (int k = 0; k < kBlockScanItems; ++k) {
+            if (i0 + k < n_blocks)
+                block_pre[i0 + k] = run;
+            run += v[k];
+        }
+        __syncthreads();  // every thread has read s_carry and s_wave_tot
+        if (threadIdx.x == 0)
+            s_carry += step_tot;
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        starts[n] = (int64_t)s_carry;
+        *n_isects_out = (int64_t)s_carry;
+    }
+}
+
+__global__ void isect_starts_finalize_kernel(int64_t n,
+                                             const uint64_t *__restrict__ block_pre,
+                                             int64_t *__restrict__ starts) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n)
+        starts[i] += (int64_t)block_pre[i / kIsectThreads];
+}
+
+// offsets[s] = the first slot whose image|tile key is that of tile slot s
+// (image * n_tiles + tile), or n when none is; one thread per slot boundary
+// i in [0, n], which fills the tile slots between the keys of slots i - 1
+// and i.  With n_dev the slot count is min(n, *n_dev).
+__global__ void tile_bounds_kernel(int64_t n, const int64_t *__restrict__ n_dev,
+                                   const uint32_t *__restrict__ keys,
+                                   int64_t n_slots, int32_t tile_n_bits,
+                                   int32_t n_tiles, int32_t *__restrict__ offsets) {
+    if (n_dev != nullptr)
+        n = min(n, *n_dev);
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i > n)
+        return;
+    const uint32_t mask = (1u << tile_n_bits) - 1u;
+    auto slot = [&](uint32_t k) {
+        return (int64_t)(k >> tile_n_bits) * n_tiles + (int64_t)(k & mask);
+    };
+    const int64_t cur = i < n ? slot(keys[i]) : n_slots;
+    const int64_t prev = i > 0 ? slot(keys[i - 1]) : -1;
+    for (int64_t s = prev + 1; s <= cur && s < n_slots; ++s)
+        offsets[s] = (int32_t)i;
+}
+
+constexpr int kSegThreads = 256;  // a multiple of the 256 digits
+constexpr int kSegWaves = kSegThreads / kWave;
+constexpr int kSegDigitBits = 8;
+constexpr int kSegRadix = 1 << kSegDigitBits;
+constexpr int kSegPasses = 32 / kSegDigitBits;
+// Tiles of up to kSegLarge rows are sorted in LDS, larger ones through
+// global scratch.
+constexpr int kSegLarge = 4096;
+
+template <int MAXK>
+struct SegSmem {
+    uint32_t keys[MAXK];
+    uint32_t vals[MAXK];
+    uint32_t cnt[kSegWaves][kSegRadix];
+    uint32_t off[kSegRadix];
+    uint32_t wave[kSegWaves];
+    uint32_t bits_or[kSegWaves];
+    uint32_t bits_and[kSegWaves];
+};
+
+__device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1)
+        v |= (uint32_t)__shfl_xor((int)v, o);
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_and_u32(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1)
+        v &= (uint32_t)__shfl_xor((int)v, o);
+    return v;
+}
+
+// The key bits that differ between the workgroup's keys (OR ^ AND of the
+// per-thread partials); digits with none of them are constant and their
+// passes leave the order unchanged.
+template <class SM>
+__device__ __forceinline__ uint32_t block_varying_bits(uint32_t o, uint32_t an,
+                                                       SM &sm) {
+    o = wave_or_u32(o);
+    an = wave_and_u32(an);
+    const int w = threadIdx.x / kWave;
+    if (lane_id() == 0) {
+        sm.bits_or[w] = o;
+        sm.bits_and[w] = an;
+    }
+    __syncthreads();
+    uint32_t bo = 0u, ba = ~0u;
+#pragma unroll
+    for (int ww = 0; ww < kSegWaves; ++ww) {
+        bo |= sm.bits_or[ww];
+        ba &= sm.bits_and[ww];
+    }
+    return bo ^ ba;
+}
+
+// Stable rank of a span of at most ITEMS * 64 keys per wave (k[j] of a lane
+// at base + 64 j + lane, valid below S, the end of the wave's span) on the
+// digit at `shift`: rank[j] is the number of earlier keys of the wave's
+// span with the same digit, and sm.cnt[w][d] the span's count of digit d.
+// Items past S are skipped as a whole.  (Comparing only the digit bits that
+// vary over the tile takes fewer ballots, but its branches cost registers
+// and occupancy: slower at config 1.)
+template <int ITEMS, class SM>
+__device__ __forceinline__ void seg_rank(const uint32_t (&k)[ITEMS], int base,
+                                         int S, int shift, SM &sm,
+                                         uint32_t (&rank)[ITEMS]) {
+    const int w = threadIdx.x / kWave;
+    const int lane = (int)lane_id();
+    for (int i = threadIdx.x; i < kSegWaves * kSegRadix; i += kSegThreads)
+        (&sm.cnt[0][0])[i] = 0u;
+    __syncthreads();
+    // items of this wave with at least one key below S (wave-uniform)
+    const int live = S > base ? min(ITEMS, (S - base + kWave - 1) / kWave) : 0;
+    uint32_t *cnt = sm.cnt[w];
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+        if (j < live) {
+            const bool valid = base + j * kWave + lane < S;
+            const uint32_t d = (k[j] >> shift) & (kSegRadix - 1);
+            const uint64_t peers = match_digit(d, kSegDigitBits, wave_ballot(valid));
+            const uint64_t before = peers & lanemask_lt();
+            uint32_t r = 0;
+            if (valid)
+                r = cnt[d] + (uint32_t)__popcll(before);
+            rank[j] = r;
+            __builtin_amdgcn_wave_barrier();
+            if (valid && before == 0)
+                cnt[d] += (uint32_t)__popcll(peers);
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+    __syncthreads();
+}
+
+// Keys per wave when S keys are split evenly over the workgroup's waves in
+// whole 64-key items (the input order is wave, item, lane).
+__device__ __forceinline__ int seg_span(int S) {
+    return (S + kSegWaves * kWave - 1) / (kSegWaves * kWave) * kWave;
+}
+
+// Tile of S <= 64 * ITEMS * kSegWaves rows, sorted in LDS.
+template <int ITEMS, int MAXK>
+__device__ void seg_sort_lds(int S, const uint32_t *__restrict__ rows_in,
+                             const uint32_t *__restrict__ depth_bits,
+                             uint64_t key_hi, int64_t *__restrict__ out_ids,
+                             int32_t *__restrict__ out_rows, SegSmem<MAXK> &sm) {
+    static_assert(ITEMS * kWave * kSegWaves <= MAXK, "tile exceeds LDS");
+    const int tid = threadIdx.x;
+    const int w = tid / kWave;
+    const int lane = (int)lane_id();
+    // the tile split evenly over the waves, in whole items: wave w holds
+    // [base, lim) = [w * span, (w + 1) * span) cut at S
+    const int span = seg_span(S);
+    const int base = w * span;
+    const int lim = min(S, base + span);
+    uint32_t k[ITEMS], v[ITEMS], rank[ITEMS];
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+        const int i = base + j * kWave + lane;
+        v[j] = i < lim ? rows_in[i] : 0u;
+    }
+    uint32_t o = 0u, an = ~0u;
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+        const int i = base + j * kWave + lane;
+        k[j] = i < lim ? depth_bits[v[j]] : 0u;
+        if (i < lim) {
+            o |= k[j];
+            an &= k[j];
+        }
+    }
+    const uint32_t varying = block_varying_bits(o, an, sm);
+    for (int p = 0; p < kSegPasses; ++p) {
+        const int shift = p * kSegDigitBits;
+        if (((varying >> shift) & (kSegRadix - 1)) == 0u)
+            continue;  // one digit value over the tile
+        seg_rank<ITEMS>(k, base, lim, shift, sm, rank);
+        {
+            // digit starts, and each wave's start inside its digit (thread d
+            // for digit d)
+            const int d = tid;
+            uint32_t c[kSegWaves], tot = 0u;
+#pragma unroll
+            for (int ww = 0; ww < kSegWaves; ++ww) {
+                c[ww] = d < kSegRadix ? sm.cnt[ww][d] : 0u;
+                tot += c[ww];
+            }
+            uint32_t total;
+            uint32_t run = block_exclusive_u32<kSegThreads>(tot, sm.wave, &total);
+            if (d < kSegRadix) {
+#pragma unroll
+                for (int ww = 0; ww < kSegWaves; ++ww) {
+                    sm.cnt[ww][d] = run;
+                    run += c[ww];
+                }
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < ITEMS; ++j) {
+            const int i = base + j * kWave + lane;
+            if (i < lim) {
+                const uint32_t d = (k[j] >> shift) & (kSegRadix - 1);
+                const uint32_t pos = sm.cnt[w][d] + rank[j];
+                sm.keys[pos] = k[j];
+                sm.vals[pos] = v[j];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < ITEMS; ++j) {
+            const int i = base + j * kWave + lane;
+            if (i < lim) {
+                k[j] = sm.keys[i];
+                v[j] = sm.vals[i];
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+        const int i = base + j * kWave + lane;
+        if (i < lim) {
+            out_ids[i] = (int64_t)(key_hi | k[j]);
+            out_rows[i] = (int32_t)v[j];
+        }
+    }
+}
+
+// Tile of more than kSegLarge rows: LSD passes through global scratch, one
+// chunk of kSegLarge keys after another, each chunk ranked in LDS and
+// written at the running digit offsets (stable: chunks in order, ranks
+// stable inside each).  Scratch pairs: p1 (own keys and values) and p2
+// (keys then values in the tile's 8-byte id range, free until the final
+// write); the prologue writes the pair that leaves the result in p1 after
+// the passes.
+__device__ void seg_sort_global(int64_t S, const uint32_t *__restrict__ rows_in,
+                                const uint32_t *__restrict__ depth_bits,
+                                uint64_t key_hi, uint32_t *__restrict__ p1k,
+                                uint32_t *__restrict__ p1v,
+                                int64_t *__restrict__ out_ids,
+                                int32_t *__restrict__ out_rows,
+                                SegSmem<kSegLarge> &sm) {
+    constexpr int ITEMS = kSegLarge / kSegThreads;
+    const int tid = threadIdx.x;
+    const int w = tid / kWave;
+    const int lane = (int)lane_id();
+    uint32_t *p2k = reinterpret_cast<uint32_t *>(out_ids);
+    uint32_t *p2v = p2k + S;
+    uint32_t o = 0u, an = ~0u;
+    for (int64_t i = tid; i < S; i += kSegThreads) {
+        const uint32_t key = depth_bits[rows_in[i]];
+        o |= key;
+        an &= key;
+    }
+    const uint32_t varying = block_varying_bits(o, an, sm);
+    int npass = 0;
+    for (int p = 0; p < kSegPasses; ++p)
+        npass += ((varying >> (p * kSegDigitBits)) & (kSegRadix - 1)) != 0u;
+    uint32_t *sk = (npass & 1) ? p2k : p1k;
+    uint32_t *sv = (npass & 1) ? p2v : p1v;
+    uint32_t *dk = (npass & 1) ? p1k : p2k;
+    uint32_t *dv = (npass & 1) ? p1v : p2v;
+    for (int64_t i = tid; i < S; i += kSegThreads) {
+        const uint32_t r = rows_in[i];
+        sk[i] = depth_bits[r];
+        sv[i] = r;
+    }
+    __threadfence_block();
+    __syncthreads();
+    for (int p = 0; p < kSegPasses; ++p) {
+        const int shift = p * kSegDigitBits;
+        if (((varying >> shift) & (kSegRadix - 1)) == 0u)
+            continue;
+        // digit totals over the tile -> running start of every digit
+        for (int i = tid; i < kSegRadix; i += kSegThreads)
+            sm.cnt[0][i] = 0u;
+        __syncthreads();
+        for (int64_t i = tid; i < S; i += kSegThreads)
+            atomicAdd(&sm.cnt[0][(sk[i] >> shift) & (kSegRadix - 1)], 1u);
+        __syncthreads();
+        {
+            uint32_t total;
+            const uint32_t o = block_exclusive_u32<kSegThreads>(
+                tid < kSegRadix ? sm.cnt[0][tid] : 0u, sm.wave, &total);
+            if (tid < kSegRadix)
+                sm.off[tid] = o;
+        }
+        __syncthreads();
+        for (int64_t c0 = 0; c0 < S; c0 += kSegLarge) {
+            const int cs = (int)(S - c0 < kSegLarge ? S - c0 : kSegLarge);
+            const int span = seg_span(cs);
+            const int base = w * span;
+            const int lim = min(cs, base + span);
+            uint32_t k[ITEMS], v[ITEMS], rank[ITEMS];
+#pragma unroll
+            for (int j = 0; j < ITEMS; ++j) {
+                const int i = base + j * kWave + lane;
+                k[j] = i < lim ? sk[c0 + i] : 0u;
+                v[j] = i < lim ? sv[c0 + i] : 0u;
+            }
+            seg_rank<ITEMS>(k, base, lim, shift, sm, rank);
+            if (tid < kSegRadix) {
+                const int d = tid;
+                uint32_t run = sm.off[d];
+#pragma unroll
+                for (int ww = 0; ww < kSegWaves; ++ww) {
+                    const uint32_t c = sm.cnt[ww][d];
+                    sm.cnt[ww][d] = run;
+                    run += c;
+                }
+                sm.off[d] = run;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < ITEMS; ++j) {
+                const int i = base + j * kWave + lane;
+                if (i < lim) {
+                    const uint32_t d = (k[j] >> shift) & (kSegRadix - 1);
+                    const uint32_t pos = sm.cnt[w][d] + rank[j];
+                    dk[pos] = k[j];
+                    dv[pos] = v[j];
+                }
+            }
+            __syncthreads();
+        }
+        __threadfence_block();
+        __syncthreads();
+        uint32_t *t = sk; sk = dk; dk = t;
+        t = sv; sv = dv; dv = t;
+    }
+    // the result is in p1 (sk == p1k), apart from the ids it is written over
+    for (int64_t i = tid; i < S; i += kSegThreads) {
+        const uint32_t key = sk[i];
+        const uint32_t r = sv[i];
+        out_ids[i] = (int64_t)(key_hi | key);
+        out_rows[i] = (int32_t)r;
+    }
+}
+
+// The tile slot's range [start, start + S) and its 64-bit key prefix.
+struct SegTile {
+    int64_t start, S;
+    uint64_t key_hi;
+};
+
+__device__ __forceinline__ SegTile seg_tile(int64_t s, int64_t n,
+                                            const int32_t *__restrict__ offsets,
+                                            int64_t n_slots, int32_t tile_n_bits,
+                                            int32_t n_tiles) {
+    SegTile t;
+    t.start = offsets[s];
+    const int64_t end = s + 1 < n_slots ? (int64_t)offsets[s + 1] : n;
+    t.S = end - t.start;
+    const uint32_t key = (uint32_t)((s / n_tiles) << tile_n_bits) |
+                         (uint32_t)(s % n_tiles);
+    t.key_hi = (uint64_t)key << 32;
+    return t;
+}
+
+// One workgroup per tile slot (image * n_tiles + tile): the tile's rows,
+// grouped by the tile sort in row order, sorted stably on their depth bits.
+// rows_in may be out_rows itself (each workgroup reads its range before it
+// writes it); p1k/p1v is scratch of at least n entries each.  Tiles of all
+// sizes share one launch: a separate launch for the few large tiles (after
+// the small ones) put their whole sort on the critical path (25 us at
+// config 1 for ~50 tiles of 2,049-2,406 rows).
+__global__ void __launch_bounds__(kSegThreads)
+    tile_depth_sort_kernel(int64_t n, const int64_t *__restrict__ n_dev,
+                           const int32_t *__restrict__ offsets, int64_t n_slots,
+                           int32_t tile_n_bits, int32_t n_tiles,
+                           const uint32_t *__restrict__ depth_bits,
+                           const uint32_t *rows_in, uint32_t *__restrict__ p1k,
+                           uint32_t *__restrict__ p1v,
+                           int64_t *__restrict__ isect_ids, int32_t *out_rows) {
+    __shared__ SegSmem<kSegLarge> sm;
+    if (n_dev != nullptr)
+        n = min(n, *n_dev);
+    const int64_t s = blockIdx.x;
+    const SegTile t = seg_tile(s, n, offsets, n_slots, tile_n_bits, n_tiles);
+    if (t.S <= 0)
+        return;
+    const uint32_t *rin = rows_in + t.start;
+    int64_t *oid = isect_ids + t.start;
+    int32_t *orow = out_rows + t.start;
+    constexpr int I = kSegLarge / kSegThreads;  // items per thread at kSegLarge
+    if (t.S <= kSegLarge / 8)
+        seg_sort_lds<I / 8>((int)t.S, rin, depth_bits, t.key_hi, oid, orow, sm);
+    else if (t.S <= kSegLarge / 4)
+        seg_sort_lds<I / 4>((int)t.S, rin, depth_bits, t.key_hi, oid, orow, sm);
+    else if (t.S <= kSegLarge / 2)
+        seg_sort_lds<I / 2>((int)t.S, rin, depth_bits, t.key_hi, oid, orow, sm);
+    else if (t.S <= kSegLarge)
+        seg_sort_lds<I>((int)t.S, rin, depth_bits, t.key_hi, oid, orow, sm);
+    else
+        seg_sort_global(t.S, rin, depth_bits, t.key_hi, p1k + t.start, p1v + t.start,
+                        oid, orow, sm);
+}
+
 struct PrepLayout {
     size_t keys_a, keys_b, vals_b, lookback, sort_ws, total;
 };
 
-// Depth keys are the float bits of positive depths (every row with tiles
-// has depth > near_plane > 0), so bit 31 never orders two such rows.
-constexpr int kDepthKeyBits = 31;
+// Depth keys are all 32 float bits of the depth, as unsigned integers: the
+// reference zero-extends them into the low word of the 64-bit id
+// (IntersectTile.cu:190-192), so a negative depth orders after every
+// positive one.
+constexpr int kDepthKeyBits = 32;
 
 inline size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
@@ -1127,4 +1635,161 @@ extern "C" int gsplat_isect_emit_sorted_dev(
                             depth_order, depth_starts, row_records, capacity,
                             depth_starts + n, workspace, workspace_bytes,
                             isect_ids, flatten_ids, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Tile-first sorted intersection (the kernels above, from
+// isect_count_rows_kernel to tile_depth_sort_kernel).
+// ---------------------------------------------------------------------------
+extern "C" size_t gsplat_isect_prepare_rows_workspace_size(int64_t n) {
+    // per-workgroup totals and prefixes
+    return 2 * align256((size_t)ceil_div(n > 0 ? n : 0, kIsectThreads) * 8);
+}
+
+extern "C" int gsplat_isect_prepare_rows(int64_t n, int64_t N, const int64_t *image_ids,
+                                         const float *means2d, const int32_t *radii,
+                                         const float *depths, const float *conics,
+                                         const float *opacities, int32_t tile_size,
+                                         int32_t tile_width, int32_t tile_height,
+                                         void *workspace, size_t workspace_bytes,
+                                         int32_t *tiles_per_gauss, int64_t *row_starts,
+                                         float *row_records, int64_t *n_isects_out,
+                                         gsplat_stream_t stream) {
+    clear_error();
+    IsectArgs a;
+    GS_TRY(make_args(n, N, 0, image_ids, means2d, radii, depths, conics,
+                     opacities, tile_size, tile_width, tile_height, a));
+    if (n == 0)
+        return GSPLAT_OK;
+    GS_REQUIRE(depths && tiles_per_gauss && row_starts && row_records && n_isects_out,
+               "isect_prepare_rows: NULL buffer");
+    GS_REQUIRE(reinterpret_cast<uintptr_t>(row_records) % 16 == 0,
+               "isect_prepare_rows: row_records must be 16-byte aligned");
+    GS_REQUIRE(n < (1ll << 31), "isect_prepare_rows: more than 2^31 rows");
+    const int64_t blocks = ceil_div(n, kIsectThreads);
+    GS_REQUIRE(workspace && workspace_bytes >= gsplat_isect_prepare_rows_workspace_size(n),
+               "isect_prepare_rows: workspace too small");
+    uint64_t *block_tot = reinterpret_cast<uint64_t *>(workspace);
+    uint64_t *block_pre = reinterpret_cast<uint64_t *>(
+        reinterpret_cast<char *>(workspace) + align256((size_t)blocks * 8));
+    hipStream_t st = as_stream(stream);
+    isect_count_rows_kernel<<<(unsigned)blocks, kIsectThreads, 0, st>>>(
+        a, tiles_per_gauss, reinterpret_cast<RowRec *>(row_records), row_starts,
+        block_tot);
+    GS_TRY(check_launch("isect_count_rows_kernel"));
+    isect_block_scan_kernel<<<1, kBlockScanThreads, 0, st>>>(
+        blocks, block_tot, block_pre, n, row_starts, n_isects_out);
+    GS_TRY(check_launch("isect_block_scan_kernel"));
+    isect_starts_finalize_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(
+        n, block_pre, row_starts);
+    return check_launch("isect_starts_finalize_kernel");
+}
+
+extern "C" size_t gsplat_isect_emit_tiles_workspace_size(int64_t n_isects) {
+    return emit_layout(n_isects > 0 ? n_isects : 0).total;
+}
+
+static int emit_tiles_impl(
+    int64_t n, int64_t N, int64_t I, const int64_t *image_ids,
+    const float *means2d, const int32_t *radii, const float *depths,
+    const float *conics, const float *opacities, int32_t tile_size,
+    int32_t tile_width, int32_t tile_height, const int64_t *row_starts,
+    const float *row_records, int64_t n_isects, const int64_t *n_dev,
+    void *workspace, size_t workspace_bytes, int64_t *isect_ids,
+    int32_t *flatten_ids, int32_t *offsets, gsplat_stream_t stream) {
+    IsectArgs a;
+    GS_TRY(make_args(n, N, I, image_ids, means2d, radii, depths, conics,
+                     opacities, tile_size, tile_width, tile_height, a));
+    GS_REQUIRE(n_isects >= 0, "isect_emit_tiles: negative n_isects");
+    GS_REQUIRE(I > 0, "isect_emit_tiles: I must be positive");
+    GS_REQUIRE(offsets != nullptr, "isect_emit_tiles: NULL offsets");
+    const int64_t n_tiles = (int64_t)tile_width * tile_height;
+    const int64_t n_slots = I * n_tiles;
+    GS_REQUIRE(n_slots < (1ll << 31), "isect_emit_tiles: more than 2^31 tiles");
+    const int ib = bit_length(I);
+    GS_REQUIRE(ib + a.tile_n_bits <= 32,
+               "isect_emit_tiles: image and tile ids need more than 32 bits");
+    hipStream_t st = as_stream(stream);
+    if (n == 0 || n_isects == 0) {
+        fill_i32_kernel<<<(unsigned)ceil_div(n_slots, 256), 256, 0, st>>>(
+            offsets, n_slots, 0);
+        return check_launch("fill_i32_kernel");
+    }
+    GS_REQUIRE(depths && row_starts && row_records && isect_ids && flatten_ids,
+               "isect_emit_tiles: NULL buffer");
+    GS_REQUIRE(reinterpret_cast<uintptr_t>(row_records) % 16 == 0,
+               "isect_emit_tiles: row_records must be 16-byte aligned");
+    GS_REQUIRE(n_isects < (1ll << 31), "isect_emit_tiles: more than 2^31 isects");
+    const EmitLayout L = emit_layout(n_isects);
+    GS_REQUIRE(workspace && workspace_bytes >= L.total,
+               "isect_emit_tiles: workspace too small");
+    char *ws = reinterpret_cast<char *>(workspace);
+    const int key_bits = a.tile_n_bits + ib;
+    const int passes = radix_sort_passes(key_bits);
+    uint32_t *ka = reinterpret_cast<uint32_t *>(ws + L.keys_a);
+    uint32_t *kb = reinterpret_cast<uint32_t *>(ws + L.keys_b);
+    uint32_t *tmp_vals = reinterpret_cast<uint32_t *>(ws + L.vals);
+    uint32_t *out_vals = reinterpret_cast<uint32_t *>(flatten_ids);
+    // the tile sort leaves the rows in flatten_ids (emit into the pair that
+    // the last pass writes out of), where the depth sort reorders them
+    uint32_t *va = passes % 2 == 1 ? tmp_vals : out_vals;
+    uint32_t *vb = passes % 2 == 1 ? out_vals : tmp_vals;
+    int32_t *chunk_first = reinterpret_cast<int32_t *>(ws + L.chunks);
+    emit_chunk_first_kernel<<<(unsigned)ceil_div(n, kIsectThreads), kIsectThreads,
+                              0, st>>>(n, row_starts, n_isects, chunk_first);
+    GS_TRY(check_launch("emit_chunk_first_kernel"));
+    const int64_t chunks = ceil_div(n_isects, kEmitSlots);
+    isect_emit_depth_kernel<<<(unsigned)ceil_div(chunks, kEmitWaves),
+                              kIsectThreads, 0, st>>>(
+        a, nullptr, row_starts, reinterpret_cast<const RowRec *>(row_records),
+        chunk_first, n_isects, n_dev, ka, va);
+    GS_TRY(check_launch("isect_emit_depth_kernel"));
+    bool in_b = false;
+    GS_TRY(radix_sort_u32(n_isects, key_bits, ka, va, kb, vb, ws + L.sort_ws,
+                          workspace_bytes - L.sort_ws, st, &in_b, nullptr, nullptr,
+                          n_dev));
+    GS_REQUIRE((in_b ? vb : va) == out_vals, "isect_emit_tiles: pass parity");
+    const uint32_t *sorted_keys = in_b ? kb : ka;
+    uint32_t *free_keys = in_b ? ka : kb;
+    tile_bounds_kernel<<<(unsigned)ceil_div(n_isects + 1, 256), 256, 0, st>>>(
+        n_isects, n_dev, sorted_keys, n_slots, a.tile_n_bits, (int32_t)n_tiles,
+        offsets);
+    GS_TRY(check_launch("tile_bounds_kernel"));
+    tile_depth_sort_kernel<<<(unsigned)n_slots, kSegThreads, 0, st>>>(
+        n_isects, n_dev, offsets, n_slots, a.tile_n_bits, (int32_t)n_tiles,
+        reinterpret_cast<const uint32_t *>(depths), out_vals, free_keys, tmp_vals,
+        isect_ids, flatten_ids);
+    return check_launch("tile_depth_sort_kernel");
+}
+
+extern "C" int gsplat_isect_emit_tiles(
+    int64_t n, int64_t N, int64_t I, const int64_t *image_ids,
+    const float *means2d, const int32_t *radii, const float *depths,
+    const float *conics, const float *opacities, int32_t tile_size,
+    int32_t tile_width, int32_t tile_height, const int64_t *row_starts,
+    const float *row_records, int64_t n_isects, void *workspace,
+    size_t workspace_bytes, int64_t *isect_ids, int32_t *flatten_ids,
+    int32_t *offsets, gsplat_stream_t stream) {
+    clear_error();
+    return emit_tiles_impl(n, N, I, image_ids, means2d, radii, depths, conics,
+                           opacities, tile_size, tile_width, tile_height, row_starts,
+                           row_records, n_isects, nullptr, workspace, workspace_bytes,
+                           isect_ids, flatten_ids, offsets, stream);
+}
+
+extern "C" int gsplat_isect_emit_tiles_dev(
+    int64_t n, int64_t N, int64_t I, const int64_t *image_ids,
+    const float *means2d, const int32_t *radii, const float *depths,
+    const float *conics, const float *opacities, int32_t tile_size,
+    int32_t tile_width, int32_t tile_height, const int64_t *row_starts,
+    const float *row_records, int64_t capacity, void *workspace,
+    size_t workspace_bytes, int64_t *isect_ids, int32_t *flatten_ids,
+    int32_t *offsets, gsplat_stream_t stream) {
+    clear_error();
+    GS_REQUIRE(row_starts != nullptr, "isect_emit_tiles_dev: NULL row_starts");
+    // the intersection count is row_starts[n], read by the kernels
+    return emit_tiles_impl(n, N, I, image_ids, means2d, radii, depths, conics,
+                           opacities, tile_size, tile_width, tile_height, row_starts,
+                           row_records, capacity, row_starts + n, workspace,
+                           workspace_bytes, isect_ids, flatten_ids, offsets, stream);
 }

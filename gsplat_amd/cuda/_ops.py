@@ -687,14 +687,15 @@ def intersect_tile(
         # N = n gives (row // n) without reading the ids
         img, N = None, n
     if sort:
-        # Rows sorted by depth, intersections emitted in that order, then a
-        # stable sort on the image|tile bits only: the reference's full-key
-        # order (a per-image segmented sort, segmented=True, is the same order
-        # because the image id occupies the top key bits).
+        # Intersections emitted in row order, stably sorted on the image|tile
+        # bits, then every tile's rows stably sorted on their depth bits: the
+        # reference's full-key order (a per-image segmented sort,
+        # segmented=True, is the same order because the image id occupies
+        # the top key bits).
         state = isect_prepare_sorted(means2d, radii, depths, conics, opacities, img,
                                      N, I, tile_size, tile_width, tile_height,
                                      tiles_per_gauss)
-        return isect_emit_sorted(state)
+        return isect_emit_sorted(state)[:3]
     cum = torch.empty(n, dtype=_I64, device=dev)
     ws = torch.empty(query("gsplat_isect_count_workspace_size", n),
                      dtype=torch.uint8, device=dev)
@@ -727,31 +728,32 @@ def isect_capacity(device: torch.device) -> Optional[int]:
 
 def isect_emit_sorted_queue(state, capacity: int) -> None:
     """Queues the second half of the sorted intersection behind the first
-    with the count read on the device (gsplat_isect_emit_sorted_dev), into
+    with the count read on the device (gsplat_isect_emit_tiles_dev), into
     buffers of ``capacity`` entries; ``isect_emit_sorted`` then only checks
     the count against the capacity."""
     dev = state["means2d"].device
     isect_ids = torch.empty(capacity, dtype=_I64, device=dev)
     flatten_ids = torch.empty(capacity, dtype=_I32, device=dev)
     ts, tw, th = state["tile"]
-    ews = torch.empty(query("gsplat_isect_emit_sorted_workspace_size", capacity),
+    offsets = torch.empty((state["I"], th, tw), dtype=_I32, device=dev)
+    ews = torch.empty(query("gsplat_isect_emit_tiles_workspace_size", capacity),
                       dtype=torch.uint8, device=dev)
-    call("gsplat_isect_emit_sorted_dev", state["n"], state["N"], state["I"],
+    call("gsplat_isect_emit_tiles_dev", state["n"], state["N"], state["I"],
          ptr(state["img"]), ptr(state["means2d"]), ptr(state["radii"]),
          ptr(state["depths"]), ptr(state["conics"]), ptr(state["opacities"]), ts, tw,
-         th, ptr(state["depth_order"]), ptr(state["depth_starts"]),
-         ptr(state["records"]), int(capacity), ptr(ews), ews.numel(), ptr(isect_ids),
-         ptr(flatten_ids), _stream(state["means2d"]))
-    state["queued"] = (int(capacity), isect_ids, flatten_ids)
+         th, ptr(state["row_starts"]), ptr(state["records"]), int(capacity), ptr(ews),
+         ews.numel(), ptr(isect_ids), ptr(flatten_ids), ptr(offsets),
+         _stream(state["means2d"]))
+    state["queued"] = (int(capacity), isect_ids, flatten_ids, offsets)
 
 
 def isect_prepare_sorted(means2d, radii, depths, conics, opacities, img, N, I,
                          tile_size, tile_width, tile_height, tiles_per_gauss):
     """First half of the sorted intersection of n > 0 rows (inputs checked by
-    the caller): the tile counts, the depth order of the rows and their first
-    slots (gsplat_isect_prepare).  The intersection count goes to a pinned
-    host word behind an event, so the caller can queue or do other work
-    before ``isect_emit_sorted`` waits for it."""
+    the caller): the tile counts, the rows' first slots in row order and
+    their sweep records (gsplat_isect_prepare_rows).  The intersection count
+    goes to a pinned host word behind an event, so the caller can queue or
+    do other work before ``isect_emit_sorted`` waits for it."""
     n = means2d.numel() // 2
     dev = means2d.device
     st = _stream(means2d)
@@ -760,18 +762,17 @@ def isect_prepare_sorted(means2d, radii, depths, conics, opacities, img, N, I,
         "depths": depths, "conics": conics, "opacities": opacities,
         "tile": (int(tile_size), int(tile_width), int(tile_height)),
         "tiles_per_gauss": tiles_per_gauss,
-        "depth_order": torch.empty(n, dtype=_I32, device=dev),
-        "depth_starts": torch.empty(n + 1, dtype=_I64, device=dev),
+        "row_starts": torch.empty(n + 1, dtype=_I64, device=dev),
         "records": torch.empty(n, 8, dtype=_F32, device=dev),
     }
     total = torch.empty(1, dtype=_I64, device=dev)
-    ws = torch.empty(query("gsplat_isect_prepare_workspace_size", n),
+    ws = torch.empty(query("gsplat_isect_prepare_rows_workspace_size", n),
                      dtype=torch.uint8, device=dev)
-    call("gsplat_isect_prepare", n, N, ptr(img), ptr(means2d), ptr(radii),
+    call("gsplat_isect_prepare_rows", n, N, ptr(img), ptr(means2d), ptr(radii),
          ptr(depths), ptr(conics), ptr(opacities), int(tile_size),
          int(tile_width), int(tile_height), ptr(ws), ws.numel(),
-         ptr(tiles_per_gauss), ptr(state["depth_order"]), ptr(state["depth_starts"]),
-         ptr(state["records"]), ptr(total), st)
+         ptr(tiles_per_gauss), ptr(state["row_starts"]), ptr(state["records"]),
+         ptr(total), st)
     host = torch.empty(1, dtype=_I64, pin_memory=True)
     host.copy_(total, non_blocking=True)
     ev = torch.cuda.Event()
@@ -782,9 +783,9 @@ def isect_prepare_sorted(means2d, radii, depths, conics, opacities, img, N, I,
 
 def isect_emit_sorted(state):
     """Second half: waits for the intersection count, then emits the
-    intersections in depth order and sorts them on the image|tile bits
-    (gsplat_isect_emit_sorted).  Returns (tiles_per_gauss, isect_ids,
-    flatten_ids)."""
+    intersections in row order, sorts them on the image|tile bits and every
+    tile's rows on their depth bits (gsplat_isect_emit_tiles).  Returns
+    (tiles_per_gauss, isect_ids, flatten_ids, isect_offsets [I, th, tw])."""
     host, ev = state["total"]
     ev.synchronize()
     n_isects = int(host[0])
@@ -792,23 +793,23 @@ def isect_emit_sorted(state):
     _ISECT_LAST[dev.index] = n_isects
     queued = state.get("queued")
     if queued is not None and n_isects <= queued[0]:
-        return state["tiles_per_gauss"], queued[1][:n_isects], queued[2][:n_isects]
+        return (state["tiles_per_gauss"], queued[1][:n_isects], queued[2][:n_isects],
+                queued[3])
     # no queued emission, or more intersections than it had room for (its
     # output is dropped): emit with the exact count
+    ts, tw, th = state["tile"]
     isect_ids = torch.empty(n_isects, dtype=_I64, device=dev)
     flatten_ids = torch.empty(n_isects, dtype=_I32, device=dev)
-    if n_isects == 0:
-        return state["tiles_per_gauss"], isect_ids, flatten_ids
-    ts, tw, th = state["tile"]
-    ews = torch.empty(query("gsplat_isect_emit_sorted_workspace_size", n_isects),
+    offsets = torch.empty((state["I"], th, tw), dtype=_I32, device=dev)
+    ews = torch.empty(query("gsplat_isect_emit_tiles_workspace_size", n_isects),
                       dtype=torch.uint8, device=dev)
-    call("gsplat_isect_emit_sorted", state["n"], state["N"], state["I"],
+    call("gsplat_isect_emit_tiles", state["n"], state["N"], state["I"],
          ptr(state["img"]), ptr(state["means2d"]), ptr(state["radii"]),
          ptr(state["depths"]), ptr(state["conics"]), ptr(state["opacities"]), ts, tw,
-         th, ptr(state["depth_order"]), ptr(state["depth_starts"]),
-         ptr(state["records"]), n_isects, ptr(ews), ews.numel(), ptr(isect_ids),
-         ptr(flatten_ids), _stream(state["means2d"]))
-    return state["tiles_per_gauss"], isect_ids, flatten_ids
+         th, ptr(state["row_starts"]), ptr(state["records"]), n_isects, ptr(ews),
+         ews.numel(), ptr(isect_ids), ptr(flatten_ids), ptr(offsets),
+         _stream(state["means2d"]))
+    return state["tiles_per_gauss"], isect_ids, flatten_ids, offsets
 
 
 def intersect_offset(isect_ids: Tensor, I: int, tile_width: int, tile_height: int) -> Tensor:

@@ -359,7 +359,8 @@ def rasterization(
     assert proj_features is not None
 
     if isect_req is not None and "state" in isect_req:
-        tiles_per_gauss, isect_ids, flatten_ids = _ops.isect_emit_sorted(
+        # the tile-first sorted intersection also gives the tile offsets
+        tiles_per_gauss, isect_ids, flatten_ids, isect_offsets = _ops.isect_emit_sorted(
             isect_req.pop("state"))
     else:
         tiles_per_gauss, isect_ids, flatten_ids = isect_tiles(
@@ -367,7 +368,7 @@ def rasterization(
             segmented=segmented, packed=packed, n_images=I, image_ids=image_ids,
             gaussian_ids=gaussian_ids, conics=conics, opacities=opacities,
         )
-    isect_offsets = isect_offset_encode(isect_ids, I, tile_width, tile_height)
+        isect_offsets = isect_offset_encode(isect_ids, I, tile_width, tile_height)
     isect_offsets = isect_offsets.reshape(batch_dims + (C, tile_height, tile_width))
     meta.update({
         "tile_width": tile_width, "tile_height": tile_height,

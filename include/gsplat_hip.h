@@ -451,6 +451,67 @@ int gsplat_isect_emit_sorted_dev(
     void *workspace, size_t workspace_bytes,
     int64_t *isect_ids, int32_t *flatten_ids, gsplat_stream_t stream);
 
+/* Tile-first sorted intersection, stage 1 of 2 (the form rasterization()
+ * uses).  Counts the tiles of every row (tiles_per_gauss [n]), gives every
+ * row its first slot in row order -- row_starts [n + 1] int64, the tile
+ * count of all rows before it (row_starts[n] = n_isects, also written to
+ * n_isects_out, device int64) -- and packs every row's sweep inputs into
+ * row_records [n, 8] float (16-byte aligned) for stage 2.  Same row/camera
+ * arguments as gsplat_isect_count; the workspace is
+ * gsplat_isect_prepare_rows_workspace_size(n) bytes.
+ * Together with stage 2 this replaces intersect_tile with sort=True and
+ * intersect_offset (gsplat/cuda/csrc/Intersect.cpp:33-164: count, cumsum,
+ * emit, the full-key radix sort of IntersectTile.cu:478-520, and the offset
+ * encoding of IntersectTile.cu:391-439). */
+size_t gsplat_isect_prepare_rows_workspace_size(int64_t n);
+int gsplat_isect_prepare_rows(
+    int64_t n, int64_t N, const int64_t *image_ids,
+    const float *means2d, const int32_t *radii, const float *depths,
+    const float *conics, const float *opacities,
+    int32_t tile_size, int32_t tile_width, int32_t tile_height,
+    void *workspace, size_t workspace_bytes, int32_t *tiles_per_gauss,
+    int64_t *row_starts, float *row_records, int64_t *n_isects_out,
+    gsplat_stream_t stream);
+
+/* Tile-first sorted intersection, stage 2 of 2.  Writes every row's tiles at
+ * its row-order slots (row_starts, row_records from stage 1), sorts the
+ * intersections stably on the image|tile bits, then sorts every tile's rows
+ * stably on their depth bits (one workgroup per tile; in LDS up to 4,096
+ * rows, through the output buffers above that).  isect_ids [n_isects] and
+ * flatten_ids [n_isects] equal the reference's full-key stable sort of the
+ * row-order emission bit for bit; offsets [I, tile_height, tile_width] int32
+ * (fully written) is the first intersection of every tile, as
+ * gsplat_isect_offsets would compute it from isect_ids. */
+size_t gsplat_isect_emit_tiles_workspace_size(int64_t n_isects);
+int gsplat_isect_emit_tiles(
+    int64_t n, int64_t N, int64_t I, const int64_t *image_ids,
+    const float *means2d, const int32_t *radii, const float *depths,
+    const float *conics, const float *opacities,
+    int32_t tile_size, int32_t tile_width, int32_t tile_height,
+    const int64_t *row_starts, const float *row_records, int64_t n_isects,
+    void *workspace, size_t workspace_bytes,
+    int64_t *isect_ids, int32_t *flatten_ids, int32_t *offsets,
+    gsplat_stream_t stream);
+
+/* Stage 2 with the intersection count read on the device (row_starts[n]),
+ * so it can be queued behind stage 1 before the host knows the count:
+ * `capacity` in place of n_isects sizes isect_ids, flatten_ids and the
+ * workspace, and the first min(n_isects, capacity) entries are written (with
+ * the offsets of those).  When n_isects <= capacity they equal
+ * gsplat_isect_emit_tiles' output; otherwise the caller must run
+ * gsplat_isect_emit_tiles with room for n_isects.  No reference
+ * counterpart: the reference reads the count on the host between the two
+ * stages (gsplat/cuda/csrc/Intersect.cpp:104-122). */
+int gsplat_isect_emit_tiles_dev(
+    int64_t n, int64_t N, int64_t I, const int64_t *image_ids,
+    const float *means2d, const int32_t *radii, const float *depths,
+    const float *conics, const float *opacities,
+    int32_t tile_size, int32_t tile_width, int32_t tile_height,
+    const int64_t *row_starts, const float *row_records, int64_t capacity,
+    void *workspace, size_t workspace_bytes,
+    int64_t *isect_ids, int32_t *flatten_ids, int32_t *offsets,
+    gsplat_stream_t stream);
+
 /* Bytes of workspace gsplat_sort_pairs_u64_u32 needs for n pairs. */
 size_t gsplat_sort_pairs_workspace_size(int64_t n);
 

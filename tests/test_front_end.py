@@ -170,11 +170,11 @@ def test_queued_emission_matches_exact_and_falls_back():
         out.append(render())
     finally:
         _ops.call = real_call
-    assert "gsplat_isect_emit_sorted_dev" not in out[0][3]
-    assert "gsplat_isect_emit_sorted_dev" in out[1][3]
-    assert "gsplat_isect_emit_sorted" not in out[1][3]
-    assert "gsplat_isect_emit_sorted_dev" in out[2][3]
-    assert "gsplat_isect_emit_sorted" in out[2][3]
+    assert "gsplat_isect_emit_tiles_dev" not in out[0][3]
+    assert "gsplat_isect_emit_tiles_dev" in out[1][3]
+    assert "gsplat_isect_emit_tiles" not in out[1][3]
+    assert "gsplat_isect_emit_tiles_dev" in out[2][3]
+    assert "gsplat_isect_emit_tiles" in out[2][3]
     for rc, ra, meta, _ in out[1:]:
         for k in ("isect_ids", "flatten_ids", "isect_offsets"):
             assert torch.equal(meta[k], out[0][2][k]), k

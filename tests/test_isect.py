@@ -149,3 +149,93 @@ def test_offsets_empty_and_zero_isects():
     from gsplat_amd.cuda._wrapper import isect_offset_encode
     offs = isect_offset_encode(torch.empty(0, dtype=torch.int64, device=DEV), 2, 5, 4)
     assert offs.shape == (2, 4, 5) and int(offs.abs().sum()) == 0
+
+
+@pytest.mark.parametrize("N", [700, 1800, 3500, 11000])
+def test_tile_first_sort_every_segment_size(N):
+    """The tile-first sorted intersection sorts each tile's rows on their
+    depth bits in LDS up to 1,024 / 2,048 / 4,096 rows and through global
+    scratch above that.  Rows with large radii put about N rows into each of
+    the 12 tiles of every image, so each N takes one of the four paths.
+    Depths are quantised (many ties, which must stay in row order) and half
+    of them negative (their zero-extended bits order after every positive
+    depth, IntersectTile.cu:190-192).  The offsets come from the same call
+    and must equal the offset encoding of the oracle's ids."""
+    from gsplat_amd.cuda import _ops
+    rng = np.random.default_rng(N)
+    C, ts, W, H = 2, 16, 64, 48
+    tw, th = math.ceil(W / ts), math.ceil(H / ts)
+    means2d = np.stack([rng.uniform(0, W, (C, N)), rng.uniform(0, H, (C, N))],
+                       -1).astype(np.float32)
+    radii = rng.integers(40, 90, (C, N, 2)).astype(np.int32)
+    radii[:, ::97] = 0  # a few rows with no tile
+    depths = (np.round(rng.uniform(-3, 3, (C, N)) * 8) / 8).astype(np.float32)
+    want = exact.isect_tiles(means2d, radii, depths, ts, tw, th)
+    per_tile = np.bincount(want[1] >> 32, minlength=C * tw * th)
+    lo = {700: 1, 1800: 1025, 3500: 2049, 11000: 4097}[N]
+    assert per_tile.max() >= lo, per_tile.max()
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    tpg = torch.empty((C, N), dtype=torch.int32, device=DEV)
+    state = _ops.isect_prepare_sorted(t(means2d), t(radii), t(depths), None, None,
+                                      None, N, C, ts, tw, th, tpg)
+    got = _ops.isect_emit_sorted(state)
+    _compare(got[:3], want)
+    np.testing.assert_array_equal(got[3].cpu().numpy().reshape(-1),
+                                  exact.isect_offset_encode(want[1], C, tw, th).reshape(-1))
+    # the queued (device-count) form with a capacity above the count
+    state = _ops.isect_prepare_sorted(t(means2d), t(radii), t(depths), None, None,
+                                      None, N, C, ts, tw, th, tpg)
+    _ops.isect_emit_sorted_queue(state, want[1].shape[0] + 1000)
+    got = _ops.isect_emit_sorted(state)
+    _compare(got[:3], want)
+    np.testing.assert_array_equal(got[3].cpu().numpy().reshape(-1),
+                                  exact.isect_offset_encode(want[1], C, tw, th).reshape(-1))
+
+
+def _depth_first(means2d, radii, depths, C, N, ts, tw, th, capacity=None):
+    """The depth-first two-stage form through the C ABI directly
+    (gsplat_isect_prepare, then gsplat_isect_emit_sorted or, with a
+    capacity, gsplat_isect_emit_sorted_dev)."""
+    from gsplat_amd.cuda._ops import _stream, call, ptr, query
+    n = C * N
+    tpg = torch.empty(n, dtype=torch.int32, device=DEV)
+    order = torch.empty(n, dtype=torch.int32, device=DEV)
+    starts = torch.empty(n + 1, dtype=torch.int64, device=DEV)
+    recs = torch.empty(n, 8, dtype=torch.float32, device=DEV)
+    total = torch.empty(1, dtype=torch.int64, device=DEV)
+    ws = torch.empty(query("gsplat_isect_prepare_workspace_size", n), dtype=torch.uint8,
+                     device=DEV)
+    st = _stream(means2d)
+    call("gsplat_isect_prepare", n, N, None, ptr(means2d), ptr(radii), ptr(depths),
+         None, None, ts, tw, th, ptr(ws), ws.numel(), ptr(tpg), ptr(order), ptr(starts),
+         ptr(recs), ptr(total), st)
+    n_isects = int(total.item())
+    size = n_isects if capacity is None else capacity
+    ids = torch.empty(size, dtype=torch.int64, device=DEV)
+    flat = torch.empty(size, dtype=torch.int32, device=DEV)
+    ews = torch.empty(query("gsplat_isect_emit_sorted_workspace_size", size),
+                      dtype=torch.uint8, device=DEV)
+    name = "gsplat_isect_emit_sorted" if capacity is None else "gsplat_isect_emit_sorted_dev"
+    call(name, n, N, C, None, ptr(means2d), ptr(radii), ptr(depths), None, None, ts, tw,
+         th, ptr(order), ptr(starts), ptr(recs), size, ptr(ews), ews.numel(), ptr(ids),
+         ptr(flat), st)
+    return tpg.reshape(C, N), ids[:n_isects], flat[:n_isects]
+
+
+def test_depth_first_form_matches_oracle():
+    """The depth-first form (rows sorted by depth over the whole array, then
+    the tile sort) stays exported: bit-exact against the oracle, with
+    quantised depths (ties) half of them negative, exact and queued."""
+    rng = np.random.default_rng(11)
+    C, N, ts, W, H = 2, 5000, 16, 200, 120
+    tw, th = math.ceil(W / ts), math.ceil(H / ts)
+    means2d = np.stack([rng.uniform(-20, W + 20, (C, N)),
+                        rng.uniform(-20, H + 20, (C, N))], -1).astype(np.float32)
+    radii = rng.integers(0, 30, (C, N, 2)).astype(np.int32)
+    depths = (np.round(rng.uniform(-3, 3, (C, N)) * 8) / 8).astype(np.float32)
+    want = exact.isect_tiles(means2d, radii, depths, ts, tw, th)
+    assert want[1].shape[0] > 20000
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    _compare(_depth_first(t(means2d), t(radii), t(depths), C, N, ts, tw, th), want)
+    _compare(_depth_first(t(means2d), t(radii), t(depths), C, N, ts, tw, th,
+                          capacity=want[1].shape[0] + 777), want)
