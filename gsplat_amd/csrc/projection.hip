@@ -79,13 +79,16 @@ struct ProjOut {
 };
 
 // ---------------------------------------------------------------------------
-// Exact forward (fixed op order, no contraction).  Returns false for culled
-// rows.  The host oracle (oracle/exact_ref.c) restates this sequence.
+// Exact forward: a fixed sequence of IEEE operations in which every a * b + c
+// is one explicit fused multiply-add (fmaf, correctly rounded on the GPU and
+// in the host's C library) and nothing else is contracted.  Returns false
+// for culled rows.  The host oracle (oracle/exact_ref.c) restates this
+// sequence operation for operation.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void quat_to_rot_exact(float w, float x, float y,
                                                   float z, float M[9]) {
 #pragma clang fp contract(off)
-    const float n2 = ((x * x + y * y) + z * z) + w * w;
+    const float n2 = fmaf(w, w, fmaf(z, z, fmaf(y, y, x * x)));
     const float inv = 1.0f / sqrtf(n2);
     x = x * inv;
     y = y * inv;
@@ -94,15 +97,22 @@ __device__ __forceinline__ void quat_to_rot_exact(float w, float x, float y,
     const float x2 = x * x, y2 = y * y, z2 = z * z;
     const float xy = x * y, xz = x * z, yz = y * z;
     const float wx = w * x, wy = w * y, wz = w * z;
-    M[0] = 1.f - 2.f * (y2 + z2);
+    M[0] = fmaf(-2.f, y2 + z2, 1.f);
     M[1] = 2.f * (xy - wz);
     M[2] = 2.f * (xz + wy);
     M[3] = 2.f * (xy + wz);
-    M[4] = 1.f - 2.f * (x2 + z2);
+    M[4] = fmaf(-2.f, x2 + z2, 1.f);
     M[5] = 2.f * (yz - wx);
     M[6] = 2.f * (xz - wy);
     M[7] = 2.f * (yz + wx);
-    M[8] = 1.f - 2.f * (x2 + y2);
+    M[8] = fmaf(-2.f, x2 + y2, 1.f);
+}
+
+// a0 b0 + a1 b1 + a2 b2 as a product and two fused multiply-adds
+__device__ __forceinline__ float dot3_exact(float a0, float b0, float a1, float b1,
+                                            float a2, float b2) {
+#pragma clang fp contract(off)
+    return fmaf(a2, b2, fmaf(a1, b1, a0 * b0));
 }
 
 __device__ __forceinline__ Sym3 covar_from_quat_scale_exact(const float *q,
@@ -118,8 +128,8 @@ __device__ __forceinline__ Sym3 covar_from_quat_scale_exact(const float *q,
         A[i * 3 + 2] = M[i * 3 + 2] * s[2];
     }
 #define GS_DOT_ROWS(i, j)                                                      \
-    ((A[(i) * 3 + 0] * A[(j) * 3 + 0] + A[(i) * 3 + 1] * A[(j) * 3 + 1]) +     \
-     A[(i) * 3 + 2] * A[(j) * 3 + 2])
+    dot3_exact(A[(i) * 3 + 0], A[(j) * 3 + 0], A[(i) * 3 + 1], A[(j) * 3 + 1],   \
+               A[(i) * 3 + 2], A[(j) * 3 + 2])
     Sym3 S;
     S.a00 = GS_DOT_ROWS(0, 0);
     S.a01 = GS_DOT_ROWS(0, 1);
@@ -139,9 +149,9 @@ __device__ __forceinline__ bool project_exact(
 #pragma clang fp contract(off)
     const float *R = cam.R;
     const float p0 = mean[0], p1 = mean[1], p2 = mean[2];
-    const float mcx = ((R[0] * p0 + R[1] * p1) + R[2] * p2) + cam.t[0];
-    const float mcy = ((R[3] * p0 + R[4] * p1) + R[5] * p2) + cam.t[1];
-    const float mcz = ((R[6] * p0 + R[7] * p1) + R[8] * p2) + cam.t[2];
+    const float mcx = fmaf(R[2], p2, fmaf(R[1], p1, fmaf(R[0], p0, cam.t[0])));
+    const float mcy = fmaf(R[5], p2, fmaf(R[4], p1, fmaf(R[3], p0, cam.t[1])));
+    const float mcz = fmaf(R[8], p2, fmaf(R[7], p1, fmaf(R[6], p0, cam.t[2])));
     if (mcz < near_plane || mcz > far_plane)
         return false;
 
@@ -164,13 +174,12 @@ __device__ __forceinline__ bool project_exact(
     for (int i = 0; i < 3; ++i)
 #pragma unroll
         for (int j = 0; j < 3; ++j)
-            Bm[i * 3 + j] = (R[i * 3 + 0] * Sf[0 * 3 + j] +
-                             R[i * 3 + 1] * Sf[1 * 3 + j]) +
-                            R[i * 3 + 2] * Sf[2 * 3 + j];
+            Bm[i * 3 + j] = dot3_exact(R[i * 3 + 0], Sf[0 * 3 + j], R[i * 3 + 1],
+                                       Sf[1 * 3 + j], R[i * 3 + 2], Sf[2 * 3 + j]);
     // Sc = B * R^T (upper triangle)
 #define GS_SC(i, j)                                                            \
-    ((Bm[(i) * 3 + 0] * R[(j) * 3 + 0] + Bm[(i) * 3 + 1] * R[(j) * 3 + 1]) +   \
-     Bm[(i) * 3 + 2] * R[(j) * 3 + 2])
+    dot3_exact(Bm[(i) * 3 + 0], R[(j) * 3 + 0], Bm[(i) * 3 + 1], R[(j) * 3 + 1], \
+               Bm[(i) * 3 + 2], R[(j) * 3 + 2])
     const float s00 = GS_SC(0, 0), s01 = GS_SC(0, 1), s02 = GS_SC(0, 2);
     const float s11 = GS_SC(1, 1), s12 = GS_SC(1, 2), s22 = GS_SC(2, 2);
 #undef GS_SC
@@ -181,8 +190,8 @@ __device__ __forceinline__ bool project_exact(
         J11 = cam.fy;
         J02 = 0.f;
         J12 = 0.f;
-        mx = cam.fx * mcx + cam.cx;
-        my = cam.fy * mcy + cam.cy;
+        mx = fmaf(cam.fx, mcx, cam.cx);
+        my = fmaf(cam.fy, mcy, cam.cy);
     } else {
         const float rz = 1.f / mcz;
         const float rz2 = rz * rz;
@@ -194,24 +203,25 @@ __device__ __forceinline__ bool project_exact(
         J11 = cam.fy * rz;
         J02 = ((-cam.fx) * tx) * rz2;
         J12 = ((-cam.fy) * ty) * rz2;
-        mx = ((cam.fx * mcx) * rz) + cam.cx;
-        my = ((cam.fy * mcy) * rz) + cam.cy;
+        mx = fmaf(cam.fx * mcx, rz, cam.cx);
+        my = fmaf(cam.fy * mcy, rz, cam.cy);
     }
     // cov2d = J Sc J^T with J = [[J00, 0, J02], [0, J11, J12]]
-    const float u0 = s00 * J00 + s02 * J02;
-    const float u1 = s01 * J00 + s12 * J02;
-    const float u2 = s02 * J00 + s22 * J02;
-    const float w1 = s11 * J11 + s12 * J12;
-    const float w2 = s12 * J11 + s22 * J12;
-    const float c00 = J00 * u0 + J02 * u2;
-    const float c01 = J11 * u1 + J12 * u2;
-    const float c11 = J11 * w1 + J12 * w2;
+    const float u0 = fmaf(s02, J02, s00 * J00);
+    const float u1 = fmaf(s12, J02, s01 * J00);
+    const float u2 = fmaf(s22, J02, s02 * J00);
+    const float w1 = fmaf(s12, J12, s11 * J11);
+    const float w2 = fmaf(s22, J12, s12 * J11);
+    const float c00 = fmaf(J02, u2, J00 * u0);
+    const float c01 = fmaf(J12, u2, J11 * u1);
+    const float c11 = fmaf(J12, w2, J11 * w1);
 
     // low-pass blur + compensation (add_blur)
-    const float det_orig = c00 * c11 - c01 * c01;
+    const float c01sq = c01 * c01;
+    const float det_orig = fmaf(c00, c11, -c01sq);
     const float c00b = c00 + eps2d;
     const float c11b = c11 + eps2d;
-    const float det = c00b * c11b - c01 * c01;
+    const float det = fmaf(c00b, c11b, -c01sq);
     if (!(det > 0.f))
         return false;
     const float comp =

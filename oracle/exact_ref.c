@@ -11,8 +11,10 @@
  *   - the natural log used by the opacity-aware extents and the exponential
  *     that turns a Gaussian's Mahalanobis term into its alpha.
  * Every floating-point operation is written out in the order the product
- * kernels use, and this file is compiled with -ffp-contract=off, so IEEE
- * single precision gives identical bits on the CPU and the GPU.
+ * kernels use -- each a * b + c that the kernels fuse as an explicit fmaf
+ * (correctly rounded in the C library as on the GPU) -- and this file is
+ * compiled with -ffp-contract=off, so IEEE single precision gives identical
+ * bits on the CPU and the GPU.
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline may load
  * this code, and only as a checker.
@@ -100,21 +102,26 @@ void oracle_portable_expf_array(const float *x, float *y, int64_t n) {
 /* Projection forward                                                       */
 /* ----------------------------------------------------------------------- */
 static void quat_to_rot(float w, float x, float y, float z, float M[9]) {
-    const float n2 = ((x * x + y * y) + z * z) + w * w;
+    const float n2 = fmaf(w, w, fmaf(z, z, fmaf(y, y, x * x)));
     const float inv = 1.0f / sqrtf(n2);
     x = x * inv; y = y * inv; z = z * inv; w = w * inv;
     const float x2 = x * x, y2 = y * y, z2 = z * z;
     const float xy = x * y, xz = x * z, yz = y * z;
     const float wx = w * x, wy = w * y, wz = w * z;
-    M[0] = 1.f - 2.f * (y2 + z2);
+    M[0] = fmaf(-2.f, y2 + z2, 1.f);
     M[1] = 2.f * (xy - wz);
     M[2] = 2.f * (xz + wy);
     M[3] = 2.f * (xy + wz);
-    M[4] = 1.f - 2.f * (x2 + z2);
+    M[4] = fmaf(-2.f, x2 + z2, 1.f);
     M[5] = 2.f * (yz - wx);
     M[6] = 2.f * (xz - wy);
     M[7] = 2.f * (yz + wx);
-    M[8] = 1.f - 2.f * (x2 + y2);
+    M[8] = fmaf(-2.f, x2 + y2, 1.f);
+}
+
+/* a0 b0 + a1 b1 + a2 b2 as a product and two fused multiply-adds */
+static float dot3(float a0, float b0, float a1, float b1, float a2, float b2) {
+    return fmaf(a2, b2, fmaf(a1, b1, a0 * b0));
 }
 
 /* returns 1 if the row survives culling */
@@ -131,9 +138,9 @@ static int project_one(const float *vm, const float *K, const float *mean,
     }
     const float fx = K[0], fy = K[4], cx = K[2], cy = K[5];
     const float p0 = mean[0], p1 = mean[1], p2 = mean[2];
-    const float mcx = ((R[0] * p0 + R[1] * p1) + R[2] * p2) + t[0];
-    const float mcy = ((R[3] * p0 + R[4] * p1) + R[5] * p2) + t[1];
-    const float mcz = ((R[6] * p0 + R[7] * p1) + R[8] * p2) + t[2];
+    const float mcx = fmaf(R[2], p2, fmaf(R[1], p1, fmaf(R[0], p0, t[0])));
+    const float mcy = fmaf(R[5], p2, fmaf(R[4], p1, fmaf(R[3], p0, t[1])));
+    const float mcz = fmaf(R[8], p2, fmaf(R[7], p1, fmaf(R[6], p0, t[2])));
     if (mcz < near_plane || mcz > far_plane) return 0;
 
     float S00, S01, S02, S11, S12, S22;
@@ -148,7 +155,7 @@ static int project_one(const float *vm, const float *K, const float *mean,
             A[i * 3 + 1] = M[i * 3 + 1] * scale[1];
             A[i * 3 + 2] = M[i * 3 + 2] * scale[2];
         }
-#define DOTR(i, j) ((A[(i)*3+0]*A[(j)*3+0] + A[(i)*3+1]*A[(j)*3+1]) + A[(i)*3+2]*A[(j)*3+2])
+#define DOTR(i, j) dot3(A[(i)*3+0], A[(j)*3+0], A[(i)*3+1], A[(j)*3+1], A[(i)*3+2], A[(j)*3+2])
         S00 = DOTR(0, 0); S01 = DOTR(0, 1); S02 = DOTR(0, 2);
         S11 = DOTR(1, 1); S12 = DOTR(1, 2); S22 = DOTR(2, 2);
 #undef DOTR
@@ -157,17 +164,17 @@ static int project_one(const float *vm, const float *K, const float *mean,
     float Bm[9];
     for (int i = 0; i < 3; ++i)
         for (int j = 0; j < 3; ++j)
-            Bm[i * 3 + j] = (R[i * 3 + 0] * Sf[0 * 3 + j] + R[i * 3 + 1] * Sf[1 * 3 + j]) +
-                            R[i * 3 + 2] * Sf[2 * 3 + j];
-#define SC(i, j) ((Bm[(i)*3+0]*R[(j)*3+0] + Bm[(i)*3+1]*R[(j)*3+1]) + Bm[(i)*3+2]*R[(j)*3+2])
+            Bm[i * 3 + j] = dot3(R[i * 3 + 0], Sf[0 * 3 + j], R[i * 3 + 1], Sf[1 * 3 + j],
+                                 R[i * 3 + 2], Sf[2 * 3 + j]);
+#define SC(i, j) dot3(Bm[(i)*3+0], R[(j)*3+0], Bm[(i)*3+1], R[(j)*3+1], Bm[(i)*3+2], R[(j)*3+2])
     const float s00 = SC(0, 0), s01 = SC(0, 1), s02 = SC(0, 2);
     const float s11 = SC(1, 1), s12 = SC(1, 2), s22 = SC(2, 2);
 #undef SC
     float J00, J02, J11, J12, mx, my;
     if (camera_model == 1) {
         J00 = fx; J11 = fy; J02 = 0.f; J12 = 0.f;
-        mx = fx * mcx + cx;
-        my = fy * mcy + cy;
+        mx = fmaf(fx, mcx, cx);
+        my = fmaf(fy, mcy, cy);
     } else {
         const float tan_fovx = (0.5f * W) / fx;
         const float tan_fovy = (0.5f * H) / fy;
@@ -183,21 +190,22 @@ static int project_one(const float *vm, const float *K, const float *mean,
         J11 = fy * rz;
         J02 = ((-fx) * tx) * rz2;
         J12 = ((-fy) * ty) * rz2;
-        mx = ((fx * mcx) * rz) + cx;
-        my = ((fy * mcy) * rz) + cy;
+        mx = fmaf(fx * mcx, rz, cx);
+        my = fmaf(fy * mcy, rz, cy);
     }
-    const float u0 = s00 * J00 + s02 * J02;
-    const float u1 = s01 * J00 + s12 * J02;
-    const float u2 = s02 * J00 + s22 * J02;
-    const float w1 = s11 * J11 + s12 * J12;
-    const float w2 = s12 * J11 + s22 * J12;
-    const float c00 = J00 * u0 + J02 * u2;
-    const float c01 = J11 * u1 + J12 * u2;
-    const float c11 = J11 * w1 + J12 * w2;
-    const float det_orig = c00 * c11 - c01 * c01;
+    const float u0 = fmaf(s02, J02, s00 * J00);
+    const float u1 = fmaf(s12, J02, s01 * J00);
+    const float u2 = fmaf(s22, J02, s02 * J00);
+    const float w1 = fmaf(s12, J12, s11 * J11);
+    const float w2 = fmaf(s22, J12, s12 * J11);
+    const float c00 = fmaf(J02, u2, J00 * u0);
+    const float c01 = fmaf(J12, u2, J11 * u1);
+    const float c11 = fmaf(J12, w2, J11 * w1);
+    const float c01sq = c01 * c01;
+    const float det_orig = fmaf(c00, c11, -c01sq);
     const float c00b = c00 + eps2d;
     const float c11b = c11 + eps2d;
-    const float det = c00b * c11b - c01 * c01;
+    const float det = fmaf(c00b, c11b, -c01sq);
     if (!(det > 0.f)) return 0;
     const float comp = sqrtf(fmaxf(MIN_COMPENSATION * MIN_COMPENSATION, det_orig / det));
     const float inv_det = 1.f / det;
