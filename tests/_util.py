@@ -85,7 +85,7 @@ def assert_close(a, b, rtol, atol, name):
                              f"rtol={rtol} atol={atol}")
 
 
-GRAD_STRICT_SLACK = 5e-3  # strict-tolerance pass rate may trail fp32's by this
+GRAD_STRICT_SLACK = 1e-3  # strict-tolerance pass rate may trail fp32's by this
 GRAD_MAX_RATIO = 2.5      # worst element may exceed fp32's worst by this factor
 GRAD_RMS_RATIO = 2.0      # RMS error may exceed fp32's by this factor
 
@@ -103,7 +103,7 @@ def assert_grad_close(got, ref64, ref32, rtol, atol, name):
     the float32 restatement's own error |ref32 - ref64|:
 
       * the fraction of elements within tol = atol + rtol |ref64| may trail
-        the float32 restatement's by at most 0.5 percentage points;
+        the float32 restatement's by at most 0.1 percentage points;
       * measured in units of tol, the RMS deviation from ref64 may be at
         most max(1, 2x) the float32 restatement's and the largest at most
         max(1, 2.5x): the worst elements are sums whose terms cancel by two
@@ -131,6 +131,7 @@ def assert_grad_close(got, ref64, ref32, rtol, atol, name):
            f"{err.max().item():.3e} (fp32 {err32.max().item():.3e}); worst element "
            f"{worst}: got {a.reshape(-1)[worst].item():.9g}, float64 "
            f"{r.reshape(-1)[worst].item():.9g}, float32 {r32.reshape(-1)[worst].item():.9g}")
+    print("[grad gate]", msg)  # shown with pytest -rP
     assert frac >= frac32 - GRAD_STRICT_SLACK, msg
     assert mx <= max(1.0, GRAD_MAX_RATIO * mx32), msg
     assert rms <= max(1.0, GRAD_RMS_RATIO * rms32), msg
