@@ -354,17 +354,18 @@ def packed_front_fwd(
         st = _stream(means)
         ws = torch.empty(query("gsplat_projection_packed_workspace_size", B, C, N),
                          dtype=torch.uint8, device=dev)
-        nnz_dev = torch.empty(1, dtype=_I64, device=dev)
+        # the kernel writes the visible count straight into pinned host
+        # memory (device-accessible at the same address), so no copy kernel
+        # sits on the stream between the projection and the colours
+        nnz_host = torch.empty(1, dtype=_I64, pin_memory=True)
         call("gsplat_projection_packed_fwd", B, C, N, ptr(means), ptr(covars),
              ptr(quats), ptr(scales), ptr(opacities), ptr(viewmats), ptr(Ks),
              int(image_width), int(image_height), float(eps2d),
              float(near_plane), float(far_plane), float(radius_clip),
              int(camera_model), ptr(ws), ws.numel(), ptr(indptr),
              ptr(batch_ids), ptr(camera_ids), ptr(gaussian_ids), ptr(radii),
-             ptr(means2d), ptr(depths), ptr(conics), ptr(comps), ptr(nnz_dev),
+             ptr(means2d), ptr(depths), ptr(conics), ptr(comps), ptr(nnz_host),
              ptr(row_of), ptr(row_opac), st)
-        nnz_host = torch.empty(1, dtype=_I64, pin_memory=True)
-        nnz_host.copy_(nnz_dev, non_blocking=True)
         copied = torch.cuda.Event()
         copied.record()
         if sh_degree is None:
@@ -765,16 +766,15 @@ def isect_prepare_sorted(means2d, radii, depths, conics, opacities, img, N, I,
         "row_starts": torch.empty(n + 1, dtype=_I64, device=dev),
         "records": torch.empty(n, 8, dtype=_F32, device=dev),
     }
-    total = torch.empty(1, dtype=_I64, device=dev)
+    # the count goes straight into pinned host memory (no copy kernel)
+    host = torch.empty(1, dtype=_I64, pin_memory=True)
     ws = torch.empty(query("gsplat_isect_prepare_rows_workspace_size", n),
                      dtype=torch.uint8, device=dev)
     call("gsplat_isect_prepare_rows", n, N, ptr(img), ptr(means2d), ptr(radii),
          ptr(depths), ptr(conics), ptr(opacities), int(tile_size),
          int(tile_width), int(tile_height), ptr(ws), ws.numel(),
          ptr(tiles_per_gauss), ptr(state["row_starts"]), ptr(state["records"]),
-         ptr(total), st)
-    host = torch.empty(1, dtype=_I64, pin_memory=True)
-    host.copy_(total, non_blocking=True)
+         ptr(host), st)
     ev = torch.cuda.Event()
     ev.record()
     state["total"] = (host, ev)

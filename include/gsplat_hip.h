@@ -141,7 +141,10 @@ size_t gsplat_projection_packed_workspace_size(int64_t B, int64_t C, int64_t N);
  * fuses (gsplat/cuda/csrc/Projection.cpp:308-437,
  *        gsplat/cuda/csrc/ProjectionEWA3DGSPacked.cu:39-398).
  * Every per-row output must have capacity for B*C*N rows; the number of rows
- * written (nnz) is stored to nnz_out (device int64).  indptr [B*C+1] int32;
+ * written (nnz) is stored to nnz_out (one int64 in device memory or in pinned
+ * host memory from hipHostMalloc, which the device writes directly: the host
+ * then reads it after the stream's next event, with no copy).  indptr [B*C+1]
+ * int32;
  * batch_ids, camera_ids, gaussian_ids int64.  row_of [B*C*N] int32
  * (optional) receives, for every (b, c, g), its packed row or -1: the inverse
  * of (batch_ids, camera_ids, gaussian_ids), used by the gathers below.
@@ -455,7 +458,8 @@ int gsplat_isect_emit_sorted_dev(
  * uses).  Counts the tiles of every row (tiles_per_gauss [n]), gives every
  * row its first slot in row order -- row_starts [n + 1] int64, the tile
  * count of all rows before it (row_starts[n] = n_isects, also written to
- * n_isects_out, device int64) -- and packs every row's sweep inputs into
+ * n_isects_out: one int64 in device or pinned host memory, as nnz_out of
+ * gsplat_projection_packed_fwd) -- and packs every row's sweep inputs into
  * row_records [n, 8] float (16-byte aligned) for stage 2.  Same row/camera
  * arguments as gsplat_isect_count; the workspace is
  * gsplat_isect_prepare_rows_workspace_size(n) bytes.
