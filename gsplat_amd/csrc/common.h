@@ -353,11 +353,16 @@ int radix_sort_ping_pong(int64_t n, int begin_bit, int end_bit, uint64_t *keys_a
 // keys as (key << 32 | low_bits[value]) into keys64_out instead of the key
 // buffer.  With n_dev the number of keys is min(n, *n_dev), read on the
 // device: n is then a capacity that sizes the launches and the workspace.
+// With counts_zeroed the caller has already cleared the words
+// radix_sort_first_counts() names (saving the sort's own clearing launch).
 int radix_sort_u32(int64_t n, int num_bits, uint32_t *keys_a, uint32_t *vals_a,
                    uint32_t *keys_b, uint32_t *vals_b, void *workspace,
                    size_t workspace_bytes, hipStream_t st, bool *result_in_b,
                    const uint32_t *low_bits, uint64_t *keys64_out,
-                   const int64_t *n_dev = nullptr);
+                   const int64_t *n_dev = nullptr, bool counts_zeroed = false);
+// The uint32 words of a sort workspace (for n keys) that must be zero when
+// the sort starts: *offset bytes into the workspace, *words long.
+void radix_sort_first_counts(int64_t n, size_t *offset, int64_t *words);
 int copy_u32(int64_t n, const uint32_t *src, uint32_t *dst, hipStream_t st);
 int copy_pairs(int64_t n, const uint64_t *ks, const uint32_t *vs, uint64_t *kd,
                uint32_t *vd, hipStream_t st);

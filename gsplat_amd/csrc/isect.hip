@@ -570,11 +570,16 @@ enum { kRowRminX, kRowRmaxX, kRowRminY, kRowRmaxY, kRowJ, kRowFlags,
        kRowFlat, kRowInts };
 
 // chunk_first[c] = the depth position whose slot range holds slot
-// c * kEmitSlots (rows without tiles own no slot).
+// c * kEmitSlots (rows without tiles own no slot).  Also clears the
+// `zero_words` words at `zero` (the tile sort's first counts) for the launch
+// that follows.
 __global__ void __launch_bounds__(kIsectThreads)
     emit_chunk_first_kernel(int64_t n, const int64_t *__restrict__ dstart,
-                            int64_t cap, int32_t *__restrict__ chunk_first) {
+                            int64_t cap, int32_t *__restrict__ chunk_first,
+                            uint32_t *__restrict__ zero, int64_t zero_words) {
     const int64_t i = (int64_t)blockIdx.x * kIsectThreads + threadIdx.x;
+    for (int64_t z = i; z < zero_words; z += (int64_t)gridDim.x * kIsectThreads)
+        zero[z] = 0u;
     if (i >= n)
         return;
     // slots at or past the capacity are not emitted (cap >= dstart[n] on
@@ -1582,8 +1587,13 @@ static int emit_sorted_impl(
     uint32_t *vb = passes % 2 == 1 ? out_vals : tmp_vals;
     hipStream_t st = as_stream(stream);
     int32_t *chunk_first = reinterpret_cast<int32_t *>(ws + L.chunks);
+    size_t z_off;
+    int64_t z_words;
+    radix_sort_first_counts(n_isects, &z_off, &z_words);
     emit_chunk_first_kernel<<<(unsigned)ceil_div(n, kIsectThreads), kIsectThreads,
-                              0, st>>>(n, depth_starts, n_isects, chunk_first);
+                              0, st>>>(n, depth_starts, n_isects, chunk_first,
+                                       reinterpret_cast<uint32_t *>(ws + L.sort_ws + z_off),
+                                       z_words);
     GS_TRY(check_launch("emit_chunk_first_kernel"));
     const int64_t chunks = ceil_div(n_isects, kEmitSlots);
     isect_emit_depth_kernel<<<(unsigned)ceil_div(chunks, kEmitWaves),
@@ -1596,7 +1606,7 @@ static int emit_sorted_impl(
     GS_TRY(radix_sort_u32(n_isects, key_bits, ka, va, kb, vb, ws + L.sort_ws,
                           workspace_bytes - L.sort_ws, st, &in_b,
                           reinterpret_cast<const uint32_t *>(depths),
-                          reinterpret_cast<uint64_t *>(isect_ids), n_dev));
+                          reinterpret_cast<uint64_t *>(isect_ids), n_dev, true));
     GS_REQUIRE((in_b ? vb : va) == out_vals, "isect_emit_sorted: pass parity");
     return GSPLAT_OK;
 }
@@ -1735,8 +1745,13 @@ static int emit_tiles_impl(
     uint32_t *va = passes % 2 == 1 ? tmp_vals : out_vals;
     uint32_t *vb = passes % 2 == 1 ? out_vals : tmp_vals;
     int32_t *chunk_first = reinterpret_cast<int32_t *>(ws + L.chunks);
+    size_t z_off;
+    int64_t z_words;
+    radix_sort_first_counts(n_isects, &z_off, &z_words);
     emit_chunk_first_kernel<<<(unsigned)ceil_div(n, kIsectThreads), kIsectThreads,
-                              0, st>>>(n, row_starts, n_isects, chunk_first);
+                              0, st>>>(n, row_starts, n_isects, chunk_first,
+                                       reinterpret_cast<uint32_t *>(ws + L.sort_ws + z_off),
+                                       z_words);
     GS_TRY(check_launch("emit_chunk_first_kernel"));
     const int64_t chunks = ceil_div(n_isects, kEmitSlots);
     isect_emit_depth_kernel<<<(unsigned)ceil_div(chunks, kEmitWaves),
@@ -1747,7 +1762,7 @@ static int emit_tiles_impl(
     bool in_b = false;
     GS_TRY(radix_sort_u32(n_isects, key_bits, ka, va, kb, vb, ws + L.sort_ws,
                           workspace_bytes - L.sort_ws, st, &in_b, nullptr, nullptr,
-                          n_dev));
+                          n_dev, true));
     GS_REQUIRE((in_b ? vb : va) == out_vals, "isect_emit_tiles: pass parity");
     const uint32_t *sorted_keys = in_b ? kb : ka;
     uint32_t *free_keys = in_b ? ka : kb;

@@ -7,21 +7,25 @@
 //
 // Per pass (digit of up to 8 bits, 1024-key tiles up to 2M keys, 4096-key
 // tiles above, so that a large sort's scatter fits one round of resident
-// workgroups):
+// workgroups), two launches:
 //   1. radix_hist_kernel    digit counts per tile with LDS atomics, written
-//                           tile-major (coalesced);
-//   2. radix_colscan_kernel one workgroup per 4 digits scans those digits'
-//                           counts over the tiles and records the digit
-//                           totals (no cross-workgroup waits);
-//   3. radix_scatter_kernel ranks every key stably inside its tile (wave64
-//                           match ballots, order wave, item, lane), reorders
-//                           the tile by digit in LDS, and writes each digit
-//                           run with consecutive threads on consecutive
-//                           addresses.
-// Three launches per digit, and no single-pass (decoupled look-back) sort:
-// on this GPU a look-back step is a cross-XCD round trip and a workgroup
-// ticket a serialized device atomic, which cost more at these sizes than the
-// two extra launch boundaries.
+//                           tile-major (coalesced), and added to the counts
+//                           of the tile's group (about sqrt(tiles) tiles,
+//                           one global atomic per digit and tile);
+//   2. radix_scatter_kernel forms its tile's prefix of every digit from the
+//                           counts of the groups before it and of the tiles
+//                           before it in its own group (about 2 sqrt(tiles)
+//                           loads per digit), ranks every key stably inside
+//                           its tile (wave64 match ballots, order wave, item,
+//                           lane), reorders the tile by digit in LDS, and
+//                           writes each digit run with consecutive threads on
+//                           consecutive addresses.  It also clears the group
+//                           counts of the next pass.
+// A column-scan launch between the two (one workgroup per 4 digits) cost
+// ~7 us per pass of pure latency at config 1.  No single-pass (decoupled
+// look-back) sort: on this GPU a look-back step is a cross-XCD round trip
+// and a workgroup ticket a serialized device atomic, which cost more at
+// these sizes than the extra launch boundary.
 // radix_sort_ping_pong alternates between two buffer pairs and reports which
 // one holds the result, so callers that fill the first pair themselves can
 // choose it to make the result land where they want it.
@@ -47,11 +51,13 @@ constexpr int kScanThreads = 256;
 constexpr int kScanItems = 8;
 constexpr int kScanTile = kScanThreads * kScanItems;
 
-// Digit counts of one tile, block-major: hist[tile * 256 + d].
+// Digit counts of one tile, block-major: hist[tile * 256 + d], also added to
+// group_hist[(tile / group_tiles) * 256 + d] (zero on entry).
 template <int ITEMS, typename K>
 __global__ void __launch_bounds__(kSortThreads)
     radix_hist_kernel(const K *__restrict__ keys, int64_t n, int shift,
                       int bits, uint32_t *__restrict__ hist,
+                      uint32_t *__restrict__ group_hist, int group_tiles,
                       const int64_t *__restrict__ n_dev) {
     constexpr int kSortItems = ITEMS;
     constexpr int kSortTile = kSortThreads * ITEMS;
@@ -83,78 +89,8 @@ __global__ void __launch_bounds__(kSortThreads)
     for (int ww = 0; ww < kSortWaves; ++ww)
         tot += s_cnt[ww][d];
     hist[(int64_t)blockIdx.x * kRadix + d] = tot;
-}
-
-// kColDigits consecutive digits per workgroup: exclusive prefix of each
-// digit's count over the tiles (prefix[tile * 256 + d]) and the digit's
-// total.  A thread reads the digits' counts of one tile as one 16-byte load
-// (the tile-major rows are 1 KiB), so the workgroups touch every row line
-// once per kColDigits digits instead of once per digit.
-constexpr int kColDigits = 4;
-
-// The counts of up to kColCache tiles per thread stay in registers between
-// the summing and the writing loop (one memory round trip instead of two).
-constexpr int kColCache = 8;
-
-__global__ void __launch_bounds__(kSortThreads)
-    radix_colscan_kernel(const uint32_t *__restrict__ hist, int64_t n_tiles,
-                         uint32_t *__restrict__ prefix,
-                         uint32_t *__restrict__ totals) {
-    __shared__ uint32_t s_wave[kSortWaves];
-    const int d0 = blockIdx.x * kColDigits;
-    const int64_t per = ceil_div(n_tiles, kSortThreads);
-    const int64_t t0 = (int64_t)threadIdx.x * per;
-    const int64_t t1 = t0 + per < n_tiles ? t0 + per : n_tiles;
-    uint4 cache[kColCache];
-#pragma unroll
-    for (int j = 0; j < kColCache; ++j)
-        cache[j] = t0 + j < t1
-                       ? *reinterpret_cast<const uint4 *>(hist + (t0 + j) * kRadix + d0)
-                       : make_uint4(0u, 0u, 0u, 0u);
-    uint32_t sum[kColDigits] = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int j = 0; j < kColCache; ++j) {
-        sum[0] += cache[j].x;
-        sum[1] += cache[j].y;
-        sum[2] += cache[j].z;
-        sum[3] += cache[j].w;
-    }
-    for (int64_t t = t0 + kColCache; t < t1; ++t) {
-        const uint4 c = *reinterpret_cast<const uint4 *>(hist + t * kRadix + d0);
-        sum[0] += c.x;
-        sum[1] += c.y;
-        sum[2] += c.z;
-        sum[3] += c.w;
-    }
-    uint32_t run[kColDigits];
-#pragma unroll
-    for (int k = 0; k < kColDigits; ++k) {
-        uint32_t total;
-        run[k] = block_exclusive_u32<kSortThreads>(sum[k], s_wave, &total);
-        if (threadIdx.x == 0)
-            totals[d0 + k] = total;
-        __syncthreads();  // s_wave is reused by the next digit's scan
-    }
-#pragma unroll
-    for (int j = 0; j < kColCache; ++j) {
-        if (t0 + j < t1) {
-            *reinterpret_cast<uint4 *>(prefix + (t0 + j) * kRadix + d0) =
-                make_uint4(run[0], run[1], run[2], run[3]);
-            run[0] += cache[j].x;
-            run[1] += cache[j].y;
-            run[2] += cache[j].z;
-            run[3] += cache[j].w;
-        }
-    }
-    for (int64_t t = t0 + kColCache; t < t1; ++t) {
-        const uint4 c = *reinterpret_cast<const uint4 *>(hist + t * kRadix + d0);
-        *reinterpret_cast<uint4 *>(prefix + t * kRadix + d0) =
-            make_uint4(run[0], run[1], run[2], run[3]);
-        run[0] += c.x;
-        run[1] += c.y;
-        run[2] += c.z;
-        run[3] += c.w;
-    }
+    if (tot != 0u)
+        atomicAdd(&group_hist[(int64_t)(blockIdx.x / group_tiles) * kRadix + d], tot);
 }
 
 // Stable scatter of one tile: ranks come from wave64 match ballots
@@ -168,12 +104,18 @@ __global__ void __launch_bounds__(kSortThreads)
                          const uint32_t *__restrict__ vals_in,
                          K *__restrict__ keys_out,
                          uint32_t *__restrict__ vals_out, int64_t n, int shift,
-                         int bits, const uint32_t *__restrict__ prefix,
-                         const uint32_t *__restrict__ totals,
+                         int bits, const uint32_t *__restrict__ hist,
+                         const uint32_t *__restrict__ group_hist, int group_tiles,
+                         int n_groups, uint32_t *__restrict__ next_group_hist,
                          const uint32_t *__restrict__ low_bits,
                          uint64_t *__restrict__ keys64_out,
                          const int64_t *__restrict__ n_dev) {
     constexpr int kSortItems = ITEMS;
+    // the next pass's group counts start from zero (this pass reads only
+    // its own); n_tiles >= n_groups, so the workgroups cover them
+    if (next_group_hist != nullptr &&
+        (int64_t)blockIdx.x * kRadix + threadIdx.x < (int64_t)n_groups * kRadix)
+        next_group_hist[(int64_t)blockIdx.x * kRadix + threadIdx.x] = 0u;
     if (n_dev != nullptr)  // key count on the device, n the capacity
         n = min(n, *n_dev);
     // workgroups past the device count have no key to move (the whole
@@ -206,12 +148,27 @@ __global__ void __launch_bounds__(kSortThreads)
         k[j] = valid ? keys_in[i] : ~(K)0;
         v[j] = valid ? vals_in[i] : 0u;
     }
-    // global start of every digit for this tile: digit base + tile prefix
+    // global start of every digit for this tile: digit base (over the digit
+    // totals) + the digit's count in the tiles before this one (the groups
+    // before this tile's group, then the tiles before it in the group)
     {
-        const uint32_t tile_prefix = prefix[(int64_t)blockIdx.x * kRadix + tid];
+        const int d = tid;
+        const int g = (int)(blockIdx.x / group_tiles);
+        uint32_t tot = 0u, pre = 0u;
+        if (d <= (int)mask) {  // digits above the pass's bits have no keys
+#pragma unroll 8
+            for (int gg = 0; gg < n_groups; ++gg) {
+                const uint32_t c = group_hist[(int64_t)gg * kRadix + d];
+                tot += c;
+                pre += gg < g ? c : 0u;
+            }
+#pragma unroll 8
+            for (int64_t tt = (int64_t)g * group_tiles; tt < (int64_t)blockIdx.x; ++tt)
+                pre += hist[tt * kRadix + d];
+        }
         uint32_t total;
-        const uint32_t dbase = block_exclusive_u32<kSortThreads>(totals[tid], s_wave, &total);
-        s_gstart[tid] = dbase + tile_prefix;
+        const uint32_t dbase = block_exclusive_u32<kSortThreads>(tot, s_wave, &total);
+        s_gstart[tid] = dbase + pre;
     }
     for (int i = tid; i < kSortWaves * kRadix; i += kSortThreads)
         (&s_cnt[0][0])[i] = 0u;
@@ -340,18 +297,32 @@ __global__ void copy_u32_kernel(const uint32_t *__restrict__ src,
 
 struct SortLayout {
     int64_t n_tiles;
-    size_t hist_off, prefix_off, totals_off, total;
+    int group_tiles, n_groups;
+    size_t hist_off, group_off[2], total;
 };
 
 SortLayout sort_layout(int64_t n) {
     SortLayout L;
     L.n_tiles = ceil_div(n > 0 ? n : 1, (int64_t)kSortThreads * sort_items(n));
+    // groups of about sqrt(tiles) tiles
+    int gt = 1;
+    while ((int64_t)gt * gt < L.n_tiles)
+        ++gt;
+    L.group_tiles = gt;
+    L.n_groups = (int)ceil_div(L.n_tiles, (int64_t)gt);
     const size_t tbytes = ((size_t)L.n_tiles * kRadix * 4 + 255) / 256 * 256;
+    const size_t gbytes = ((size_t)L.n_groups * kRadix * 4 + 255) / 256 * 256;
     L.hist_off = 0;
-    L.prefix_off = tbytes;
-    L.totals_off = 2 * tbytes;
-    L.total = L.totals_off + kRadix * 4;
+    L.group_off[0] = tbytes;
+    L.group_off[1] = tbytes + gbytes;
+    L.total = tbytes + 2 * gbytes;
     return L;
+}
+
+__global__ void zero_u32_kernel(uint32_t *__restrict__ p, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n)
+        p[i] = 0u;
 }
 
 }  // namespace
@@ -370,7 +341,7 @@ int radix_sort_impl(int64_t n, int begin_bit, int end_bit, K *keys_a,
                     uint32_t *vals_a, K *keys_b, uint32_t *vals_b, void *workspace,
                     size_t workspace_bytes, hipStream_t st, bool *result_in_b,
                     const uint32_t *low_bits, uint64_t *keys64_out,
-                    const int64_t *n_dev) {
+                    const int64_t *n_dev, bool counts_zeroed) {
     *result_in_b = false;
     const int num_bits = end_bit - begin_bit;
     if (n == 0 || num_bits <= 0)
@@ -381,35 +352,40 @@ int radix_sort_impl(int64_t n, int begin_bit, int end_bit, K *keys_a,
                "radix sort: workspace too small");
     char *ws = reinterpret_cast<char *>(workspace);
     uint32_t *hist = reinterpret_cast<uint32_t *>(ws + L.hist_off);
-    uint32_t *prefix = reinterpret_cast<uint32_t *>(ws + L.prefix_off);
-    uint32_t *totals = reinterpret_cast<uint32_t *>(ws + L.totals_off);
+    uint32_t *group[2] = {reinterpret_cast<uint32_t *>(ws + L.group_off[0]),
+                          reinterpret_cast<uint32_t *>(ws + L.group_off[1])};
     const int passes = radix_sort_passes(num_bits);
     int shift = begin_bit;
     K *ksrc = keys_a, *kdst = keys_b;
     uint32_t *vsrc = vals_a, *vdst = vals_b;
     const bool small = sort_items(n) == kSortItemsSmall;
+    const int64_t gwords = (int64_t)L.n_groups * kRadix;
+    if (!counts_zeroed) {
+        zero_u32_kernel<<<(unsigned)ceil_div(gwords, 256), 256, 0, st>>>(group[0],
+                                                                          gwords);
+        GS_TRY(check_launch("zero_u32_kernel"));
+    }
     for (int p = 0; p < passes; ++p) {
         const int remaining = end_bit - shift;
         const int bits = (remaining + (passes - p) - 1) / (passes - p);
         uint64_t *k64 = p == passes - 1 ? keys64_out : nullptr;
+        uint32_t *gcur = group[p & 1];
+        uint32_t *gnext = p + 1 < passes ? group[(p + 1) & 1] : nullptr;
         if (small)
             radix_hist_kernel<kSortItemsSmall, K><<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
-                ksrc, n, shift, bits, hist, n_dev);
+                ksrc, n, shift, bits, hist, gcur, L.group_tiles, n_dev);
         else
             radix_hist_kernel<kSortItemsLarge, K><<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
-                ksrc, n, shift, bits, hist, n_dev);
+                ksrc, n, shift, bits, hist, gcur, L.group_tiles, n_dev);
         GS_TRY(check_launch("radix_hist_kernel"));
-        radix_colscan_kernel<<<kRadix / kColDigits, kSortThreads, 0, st>>>(
-            hist, L.n_tiles, prefix, totals);
-        GS_TRY(check_launch("radix_colscan_kernel"));
         if (small)
             radix_scatter_kernel<kSortItemsSmall, K><<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
-                ksrc, vsrc, kdst, vdst, n, shift, bits, prefix, totals, low_bits, k64,
-                n_dev);
+                ksrc, vsrc, kdst, vdst, n, shift, bits, hist, gcur, L.group_tiles,
+                L.n_groups, gnext, low_bits, k64, n_dev);
         else
             radix_scatter_kernel<kSortItemsLarge, K><<<(unsigned)L.n_tiles, kSortThreads, 0, st>>>(
-                ksrc, vsrc, kdst, vdst, n, shift, bits, prefix, totals, low_bits, k64,
-                n_dev);
+                ksrc, vsrc, kdst, vdst, n, shift, bits, hist, gcur, L.group_tiles,
+                L.n_groups, gnext, low_bits, k64, n_dev);
         GS_TRY(check_launch("radix_scatter_kernel"));
         shift += bits;
         K *tk = ksrc; ksrc = kdst; kdst = tk;
@@ -425,20 +401,26 @@ int radix_sort_ping_pong(int64_t n, int begin_bit, int end_bit, uint64_t *keys_a
                          hipStream_t st, bool *result_in_b) {
     return radix_sort_impl<uint64_t>(n, begin_bit, end_bit, keys_a, vals_a, keys_b,
                                      vals_b, workspace, workspace_bytes, st,
-                                     result_in_b, nullptr, nullptr, nullptr);
+                                     result_in_b, nullptr, nullptr, nullptr, false);
 }
 
 int radix_sort_u32(int64_t n, int num_bits, uint32_t *keys_a, uint32_t *vals_a,
                    uint32_t *keys_b, uint32_t *vals_b, void *workspace,
                    size_t workspace_bytes, hipStream_t st, bool *result_in_b,
                    const uint32_t *low_bits, uint64_t *keys64_out,
-                   const int64_t *n_dev) {
+                   const int64_t *n_dev, bool counts_zeroed) {
     GS_REQUIRE(num_bits >= 0 && num_bits <= 32, "radix sort: num_bits in [0, 32]");
     GS_REQUIRE(keys64_out == nullptr || (low_bits != nullptr && num_bits > 0),
                "radix sort: 64-bit output needs low bits and at least one pass");
     return radix_sort_impl<uint32_t>(n, 0, num_bits, keys_a, vals_a, keys_b, vals_b,
                                      workspace, workspace_bytes, st, result_in_b,
-                                     low_bits, keys64_out, n_dev);
+                                     low_bits, keys64_out, n_dev, counts_zeroed);
+}
+
+void radix_sort_first_counts(int64_t n, size_t *offset, int64_t *words) {
+    const SortLayout L = sort_layout(n);
+    *offset = L.group_off[0];
+    *words = (int64_t)L.n_groups * kRadix;
 }
 
 int copy_pairs(int64_t n, const uint64_t *ks, const uint32_t *vs, uint64_t *kd,
