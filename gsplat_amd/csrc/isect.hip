@@ -905,26 +905,45 @@ __global__ void isect_starts_finalize_kernel(int64_t n,
 }
 
 // offsets[s] = the first slot whose image|tile key is that of tile slot s
-// (image * n_tiles + tile), or n when none is; one thread per slot boundary
-// i in [0, n], which fills the tile slots between the keys of slots i - 1
-// and i.  With n_dev the slot count is min(n, *n_dev).
+// (image * n_tiles + tile), or n when none is.  Every slot boundary i in
+// [0, n] fills the tile slots between the keys of slots i - 1 and i; a
+// thread takes four consecutive boundaries with one 16-byte load of their
+// keys (keys is 16-byte aligned and padded to a multiple of 4 entries).
+// With n_dev the slot count is min(n, *n_dev).
+constexpr int kBoundsPer = 4;
+
 __global__ void tile_bounds_kernel(int64_t n, const int64_t *__restrict__ n_dev,
                                    const uint32_t *__restrict__ keys,
                                    int64_t n_slots, int32_t tile_n_bits,
                                    int32_t n_tiles, int32_t *__restrict__ offsets) {
     if (n_dev != nullptr)
         n = min(n, *n_dev);
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i > n)
+    const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * kBoundsPer;
+    if (i0 > n)
         return;
     const uint32_t mask = (1u << tile_n_bits) - 1u;
     auto slot = [&](uint32_t k) {
         return (int64_t)(k >> tile_n_bits) * n_tiles + (int64_t)(k & mask);
     };
-    const int64_t cur = i < n ? slot(keys[i]) : n_slots;
-    const int64_t prev = i > 0 ? slot(keys[i - 1]) : -1;
-    for (int64_t s = prev + 1; s <= cur && s < n_slots; ++s)
-        offsets[s] = (int32_t)i;
+    uint32_t k[kBoundsPer + 1];  // keys of slots i0 - 1 .. i0 + 3
+    k[0] = i0 > 0 ? keys[i0 - 1] : 0u;
+    if (i0 < n) {
+        const uint4 q = *reinterpret_cast<const uint4 *>(keys + i0);
+        k[1] = q.x;
+        k[2] = q.y;
+        k[3] = q.z;
+        k[4] = q.w;
+    }
+#pragma unroll
+    for (int j = 0; j < kBoundsPer; ++j) {
+        const int64_t i = i0 + j;
+        if (i > n)
+            break;
+        const int64_t cur = i < n ? slot(k[j + 1]) : n_slots;
+        const int64_t prev = i > 0 ? slot(k[j]) : -1;
+        for (int64_t s = prev + 1; s <= cur && s < n_slots; ++s)
+            offsets[s] = (int32_t)i;
+    }
 }
 
 constexpr int kSegThreads = 256;  // a multiple of the 256 digits
@@ -1766,7 +1785,7 @@ static int emit_tiles_impl(
     GS_REQUIRE((in_b ? vb : va) == out_vals, "isect_emit_tiles: pass parity");
     const uint32_t *sorted_keys = in_b ? kb : ka;
     uint32_t *free_keys = in_b ? ka : kb;
-    tile_bounds_kernel<<<(unsigned)ceil_div(n_isects + 1, 256), 256, 0, st>>>(
+    tile_bounds_kernel<<<(unsigned)ceil_div(n_isects + 1, 256 * kBoundsPer), 256, 0, st>>>(
         n_isects, n_dev, sorted_keys, n_slots, a.tile_n_bits, (int32_t)n_tiles,
         offsets);
     GS_TRY(check_launch("tile_bounds_kernel"));
