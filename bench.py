@@ -92,9 +92,11 @@ def _algorithmic_bytes(name, ctx):
     pix, D, tiles = ctx["pixels"], ctx["D"], ctx["tiles"]
     K = ctx["K"]
     gauss2d = 8 + 12 + 4 + F32 * D  # means2d, conic, opacity, colour
-    if name == "gsplat_rasterize_fwd":
+    # the replay forms move the same inputs and outputs; their replay state
+    # is scratch between the two launches
+    if name in ("gsplat_rasterize_fwd", "gsplat_rasterize_fwd_replay"):
         return n_isects * (4 + gauss2d) + tiles * 4 + pix * (F32 * D + 4 + 4 + 4)
-    if name == "gsplat_rasterize_bwd":
+    if name in ("gsplat_rasterize_bwd", "gsplat_rasterize_bwd_replay"):
         return (n_isects * (4 + gauss2d) + tiles * 4 + pix * (4 + 4 + F32 * D + 4)
                 + nnz * (8 + 12 + F32 * D + 4))
     if name == "gsplat_projection_packed_fwd":

@@ -109,6 +109,15 @@ _SIGNATURES = {
         c_int64, c_int64, c_int64, c_int32, _P, _P, _P, _P, _P, _P,
         c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P,
         _P, _P, _P, _P, _P, _P, _P, _P],
+    "gsplat_rasterize_replay_size": [c_int64, c_int32, c_int32, c_int32, c_int64, c_int32],
+    "gsplat_rasterize_fwd_replay": [
+        c_int64, c_int64, c_int64, c_int32, _P, _P, _P, _P, _P, _P,
+        c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P, _P,
+        c_size_t, _P],
+    "gsplat_rasterize_bwd_replay": [
+        c_int64, c_int64, c_int64, c_int32, _P, _P, _P, _P, _P, _P,
+        c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P,
+        _P, _P, _P, _P, _P, _P, _P, c_size_t, _P],
     "gsplat_quat_scale_to_covar_preci_fwd": [c_int64, _P, _P, c_int32, _P, _P, _P],
     "gsplat_quat_scale_to_covar_preci_bwd": [
         c_int64, _P, _P, c_int32, _P, _P, _P, _P, _P],
@@ -130,6 +139,7 @@ _RESTYPES = {
     "gsplat_last_error": ctypes.c_char_p,
     "gsplat_version": ctypes.c_char_p,
     "gsplat_projection_packed_workspace_size": c_size_t,
+    "gsplat_rasterize_replay_size": c_size_t,
     "gsplat_projection_packed_fwd_noalloc_max_rows": c_int64,
     "gsplat_isect_count_workspace_size": c_size_t,
     "gsplat_sort_pairs_workspace_size": c_size_t,

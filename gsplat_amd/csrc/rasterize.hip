@@ -47,6 +47,35 @@ struct RasterArgs {
     const int32_t *tile_offsets, *flatten_ids;
 };
 
+// Replay state written by the forward for a backward split into units of
+// one part: Q = tile_size^2 / 4 consecutive intersections of a tile.
+//   records  per part boundary m >= 1 of a tile, per pixel of the tile: the
+//            transmittance before part m and the colour part m composited
+//            (float32, summed from zero within the part); record slot
+//            (range_start + m * Q - 1) / Q, so slots of different tiles
+//            never meet and ceil(n_isects / Q) slots cover every tile;
+//   units    (tile, part) pairs of every part up to the tile's last
+//            contributor, appended per tile by the forward;
+//   count    the number of units (zeroed before the forward).
+// A unit's backward starts from its end boundary's record instead of
+// replaying every part behind it, so the units of one tile run side by side
+// and no workgroup holds a long tile at the end of the launch.
+struct ReplayState {
+    uint32_t *count;
+    int2 *units;
+    float *records;
+};
+
+// Replay parts per forward batch: a part is BS / kReplayParts consecutive
+// intersections of a tile.
+constexpr int kReplayParts = 4;
+
+// record slot of a tile's part boundary m >= 1 (parts of q intersections)
+__device__ __forceinline__ int64_t replay_record_slot(int32_t range_start, int m,
+                                                      int q) {
+    return ((int64_t)range_start + (int64_t)m * q - 1) / q;
+}
+
 // exact (uncontracted) Mahalanobis term; the host oracle uses this order
 __device__ __forceinline__ float gauss_sigma(float a, float b, float c,
                                              float dx, float dy) {
@@ -133,6 +162,38 @@ __device__ __forceinline__ int wave_work_list(const uint8_t *wmask, int t0,
     return n_work;
 }
 
+// wave_work_list that also gives, for every replay part q (slots
+// [q Q, (q + 1) Q)), the list position where the part's items end.
+template <int Q, int NQ, typename SlotT>
+__device__ __forceinline__ int wave_work_list_parts(const uint8_t *wmask, int n,
+                                                    int wave, SlotT *list,
+                                                    int (&part_end)[NQ]) {
+    int n_work = 0;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+        part_end[q] = -1;
+    for (int c0 = 0; c0 < n; c0 += kWave) {
+        const int slot = c0 + (int)lane_id();
+        const bool take = slot < n && ((wmask[slot] >> wave) & 1u);
+        const uint64_t bal = wave_ballot(take);
+        if (take)
+            list[n_work + __popcll(bal & lanemask_lt())] = (SlotT)slot;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const int e = (q + 1) * Q - c0;  // part end relative to the chunk
+            if (e > 0 && e <= kWave)
+                part_end[q] = n_work + __popcll(e == kWave ? bal : bal & ((1ull << e) - 1));
+        }
+        n_work += __popcll(bal);
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+        if (part_end[q] < 0)
+            part_end[q] = n_work;
+    return n_work;
+}
+
 __device__ __forceinline__ void tile_coords(const RasterArgs &a, int64_t gid,
                                             int64_t &image, int32_t &tile,
                                             int32_t &ty, int32_t &tx) {
@@ -164,13 +225,14 @@ template <int CDIM, int TILE>
 __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
     const RasterArgs a, float *__restrict__ render_colors,
     float *__restrict__ render_alphas, int32_t *__restrict__ last_ids,
-    float *__restrict__ render_T) {
+    float *__restrict__ render_T, const ReplayState rs) {
     constexpr int BS = TileShape<TILE>::BS;
     constexpr int NW = (BS + kWave - 1) / kWave;       // waves per tile
     constexpr int WROWS = (kWave < BS ? kWave : BS) / TILE;  // rows per wave
     __shared__ FwdSlot<CDIM> s_slot[BS];
     __shared__ uint8_t s_wmask[BS];       // waves a Gaussian can reach
     __shared__ uint8_t s_list[NW][BS];    // per-wave work list
+    __shared__ int32_t s_last;            // the tile's last contributor
 
     int64_t image;
     int32_t tile, ty, tx;
@@ -210,11 +272,18 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
     // combine in scalar registers, and the selects read the mask directly
     const uint64_t lanes_m = wave_ballot(true);
     uint64_t done_m = wave_ballot(!inside);
-    float acc[CDIM];
+    // the colour is summed per batch (seg, from zero) and the batch sums into
+    // acc; a batch sum is also what the replay records keep
+    float acc[CDIM], seg[CDIM];
 #pragma unroll
-    for (int k = 0; k < CDIM; ++k)
+    for (int k = 0; k < CDIM; ++k) {
         acc[k] = 0.f;
+        seg[k] = 0.f;
+    }
+    if (tr == 0)
+        s_last = -1;
 
+    constexpr int Q = BS / kReplayParts;   // intersections per replay part
     for (int b = 0; b < num_batches; ++b) {
         if (__syncthreads_count(__builtin_amdgcn_inverse_ballot_w64(done_m)) >= BS)
             break;
@@ -243,12 +312,26 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
         // the staged Gaussians whose alpha support reaches this wave's strip
         // (no other can composite on its pixels), in depth order
         const int wave = tr / kWave;
-        const int n_work = wave_work_list(s_wmask, 0, batch_size, wave, s_list[wave]);
+        // Replay part q of the batch covers slots [q Q, (q + 1) Q): the
+        // work list is walked part by part, and at the end of each part its
+        // record gets, for the pixels not yet done when it started, T at its
+        // start and the colour it composited; the part's colour joins the
+        // total.
+        int part_end[kReplayParts];
+        const int n_work = wave_work_list_parts<Q>(s_wmask, batch_size, wave,
+                                                   s_list[wave], part_end);
+        const int n_parts = (batch_size + Q - 1) / Q;
+        int n = 0;
+        for (int q = 0; q < n_parts; ++q) {
+        const float T_part = T;
+        const uint64_t done_part = done_m;
         // wave-uniform loop; a lane that is done (or skips a Gaussian) is
         // carried by selects, not branches
-        for (int n = 0; n < n_work; ++n) {
-            if (done_m == lanes_m)
+        for (; n < part_end[q]; ++n) {
+            if (done_m == lanes_m) {
+                n = n_work;
                 break;
+            }
             const int t = s_list[wave][n];
             const FwdSlot<CDIM> &sl = s_slot[t];
             const float4 geo = sl.geo;
@@ -273,7 +356,7 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
             const float w = upd ? alpha * T : 0.f;
 #pragma unroll
             for (int k = 0; k < CDIM; ++k)
-                acc[k] = fmaf(sl.col[k], w, acc[k]);
+                seg[k] = fmaf(sl.col[k], w, seg[k]);
             // read unconditionally: a conditional read becomes another
             // exec-masked branch around one LDS load
             int32_t slot_idx = __float_as_int(sl.col[CDIM]);
@@ -281,6 +364,36 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
             cur_idx = upd ? slot_idx : cur_idx;
             T = upd ? next_T : T;
             done_m |= take_m & stop_m;
+        }
+        const int m = b * kReplayParts + q;
+        if (rs.records != nullptr && m >= 1 &&
+            !__builtin_amdgcn_inverse_ballot_w64(done_part)) {
+            float *rec = rs.records + replay_record_slot(range_start, m, Q) *
+                                          (int64_t)((1 + CDIM) * BS);
+            rec[tr] = T_part;
+#pragma unroll
+            for (int k = 0; k < CDIM; ++k)
+                rec[(1 + k) * BS + tr] = seg[k];
+        }
+#pragma unroll
+        for (int k = 0; k < CDIM; ++k) {
+            acc[k] += seg[k];
+            seg[k] = 0.f;
+        }
+        }
+    }
+    if (rs.units != nullptr) {
+        // one replay unit per part up to the tile's last contributor (a pixel
+        // composited something iff its T dropped below 1)
+        __syncthreads();
+        if (inside && T < 1.f)
+            atomicMax(&s_last, cur_idx);
+        __syncthreads();
+        if (tr == 0 && s_last >= range_start) {
+            const int nu = (s_last - range_start) / Q + 1;
+            const uint32_t base = atomicAdd(rs.count, (uint32_t)nu);
+            for (int u = 0; u < nu; ++u)
+                rs.units[base + u] = make_int2((int32_t)blockIdx.x, u);
         }
     }
     if (inside) {
@@ -411,7 +524,8 @@ __device__ __forceinline__ void rasterize_bwd_tile(
     const float *__restrict__ v_render_alphas,
     float *__restrict__ v_means2d_abs, float *__restrict__ v_means2d,
     float *__restrict__ v_conics, float *__restrict__ v_colors,
-    float *__restrict__ v_opacities, BwdSmem<CDIM, TILE, ABS> &sm) {
+    float *__restrict__ v_opacities, BwdSmem<CDIM, TILE, ABS> &sm,
+    int32_t unit, const float *__restrict__ records) {
     using SH = BwdShape<TILE>;
     constexpr int NB = SH::BATCH;
     constexpr int PX = SH::PX;
@@ -503,7 +617,49 @@ __device__ __forceinline__ void rasterize_bwd_tile(
     atomicMax(&s_tile_bin, wave_bin);
     __syncthreads();
     const int32_t replay_end = min(range_end, s_tile_bin + 1);
-    const int num_batches = max(0, replay_end - range_start + NB - 1) / NB;
+    // Whole tile (unit < 0): batches of NB back from replay_end.  One unit:
+    // the forward's replay part `unit` of the tile, [lo, min(lo + Q,
+    // replay_end)), starting from the forward's record at its end boundary:
+    // T there, and the colour composited behind it as the sum of the later
+    // parts' records (in double).
+    int num_batches;
+    int32_t first_end, lo;
+    if (unit < 0) {
+        num_batches = max(0, replay_end - range_start + NB - 1) / NB;
+        first_end = replay_end - 1;
+        lo = range_start;
+    } else {
+        constexpr int Q = NB / kReplayParts;
+        const int nu = max(0, replay_end - range_start + Q - 1) / Q;
+        if (unit >= nu)
+            return;
+        num_batches = 1;
+        lo = range_start + unit * Q;
+        first_end = min(lo + Q, replay_end) - 1;
+        if (unit < nu - 1) {
+            // A pixel whose last contributor lies before part m was done
+            // before m: the forward kept no record for it there, its T at m is
+            // the final one and m composited nothing on it.
+            constexpr int RS = (1 + CDIM) * NB;  // floats per record
+#pragma unroll
+            for (int p = 0; p < PX; ++p) {
+                const int lp = (PX * (tr / TILE) + p) * TILE + tr % TILE;
+                double bv = 0.0;
+                for (int m = unit + 1; m < nu && bin_final[p] >= range_start + m * Q;
+                     ++m) {
+                    const float *r = records + replay_record_slot(range_start, m, Q) * RS;
+                    if (m == unit + 1) {
+                        T[p] = r[lp];
+                        T64[p] = (double)T[p];
+                    }
+#pragma unroll
+                    for (int k = 0; k < CDIM; ++k)
+                        bv += (double)r[(1 + k) * NB + lp] * (double)v_c[p][k];
+                }
+                Bv[p] = bv;
+            }
+        }
+    }
 
     // the tile-sum slot this lane adds from every reduced register
     using RR = RowReduce<NACC>;
@@ -518,13 +674,13 @@ __device__ __forceinline__ void rasterize_bwd_tile(
     // that flush.
     for (int b = 0; b < num_batches; ++b) {
         __syncthreads();
-        const int32_t batch_end = replay_end - 1 - b * NB;
-        const int batch_size = min(NB, batch_end + 1 - range_start);
+        const int32_t batch_end = first_end - b * NB;
+        const int batch_size = min(NB, batch_end + 1 - lo);
 #pragma unroll
         for (int q = 0; q < SLOTS; ++q) {
             const int slot = tr + q * NT;
             const int32_t idx = batch_end - slot;
-            if (idx >= range_start) {
+            if (idx >= lo) {
                 const int32_t g = a.flatten_ids[idx];
                 s_gid[slot] = g;
                 const float2 xy = reinterpret_cast<const float2 *>(a.means2d)[g];
@@ -721,24 +877,34 @@ __global__ void __launch_bounds__(BwdShape<TILE>::THREADS) rasterize_bwd_kernel(
     float *__restrict__ v_means2d_abs, float *__restrict__ v_means2d,
     float *__restrict__ v_conics, float *__restrict__ v_colors,
     float *__restrict__ v_opacities, uint32_t *__restrict__ tile_counter,
-    int64_t n_tiles_total) {
+    int64_t n_tiles_total, const ReplayState rs) {
     __shared__ BwdSmem<CDIM, TILE, ABS> sm;
     const bool queue = tile_counter != nullptr;
-    int64_t gid = blockIdx.x;
+    // with replay state the queue hands out the forward's units, otherwise
+    // whole tiles
+    const int64_t n_work = rs.units != nullptr ? (int64_t)*rs.count : n_tiles_total;
+    int64_t k = blockIdx.x;
     while (true) {
         if (queue) {
-            __syncthreads();  // the previous tile is finished with the LDS
+            __syncthreads();  // the previous unit is finished with the LDS
             if (threadIdx.x == 0)
                 sm.next_tile = atomicAdd(tile_counter, 1u);
             __syncthreads();
-            gid = sm.next_tile;
+            k = sm.next_tile;
         }
-        if (gid >= n_tiles_total)
+        if (k >= n_work)
             break;
+        int64_t gid = k;
+        int32_t unit = -1;
+        if (rs.units != nullptr) {
+            const int2 e = rs.units[k];
+            gid = e.x;
+            unit = e.y;
+        }
         rasterize_bwd_tile<CDIM, TILE, ABS>(
             a, gid, render_alphas, render_T, last_ids, v_render_colors,
             v_render_alphas, v_means2d_abs, v_means2d, v_conics, v_colors,
-            v_opacities, sm);
+            v_opacities, sm, unit, rs.records);
         if (!queue)
             break;
     }
@@ -900,6 +1066,130 @@ int check_raster(const RasterArgs &a, int cdim) {
 
 using namespace gs;
 
+namespace {
+
+__global__ void replay_clear_kernel(uint32_t *count) { *count = 0u; }
+
+// Replay workspace: [count, padded to 256 B][units][records], each part
+// 256-byte aligned.
+struct ReplayLayout {
+    int64_t n_records, max_units;
+    size_t units_off, records_off, bytes;
+};
+
+ReplayLayout replay_layout(int64_t I, int32_t tile_width, int32_t tile_height,
+                           int32_t tile_size, int64_t n_isects, int32_t cdim) {
+    const int64_t bs = (int64_t)tile_size * tile_size;
+    const int64_t q = bs / kReplayParts;
+    ReplayLayout l;
+    l.n_records = q > 0 ? (n_isects + q - 1) / q : 0;
+    l.max_units = l.n_records + I * (int64_t)tile_width * tile_height;
+    auto up = [](size_t v) { return (v + 255) / 256 * 256; };
+    l.units_off = 256;
+    l.records_off = l.units_off + up((size_t)l.max_units * sizeof(int2));
+    l.bytes = l.records_off +
+              (size_t)l.n_records * (size_t)bs * (size_t)(1 + cdim) * sizeof(float);
+    return l;
+}
+
+int replay_state(void *ws, size_t ws_bytes, const RasterArgs &a, int cdim,
+                 ReplayState *rs) {
+    const ReplayLayout l = replay_layout(a.I, a.tile_width, a.tile_height,
+                                         a.tile_size, a.n_isects, cdim);
+    GS_REQUIRE(ws != nullptr, "rasterize replay: NULL replay workspace");
+    GS_REQUIRE(ws_bytes >= l.bytes,
+               "rasterize replay: workspace of " + std::to_string(ws_bytes) +
+                   " bytes, " + std::to_string(l.bytes) + " needed");
+    GS_REQUIRE(((uintptr_t)ws & 255u) == 0,
+               "rasterize replay: workspace must be 256-byte aligned");
+    char *base = static_cast<char *>(ws);
+    rs->count = reinterpret_cast<uint32_t *>(base);
+    rs->units = reinterpret_cast<int2 *>(base + l.units_off);
+    rs->records = reinterpret_cast<float *>(base + l.records_off);
+    return GSPLAT_OK;
+}
+
+int rasterize_fwd_impl(const RasterArgs &a, int32_t cdim, float *render_colors,
+                       float *render_alphas, int32_t *last_ids,
+                       float *render_transmittance, const ReplayState &rs,
+                       gsplat_stream_t stream) {
+    if (a.I == 0)
+        return GSPLAT_OK;
+    GS_REQUIRE(render_colors && render_alphas && last_ids,
+               "rasterize_fwd: NULL output");
+    const int64_t blocks = a.I * (int64_t)a.tile_width * a.tile_height;
+    GS_REQUIRE(blocks < (1ll << 31), "rasterize_fwd: too many tiles");
+    hipStream_t st = as_stream(stream);
+    if (rs.count != nullptr) {
+        replay_clear_kernel<<<1, 1, 0, st>>>(rs.count);
+        GS_TRY(check_launch("replay_clear_kernel"));
+    }
+#define GS_FWD(C, TILE)                                                        \
+    rasterize_fwd_kernel<C, TILE><<<(unsigned)blocks, TILE * TILE, 0, st>>>(   \
+        a, render_colors, render_alphas, last_ids, render_transmittance, rs)
+    if (a.tile_size == 16) {
+        GS_CDIM_SWITCH(cdim, GS_FWD, 16)
+    } else if (a.tile_size == 8) {
+        GS_CDIM_SWITCH(cdim, GS_FWD, 8)
+    } else {
+        GS_CDIM_SWITCH(cdim, GS_FWD, 4)
+    }
+#undef GS_FWD
+    return check_launch("rasterize_fwd_kernel");
+}
+
+int rasterize_bwd_impl(const RasterArgs &a, int32_t cdim,
+                       const float *render_alphas,
+                       const float *render_transmittance, const int32_t *last_ids,
+                       const float *v_render_colors, const float *v_render_alphas,
+                       float *v_means2d_abs, float *v_means2d, float *v_conics,
+                       float *v_colors, float *v_opacities, uint32_t *tile_counter,
+                       const ReplayState &rs, gsplat_stream_t stream) {
+    if (a.I == 0 || a.n_isects == 0)
+        return GSPLAT_OK;
+    GS_REQUIRE((render_alphas || render_transmittance) && last_ids &&
+                   v_render_colors,
+               "rasterize_bwd: NULL input");
+    GS_REQUIRE(v_means2d && v_conics && v_colors && v_opacities,
+               "rasterize_bwd: NULL gradient output");
+    const int64_t blocks = a.I * (int64_t)a.tile_width * a.tile_height;
+    GS_REQUIRE(blocks < (1ll << 31), "rasterize_bwd: too many tiles");
+    hipStream_t st = as_stream(stream);
+    // the replayed units are known on the device only: a resident grid takes
+    // them from the counter, sized for the most units there can be
+    const int64_t work = rs.units != nullptr
+                             ? replay_layout(a.I, a.tile_width, a.tile_height,
+                                             a.tile_size, a.n_isects, cdim).max_units
+                             : blocks;
+#define GS_BWD(C, TILE, ABS)                                                   \
+    {                                                                          \
+        auto kern = rasterize_bwd_kernel<C, TILE, ABS>;                        \
+        int64_t grid = work;                                                   \
+        if (tile_counter != nullptr)                                           \
+            GS_TRY(resident_grid((const void *)kern, BwdShape<TILE>::THREADS,  \
+                                 work, &grid));                                \
+        kern<<<(unsigned)grid, BwdShape<TILE>::THREADS, 0, st>>>(              \
+            a, render_alphas, render_transmittance, last_ids, v_render_colors, \
+            v_render_alphas, v_means2d_abs, v_means2d, v_conics, v_colors,     \
+            v_opacities, tile_counter, blocks, rs);                            \
+    }
+    const bool abs = v_means2d_abs != nullptr;
+    if (a.tile_size == 16) {
+        if (abs) { GS_CDIM_SWITCH(cdim, GS_BWD, 16, true) }
+        else { GS_CDIM_SWITCH(cdim, GS_BWD, 16, false) }
+    } else if (a.tile_size == 8) {
+        if (abs) { GS_CDIM_SWITCH(cdim, GS_BWD, 8, true) }
+        else { GS_CDIM_SWITCH(cdim, GS_BWD, 8, false) }
+    } else {
+        if (abs) { GS_CDIM_SWITCH(cdim, GS_BWD, 4, true) }
+        else { GS_CDIM_SWITCH(cdim, GS_BWD, 4, false) }
+    }
+#undef GS_BWD
+    return check_launch("rasterize_bwd_kernel");
+}
+
+}  // namespace
+
 extern "C" int gsplat_rasterize_fwd(
     int64_t I, int64_t n_rows, int64_t n_isects, int32_t cdim,
     const float *means2d, const float *conics, const float *colors,
@@ -913,25 +1203,40 @@ extern "C" int gsplat_rasterize_fwd(
                  backgrounds, masks, image_width, image_height, tile_size,
                  tile_width, tile_height, tile_offsets, flatten_ids};
     GS_TRY(check_raster(a, cdim));
-    if (I == 0)
-        return GSPLAT_OK;
-    GS_REQUIRE(render_colors && render_alphas && last_ids,
-               "rasterize_fwd: NULL output");
-    const int64_t blocks = I * (int64_t)tile_width * tile_height;
-    GS_REQUIRE(blocks < (1ll << 31), "rasterize_fwd: too many tiles");
-    hipStream_t st = as_stream(stream);
-#define GS_FWD(C, TILE)                                                        \
-    rasterize_fwd_kernel<C, TILE><<<(unsigned)blocks, TILE * TILE, 0, st>>>(   \
-        a, render_colors, render_alphas, last_ids, render_transmittance)
-    if (tile_size == 16) {
-        GS_CDIM_SWITCH(cdim, GS_FWD, 16)
-    } else if (tile_size == 8) {
-        GS_CDIM_SWITCH(cdim, GS_FWD, 8)
-    } else {
-        GS_CDIM_SWITCH(cdim, GS_FWD, 4)
-    }
-#undef GS_FWD
-    return check_launch("rasterize_fwd_kernel");
+    return rasterize_fwd_impl(a, cdim, render_colors, render_alphas, last_ids,
+                              render_transmittance, ReplayState{}, stream);
+}
+
+extern "C" size_t gsplat_rasterize_replay_size(int64_t I, int32_t tile_width,
+                                               int32_t tile_height,
+                                               int32_t tile_size,
+                                               int64_t n_isects, int32_t cdim) {
+    if (I < 0 || tile_width < 0 || tile_height < 0 || tile_size <= 0 ||
+        n_isects < 0 || cdim <= 0)
+        return 0;
+    return replay_layout(I, tile_width, tile_height, tile_size, n_isects, cdim).bytes;
+}
+
+extern "C" int gsplat_rasterize_fwd_replay(
+    int64_t I, int64_t n_rows, int64_t n_isects, int32_t cdim,
+    const float *means2d, const float *conics, const float *colors,
+    const float *opacities, const float *backgrounds, const uint8_t *masks,
+    int32_t image_width, int32_t image_height, int32_t tile_size,
+    int32_t tile_width, int32_t tile_height, const int32_t *tile_offsets,
+    const int32_t *flatten_ids, float *render_colors, float *render_alphas,
+    int32_t *last_ids, float *render_transmittance, void *replay,
+    size_t replay_bytes, gsplat_stream_t stream) {
+    clear_error();
+    RasterArgs a{I, n_rows, n_isects, means2d, conics, colors, opacities,
+                 backgrounds, masks, image_width, image_height, tile_size,
+                 tile_width, tile_height, tile_offsets, flatten_ids};
+    GS_TRY(check_raster(a, cdim));
+    GS_REQUIRE(render_transmittance != nullptr,
+               "rasterize_fwd_replay: NULL render_transmittance");
+    ReplayState rs{};
+    GS_TRY(replay_state(replay, replay_bytes, a, cdim, &rs));
+    return rasterize_fwd_impl(a, cdim, render_colors, render_alphas, last_ids,
+                              render_transmittance, rs, stream);
 }
 
 extern "C" int gsplat_rasterize_bwd(
@@ -951,41 +1256,40 @@ extern "C" int gsplat_rasterize_bwd(
                  backgrounds, masks, image_width, image_height, tile_size,
                  tile_width, tile_height, tile_offsets, flatten_ids};
     GS_TRY(check_raster(a, cdim));
-    if (I == 0 || n_isects == 0)
-        return GSPLAT_OK;
-    GS_REQUIRE((render_alphas || render_transmittance) && last_ids &&
-                   v_render_colors,
-               "rasterize_bwd: NULL input");
-    GS_REQUIRE(v_means2d && v_conics && v_colors && v_opacities,
-               "rasterize_bwd: NULL gradient output");
-    const int64_t blocks = I * (int64_t)tile_width * tile_height;
-    GS_REQUIRE(blocks < (1ll << 31), "rasterize_bwd: too many tiles");
-    hipStream_t st = as_stream(stream);
-#define GS_BWD(C, TILE, ABS)                                                   \
-    {                                                                          \
-        auto kern = rasterize_bwd_kernel<C, TILE, ABS>;                        \
-        int64_t grid = blocks;                                                 \
-        if (tile_counter != nullptr)                                           \
-            GS_TRY(resident_grid((const void *)kern, BwdShape<TILE>::THREADS,  \
-                                 blocks, &grid));                              \
-        kern<<<(unsigned)grid, BwdShape<TILE>::THREADS, 0, st>>>(              \
-            a, render_alphas, render_transmittance, last_ids, v_render_colors, \
-            v_render_alphas, v_means2d_abs, v_means2d, v_conics, v_colors,     \
-            v_opacities, tile_counter, blocks);                                \
-    }
-    const bool abs = v_means2d_abs != nullptr;
-    if (tile_size == 16) {
-        if (abs) { GS_CDIM_SWITCH(cdim, GS_BWD, 16, true) }
-        else { GS_CDIM_SWITCH(cdim, GS_BWD, 16, false) }
-    } else if (tile_size == 8) {
-        if (abs) { GS_CDIM_SWITCH(cdim, GS_BWD, 8, true) }
-        else { GS_CDIM_SWITCH(cdim, GS_BWD, 8, false) }
-    } else {
-        if (abs) { GS_CDIM_SWITCH(cdim, GS_BWD, 4, true) }
-        else { GS_CDIM_SWITCH(cdim, GS_BWD, 4, false) }
-    }
-#undef GS_BWD
-    return check_launch("rasterize_bwd_kernel");
+    return rasterize_bwd_impl(a, cdim, render_alphas, render_transmittance,
+                              last_ids, v_render_colors, v_render_alphas,
+                              v_means2d_abs, v_means2d, v_conics, v_colors,
+                              v_opacities, tile_counter, ReplayState{}, stream);
+}
+
+extern "C" int gsplat_rasterize_bwd_replay(
+    int64_t I, int64_t n_rows, int64_t n_isects, int32_t cdim,
+    const float *means2d, const float *conics, const float *colors,
+    const float *opacities, const float *backgrounds, const uint8_t *masks,
+    int32_t image_width, int32_t image_height, int32_t tile_size,
+    int32_t tile_width, int32_t tile_height, const int32_t *tile_offsets,
+    const int32_t *flatten_ids, const float *render_transmittance,
+    const int32_t *last_ids, const float *v_render_colors,
+    const float *v_render_alphas, float *v_means2d_abs, float *v_means2d,
+    float *v_conics, float *v_colors, float *v_opacities,
+    uint32_t *tile_counter, const void *replay, size_t replay_bytes,
+    gsplat_stream_t stream) {
+    clear_error();
+    RasterArgs a{I, n_rows, n_isects, means2d, conics, colors, opacities,
+                 backgrounds, masks, image_width, image_height, tile_size,
+                 tile_width, tile_height, tile_offsets, flatten_ids};
+    GS_TRY(check_raster(a, cdim));
+    GS_REQUIRE(render_transmittance != nullptr,
+               "rasterize_bwd_replay: NULL render_transmittance");
+    GS_REQUIRE(tile_counter != nullptr,
+               "rasterize_bwd_replay: NULL tile_counter (the units are taken "
+               "from it)");
+    ReplayState rs{};
+    GS_TRY(replay_state(const_cast<void *>(replay), replay_bytes, a, cdim, &rs));
+    return rasterize_bwd_impl(a, cdim, nullptr, render_transmittance, last_ids,
+                              v_render_colors, v_render_alphas, v_means2d_abs,
+                              v_means2d, v_conics, v_colors, v_opacities,
+                              tile_counter, rs, stream);
 }
 
 // Shared argument handling of the two indices entry points.  The op has no

@@ -875,6 +875,44 @@ def rasterize_fwd_with_transmittance(
     return renders, alphas, last_ids, transmittance
 
 
+def rasterize_fwd_replay(
+    means2d: Tensor,
+    conics: Tensor,
+    colors: Tensor,
+    opacities: Tensor,
+    backgrounds: Optional[Tensor],
+    masks: Optional[Tensor],
+    image_width: int,
+    image_height: int,
+    tile_size: int,
+    tile_offsets: Tensor,
+    flatten_ids: Tensor,
+) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """``rasterize_fwd_with_transmittance`` that also fills the replay state of
+    ``rasterize_bwd_replay`` (per-pixel records at every batch boundary of a
+    tile and the list of replay units); returns it as a fifth output."""
+    image_dims, I, n_rows, tw, th = _raster_common(
+        means2d, conics, colors, opacities, backgrounds, masks, tile_offsets,
+        flatten_ids)
+    channels = colors.shape[-1]
+    dev = means2d.device
+    H, W = int(image_height), int(image_width)
+    renders = torch.empty(image_dims + (H, W, channels), dtype=_F32, device=dev)
+    alphas = torch.empty(image_dims + (H, W, 1), dtype=_F32, device=dev)
+    last_ids = torch.empty(image_dims + (H, W), dtype=_I32, device=dev)
+    transmittance = torch.empty(image_dims + (H, W), dtype=_F32, device=dev)
+    n_isects = flatten_ids.numel()
+    replay = torch.empty(query("gsplat_rasterize_replay_size", I, tw, th, int(tile_size),
+                               n_isects, channels), dtype=torch.uint8, device=dev)
+    call("gsplat_rasterize_fwd_replay", I, n_rows, n_isects, channels,
+         ptr(means2d), ptr(conics), ptr(colors), ptr(opacities),
+         ptr(backgrounds), ptr(masks), W, H, int(tile_size), tw, th,
+         ptr(tile_offsets), ptr(flatten_ids), ptr(renders), ptr(alphas),
+         ptr(last_ids), ptr(transmittance), ptr(replay), replay.numel(),
+         _stream(means2d))
+    return renders, alphas, last_ids, transmittance, replay
+
+
 def rasterize_to_pixels_3dgs_fwd(
     means2d: Tensor,
     conics: Tensor,
@@ -955,6 +993,55 @@ def rasterize_to_pixels_3dgs_bwd(
          ptr(v_render_alphas), ptr(v_means2d_abs), ptr(v_means2d),
          ptr(v_conics), ptr(v_colors), ptr(v_opacities), ptr(tile_counter),
          _stream(means2d))
+    return v_means2d_abs, v_means2d, v_conics, v_colors, v_opacities
+
+
+def rasterize_bwd_replay(
+    means2d: Tensor,
+    conics: Tensor,
+    colors: Tensor,
+    opacities: Tensor,
+    backgrounds: Optional[Tensor],
+    masks: Optional[Tensor],
+    image_width: int,
+    image_height: int,
+    tile_size: int,
+    tile_offsets: Tensor,
+    flatten_ids: Tensor,
+    render_transmittance: Tensor,
+    last_ids: Tensor,
+    replay: Tensor,
+    v_render_colors: Tensor,
+    v_render_alphas: Optional[Tensor],
+    absgrad: bool,
+):
+    """``rasterize_to_pixels_3dgs_bwd`` from the state of
+    ``rasterize_fwd_replay`` on the same inputs: the replay runs one unit per
+    forward batch instead of one per tile."""
+    image_dims, I, n_rows, tw, th = _raster_common(
+        means2d, conics, colors, opacities, backgrounds, masks, tile_offsets,
+        flatten_ids)
+    check_input(render_transmittance, "render_transmittance", _F32)
+    check_input(last_ids, "last_ids", _I32)
+    check_input(replay, "replay", torch.uint8)
+    check_input(v_render_colors, "v_render_colors", _F32)
+    check_input(v_render_alphas, "v_render_alphas", _F32)
+    channels = colors.shape[-1]
+    likes = [means2d, conics, colors, opacities] + ([means2d] if absgrad else [])
+    sizes = [t.numel() for t in likes] + [1]
+    parts = torch.zeros(sum(sizes), dtype=_F32, device=means2d.device).split(sizes)
+    v_means2d, v_conics, v_colors, v_opacities = (
+        parts[k].view(likes[k].shape) for k in range(4))
+    v_means2d_abs = parts[4].view(means2d.shape) if absgrad else None
+    tile_counter = parts[-1]
+    call("gsplat_rasterize_bwd_replay", I, n_rows, flatten_ids.numel(), channels,
+         ptr(means2d), ptr(conics), ptr(colors), ptr(opacities),
+         ptr(backgrounds), ptr(masks), int(image_width), int(image_height),
+         int(tile_size), tw, th, ptr(tile_offsets), ptr(flatten_ids),
+         ptr(render_transmittance), ptr(last_ids), ptr(v_render_colors),
+         ptr(v_render_alphas), ptr(v_means2d_abs), ptr(v_means2d),
+         ptr(v_conics), ptr(v_colors), ptr(v_opacities), ptr(tile_counter),
+         ptr(replay), replay.numel(), _stream(means2d))
     return v_means2d_abs, v_means2d, v_conics, v_colors, v_opacities
 
 

@@ -861,13 +861,23 @@ class _RasterizeToPixels(torch.autograd.Function):
     @staticmethod
     def forward(ctx, means2d, conics, colors, opacities, backgrounds, masks,
                 width, height, tile_size, isect_offsets, flatten_ids, absgrad):
-        render_colors, render_alphas, last_ids, render_T = \
-            _ops.rasterize_fwd_with_transmittance(
-                means2d, conics, colors, opacities, backgrounds, masks, width,
-                height, tile_size, isect_offsets, flatten_ids)
+        # With gradients ahead the forward also keeps the replay state, so
+        # the backward runs one unit per forward batch instead of one per
+        # tile (the reference replays whole tiles).
+        if any(ctx.needs_input_grad[:5]):
+            render_colors, render_alphas, last_ids, render_T, replay = \
+                _ops.rasterize_fwd_replay(
+                    means2d, conics, colors, opacities, backgrounds, masks,
+                    width, height, tile_size, isect_offsets, flatten_ids)
+        else:
+            render_colors, render_alphas, last_ids, render_T = \
+                _ops.rasterize_fwd_with_transmittance(
+                    means2d, conics, colors, opacities, backgrounds, masks,
+                    width, height, tile_size, isect_offsets, flatten_ids)
+            replay = None
         ctx.save_for_backward(means2d, conics, colors, opacities, backgrounds,
                               masks, isect_offsets, flatten_ids, render_T,
-                              last_ids)
+                              last_ids, replay)
         ctx.width = width
         ctx.height = height
         ctx.tile_size = tile_size
@@ -880,20 +890,28 @@ class _RasterizeToPixels(torch.autograd.Function):
     def backward(ctx, v_render_colors: Optional[Tensor],
                  v_render_alphas: Optional[Tensor]):
         (means2d, conics, colors, opacities, backgrounds, masks, isect_offsets,
-         flatten_ids, render_T, last_ids) = ctx.saved_tensors
+         flatten_ids, render_T, last_ids, replay) = ctx.saved_tensors
         if v_render_colors is None and v_render_alphas is None:
             return (None,) * 12
         if v_render_colors is None:
             v_render_colors = render_T.new_zeros((*render_T.shape, colors.shape[-1]))
-        # render_alphas = 1 - T is only needed when T is absent; pass T's
-        # storage as the (unused) alphas argument to satisfy the op's checks.
-        (v_means2d_abs, v_means2d, v_conics, v_colors,
-         v_opacities) = _ops.rasterize_to_pixels_3dgs_bwd(
-            means2d, conics, colors, opacities, backgrounds, masks, ctx.width,
-            ctx.height, ctx.tile_size, isect_offsets, flatten_ids,
-            render_T, last_ids, v_render_colors.contiguous(),
-            None if v_render_alphas is None else v_render_alphas.contiguous(),
-            ctx.absgrad, render_transmittance=render_T)
+        v_alphas = None if v_render_alphas is None else v_render_alphas.contiguous()
+        if replay is not None:
+            (v_means2d_abs, v_means2d, v_conics, v_colors,
+             v_opacities) = _ops.rasterize_bwd_replay(
+                means2d, conics, colors, opacities, backgrounds, masks, ctx.width,
+                ctx.height, ctx.tile_size, isect_offsets, flatten_ids,
+                render_T, last_ids, replay, v_render_colors.contiguous(), v_alphas,
+                ctx.absgrad)
+        else:
+            # render_alphas = 1 - T is only read when T is absent; T's storage
+            # stands in for it to satisfy the op's checks
+            (v_means2d_abs, v_means2d, v_conics, v_colors,
+             v_opacities) = _ops.rasterize_to_pixels_3dgs_bwd(
+                means2d, conics, colors, opacities, backgrounds, masks, ctx.width,
+                ctx.height, ctx.tile_size, isect_offsets, flatten_ids,
+                render_T, last_ids, v_render_colors.contiguous(), v_alphas,
+                ctx.absgrad, render_transmittance=render_T)
         if ctx.absgrad:
             prev = getattr(means2d, "absgrad", None)
             if prev is not None and getattr(means2d, "_absgrad_pass", None) is \

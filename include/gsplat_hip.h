@@ -594,6 +594,55 @@ int gsplat_rasterize_bwd(
     float *v_colors, float *v_opacities, uint32_t *tile_counter,
     gsplat_stream_t stream);
 
+/* Replay state for a backward that runs one unit per forward batch instead
+ * of one per tile.  Pair of gsplat_rasterize_fwd / gsplat_rasterize_bwd: the
+ * reference runs rasterize_to_pixels_3dgs_fwd then _bwd
+ * (gsplat/cuda/_wrapper.py:1709-1836) with the backward replaying each tile
+ * back to front from its end; these two keep that arithmetic but split each
+ * tile's replay at the forward's batch boundaries (tile_size^2 consecutive
+ * intersections of the tile), so the parts of one tile run in parallel.
+ *
+ * gsplat_rasterize_replay_size: bytes of the replay workspace (256-byte
+ *   aligned) for these sizes; 0 for invalid sizes.  It holds, per batch
+ *   boundary of every tile, each pixel's transmittance there and the colour
+ *   the next batch composited (4 * (1 + CDIM) bytes per pixel per
+ *   boundary), and the list of (tile, batch) units up to each tile's last
+ *   contributor.
+ * gsplat_rasterize_fwd_replay: gsplat_rasterize_fwd (render_transmittance
+ *   required) that also fills the replay workspace.
+ * gsplat_rasterize_bwd_replay: gsplat_rasterize_bwd with
+ *   render_transmittance, tile_counter and the replay workspace of the
+ *   forward call on the same inputs all required (render_alphas is not
+ *   needed).  The gradients agree with gsplat_rasterize_bwd's to float32
+ *   summation order. */
+size_t gsplat_rasterize_replay_size(
+    int64_t I, int32_t tile_width, int32_t tile_height, int32_t tile_size,
+    int64_t n_isects, int32_t cdim);
+
+int gsplat_rasterize_fwd_replay(
+    int64_t I, int64_t n_rows, int64_t n_isects, int32_t cdim,
+    const float *means2d, const float *conics, const float *colors,
+    const float *opacities, const float *backgrounds, const uint8_t *masks,
+    int32_t image_width, int32_t image_height, int32_t tile_size,
+    int32_t tile_width, int32_t tile_height,
+    const int32_t *tile_offsets, const int32_t *flatten_ids,
+    float *render_colors, float *render_alphas, int32_t *last_ids,
+    float *render_transmittance, void *replay, size_t replay_bytes,
+    gsplat_stream_t stream);
+
+int gsplat_rasterize_bwd_replay(
+    int64_t I, int64_t n_rows, int64_t n_isects, int32_t cdim,
+    const float *means2d, const float *conics, const float *colors,
+    const float *opacities, const float *backgrounds, const uint8_t *masks,
+    int32_t image_width, int32_t image_height, int32_t tile_size,
+    int32_t tile_width, int32_t tile_height,
+    const int32_t *tile_offsets, const int32_t *flatten_ids,
+    const float *render_transmittance, const int32_t *last_ids,
+    const float *v_render_colors, const float *v_render_alphas,
+    float *v_means2d_abs, float *v_means2d, float *v_conics,
+    float *v_colors, float *v_opacities, uint32_t *tile_counter,
+    const void *replay, size_t replay_bytes, gsplat_stream_t stream);
+
 /* Rasterize to indices: the (Gaussian, pixel) pairs each pixel composites
  * over the isect batches [range_start, range_end) of its tile (batches of
  * tile_size^2, front to back), starting from the pixel's transmittance

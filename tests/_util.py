@@ -26,10 +26,12 @@ def small_scene(seed=0, N=2000, C=2, W=160, H=120, f=150.0, opac_range=(0.05, 1.
     return means, quats, scales, opac, vm, K, W, H
 
 
-def projected_2d(seed=0, N=2000, C=2, W=160, H=120, tile=16, D=3, packed=False):
+def projected_2d(seed=0, N=2000, C=2, W=160, H=120, tile=16, D=3, packed=False,
+                 **scene_kw):
     """Exact-oracle projection + intersection of a random scene: the float32
-    inputs of the rasterizer and its tile lists (numpy/torch CPU)."""
-    means, quats, scales, opac, vm, K, W, H = small_scene(seed, N, C, W, H)
+    inputs of the rasterizer and its tile lists (numpy/torch CPU).
+    ``scene_kw`` goes to small_scene (opacity and scale ranges, spread)."""
+    means, quats, scales, opac, vm, K, W, H = small_scene(seed, N, C, W, H, **scene_kw)
     ex = exact.projection_fwd(means.numpy(), None, quats.numpy(), scales.numpy(),
                               opac.numpy(), vm.numpy(), K.numpy(), W, H)
     g = torch.Generator().manual_seed(seed + 1)

@@ -39,7 +39,9 @@ def test_header_declares_the_survey_export_list():
                      "gsplat_adam", "gsplat_quat_scale_to_covar_preci_fwd",
                      "gsplat_quat_scale_to_covar_preci_bwd",
                      "gsplat_rasterize_to_indices_count",
-                     "gsplat_rasterize_to_indices_write", "gsplat_isect_emit_sorted_dev"]:
+                     "gsplat_rasterize_to_indices_write", "gsplat_isect_emit_sorted_dev",
+                     "gsplat_rasterize_replay_size", "gsplat_rasterize_fwd_replay",
+                     "gsplat_rasterize_bwd_replay"]:
         assert required in names, required
 
 
@@ -76,6 +78,31 @@ def test_argument_errors_are_reported_without_a_gpu(lib_path):
     with pytest.raises(RuntimeError, match="exceed the static scratch"):
         _lib.call("gsplat_projection_packed_fwd_noalloc", 1, 1, limit + 1, 8, None, 8, 8,
                   None, 8, 8, 16, 16, 0.3, 0.01, 1e10, 0.0, 0, *fake, None, None, None)
+
+
+def test_replay_workspace_size_and_checks_without_a_gpu(lib_path):
+    """The replay workspace: 256 B of count, the unit list (records + tiles
+    entries of 8 B, padded to 256 B), then ceil(n_isects / Q) records of
+    tile_size^2 pixels x (1 + CDIM) floats, Q = tile_size^2 / 4; a short or
+    missing workspace is refused before the device is touched (the fake
+    pointers are never read)."""
+    from gsplat_amd import _lib
+    q, n_isects, cdim, tiles = 64, 1000, 3, 6
+    n_rec = -(-n_isects // q)
+    units = -(-(n_rec + tiles) * 8 // 256) * 256
+    want = 256 + units + n_rec * 256 * (1 + cdim) * 4
+    assert _lib.query("gsplat_rasterize_replay_size", 1, 3, 2, 16, n_isects, cdim) == want
+    assert _lib.query("gsplat_rasterize_replay_size", 1, 3, 2, 16, -1, cdim) == 0
+    f = 256  # a fake, aligned device address
+    args = [1, 50, n_isects, cdim, f, f, f, f, None, None, 40, 30, 16, 3, 2, f, f]
+    with pytest.raises(RuntimeError, match="workspace"):
+        _lib.call("gsplat_rasterize_bwd_replay", *args, f, f, f, None, None, f, f, f, f,
+                  f, f, want - 1, None)
+    with pytest.raises(RuntimeError, match="NULL replay"):
+        _lib.call("gsplat_rasterize_fwd_replay", *args, f, f, f, f, None, want, None)
+    with pytest.raises(RuntimeError, match="tile_counter"):
+        _lib.call("gsplat_rasterize_bwd_replay", *args, f, f, f, None, None, f, f, f, f,
+                  None, f, want, None)
 
 
 def test_reference_op_schemas_registered():

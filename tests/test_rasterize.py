@@ -220,3 +220,80 @@ def test_reference_schema_fwd_bwd_without_transmittance():
     assert bool((v_abs + 1e-6 >= v_m2.abs()).all())
     # the scaling matters: pixels near the 1e-4 cutoff carry few bits of T'
     assert float((s - 1).abs().max()) > 1e-5
+
+
+def _direct_grads(data, D, bg, mk, v_rc, v_ra, replay):
+    """Gradients through the C-ABI ops directly: the forward with its saved
+    transmittance, then either the per-batch replay (rasterize_bwd_replay,
+    what rasterization() runs) or the whole-tile replay from T."""
+    from gsplat_amd.cuda import _ops
+    W, H, ts = data["W"], data["H"], data["tile"]
+    ins = [data[k].to(DEV) for k in ("means2d", "conics", "colors", "opacities")]
+    bgd = bg.to(DEV) if bg is not None else None
+    mkd = mk.to(DEV) if mk is not None else None
+    offs, fl = data["offsets"].to(DEV), data["flatten_ids"].to(DEV)
+    if replay:
+        rc, ra, last, T, state = _ops.rasterize_fwd_replay(
+            *ins, bgd, mkd, W, H, ts, offs, fl)
+        grads = _ops.rasterize_bwd_replay(
+            *ins, bgd, mkd, W, H, ts, offs, fl, T, last, state, v_rc.to(DEV),
+            v_ra.to(DEV), False)
+        n_units = int(state[:4].cpu().view(torch.int32)[0])
+    else:
+        rc, ra, last, T = _ops.rasterize_fwd_with_transmittance(
+            *ins, bgd, mkd, W, H, ts, offs, fl)
+        grads = _ops.rasterize_to_pixels_3dgs_bwd(
+            *ins, bgd, mkd, W, H, ts, offs, fl, ra, last, v_rc.to(DEV),
+            v_ra.to(DEV), False, render_transmittance=T)
+        n_units = None
+    torch.cuda.synchronize()
+    return rc, ra, grads[1:], n_units
+
+
+@pytest.mark.parametrize("D,tile", [(3, 16), (3, 8), (4, 16), (32, 16)])
+def test_replay_units_match_oracle_on_deep_tiles(D, tile):
+    """Deep tiles (many faint, large Gaussians: several forward batches per
+    tile and pixels that stay unsaturated) through the per-batch units that
+    start from the forward's records, held to the oracle's gradients; the
+    units must really split tiles (more units than tiles).
+
+    The whole-tile replay from the final T runs too, for the renders only: on
+    such tiles it recovers each T by dividing the final float32 T back over
+    hundreds of Gaussians, which cannot undo the forward's float32 roundings
+    of the steps behind, and its conic gradients drift past the float32
+    restatement's (3.2x its worst element at tile 8).  The units restart
+    from the forward's own T at every batch boundary."""
+    data = projected_2d(seed=70 + D + tile, N=3000, C=1, W=96, H=64, tile=tile, D=D,
+                        opac_range=(0.02, 0.2), scale_range=(0.05, 0.3), spread=0.8)
+    W, H, ts, C = data["W"], data["H"], data["tile"], data["C"]
+    g = torch.Generator().manual_seed(5)
+    bg = torch.rand(C, D, generator=g)
+    mk = torch.rand(data["offsets"].shape, generator=g) > 0.15
+    v_rc = torch.randn(C, H, W, D, generator=g)
+    v_ra = torch.randn(C, H, W, 1, generator=g)
+    m2, con, col, op = (data[k] for k in ("means2d", "conics", "colors", "opacities"))
+    ins_ref = [t.double().requires_grad_() for t in (m2, con, col, op)]
+    rc_r, ra_r, info = torch_ref.rasterize_to_pixels_ref(
+        *ins_ref, W, H, ts, data["offsets"], data["flatten_ids"],
+        backgrounds=bg.double(), masks=mk)
+    ((rc_r * v_rc.double()).sum() + (ra_r * v_ra.double()).sum()).backward()
+    ins32 = [t.float().clone().requires_grad_() for t in (m2, con, col, op)]
+    rc32, ra32, _ = torch_ref.rasterize_to_pixels_ref(
+        *ins32, W, H, ts, data["offsets"], data["flatten_ids"],
+        backgrounds=bg.float(), masks=mk, dtype=torch.float32)
+    ((rc32 * v_rc).sum() + (ra32 * v_ra).sum()).backward()
+    alpha32 = (np.float32(1.0) - info["transmittance"]).astype(np.float32)
+    n_tiles = int(mk.sum())
+    per_tile = np.diff(np.append(data["offsets"].numpy().ravel(),
+                                 data["flatten_ids"].numel()))
+    assert per_tile.max() > 3 * tile * tile, "scene too shallow for several batches"
+    for replay in (True, False):
+        rc, ra, grads, n_units = _direct_grads(data, D, bg, mk, v_rc, v_ra, replay)
+        np.testing.assert_array_equal(ra.cpu().numpy()[..., 0], alpha32)
+        assert_close(rc.cpu(), rc_r.detach(), RTOL, ATOL, "render_colors")
+        if not replay:
+            continue
+        assert n_units > n_tiles, (n_units, n_tiles)
+        for name, a, b, b32 in zip(("v_means2d", "v_conics", "v_colors", "v_opacities"),
+                                   grads, ins_ref, ins32):
+            assert_grad_close(a, b.grad, b32.grad, RTOL, ATOL, name)
