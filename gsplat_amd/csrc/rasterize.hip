@@ -525,7 +525,8 @@ __device__ __forceinline__ void rasterize_bwd_tile(
     float *__restrict__ v_means2d_abs, float *__restrict__ v_means2d,
     float *__restrict__ v_conics, float *__restrict__ v_colors,
     float *__restrict__ v_opacities, BwdSmem<CDIM, TILE, ABS> &sm,
-    int32_t unit, const float *__restrict__ records) {
+    int32_t unit, const float *__restrict__ records,
+    uint32_t *__restrict__ queue_counter, uint32_t &queue_next) {
     using SH = BwdShape<TILE>;
     constexpr int NB = SH::BATCH;
     constexpr int PX = SH::PX;
@@ -707,6 +708,11 @@ __device__ __forceinline__ void rasterize_bwd_tile(
                 s_acc[slot * NACC + k] = 0.f;
         }
         __syncthreads();
+        // The next queue entry is taken here, by one thread, and read only
+        // after this unit: the atomic's latency (long while many workgroups
+        // take entries at once) passes behind the work below.
+        if (b == 0 && queue_counter != nullptr && tr == 0)
+            queue_next = atomicAdd(queue_counter, 1u);
 
         // this wave's work list, in slot order: Gaussians in front of the
         // wave's last contributor (slots t with isect index batch_end - t >
@@ -883,17 +889,9 @@ __global__ void __launch_bounds__(BwdShape<TILE>::THREADS) rasterize_bwd_kernel(
     // with replay state the queue hands out the forward's units, otherwise
     // whole tiles
     const int64_t n_work = rs.units != nullptr ? (int64_t)*rs.count : n_tiles_total;
+    // entry k = blockIdx.x first, then gridDim.x + the counter's values
     int64_t k = blockIdx.x;
-    while (true) {
-        if (queue) {
-            __syncthreads();  // the previous unit is finished with the LDS
-            if (threadIdx.x == 0)
-                sm.next_tile = atomicAdd(tile_counter, 1u);
-            __syncthreads();
-            k = sm.next_tile;
-        }
-        if (k >= n_work)
-            break;
+    while (k < n_work) {
         int64_t gid = k;
         int32_t unit = -1;
         if (rs.units != nullptr) {
@@ -901,12 +899,22 @@ __global__ void __launch_bounds__(BwdShape<TILE>::THREADS) rasterize_bwd_kernel(
             gid = e.x;
             unit = e.y;
         }
+        uint32_t next = 0xffffffffu;  // thread 0's next entry, once taken
         rasterize_bwd_tile<CDIM, TILE, ABS>(
             a, gid, render_alphas, render_T, last_ids, v_render_colors,
             v_render_alphas, v_means2d_abs, v_means2d, v_conics, v_colors,
-            v_opacities, sm, unit, rs.records);
+            v_opacities, sm, unit, rs.records, queue ? tile_counter : nullptr,
+            next);
         if (!queue)
             break;
+        __syncthreads();  // the unit is finished with the LDS
+        if (threadIdx.x == 0) {
+            if (next == 0xffffffffu)  // the unit ended before taking one
+                next = atomicAdd(tile_counter, 1u);
+            sm.next_tile = (int64_t)gridDim.x + next;
+        }
+        __syncthreads();
+        k = sm.next_tile;
     }
 }
 
