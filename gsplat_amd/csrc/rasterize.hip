@@ -489,11 +489,9 @@ template <int TILE> struct BwdShape {
     static constexpr int BS = TILE * TILE;       // pixels of a tile
     static constexpr int PX = TILE == 16 ? 2 : 1;
     static constexpr int THREADS = BS / PX;
-    // Gaussians staged per batch (PX per thread).  Half as many would halve
-    // the LDS per workgroup (about 90 B per staged Gaussian) and allow more
-    // resident waves, but measured slower: the per-batch staging and
-    // barriers then cost more than the latency the extra waves hide.
-    static constexpr int BATCH = BS;
+    // Gaussians staged per batch: one replay part of the forward (a quarter
+    // of its batch), so a replay unit is one batch
+    static constexpr int BATCH = BS / kReplayParts;
     static constexpr int ROWS = THREADS >= 64 ? 4 : THREADS / 16;
     static constexpr int LAST = 16 * ROWS - 1;   // lane holding a wave sum
     static_assert(THREADS % 16 == 0, "whole 16-lane rows");
@@ -508,7 +506,7 @@ template <int CDIM, int TILE, bool ABS> struct BwdSmem {
     float4 geo[NB];
     float4 con[NB];
     float col[NB * CDIM];
-    float acc[NACC * NB];
+    float acc[NW][NACC * NB];  // per-wave sums (each wave writes its own)
     int32_t gid[NB];
     uint8_t wmask[NB];        // waves a Gaussian can reach
     uint8_t list[NW][NB];     // per-wave work list (slots < 256)
@@ -531,14 +529,14 @@ __device__ __forceinline__ void rasterize_bwd_tile(
     constexpr int NB = SH::BATCH;
     constexpr int PX = SH::PX;
     constexpr int NT = SH::THREADS;
-    constexpr int SLOTS = NB / NT;  // staged Gaussians per thread
+    constexpr int SLOTS = NB > NT ? NB / NT : 1;  // staged Gaussians per thread
     // per-Gaussian sums: xy(2), conic(3), colour(CDIM), opacity(1) [, |xy|(2)]
     constexpr int NACC = 2 + 3 + CDIM + 1 + (ABS ? 2 : 0);
     constexpr int NW = (NT + kWave - 1) / kWave;  // waves per tile
     float4 *s_geo = sm.geo;
     float4 *s_con = sm.con;
     float *s_col = sm.col;
-    float *s_acc = sm.acc;
+    auto &s_acc = sm.acc;
     int32_t *s_gid = sm.gid;
     uint8_t *s_wmask = sm.wmask;
     auto &s_list = sm.list;
@@ -630,7 +628,8 @@ __device__ __forceinline__ void rasterize_bwd_tile(
         first_end = replay_end - 1;
         lo = range_start;
     } else {
-        constexpr int Q = NB / kReplayParts;
+        constexpr int Q = NB;  // a replay part is one batch
+        static_assert(NB * kReplayParts == SH::BS, "part size");
         const int nu = max(0, replay_end - range_start + Q - 1) / Q;
         if (unit >= nu)
             return;
@@ -641,7 +640,7 @@ __device__ __forceinline__ void rasterize_bwd_tile(
             // A pixel whose last contributor lies before part m was done
             // before m: the forward kept no record for it there, its T at m is
             // the final one and m composited nothing on it.
-            constexpr int RS = (1 + CDIM) * NB;  // floats per record
+            constexpr int RS = (1 + CDIM) * SH::BS;  // floats per record
 #pragma unroll
             for (int p = 0; p < PX; ++p) {
                 const int lp = (PX * (tr / TILE) + p) * TILE + tr % TILE;
@@ -655,7 +654,7 @@ __device__ __forceinline__ void rasterize_bwd_tile(
                     }
 #pragma unroll
                     for (int k = 0; k < CDIM; ++k)
-                        bv += (double)r[(1 + k) * NB + lp] * (double)v_c[p][k];
+                        bv += (double)r[(1 + k) * SH::BS + lp] * (double)v_c[p][k];
                 }
                 Bv[p] = bv;
             }
@@ -680,6 +679,8 @@ __device__ __forceinline__ void rasterize_bwd_tile(
 #pragma unroll
         for (int q = 0; q < SLOTS; ++q) {
             const int slot = tr + q * NT;
+            if (slot >= NB)
+                break;
             const int32_t idx = batch_end - slot;
             if (idx >= lo) {
                 const int32_t g = a.flatten_ids[idx];
@@ -704,8 +705,10 @@ __device__ __forceinline__ void rasterize_bwd_tile(
                 s_wmask[slot] = 0;
             }
 #pragma unroll
-            for (int k = 0; k < NACC; ++k)
-                s_acc[slot * NACC + k] = 0.f;
+            for (int w = 0; w < NW; ++w)
+#pragma unroll
+                for (int k = 0; k < NACC; ++k)
+                    s_acc[w][slot * NACC + k] = 0.f;
         }
         __syncthreads();
         // The next queue entry is taken here, by one thread, and read only
@@ -826,14 +829,25 @@ __device__ __forceinline__ void rasterize_bwd_tile(
                 gv[6 + CDIM] = ax;
                 gv[7 + CDIM] = ay;
             }
-            // sums over each 16-lane row, one value per lane, added to the
-            // tile's LDS sums (rows of a wave add to the same slots)
+            // sums over each 16-lane row, one value per lane; then the four
+            // rows summed by two cross-row swaps (lanes l and l ^ 32, then
+            // rows 2r and 2r + 1), and the wave's sums stored by the first
+            // row into the wave's own slots: no LDS atomics
             float red[RR::N4];
             row_reduce<NACC>(gv, red);
 #pragma unroll
-            for (int f = 0; f < RR::N4; ++f)
-                if (red_slot[f] >= 0)
-                    atomicAdd(&s_acc[t * NACC + red_slot[f]], red[f]);
+            for (int f = 0; f < RR::N4; ++f) {
+                if constexpr (SH::ROWS == 4) {
+                    const uint32_t u = __float_as_uint(red[f]);
+                    const auto h = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+                    const float s2 = __uint_as_float(h[0]) + __uint_as_float(h[1]);
+                    const uint32_t u2 = __float_as_uint(s2);
+                    const auto r = __builtin_amdgcn_permlane16_swap(u2, u2, false, false);
+                    red[f] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+                }
+                if (lane_id() < 16u && red_slot[f] >= 0)
+                    s_acc[wave][t * NACC + red_slot[f]] = red[f];
+            }
         }
         __syncthreads();
 #pragma unroll
@@ -845,8 +859,12 @@ __device__ __forceinline__ void rasterize_bwd_tile(
                 const int32_t g = s_gid[slot];
                 float acc[NACC];
 #pragma unroll
-                for (int k = 0; k < NACC; ++k)
-                    acc[k] = s_acc[slot * NACC + k];
+                for (int k = 0; k < NACC; ++k) {
+                    acc[k] = s_acc[0][slot * NACC + k];
+#pragma unroll
+                    for (int w = 1; w < NW; ++w)
+                        acc[k] += s_acc[w][slot * NACC + k];
+                }
                 auto add = [](float *p, float v) {
                     if (v != 0.f)
                         atomic_add_f32(p, v);
