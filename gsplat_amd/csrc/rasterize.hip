@@ -850,39 +850,32 @@ __device__ __forceinline__ void rasterize_bwd_tile(
             }
         }
         __syncthreads();
+        // Flush: the batch's (slot, sum) pairs spread over all threads, one
+        // global atomic each, the two waves' sums added first.  A sum that
+        // is zero (a Gaussian no pixel took, or a term that vanished) adds
+        // nothing and is skipped.
+        for (int e = tr; e < batch_size * NACC; e += NT) {
+            const int slot = e / NACC;
+            const int k = e - slot * NACC;
+            float v = s_acc[0][e];
 #pragma unroll
-        for (int q = 0; q < SLOTS; ++q) {
-            const int slot = tr + q * NT;
-            // a sum that is zero (a Gaussian no pixel took, or a term that
-            // vanished) adds nothing and is skipped
-            if (slot < batch_size) {
-                const int32_t g = s_gid[slot];
-                float acc[NACC];
-#pragma unroll
-                for (int k = 0; k < NACC; ++k) {
-                    acc[k] = s_acc[0][slot * NACC + k];
-#pragma unroll
-                    for (int w = 1; w < NW; ++w)
-                        acc[k] += s_acc[w][slot * NACC + k];
-                }
-                auto add = [](float *p, float v) {
-                    if (v != 0.f)
-                        atomic_add_f32(p, v);
-                };
-                add(v_means2d + (int64_t)g * 2 + 0, acc[0]);
-                add(v_means2d + (int64_t)g * 2 + 1, acc[1]);
-                add(v_conics + (int64_t)g * 3 + 0, acc[2]);
-                add(v_conics + (int64_t)g * 3 + 1, acc[3]);
-                add(v_conics + (int64_t)g * 3 + 2, acc[4]);
-#pragma unroll
-                for (int k = 0; k < CDIM; ++k)
-                    add(v_colors + (int64_t)g * CDIM + k, acc[5 + k]);
-                add(v_opacities + g, acc[5 + CDIM]);
-                if constexpr (ABS) {
-                    add(v_means2d_abs + (int64_t)g * 2 + 0, acc[6 + CDIM]);
-                    add(v_means2d_abs + (int64_t)g * 2 + 1, acc[7 + CDIM]);
-                }
-            }
+            for (int w = 1; w < NW; ++w)
+                v += s_acc[w][e];
+            if (v == 0.f)
+                continue;
+            const int64_t g = s_gid[slot];
+            float *dst;
+            if (k < 2)
+                dst = v_means2d + g * 2 + k;
+            else if (k < 5)
+                dst = v_conics + g * 3 + (k - 2);
+            else if (k < 5 + CDIM)
+                dst = v_colors + g * CDIM + (k - 5);
+            else if (k == 5 + CDIM)
+                dst = v_opacities + g;
+            else
+                dst = v_means2d_abs + g * 2 + (k - 6 - CDIM);
+            atomic_add_f32(dst, v);
         }
     }
 }
