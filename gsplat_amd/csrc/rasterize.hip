@@ -56,7 +56,8 @@ struct RasterArgs {
 //            never meet and ceil(n_isects / Q) slots cover every tile;
 //   units    (tile, part) pairs of every part up to the tile's last
 //            contributor, appended per tile by the forward;
-//   count    the number of units (zeroed before the forward).
+//   count    the number of units (zeroed before the forward);
+//   tile_last per tile with units: the isect index of its last contributor.
 // A unit's backward starts from its end boundary's record instead of
 // replaying every part behind it, so the units of one tile run side by side
 // and no workgroup holds a long tile at the end of the launch.
@@ -64,6 +65,7 @@ struct ReplayState {
     uint32_t *count;
     int2 *units;
     float *records;
+    int32_t *tile_last;  // per tile: its last contributor's isect index, or -1
 };
 
 // Replay parts per forward batch: a part is BS / kReplayParts consecutive
@@ -390,6 +392,7 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
             atomicMax(&s_last, cur_idx);
         __syncthreads();
         if (tr == 0 && s_last >= range_start) {
+            rs.tile_last[blockIdx.x] = s_last;
             const int nu = (s_last - range_start) / Q + 1;
             const uint32_t base = atomicAdd(rs.count, (uint32_t)nu);
             for (int u = 0; u < nu; ++u)
@@ -524,6 +527,7 @@ __device__ __forceinline__ void rasterize_bwd_tile(
     float *__restrict__ v_conics, float *__restrict__ v_colors,
     float *__restrict__ v_opacities, BwdSmem<CDIM, TILE, ABS> &sm,
     int32_t unit, const float *__restrict__ records,
+    const int32_t *__restrict__ tile_last,
     uint32_t *__restrict__ queue_counter, uint32_t &queue_next) {
     using SH = BwdShape<TILE>;
     constexpr int NB = SH::BATCH;
@@ -556,8 +560,24 @@ __device__ __forceinline__ void rasterize_bwd_tile(
     const int32_t range_end = (image == a.I - 1 && tile == n_tiles - 1)
                                   ? (int32_t)a.n_isects
                                   : offs[tile + 1];
-    if (tr == 0)
+    // One unit: its replay range is known from the forward's tile_last, so
+    // its rows are loaded now, beside the pixel state below.
+    int32_t unit_end = 0;
+    constexpr int SLOTS_U = NB > NT ? NB / NT : 1;
+    int32_t g_pref[SLOTS_U];
+    if (unit >= 0) {
+        unit_end = min(range_end, tile_last[tile_gid] + 1);
+        const int32_t lo_u = range_start + unit * NB;
+        const int32_t end_u = min(lo_u + NB, unit_end) - 1;
+#pragma unroll
+        for (int q = 0; q < SLOTS_U; ++q) {
+            const int slot = tr + q * NT;
+            const int32_t idx = end_u - slot;
+            g_pref[q] = (slot < NB && idx >= lo_u) ? a.flatten_ids[idx] : 0;
+        }
+    } else if (tr == 0) {
         s_tile_bin = -1;
+    }
 
     // per-pixel state; pixel p of thread tr is (row PX * (tr / TILE) + p,
     // column tr % TILE) of the tile, so a thread's pixels share one column
@@ -611,11 +631,15 @@ __device__ __forceinline__ void rasterize_bwd_tile(
     // The forward saturates most pixels long before the end of the tile's
     // range (on dense scenes after a small fraction of it); every Gaussian
     // behind the tile's last contributor has a zero gradient, so the replay
-    // starts there instead of at the end of the range.
-    __syncthreads();
-    atomicMax(&s_tile_bin, wave_bin);
-    __syncthreads();
-    const int32_t replay_end = min(range_end, s_tile_bin + 1);
+    // starts there instead of at the end of the range.  A unit has it from
+    // the forward; a whole tile takes the maximum of its pixels' last_ids.
+    int32_t replay_end = unit_end;
+    if (unit < 0) {
+        __syncthreads();
+        atomicMax(&s_tile_bin, wave_bin);
+        __syncthreads();
+        replay_end = min(range_end, s_tile_bin + 1);
+    }
     // Whole tile (unit < 0): batches of NB back from replay_end.  One unit:
     // the forward's replay part `unit` of the tile, [lo, min(lo + Q,
     // replay_end)), starting from the forward's record at its end boundary:
@@ -683,7 +707,7 @@ __device__ __forceinline__ void rasterize_bwd_tile(
                 break;
             const int32_t idx = batch_end - slot;
             if (idx >= lo) {
-                const int32_t g = a.flatten_ids[idx];
+                const int32_t g = unit >= 0 ? g_pref[q] : a.flatten_ids[idx];
                 s_gid[slot] = g;
                 const float2 xy = reinterpret_cast<const float2 *>(a.means2d)[g];
                 const float o = a.opacities[g];
@@ -914,8 +938,8 @@ __global__ void __launch_bounds__(BwdShape<TILE>::THREADS) rasterize_bwd_kernel(
         rasterize_bwd_tile<CDIM, TILE, ABS>(
             a, gid, render_alphas, render_T, last_ids, v_render_colors,
             v_render_alphas, v_means2d_abs, v_means2d, v_conics, v_colors,
-            v_opacities, sm, unit, rs.records, queue ? tile_counter : nullptr,
-            next);
+            v_opacities, sm, unit, rs.records, rs.tile_last,
+            queue ? tile_counter : nullptr, next);
         if (!queue)
             break;
         __syncthreads();  // the unit is finished with the LDS
@@ -1092,8 +1116,8 @@ __global__ void replay_clear_kernel(uint32_t *count) { *count = 0u; }
 // Replay workspace: [count, padded to 256 B][units][records], each part
 // 256-byte aligned.
 struct ReplayLayout {
-    int64_t n_records, max_units;
-    size_t units_off, records_off, bytes;
+    int64_t n_records, max_units, n_tiles;
+    size_t units_off, tile_last_off, records_off, bytes;
 };
 
 ReplayLayout replay_layout(int64_t I, int32_t tile_width, int32_t tile_height,
@@ -1102,10 +1126,12 @@ ReplayLayout replay_layout(int64_t I, int32_t tile_width, int32_t tile_height,
     const int64_t q = bs / kReplayParts;
     ReplayLayout l;
     l.n_records = q > 0 ? (n_isects + q - 1) / q : 0;
-    l.max_units = l.n_records + I * (int64_t)tile_width * tile_height;
+    l.n_tiles = I * (int64_t)tile_width * tile_height;
+    l.max_units = l.n_records + l.n_tiles;
     auto up = [](size_t v) { return (v + 255) / 256 * 256; };
     l.units_off = 256;
-    l.records_off = l.units_off + up((size_t)l.max_units * sizeof(int2));
+    l.tile_last_off = l.units_off + up((size_t)l.max_units * sizeof(int2));
+    l.records_off = l.tile_last_off + up((size_t)l.n_tiles * sizeof(int32_t));
     l.bytes = l.records_off +
               (size_t)l.n_records * (size_t)bs * (size_t)(1 + cdim) * sizeof(float);
     return l;
@@ -1125,6 +1151,7 @@ int replay_state(void *ws, size_t ws_bytes, const RasterArgs &a, int cdim,
     rs->count = reinterpret_cast<uint32_t *>(base);
     rs->units = reinterpret_cast<int2 *>(base + l.units_off);
     rs->records = reinterpret_cast<float *>(base + l.records_off);
+    rs->tile_last = reinterpret_cast<int32_t *>(base + l.tile_last_off);
     return GSPLAT_OK;
 }
 

@@ -82,7 +82,8 @@ def test_argument_errors_are_reported_without_a_gpu(lib_path):
 
 def test_replay_workspace_size_and_checks_without_a_gpu(lib_path):
     """The replay workspace: 256 B of count, the unit list (records + tiles
-    entries of 8 B, padded to 256 B), then ceil(n_isects / Q) records of
+    entries of 8 B, padded to 256 B), each tile's last contributor (4 B,
+    padded to 256 B), then ceil(n_isects / Q) records of
     tile_size^2 pixels x (1 + CDIM) floats, Q = tile_size^2 / 4; a short or
     missing workspace is refused before the device is touched (the fake
     pointers are never read)."""
@@ -90,7 +91,8 @@ def test_replay_workspace_size_and_checks_without_a_gpu(lib_path):
     q, n_isects, cdim, tiles = 64, 1000, 3, 6
     n_rec = -(-n_isects // q)
     units = -(-(n_rec + tiles) * 8 // 256) * 256
-    want = 256 + units + n_rec * 256 * (1 + cdim) * 4
+    tile_last = -(-tiles * 4 // 256) * 256
+    want = 256 + units + tile_last + n_rec * 256 * (1 + cdim) * 4
     assert _lib.query("gsplat_rasterize_replay_size", 1, 3, 2, 16, n_isects, cdim) == want
     assert _lib.query("gsplat_rasterize_replay_size", 1, 3, 2, 16, -1, cdim) == 0
     f = 256  # a fake, aligned device address
