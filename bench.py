@@ -118,6 +118,10 @@ def _algorithmic_bytes(name, ctx):
     if name == "gsplat_sh_rows_bwd":
         return (N * 4 * ctx["C"] + nnz * (12 + 12 * K + 12)
                 + N * (12 * K + 12))
+    if name in ("gsplat_isect_emit_tiles", "gsplat_isect_emit_tiles_dev"):
+        # the rows' 32-byte sweep records and starts in; sorted 64-bit ids,
+        # rows and tile offsets out
+        return nnz * (32 + 8) + n_isects * (8 + 4) + tiles * 4
     if name == "gsplat_adam_multi":
         return ctx.get("adam_elems", 0) * 28
     return None
