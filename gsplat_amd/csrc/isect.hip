@@ -787,8 +787,8 @@ __global__ void __launch_bounds__(kIsectThreads)
 //
 //   1. isect_count_rows_kernel: every row's tile count and sweep record,
 //      and the row-order exclusive prefix of the counts (prefix inside each
-//      workgroup, one workgroup scanning the workgroup totals, a pass adding
-//      them); starts[n] = n_isects.  A decoupled look-back over the ~2,600
+//      workgroup; isect_starts_scan_kernel adds the totals of the
+//      workgroups before); starts[n] = n_isects.  A decoupled look-back over the ~2,600
 //      workgroups of this VALU-heavy kernel took 71 us at config 1, against
 //      24 us for the counts alone: every waiting workgroup polls its
 //      predecessors' status words through the device-coherent level.
@@ -799,8 +799,10 @@ __global__ void __launch_bounds__(kIsectThreads)
 //   4. tile_bounds_kernel: the first slot of every tile from the sorted keys
 //      (the reference's isect_offset_encode).
 //   5. tile_depth_sort_kernel: one workgroup per tile sorts the tile's rows
-//      stably on their 32 depth bits -- in LDS up to 4,096 rows, through
-//      global scratch above -- and writes the 64-bit ids and the rows.
+//      stably on their 32 depth bits -- in LDS up to 3,072 rows (radix
+//      passes over the top 16 bits of the tile's depth range, then the
+//      rows that tie on those bits by insertion), through global scratch
+//      above -- and writes the 64-bit ids and the rows.
 // The reference sorts stably on image|tile|depth over row-order emission,
 // which orders by (image|tile, depth bits, row); steps 3 and 5 produce that
 // order.  The depth order is taken per tile (~1,000 rows at config 1) in LDS
@@ -834,7 +836,7 @@ __global__ void __launch_bounds__(kIsectThreads)
     }
     if (idx < a.n) {
         tiles_per_gauss[idx] = cnt;
-        // the prefix inside the workgroup; isect_starts_finalize_kernel adds
+        // the prefix inside the workgroup; isect_starts_scan_kernel adds
         // the workgroup's own prefix
         starts[idx] = (int64_t)(wave_off + incl - (uint64_t)cnt);
     }
@@ -842,67 +844,58 @@ __global__ void __launch_bounds__(kIsectThreads)
         block_tot[blockIdx.x] = total;
 }
 
-// Exclusive prefix of the per-workgroup totals of isect_count_rows_kernel,
-// by one workgroup (4 totals per thread per step, a running carry between
-// steps); writes starts[n] and *n_isects_out.
-constexpr int kBlockScanThreads = 1024;
-constexpr int kBlockScanItems = 4;
+// Row starts from the per-workgroup prefixes of isect_count_rows_kernel, in
+// one launch: each workgroup takes kStartsGroup consecutive count
+// workgroups, sums the totals of all count workgroups before them (a
+// block-wide reduction, the totals being few: ~2,600 at config 1) and adds
+// the running prefix to their rows.  The last workgroup writes starts[n]
+// and *n_isects_out.  (One workgroup scanning the totals and a second pass
+// adding them took 4.7 + 4.3 us at config 1.)
+constexpr int kStartsGroup = 8;
 
-__global__ void __launch_bounds__(kBlockScanThreads)
-    isect_block_scan_kernel(int64_t n_blocks, const uint64_t *__restrict__ block_tot,
-                            uint64_t *__restrict__ block_pre, int64_t n,
-                            int64_t *__restrict__ starts,
-                            int64_t *__restrict__ n_isects_out) {
-    __shared__ uint64_t s_wave_tot[kBlockScanThreads / kWave];
-    __shared__ uint64_t s_carry;
-    if (threadIdx.x == 0)
-        s_carry = 0;
-    constexpr int kStep = kBlockScanThreads * kBlockScanItems;
-    const uint32_t wave = threadIdx.x / kWave;
-    for (int64_t b0 = 0; b0 < n_blocks; b0 += kStep) {
-        const int64_t i0 = b0 + (int64_t)threadIdx.x * kBlockScanItems;
-        uint64_t v[kBlockScanItems], sum = 0;
+__global__ void __launch_bounds__(kIsectThreads)
+    isect_starts_scan_kernel(int64_t n, int64_t n_blocks,
+                             const uint64_t *__restrict__ block_tot,
+                             int64_t *__restrict__ starts,
+                             int64_t *__restrict__ n_isects_out) {
+    __shared__ uint64_t s_wave[kIsectThreads / kWave];
+    __shared__ uint64_t s_grp[kStartsGroup];
+    const int64_t b0 = (int64_t)blockIdx.x * kStartsGroup;
+    // every load is issued before the reduction: the rows' own prefixes,
+    // the group's totals and the totals before the group
+    int64_t own[kStartsGroup];
 #pragma unroll
-        for (int k = 0; k < kBlockScanItems; ++k) {
-            v[k] = i0 + k < n_blocks ? block_tot[i0 + k] : 0ull;
-            sum += v[k];
-        }
-        const uint64_t incl = wave_inclusive_scan_u64(sum);
-        if (lane_id() == kWave - 1)
-            s_wave_tot[wave] = incl;
-        __syncthreads();
-        uint64_t off = s_carry, step_tot = 0;
-#pragma unroll
-        for (int w = 0; w < kBlockScanThreads / kWave; ++w) {
-            const uint64_t t = s_wave_tot[w];
-            off += (w < (int)wave) ? t : 0ull;
-            step_tot += t;
-        }
-        uint64_t run = off + incl - sum;
-#pragma unroll
-        for (int k = 0; k < kBlockScanItems; ++k) {
-            if (i0 + k < n_blocks)
-                block_pre[i0 + k] = run;
-            run += v[k];
-        }
-        __syncthreads();  // every thread has read s_carry and s_wave_tot
-        if (threadIdx.x == 0)
-            s_carry += step_tot;
-        __syncthreads();
+    for (int k = 0; k < kStartsGroup; ++k) {
+        const int64_t i = (b0 + k) * kIsectThreads + threadIdx.x;
+        own[k] = i < n ? starts[i] : 0;
     }
-    if (threadIdx.x == 0) {
-        starts[n] = (int64_t)s_carry;
-        *n_isects_out = (int64_t)s_carry;
+    if (threadIdx.x < kStartsGroup)
+        s_grp[threadIdx.x] =
+            b0 + threadIdx.x < n_blocks ? block_tot[b0 + threadIdx.x] : 0ull;
+    uint64_t sum = 0;
+    for (int64_t b = threadIdx.x; b < b0; b += kIsectThreads)
+        sum += block_tot[b];
+    sum = wave_inclusive_scan_u64(sum);
+    if (lane_id() == kWave - 1)
+        s_wave[threadIdx.x / kWave] = sum;
+    __syncthreads();
+    uint64_t run = 0;
+#pragma unroll
+    for (int w = 0; w < kIsectThreads / kWave; ++w)
+        run += s_wave[w];
+#pragma unroll
+    for (int k = 0; k < kStartsGroup; ++k) {
+        const int64_t i = (b0 + k) * kIsectThreads + threadIdx.x;
+        if (i < n)
+            starts[i] = own[k] + (int64_t)run;
+        run += s_grp[k];
+    }
+    if (threadIdx.x == 0 && b0 + kStartsGroup >= n_blocks) {
+        starts[n] = (int64_t)run;
+        *n_isects_out = (int64_t)run;
     }
 }
 
-__global__ void isect_starts_finalize_kernel(int64_t n,
-                                             const uint64_t *__restrict__ block_pre,
-                                             int64_t *__restrict__ starts) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n)
-        starts[i] += (int64_t)block_pre[i / kIsectThreads];
-}
 
 // offsets[s] = the first slot whose image|tile key is that of tile slot s
 // (image * n_tiles + tile), or n when none is.  Every slot boundary i in
@@ -953,7 +946,7 @@ constexpr int kSegRadix = 1 << kSegDigitBits;
 constexpr int kSegPasses = 32 / kSegDigitBits;
 // Tiles of up to kSegLarge rows are sorted in LDS, larger ones through
 // global scratch.
-constexpr int kSegLarge = 4096;
+constexpr int kSegLarge = 3072;
 
 template <int MAXK>
 struct SegSmem {
@@ -1047,42 +1040,20 @@ __device__ __forceinline__ int seg_span(int S) {
     return (S + kSegWaves * kWave - 1) / (kSegWaves * kWave) * kWave;
 }
 
-// Tile of S <= 64 * ITEMS * kSegWaves rows, sorted in LDS.
+// LSD passes over the 8-bit digits of bits [lo_bit, hi_bit) of the keys k
+// (wave w's items at base + 64 j + lane, valid below lim): each pass ranks
+// stably, reorders the tile through LDS and reloads every thread's items, so
+// after the last pass both the registers and sm.keys/sm.vals hold the order.
 template <int ITEMS, int MAXK>
-__device__ void seg_sort_lds(int S, const uint32_t *__restrict__ rows_in,
-                             const uint32_t *__restrict__ depth_bits,
-                             uint64_t key_hi, int64_t *__restrict__ out_ids,
-                             int32_t *__restrict__ out_rows, SegSmem<MAXK> &sm) {
-    static_assert(ITEMS * kWave * kSegWaves <= MAXK, "tile exceeds LDS");
+__device__ __forceinline__ void seg_lsd_passes(uint32_t (&k)[ITEMS],
+                                               uint32_t (&v)[ITEMS], int base,
+                                               int lim, int lo_bit, int hi_bit,
+                                               SegSmem<MAXK> &sm) {
     const int tid = threadIdx.x;
     const int w = tid / kWave;
     const int lane = (int)lane_id();
-    // the tile split evenly over the waves, in whole items: wave w holds
-    // [base, lim) = [w * span, (w + 1) * span) cut at S
-    const int span = seg_span(S);
-    const int base = w * span;
-    const int lim = min(S, base + span);
-    uint32_t k[ITEMS], v[ITEMS], rank[ITEMS];
-#pragma unroll
-    for (int j = 0; j < ITEMS; ++j) {
-        const int i = base + j * kWave + lane;
-        v[j] = i < lim ? rows_in[i] : 0u;
-    }
-    uint32_t o = 0u, an = ~0u;
-#pragma unroll
-    for (int j = 0; j < ITEMS; ++j) {
-        const int i = base + j * kWave + lane;
-        k[j] = i < lim ? depth_bits[v[j]] : 0u;
-        if (i < lim) {
-            o |= k[j];
-            an &= k[j];
-        }
-    }
-    const uint32_t varying = block_varying_bits(o, an, sm);
-    for (int p = 0; p < kSegPasses; ++p) {
-        const int shift = p * kSegDigitBits;
-        if (((varying >> shift) & (kSegRadix - 1)) == 0u)
-            continue;  // one digit value over the tile
+    uint32_t rank[ITEMS];
+    for (int shift = lo_bit; shift < hi_bit; shift += kSegDigitBits) {
         seg_rank<ITEMS>(k, base, lim, shift, sm, rank);
         {
             // digit starts, and each wave's start inside its digit (thread d
@@ -1126,11 +1097,148 @@ __device__ void seg_sort_lds(int S, const uint32_t *__restrict__ rows_in,
         }
         __syncthreads();
     }
+}
+
+// Block-wide minimum and maximum of the threads' partials.
+template <class SM>
+__device__ __forceinline__ void block_min_max(uint32_t lo, uint32_t hi, SM &sm,
+                                              uint32_t &kmin, uint32_t &kmax) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        lo = min(lo, (uint32_t)__shfl_xor((int)lo, o));
+        hi = max(hi, (uint32_t)__shfl_xor((int)hi, o));
+    }
+    const int w = threadIdx.x / kWave;
+    if (lane_id() == 0) {
+        sm.bits_or[w] = lo;
+        sm.bits_and[w] = hi;
+    }
+    __syncthreads();
+    kmin = ~0u;
+    kmax = 0u;
+#pragma unroll
+    for (int ww = 0; ww < kSegWaves; ++ww) {
+        kmin = min(kmin, sm.bits_or[ww]);
+        kmax = max(kmax, sm.bits_and[ww]);
+    }
+}
+
+// Key bits the LDS sort ranks by radix passes: the top kSegCoarseBits bits
+// of the tile's key range (two passes); runs of keys equal in those bits are
+// then put in order by transposition, stably, within 2 kSegRunMax phases
+// (else passes over every bit of the range follow).
+constexpr int kSegCoarseBits = 16;
+constexpr int kSegRunMax = 32;
+
+// Tile of S <= 64 * ITEMS * kSegWaves rows, sorted in LDS.  The keys are
+// ranked relative to the tile's smallest key, on the top bits of the range
+// first: a stable sort on k >> c (the passes) followed by a stable sort of
+// every run of equal k >> c (transposition) is the stable sort on k, since
+// k >> c is monotone in k.  A tile whose runs are not sorted within the
+// phase limit is sorted again by passes over all bits of k, starting from
+// the order reached; that order keeps equal keys in input order (their
+// coarse keys are equal too, and transposition never swaps them), so the
+// result is the same stable sort.
+template <int ITEMS, int MAXK>
+__device__ void seg_sort_lds(int S, const uint32_t *__restrict__ rows_in,
+                             const uint32_t *__restrict__ depth_bits,
+                             uint64_t key_hi, int64_t *__restrict__ out_ids,
+                             int32_t *__restrict__ out_rows, SegSmem<MAXK> &sm) {
+    static_assert(ITEMS * kWave * kSegWaves <= MAXK, "tile exceeds LDS");
+    const int tid = threadIdx.x;
+    const int w = tid / kWave;
+    const int lane = (int)lane_id();
+    // the tile split evenly over the waves, in whole items: wave w holds
+    // [base, lim) = [w * span, (w + 1) * span) cut at S
+    const int span = seg_span(S);
+    const int base = w * span;
+    const int lim = min(S, base + span);
+    uint32_t k[ITEMS], v[ITEMS];
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+        const int i = base + j * kWave + lane;
+        v[j] = i < lim ? rows_in[i] : 0u;
+    }
+    uint32_t lo = ~0u, hi = 0u;
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+        const int i = base + j * kWave + lane;
+        k[j] = i < lim ? depth_bits[v[j]] : 0u;
+        if (i < lim) {
+            lo = min(lo, k[j]);
+            hi = max(hi, k[j]);
+        }
+    }
+    uint32_t kmin, kmax;
+    block_min_max(lo, hi, sm, kmin, kmax);
+    const uint32_t range = kmax - kmin;
+    const int bits = range != 0u ? 32 - __clz((int)range) : 0;
+    const int coarse = bits > kSegCoarseBits ? bits - kSegCoarseBits : 0;
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j)
+        k[j] -= kmin;
+    // one round of passes over the coarse bits, and a second over all bits
+    // only if a run is too long (a single call site keeps one copy of the
+    // unrolled passes)
+    for (int lo_bit = coarse;;) {
+        seg_lsd_passes<ITEMS>(k, v, base, lim, lo_bit, bits, sm);
+        if (lo_bit == 0)
+            break;
+        // runs of equal coarse key (the passes left the order in LDS), put
+        // in order by odd-even transposition: each phase compares the
+        // disjoint pairs (i, i + 1) of one parity and swaps those with equal
+        // coarse keys out of order (equal keys never move, so the result is
+        // stable).  A full round (both parities) without a swap leaves every
+        // run sorted; a run of L keys needs at most L phases, and a tile
+        // still swapping after 2 kSegRunMax phases takes the full passes.
+        bool long_run = false;
+        constexpr int PAIRS = (ITEMS + 1) / 2;  // pairs per thread and phase
+        for (int ph = 0, quiet = 0;; ++ph) {
+            const int par = ph & 1;
+            bool swapped = false;
+#pragma unroll
+            for (int r = 0; r < PAIRS; ++r) {
+                const int i = 2 * (tid + r * kSegThreads) + par;
+                if (i + 1 < S) {
+                    const uint32_t ka = sm.keys[i], kb = sm.keys[i + 1];
+                    if ((ka >> lo_bit) == (kb >> lo_bit) && ka > kb) {
+                        const uint32_t va = sm.vals[i], vb = sm.vals[i + 1];
+                        sm.keys[i] = kb;
+                        sm.keys[i + 1] = ka;
+                        sm.vals[i] = vb;
+                        sm.vals[i + 1] = va;
+                        swapped = true;
+                    }
+                }
+            }
+            quiet = __syncthreads_or(swapped) ? 0 : quiet + 1;
+            if (quiet == 2)
+                break;
+            if (ph >= 2 * kSegRunMax) {
+                long_run = true;
+                break;
+            }
+        }
+        // long_run is the same in every thread (set from a block-wide vote)
+        const bool any_long = long_run;
+#pragma unroll
+        for (int j = 0; j < ITEMS; ++j) {
+            const int i = base + j * kWave + lane;
+            if (i < lim) {
+                k[j] = sm.keys[i];
+                v[j] = sm.vals[i];
+            }
+        }
+        if (!any_long)
+            break;
+        __syncthreads();
+        lo_bit = 0;
+    }
 #pragma unroll
     for (int j = 0; j < ITEMS; ++j) {
         const int i = base + j * kWave + lane;
         if (i < lim) {
-            out_ids[i] = (int64_t)(key_hi | k[j]);
+            out_ids[i] = (int64_t)(key_hi | (k[j] + kmin));
             out_rows[i] = (int32_t)v[j];
         }
     }
@@ -1273,7 +1381,10 @@ __device__ __forceinline__ SegTile seg_tile(int64_t s, int64_t n,
 // writes it); p1k/p1v is scratch of at least n entries each.  Tiles of all
 // sizes share one launch: a separate launch for the few large tiles (after
 // the small ones) put their whole sort on the critical path (25 us at
-// config 1 for ~50 tiles of 2,049-2,406 rows).
+// config 1 for ~50 tiles of 2,049-2,406 rows).  The LDS holds 3,072 rows
+// (30 KB, five workgroups per CU): 4,096 rows (38 KB, four per CU) took
+// 62.5 us at config 1 against 56-58 us, 2,048 rows (seven per CU, the
+// ~50 larger tiles through global scratch) 92 us.
 __global__ void __launch_bounds__(kSegThreads)
     tile_depth_sort_kernel(int64_t n, const int64_t *__restrict__ n_dev,
                            const int32_t *__restrict__ offsets, int64_t n_slots,
@@ -1292,12 +1403,14 @@ __global__ void __launch_bounds__(kSegThreads)
     const uint32_t *rin = rows_in + t.start;
     int64_t *oid = isect_ids + t.start;
     int32_t *orow = out_rows + t.start;
+    // keys per thread: a tile of S rows needs S <= ITEMS * kSegThreads
     constexpr int I = kSegLarge / kSegThreads;  // items per thread at kSegLarge
-    if (t.S <= kSegLarge / 8)
+    static_assert(I * kSegThreads == kSegLarge && I >= 8, "LDS tile size");
+    if (t.S <= (I / 8) * kSegThreads)
         seg_sort_lds<I / 8>((int)t.S, rin, depth_bits, t.key_hi, oid, orow, sm);
-    else if (t.S <= kSegLarge / 4)
+    else if (t.S <= (I / 4) * kSegThreads)
         seg_sort_lds<I / 4>((int)t.S, rin, depth_bits, t.key_hi, oid, orow, sm);
-    else if (t.S <= kSegLarge / 2)
+    else if (t.S <= (I / 2) * kSegThreads)
         seg_sort_lds<I / 2>((int)t.S, rin, depth_bits, t.key_hi, oid, orow, sm);
     else if (t.S <= kSegLarge)
         seg_sort_lds<I>((int)t.S, rin, depth_bits, t.key_hi, oid, orow, sm);
@@ -1671,8 +1784,8 @@ extern "C" int gsplat_isect_emit_sorted_dev(
 // isect_count_rows_kernel to tile_depth_sort_kernel).
 // ---------------------------------------------------------------------------
 extern "C" size_t gsplat_isect_prepare_rows_workspace_size(int64_t n) {
-    // per-workgroup totals and prefixes
-    return 2 * align256((size_t)ceil_div(n > 0 ? n : 0, kIsectThreads) * 8);
+    // per-workgroup totals
+    return align256((size_t)ceil_div(n > 0 ? n : 0, kIsectThreads) * 8);
 }
 
 extern "C" int gsplat_isect_prepare_rows(int64_t n, int64_t N, const int64_t *image_ids,
@@ -1699,19 +1812,14 @@ extern "C" int gsplat_isect_prepare_rows(int64_t n, int64_t N, const int64_t *im
     GS_REQUIRE(workspace && workspace_bytes >= gsplat_isect_prepare_rows_workspace_size(n),
                "isect_prepare_rows: workspace too small");
     uint64_t *block_tot = reinterpret_cast<uint64_t *>(workspace);
-    uint64_t *block_pre = reinterpret_cast<uint64_t *>(
-        reinterpret_cast<char *>(workspace) + align256((size_t)blocks * 8));
     hipStream_t st = as_stream(stream);
     isect_count_rows_kernel<<<(unsigned)blocks, kIsectThreads, 0, st>>>(
         a, tiles_per_gauss, reinterpret_cast<RowRec *>(row_records), row_starts,
         block_tot);
     GS_TRY(check_launch("isect_count_rows_kernel"));
-    isect_block_scan_kernel<<<1, kBlockScanThreads, 0, st>>>(
-        blocks, block_tot, block_pre, n, row_starts, n_isects_out);
-    GS_TRY(check_launch("isect_block_scan_kernel"));
-    isect_starts_finalize_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(
-        n, block_pre, row_starts);
-    return check_launch("isect_starts_finalize_kernel");
+    isect_starts_scan_kernel<<<(unsigned)ceil_div(blocks, kStartsGroup), kIsectThreads,
+                               0, st>>>(n, blocks, block_tot, row_starts, n_isects_out);
+    return check_launch("isect_starts_scan_kernel");
 }
 
 extern "C" size_t gsplat_isect_emit_tiles_workspace_size(int64_t n_isects) {

@@ -151,12 +151,13 @@ def test_offsets_empty_and_zero_isects():
     assert offs.shape == (2, 4, 5) and int(offs.abs().sum()) == 0
 
 
-@pytest.mark.parametrize("N", [700, 1800, 3500, 11000])
+@pytest.mark.parametrize("N", [200, 700, 1400, 2800, 11000])
 def test_tile_first_sort_every_segment_size(N):
     """The tile-first sorted intersection sorts each tile's rows on their
-    depth bits in LDS up to 1,024 / 2,048 / 4,096 rows and through global
-    scratch above that.  Rows with large radii put about N rows into each of
-    the 12 tiles of every image, so each N takes one of the four paths.
+    depth bits in LDS up to 256 / 768 / 1,536 / 3,072 rows (1, 3, 6 or 12
+    keys per thread) and through global scratch above that.  Rows with large
+    radii put about N rows into each of the 12 tiles of every image, so each
+    N takes one of the five paths.
     Depths are quantised (many ties, which must stay in row order) and half
     of them negative (their zero-extended bits order after every positive
     depth, IntersectTile.cu:190-192).  The offsets come from the same call
@@ -172,8 +173,9 @@ def test_tile_first_sort_every_segment_size(N):
     depths = (np.round(rng.uniform(-3, 3, (C, N)) * 8) / 8).astype(np.float32)
     want = exact.isect_tiles(means2d, radii, depths, ts, tw, th)
     per_tile = np.bincount(want[1] >> 32, minlength=C * tw * th)
-    lo = {700: 1, 1800: 1025, 3500: 2049, 11000: 4097}[N]
-    assert per_tile.max() >= lo, per_tile.max()
+    lo, hi = {200: (1, 256), 700: (257, 768), 1400: (769, 1536), 2800: (1537, 3072),
+              11000: (3073, None)}[N]
+    assert per_tile.max() >= lo and (hi is None or per_tile.max() <= hi), per_tile.max()
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
     tpg = torch.empty((C, N), dtype=torch.int32, device=DEV)
     state = _ops.isect_prepare_sorted(t(means2d), t(radii), t(depths), None, None,
@@ -190,6 +192,36 @@ def test_tile_first_sort_every_segment_size(N):
     _compare(got[:3], want)
     np.testing.assert_array_equal(got[3].cpu().numpy().reshape(-1),
                                   exact.isect_offset_encode(want[1], C, tw, th).reshape(-1))
+
+
+@pytest.mark.parametrize("group,negative", [(12, False), (12, True), (80, False)])
+def test_tile_depth_sort_clustered_depths(group, negative):
+    """Depths in clusters of about `group` rows per tile, each cluster a few
+    dozen float ulps wide in random row order, clusters 0.01 apart and a few
+    far depths (12.0, or -1.0 whose bits order last) widening every tile's
+    range.  The per-tile sort ranks the top bits of the range by radix passes
+    and orders the rows that tie on those bits afterwards: clusters of 12 are
+    such runs with their low bits out of order, clusters of 80 exceed the
+    run limit and take the full-key passes.  The ids must equal the oracle's
+    stable sort (IntersectTile.cu:496-505)."""
+    from gsplat_amd.cuda import _ops
+    N = 1500
+    rng = np.random.default_rng(group + int(negative))
+    C, ts, W, H = 1, 16, 64, 48
+    tw, th = math.ceil(W / ts), math.ceil(H / ts)
+    means2d = np.stack([rng.uniform(0, W, (C, N)), rng.uniform(0, H, (C, N))],
+                       -1).astype(np.float32)
+    radii = rng.integers(40, 90, (C, N, 2)).astype(np.int32)
+    g = rng.integers(0, max(N // group, 1), (C, N))
+    depths = (2.0 + 0.01 * g + rng.uniform(0, 2e-5, (C, N))).astype(np.float32)
+    depths[:, ::150] = -1.0 if negative else 12.0
+    want = exact.isect_tiles(means2d, radii, depths, ts, tw, th)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    tpg = torch.empty((C, N), dtype=torch.int32, device=DEV)
+    state = _ops.isect_prepare_sorted(t(means2d), t(radii), t(depths), None, None,
+                                      None, N, C, ts, tw, th, tpg)
+    got = _ops.isect_emit_sorted(state)
+    _compare(got[:3], want)
 
 
 def _depth_first(means2d, radii, depths, C, N, ts, tw, th, capacity=None):
