@@ -275,7 +275,12 @@ struct FwdArgs {
 __device__ __forceinline__ void split_row(const FwdArgs &a, int64_t row,
                                           int64_t &bc, int64_t &g,
                                           int64_t &bg) {
-    if (a.idx32) {
+    if (a.B * a.C == 1) {
+        // one image: no division
+        bc = 0;
+        g = row;
+        bg = row;
+    } else if (a.idx32) {
         const uint32_t r = (uint32_t)row, n = (uint32_t)a.N;
         const uint32_t q = r / n;
         bc = q;
@@ -374,16 +379,27 @@ __global__ void __launch_bounds__(kPackThreads) projection_packed_fwd_kernel(
     const uint32_t wave = threadIdx.x / kWave;
     const uint32_t lane = lane_id();
 
-    // phase 0: row indices and every input of the thread's rows (rows past
-    // the end read the last row and are dropped)
-    int64_t bc[kPackItems], g[kPackItems];
+    // phase 0: row indices, the camera of the wave's first row, then every
+    // input of the thread's rows (rows past the end read the last row and
+    // are dropped).  The camera is loaded before the rows: loads complete in
+    // issue order, so waiting for the camera does not wait for the rows, and
+    // projecting slice j waits only for the loads of slices 0..j.
+    int64_t bc[kPackItems], g[kPackItems], bgs[kPackItems];
+#pragma unroll
+    for (int j = 0; j < kPackItems; ++j) {
+        const int64_t row = base + (int64_t)j * kPackThreads + threadIdx.x;
+        split_row(a, row < n_rows ? row : n_rows - 1, bc[j], g[j], bgs[j]);
+    }
+    const int64_t bc0 =
+        ((int64_t)__builtin_amdgcn_readfirstlane((int)(bc[0] >> 32)) << 32) |
+        (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)bc[0]);
+    Cam cam0;
+    load_cam(a.viewmats + bc0 * 16, a.Ks + bc0 * 9, cam0);
     float mean[kPackItems][3], quat[kPackItems][4], scale[kPackItems][3];
     float cov[kPackItems][6], opac[kPackItems];
 #pragma unroll
     for (int j = 0; j < kPackItems; ++j) {
-        const int64_t row = base + (int64_t)j * kPackThreads + threadIdx.x;
-        int64_t bg;
-        split_row(a, row < n_rows ? row : n_rows - 1, bc[j], g[j], bg);
+        const int64_t bg = bgs[j];
 #pragma unroll
         for (int k = 0; k < 3; ++k)
             mean[j][k] = a.means[bg * 3 + k];
@@ -402,21 +418,14 @@ __global__ void __launch_bounds__(kPackThreads) projection_packed_fwd_kernel(
         opac[j] = a.opacities ? a.opacities[bg] : 0.f;
     }
 
-    // phase 1: project; the camera is loaded once (scalar loads) when all
-    // rows of the wave belong to one camera row
-    const int64_t bc0 =
-        ((int64_t)__builtin_amdgcn_readfirstlane((int)(bc[0] >> 32)) << 32) |
-        (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)bc[0]);
+    // phase 1: project; the camera loaded above serves every row when all
+    // rows of the wave belong to its camera row
     bool mixed = false;
 #pragma unroll
     for (int j = 0; j < kPackItems; ++j)
         mixed |= bc[j] != bc0;
     const bool one_cam = !wave_ballot(mixed);
-    Cam cam0;
-    if (one_cam) {
-        load_cam(a.viewmats + bc0 * 16, a.Ks + bc0 * 9, cam0);
-        set_fwd_limits(cam0, a.W, a.H);
-    }
+    set_fwd_limits(cam0, a.W, a.H);
     ProjOut o[kPackItems];
     uint64_t bal[kPackItems];
 #pragma unroll
