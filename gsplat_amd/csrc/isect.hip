@@ -944,9 +944,10 @@ constexpr int kSegWaves = kSegThreads / kWave;
 constexpr int kSegDigitBits = 8;
 constexpr int kSegRadix = 1 << kSegDigitBits;
 constexpr int kSegPasses = 32 / kSegDigitBits;
-// Tiles of up to kSegLarge rows are sorted in LDS, larger ones through
-// global scratch.
-constexpr int kSegLarge = 3072;
+// Tiles of up to CAP rows are sorted in LDS, larger ones through global
+// scratch; the kernel comes in two LDS capacities (tile_depth_sort_kernel).
+constexpr int kSegCapSmall = 3072;
+constexpr int kSegCapLarge = 4096;
 
 template <int MAXK>
 struct SegSmem {
@@ -1244,21 +1245,22 @@ __device__ void seg_sort_lds(int S, const uint32_t *__restrict__ rows_in,
     }
 }
 
-// Tile of more than kSegLarge rows: LSD passes through global scratch, one
-// chunk of kSegLarge keys after another, each chunk ranked in LDS and
+// Tile of more than CAP rows: LSD passes through global scratch, one
+// chunk of CAP keys after another, each chunk ranked in LDS and
 // written at the running digit offsets (stable: chunks in order, ranks
 // stable inside each).  Scratch pairs: p1 (own keys and values) and p2
 // (keys then values in the tile's 8-byte id range, free until the final
 // write); the prologue writes the pair that leaves the result in p1 after
 // the passes.
+template <int CAP>
 __device__ void seg_sort_global(int64_t S, const uint32_t *__restrict__ rows_in,
                                 const uint32_t *__restrict__ depth_bits,
                                 uint64_t key_hi, uint32_t *__restrict__ p1k,
                                 uint32_t *__restrict__ p1v,
                                 int64_t *__restrict__ out_ids,
                                 int32_t *__restrict__ out_rows,
-                                SegSmem<kSegLarge> &sm) {
-    constexpr int ITEMS = kSegLarge / kSegThreads;
+                                SegSmem<CAP> &sm) {
+    constexpr int ITEMS = CAP / kSegThreads;
     const int tid = threadIdx.x;
     const int w = tid / kWave;
     const int lane = (int)lane_id();
@@ -1304,8 +1306,8 @@ __device__ void seg_sort_global(int64_t S, const uint32_t *__restrict__ rows_in,
                 sm.off[tid] = o;
         }
         __syncthreads();
-        for (int64_t c0 = 0; c0 < S; c0 += kSegLarge) {
-            const int cs = (int)(S - c0 < kSegLarge ? S - c0 : kSegLarge);
+        for (int64_t c0 = 0; c0 < S; c0 += CAP) {
+            const int cs = (int)(S - c0 < CAP ? S - c0 : CAP);
             const int span = seg_span(cs);
             const int base = w * span;
             const int lim = min(cs, base + span);
@@ -1381,10 +1383,14 @@ __device__ __forceinline__ SegTile seg_tile(int64_t s, int64_t n,
 // writes it); p1k/p1v is scratch of at least n entries each.  Tiles of all
 // sizes share one launch: a separate launch for the few large tiles (after
 // the small ones) put their whole sort on the critical path (25 us at
-// config 1 for ~50 tiles of 2,049-2,406 rows).  The LDS holds 3,072 rows
-// (30 KB, five workgroups per CU): 4,096 rows (38 KB, four per CU) took
-// 62.5 us at config 1 against 56-58 us, 2,048 rows (seven per CU, the
-// ~50 larger tiles through global scratch) 92 us.
+// config 1 for ~50 tiles of 2,049-2,406 rows).  The LDS holds CAP rows:
+// 3,072 (30 KB, five workgroups per CU) where tiles average up to
+// kSegDeepMean rows, else 4,096 (38 KB, four per CU).  At config 1 (1,158
+// rows a tile on average) 4,096 took 62.5 us against 56-58 us and 2,048
+// (seven per CU, the ~50 larger tiles through global scratch) 92 us; at
+// config 4 (1,874 on average, 729 tiles of 3,073-3,802 rows) 3,072 sends a
+// fifth of the rows through global scratch.
+template <int CAP>
 __global__ void __launch_bounds__(kSegThreads)
     tile_depth_sort_kernel(int64_t n, const int64_t *__restrict__ n_dev,
                            const int32_t *__restrict__ offsets, int64_t n_slots,
@@ -1393,7 +1399,7 @@ __global__ void __launch_bounds__(kSegThreads)
                            const uint32_t *rows_in, uint32_t *__restrict__ p1k,
                            uint32_t *__restrict__ p1v,
                            int64_t *__restrict__ isect_ids, int32_t *out_rows) {
-    __shared__ SegSmem<kSegLarge> sm;
+    __shared__ SegSmem<CAP> sm;
     if (n_dev != nullptr)
         n = min(n, *n_dev);
     const int64_t s = blockIdx.x;
@@ -1404,20 +1410,23 @@ __global__ void __launch_bounds__(kSegThreads)
     int64_t *oid = isect_ids + t.start;
     int32_t *orow = out_rows + t.start;
     // keys per thread: a tile of S rows needs S <= ITEMS * kSegThreads
-    constexpr int I = kSegLarge / kSegThreads;  // items per thread at kSegLarge
-    static_assert(I * kSegThreads == kSegLarge && I >= 8, "LDS tile size");
+    constexpr int I = CAP / kSegThreads;  // items per thread at CAP
+    static_assert(I * kSegThreads == CAP && I >= 8, "LDS tile size");
     if (t.S <= (I / 8) * kSegThreads)
         seg_sort_lds<I / 8>((int)t.S, rin, depth_bits, t.key_hi, oid, orow, sm);
     else if (t.S <= (I / 4) * kSegThreads)
         seg_sort_lds<I / 4>((int)t.S, rin, depth_bits, t.key_hi, oid, orow, sm);
     else if (t.S <= (I / 2) * kSegThreads)
         seg_sort_lds<I / 2>((int)t.S, rin, depth_bits, t.key_hi, oid, orow, sm);
-    else if (t.S <= kSegLarge)
+    else if (t.S <= CAP)
         seg_sort_lds<I>((int)t.S, rin, depth_bits, t.key_hi, oid, orow, sm);
     else
-        seg_sort_global(t.S, rin, depth_bits, t.key_hi, p1k + t.start, p1v + t.start,
-                        oid, orow, sm);
+        seg_sort_global<CAP>(t.S, rin, depth_bits, t.key_hi, p1k + t.start,
+                             p1v + t.start, oid, orow, sm);
 }
+
+// Mean rows per tile above which the depth sort takes the 4,096-row LDS.
+constexpr int64_t kSegDeepMean = 1500;
 
 struct PrepLayout {
     size_t keys_a, keys_b, vals_b, lookback, sort_ws, total;
@@ -1897,10 +1906,18 @@ static int emit_tiles_impl(
         n_isects, n_dev, sorted_keys, n_slots, a.tile_n_bits, (int32_t)n_tiles,
         offsets);
     GS_TRY(check_launch("tile_bounds_kernel"));
-    tile_depth_sort_kernel<<<(unsigned)n_slots, kSegThreads, 0, st>>>(
-        n_isects, n_dev, offsets, n_slots, a.tile_n_bits, (int32_t)n_tiles,
-        reinterpret_cast<const uint32_t *>(depths), out_vals, free_keys, tmp_vals,
-        isect_ids, flatten_ids);
+    // n_isects is the count or, with n_dev, the capacity sized from the
+    // previous call's count: either way the mean tile depth of this scene
+    if (n_isects > kSegDeepMean * n_slots)
+        tile_depth_sort_kernel<kSegCapLarge><<<(unsigned)n_slots, kSegThreads, 0, st>>>(
+            n_isects, n_dev, offsets, n_slots, a.tile_n_bits, (int32_t)n_tiles,
+            reinterpret_cast<const uint32_t *>(depths), out_vals, free_keys, tmp_vals,
+            isect_ids, flatten_ids);
+    else
+        tile_depth_sort_kernel<kSegCapSmall><<<(unsigned)n_slots, kSegThreads, 0, st>>>(
+            n_isects, n_dev, offsets, n_slots, a.tile_n_bits, (int32_t)n_tiles,
+            reinterpret_cast<const uint32_t *>(depths), out_vals, free_keys, tmp_vals,
+            isect_ids, flatten_ids);
     return check_launch("tile_depth_sort_kernel");
 }
 

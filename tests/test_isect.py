@@ -154,10 +154,11 @@ def test_offsets_empty_and_zero_isects():
 @pytest.mark.parametrize("N", [200, 700, 1400, 2800, 11000])
 def test_tile_first_sort_every_segment_size(N):
     """The tile-first sorted intersection sorts each tile's rows on their
-    depth bits in LDS up to 256 / 768 / 1,536 / 3,072 rows (1, 3, 6 or 12
-    keys per thread) and through global scratch above that.  Rows with large
-    radii put about N rows into each of the 12 tiles of every image, so each
-    N takes one of the five paths.
+    depth bits in LDS (3,072 rows where tiles average up to 1,500 rows,
+    else 4,096) and through global scratch above that.  Rows with large
+    radii put about N rows into each of the 12 tiles of every image: N up to
+    1,400 takes the 1-, 3- and 6-key paths of the smaller LDS, 2,800 the
+    16-key path of the larger one and 11,000 its global scratch.
     Depths are quantised (many ties, which must stay in row order) and half
     of them negative (their zero-extended bits order after every positive
     depth, IntersectTile.cu:190-192).  The offsets come from the same call
@@ -188,6 +189,46 @@ def test_tile_first_sort_every_segment_size(N):
     state = _ops.isect_prepare_sorted(t(means2d), t(radii), t(depths), None, None,
                                       None, N, C, ts, tw, th, tpg)
     _ops.isect_emit_sorted_queue(state, want[1].shape[0] + 1000)
+    got = _ops.isect_emit_sorted(state)
+    _compare(got[:3], want)
+    np.testing.assert_array_equal(got[3].cpu().numpy().reshape(-1),
+                                  exact.isect_offset_encode(want[1], C, tw, th).reshape(-1))
+
+
+@pytest.mark.parametrize("counts", [
+    # mean 983 rows a tile: the 3,072-row LDS (1, 3, 6 or 12 keys a thread,
+    # then global scratch)
+    (200, 700, 1400, 2800, 6000, 100, 100, 100, 100, 100, 100, 100),
+    # mean 2,950: the 4,096-row LDS (2, 4, 8 or 16 keys a thread, then global
+    # scratch)
+    (200, 700, 1500, 3000, 6000, 4000, 4000, 4000, 4000, 4000, 2000, 2000),
+])
+def test_tile_depth_sort_every_path(counts):
+    """Rows of radius 2 px at tile centres, so every row lands in one tile and
+    each tile of the 3 x 4 image holds the given number of rows.  The mean
+    tile depth picks the LDS capacity of the per-tile depth sort, and the
+    tiles' sizes take every path of that capacity.  Depths are quantised
+    (ties stay in row order) and a third of them negative (zero-extended
+    bits order after every positive depth, IntersectTile.cu:190-192).  Ids,
+    rows and offsets must equal the oracle's."""
+    from gsplat_amd.cuda import _ops
+    rng = np.random.default_rng(sum(counts))
+    C, ts, tw, th = 1, 16, 4, 3
+    W, H = tw * ts, th * ts
+    tile_of = np.repeat(np.arange(tw * th), counts)
+    rng.shuffle(tile_of)
+    N = tile_of.size
+    cx = (tile_of % tw) * ts + 8 + rng.uniform(-4, 4, N)
+    cy = (tile_of // tw) * ts + 8 + rng.uniform(-4, 4, N)
+    means2d = np.stack([cx, cy], -1)[None].astype(np.float32)
+    radii = np.full((C, N, 2), 2, dtype=np.int32)
+    depths = (np.round(rng.uniform(-2, 4, (C, N)) * 16) / 16).astype(np.float32)
+    want = exact.isect_tiles(means2d, radii, depths, ts, tw, th)
+    np.testing.assert_array_equal(np.bincount(want[1] >> 32, minlength=tw * th), counts)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    tpg = torch.empty((C, N), dtype=torch.int32, device=DEV)
+    state = _ops.isect_prepare_sorted(t(means2d), t(radii), t(depths), None, None,
+                                      None, N, C, ts, tw, th, tpg)
     got = _ops.isect_emit_sorted(state)
     _compare(got[:3], want)
     np.testing.assert_array_equal(got[3].cpu().numpy().reshape(-1),
