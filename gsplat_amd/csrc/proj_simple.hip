@@ -85,6 +85,10 @@ __global__ void __launch_bounds__(kSimpleThreads)
     covars2d[r * 4 + 3] = a11 * j11 + a12 * j12;
 }
 
+// The backward runs in double from the float32 inputs: dL/dS = J^T G J and
+// the Jacobian VJP sum terms that cancel (float32 put single elements of
+// v_covars past rtol 1e-4 where the float32 restatement of the same math
+// stays within it).  The clamp decisions are the forward's float32 ones.
 __global__ void __launch_bounds__(kSimpleThreads)
     proj_simple_bwd_kernel(int64_t rows, int64_t N, const float *__restrict__ means,
                            const float *__restrict__ covars,
@@ -97,42 +101,44 @@ __global__ void __launch_bounds__(kSimpleThreads)
     if (r >= rows)
         return;
     const float *K = Ks + (r / N) * 9;
-    const float fx = K[0], cx = K[2], fy = K[4], cy = K[5];
-    (void)cx;
-    (void)cy;
-    const float x = means[r * 3 + 0], y = means[r * 3 + 1], z = means[r * 3 + 2];
-    float S[9];
+    const float fxf = K[0], cxf = K[2], fyf = K[4], cyf = K[5];
+    const double fx = fxf, fy = fyf;
+    const float xf = means[r * 3 + 0], yf = means[r * 3 + 1], zf = means[r * 3 + 2];
+    const double x = xf, y = yf, z = zf;
+    double S[9];
 #pragma unroll
     for (int k = 0; k < 9; ++k)
         S[k] = covars[r * 9 + k];
-    const float gm0 = v_means2d[r * 2 + 0], gm1 = v_means2d[r * 2 + 1];
-    const float G[4] = {v_covars2d[r * 4 + 0], v_covars2d[r * 4 + 1],
-                        v_covars2d[r * 4 + 2], v_covars2d[r * 4 + 3]};
-    float j00, j11, j02, j12;
-    float rz = 0.f, rz2 = 0.f, tx = 0.f, ty = 0.f;
+    const double gm0 = v_means2d[r * 2 + 0], gm1 = v_means2d[r * 2 + 1];
+    const double G[4] = {v_covars2d[r * 4 + 0], v_covars2d[r * 4 + 1],
+                         v_covars2d[r * 4 + 2], v_covars2d[r * 4 + 3]};
+    double j00, j11, j02, j12;
+    double rz = 0.0, rz2 = 0.0, tx = 0.0, ty = 0.0;
     bool in_x = true, in_y = true;
     if (ortho) {
         j00 = fx;
         j11 = fy;
-        j02 = 0.f;
-        j12 = 0.f;
+        j02 = 0.0;
+        j12 = 0.0;
     } else {
-        const PinholeLimits L = pinhole_limits(fx, fy, cx, cy, W, H);
-        rz = 1.f / z;
-        rz2 = rz * rz;
-        const float ux = x * rz, uy = y * rz;
+        // the forward's float32 clamp (limits and x/z, y/z)
+        const PinholeLimits L = pinhole_limits(fxf, fyf, cxf, cyf, W, H);
+        const float rzf = 1.f / zf;
+        const float ux = xf * rzf, uy = yf * rzf;
         in_x = ux <= L.lim_x_pos && ux >= -L.lim_x_neg;
         in_y = uy <= L.lim_y_pos && uy >= -L.lim_y_neg;
-        tx = z * fminf(L.lim_x_pos, fmaxf(-L.lim_x_neg, ux));
-        ty = z * fminf(L.lim_y_pos, fmaxf(-L.lim_y_neg, uy));
+        rz = 1.0 / z;
+        rz2 = rz * rz;
+        tx = z * (double)fminf(L.lim_x_pos, fmaxf(-L.lim_x_neg, ux));
+        ty = z * (double)fminf(L.lim_y_pos, fmaxf(-L.lim_y_neg, uy));
         j00 = fx * rz;
         j11 = fy * rz;
         j02 = -fx * tx * rz2;
         j12 = -fy * ty * rz2;
     }
     // dL/dS = J^T G J   (J: rows (j00, 0, j02), (0, j11, j12))
-    const float Jm[6] = {j00, 0.f, j02, 0.f, j11, j12};
-    float GJ[6];  // G J (2x3)
+    const double Jm[6] = {j00, 0.0, j02, 0.0, j11, j12};
+    double GJ[6];  // G J (2x3)
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
         GJ[c] = G[0] * Jm[c] + G[1] * Jm[3 + c];
@@ -142,22 +148,22 @@ __global__ void __launch_bounds__(kSimpleThreads)
     for (int i = 0; i < 3; ++i)
 #pragma unroll
         for (int c = 0; c < 3; ++c)
-            v_covars[r * 9 + i * 3 + c] = Jm[i] * GJ[c] + Jm[3 + i] * GJ[3 + c];
+            v_covars[r * 9 + i * 3 + c] = (float)(Jm[i] * GJ[c] + Jm[3 + i] * GJ[3 + c]);
 
     if (ortho) {
-        v_means[r * 3 + 0] = fx * gm0;
-        v_means[r * 3 + 1] = fy * gm1;
+        v_means[r * 3 + 0] = (float)(fx * gm0);
+        v_means[r * 3 + 1] = (float)(fy * gm1);
         v_means[r * 3 + 2] = 0.f;
         return;
     }
     // dL/dJ = G J S^T + G^T J S; only J00, J11, J02, J12 depend on the mean
-    float GtJ[6];  // G^T J
+    double GtJ[6];  // G^T J
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
         GtJ[c] = G[0] * Jm[c] + G[2] * Jm[3 + c];
         GtJ[3 + c] = G[1] * Jm[c] + G[3] * Jm[3 + c];
     }
-    float vJ[6];
+    double vJ[6];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -166,28 +172,28 @@ __global__ void __launch_bounds__(kSimpleThreads)
                              GJ[i * 3 + 2] * S[c * 3 + 2]) +
                             (GtJ[i * 3 + 0] * S[0 * 3 + c] + GtJ[i * 3 + 1] * S[1 * 3 + c] +
                              GtJ[i * 3 + 2] * S[2 * 3 + c]);
-    const float rz3 = rz2 * rz;
-    float vx = fx * rz * gm0;
-    float vy = fy * rz * gm1;
-    float vz = -(fx * x * gm0 + fy * y * gm1) * rz2;
+    const double rz3 = rz2 * rz;
+    double vx = fx * rz * gm0;
+    double vy = fy * rz * gm1;
+    double vz = -(fx * x * gm0 + fy * y * gm1) * rz2;
     // J00 = fx/z, J11 = fy/z
     vz += -fx * rz2 * vJ[0] - fy * rz2 * vJ[4];
     // J02 = -fx tx/z^2 with tx = x inside the clamp, z*limit outside it
     if (in_x) {
         vx += -fx * rz2 * vJ[2];
-        vz += 2.f * fx * tx * rz3 * vJ[2];
+        vz += 2.0 * fx * tx * rz3 * vJ[2];
     } else {
         vz += fx * tx * rz3 * vJ[2];
     }
     if (in_y) {
         vy += -fy * rz2 * vJ[5];
-        vz += 2.f * fy * ty * rz3 * vJ[5];
+        vz += 2.0 * fy * ty * rz3 * vJ[5];
     } else {
         vz += fy * ty * rz3 * vJ[5];
     }
-    v_means[r * 3 + 0] = vx;
-    v_means[r * 3 + 1] = vy;
-    v_means[r * 3 + 2] = vz;
+    v_means[r * 3 + 0] = (float)vx;
+    v_means[r * 3 + 1] = (float)vy;
+    v_means[r * 3 + 2] = (float)vz;
 }
 
 int check_camera_model(int32_t camera_model, const char *what) {

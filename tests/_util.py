@@ -110,7 +110,9 @@ def assert_grad_close(got, ref64, ref32, rtol, atol, name):
         most max(1, 1.5x) the float32 restatement's and the largest at most
         max(1, 2x): the worst elements are sums whose terms cancel by two
         to three orders of magnitude, and two float32 summation orders of the
-        same terms land up to ~2x apart on them.
+        same terms land up to ~2x apart on them;
+      * where the float32 restatement holds rtol/atol on every element, the
+        gradient must too (the elementwise tolerance as a hard gate).
 
     Returns the report line."""
     a = got.detach().double().cpu()
@@ -135,6 +137,8 @@ def assert_grad_close(got, ref64, ref32, rtol, atol, name):
            f"{r.reshape(-1)[worst].item():.9g}, float32 {r32.reshape(-1)[worst].item():.9g}")
     print("[grad gate]", msg)  # shown with pytest -rP
     assert frac >= frac32 - GRAD_STRICT_SLACK, msg
+    if frac32 == 1.0:
+        assert frac == 1.0, "elementwise tolerance (float32 holds it): " + msg
     assert mx <= max(1.0, GRAD_MAX_RATIO * mx32), msg
     assert rms <= max(1.0, GRAD_RMS_RATIO * rms32), msg
     return msg
