@@ -113,11 +113,11 @@ _SIGNATURES = {
     "gsplat_rasterize_fwd_replay": [
         c_int64, c_int64, c_int64, c_int32, _P, _P, _P, _P, _P, _P,
         c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P, _P,
-        c_size_t, _P],
+        c_size_t, c_int32, _P],
     "gsplat_rasterize_bwd_replay": [
         c_int64, c_int64, c_int64, c_int32, _P, _P, _P, _P, _P, _P,
         c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P,
-        _P, _P, _P, _P, _P, _P, _P, c_size_t, _P],
+        _P, _P, _P, _P, _P, _P, _P, c_size_t, _P, c_int32, _P],
     "gsplat_quat_scale_to_covar_preci_fwd": [c_int64, _P, _P, c_int32, _P, _P, _P],
     "gsplat_quat_scale_to_covar_preci_bwd": [
         c_int64, _P, _P, c_int32, _P, _P, _P, _P, _P],

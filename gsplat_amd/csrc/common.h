@@ -24,6 +24,9 @@ constexpr float kMaxAlpha = 0.99f;
 constexpr float kTransmittanceThreshold = 1e-4f;
 constexpr float kMinCompensation = 0.005f;
 constexpr float kMinOneMinusAlpha = 1e-6f;
+// clamp of the alpha that divides the expected depth (render_alphas.clamp(
+// min=1e-10), gsplat/rendering.py:1259-1267)
+constexpr float kMinExpectedDepthAlpha = 1e-10f;
 
 constexpr int kWave = 64;
 

@@ -45,6 +45,13 @@ struct RasterArgs {
     const uint8_t *masks;
     int32_t W, H, tile_size, tile_width, tile_height;
     const int32_t *tile_offsets, *flatten_ids;
+    // Expected depth (render modes ED, RGB+ED): the forward writes colour
+    // channel ed_channel divided by max(alpha, 1e-10), the division
+    // rendering.py:1259-1267 applies to the render; the backward takes the
+    // gradient of that output (ed_out: the forward's render_colors) back
+    // through it.  -1: no channel is divided.
+    int32_t ed_channel = -1;
+    const float *ed_out = nullptr;
 };
 
 // Replay state written by the forward for a backward split into units of
@@ -400,12 +407,23 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
         }
     }
     if (inside) {
-        render_alphas[pix] = 1.f - T;
+        const float alpha_out = 1.f - T;
+        render_alphas[pix] = alpha_out;
+        // the expected-depth channel over the clamped alpha, in the render's
+        // float32 as the reference's division (rendering.py:1259-1267)
+        float v_ed = 0.f;
 #pragma unroll
-        for (int k = 0; k < CDIM; ++k)
-            render_colors[pix * CDIM + k] =
-                a.backgrounds ? acc[k] + T * a.backgrounds[image * CDIM + k]
-                              : acc[k];
+        for (int k = 0; k < CDIM; ++k) {
+            const float v = a.backgrounds ? acc[k] + T * a.backgrounds[image * CDIM + k]
+                                          : acc[k];
+            if (k == a.ed_channel)
+                v_ed = v;
+            else
+                render_colors[pix * CDIM + k] = v;
+        }
+        if (a.ed_channel >= 0)
+            render_colors[pix * CDIM + a.ed_channel] =
+                v_ed / fmaxf(alpha_out, kMinExpectedDepthAlpha);
         last_ids[pix] = cur_idx;
         if (render_T != nullptr)
             render_T[pix] = T;
@@ -611,15 +629,35 @@ __device__ __forceinline__ void rasterize_bwd_tile(
         T[p] = T_final;
         bin_final[p] = inside ? last_ids[pix] : -1;
         wave_bin = max(wave_bin, bin_final[p]);
-        float bg_dot = 0.f;
 #pragma unroll
-        for (int k = 0; k < CDIM; ++k) {
+        for (int k = 0; k < CDIM; ++k)
             v_c[p][k] = inside ? v_render_colors[pix * CDIM + k] : 0.f;
-            if (a.backgrounds)
+        float v_a = (inside && v_render_alphas != nullptr) ? v_render_alphas[pix]
+                                                           : 0.f;
+        if (a.ed_channel >= 0 && inside) {
+            // out = v / max(alpha, 1e-10): dL/dv = g / den, and the alpha
+            // output gets -g v / den^2 = -(g / den) out where the clamp
+            // passes.  This runs for every unit of a tile, so g / den is the
+            // hardware reciprocal (1 ulp) times g, not a division sequence.
+            const float alpha_out = 1.f - T_final;
+            const float den = fmaxf(alpha_out, kMinExpectedDepthAlpha);
+            float g = 0.f;
+#pragma unroll
+            for (int k = 0; k < CDIM; ++k)
+                g = k == a.ed_channel ? v_c[p][k] : g;
+            const float gd = g * __builtin_amdgcn_rcpf(den);
+#pragma unroll
+            for (int k = 0; k < CDIM; ++k)
+                v_c[p][k] = k == a.ed_channel ? gd : v_c[p][k];
+            if (alpha_out >= kMinExpectedDepthAlpha)
+                v_a -= gd * a.ed_out[pix * CDIM + a.ed_channel];
+        }
+        float bg_dot = 0.f;
+        if (a.backgrounds) {
+#pragma unroll
+            for (int k = 0; k < CDIM; ++k)
                 bg_dot += a.backgrounds[image * CDIM + k] * v_c[p][k];
         }
-        const float v_a = (inside && v_render_alphas != nullptr) ? v_render_alphas[pix]
-                                                                 : 0.f;
         // d loss / d alpha_g = T_g (c_g . v_c) - (B_g - K) / (1 - alpha_g)
         // with B_g = sum over the Gaussians behind g (already replayed) of
         // (c . v_c) alpha T, and K = T_final (v_alpha - bg . v_c): the
@@ -1271,7 +1309,7 @@ extern "C" int gsplat_rasterize_fwd_replay(
     int32_t tile_width, int32_t tile_height, const int32_t *tile_offsets,
     const int32_t *flatten_ids, float *render_colors, float *render_alphas,
     int32_t *last_ids, float *render_transmittance, void *replay,
-    size_t replay_bytes, gsplat_stream_t stream) {
+    size_t replay_bytes, int32_t expected_depth_channel, gsplat_stream_t stream) {
     clear_error();
     RasterArgs a{I, n_rows, n_isects, means2d, conics, colors, opacities,
                  backgrounds, masks, image_width, image_height, tile_size,
@@ -1279,6 +1317,9 @@ extern "C" int gsplat_rasterize_fwd_replay(
     GS_TRY(check_raster(a, cdim));
     GS_REQUIRE(render_transmittance != nullptr,
                "rasterize_fwd_replay: NULL render_transmittance");
+    GS_REQUIRE(expected_depth_channel >= -1 && expected_depth_channel < cdim,
+               "rasterize_fwd_replay: expected_depth_channel out of range");
+    a.ed_channel = expected_depth_channel;
     ReplayState rs{};
     GS_TRY(replay_state(replay, replay_bytes, a, cdim, &rs));
     return rasterize_fwd_impl(a, cdim, render_colors, render_alphas, last_ids,
@@ -1319,6 +1360,7 @@ extern "C" int gsplat_rasterize_bwd_replay(
     const float *v_render_alphas, float *v_means2d_abs, float *v_means2d,
     float *v_conics, float *v_colors, float *v_opacities,
     uint32_t *tile_counter, const void *replay, size_t replay_bytes,
+    const float *render_colors, int32_t expected_depth_channel,
     gsplat_stream_t stream) {
     clear_error();
     RasterArgs a{I, n_rows, n_isects, means2d, conics, colors, opacities,
@@ -1327,6 +1369,12 @@ extern "C" int gsplat_rasterize_bwd_replay(
     GS_TRY(check_raster(a, cdim));
     GS_REQUIRE(render_transmittance != nullptr,
                "rasterize_bwd_replay: NULL render_transmittance");
+    GS_REQUIRE(expected_depth_channel >= -1 && expected_depth_channel < cdim,
+               "rasterize_bwd_replay: expected_depth_channel out of range");
+    GS_REQUIRE(expected_depth_channel < 0 || render_colors != nullptr,
+               "rasterize_bwd_replay: the expected-depth channel needs render_colors");
+    a.ed_channel = expected_depth_channel;
+    a.ed_out = render_colors;
     GS_REQUIRE(tile_counter != nullptr,
                "rasterize_bwd_replay: NULL tile_counter (the units are taken "
                "from it)");

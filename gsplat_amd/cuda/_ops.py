@@ -887,10 +887,13 @@ def rasterize_fwd_replay(
     tile_size: int,
     tile_offsets: Tensor,
     flatten_ids: Tensor,
+    expected_depth_channel: int = -1,
 ) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """``rasterize_fwd_with_transmittance`` that also fills the replay state of
     ``rasterize_bwd_replay`` (per-pixel records at every batch boundary of a
-    tile and the list of replay units); returns it as a fifth output."""
+    tile and the list of replay units); returns it as a fifth output.  With
+    ``expected_depth_channel`` >= 0 that channel of the render is divided by
+    max(alpha, 1e-10) (rendering.py:1259-1267)."""
     image_dims, I, n_rows, tw, th = _raster_common(
         means2d, conics, colors, opacities, backgrounds, masks, tile_offsets,
         flatten_ids)
@@ -909,7 +912,7 @@ def rasterize_fwd_replay(
          ptr(backgrounds), ptr(masks), W, H, int(tile_size), tw, th,
          ptr(tile_offsets), ptr(flatten_ids), ptr(renders), ptr(alphas),
          ptr(last_ids), ptr(transmittance), ptr(replay), replay.numel(),
-         _stream(means2d))
+         int(expected_depth_channel), _stream(means2d))
     return renders, alphas, last_ids, transmittance, replay
 
 
@@ -1014,10 +1017,14 @@ def rasterize_bwd_replay(
     v_render_colors: Tensor,
     v_render_alphas: Optional[Tensor],
     absgrad: bool,
+    render_colors: Optional[Tensor] = None,
+    expected_depth_channel: int = -1,
 ):
     """``rasterize_to_pixels_3dgs_bwd`` from the state of
     ``rasterize_fwd_replay`` on the same inputs: the replay runs one unit per
-    forward batch instead of one per tile."""
+    forward batch instead of one per tile.  With ``expected_depth_channel``
+    >= 0 (the forward's, whose ``render_colors`` must be given) the colour
+    gradient of that channel is taken through its division by the alpha."""
     image_dims, I, n_rows, tw, th = _raster_common(
         means2d, conics, colors, opacities, backgrounds, masks, tile_offsets,
         flatten_ids)
@@ -1026,6 +1033,10 @@ def rasterize_bwd_replay(
     check_input(replay, "replay", torch.uint8)
     check_input(v_render_colors, "v_render_colors", _F32)
     check_input(v_render_alphas, "v_render_alphas", _F32)
+    check_input(render_colors, "render_colors", _F32)
+    if expected_depth_channel >= 0 and (
+            render_colors is None or render_colors.shape != v_render_colors.shape):
+        raise RuntimeError("the expected-depth channel needs the forward's render_colors")
     channels = colors.shape[-1]
     likes = [means2d, conics, colors, opacities] + ([means2d] if absgrad else [])
     sizes = [t.numel() for t in likes] + [1]
@@ -1041,7 +1052,8 @@ def rasterize_bwd_replay(
          ptr(render_transmittance), ptr(last_ids), ptr(v_render_colors),
          ptr(v_render_alphas), ptr(v_means2d_abs), ptr(v_means2d),
          ptr(v_conics), ptr(v_colors), ptr(v_opacities), ptr(tile_counter),
-         ptr(replay), replay.numel(), _stream(means2d))
+         ptr(replay), replay.numel(), ptr(render_colors), int(expected_depth_channel),
+         _stream(means2d))
     return v_means2d_abs, v_means2d, v_conics, v_colors, v_opacities
 
 

@@ -314,6 +314,32 @@ def rasterize_to_pixels(
     more than 33 channels are rendered in 32-channel chunks (for absgrad, the
     chunks' |dL/dmean2d| are summed).
     """
+    return _rasterize_to_pixels(
+        means2d, conics, colors, opacities, image_width, image_height, tile_size,
+        isect_offsets, flatten_ids, backgrounds, masks, packed, absgrad)
+
+
+def _rasterize_to_pixels(
+    means2d: Tensor,
+    conics: Tensor,
+    colors: Tensor,
+    opacities: Tensor,
+    image_width: int,
+    image_height: int,
+    tile_size: int,
+    isect_offsets: Tensor,
+    flatten_ids: Tensor,
+    backgrounds: Optional[Tensor] = None,
+    masks: Optional[Tensor] = None,
+    packed: bool = False,
+    absgrad: bool = False,
+    expected_depth_channel: int = -1,
+) -> Tuple[Tensor, Tensor]:
+    """rasterize_to_pixels; with ``expected_depth_channel`` >= 0 (at most 33
+    channels) that channel of the render comes out divided by
+    max(alpha, 1e-10), the expected depth rasterization() forms for render
+    modes ED and RGB+ED (rendering.py:1259-1267), inside the rasterizer
+    kernels instead of by torch ops on the render and their backward."""
     image_dims = means2d.shape[:-2]
     channels = colors.shape[-1]
     device = means2d.device
@@ -364,7 +390,7 @@ def rasterize_to_pixels(
         rc, ra = _RasterizeToPixels.apply(
             means2d, conics, cols.contiguous(), opacities, bgs, masks,
             image_width, image_height, tile_size, isect_offsets, flatten_ids,
-            absgrad,
+            absgrad, expected_depth_channel,
         )
         if pc != c:
             rc = rc[..., :c]
@@ -372,6 +398,9 @@ def rasterize_to_pixels(
 
     if channels <= SUPPORTED_CHANNELS[-1]:
         return one(colors, backgrounds)
+    if expected_depth_channel >= 0:
+        raise ValueError("the in-kernel expected depth takes at most "
+                         f"{SUPPORTED_CHANNELS[-1]} channels")
     outs, alphas = [], None
     for s in range(0, channels, CHANNEL_CHUNK):
         rc, ra = one(
@@ -860,7 +889,8 @@ class _RasterizeToPixels(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, means2d, conics, colors, opacities, backgrounds, masks,
-                width, height, tile_size, isect_offsets, flatten_ids, absgrad):
+                width, height, tile_size, isect_offsets, flatten_ids, absgrad,
+                ed_channel=-1):
         # With gradients ahead the forward also keeps the replay state, so
         # the backward runs one unit per forward batch instead of one per
         # tile (the reference replays whole tiles).
@@ -868,16 +898,22 @@ class _RasterizeToPixels(torch.autograd.Function):
             render_colors, render_alphas, last_ids, render_T, replay = \
                 _ops.rasterize_fwd_replay(
                     means2d, conics, colors, opacities, backgrounds, masks,
-                    width, height, tile_size, isect_offsets, flatten_ids)
+                    width, height, tile_size, isect_offsets, flatten_ids,
+                    expected_depth_channel=ed_channel)
         else:
             render_colors, render_alphas, last_ids, render_T = \
                 _ops.rasterize_fwd_with_transmittance(
                     means2d, conics, colors, opacities, backgrounds, masks,
                     width, height, tile_size, isect_offsets, flatten_ids)
             replay = None
+            if ed_channel >= 0:
+                # no backward: the division in place (rendering.py:1259-1267)
+                render_colors[..., ed_channel] /= render_alphas[..., 0].clamp(min=1e-10)
         ctx.save_for_backward(means2d, conics, colors, opacities, backgrounds,
                               masks, isect_offsets, flatten_ids, render_T,
-                              last_ids, replay)
+                              last_ids, replay,
+                              render_colors if ed_channel >= 0 else None)
+        ctx.ed_channel = ed_channel
         ctx.width = width
         ctx.height = height
         ctx.tile_size = tile_size
@@ -890,9 +926,9 @@ class _RasterizeToPixels(torch.autograd.Function):
     def backward(ctx, v_render_colors: Optional[Tensor],
                  v_render_alphas: Optional[Tensor]):
         (means2d, conics, colors, opacities, backgrounds, masks, isect_offsets,
-         flatten_ids, render_T, last_ids, replay) = ctx.saved_tensors
+         flatten_ids, render_T, last_ids, replay, render_colors) = ctx.saved_tensors
         if v_render_colors is None and v_render_alphas is None:
-            return (None,) * 12
+            return (None,) * 13
         if v_render_colors is None:
             v_render_colors = render_T.new_zeros((*render_T.shape, colors.shape[-1]))
         v_alphas = None if v_render_alphas is None else v_render_alphas.contiguous()
@@ -902,7 +938,8 @@ class _RasterizeToPixels(torch.autograd.Function):
                 means2d, conics, colors, opacities, backgrounds, masks, ctx.width,
                 ctx.height, ctx.tile_size, isect_offsets, flatten_ids,
                 render_T, last_ids, replay, v_render_colors.contiguous(), v_alphas,
-                ctx.absgrad)
+                ctx.absgrad, render_colors=render_colors,
+                expected_depth_channel=ctx.ed_channel)
         else:
             # render_alphas = 1 - T is only read when T is absent; T's storage
             # stands in for it to satisfy the op's checks
@@ -925,4 +962,4 @@ class _RasterizeToPixels(torch.autograd.Function):
         else:
             v_backgrounds = None
         return (v_means2d, v_conics, v_colors, v_opacities, v_backgrounds,
-                None, None, None, None, None, None, None)
+                None, None, None, None, None, None, None, None)

@@ -21,12 +21,14 @@ from typing_extensions import Literal
 
 from .cuda import _ops
 from .cuda._wrapper import (
+    SUPPORTED_CHANNELS,
     CameraModel,
     Grad2dStatsSlot,
     _PackedFrontEnd,
     _PackedRowsGather,
     _PackedSphericalHarmonics,
     _project,
+    _rasterize_to_pixels,
     isect_offset_encode,
     isect_tiles,
     rasterize_to_pixels,
@@ -378,7 +380,16 @@ def rasterization(
         "n_batches": B, "n_cameras": C,
     })
 
-    if proj_features.shape[-1] > channel_chunk:
+    # the expected depth divided by the alpha inside the rasterizer
+    # (rendering.py:1259-1267 forms it with torch ops on the render)
+    ed_in_kernel = (render_mode_has_expected_depth(render_mode) and extra_signals is None
+                    and proj_features.shape[-1] <= min(channel_chunk, SUPPORTED_CHANNELS[-1]))
+    if ed_in_kernel:
+        render_colors, render_alphas = _rasterize_to_pixels(
+            means2d, conics, proj_features, opacities, width, height, tile_size,
+            isect_offsets, flatten_ids, backgrounds=backgrounds, packed=packed,
+            absgrad=absgrad, expected_depth_channel=proj_features.shape[-1] - 1)
+    elif proj_features.shape[-1] > channel_chunk:
         n_chunks = (proj_features.shape[-1] + channel_chunk - 1) // channel_chunk
         render_colors, render_alphas = [], []
         for i in range(n_chunks):
@@ -408,7 +419,7 @@ def rasterization(
             render_colors = torch.cat([render_colors[..., 0:D], render_depth], dim=-1)
         else:
             render_colors = render_colors[..., 0:D]
-    elif render_mode_has_expected_depth(render_mode):
+    elif render_mode_has_expected_depth(render_mode) and not ed_in_kernel:
         render_colors = torch.cat(
             [render_colors[..., :-1],
              render_colors[..., -1:] / render_alphas.clamp(min=1e-10)], dim=-1)

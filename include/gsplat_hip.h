@@ -614,7 +614,14 @@ int gsplat_rasterize_bwd(
  *   render_transmittance, tile_counter and the replay workspace of the
  *   forward call on the same inputs all required (render_alphas is not
  *   needed).  The gradients agree with gsplat_rasterize_bwd's to float32
- *   summation order. */
+ *   summation order.
+ * expected_depth_channel (-1 for none; no counterpart in the reference op,
+ *   whose caller does this in torch, gsplat/rendering.py:1259-1267): the
+ *   forward writes that colour channel divided by max(alpha, 1e-10), the
+ *   expected depth of render modes ED and RGB+ED, and the backward (given
+ *   the forward's render_colors and the same channel) takes
+ *   v_render_colors as the gradient of that divided output, adding the
+ *   division's alpha term to the alpha gradient. */
 size_t gsplat_rasterize_replay_size(
     int64_t I, int32_t tile_width, int32_t tile_height, int32_t tile_size,
     int64_t n_isects, int32_t cdim);
@@ -628,7 +635,7 @@ int gsplat_rasterize_fwd_replay(
     const int32_t *tile_offsets, const int32_t *flatten_ids,
     float *render_colors, float *render_alphas, int32_t *last_ids,
     float *render_transmittance, void *replay, size_t replay_bytes,
-    gsplat_stream_t stream);
+    int32_t expected_depth_channel, gsplat_stream_t stream);
 
 int gsplat_rasterize_bwd_replay(
     int64_t I, int64_t n_rows, int64_t n_isects, int32_t cdim,
@@ -641,7 +648,8 @@ int gsplat_rasterize_bwd_replay(
     const float *v_render_colors, const float *v_render_alphas,
     float *v_means2d_abs, float *v_means2d, float *v_conics,
     float *v_colors, float *v_opacities, uint32_t *tile_counter,
-    const void *replay, size_t replay_bytes, gsplat_stream_t stream);
+    const void *replay, size_t replay_bytes, const float *render_colors,
+    int32_t expected_depth_channel, gsplat_stream_t stream);
 
 /* Rasterize to indices: the (Gaussian, pixel) pairs each pixel composites
  * over the isect batches [range_start, range_end) of its tile (batches of

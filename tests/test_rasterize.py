@@ -136,6 +136,58 @@ def test_rasterize_last_ids_match_oracle():
                                   (np.float32(1.0) - info["transmittance"]).astype(np.float32))
 
 
+@pytest.mark.parametrize("D,bg,packed", [(4, False, True), (4, True, False), (1, False, True)])
+def test_rasterize_expected_depth_in_kernel(D, bg, packed):
+    """The expected-depth channel divided by max(alpha, 1e-10) inside the
+    rasterizer (render modes RGB+ED and ED) against the reference's torch
+    form of it (rendering.py:1259-1267) applied to the float64 and float32
+    restatements: render within rtol/atol, gradients through the gate, and
+    the render bit for bit equal to the same division by torch of the plain
+    kernel's output."""
+    from gsplat_amd.cuda._wrapper import _rasterize_to_pixels, rasterize_to_pixels
+    data = projected_2d(seed=70 + D, N=2000, C=2, D=D, packed=packed)
+    W, H, ts, C = data["W"], data["H"], data["tile"], data["C"]
+    m2, con, op, col = data["means2d"], data["conics"], data["opacities"], data["colors"]
+    offs, fl = data["offsets"], data["flatten_ids"]
+    g = torch.Generator().manual_seed(12)
+    bgt = torch.rand(C, D, generator=g) if bg else None
+    v_rc = torch.randn(C, H, W, D, generator=g)
+    v_ra = torch.randn(C, H, W, 1, generator=g)
+
+    def ed(rc, ra):
+        return torch.cat([rc[..., :-1], rc[..., -1:] / ra.clamp(min=1e-10)], dim=-1)
+
+    outs = {}
+    for name, dtype in (("64", torch.float64), ("32", torch.float32)):
+        ins = [t.to(dtype).clone().requires_grad_() for t in (m2, con, col, op)]
+        rc, ra, _ = torch_ref.rasterize_to_pixels_ref(
+            ins[0], ins[1], ins[2], ins[3], W, H, ts, offs, fl,
+            backgrounds=None if bgt is None else bgt.to(dtype), dtype=dtype)
+        rc = ed(rc, ra)
+        ((rc * v_rc.to(dtype)).sum() + (ra * v_ra.to(dtype)).sum()).backward()
+        outs[name] = (rc.detach(), ins)
+    ins = [t.clone().to(DEV).requires_grad_() for t in (m2, con, col, op)]
+    bgd = bgt.to(DEV) if bgt is not None else None
+    rc, ra = _rasterize_to_pixels(ins[0], ins[1], ins[2], ins[3], W, H, ts, offs.to(DEV),
+                                  fl.to(DEV), backgrounds=bgd, packed=packed,
+                                  expected_depth_channel=D - 1)
+    ((rc * v_rc.to(DEV)).sum() + (ra * v_ra.to(DEV)).sum()).backward()
+    assert_close(rc.cpu(), outs["64"][0], RTOL, ATOL, "render_colors (ED)")
+    for k, name in enumerate(("v_means2d", "v_conics", "v_colors", "v_opacities")):
+        assert_grad_close(ins[k].grad, outs["64"][1][k].grad, outs["32"][1][k].grad,
+                          RTOL, ATOL, name)
+    with torch.no_grad():
+        rc0, ra0 = rasterize_to_pixels(m2.to(DEV), con.to(DEV), col.to(DEV), op.to(DEV), W,
+                                       H, ts, offs.to(DEV), fl.to(DEV), backgrounds=bgd,
+                                       packed=packed)
+        rc1, _ = _rasterize_to_pixels(m2.to(DEV), con.to(DEV), col.to(DEV), op.to(DEV), W,
+                                      H, ts, offs.to(DEV), fl.to(DEV), backgrounds=bgd,
+                                      packed=packed, expected_depth_channel=D - 1)
+    want = ed(rc0, ra0).cpu().numpy()
+    np.testing.assert_array_equal(rc.detach().cpu().numpy(), want)
+    np.testing.assert_array_equal(rc1.cpu().numpy(), want)
+
+
 def test_rasterize_unused_alpha_gradient():
     """A loss on the colours only: the alpha gradient reaches the backward as
     None (no zero tensor) and gives the same gradients as an explicit zero
