@@ -1,4 +1,4 @@
-"""BASELINE configurations 1, 3 and 4 at their full sizes on the GPU, through
+"""BASELINE configurations 1 to 4 at their full sizes on the GPU, through
 ``rasterization()`` (gsplat/rendering.py:256-1273), against the host oracle.
 
 Every full-size run is checked on all of its intersections: ``isect_ids``,
@@ -7,7 +7,7 @@ intersection of the oracle's projection (C restatement).  Pixels are checked on
 a strided sample of tiles, where the oracle composites exactly the Gaussians
 the kernels do: ``render_alphas`` bit-exact (1 - T with T the float32 running
 product), colours within rtol 1e-4 / atol 1e-5 of the float64 restatement.
-Gradients (configs 1 and 4) come from an upstream gradient that is nonzero on
+Gradients (configs 1, 2 and 4) come from an upstream gradient that is nonzero on
 the sampled tiles only, so the oracle's autograd over those tiles gives the
 whole gradient; they are held to rtol 1e-4 / atol 1e-5 at the float32 floor
 (tests/_util.py:assert_grad_close) over every Gaussian the sample touches.
@@ -52,7 +52,7 @@ def _oracle(params, transform, scene, sample, dtype, v_rc, v_ra, backward):
     rc, ra, meta = torch_ref.rasterization_ref(
         means, quats, scales, opac, colors, scene.viewmats, scene.Ks, scene.width,
         scene.height, sh_degree=scene.sh_degree, dtype=dtype, tile_subset=sample,
-        restrict_rows=True)
+        restrict_rows=True, **scene.kwargs)
     grads = None
     if backward:
         ((rc * v_rc.to(dtype)).sum() + (ra * v_ra.to(dtype)).sum()).backward()
@@ -121,6 +121,40 @@ def test_cfg1_full_size_fwd_bwd_queued_stage():
         ((rc * v_rc.to(DEV)).sum() + (ra * v_ra.to(DEV)).sum()).backward()
         print(f"[cfg1] call {call}: {meta['isect_ids'].numel()} intersections", flush=True)
         _check_forward(meta, rc, ra, meta_r, rc_r, ra_r, pix)
+    _check_grads({k: v.grad.cpu() for k, v in gl.items()}, g64, g32)
+
+
+def test_cfg2_full_size_rgb_ed_fwd_bwd():
+    """500k Gaussians, SH1, 8 cameras on a ring (960x540 each), packed,
+    render mode RGB+ED (the expected depth divided inside the rasterizer),
+    fwd+bwd: all 12M intersections over the 8 images bit-exact, pixels and
+    gradients on a tile sample spread over every camera."""
+    import gsplat_amd as gs
+    scene = make_scene(2)
+    C, H, W = scene.viewmats.shape[0], scene.height, scene.width
+    th, tw = math.ceil(H / TILE), math.ceil(W / TILE)
+    sample = _tile_sample(C, th, tw, 211)
+    assert len(np.unique(sample // (th * tw))) == C
+    pix = _pixel_mask(C, H, W, th, tw, sample)
+    g = torch.Generator().manual_seed(2)
+    v_rc = torch.randn(C, H, W, 4, generator=g) * pix[..., None]
+    v_ra = torch.randn(C, H, W, 1, generator=g) * pix[..., None]
+    params = {k: getattr(scene, k) for k in ("means", "quats", "scales", "opacities",
+                                             "colors")}
+    rc_r, ra_r, meta_r, g64 = _oracle(params, _plain, scene, sample, torch.float64,
+                                      v_rc, v_ra, True)
+    _, _, _, g32 = _oracle(params, _plain, scene, sample, torch.float32, v_rc, v_ra, True)
+    assert meta_r["n_isects"] > 10_000_000
+
+    gl = {k: v.to(DEV).requires_grad_() for k, v in params.items()}
+    rc, ra, meta = gs.rasterization(gl["means"], gl["quats"], gl["scales"],
+                                    gl["opacities"], gl["colors"],
+                                    scene.viewmats.to(DEV), scene.Ks.to(DEV), W, H,
+                                    sh_degree=scene.sh_degree, **scene.kwargs)
+    assert rc.shape == (C, H, W, 4)
+    ((rc * v_rc.to(DEV)).sum() + (ra * v_ra.to(DEV)).sum()).backward()
+    print(f"[cfg2] {meta['isect_ids'].numel()} intersections", flush=True)
+    _check_forward(meta, rc, ra, meta_r, rc_r, ra_r, pix)
     _check_grads({k: v.grad.cpu() for k, v in gl.items()}, g64, g32)
 
 
