@@ -113,7 +113,7 @@ _SIGNATURES = {
     "gsplat_rasterize_fwd_replay": [
         c_int64, c_int64, c_int64, c_int32, _P, _P, _P, _P, _P, _P,
         c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P, _P,
-        c_size_t, c_int32, _P],
+        c_size_t, c_int32, _P, c_int64, _P],
     "gsplat_rasterize_bwd_replay": [
         c_int64, c_int64, c_int64, c_int32, _P, _P, _P, _P, _P, _P,
         c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P,

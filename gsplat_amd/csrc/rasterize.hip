@@ -73,6 +73,11 @@ struct ReplayState {
     int2 *units;
     float *records;
     int32_t *tile_last;  // per tile: its last contributor's isect index, or -1
+    // optional: a buffer the forward also zero-fills, each workgroup a
+    // slice (the backward's atomic accumulators, so that no fill launch
+    // runs between the loss and the backward)
+    float *zero;
+    int64_t zero_n;
 };
 
 // Replay parts per forward batch: a part is BS / kReplayParts consecutive
@@ -253,6 +258,16 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
     const int64_t pix = ((int64_t)image * a.H + i) * a.W + j;
     const float px = (float)j + 0.5f, py = (float)i + 0.5f;
     const int64_t n_tiles = (int64_t)a.tile_width * a.tile_height;
+
+    if (rs.zero != nullptr) {
+        // this workgroup's slice of the buffer to clear; the stores drain
+        // while the tile composites
+        const int64_t per = (rs.zero_n + gridDim.x - 1) / gridDim.x;
+        const int64_t z0 = (int64_t)blockIdx.x * per;
+        const int64_t z1 = min(z0 + per, rs.zero_n);
+        for (int64_t z = z0 + tr; z < z1; z += TILE * TILE)
+            rs.zero[z] = 0.f;
+    }
 
     if (a.masks != nullptr && !a.masks[image * n_tiles + tile]) {
         if (inside) {
@@ -1151,6 +1166,12 @@ namespace {
 
 __global__ void replay_clear_kernel(uint32_t *count) { *count = 0u; }
 
+__global__ void zero_f32_kernel(float *p, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n)
+        p[i] = 0.f;
+}
+
 // Replay workspace: [count, padded to 256 B][units][records], each part
 // 256-byte aligned.
 struct ReplayLayout {
@@ -1197,8 +1218,15 @@ int rasterize_fwd_impl(const RasterArgs &a, int32_t cdim, float *render_colors,
                        float *render_alphas, int32_t *last_ids,
                        float *render_transmittance, const ReplayState &rs,
                        gsplat_stream_t stream) {
-    if (a.I == 0)
+    if (a.I == 0 || a.tile_width == 0 || a.tile_height == 0) {
+        // no tile workgroups: the buffer to clear gets a launch of its own
+        if (rs.zero != nullptr && rs.zero_n > 0) {
+            zero_f32_kernel<<<(unsigned)ceil_div(rs.zero_n, 256), 256, 0,
+                              as_stream(stream)>>>(rs.zero, rs.zero_n);
+            return check_launch("zero_f32_kernel");
+        }
         return GSPLAT_OK;
+    }
     GS_REQUIRE(render_colors && render_alphas && last_ids,
                "rasterize_fwd: NULL output");
     const int64_t blocks = a.I * (int64_t)a.tile_width * a.tile_height;
@@ -1309,7 +1337,8 @@ extern "C" int gsplat_rasterize_fwd_replay(
     int32_t tile_width, int32_t tile_height, const int32_t *tile_offsets,
     const int32_t *flatten_ids, float *render_colors, float *render_alphas,
     int32_t *last_ids, float *render_transmittance, void *replay,
-    size_t replay_bytes, int32_t expected_depth_channel, gsplat_stream_t stream) {
+    size_t replay_bytes, int32_t expected_depth_channel, float *zero_fill,
+    int64_t zero_fill_count, gsplat_stream_t stream) {
     clear_error();
     RasterArgs a{I, n_rows, n_isects, means2d, conics, colors, opacities,
                  backgrounds, masks, image_width, image_height, tile_size,
@@ -1320,8 +1349,12 @@ extern "C" int gsplat_rasterize_fwd_replay(
     GS_REQUIRE(expected_depth_channel >= -1 && expected_depth_channel < cdim,
                "rasterize_fwd_replay: expected_depth_channel out of range");
     a.ed_channel = expected_depth_channel;
+    GS_REQUIRE(zero_fill_count >= 0 && (zero_fill_count == 0 || zero_fill != nullptr),
+               "rasterize_fwd_replay: NULL zero_fill with a nonzero count");
     ReplayState rs{};
     GS_TRY(replay_state(replay, replay_bytes, a, cdim, &rs));
+    rs.zero = zero_fill_count > 0 ? zero_fill : nullptr;
+    rs.zero_n = zero_fill_count;
     return rasterize_fwd_impl(a, cdim, render_colors, render_alphas, last_ids,
                               render_transmittance, rs, stream);
 }

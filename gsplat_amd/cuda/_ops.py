@@ -888,12 +888,15 @@ def rasterize_fwd_replay(
     tile_offsets: Tensor,
     flatten_ids: Tensor,
     expected_depth_channel: int = -1,
-) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    absgrad: Optional[bool] = None,
+):
     """``rasterize_fwd_with_transmittance`` that also fills the replay state of
     ``rasterize_bwd_replay`` (per-pixel records at every batch boundary of a
     tile and the list of replay units); returns it as a fifth output.  With
     ``expected_depth_channel`` >= 0 that channel of the render is divided by
-    max(alpha, 1e-10) (rendering.py:1259-1267)."""
+    max(alpha, 1e-10) (rendering.py:1259-1267).  With ``absgrad`` not None
+    the launch also zero-fills the accumulators of ``rasterize_bwd_replay``
+    (its ``accum``, returned as a sixth output)."""
     image_dims, I, n_rows, tw, th = _raster_common(
         means2d, conics, colors, opacities, backgrounds, masks, tile_offsets,
         flatten_ids)
@@ -907,13 +910,27 @@ def rasterize_fwd_replay(
     n_isects = flatten_ids.numel()
     replay = torch.empty(query("gsplat_rasterize_replay_size", I, tw, th, int(tile_size),
                                n_isects, channels), dtype=torch.uint8, device=dev)
+    accum = None
+    if absgrad is not None:
+        accum = torch.empty(_bwd_accum_words(means2d, conics, colors, opacities, absgrad),
+                            dtype=_F32, device=dev)
     call("gsplat_rasterize_fwd_replay", I, n_rows, n_isects, channels,
          ptr(means2d), ptr(conics), ptr(colors), ptr(opacities),
          ptr(backgrounds), ptr(masks), W, H, int(tile_size), tw, th,
          ptr(tile_offsets), ptr(flatten_ids), ptr(renders), ptr(alphas),
          ptr(last_ids), ptr(transmittance), ptr(replay), replay.numel(),
-         int(expected_depth_channel), _stream(means2d))
-    return renders, alphas, last_ids, transmittance, replay
+         int(expected_depth_channel), ptr(accum), 0 if accum is None else accum.numel(),
+         _stream(means2d))
+    if absgrad is None:
+        return renders, alphas, last_ids, transmittance, replay
+    return renders, alphas, last_ids, transmittance, replay, accum
+
+
+def _bwd_accum_words(means2d, conics, colors, opacities, absgrad: bool) -> int:
+    """Floats of the backward's accumulators: v_means2d, v_conics, v_colors,
+    v_opacities (, v_means2d_abs) and the one-word unit counter."""
+    n = means2d.numel() + conics.numel() + colors.numel() + opacities.numel() + 1
+    return n + (means2d.numel() if absgrad else 0)
 
 
 def rasterize_to_pixels_3dgs_fwd(
@@ -1019,12 +1036,15 @@ def rasterize_bwd_replay(
     absgrad: bool,
     render_colors: Optional[Tensor] = None,
     expected_depth_channel: int = -1,
+    accum: Optional[Tensor] = None,
 ):
     """``rasterize_to_pixels_3dgs_bwd`` from the state of
     ``rasterize_fwd_replay`` on the same inputs: the replay runs one unit per
     forward batch instead of one per tile.  With ``expected_depth_channel``
     >= 0 (the forward's, whose ``render_colors`` must be given) the colour
-    gradient of that channel is taken through its division by the alpha."""
+    gradient of that channel is taken through its division by the alpha.
+    ``accum`` is the zeroed accumulator buffer of ``rasterize_fwd_replay``
+    (used once; None allocates a zeroed one)."""
     image_dims, I, n_rows, tw, th = _raster_common(
         means2d, conics, colors, opacities, backgrounds, masks, tile_offsets,
         flatten_ids)
@@ -1040,7 +1060,14 @@ def rasterize_bwd_replay(
     channels = colors.shape[-1]
     likes = [means2d, conics, colors, opacities] + ([means2d] if absgrad else [])
     sizes = [t.numel() for t in likes] + [1]
-    parts = torch.zeros(sum(sizes), dtype=_F32, device=means2d.device).split(sizes)
+    if accum is not None:
+        check_input(accum, "accum", _F32)
+        if accum.numel() != sum(sizes):
+            raise RuntimeError("accum does not match the backward's accumulators")
+        buf = accum
+    else:
+        buf = torch.zeros(sum(sizes), dtype=_F32, device=means2d.device)
+    parts = buf.split(sizes)
     v_means2d, v_conics, v_colors, v_opacities = (
         parts[k].view(likes[k].shape) for k in range(4))
     v_means2d_abs = parts[4].view(means2d.shape) if absgrad else None

@@ -894,12 +894,14 @@ class _RasterizeToPixels(torch.autograd.Function):
         # With gradients ahead the forward also keeps the replay state, so
         # the backward runs one unit per forward batch instead of one per
         # tile (the reference replays whole tiles).
+        accum = None
         if any(ctx.needs_input_grad[:5]):
-            render_colors, render_alphas, last_ids, render_T, replay = \
+            # the launch also zero-fills the backward's accumulators
+            render_colors, render_alphas, last_ids, render_T, replay, accum = \
                 _ops.rasterize_fwd_replay(
                     means2d, conics, colors, opacities, backgrounds, masks,
                     width, height, tile_size, isect_offsets, flatten_ids,
-                    expected_depth_channel=ed_channel)
+                    expected_depth_channel=ed_channel, absgrad=absgrad)
         else:
             render_colors, render_alphas, last_ids, render_T = \
                 _ops.rasterize_fwd_with_transmittance(
@@ -914,6 +916,9 @@ class _RasterizeToPixels(torch.autograd.Function):
                               last_ids, replay,
                               render_colors if ed_channel >= 0 else None)
         ctx.ed_channel = ed_channel
+        # zeroed by the forward, consumed by the first backward (a second
+        # backward through a retained graph takes fresh zeros)
+        ctx.accum = accum
         ctx.width = width
         ctx.height = height
         ctx.tile_size = tile_size
@@ -939,7 +944,8 @@ class _RasterizeToPixels(torch.autograd.Function):
                 ctx.height, ctx.tile_size, isect_offsets, flatten_ids,
                 render_T, last_ids, replay, v_render_colors.contiguous(), v_alphas,
                 ctx.absgrad, render_colors=render_colors,
-                expected_depth_channel=ctx.ed_channel)
+                expected_depth_channel=ctx.ed_channel, accum=ctx.accum)
+            ctx.accum = None
         else:
             # render_alphas = 1 - T is only read when T is absent; T's storage
             # stands in for it to satisfy the op's checks

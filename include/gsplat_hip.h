@@ -621,7 +621,11 @@ int gsplat_rasterize_bwd(
  *   expected depth of render modes ED and RGB+ED, and the backward (given
  *   the forward's render_colors and the same channel) takes
  *   v_render_colors as the gradient of that divided output, adding the
- *   division's alpha term to the alpha gradient. */
+ *   division's alpha term to the alpha gradient.
+ * zero_fill, zero_fill_count (NULL, 0 for none; no counterpart in the
+ *   reference): a float buffer the forward launch also sets to zero, for
+ *   the gradient accumulators gsplat_rasterize_bwd_replay adds into, so
+ *   that no fill runs between the forward and the backward. */
 size_t gsplat_rasterize_replay_size(
     int64_t I, int32_t tile_width, int32_t tile_height, int32_t tile_size,
     int64_t n_isects, int32_t cdim);
@@ -635,7 +639,8 @@ int gsplat_rasterize_fwd_replay(
     const int32_t *tile_offsets, const int32_t *flatten_ids,
     float *render_colors, float *render_alphas, int32_t *last_ids,
     float *render_transmittance, void *replay, size_t replay_bytes,
-    int32_t expected_depth_channel, gsplat_stream_t stream);
+    int32_t expected_depth_channel, float *zero_fill, int64_t zero_fill_count,
+    gsplat_stream_t stream);
 
 int gsplat_rasterize_bwd_replay(
     int64_t I, int64_t n_rows, int64_t n_isects, int32_t cdim,

@@ -188,6 +188,32 @@ def test_rasterize_expected_depth_in_kernel(D, bg, packed):
     np.testing.assert_array_equal(rc1.cpu().numpy(), want)
 
 
+def test_rasterize_backward_twice_through_retained_graph():
+    """The forward zero-fills the backward's accumulators; the first backward
+    adds into them and a second backward through the retained graph starts
+    from fresh zeros: both give the same gradients."""
+    from gsplat_amd.cuda._wrapper import rasterize_to_pixels
+    data = projected_2d(seed=61, N=2000, C=2, D=3, packed=True)
+    W, H, ts = data["W"], data["H"], data["tile"]
+    ins = [data[k].clone().to(DEV).requires_grad_()
+           for k in ("means2d", "conics", "colors", "opacities")]
+    rc, ra = rasterize_to_pixels(ins[0], ins[1], ins[2], ins[3], W, H, ts,
+                                 data["offsets"].to(DEV), data["flatten_ids"].to(DEV),
+                                 packed=True)
+    g = torch.Generator().manual_seed(4)
+    loss = (rc * torch.randn(rc.shape, generator=g).to(DEV)).sum() + \
+        (ra * torch.randn(ra.shape, generator=g).to(DEV)).sum()
+    loss.backward(retain_graph=True)
+    first = [t.grad.clone() for t in ins]
+    for t in ins:
+        t.grad = None
+    loss.backward()
+    for name, a, b in zip(("v_means2d", "v_conics", "v_colors", "v_opacities"),
+                          first, (t.grad for t in ins)):
+        assert bool(a.abs().sum() > 0), name
+        assert_close(b.cpu(), a.cpu(), RTOL, ATOL, name)
+
+
 def test_rasterize_unused_alpha_gradient():
     """A loss on the colours only: the alpha gradient reaches the backward as
     None (no zero tensor) and gives the same gradients as an explicit zero
