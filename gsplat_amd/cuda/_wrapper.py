@@ -963,7 +963,12 @@ class _RasterizeToPixels(torch.autograd.Function):
             means2d.absgrad = v_means2d_abs
             means2d._absgrad_pass = torch._C._current_graph_task_id()
         if ctx.needs_input_grad[4]:
-            v_backgrounds = (v_render_colors * render_T[..., None]).sum(
+            v_bg_colors = v_render_colors
+            if ctx.ed_channel >= 0:
+                # the divided channel: d out / d background = T / max(alpha, 1e-10)
+                v_bg_colors = v_render_colors.clone()
+                v_bg_colors[..., ctx.ed_channel] /= (1.0 - render_T).clamp(min=1e-10)
+            v_backgrounds = (v_bg_colors * render_T[..., None]).sum(
                 dim=(-3, -2))
         else:
             v_backgrounds = None

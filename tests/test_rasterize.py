@@ -160,14 +160,15 @@ def test_rasterize_expected_depth_in_kernel(D, bg, packed):
     outs = {}
     for name, dtype in (("64", torch.float64), ("32", torch.float32)):
         ins = [t.to(dtype).clone().requires_grad_() for t in (m2, con, col, op)]
+        bgr = bgt.to(dtype).clone().requires_grad_() if bg else None
         rc, ra, _ = torch_ref.rasterize_to_pixels_ref(
             ins[0], ins[1], ins[2], ins[3], W, H, ts, offs, fl,
-            backgrounds=None if bgt is None else bgt.to(dtype), dtype=dtype)
+            backgrounds=bgr, dtype=dtype)
         rc = ed(rc, ra)
         ((rc * v_rc.to(dtype)).sum() + (ra * v_ra.to(dtype)).sum()).backward()
-        outs[name] = (rc.detach(), ins)
+        outs[name] = (rc.detach(), ins, bgr)
     ins = [t.clone().to(DEV).requires_grad_() for t in (m2, con, col, op)]
-    bgd = bgt.to(DEV) if bgt is not None else None
+    bgd = bgt.to(DEV).requires_grad_() if bgt is not None else None
     rc, ra = _rasterize_to_pixels(ins[0], ins[1], ins[2], ins[3], W, H, ts, offs.to(DEV),
                                   fl.to(DEV), backgrounds=bgd, packed=packed,
                                   expected_depth_channel=D - 1)
@@ -176,6 +177,10 @@ def test_rasterize_expected_depth_in_kernel(D, bg, packed):
     for k, name in enumerate(("v_means2d", "v_conics", "v_colors", "v_opacities")):
         assert_grad_close(ins[k].grad, outs["64"][1][k].grad, outs["32"][1][k].grad,
                           RTOL, ATOL, name)
+    if bg:
+        assert_grad_close(bgd.grad, outs["64"][2].grad, outs["32"][2].grad, RTOL, ATOL,
+                          "v_backgrounds")
+        bgd = bgd.detach()
     with torch.no_grad():
         rc0, ra0 = rasterize_to_pixels(m2.to(DEV), con.to(DEV), col.to(DEV), op.to(DEV), W,
                                        H, ts, offs.to(DEV), fl.to(DEV), backgrounds=bgd,
