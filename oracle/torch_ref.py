@@ -55,6 +55,15 @@ def quat_scale_to_covar(quats: Tensor, scales: Tensor) -> Tensor:
     return M @ M.transpose(-1, -2)
 
 
+def camera_centers(viewmats: Tensor) -> Tensor:
+    """World position -R^T t of the camera of each world->camera matrix
+    [..., 4, 4] (gsplat/rendering.py:216-224); the SH view direction of a
+    Gaussian is its mean minus this point (rendering.py:227-253)."""
+    R = viewmats[..., :3, :3]
+    t = viewmats[..., :3, 3:]
+    return -(R.transpose(-1, -2) @ t)[..., 0]
+
+
 def covar6_to_mat(c6: Tensor) -> Tensor:
     a, b, c, d, e, f = torch.unbind(c6, dim=-1)
     return torch.stack([a, b, c, b, d, e, c, e, f], dim=-1).reshape(c6.shape[:-1] + (3, 3))
@@ -436,8 +445,7 @@ def rasterization_ref(means, quats, scales, opacities, colors, viewmats, Ks,
     comp_rows = torch.zeros(n_need, dtype=dtype) if calc_comp else None
     feat_parts = []
     if sh_degree is not None:
-        campos = -(viewmats[:, :3, :3].transpose(-1, -2).to(dtype)
-                   @ viewmats[:, :3, 3:].to(dtype))[..., 0]
+        campos = camera_centers(viewmats.to(dtype))
     for c in range(C):
         sel_c = np.nonzero(cam_need == c)[0]
         if sel_c.size == 0:

@@ -104,3 +104,9 @@ def test_cfg1_reduced_sh3_unpacked():
 
 def test_cfg2_reduced_multiview_rgb_ed():
     _check(_downscale(make_scene(2, n=20_000), 4), render_mode="RGB+ED")
+
+
+def test_cfg2_reduced_multiview_unpacked():
+    # the dense path's view directions (rendering.py:compute_directions) under
+    # eight look-at cameras whose rotations are not symmetric
+    _check(_downscale(make_scene(2, n=8_000), 4), packed=False)
