@@ -18,10 +18,17 @@ import torch
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libgsplat_hip.so"
 
 _P = c_void_p
+# The interface _SIGNATURES below was written against: abi.header_abi_hash()
+# of include/gsplat_hip.h.  load() refuses a library built from any other
+# header, and a CPU test keeps this digest and _SIGNATURES equal to the
+# header's.  Change all three together.
+_ABI_VERSION = "f08ef0b7db4794cc"
+
 # name -> argtypes (restype int unless listed in _RESTYPES)
 _SIGNATURES = {
     "gsplat_last_error": [],
     "gsplat_version": [],
+    "gsplat_abi_version": [],
     "gsplat_projection_simple_fwd": [
         c_int64, c_int64, c_int64, _P, _P, _P, c_int32, c_int32, c_int32, _P, _P, _P],
     "gsplat_projection_simple_bwd": [
@@ -138,6 +145,7 @@ _SIGNATURES = {
 _RESTYPES = {
     "gsplat_last_error": ctypes.c_char_p,
     "gsplat_version": ctypes.c_char_p,
+    "gsplat_abi_version": ctypes.c_char_p,
     "gsplat_projection_packed_workspace_size": c_size_t,
     "gsplat_rasterize_replay_size": c_size_t,
     "gsplat_projection_packed_fwd_noalloc_max_rows": c_int64,
@@ -169,17 +177,37 @@ class AdamTensor(ctypes.Structure):
 _lib: Optional[ctypes.CDLL] = None
 
 
+_REBUILD = "build it with `python gsplat_amd/build.py`"
+
+
 def load() -> ctypes.CDLL:
-    """Load libgsplat_hip.so (once) and declare its signatures."""
+    """Load libgsplat_hip.so (once), check that it was built from the
+    interface this binding was written against, and declare its signatures.
+    A library of another interface is refused before any entry point is
+    bound or called."""
     global _lib
     if _lib is not None:
         return _lib
     if not LIB_PATH.exists():
         raise RuntimeError(
-            f"{LIB_PATH} is missing: build it with `python -m gsplat_amd.build` "
+            f"{LIB_PATH} is missing: {_REBUILD} "
             "(the HIP kernels are the only implementation; there is no fallback)"
         )
     lib = ctypes.CDLL(str(LIB_PATH))
+    try:
+        abi_fn = lib.gsplat_abi_version
+    except AttributeError:
+        raise RuntimeError(
+            f"{LIB_PATH} reports no interface version (gsplat_abi_version is "
+            f"missing); this binding expects ABI {_ABI_VERSION}: {_REBUILD}") from None
+    abi_fn.argtypes = []
+    abi_fn.restype = ctypes.c_char_p
+    got = (abi_fn() or b"").decode(errors="replace")
+    if got != _ABI_VERSION:
+        raise RuntimeError(
+            f"{LIB_PATH} was built from interface ABI {got}, but this binding "
+            f"(gsplat_amd/_lib.py) was written for ABI {_ABI_VERSION}; calling it "
+            f"could pass arguments of the wrong type: {_REBUILD}")
     for name, argtypes in _SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = argtypes

@@ -6,7 +6,8 @@ linked into ``gsplat_amd/lib/libgsplat_hip.so``, the C-ABI library declared in
 it can be loaded from any host language; the Python package reaches it through
 ``ctypes`` (``gsplat_amd/_lib.py``).
 
-Run ``python -m gsplat_amd.build`` (or ``__graft_entry__.build()``).
+Run ``python gsplat_amd/build.py`` (or ``__graft_entry__.build()``): by path, since
+importing the package loads the library this rebuilds.
 """
 
 from __future__ import annotations
@@ -19,6 +20,19 @@ import sys
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
+
+
+def _header_abi_hash() -> str:
+    """abi.header_abi_hash(), with abi.py loaded by path: importing the
+    package would load the library that is about to be rebuilt (and refuse a
+    stale one)."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("_gsplat_amd_abi", PKG_DIR / "abi.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod.header_abi_hash()
+
 CSRC = PKG_DIR / "csrc"
 LIB_DIR = PKG_DIR / "lib"
 OBJ_DIR = LIB_DIR / "obj"
@@ -47,9 +61,9 @@ HIP_FLAGS = [
 ]
 
 
-def _compile(src: Path) -> Path:
+def _compile(src: Path, defines=()) -> Path:
     obj = OBJ_DIR / (src.stem + ".o")
-    cmd = [HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *HIP_FLAGS, *defines, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(
@@ -68,8 +82,10 @@ def build(verbose: bool = True, jobs: int | None = None) -> Path:
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     jobs = jobs or min(8, os.cpu_count() or 4)
+    # the interface digest the library reports from gsplat_abi_version()
+    defines = [f'-DGSPLAT_ABI_HASH="{_header_abi_hash()}"']
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, sources))
+        objs = list(ex.map(lambda s: _compile(s, defines), sources))
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
            *map(str, objs)]

@@ -50,3 +50,12 @@ extern "C" const char *gsplat_last_error(void) {
 extern "C" const char *gsplat_version(void) {
     return "gsplat_hip 0.1.0 gfx950";
 }
+
+// The build passes the digest of include/gsplat_hip.h's declarations.
+#ifndef GSPLAT_ABI_HASH
+#error "GSPLAT_ABI_HASH must be defined by the build (digest of include/gsplat_hip.h)"
+#endif
+
+extern "C" const char *gsplat_abi_version(void) {
+    return GSPLAT_ABI_HASH;
+}

@@ -55,6 +55,15 @@ const char *gsplat_last_error(void);
 /* Library version string, e.g. "gsplat_hip 0.1.0 gfx950". */
 const char *gsplat_version(void);
 
+/* Identity of the interface the library was built from: 16 hex digits of
+ * SHA-256 over this header's declarations (comments and whitespace removed;
+ * gsplat_amd/abi.py:header_abi_hash).  A binding compares it with the digest
+ * of the header it was written against and refuses a library that differs,
+ * before binding any entry point.  No counterpart in the reference, whose op
+ * schemas are compiled into the same module as its kernels
+ * (gsplat/cuda/ext.cpp:711-808), so its callers cannot disagree with them. */
+const char *gsplat_abi_version(void);
+
 /* ------------------------------------------------------------------------ */
 /* Projection (EWA splatting of 3D Gaussians to 2D conics).                  */
 /* ------------------------------------------------------------------------ */

@@ -61,6 +61,55 @@ def test_library_loads_and_reports_version(lib_path):
     assert _lib.version().startswith("gsplat_hip")
 
 
+def test_binding_was_written_for_this_header():
+    """_lib's recorded interface digest and every hand-typed ctypes
+    signature equal the header's declarations, so a header change that the
+    binding did not follow fails here, on the CPU."""
+    import ctypes
+
+    from gsplat_amd import _lib, abi
+    assert _lib._ABI_VERSION == abi.header_abi_hash(), "update _lib._ABI_VERSION"
+    protos = abi.header_prototypes()
+    assert set(protos) == set(_lib._SIGNATURES)
+    arg = {"int64_t": ctypes.c_int64, "int32_t": ctypes.c_int32, "int": ctypes.c_int32,
+           "float": ctypes.c_float, "size_t": ctypes.c_size_t,
+           "gsplat_stream_t": ctypes.c_void_p}
+    ret = {"int": ctypes.c_int, "size_t": ctypes.c_size_t, "int64_t": ctypes.c_int64,
+           "const char*": ctypes.c_char_p}
+    for name, (restype, params) in protos.items():
+        want = [ctypes.c_void_p if t.endswith("*") else arg[t] for t in params]
+        assert _lib._SIGNATURES[name] == want, name
+        assert _lib._RESTYPES.get(name, ctypes.c_int) == ret[restype], name
+
+
+def test_built_library_reports_the_header_abi(lib_path):
+    from gsplat_amd import _lib, abi
+    assert _lib.load().gsplat_abi_version().decode() == abi.header_abi_hash()
+
+
+@pytest.mark.parametrize("reported", ["0123456789abcdef", None])
+def test_load_refuses_a_library_of_another_interface(reported, tmp_path, monkeypatch):
+    """A stub library whose interface digest differs (or is absent) is
+    refused by load() with both versions named, before any signature is
+    bound: calling it would pass arguments of the wrong types."""
+    from gsplat_amd import _lib
+    src = tmp_path / "stub.c"
+    body = 'const char *gsplat_version(void) { return "stub"; }\n'
+    if reported is not None:
+        body += f'const char *gsplat_abi_version(void) {{ return "{reported}"; }}\n'
+    src.write_text(body)
+    so = tmp_path / "libgsplat_hip.so"
+    subprocess.run(["gcc", "-shared", "-fPIC", "-o", str(so), str(src)], check=True)
+    monkeypatch.setattr(_lib, "LIB_PATH", so)
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(RuntimeError) as err:
+        _lib.load()
+    msg = str(err.value)
+    assert _lib._ABI_VERSION in msg
+    assert (reported in msg) if reported else ("gsplat_abi_version is missing" in msg)
+    assert _lib._lib is None
+
+
 def test_argument_errors_are_reported_without_a_gpu(lib_path):
     from gsplat_amd import _lib
     with pytest.raises(RuntimeError, match="degree"):
