@@ -22,7 +22,7 @@ _P = c_void_p
 # of include/gsplat_hip.h.  load() refuses a library built from any other
 # header, and a CPU test keeps this digest and _SIGNATURES equal to the
 # header's.  Change all three together.
-_ABI_VERSION = "f08ef0b7db4794cc"
+_ABI_VERSION = "88be6fa70834cd68"
 
 # name -> argtypes (restype int unless listed in _RESTYPES)
 _SIGNATURES = {
@@ -120,7 +120,7 @@ _SIGNATURES = {
     "gsplat_rasterize_fwd_replay": [
         c_int64, c_int64, c_int64, c_int32, _P, _P, _P, _P, _P, _P,
         c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P, _P,
-        c_size_t, c_int32, _P, c_int64, _P],
+        c_size_t, c_int32, _P, _P, c_int64, _P],
     "gsplat_rasterize_bwd_replay": [
         c_int64, c_int64, c_int64, c_int32, _P, _P, _P, _P, _P, _P,
         c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P,

@@ -47,11 +47,12 @@ struct RasterArgs {
     const int32_t *tile_offsets, *flatten_ids;
     // Expected depth (render modes ED, RGB+ED): the forward writes colour
     // channel ed_channel divided by max(alpha, 1e-10), the division
-    // rendering.py:1259-1267 applies to the render; the backward takes the
-    // gradient of that output (ed_out: the forward's render_colors) back
-    // through it.  -1: no channel is divided.
+    // rendering.py:1259-1267 applies to the render, and (when ed_depth is
+    // set) the same value per pixel into ed_depth [I,H,W]; the backward reads
+    // that output from ed_depth to take the gradient back through the
+    // division.  -1: no channel is divided.
     int32_t ed_channel = -1;
-    const float *ed_out = nullptr;
+    float *ed_depth = nullptr;
 };
 
 // Replay state written by the forward for a backward split into units of
@@ -436,9 +437,12 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
             else
                 render_colors[pix * CDIM + k] = v;
         }
-        if (a.ed_channel >= 0)
-            render_colors[pix * CDIM + a.ed_channel] =
-                v_ed / fmaxf(alpha_out, kMinExpectedDepthAlpha);
+        if (a.ed_channel >= 0) {
+            const float ed = v_ed / fmaxf(alpha_out, kMinExpectedDepthAlpha);
+            render_colors[pix * CDIM + a.ed_channel] = ed;
+            if (a.ed_depth != nullptr)
+                a.ed_depth[pix] = ed;
+        }
         last_ids[pix] = cur_idx;
         if (render_T != nullptr)
             render_T[pix] = T;
@@ -665,7 +669,7 @@ __device__ __forceinline__ void rasterize_bwd_tile(
             for (int k = 0; k < CDIM; ++k)
                 v_c[p][k] = k == a.ed_channel ? gd : v_c[p][k];
             if (alpha_out >= kMinExpectedDepthAlpha)
-                v_a -= gd * a.ed_out[pix * CDIM + a.ed_channel];
+                v_a -= gd * a.ed_depth[pix];
         }
         float bg_dot = 0.f;
         if (a.backgrounds) {
@@ -1337,8 +1341,8 @@ extern "C" int gsplat_rasterize_fwd_replay(
     int32_t tile_width, int32_t tile_height, const int32_t *tile_offsets,
     const int32_t *flatten_ids, float *render_colors, float *render_alphas,
     int32_t *last_ids, float *render_transmittance, void *replay,
-    size_t replay_bytes, int32_t expected_depth_channel, float *zero_fill,
-    int64_t zero_fill_count, gsplat_stream_t stream) {
+    size_t replay_bytes, int32_t expected_depth_channel, float *expected_depth,
+    float *zero_fill, int64_t zero_fill_count, gsplat_stream_t stream) {
     clear_error();
     RasterArgs a{I, n_rows, n_isects, means2d, conics, colors, opacities,
                  backgrounds, masks, image_width, image_height, tile_size,
@@ -1349,6 +1353,7 @@ extern "C" int gsplat_rasterize_fwd_replay(
     GS_REQUIRE(expected_depth_channel >= -1 && expected_depth_channel < cdim,
                "rasterize_fwd_replay: expected_depth_channel out of range");
     a.ed_channel = expected_depth_channel;
+    a.ed_depth = expected_depth_channel >= 0 ? expected_depth : nullptr;
     GS_REQUIRE(zero_fill_count >= 0 && (zero_fill_count == 0 || zero_fill != nullptr),
                "rasterize_fwd_replay: NULL zero_fill with a nonzero count");
     ReplayState rs{};
@@ -1393,7 +1398,7 @@ extern "C" int gsplat_rasterize_bwd_replay(
     const float *v_render_alphas, float *v_means2d_abs, float *v_means2d,
     float *v_conics, float *v_colors, float *v_opacities,
     uint32_t *tile_counter, const void *replay, size_t replay_bytes,
-    const float *render_colors, int32_t expected_depth_channel,
+    const float *expected_depth, int32_t expected_depth_channel,
     gsplat_stream_t stream) {
     clear_error();
     RasterArgs a{I, n_rows, n_isects, means2d, conics, colors, opacities,
@@ -1404,10 +1409,11 @@ extern "C" int gsplat_rasterize_bwd_replay(
                "rasterize_bwd_replay: NULL render_transmittance");
     GS_REQUIRE(expected_depth_channel >= -1 && expected_depth_channel < cdim,
                "rasterize_bwd_replay: expected_depth_channel out of range");
-    GS_REQUIRE(expected_depth_channel < 0 || render_colors != nullptr,
-               "rasterize_bwd_replay: the expected-depth channel needs render_colors");
+    GS_REQUIRE(expected_depth_channel < 0 || expected_depth != nullptr,
+               "rasterize_bwd_replay: the expected-depth channel needs the "
+               "forward's expected_depth");
     a.ed_channel = expected_depth_channel;
-    a.ed_out = render_colors;
+    a.ed_depth = const_cast<float *>(expected_depth);
     GS_REQUIRE(tile_counter != nullptr,
                "rasterize_bwd_replay: NULL tile_counter (the units are taken "
                "from it)");

@@ -875,6 +875,39 @@ def rasterize_fwd_with_transmittance(
     return renders, alphas, last_ids, transmittance
 
 
+class RasterReplay:
+    """What ``rasterize_fwd_replay`` keeps for ``rasterize_bwd_replay``: the
+    replay records and unit list (``records``), the zeroed accumulators of
+    the backward (``accum``, used once, or None) and the expected-depth
+    channel of the render (``expected_depth`` [..., H, W], or None) with its
+    index ``channel`` (-1 for none)."""
+
+    __slots__ = ("records", "accum", "expected_depth", "channel")
+
+    def __init__(self, records, accum, expected_depth, channel):
+        self.records = records
+        self.accum = accum
+        self.expected_depth = expected_depth
+        self.channel = channel
+
+
+# Largest replay workspace (bytes) one rasterizer call may allocate.  The
+# records take 16 (1 + C) bytes per intersection for C channels (a record of
+# T and the C colour sums for each of a tile's pixels at every 64th
+# intersection of its range), allocated for the whole range although only the
+# boundaries a pixel is still active at are written.  Above this budget the
+# forward keeps no replay state and the backward replays whole tiles from the
+# final transmittance (gsplat_rasterize_bwd), as the reference does.
+replay_budget_bytes = 8 << 30
+
+
+def rasterize_replay_bytes(image_dims_numel: int, tile_width: int, tile_height: int,
+                           tile_size: int, n_isects: int, channels: int) -> int:
+    """Bytes of the replay workspace ``rasterize_fwd_replay`` allocates."""
+    return query("gsplat_rasterize_replay_size", image_dims_numel, tile_width,
+                 tile_height, int(tile_size), n_isects, channels)
+
+
 def rasterize_fwd_replay(
     means2d: Tensor,
     conics: Tensor,
@@ -890,13 +923,13 @@ def rasterize_fwd_replay(
     expected_depth_channel: int = -1,
     absgrad: Optional[bool] = None,
 ):
-    """``rasterize_fwd_with_transmittance`` that also fills the replay state of
+    """``rasterize_fwd_with_transmittance`` that also keeps the replay state of
     ``rasterize_bwd_replay`` (per-pixel records at every batch boundary of a
-    tile and the list of replay units); returns it as a fifth output.  With
-    ``expected_depth_channel`` >= 0 that channel of the render is divided by
-    max(alpha, 1e-10) (rendering.py:1259-1267).  With ``absgrad`` not None
-    the launch also zero-fills the accumulators of ``rasterize_bwd_replay``
-    (its ``accum``, returned as a sixth output)."""
+    tile and the list of replay units), returned as a ``RasterReplay`` fifth
+    output.  With ``expected_depth_channel`` >= 0 that channel of the render
+    is divided by max(alpha, 1e-10) (rendering.py:1259-1267) and kept in the
+    state for the backward.  With ``absgrad`` not None the launch also
+    zero-fills the accumulators of ``rasterize_bwd_replay``."""
     image_dims, I, n_rows, tw, th = _raster_common(
         means2d, conics, colors, opacities, backgrounds, masks, tile_offsets,
         flatten_ids)
@@ -908,22 +941,24 @@ def rasterize_fwd_replay(
     last_ids = torch.empty(image_dims + (H, W), dtype=_I32, device=dev)
     transmittance = torch.empty(image_dims + (H, W), dtype=_F32, device=dev)
     n_isects = flatten_ids.numel()
-    replay = torch.empty(query("gsplat_rasterize_replay_size", I, tw, th, int(tile_size),
-                               n_isects, channels), dtype=torch.uint8, device=dev)
+    records = torch.empty(rasterize_replay_bytes(I, tw, th, tile_size, n_isects, channels),
+                          dtype=torch.uint8, device=dev)
     accum = None
     if absgrad is not None:
         accum = torch.empty(_bwd_accum_words(means2d, conics, colors, opacities, absgrad),
                             dtype=_F32, device=dev)
+    ed = None
+    if expected_depth_channel >= 0:
+        ed = torch.empty(image_dims + (H, W), dtype=_F32, device=dev)
     call("gsplat_rasterize_fwd_replay", I, n_rows, n_isects, channels,
          ptr(means2d), ptr(conics), ptr(colors), ptr(opacities),
          ptr(backgrounds), ptr(masks), W, H, int(tile_size), tw, th,
          ptr(tile_offsets), ptr(flatten_ids), ptr(renders), ptr(alphas),
-         ptr(last_ids), ptr(transmittance), ptr(replay), replay.numel(),
-         int(expected_depth_channel), ptr(accum), 0 if accum is None else accum.numel(),
-         _stream(means2d))
-    if absgrad is None:
-        return renders, alphas, last_ids, transmittance, replay
-    return renders, alphas, last_ids, transmittance, replay, accum
+         ptr(last_ids), ptr(transmittance), ptr(records), records.numel(),
+         int(expected_depth_channel), ptr(ed), ptr(accum),
+         0 if accum is None else accum.numel(), _stream(means2d))
+    return (renders, alphas, last_ids, transmittance,
+            RasterReplay(records, accum, ed, int(expected_depth_channel)))
 
 
 def _bwd_accum_words(means2d, conics, colors, opacities, absgrad: bool) -> int:
@@ -1030,36 +1065,33 @@ def rasterize_bwd_replay(
     flatten_ids: Tensor,
     render_transmittance: Tensor,
     last_ids: Tensor,
-    replay: Tensor,
+    replay: RasterReplay,
     v_render_colors: Tensor,
     v_render_alphas: Optional[Tensor],
     absgrad: bool,
-    render_colors: Optional[Tensor] = None,
-    expected_depth_channel: int = -1,
-    accum: Optional[Tensor] = None,
 ):
     """``rasterize_to_pixels_3dgs_bwd`` from the state of
     ``rasterize_fwd_replay`` on the same inputs: the replay runs one unit per
-    forward batch instead of one per tile.  With ``expected_depth_channel``
-    >= 0 (the forward's, whose ``render_colors`` must be given) the colour
-    gradient of that channel is taken through its division by the alpha.
-    ``accum`` is the zeroed accumulator buffer of ``rasterize_fwd_replay``
-    (used once; None allocates a zeroed one)."""
+    forward batch instead of one per tile.  With the forward's expected-depth
+    channel the colour gradient of that channel is taken through its division
+    by the alpha.  The state's zeroed accumulators are used once; a second
+    backward allocates fresh zeros."""
     image_dims, I, n_rows, tw, th = _raster_common(
         means2d, conics, colors, opacities, backgrounds, masks, tile_offsets,
         flatten_ids)
     check_input(render_transmittance, "render_transmittance", _F32)
     check_input(last_ids, "last_ids", _I32)
-    check_input(replay, "replay", torch.uint8)
+    check_input(replay.records, "replay records", torch.uint8)
     check_input(v_render_colors, "v_render_colors", _F32)
     check_input(v_render_alphas, "v_render_alphas", _F32)
-    check_input(render_colors, "render_colors", _F32)
-    if expected_depth_channel >= 0 and (
-            render_colors is None or render_colors.shape != v_render_colors.shape):
-        raise RuntimeError("the expected-depth channel needs the forward's render_colors")
+    check_input(replay.expected_depth, "expected_depth", _F32)
+    if replay.channel >= 0 and (replay.expected_depth is None or
+                                replay.expected_depth.shape != v_render_colors.shape[:-1]):
+        raise RuntimeError("the expected-depth channel needs the forward's expected depth")
     channels = colors.shape[-1]
     likes = [means2d, conics, colors, opacities] + ([means2d] if absgrad else [])
     sizes = [t.numel() for t in likes] + [1]
+    accum, replay.accum = replay.accum, None
     if accum is not None:
         check_input(accum, "accum", _F32)
         if accum.numel() != sum(sizes):
@@ -1079,8 +1111,8 @@ def rasterize_bwd_replay(
          ptr(render_transmittance), ptr(last_ids), ptr(v_render_colors),
          ptr(v_render_alphas), ptr(v_means2d_abs), ptr(v_means2d),
          ptr(v_conics), ptr(v_colors), ptr(v_opacities), ptr(tile_counter),
-         ptr(replay), replay.numel(), ptr(render_colors), int(expected_depth_channel),
-         _stream(means2d))
+         ptr(replay.records), replay.records.numel(), ptr(replay.expected_depth),
+         replay.channel, _stream(means2d))
     return v_means2d_abs, v_means2d, v_conics, v_colors, v_opacities
 
 

@@ -14,6 +14,7 @@ kernels of libgsplat_hip.so, reached through ``_ops``.
 from __future__ import annotations
 
 import math
+import weakref
 from typing import Callable, Optional, Tuple
 
 import torch
@@ -356,7 +357,12 @@ def _rasterize_to_pixels(
         assert colors.shape == image_dims + (N, channels), colors.shape
         assert opacities.shape == image_dims + (N,), opacities.shape
     if backgrounds is not None:
-        assert backgrounds.shape == image_dims + (channels,), backgrounds.shape
+        # one background per image: packed rows carry no image dims, so the
+        # images are those of the tile grid (the reference checks packed
+        # backgrounds against the rows' empty dims, _wrapper.py:884-886,
+        # which no [..., C, channels] background passes)
+        bg_dims = tuple(isect_offsets.shape[:-2]) if packed else image_dims
+        assert backgrounds.shape == bg_dims + (channels,), backgrounds.shape
         backgrounds = backgrounds.contiguous()
     if masks is not None:
         assert masks.shape == isect_offsets.shape, masks.shape
@@ -772,13 +778,29 @@ class Grad2dStatsSlot:
     """Carries a densification-statistics request from the caller to the
     packed front end's backward (``gsplat_amd.strategy.stats.fuse_grad2d_stats``
     fills it between the forward and ``backward()``): the projection backward
-    then accumulates the statistics in its own pass."""
+    then accumulates the statistics in its own pass.
+
+    The first backward through the node consumes the request, so a second
+    backward through a retained graph adds nothing; a request whose backward
+    never runs adds nothing either.  The slot holds ``means2d`` (whose
+    ``absgrad`` the statistics read) only weakly: the node's context holds the
+    slot, and a strong reference would make means2d -> its node -> the slot
+    -> means2d a cycle that keeps a step's buffers alive until Python's
+    cyclic collector runs."""
 
     def __init__(self, width: int, height: int, n_cameras: int):
         self.scale_x = width / 2.0 * n_cameras
         self.scale_y = height / 2.0 * n_cameras
-        self.means2d: Optional[Tensor] = None
+        self._means2d = None
         self.request = None  # (grad2d, count, absgrad)
+
+    @property
+    def means2d(self) -> Optional[Tensor]:
+        return None if self._means2d is None else self._means2d()
+
+    @means2d.setter
+    def means2d(self, t: Optional[Tensor]) -> None:
+        self._means2d = None if t is None else weakref.ref(t)
 
 
 class _PackedFrontEnd(torch.autograd.Function):
@@ -861,11 +883,18 @@ class _PackedFrontEnd(torch.autograd.Function):
         stats = None
         slot = ctx.stats_slot
         if slot is not None and slot.request is not None:
-            grad2d, count, absgrad = slot.request
-            rows = getattr(slot.means2d, "absgrad", None) if absgrad else v_means2d
-            if rows is None:
-                raise RuntimeError("fused densification statistics need absgrad=True "
-                                   "in rasterization()")
+            (grad2d, count, absgrad), slot.request = slot.request, None
+            rows = v_means2d
+            if absgrad:
+                m2d = slot.means2d
+                if m2d is None:
+                    raise RuntimeError(
+                        "fused densification statistics read meta['means2d'].absgrad: "
+                        "keep rasterization()'s meta alive until backward() has run")
+                rows = getattr(m2d, "absgrad", None)
+                if rows is None:
+                    raise RuntimeError("fused densification statistics need "
+                                       "absgrad=True in rasterization()")
             stats = (rows.contiguous(), slot.scale_x, slot.scale_y, grad2d, count)
         res = _ops.projection_packed_bwd_rows(
             means, covars, quats, scales, viewmats, Ks, ctx.width, ctx.height,
@@ -893,11 +922,20 @@ class _RasterizeToPixels(torch.autograd.Function):
                 ed_channel=-1):
         # With gradients ahead the forward also keeps the replay state, so
         # the backward runs one unit per forward batch instead of one per
-        # tile (the reference replays whole tiles).
-        accum = None
-        if any(ctx.needs_input_grad[:5]):
+        # tile (the reference replays whole tiles), unless that state would
+        # exceed _ops.replay_budget_bytes.
+        replay = None
+        ed_depth = None
+        grads = any(ctx.needs_input_grad[:5])
+        if grads:
+            th, tw = isect_offsets.shape[-2:]
+            n_images = math.prod(isect_offsets.shape[:-2])
+            replay_bytes = _ops.rasterize_replay_bytes(
+                n_images, tw, th, tile_size, flatten_ids.numel(), colors.shape[-1])
+            grads_by_replay = replay_bytes <= _ops.replay_budget_bytes
+        if grads and grads_by_replay:
             # the launch also zero-fills the backward's accumulators
-            render_colors, render_alphas, last_ids, render_T, replay, accum = \
+            render_colors, render_alphas, last_ids, render_T, replay = \
                 _ops.rasterize_fwd_replay(
                     means2d, conics, colors, opacities, backgrounds, masks,
                     width, height, tile_size, isect_offsets, flatten_ids,
@@ -907,18 +945,20 @@ class _RasterizeToPixels(torch.autograd.Function):
                 _ops.rasterize_fwd_with_transmittance(
                     means2d, conics, colors, opacities, backgrounds, masks,
                     width, height, tile_size, isect_offsets, flatten_ids)
-            replay = None
             if ed_channel >= 0:
-                # no backward: the division in place (rendering.py:1259-1267)
+                # the division in place (rendering.py:1259-1267); a backward
+                # takes it back in torch from the divided channel
                 render_colors[..., ed_channel] /= render_alphas[..., 0].clamp(min=1e-10)
+                if grads:
+                    ed_depth = render_colors[..., ed_channel].clone()
         ctx.save_for_backward(means2d, conics, colors, opacities, backgrounds,
                               masks, isect_offsets, flatten_ids, render_T,
-                              last_ids, replay,
-                              render_colors if ed_channel >= 0 else None)
+                              last_ids, ed_depth)
+        # the replay records and zeroed accumulators; the accumulators are
+        # consumed by the first backward (a second backward through a
+        # retained graph takes fresh zeros)
+        ctx.replay = replay
         ctx.ed_channel = ed_channel
-        # zeroed by the forward, consumed by the first backward (a second
-        # backward through a retained graph takes fresh zeros)
-        ctx.accum = accum
         ctx.width = width
         ctx.height = height
         ctx.tile_size = tile_size
@@ -931,29 +971,37 @@ class _RasterizeToPixels(torch.autograd.Function):
     def backward(ctx, v_render_colors: Optional[Tensor],
                  v_render_alphas: Optional[Tensor]):
         (means2d, conics, colors, opacities, backgrounds, masks, isect_offsets,
-         flatten_ids, render_T, last_ids, replay, render_colors) = ctx.saved_tensors
+         flatten_ids, render_T, last_ids, ed_depth) = ctx.saved_tensors
         if v_render_colors is None and v_render_alphas is None:
             return (None,) * 13
         if v_render_colors is None:
             v_render_colors = render_T.new_zeros((*render_T.shape, colors.shape[-1]))
         v_alphas = None if v_render_alphas is None else v_render_alphas.contiguous()
-        if replay is not None:
+        if ctx.replay is not None:
             (v_means2d_abs, v_means2d, v_conics, v_colors,
              v_opacities) = _ops.rasterize_bwd_replay(
                 means2d, conics, colors, opacities, backgrounds, masks, ctx.width,
                 ctx.height, ctx.tile_size, isect_offsets, flatten_ids,
-                render_T, last_ids, replay, v_render_colors.contiguous(), v_alphas,
-                ctx.absgrad, render_colors=render_colors,
-                expected_depth_channel=ctx.ed_channel, accum=ctx.accum)
-            ctx.accum = None
+                render_T, last_ids, ctx.replay, v_render_colors.contiguous(), v_alphas,
+                ctx.absgrad)
         else:
+            v_rc = v_render_colors
+            if ctx.ed_channel >= 0:
+                # out = v / max(alpha, 1e-10): dL/dv = g / den, and the alpha
+                # output gets -(g / den) out where the clamp passes
+                alpha = 1.0 - render_T
+                gd = v_render_colors[..., ctx.ed_channel] / alpha.clamp(min=1e-10)
+                v_rc = v_render_colors.clone()
+                v_rc[..., ctx.ed_channel] = gd
+                v_a = (-(gd * ed_depth) * (alpha >= 1e-10))[..., None]
+                v_alphas = (v_a if v_alphas is None else v_alphas + v_a).contiguous()
             # render_alphas = 1 - T is only read when T is absent; T's storage
             # stands in for it to satisfy the op's checks
             (v_means2d_abs, v_means2d, v_conics, v_colors,
              v_opacities) = _ops.rasterize_to_pixels_3dgs_bwd(
                 means2d, conics, colors, opacities, backgrounds, masks, ctx.width,
                 ctx.height, ctx.tile_size, isect_offsets, flatten_ids,
-                render_T, last_ids, v_render_colors.contiguous(), v_alphas,
+                render_T, last_ids, v_rc.contiguous(), v_alphas,
                 ctx.absgrad, render_transmittance=render_T)
         if ctx.absgrad:
             prev = getattr(means2d, "absgrad", None)

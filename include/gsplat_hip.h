@@ -627,10 +627,12 @@ int gsplat_rasterize_bwd(
  * expected_depth_channel (-1 for none; no counterpart in the reference op,
  *   whose caller does this in torch, gsplat/rendering.py:1259-1267): the
  *   forward writes that colour channel divided by max(alpha, 1e-10), the
- *   expected depth of render modes ED and RGB+ED, and the backward (given
- *   the forward's render_colors and the same channel) takes
- *   v_render_colors as the gradient of that divided output, adding the
- *   division's alpha term to the alpha gradient.
+ *   expected depth of render modes ED and RGB+ED, into render_colors and
+ *   (when expected_depth is not NULL) into expected_depth [I,H,W]; the
+ *   backward, given that expected_depth and the same channel, takes
+ *   v_render_colors as the gradient of the divided output, adding the
+ *   division's alpha term to the alpha gradient.  The caller keeps only the
+ *   one channel for the backward, not the returned render.
  * zero_fill, zero_fill_count (NULL, 0 for none; no counterpart in the
  *   reference): a float buffer the forward launch also sets to zero, for
  *   the gradient accumulators gsplat_rasterize_bwd_replay adds into, so
@@ -648,8 +650,8 @@ int gsplat_rasterize_fwd_replay(
     const int32_t *tile_offsets, const int32_t *flatten_ids,
     float *render_colors, float *render_alphas, int32_t *last_ids,
     float *render_transmittance, void *replay, size_t replay_bytes,
-    int32_t expected_depth_channel, float *zero_fill, int64_t zero_fill_count,
-    gsplat_stream_t stream);
+    int32_t expected_depth_channel, float *expected_depth, float *zero_fill,
+    int64_t zero_fill_count, gsplat_stream_t stream);
 
 int gsplat_rasterize_bwd_replay(
     int64_t I, int64_t n_rows, int64_t n_isects, int32_t cdim,
@@ -662,7 +664,7 @@ int gsplat_rasterize_bwd_replay(
     const float *v_render_colors, const float *v_render_alphas,
     float *v_means2d_abs, float *v_means2d, float *v_conics,
     float *v_colors, float *v_opacities, uint32_t *tile_counter,
-    const void *replay, size_t replay_bytes, const float *render_colors,
+    const void *replay, size_t replay_bytes, const float *expected_depth,
     int32_t expected_depth_channel, gsplat_stream_t stream);
 
 /* Rasterize to indices: the (Gaussian, pixel) pairs each pixel composites

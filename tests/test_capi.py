@@ -150,19 +150,20 @@ def test_replay_workspace_size_and_checks_without_a_gpu(lib_path):
         _lib.call("gsplat_rasterize_bwd_replay", *args, f, f, f, None, None, f, f, f, f,
                   f, f, want - 1, None, -1, None)
     with pytest.raises(RuntimeError, match="NULL replay"):
-        _lib.call("gsplat_rasterize_fwd_replay", *args, f, f, f, f, None, want, -1, None, 0,
-                  None)
+        _lib.call("gsplat_rasterize_fwd_replay", *args, f, f, f, f, None, want, -1, None,
+                  None, 0, None)
     with pytest.raises(RuntimeError, match="zero_fill"):
-        _lib.call("gsplat_rasterize_fwd_replay", *args, f, f, f, f, f, want, -1, None, 5,
-                  None)
+        _lib.call("gsplat_rasterize_fwd_replay", *args, f, f, f, f, f, want, -1, None,
+                  None, 5, None)
     with pytest.raises(RuntimeError, match="tile_counter"):
         _lib.call("gsplat_rasterize_bwd_replay", *args, f, f, f, None, None, f, f, f, f,
                   None, f, want, None, -1, None)
-    # the expected-depth channel: in range, and the backward needs the render
+    # the expected-depth channel: in range, and the backward needs the
+    # forward's copy of it
     with pytest.raises(RuntimeError, match="expected_depth_channel"):
-        _lib.call("gsplat_rasterize_fwd_replay", *args, f, f, f, f, f, want, cdim, None, 0,
-                  None)
-    with pytest.raises(RuntimeError, match="render_colors"):
+        _lib.call("gsplat_rasterize_fwd_replay", *args, f, f, f, f, f, want, cdim, f,
+                  None, 0, None)
+    with pytest.raises(RuntimeError, match="expected_depth"):
         _lib.call("gsplat_rasterize_bwd_replay", *args, f, f, f, None, None, f, f, f, f,
                   f, f, want, None, cdim - 1, None)
 

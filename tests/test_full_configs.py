@@ -204,7 +204,7 @@ def test_cfg4_full_size_optimizer_step():
     six tensors (118M elements, the config's learning rates)."""
     import gsplat_amd as gs
     from gsplat_amd.cuda import _ops
-    from gsplat_amd.strategy.stats import accumulate_grad2d_stats
+    from gsplat_amd.strategy.stats import accumulate_grad2d_stats, fuse_grad2d_stats
     scene = make_scene(4)
     C, H, W = 1, scene.height, scene.width
     N = scene.means.shape[0]
@@ -230,19 +230,32 @@ def test_cfg4_full_size_optimizer_step():
     rc, ra, meta = gs.rasterization(means, quats, scales, opac, colors,
                                     scene.viewmats.to(DEV), scene.Ks.to(DEV), W, H,
                                     sh_degree=3, absgrad=True)
+    # densification statistics accumulated by the projection backward, onto a
+    # running state, as bench.py --config 4 takes them
+    gs_ = torch.Generator().manual_seed(6)
+    prev_g = torch.rand(N, generator=gs_)
+    prev_c = torch.randint(0, 5, (N,), generator=gs_).float()
+    grad2d, count, fused = fuse_grad2d_stats(meta, prev_g.to(DEV), prev_c.to(DEV), N,
+                                             absgrad=True)
+    assert fused
     ((rc * v_rc.to(DEV)).sum() + (ra * v_ra.to(DEV)).sum()).backward()
     print(f"[cfg4] {meta['isect_ids'].numel()} intersections", flush=True)
     _check_forward(meta, rc, ra, meta_r, rc_r, ra_r, pix)
     _check_grads({k: v.grad.cpu() for k, v in params.items()}, g64, g32)
 
-    # densification statistics of the step's own absgrad (strategy/default.py:235-268)
-    grad2d, count = accumulate_grad2d_stats(meta, None, None, N, packed=True, absgrad=True)
+    # the statistics of the step's own absgrad (strategy/default.py:235-268)
     absgrad = meta["means2d"].absgrad.detach().cpu()
     assert float(absgrad.abs().sum()) > 0
     r_g, r_c = torch_ref.grad2d_stats_ref(absgrad, meta["gaussian_ids"].cpu(), None, N, W,
-                                         H, C)
+                                         H, C, prev_g, prev_c)
     assert torch.equal(count.cpu().double(), r_c)
-    assert_close(grad2d.cpu(), r_g, 1e-5, 1e-9, "grad2d")
+    assert_close(grad2d.cpu(), r_g, 1e-5, 1e-9, "grad2d (fused)")
+    # and the separate pass over the same rows from zero
+    sep_g, sep_c = accumulate_grad2d_stats(meta, None, None, N, packed=True, absgrad=True)
+    r_g0, r_c0 = torch_ref.grad2d_stats_ref(absgrad, meta["gaussian_ids"].cpu(), None, N,
+                                           W, H, C)
+    assert torch.equal(sep_c.cpu().double(), r_c0)
+    assert_close(sep_g.cpu(), r_g0, 1e-5, 1e-9, "grad2d (separate)")
 
     # fused Adam over all six tensors from a nonzero state, bit for bit
     lrs = {"means": 1.6e-4, "log_scales": 5e-3, "quats": 1e-3, "opacity_logits": 5e-2,

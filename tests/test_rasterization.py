@@ -110,3 +110,41 @@ def test_cfg2_reduced_multiview_unpacked():
     # the dense path's view directions (rendering.py:compute_directions) under
     # eight look-at cameras whose rotations are not symmetric
     _check(_downscale(make_scene(2, n=8_000), 4), packed=False)
+
+
+@pytest.mark.parametrize("render_mode,bg", [("RGB", True), ("RGB+ED", False)])
+def test_whole_tile_backward_above_the_replay_budget(render_mode, bg, monkeypatch):
+    # a replay workspace over the budget: the forward keeps no replay state
+    # and the backward replays whole tiles from the final T (the expected
+    # depth's division then taken back in torch)
+    from gsplat_amd.cuda import _ops
+    monkeypatch.setattr(_ops, "replay_budget_bytes", 0)
+    _check(_downscale(make_scene(2, n=8_000), 4), render_mode=render_mode, bg=bg)
+
+
+@pytest.mark.parametrize("budget", [None, 0])
+def test_returned_expected_depth_render_may_be_edited_in_place(budget, monkeypatch):
+    """The backward keeps its own copy of the expected-depth channel, not the
+    returned render, so the caller may edit the render in place."""
+    import gsplat_amd as gs
+    from gsplat_amd.cuda import _ops
+    if budget is not None:
+        monkeypatch.setattr(_ops, "replay_budget_bytes", budget)
+    scene = _downscale(make_scene(2, n=4_000), 8)
+    grads = []
+    for in_place in (False, True):
+        leaves = [getattr(scene, k).to(DEV).requires_grad_() for k in
+                  ("means", "quats", "scales", "opacities", "colors")]
+        rc, ra, _ = gs.rasterization(*leaves, scene.viewmats.to(DEV), scene.Ks.to(DEV),
+                                     scene.width, scene.height, sh_degree=scene.sh_degree,
+                                     render_mode="RGB+ED")
+        w = torch.tensor([0.5, 2.0, 1.0, 3.0], device=DEV)
+        if in_place:
+            rc.mul_(w)
+        else:
+            rc = rc * w
+        v = torch.randn(rc.shape, generator=torch.Generator().manual_seed(4)).to(DEV)
+        ((rc * v).sum() + ra.sum()).backward()
+        grads.append([t.grad for t in leaves])
+    for a, b in zip(*grads):
+        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-7)

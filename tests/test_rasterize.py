@@ -321,7 +321,7 @@ def _direct_grads(data, D, bg, mk, v_rc, v_ra, replay):
         grads = _ops.rasterize_bwd_replay(
             *ins, bgd, mkd, W, H, ts, offs, fl, T, last, state, v_rc.to(DEV),
             v_ra.to(DEV), False)
-        n_units = int(state[:4].cpu().view(torch.int32)[0])
+        n_units = int(state.records[:4].cpu().view(torch.int32)[0])
     else:
         rc, ra, last, T = _ops.rasterize_fwd_with_transmittance(
             *ins, bgd, mkd, W, H, ts, offs, fl)

@@ -119,3 +119,57 @@ def test_grad2d_stats_fused_into_projection_backward(C, absgrad):
     assert torch.equal(count.cpu().double(), ref_c)
     _check(grad2d, ref_g)
     torch.testing.assert_close(grad2d, sep_g, rtol=1e-6, atol=1e-9)
+
+
+def _fused_stats_step(seed=40, N=8_000):
+    import gsplat_amd as gs
+    from tests._util import small_scene
+    means, quats, scales, opac, vm, K, W, H = small_scene(seed=seed, N=N, C=1)
+    g = torch.Generator().manual_seed(seed)
+    colors = torch.rand(means.shape[0], 3, generator=g)
+    ins = [t.to(DEV).requires_grad_() for t in (means, quats, scales, opac, colors)]
+    rc, ra, meta = gs.rasterization(*ins, vm.to(DEV), K.to(DEV), W, H, absgrad=True)
+    target = torch.rand(rc.shape, generator=g).to(DEV)
+    return rc, ra, meta, target, means.shape[0]
+
+
+def test_fused_stats_are_counted_once_with_a_retained_graph():
+    """A second backward through a retained graph adds no statistics: the
+    request is consumed by the first (strategy/default.py:235-268 runs once
+    per step)."""
+    from gsplat_amd.strategy.stats import accumulate_grad2d_stats, fuse_grad2d_stats
+    rc, ra, meta, target, N = _fused_stats_step()
+    grad2d, count, fused = fuse_grad2d_stats(meta, None, None, N)
+    assert fused
+    loss = (rc - target).abs().mean()
+    loss.backward(retain_graph=True)
+    g1, c1 = grad2d.clone(), count.clone()
+    loss.backward()
+    assert torch.equal(count, c1) and torch.equal(grad2d, g1)
+    sep_g, sep_c = accumulate_grad2d_stats(meta, None, None, N, packed=True)
+    assert float(sep_c.sum()) > 0
+    assert torch.equal(count, sep_c)
+    torch.testing.assert_close(grad2d, sep_g, rtol=1e-6, atol=1e-9)
+
+
+@pytest.mark.parametrize("backward", [True, False])
+def test_step_outputs_are_freed_without_the_cyclic_collector(backward):
+    """The fused-statistics slot holds means2d weakly, so dropping a step's
+    outputs frees them at once (no reference cycle through the node)."""
+    import gc
+    import weakref
+    from gsplat_amd.strategy.stats import fuse_grad2d_stats
+    gc.collect()
+    gc.disable()
+    try:
+        rc, ra, meta, target, N = _fused_stats_step(seed=41)
+        grad2d, count, _ = fuse_grad2d_stats(meta, None, None, N)
+        if backward:
+            (rc - target).abs().mean().backward()
+            assert float(count.sum()) > 0
+        refs = [weakref.ref(meta["means2d"]), weakref.ref(meta["conics"]),
+                weakref.ref(rc)]
+        del rc, ra, meta, target
+        assert all(r() is None for r in refs), [r() is None for r in refs]
+    finally:
+        gc.enable()
