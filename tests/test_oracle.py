@@ -721,3 +721,75 @@ def test_precision_oracle_is_the_covariance_inverse():
     R = torch_ref.quat_to_rotmat(q)
     P = R @ torch.diag_embed(1.0 / s ** 2) @ R.transpose(-1, -2)
     torch.testing.assert_close(C @ P, torch.eye(3, dtype=torch.float64).expand(64, 3, 3))
+
+
+# --------------------------------------------------------------------------
+# Rows decided by the float operation order
+# --------------------------------------------------------------------------
+def _separate_multiply_add_oracle(tmp_path):
+    """The C oracle with every fused multiply-add taken as a rounded product
+    plus a rounded sum (what a compiler that contracts nothing computes)."""
+    import ctypes
+    import subprocess
+    src = (exact._HERE / "exact_ref.c").read_text()
+    head = "#include <string.h>\n"
+    assert src.count(head) == 1
+    src = src.replace("fmaf(", "sep_fma(")
+    src = src.replace(head, head + "static float sep_fma(float a, float b, float c) "
+                      "{ return a * b + c; }\n")
+    path = tmp_path / "sep.c"
+    path.write_text(src)
+    so = tmp_path / "libsep.so"
+    subprocess.run(["gcc", "-O2", "-fPIC", "-shared", "-std=c11", "-ffp-contract=off",
+                    "-o", str(so), str(path), "-lm"], check=True)
+    return ctypes.CDLL(str(so))
+
+
+def test_rows_decided_by_the_multiply_add_rounding_at_config1(tmp_path):
+    """Integer outputs are bit-exact against the oracle, whose every a * b + c
+    on the decision path is one fused multiply-add, as in the kernels.  A
+    build that rounds the product separately (a compiler that contracts
+    nothing; which products a CUDA build contracts is its compiler's choice)
+    differs only on rows whose radius ceil or tile edge falls within a few
+    ulp of an integer boundary.  This counts them on the full config-1 scene
+    (1M Gaussians, 1280x720): visibility, radii, and the per-row tile sets."""
+    from gsplat_amd._helper import make_scene
+    sc = make_scene(1)
+    ts = 16
+    tw, th = math.ceil(sc.width / ts), math.ceil(sc.height / ts)
+
+    def run():
+        p = exact.projection_fwd(sc.means.numpy(), None, sc.quats.numpy(),
+                                 sc.scales.numpy(), sc.opacities.numpy(),
+                                 sc.viewmats.numpy(), sc.Ks.numpy(), sc.width, sc.height)
+        v = p["valid"][0]
+        rows = np.nonzero(v)[0]
+        cnt, ids, fl = exact.isect_tiles(p["means2d"][0][rows], p["radii"][0][rows],
+                                         p["depths"][0][rows], ts, tw, th, sort=False,
+                                         packed=True, n_images=1,
+                                         image_ids=np.zeros(rows.size, np.int64),
+                                         conics=p["conics"][0][rows],
+                                         opacities=sc.opacities.numpy()[rows])
+        tiles = {}
+        starts = np.concatenate([[0], np.cumsum(cnt)])
+        tile_of = (ids >> 32) & ((1 << 12) - 1)
+        for k, r in enumerate(rows):
+            tiles[r] = tile_of[starts[k]:starts[k + 1]].tobytes()
+        return v, p["radii"][0], tiles, int(ids.size)
+
+    v_f, rad_f, tiles_f, n_f = run()
+    saved = exact._lib
+    try:
+        exact._lib = _separate_multiply_add_oracle(tmp_path)
+        v_s, rad_s, tiles_s, n_s = run()
+    finally:
+        exact._lib = saved
+    vis = np.nonzero(v_f != v_s)[0]
+    both = np.nonzero(v_f & v_s)[0]
+    rad = both[(rad_f[both] != rad_s[both]).any(-1)]
+    til = [r for r in both if tiles_f[r] != tiles_s[r]]
+    print(f"[fma rows] config 1: {v_f.sum()} visible rows, {n_f} intersections; "
+          f"separate multiply-add changes visibility of {vis.size}, radii of {rad.size}, "
+          f"tile sets of {len(til)} rows ({n_s - n_f:+d} intersections)")
+    assert v_f.sum() > 600_000
+    assert vis.size + rad.size + len(til) < 1e-3 * v_f.sum()
