@@ -159,6 +159,58 @@ __device__ __forceinline__ uint32_t strip_mask(float4 box, int32_t tx,
     return m;
 }
 
+// strip_mask refined by the ellipse itself.  For d = mean - pixel centre,
+// sigma(d) = 1/2 (a u^2 + c v^2) + b u v is convex, so over a strip's
+// rectangle of pixel centres it is 0 when the mean lies inside and otherwise
+// smallest on an edge, where it is a parabola with its vertex at
+// u = -b v / a (rows) or v = -b u / c (columns), clamped to the edge.  A
+// strip is dropped when that minimum exceeds sig_max by more than 10^-3
+// sig_max + 10^-4 S, with S = 1/2 a U^2 + |b| U V + 1/2 c V^2 (U, V the
+// largest |u|, |v| over the strip) bounding every term gauss_sigma adds:
+// its float rounding, and this evaluation's, are below 10^-6 S, and an
+// inexact vertex only raises the parabola by a second-order amount.  So a
+// dropped strip holds no pixel centre with gauss_sigma <= sig_max.  Only
+// positive definite conics are refined (the others keep the box's mask).
+template <int TILE, int NW, int WROWS>
+__device__ __forceinline__ uint32_t strip_mask_exact(uint32_t m, float mx, float my,
+                                                     float a, float b, float c,
+                                                     float sig_max, int32_t tx,
+                                                     int32_t ty) {
+    if (m == 0u || !(a > 0.f) || !(c > 0.f) || !(a * c - b * b > 0.f))
+        return m;
+    const float cx0 = (float)(tx * TILE) + 0.5f;
+    const float u0 = mx - (cx0 + (float)(TILE - 1)), u1 = mx - cx0;
+    const float ia = __builtin_amdgcn_rcpf(a), ic = __builtin_amdgcn_rcpf(c);
+    const float U = fmaxf(fabsf(u0), fabsf(u1));
+    const bool u_in = u0 <= 0.f && u1 >= 0.f;
+    const float ab = fabsf(b);
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        if (!((m >> w) & 1u))
+            continue;
+        const float cy0 = (float)(ty * TILE + w * WROWS) + 0.5f;
+        const float v0 = my - (cy0 + (float)(WROWS - 1)), v1 = my - cy0;
+        if (u_in && v0 <= 0.f && v1 >= 0.f)
+            continue;
+        // rows v = v0 and v = v1
+        const float ua = fminf(u1, fmaxf(u0, -b * v0 * ia));
+        const float ub = fminf(u1, fmaxf(u0, -b * v1 * ia));
+        const float qa = 0.5f * (a * ua * ua + c * v0 * v0) + b * ua * v0;
+        const float qb = 0.5f * (a * ub * ub + c * v1 * v1) + b * ub * v1;
+        // columns u = u0 and u = u1
+        const float va = fminf(v1, fmaxf(v0, -b * u0 * ic));
+        const float vb = fminf(v1, fmaxf(v0, -b * u1 * ic));
+        const float qc = 0.5f * (a * u0 * u0 + c * va * va) + b * u0 * va;
+        const float qd = 0.5f * (a * u1 * u1 + c * vb * vb) + b * u1 * vb;
+        const float qmin = fminf(fminf(qa, qb), fminf(qc, qd));
+        const float V = fmaxf(fabsf(v0), fabsf(v1));
+        const float S = 0.5f * (a * U * U + c * V * V) + ab * U * V;
+        if (qmin > sig_max + 1e-3f * sig_max + 1e-4f * S)
+            m &= ~(1u << w);
+    }
+    return m;
+}
+
 // Appends, in slot order, the slots s < n whose strip mask holds this wave's
 // bit to list; returns the count (uniform over the wave).
 template <typename SlotT>
@@ -329,8 +381,10 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
             for (int k = 0; k < CDIM; ++k)
                 sl.col[k] = a.colors[(int64_t)g * CDIM + k];
             sl.col[CDIM] = __int_as_float(idx);
-            s_wmask[tr] = (uint8_t)strip_mask<TILE, NW, WROWS>(
-                alpha_support_box(xy.x, xy.y, ca, cb, cc, sig_max), tx, ty);
+            s_wmask[tr] = (uint8_t)strip_mask_exact<TILE, NW, WROWS>(
+                strip_mask<TILE, NW, WROWS>(
+                    alpha_support_box(xy.x, xy.y, ca, cb, cc, sig_max), tx, ty),
+                xy.x, xy.y, ca, cb, cc, sig_max, tx, ty);
         }
         __syncthreads();
         const int batch_size = min(BS, range_end - batch_start);
@@ -780,8 +834,10 @@ __device__ __forceinline__ void rasterize_bwd_tile(
                 // which waves' pixel strips the Gaussian's alpha support can
                 // reach (wave w holds rows w * WROWS .. of the tile)
                 constexpr int WROWS = (kWave < NT ? kWave : NT) * PX / TILE;
-                s_wmask[slot] = (uint8_t)strip_mask<TILE, NW, WROWS>(
-                    alpha_support_box(xy.x, xy.y, ca, cb, cc, sig_max), tx, ty);
+                s_wmask[slot] = (uint8_t)strip_mask_exact<TILE, NW, WROWS>(
+                    strip_mask<TILE, NW, WROWS>(
+                        alpha_support_box(xy.x, xy.y, ca, cb, cc, sig_max), tx, ty),
+                    xy.x, xy.y, ca, cb, cc, sig_max, tx, ty);
             } else {
                 s_wmask[slot] = 0;
             }

@@ -125,7 +125,10 @@ def test_whole_tile_backward_above_the_replay_budget(render_mode, bg, monkeypatc
 @pytest.mark.parametrize("budget", [None, 0])
 def test_returned_expected_depth_render_may_be_edited_in_place(budget, monkeypatch):
     """The backward keeps its own copy of the expected-depth channel, not the
-    returned render, so the caller may edit the render in place."""
+    returned render, so the caller may edit the render in place.  Reading the
+    edited render would scale the depth term by 3; the two runs may differ
+    only by the rounding of the gradient atomics, whose order varies from run
+    to run (up to ~2e-5 relative where a Gaussian's per-tile terms cancel)."""
     import gsplat_amd as gs
     from gsplat_amd.cuda import _ops
     if budget is not None:
@@ -147,4 +150,4 @@ def test_returned_expected_depth_render_may_be_edited_in_place(budget, monkeypat
         ((rc * v).sum() + ra.sum()).backward()
         grads.append([t.grad for t in leaves])
     for a, b in zip(*grads):
-        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-7)
+        torch.testing.assert_close(a, b, rtol=1e-4, atol=1e-5)
