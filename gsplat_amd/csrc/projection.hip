@@ -270,26 +270,35 @@ struct FwdArgs {
     bool idx32;  // B * C * N < 2^31: row index arithmetic in 32 bits
 };
 
-// row = (b * C + c) * N + g  ->  bc = b * C + c, g, and the Gaussian's input
-// row b * N + g
+// row = (b * C + c) * N + g  ->  bc = b * C + c, g, the Gaussian's input
+// row b * N + g, and (optionally) b and c themselves
 __device__ __forceinline__ void split_row(const FwdArgs &a, int64_t row,
-                                          int64_t &bc, int64_t &g,
-                                          int64_t &bg) {
+                                          int64_t &bc, int64_t &g, int64_t &bg,
+                                          int64_t *b_out = nullptr,
+                                          int64_t *c_out = nullptr) {
+    int64_t b;
     if (a.B * a.C == 1) {
         // one image: no division
         bc = 0;
         g = row;
         bg = row;
+        b = 0;
     } else if (a.idx32) {
         const uint32_t r = (uint32_t)row, n = (uint32_t)a.N;
         const uint32_t q = r / n;
         bc = q;
         g = r - q * n;
-        bg = (int64_t)(q / (uint32_t)a.C) * a.N + g;
+        b = q / (uint32_t)a.C;
+        bg = b * a.N + g;
     } else {
         bc = row / a.N;
         g = row - bc * a.N;
-        bg = (bc / a.C) * a.N + g;
+        b = bc / a.C;
+        bg = b * a.N + g;
+    }
+    if (b_out != nullptr) {
+        *b_out = b;
+        *c_out = bc - b * a.C;
     }
 }
 
@@ -384,11 +393,13 @@ __global__ void __launch_bounds__(kPackThreads) projection_packed_fwd_kernel(
     // are dropped).  The camera is loaded before the rows: loads complete in
     // issue order, so waiting for the camera does not wait for the rows, and
     // projecting slice j waits only for the loads of slices 0..j.
-    int64_t bc[kPackItems], g[kPackItems], bgs[kPackItems];
+    int64_t bc[kPackItems], g[kPackItems], bgs[kPackItems], bi[kPackItems],
+        ci[kPackItems];
 #pragma unroll
     for (int j = 0; j < kPackItems; ++j) {
         const int64_t row = base + (int64_t)j * kPackThreads + threadIdx.x;
-        split_row(a, row < n_rows ? row : n_rows - 1, bc[j], g[j], bgs[j]);
+        split_row(a, row < n_rows ? row : n_rows - 1, bc[j], g[j], bgs[j], &bi[j],
+                  &ci[j]);
     }
     const int64_t bc0 =
         ((int64_t)__builtin_amdgcn_readfirstlane((int)(bc[0] >> 32)) << 32) |
@@ -485,8 +496,8 @@ __global__ void __launch_bounds__(kPackThreads) projection_packed_fwd_kernel(
             row_of[row] = valid ? (int32_t)pos : -1;
         if (!valid)
             continue;
-        batch_ids[pos] = bc[j] / a.C;
-        camera_ids[pos] = bc[j] % a.C;
+        batch_ids[pos] = bi[j];
+        camera_ids[pos] = ci[j];
         gaussian_ids[pos] = g[j];
         reinterpret_cast<int2 *>(radii)[pos] = make_int2(o[j].rx, o[j].ry);
         reinterpret_cast<float2 *>(means2d)[pos] = make_float2(o[j].mx, o[j].my);
