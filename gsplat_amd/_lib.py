@@ -22,7 +22,7 @@ _P = c_void_p
 # of include/gsplat_hip.h.  load() refuses a library built from any other
 # header, and a CPU test keeps this digest and _SIGNATURES equal to the
 # header's.  Change all three together.
-_ABI_VERSION = "88be6fa70834cd68"
+_ABI_VERSION = "5c25e0a7eb4c21f2"
 
 # name -> argtypes (restype int unless listed in _RESTYPES)
 _SIGNATURES = {
@@ -98,6 +98,11 @@ _SIGNATURES = {
     "gsplat_isect_prepare_rows": [
         c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int32, c_int32, c_int32,
         _P, c_size_t, _P, _P, _P, _P, _P],
+    "gsplat_sh_rows_fwd_isect_count": [
+        c_int64, c_int64, c_int64, c_int32, c_int32, _P, _P, _P, _P, _P,
+        c_int64, _P, _P, _P, _P, _P, _P, _P, c_int32, c_int32, c_int32,
+        _P, c_size_t, _P, _P, _P, _P],
+    "gsplat_isect_row_starts": [c_int64, _P, c_size_t, _P, _P, _P],
     "gsplat_isect_emit_tiles_workspace_size": [c_int64],
     "gsplat_isect_emit_tiles": [
         c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int32, c_int32,

@@ -16,7 +16,10 @@
 // defined float->int conversion (saturating, NaN -> 0) and a portable log, so
 // the C host oracle reproduces the integer outputs bit for bit.  Count and
 // emit call the same device function, so the two passes agree exactly.
+#include <algorithm>
+
 #include "radix.h"
+#include "sh_rows.h"
 
 namespace gs {
 namespace {
@@ -808,16 +811,17 @@ __global__ void __launch_bounds__(kIsectThreads)
 // order.  The depth order is taken per tile (~1,000 rows at config 1) in LDS
 // instead of over all rows through device memory.
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(kIsectThreads)
-    isect_count_rows_kernel(const IsectArgs a, int32_t *__restrict__ tiles_per_gauss,
-                            RowRec *__restrict__ recs,
-                            int64_t *__restrict__ starts,
-                            uint64_t *__restrict__ block_tot) {
+// The rows [blk * kIsectThreads, ...) of isect_count_rows_kernel from their
+// records (`rec` holds row_record of the thread's row where it is below
+// a.n): a whole workgroup, which it synchronises.
+__device__ __forceinline__ void isect_count_rows_from(
+    const IsectArgs &a, int64_t blk, const RowRec &rec,
+    int32_t *__restrict__ tiles_per_gauss, RowRec *__restrict__ recs,
+    int64_t *__restrict__ starts, uint64_t *__restrict__ block_tot) {
     __shared__ uint64_t s_wave_tot[kIsectThreads / kWave];
-    const int64_t idx = (int64_t)blockIdx.x * kIsectThreads + threadIdx.x;
+    const int64_t idx = blk * kIsectThreads + threadIdx.x;
     int32_t cnt = 0;
     if (idx < a.n) {
-        const RowRec rec = row_record(a, idx);
         recs[idx] = rec;
         Sweep sw;
         cnt = sweep_setup_rec(a, rec, &sw) ? sweep_tiles<false>(a, sw, nullptr) : 0;
@@ -841,7 +845,51 @@ __global__ void __launch_bounds__(kIsectThreads)
         starts[idx] = (int64_t)(wave_off + incl - (uint64_t)cnt);
     }
     if (threadIdx.x == 0)
-        block_tot[blockIdx.x] = total;
+        block_tot[blk] = total;
+}
+
+__global__ void __launch_bounds__(kIsectThreads)
+    isect_count_rows_kernel(const IsectArgs a, int32_t *__restrict__ tiles_per_gauss,
+                            RowRec *__restrict__ recs,
+                            int64_t *__restrict__ starts,
+                            uint64_t *__restrict__ block_tot) {
+    const int64_t idx = (int64_t)blockIdx.x * kIsectThreads + threadIdx.x;
+    RowRec rec{};
+    if (idx < a.n)
+        rec = row_record(a, idx);
+    isect_count_rows_from(a, blockIdx.x, rec, tiles_per_gauss, recs, starts, block_tot);
+}
+
+// The packed rows' SH colours and their tile counts in one launch.  Thread i
+// takes Gaussian i's colours and packed row i's tile count.  Its count row
+// is loaded first and its coefficient row after; loads complete in issue
+// order, so the tile sweep (arithmetic) runs while the coefficient row (the
+// SH forward's wait) is still in flight, where the two kernels one after
+// the other each waited alone.  The row count comes from the device
+// (*n_dev, written by the projection); rows at or past it count nothing.
+static_assert(kShThreads == kIsectThreads, "one workgroup shape for both parts");
+
+template <int DEG>
+__global__ void __launch_bounds__(kIsectThreads)
+    sh_rows_count_kernel(const ShRowsArgs sa, float *__restrict__ colors, IsectArgs ia,
+                         const int32_t *__restrict__ n_dev,
+                         int32_t *__restrict__ tiles_per_gauss,
+                         RowRec *__restrict__ recs, int64_t *__restrict__ starts,
+                         uint64_t *__restrict__ block_tot) {
+    const int64_t blk = blockIdx.x;
+    const int64_t i = blk * kIsectThreads + threadIdx.x;
+    const int64_t n = *n_dev;
+    const bool counting = blk * kIsectThreads < n;  // the whole workgroup
+    ia.n = n;
+    RowRec rec{};
+    if (i < n)
+        rec = row_record(ia, i);
+    ShRowIn<DEG> in;
+    const bool vis = sh_rows_fwd_load<DEG>(sa, i, in);
+    if (counting)
+        isect_count_rows_from(ia, blk, rec, tiles_per_gauss, recs, starts, block_tot);
+    if (vis)
+        sh_rows_fwd_eval<DEG>(sa, colors, i, in);
 }
 
 // Row starts from the per-workgroup prefixes of isect_count_rows_kernel, in
@@ -1828,6 +1876,76 @@ extern "C" int gsplat_isect_prepare_rows(int64_t n, int64_t N, const int64_t *im
     GS_TRY(check_launch("isect_count_rows_kernel"));
     isect_starts_scan_kernel<<<(unsigned)ceil_div(blocks, kStartsGroup), kIsectThreads,
                                0, st>>>(n, blocks, block_tot, row_starts, n_isects_out);
+    return check_launch("isect_starts_scan_kernel");
+}
+
+extern "C" int gsplat_sh_rows_fwd_isect_count(
+    int64_t B, int64_t C, int64_t N, int32_t K, int32_t degree, const float *means,
+    const float *viewmats, const float *coeffs, const int32_t *row_of, float *colors,
+    int64_t n_cap, const int32_t *n_dev, const int64_t *image_ids,
+    const float *means2d, const int32_t *radii, const float *depths,
+    const float *conics, const float *opacities, int32_t tile_size,
+    int32_t tile_width, int32_t tile_height, void *workspace, size_t workspace_bytes,
+    int32_t *tiles_per_gauss, int64_t *row_starts, float *row_records,
+    gsplat_stream_t stream) {
+    clear_error();
+    GS_REQUIRE(B >= 0 && C >= 0 && N >= 0 && K > 0, "sh_rows_fwd_isect_count: bad sizes");
+    GS_REQUIRE(degree >= 0 && degree <= 4, "sh_rows_fwd_isect_count: degree must be in [0, 4]");
+    GS_REQUIRE((degree + 1) * (degree + 1) <= K,
+               "sh_rows_fwd_isect_count: K too small for the degree");
+    GS_REQUIRE(n_cap >= 0 && n_cap <= B * C * N,
+               "sh_rows_fwd_isect_count: n_cap must be at most B*C*N");
+    IsectArgs ia;
+    // image of a row: image_ids[row] with several images, else row / n_cap (0)
+    GS_TRY(make_args(n_cap, image_ids ? 0 : (n_cap > 0 ? n_cap : 1), 0, image_ids,
+                     means2d, radii, depths, conics, opacities, tile_size, tile_width,
+                     tile_height, ia));
+    if (B * N == 0 || C == 0)
+        return GSPLAT_OK;
+    GS_REQUIRE(means && viewmats && coeffs && row_of && colors && n_dev,
+               "sh_rows_fwd_isect_count: NULL buffer");
+    GS_REQUIRE(depths && conics && opacities && tiles_per_gauss && row_starts && row_records,
+               "sh_rows_fwd_isect_count: NULL buffer");
+    GS_REQUIRE(reinterpret_cast<uintptr_t>(row_records) % 16 == 0,
+               "sh_rows_fwd_isect_count: row_records must be 16-byte aligned");
+    GS_REQUIRE(n_cap < (1ll << 31), "sh_rows_fwd_isect_count: more than 2^31 rows");
+    GS_REQUIRE(workspace &&
+                   workspace_bytes >= gsplat_isect_prepare_rows_workspace_size(n_cap),
+               "sh_rows_fwd_isect_count: workspace too small");
+    const int nb = (degree + 1) * (degree + 1);
+    ShRowsArgs sa{B, C, N, K, means, viewmats, coeffs, row_of,
+                  (K == nb) && aligned16(coeffs)};
+    const int64_t grid = std::max(ceil_div(B * N, (int64_t)kShThreads),
+                                  ceil_div(n_cap, (int64_t)kIsectThreads));
+    uint64_t *block_tot = reinterpret_cast<uint64_t *>(workspace);
+    RowRec *recs = reinterpret_cast<RowRec *>(row_records);
+    hipStream_t st = as_stream(stream);
+#define GS_SHC(DEG)                                                            \
+    sh_rows_count_kernel<DEG><<<(unsigned)grid, kIsectThreads, 0, st>>>(       \
+        sa, colors, ia, n_dev, tiles_per_gauss, recs, row_starts, block_tot)
+    switch (degree) {
+    case 0: GS_SHC(0); break;
+    case 1: GS_SHC(1); break;
+    case 2: GS_SHC(2); break;
+    case 3: GS_SHC(3); break;
+    default: GS_SHC(4); break;
+    }
+#undef GS_SHC
+    return check_launch("sh_rows_count_kernel");
+}
+
+extern "C" int gsplat_isect_row_starts(int64_t n, const void *workspace,
+                                       size_t workspace_bytes, int64_t *row_starts,
+                                       int64_t *n_isects_out, gsplat_stream_t stream) {
+    clear_error();
+    GS_REQUIRE(n > 0 && n < (1ll << 31), "isect_row_starts: n must be in [1, 2^31)");
+    GS_REQUIRE(row_starts && n_isects_out, "isect_row_starts: NULL buffer");
+    GS_REQUIRE(workspace && workspace_bytes >= gsplat_isect_prepare_rows_workspace_size(n),
+               "isect_row_starts: workspace too small");
+    const int64_t blocks = ceil_div(n, (int64_t)kIsectThreads);
+    isect_starts_scan_kernel<<<(unsigned)ceil_div(blocks, kStartsGroup), kIsectThreads,
+                               0, as_stream(stream)>>>(
+        n, blocks, reinterpret_cast<const uint64_t *>(workspace), row_starts, n_isects_out);
     return check_launch("isect_starts_scan_kernel");
 }
 

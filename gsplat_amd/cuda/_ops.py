@@ -315,7 +315,10 @@ def packed_front_fwd(
     opacities that are used as they are, i.e. without compensations), the
     first half of the sorted tile intersection of the rows is queued right
     after the wait, before the host slices the outputs, and its state is
-    left in ``isect["state"]`` for ``isect_emit_sorted``."""
+    left in ``isect["state"]`` for ``isect_emit_sorted``.  With SH colours
+    of one batch, the rows' tile counts share the colour launch
+    (gsplat_sh_rows_fwd_isect_count) and only the row starts follow the
+    wait."""
     _check_proj_inputs(means, covars, quats, scales, opacities, viewmats, Ks)
     if opacities is None:
         raise RuntimeError("packed_front_fwd: opacities are required")
@@ -368,9 +371,33 @@ def packed_front_fwd(
              ptr(row_of), ptr(row_opac), st)
         copied = torch.cuda.Event()
         copied.record()
+        I = B * C
+        tile_first = isect is not None and (
+            int(I).bit_length()
+            + (int(isect["tile_width"]) * int(isect["tile_height"])).bit_length()) <= 32
+        counted = None
         if sh_degree is None:
             call("gsplat_rows_gather", B, C, N, D, ptr(features), ptr(row_of),
                  ptr(row_colors), st)
+        elif tile_first and B == 1:
+            # the colours and the intersection's tile counts in one launch,
+            # over the rows the projection counted on the device
+            # (indptr[I]); the host's wait below then overlaps them both
+            counted = {
+                "tpg": torch.empty(cap, dtype=_I32, device=dev),
+                "row_starts": torch.empty(cap + 1, dtype=_I64, device=dev),
+                "records": torch.empty(cap, 8, dtype=_F32, device=dev),
+                "ws": torch.empty(query("gsplat_isect_prepare_rows_workspace_size", cap),
+                                  dtype=torch.uint8, device=dev),
+            }
+            call("gsplat_sh_rows_fwd_isect_count", B, C, N, K, int(sh_degree),
+                 ptr(means), ptr(viewmats), ptr(features), ptr(row_of), ptr(row_colors),
+                 cap, ptr(indptr[I:]), ptr(camera_ids) if I > 1 else None,
+                 ptr(means2d), ptr(radii), ptr(depths), ptr(conics), ptr(row_opac),
+                 int(isect["tile_size"]), int(isect["tile_width"]),
+                 int(isect["tile_height"]), ptr(counted["ws"]), counted["ws"].numel(),
+                 ptr(counted["tpg"]), ptr(counted["row_starts"]),
+                 ptr(counted["records"]), st)
         else:
             call("gsplat_sh_rows_fwd", B, C, N, K, int(sh_degree), ptr(means),
                  ptr(viewmats), ptr(features), ptr(row_of), ptr(row_colors), st)
@@ -378,17 +405,21 @@ def packed_front_fwd(
         nnz = int(nnz_host[0])
         if isect is not None and nnz > 0:
             ts, tw, th = isect["tile_size"], isect["tile_width"], isect["tile_height"]
-            I = B * C
-            if (int(I).bit_length() + (int(tw) * int(th)).bit_length()) <= 32:
+            if tile_first:
                 if I == 1:
                     img = None
                 else:
                     img = (camera_ids[:nnz] if B == 1
                            else batch_ids[:nnz] * C + camera_ids[:nnz])
-                state = isect_prepare_sorted(
-                    means2d[:nnz], radii[:nnz], depths[:nnz], conics[:nnz],
-                    row_opac[:nnz], img, nnz if I == 1 else 0, I, ts, tw, th,
-                    torch.empty(nnz, dtype=_I32, device=dev))
+                if counted is not None:
+                    state = isect_prepare_counted(
+                        counted, means2d[:nnz], radii[:nnz], depths[:nnz], conics[:nnz],
+                        row_opac[:nnz], img, nnz if I == 1 else 0, I, ts, tw, th)
+                else:
+                    state = isect_prepare_sorted(
+                        means2d[:nnz], radii[:nnz], depths[:nnz], conics[:nnz],
+                        row_opac[:nnz], img, nnz if I == 1 else 0, I, ts, tw, th,
+                        torch.empty(nnz, dtype=_I32, device=dev))
                 cap = isect_capacity(dev)
                 if cap is not None:
                     isect_emit_sorted_queue(state, cap)
@@ -775,6 +806,30 @@ def isect_prepare_sorted(means2d, radii, depths, conics, opacities, img, N, I,
          int(tile_width), int(tile_height), ptr(ws), ws.numel(),
          ptr(tiles_per_gauss), ptr(state["row_starts"]), ptr(state["records"]),
          ptr(host), st)
+    ev = torch.cuda.Event()
+    ev.record()
+    state["total"] = (host, ev)
+    return state
+
+
+def isect_prepare_counted(counted, means2d, radii, depths, conics, opacities, img, N,
+                          I, tile_size, tile_width, tile_height):
+    """isect_prepare_sorted's state for n > 0 rows whose tile counts, count
+    prefixes and sweep records gsplat_sh_rows_fwd_isect_count already wrote
+    into the capacity-sized buffers of ``counted``: only the row starts and
+    the intersection count remain (gsplat_isect_row_starts)."""
+    n = means2d.numel() // 2
+    state = {
+        "n": n, "N": N, "I": int(I), "img": img, "means2d": means2d, "radii": radii,
+        "depths": depths, "conics": conics, "opacities": opacities,
+        "tile": (int(tile_size), int(tile_width), int(tile_height)),
+        "tiles_per_gauss": counted["tpg"][:n],
+        "row_starts": counted["row_starts"][:n + 1],
+        "records": counted["records"][:n],
+    }
+    host = torch.empty(1, dtype=_I64, pin_memory=True)
+    call("gsplat_isect_row_starts", n, ptr(counted["ws"]), counted["ws"].numel(),
+         ptr(state["row_starts"]), ptr(host), _stream(means2d))
     ev = torch.cuda.Event()
     ev.record()
     state["total"] = (host, ev)

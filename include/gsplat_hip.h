@@ -486,6 +486,37 @@ int gsplat_isect_prepare_rows(
     int64_t *row_starts, float *row_records, int64_t *n_isects_out,
     gsplat_stream_t stream);
 
+/* Stage 1 split in two launches with the SH colours of the packed rows in
+ * the first: gsplat_sh_rows_fwd's colours and the tile counts, in-workgroup
+ * count prefixes and sweep records of gsplat_isect_prepare_rows, computed by
+ * one launch whose workgroups alternate between the two kinds (the colour
+ * rows wait on memory, the tile sweep on arithmetic, so the CUs run both at
+ * once).  It replaces the SH evaluation of the packed rows
+ * (gsplat/cuda/csrc/SphericalHarmonicsCUDA.cu:391-462, called from
+ * rendering.py:845-873) and the count pass of Intersect.cpp:79-101.
+ * Colour arguments as gsplat_sh_rows_fwd.  The intersection rows are the
+ * first *n_dev of n_cap (n_dev: one int32 in device memory, such as the
+ * packed projection's indptr[B*C]; n_cap <= B*C*N sizes every row buffer);
+ * image_ids as gsplat_isect_prepare_rows (NULL for one image).  The
+ * workspace (gsplat_isect_prepare_rows_workspace_size(n_cap) bytes) then goes
+ * unchanged to gsplat_isect_row_starts, which finishes row_starts. */
+int gsplat_sh_rows_fwd_isect_count(
+    int64_t B, int64_t C, int64_t N, int32_t K, int32_t degree, const float *means,
+    const float *viewmats, const float *coeffs, const int32_t *row_of, float *colors,
+    int64_t n_cap, const int32_t *n_dev, const int64_t *image_ids,
+    const float *means2d, const int32_t *radii, const float *depths,
+    const float *conics, const float *opacities, int32_t tile_size,
+    int32_t tile_width, int32_t tile_height, void *workspace, size_t workspace_bytes,
+    int32_t *tiles_per_gauss, int64_t *row_starts, float *row_records,
+    gsplat_stream_t stream);
+
+/* The second launch of that split: row_starts [n + 1] and *n_isects_out for
+ * the n rows (= *n_dev) gsplat_sh_rows_fwd_isect_count counted, as
+ * gsplat_isect_prepare_rows writes them (the cumsum of Intersect.cpp:104-105). */
+int gsplat_isect_row_starts(
+    int64_t n, const void *workspace, size_t workspace_bytes, int64_t *row_starts,
+    int64_t *n_isects_out, gsplat_stream_t stream);
+
 /* Tile-first sorted intersection, stage 2 of 2.  Writes every row's tiles at
  * its row-order slots (row_starts, row_records from stage 1), sorts the
  * intersections stably on the image|tile bits, then sorts every tile's rows

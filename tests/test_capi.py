@@ -41,7 +41,8 @@ def test_header_declares_the_survey_export_list():
                      "gsplat_rasterize_to_indices_count",
                      "gsplat_rasterize_to_indices_write", "gsplat_isect_emit_sorted_dev",
                      "gsplat_rasterize_replay_size", "gsplat_rasterize_fwd_replay",
-                     "gsplat_rasterize_bwd_replay"]:
+                     "gsplat_rasterize_bwd_replay", "gsplat_sh_rows_fwd_isect_count",
+                     "gsplat_isect_row_starts"]:
         assert required in names, required
 
 
@@ -127,6 +128,37 @@ def test_argument_errors_are_reported_without_a_gpu(lib_path):
     with pytest.raises(RuntimeError, match="exceed the static scratch"):
         _lib.call("gsplat_projection_packed_fwd_noalloc", 1, 1, limit + 1, 8, None, 8, 8,
                   None, 8, 8, 16, 16, 0.3, 0.01, 1e10, 0.0, 0, *fake, None, None, None)
+
+
+def test_fused_colour_and_count_checks_without_a_gpu(lib_path):
+    """gsplat_sh_rows_fwd_isect_count and gsplat_isect_row_starts refuse bad
+    sizes, a short workspace and missing buffers before the device is
+    touched (the fake pointers are never read)."""
+    from gsplat_amd import _lib
+    f = 256
+    ws = _lib.query("gsplat_isect_prepare_rows_workspace_size", 1000)
+    base = [1, 2, 500, 16, 3, f, f, f, f, f, 1000, f, f, f, f, f, f, f, 16, 4, 3,
+            f, ws, f, f, f, None]
+    args = list(base)
+    args[4] = 5
+    with pytest.raises(RuntimeError, match="degree"):
+        _lib.call("gsplat_sh_rows_fwd_isect_count", *args)
+    args = list(base)
+    args[10] = 1001
+    with pytest.raises(RuntimeError, match="n_cap"):
+        _lib.call("gsplat_sh_rows_fwd_isect_count", *args)
+    args = list(base)
+    args[22] = ws - 1
+    with pytest.raises(RuntimeError, match="workspace"):
+        _lib.call("gsplat_sh_rows_fwd_isect_count", *args)
+    args = list(base)
+    args[11] = None
+    with pytest.raises(RuntimeError, match="NULL"):
+        _lib.call("gsplat_sh_rows_fwd_isect_count", *args)
+    with pytest.raises(RuntimeError, match="workspace"):
+        _lib.call("gsplat_isect_row_starts", 1000, f, ws - 1, f, f, None)
+    with pytest.raises(RuntimeError, match="n must be"):
+        _lib.call("gsplat_isect_row_starts", 0, f, ws, f, f, None)
 
 
 def test_replay_workspace_size_and_checks_without_a_gpu(lib_path):

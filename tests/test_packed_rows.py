@@ -87,3 +87,71 @@ def test_sh_rows_fwd_bwd(degree, C):
     assert_close(col.cpu(), r64.detach(), 1e-4, 1e-5, "colors")
     print(assert_grad_close(gc.grad, c64, c32, 1e-4, 1e-5, "v_coeffs"))
     print(assert_grad_close(gm.grad, m64, m32, 1e-4, 1e-5, "v_means"))
+
+
+@pytest.mark.parametrize("degree,C", [(3, 1), (1, 3), (0, 2), (4, 1)])
+def test_fused_colours_and_tile_counts_match_the_separate_launches(degree, C):
+    """gsplat_sh_rows_fwd_isect_count + gsplat_isect_row_starts against
+    gsplat_sh_rows_fwd and gsplat_isect_prepare_rows on the same packed rows:
+    colours, tile counts, row starts, the intersection count and the sweep
+    records equal bit for bit; the row count is read from indptr[C] on the
+    device, and the capacity-sized buffers past it are not written."""
+    import math
+
+    from gsplat_amd._lib import call, ptr, query
+    from gsplat_amd.cuda import _ops
+    means, quats, scales, opac, vm, K, W, H = small_scene(seed=40 + degree, N=3000, C=C)
+    N = means.shape[0]
+    gen = torch.Generator().manual_seed(7)
+    coeffs = torch.randn(1, N, (degree + 1) ** 2, 3, generator=gen).to(DEV)
+    md, vmd = means.to(DEV)[None], vm.to(DEV)[None]
+    out = _ops.projection_packed_fwd_with_row_map(
+        means.to(DEV), None, quats.to(DEV), scales.to(DEV), opac.to(DEV),
+        vm.to(DEV), K.to(DEV), W, H, 0.3, 0.01, 1e10, 0.0, False, 0)
+    indptr, b, c, g, radii, m2, dep, con, comp, row_of = out
+    nnz = m2.shape[0]
+    cap = C * N
+    assert 0 < nnz < cap
+    row_opac = opac.to(DEV)[g]
+    ts = 16
+    tw, th = math.ceil(W / ts), math.ceil(H / ts)
+    img = c if C > 1 else None
+
+    # separate launches
+    colors_ref = _ops.sh_rows_fwd(degree, md, vmd, coeffs, row_of, nnz)
+    state = _ops.isect_prepare_sorted(m2, radii, dep, con, row_opac, img,
+                                      nnz if C == 1 else 0, C, ts, tw, th,
+                                      torch.empty(nnz, dtype=torch.int32, device=DEV))
+    torch.cuda.synchronize()
+    n_isects_ref = int(state["total"][0][0])
+
+    # fused: capacity-sized inputs and outputs, the row count on the device
+    def padded(t, fill=0):
+        full = torch.full((cap,) + tuple(t.shape[1:]), fill, dtype=t.dtype, device=DEV)
+        full[:nnz] = t
+        return full
+    m2c, radc, depc, conc, opc = (padded(t) for t in (m2, radii, dep, con, row_opac))
+    imgc = padded(c) if C > 1 else None
+    sentinel = -7
+    colors = torch.full((cap, 3), float(sentinel), device=DEV)
+    tpg = torch.full((cap,), sentinel, dtype=torch.int32, device=DEV)
+    starts = torch.full((cap + 1,), sentinel, dtype=torch.int64, device=DEV)
+    recs = torch.full((cap, 8), float(sentinel), device=DEV)
+    ws = torch.empty(query("gsplat_isect_prepare_rows_workspace_size", cap),
+                     dtype=torch.uint8, device=DEV)
+    n_isects = torch.empty(1, dtype=torch.int64, device=DEV)
+    call("gsplat_sh_rows_fwd_isect_count", 1, C, N, coeffs.shape[-2], degree, ptr(md),
+         ptr(vmd), ptr(coeffs), ptr(row_of), ptr(colors), cap, ptr(indptr[C:]),
+         ptr(imgc), ptr(m2c), ptr(radc), ptr(depc), ptr(conc), ptr(opc), ts, tw, th,
+         ptr(ws), ws.numel(), ptr(tpg), ptr(starts), ptr(recs), 0)
+    call("gsplat_isect_row_starts", nnz, ptr(ws), ws.numel(), ptr(starts),
+         ptr(n_isects), 0)
+    torch.cuda.synchronize()
+    assert torch.equal(colors[:nnz], colors_ref)
+    assert torch.equal(tpg[:nnz], state["tiles_per_gauss"])
+    assert torch.equal(starts[:nnz + 1], state["row_starts"])
+    assert int(n_isects) == n_isects_ref == int(state["row_starts"][-1])
+    assert torch.equal(recs[:nnz], state["records"])
+    # nothing past the row count
+    assert bool((tpg[nnz:] == sentinel).all()) and bool((starts[nnz + 1:] == sentinel).all())
+    assert bool((recs[nnz:] == sentinel).all()) and bool((colors[nnz:] == sentinel).all())
