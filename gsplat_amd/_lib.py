@@ -22,7 +22,7 @@ _P = c_void_p
 # of include/gsplat_hip.h.  load() refuses a library built from any other
 # header, and a CPU test keeps this digest and _SIGNATURES equal to the
 # header's.  Change all three together.
-_ABI_VERSION = "5c25e0a7eb4c21f2"
+_ABI_VERSION = "32d339af5a896531"
 
 # name -> argtypes (restype int unless listed in _RESTYPES)
 _SIGNATURES = {
@@ -63,6 +63,11 @@ _SIGNATURES = {
         c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P,
         c_int32, c_int32, c_float, c_int32,
         _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+    "gsplat_projection_packed_bwd_rows_sh": [
+        c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P,
+        c_int32, c_int32, c_float, c_int32,
+        _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+        c_float, c_float, _P, _P, c_int32, c_int32, _P, _P, _P, _P],
     "gsplat_projection_packed_bwd_rows_stats": [
         c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P,
         c_int32, c_int32, c_float, c_int32,

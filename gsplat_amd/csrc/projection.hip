@@ -23,7 +23,7 @@
 //     the C cameras, so gradients need no atomics and are deterministic.
 #include <mutex>
 
-#include "common.h"
+#include "sh_rows.h"
 
 namespace gs {
 namespace {
@@ -910,15 +910,17 @@ __device__ __forceinline__ void flush_viewmat_grad(float *v_viewmat,
     __syncthreads();
 }
 
+// One thread per (b, g) of workgroup `blk`; loops over the C cameras.  The
+// rows are the dense (b, c, g) rows (visible when both radii are positive)
+// or, with row_of, the packed rows row_of[(b C + c) N + g] (visible when
+// >= 0).  vm_add (three floats per thread, or NULL) is added to v_means
+// like a.v_means_add.
 template <bool kWantCam>
-__global__ void __launch_bounds__(kProjThreads)
-    projection_fused_bwd_kernel(const BwdArgs a, const int32_t *__restrict__ radii,
-                                const int32_t *__restrict__ row_of) {
-    __shared__ float s_red[(kProjThreads / kWave) * 12];
-    // one thread per (b, g); loops over the C cameras.  The rows are the
-    // dense (b, c, g) rows (visible when both radii are positive) or, with
-    // row_of, the packed rows row_of[(b C + c) N + g] (visible when >= 0).
-    const int64_t bg = (int64_t)blockIdx.x * kProjThreads + threadIdx.x;
+__device__ __forceinline__ void projection_bwd_gaussian(
+    const BwdArgs &a, const int32_t *__restrict__ radii,
+    const int32_t *__restrict__ row_of, int64_t blk, const float *vm_add,
+    float *s_red) {
+    const int64_t bg = blk * kProjThreads + threadIdx.x;
     const bool in_range = bg < a.B * a.N;
     const int64_t b = in_range ? bg / a.N : 0;
     const int64_t g = in_range ? bg % a.N : 0;
@@ -995,7 +997,7 @@ __global__ void __launch_bounds__(kProjThreads)
         if (want_cam) {
             // b is uniform over the block unless the block straddles two
             // batches (only when N is not a multiple of the block size).
-            const int64_t first = (int64_t)blockIdx.x * kProjThreads;
+            const int64_t first = blk * kProjThreads;
             const int64_t last_row = first + kProjThreads - 1 < a.B * a.N - 1
                                          ? first + kProjThreads - 1
                                          : a.B * a.N - 1;
@@ -1021,7 +1023,11 @@ __global__ void __launch_bounds__(kProjThreads)
         // rounded to float32 before the added term: the sum autograd forms
         // when the two gradients of the means come from separate nodes
         float vm[3] = {(float)v_mean[0], (float)v_mean[1], (float)v_mean[2]};
-        if (a.v_means_add != nullptr) {
+        if (vm_add != nullptr) {
+#pragma unroll
+            for (int k = 0; k < 3; ++k)
+                vm[k] += vm_add[k];
+        } else if (a.v_means_add != nullptr) {
 #pragma unroll
             for (int k = 0; k < 3; ++k)
                 vm[k] += a.v_means_add[bg * 3 + k];
@@ -1068,6 +1074,34 @@ __global__ void __launch_bounds__(kProjThreads)
             a.v_scales[bg * 3 + 2] = (float)v_s[2];
         }
     }
+}
+
+template <bool kWantCam>
+__global__ void __launch_bounds__(kProjThreads)
+    projection_fused_bwd_kernel(const BwdArgs a, const int32_t *__restrict__ radii,
+                                const int32_t *__restrict__ row_of) {
+    __shared__ float s_red[(kProjThreads / kWave) * 12];
+    projection_bwd_gaussian<kWantCam>(a, radii, row_of, blockIdx.x, nullptr, s_red);
+}
+
+// The packed path's backward through the row map with the SH colours' in the
+// same launch: each workgroup first runs the SH backward of its 256
+// Gaussians (coalesced coefficient tiles through LDS, dense v_coeffs rows),
+// which keeps each thread's direction term of dL/dmean in registers, then
+// their geometry backward, which adds that term.  Workgroups in the
+// memory-bound SH part and in the latency-bound double-precision part share
+// the CUs, and the direction term makes no round trip through memory.
+static_assert(kProjThreads == kShThreads, "one workgroup shape for both parts");
+
+template <int DEG>
+__global__ void __launch_bounds__(kProjThreads)
+    sh_projection_bwd_kernel(const BwdArgs a, const ShRowsArgs sa,
+                             const float *__restrict__ v_colors,
+                             float *__restrict__ v_coeffs,
+                             const int32_t *__restrict__ row_of) {
+    float vm[3];
+    sh_rows_bwd_block<DEG>(sa, v_colors, v_coeffs, (int64_t)blockIdx.x * kShThreads, vm);
+    projection_bwd_gaussian<false>(a, nullptr, row_of, blockIdx.x, vm, nullptr);
 }
 
 __global__ void __launch_bounds__(kProjThreads) projection_packed_bwd_kernel(
@@ -1631,6 +1665,65 @@ extern "C" int gsplat_projection_packed_bwd_rows_stats(
               v_viewmats, v_row_opacities, v_opacities, v_means_add,
               stat_grads, stat_scale_x, stat_scale_y, grad2d, count};
     return packed_bwd_rows_launch(a, row_of, as_stream(stream));
+}
+
+extern "C" int gsplat_projection_packed_bwd_rows_sh(
+    int64_t B, int64_t C, int64_t N, const float *means, const float *covars,
+    const float *quats, const float *scales, const float *viewmats,
+    const float *Ks, int32_t image_width, int32_t image_height, float eps2d,
+    int32_t camera_model, const int32_t *row_of, const float *conics,
+    const float *compensations, const float *v_means2d, const float *v_depths,
+    const float *v_conics, const float *v_compensations, float *v_means,
+    float *v_covars, float *v_quats, float *v_scales, const float *v_row_opacities,
+    float *v_opacities, const float *stat_grads, float stat_scale_x,
+    float stat_scale_y, float *grad2d, float *count, int32_t K, int32_t degree,
+    const float *coeffs, const float *v_colors, float *v_coeffs,
+    gsplat_stream_t stream) {
+    clear_error();
+    GS_TRY(check_common(B, C, N, means, covars, quats, scales, viewmats, Ks,
+                        image_width, image_height, camera_model));
+    const bool stats = stat_grads != nullptr || grad2d != nullptr || count != nullptr;
+    if (stats) {
+        GS_REQUIRE(stat_grads && grad2d && count,
+                   "projection_packed_bwd_rows_sh: NULL statistics buffer");
+        GS_REQUIRE(B == 1, "projection_packed_bwd_rows_sh: statistics for one batch only");
+    }
+    GS_REQUIRE(degree >= 0 && degree <= 4,
+               "projection_packed_bwd_rows_sh: degree must be in [0, 4]");
+    const int nb = (degree + 1) * (degree + 1);
+    GS_REQUIRE(K >= nb, "projection_packed_bwd_rows_sh: K too small for the degree");
+    if (B * N == 0)
+        return GSPLAT_OK;
+    GS_REQUIRE(v_means && coeffs && v_colors && v_coeffs,
+               "projection_packed_bwd_rows_sh: NULL buffer");
+    GS_REQUIRE((v_row_opacities == nullptr) == (v_opacities == nullptr),
+               "projection_packed_bwd_rows_sh: v_row_opacities and v_opacities go together");
+    GS_REQUIRE(row_of && conics && v_means2d && v_conics,
+               "projection_packed_bwd_rows_sh: NULL buffer");
+    GS_REQUIRE(v_compensations == nullptr || compensations != nullptr,
+               "projection_packed_bwd_rows_sh: v_compensations needs compensations");
+    BwdArgs a{B, C, N, means, covars, quats, scales, viewmats, Ks,
+              (float)image_width, (float)image_height, eps2d, camera_model,
+              conics, compensations, v_means2d, v_depths, v_conics,
+              v_compensations, v_means, v_covars, v_quats, v_scales,
+              nullptr, v_row_opacities, v_opacities, nullptr,
+              stat_grads, stat_scale_x, stat_scale_y, grad2d, count};
+    ShRowsArgs sa{B, C, N, K, means, viewmats, coeffs, row_of,
+                  (K == nb) && aligned16(coeffs) && aligned16(v_coeffs)};
+    const unsigned grid = (unsigned)ceil_div(B * N, kProjThreads);
+    hipStream_t st = as_stream(stream);
+#define GS_SHP(DEG)                                                            \
+    sh_projection_bwd_kernel<DEG><<<grid, kProjThreads, 0, st>>>(a, sa, v_colors, \
+                                                                v_coeffs, row_of)
+    switch (degree) {
+    case 0: GS_SHP(0); break;
+    case 1: GS_SHP(1); break;
+    case 2: GS_SHP(2); break;
+    case 3: GS_SHP(3); break;
+    default: GS_SHP(4); break;
+    }
+#undef GS_SHP
+    return check_launch("sh_projection_bwd_kernel");
 }
 
 extern "C" int gsplat_projection_packed_bwd(

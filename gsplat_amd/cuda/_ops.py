@@ -606,6 +606,80 @@ def projection_packed_bwd_rows(
     return v_means, v_covars, v_quats, v_scales, v_viewmats
 
 
+def projection_packed_bwd_rows_sh(
+    means: Tensor,
+    covars: Optional[Tensor],
+    quats: Optional[Tensor],
+    scales: Optional[Tensor],
+    viewmats: Tensor,
+    Ks: Tensor,
+    image_width: int,
+    image_height: int,
+    eps2d: float,
+    camera_model: int,
+    row_of: Tensor,
+    conics: Tensor,
+    compensations: Optional[Tensor],
+    v_means2d: Tensor,
+    v_depths: Optional[Tensor],
+    v_conics: Tensor,
+    v_compensations: Optional[Tensor],
+    degree: int,
+    coeffs: Tensor,
+    v_colors: Tensor,
+    v_row_opacities: Optional[Tensor] = None,
+    stats: Optional[Tuple[Tensor, float, float, Tensor, Tensor]] = None,
+):
+    """projection_packed_bwd_rows (no view-matrix gradients) with the SH
+    colours' backward of the same rows in the same launch
+    (gsplat_projection_packed_bwd_rows_sh): the SH direction term is added to
+    v_means inside the launch.  coeffs [..., N, K, 3] as the forward's,
+    v_colors [nnz, 3].  Returns (v_means, v_covars, v_quats, v_scales,
+    v_opacities or None, v_coeffs)."""
+    _check_proj_inputs(means, covars, quats, scales, None, viewmats, Ks)
+    check_input(row_of, "row_of", _I32)
+    for t, n in ((conics, "conics"), (v_means2d, "v_means2d"), (v_depths, "v_depths"),
+                 (v_conics, "v_conics"), (compensations, "compensations"),
+                 (v_compensations, "v_compensations"), (coeffs, "coeffs"),
+                 (v_colors, "v_colors")):
+        check_input(t, n)
+    check_input(v_row_opacities, "v_row_opacities", _F32)
+    batch_dims, B, C, N = _proj_dims(means, viewmats)
+    K = coeffs.shape[-2]
+    if tuple(coeffs.shape) != tuple(batch_dims) + (N, K, 3) or v_colors.shape != conics.shape:
+        raise RuntimeError("projection_packed_bwd_rows_sh: coeffs must be [..., N, K, 3] "
+                           "and v_colors [nnz, 3]")
+    if conics.shape[0] == 0:
+        raise RuntimeError("projection_packed_bwd_rows_sh: no visible row (use the "
+                           "separate backward passes)")
+    v_means = torch.empty_like(means)
+    v_covars = torch.empty_like(covars) if covars is not None else None
+    v_quats = torch.empty_like(quats) if covars is None else None
+    v_scales = torch.empty_like(scales) if covars is None else None
+    v_coeffs = torch.empty_like(coeffs)
+    v_opacities = (torch.empty(means.shape[:-1], dtype=_F32, device=means.device)
+                   if v_row_opacities is not None else None)
+    grads = grad2d = count = None
+    sx = sy = 0.0
+    if stats is not None:
+        grads, sx, sy, grad2d, count = stats
+        check_input(grads, "stat_grads", _F32)
+        check_input(grad2d, "grad2d", _F32)
+        check_input(count, "count", _F32)
+        if grads.shape != conics[:, :2].shape or grad2d.numel() != N or count.numel() != N:
+            raise RuntimeError("projection_packed_bwd_rows_sh: statistics buffers must be "
+                               "[nnz, 2] row gradients and [N] accumulators")
+    call("gsplat_projection_packed_bwd_rows_sh", B, C, N, ptr(means), ptr(covars),
+         ptr(quats), ptr(scales), ptr(viewmats), ptr(Ks), int(image_width),
+         int(image_height), float(eps2d), int(camera_model), ptr(row_of), ptr(conics),
+         ptr(compensations), ptr(v_means2d), ptr(v_depths), ptr(v_conics),
+         ptr(v_compensations), ptr(v_means), ptr(v_covars), ptr(v_quats), ptr(v_scales),
+         ptr(v_row_opacities), ptr(v_opacities), ptr(grads), float(sx), float(sy),
+         ptr(grad2d), ptr(count), K, int(degree), ptr(coeffs), ptr(v_colors),
+         ptr(v_coeffs), _stream(means))
+    return v_means, v_covars, v_quats, v_scales, v_opacities, v_coeffs
+
+
 # --------------------------------------------------------------------------
 # Packed rows driven by Gaussian (replace the gathers / index_put scatters of
 # the packed path, rendering.py:95-213, 782, 845-873)

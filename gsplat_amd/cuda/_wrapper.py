@@ -855,9 +855,16 @@ class _PackedFrontEnd(torch.autograd.Function):
         B = math.prod(batch_dims)
         need = ctx.needs_input_grad
         # colour VJP first: its direction term is added to v_means below
+        # (for SH colours of visible rows seen by one camera, inside the
+        # geometry backward's launch, gsplat_projection_packed_bwd_rows_sh:
+        # config 1 115 -> 107 us, config 4 245 -> 225 us, but eight cameras
+        # (config 2) 117 -> 128 us, where the geometry part's camera loop
+        # dominates)
         v_features = None
         v_means_sh = None
-        if v_row_colors is not None and (need[5] or need[0]):
+        sh_fused = (v_row_colors is not None and (need[5] or need[0])
+                    and ctx.sh_degree is not None and conics.shape[0] > 0 and C == 1)
+        if v_row_colors is not None and (need[5] or need[0]) and not sh_fused:
             v_row_colors = v_row_colors.contiguous()
             if ctx.sh_degree is None:
                 if need[5]:
@@ -896,14 +903,24 @@ class _PackedFrontEnd(torch.autograd.Function):
                     raise RuntimeError("fused densification statistics need "
                                        "absgrad=True in rasterization()")
             stats = (rows.contiguous(), slot.scale_x, slot.scale_y, grad2d, count)
-        res = _ops.projection_packed_bwd_rows(
-            means, covars, quats, scales, viewmats, Ks, ctx.width, ctx.height,
-            ctx.eps2d, ctx.camera_model_type, row_of, conics, compensations,
-            v_means2d, None if v_depths is None else v_depths.contiguous(),
-            v_conics, v_compensations, False, v_row_opacities=v_row_opac,
-            v_means_add=v_means_sh, stats=stats)
-        v_means, v_covars, v_quats, v_scales = res[:4]
-        v_opacities = res[5] if v_row_opac is not None else None
+        if sh_fused:
+            res = _ops.projection_packed_bwd_rows_sh(
+                means, covars, quats, scales, viewmats, Ks, ctx.width, ctx.height,
+                ctx.eps2d, ctx.camera_model_type, row_of, conics, compensations,
+                v_means2d, None if v_depths is None else v_depths.contiguous(),
+                v_conics, v_compensations, ctx.sh_degree, features,
+                v_row_colors.contiguous(), v_row_opacities=v_row_opac, stats=stats)
+            v_means, v_covars, v_quats, v_scales, v_opacities, v_coeffs = res
+            v_features = v_coeffs if need[5] else None
+        else:
+            res = _ops.projection_packed_bwd_rows(
+                means, covars, quats, scales, viewmats, Ks, ctx.width, ctx.height,
+                ctx.eps2d, ctx.camera_model_type, row_of, conics, compensations,
+                v_means2d, None if v_depths is None else v_depths.contiguous(),
+                v_conics, v_compensations, False, v_row_opacities=v_row_opac,
+                v_means_add=v_means_sh, stats=stats)
+            v_means, v_covars, v_quats, v_scales = res[:4]
+            v_opacities = res[5] if v_row_opac is not None else None
         return (v_means if need[0] else None,
                 v_covars if need[1] else None,
                 v_quats if need[2] else None,

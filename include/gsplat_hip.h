@@ -349,6 +349,30 @@ int gsplat_sh_rows_bwd(
     const int32_t *row_of, const float *v_colors, float *v_coeffs,
     float *v_means, gsplat_stream_t stream);
 
+/* gsplat_sh_rows_bwd and gsplat_projection_packed_bwd_rows_stats in one
+ * launch, for rasterization()'s packed front end: every workgroup runs the
+ * SH backward of its 256 Gaussians (v_coeffs [B,N,K,3], fully written),
+ * keeps each Gaussian's direction term of dL/dmean in registers, then runs
+ * their geometry backward and adds that term to v_means (required).  The
+ * results equal the two calls with the SH call's v_means passed as
+ * v_means_add.  No view-matrix gradients; the statistics buffers
+ * (stat_grads, grad2d, count) are all NULL or all given (one batch).
+ * Replaces the backward of the packed rows' SH evaluation and of
+ * projection_ewa_3dgs_packed (SphericalHarmonicsCUDA.cu:465-552,
+ * Projection.cpp:439-576). */
+int gsplat_projection_packed_bwd_rows_sh(
+    int64_t B, int64_t C, int64_t N, const float *means, const float *covars,
+    const float *quats, const float *scales, const float *viewmats,
+    const float *Ks, int32_t image_width, int32_t image_height, float eps2d,
+    int32_t camera_model, const int32_t *row_of, const float *conics,
+    const float *compensations, const float *v_means2d, const float *v_depths,
+    const float *v_conics, const float *v_compensations, float *v_means,
+    float *v_covars, float *v_quats, float *v_scales, const float *v_row_opacities,
+    float *v_opacities, const float *stat_grads, float stat_scale_x,
+    float stat_scale_y, float *grad2d, float *count, int32_t K, int32_t degree,
+    const float *coeffs, const float *v_colors, float *v_coeffs,
+    gsplat_stream_t stream);
+
 /* out[row_of[b,c,g]] = src[b,g] for every packed row: the per-Gaussian
  * feature gather of the packed path (opacities / colours,
  * gsplat/rendering.py:782, 170-213).  src [B,N,F], out [nnz,F]. */

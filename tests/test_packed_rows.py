@@ -155,3 +155,54 @@ def test_fused_colours_and_tile_counts_match_the_separate_launches(degree, C):
     # nothing past the row count
     assert bool((tpg[nnz:] == sentinel).all()) and bool((starts[nnz + 1:] == sentinel).all())
     assert bool((recs[nnz:] == sentinel).all()) and bool((colors[nnz:] == sentinel).all())
+
+
+@pytest.mark.parametrize("degree,C,stats", [(3, 1, True), (1, 3, False), (4, 2, False),
+                                            (0, 1, True)])
+def test_fused_colour_and_geometry_backward_matches_the_separate_passes(degree, C, stats):
+    """gsplat_projection_packed_bwd_rows_sh against gsplat_sh_rows_bwd then
+    gsplat_projection_packed_bwd_rows(_stats) with the SH call's v_means as
+    v_means_add: every gradient (coefficients, means, quaternions, scales,
+    opacities) and the densification statistics equal bit for bit."""
+    from gsplat_amd.cuda import _ops
+    means, quats, scales, opac, vm, K, W, H = small_scene(seed=60 + degree, N=2500, C=C)
+    N = means.shape[0]
+    gen = torch.Generator().manual_seed(8)
+    coeffs = torch.randn(1, N, (degree + 1) ** 2 + 2, 3, generator=gen).to(DEV)
+    out = _ops.projection_packed_fwd_with_row_map(
+        means.to(DEV), None, quats.to(DEV), scales.to(DEV), opac.to(DEV),
+        vm.to(DEV), K.to(DEV), W, H, 0.3, 0.01, 1e10, 0.0, False, 0)
+    indptr, b, c, g, radii, m2, dep, con, comp, row_of = out
+    nnz = m2.shape[0]
+    args = (means.to(DEV)[None], None, quats.to(DEV)[None], scales.to(DEV)[None],
+            vm.to(DEV)[None], K.to(DEV)[None], W, H, 0.3, 0, row_of, con, None)
+    v_m2 = torch.randn(nnz, 2, generator=gen).to(DEV)
+    v_dep = torch.randn(nnz, generator=gen).to(DEV)
+    v_con = torch.randn(nnz, 3, generator=gen).to(DEV)
+    v_col = torch.randn(nnz, 3, generator=gen).to(DEV)
+    v_rop = torch.randn(nnz, generator=gen).to(DEV)
+
+    def stats_bufs():
+        if not stats:
+            return None
+        return (torch.randn(nnz, 2, generator=torch.Generator().manual_seed(9)).to(DEV),
+                640.0, 360.0, torch.full((N,), 0.5, device=DEV),
+                torch.full((N,), 2.0, device=DEV))
+
+    v_coeffs_ref, v_means_sh = _ops.sh_rows_bwd(degree, args[0], args[4], coeffs, row_of,
+                                                v_col)
+    st_ref = stats_bufs()
+    ref = _ops.projection_packed_bwd_rows(*args, v_m2, v_dep, v_con, None, False,
+                                          v_row_opacities=v_rop, v_means_add=v_means_sh,
+                                          stats=st_ref)
+    st = stats_bufs()
+    got = _ops.projection_packed_bwd_rows_sh(*args, v_m2, v_dep, v_con, None, degree,
+                                             coeffs, v_col, v_row_opacities=v_rop,
+                                             stats=st)
+    torch.cuda.synchronize()
+    for name, x, y in (("v_means", got[0], ref[0]), ("v_quats", got[2], ref[2]),
+                       ("v_scales", got[3], ref[3]), ("v_opacities", got[4], ref[5]),
+                       ("v_coeffs", got[5], v_coeffs_ref)):
+        assert torch.equal(x, y), name
+    if stats:
+        assert torch.equal(st[3], st_ref[3]) and torch.equal(st[4], st_ref[4])
