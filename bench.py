@@ -118,6 +118,19 @@ def _algorithmic_bytes(name, ctx):
     if name == "gsplat_sh_rows_bwd":
         return (N * 4 * ctx["C"] + nnz * (12 + 12 * K + 12)
                 + N * (12 * K + 12))
+    if name == "gsplat_sh_rows_fwd_isect_count":
+        # gsplat_sh_rows_fwd plus the count pass: the rows' 32-byte sweep
+        # inputs in; their counts, in-block prefixes and records out
+        return (N * 4 * ctx["C"] + nnz * (12 + 12 * K) + nnz * 12
+                + nnz * (32 + 4 + 8 + 32))
+    if name == "gsplat_isect_row_starts":
+        return nnz * 16
+    if name == "gsplat_projection_packed_bwd_rows_sh":
+        # gsplat_projection_packed_bwd_rows plus the SH backward's
+        # coefficients and colour gradients in and dense v_coeffs out (the
+        # row map, the means and v_means counted once)
+        return (N * 4 * ctx["C"] + nnz * (44 + 12 + 8 + 4 + 12) + N * 40
+                + nnz * (12 * K + 12) + N * 12 * K)
     if name in ("gsplat_isect_emit_tiles", "gsplat_isect_emit_tiles_dev"):
         # the rows' 32-byte sweep records and starts in; sorted 64-bit ids,
         # rows and tile offsets out
