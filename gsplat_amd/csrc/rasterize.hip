@@ -674,7 +674,7 @@ __device__ __forceinline__ void rasterize_bwd_tile(
     // column tr % TILE) of the tile, so a thread's pixels share one column
     // (one dx per Gaussian)
     const float px = (float)(tx * TILE + tr % TILE) + 0.5f;
-    float py[PX], T[PX], Kv[PX];
+    float py[PX], Kv[PX];
     double Bv[PX];
     double T64[PX];
     int32_t bin_final[PX];
@@ -699,7 +699,6 @@ __device__ __forceinline__ void rasterize_bwd_tile(
         // from the fp32 reciprocal, so T keeps only the forward's own rounding
         // instead of one extra float32 rounding per Gaussian behind it.
         T64[p] = (double)T_final;
-        T[p] = T_final;
         bin_final[p] = inside ? last_ids[pix] : -1;
         wave_bin = max(wave_bin, bin_final[p]);
 #pragma unroll
@@ -784,8 +783,7 @@ __device__ __forceinline__ void rasterize_bwd_tile(
                      ++m) {
                     const float *r = records + replay_record_slot(range_start, m, Q) * RS;
                     if (m == unit + 1) {
-                        T[p] = r[lp];
-                        T64[p] = (double)T[p];
+                        T64[p] = (double)r[lp];
                     }
 #pragma unroll
                     for (int k = 0; k < CDIM; ++k)
@@ -795,6 +793,12 @@ __device__ __forceinline__ void rasterize_bwd_tile(
             }
         }
     }
+
+    // B - K, the running sum the loop carries (B grows, K is fixed)
+    double BK[PX];
+#pragma unroll
+    for (int p = 0; p < PX; ++p)
+        BK[p] = Bv[p] - (double)Kv[p];
 
     // the tile-sum slot this lane adds from every reduced register
     using RR = RowReduce<NACC>;
@@ -860,19 +864,10 @@ __device__ __forceinline__ void rasterize_bwd_tile(
         // support reaches the wave's pixels
         const int t0 = max(0, batch_end - wave_bin_final);
         const int n_work = wave_work_list(s_wmask, t0, batch_size, wave, s_list[wave]);
-        // software pipeline: the next work item's slot and geometry are read
-        // one iteration ahead, so the two dependent LDS round trips overlap
-        // the current Gaussian's arithmetic
-        int t_nx = n_work > 0 ? (int)s_list[wave][0] : 0;
-        float4 geo_nx = s_geo[t_nx], con_nx = s_con[t_nx];
-        for (int n = 0; n < n_work; ++n) {
-            const int t = t_nx;
+        // One work item: Gaussian t of the batch on this wave's pixels.
+        auto work_item = [&](const int t, const float4 geo,
+                             const float4 con) __attribute__((always_inline)) {
             const int32_t isect = batch_end - t;
-            const float4 geo = geo_nx;
-            const float4 con = con_nx;
-            t_nx = s_list[wave][min(n + 1, n_work - 1)];
-            geo_nx = s_geo[t_nx];
-            con_nx = s_con[t_nx];
             const float dx = geo.x - px;
             float dy[PX], sigma[PX];
             bool valid[PX];
@@ -890,7 +885,7 @@ __device__ __forceinline__ void rasterize_bwd_tile(
                 any_m |= valid_m;
             }
             if (any_m == 0)
-                continue;
+                return;
             // Branch-free over the lane's pixels: an invalid pixel runs the
             // same arithmetic and its contributions are zeroed through
             // selects (fac, w, T64), so nothing is carried through divergent
@@ -918,8 +913,7 @@ __device__ __forceinline__ void rasterize_bwd_tile(
                 double r = (double)ra;
                 r = __builtin_fma(r, __builtin_fma(-d, r, 1.0), r);
                 T64[p] = valid[p] ? T64[p] * r : T64[p];
-                T[p] = (float)T64[p];
-                const float fac = valid[p] ? alpha * T[p] : 0.f;
+                const float fac = valid[p] ? alpha * (float)T64[p] : 0.f;
                 float scv = 0.f;
 #pragma unroll
                 for (int k = 0; k < CDIM; ++k) {
@@ -927,21 +921,20 @@ __device__ __forceinline__ void rasterize_bwd_tile(
                     cg[k] += fac * v_c[p][k];
                 }
                 // The two terms cancel for a Gaussian in front of much of
-                // the pixel's colour (Bv holds the colour behind it), so the
-                // difference and the running sum are taken in double: in
-                // float32 they put the conic gradient of such Gaussians up
-                // to 2.8x further from the exact value than a float32
+                // the pixel's colour (BK holds the colour behind it less K),
+                // so the difference and the running sum are taken in double:
+                // in float32 they put the conic gradient of such Gaussians
+                // up to 2.8x further from the exact value than a float32
                 // autograd evaluation of the same formula.
-                const float v_alpha =
-                    (float)(T64[p] * (double)scv - (Bv[p] - (double)Kv[p]) * r);
-                Bv[p] += (double)fac * (double)scv;
+                const float v_alpha = (float)(T64[p] * (double)scv - BK[p] * r);
+                BK[p] += (double)fac * (double)scv;
                 // a clamped alpha does not depend on the Gaussian's geometry
                 // or opacity
                 const float w = (valid[p] && !clamped) ? vis * v_alpha : 0.f;
-                Vo += w;
                 const float vs = -geo.z * w;
-                V += vs;
                 const float vy = vs * dy[p];
+                Vo += w;
+                V += vs;
                 Vy += vy;
                 Vyy += vy * dy[p];
                 if constexpr (ABS) {
@@ -985,6 +978,23 @@ __device__ __forceinline__ void rasterize_bwd_tile(
                 if (lane_id() < 16u && red_slot[f] >= 0)
                     s_acc[wave][t * NACC + red_slot[f]] = red[f];
             }
+        };
+        // Software pipeline over pairs of items: the next item's slot and
+        // geometry are read one item ahead, into the other of two register
+        // sets, so the two dependent LDS round trips overlap the current
+        // item's arithmetic and no register copies carry them over.
+        int t_a = n_work > 0 ? (int)s_list[wave][0] : 0;
+        float4 geo_a = s_geo[t_a], con_a = s_con[t_a];
+        for (int n = 0; n < n_work; n += 2) {
+            const int t_b = s_list[wave][min(n + 1, n_work - 1)];
+            const float4 geo_b = s_geo[t_b], con_b = s_con[t_b];
+            work_item(t_a, geo_a, con_a);
+            if (n + 1 >= n_work)
+                break;
+            t_a = s_list[wave][min(n + 2, n_work - 1)];
+            geo_a = s_geo[t_a];
+            con_a = s_con[t_a];
+            work_item(t_b, geo_b, con_b);
         }
         __syncthreads();
         // Flush: the batch's (slot, sum) pairs spread over all threads, one
