@@ -288,8 +288,15 @@ template <int CDIM> struct FwdSlot {
     float col[(CDIM + 1 + 3) / 4 * 4];    // CDIM colours, isect index bits, pad
 };
 
+// Eight waves per SIMD for the 16x16 kernel of up to five channels: its
+// registers fit 64 VGPRs without spills, and the two prefetch register sets
+// of the work loop would otherwise cost one wave of occupancy.
+template <int CDIM, int TILE> constexpr int fwd_min_waves() {
+    return (TILE == 16 && CDIM <= 5) ? 8 : 1;
+}
+
 template <int CDIM, int TILE>
-__global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
+__global__ void __launch_bounds__(TILE * TILE, (fwd_min_waves<CDIM, TILE>())) rasterize_fwd_kernel(
     const RasterArgs a, float *__restrict__ render_colors,
     float *__restrict__ render_alphas, int32_t *__restrict__ last_ids,
     float *__restrict__ render_T, const ReplayState rs) {
@@ -400,27 +407,16 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
         const int n_work = wave_work_list_parts<Q>(s_wmask, batch_size, wave,
                                                    s_list[wave], part_end);
         const int n_parts = (batch_size + Q - 1) / Q;
-        int n = 0;
-        for (int q = 0; q < n_parts; ++q) {
-        const float T_part = T;
-        const uint64_t done_part = done_m;
-        // wave-uniform loop; a lane that is done (or skips a Gaussian) is
-        // carried by selects, not branches
-        for (; n < part_end[q]; ++n) {
-            if (done_m == lanes_m) {
-                n = n_work;
-                break;
-            }
-            const int t = s_list[wave][n];
+        // One work item: staged Gaussian t on this wave's strip.
+        auto work_item = [&](const int t, const float4 geo,
+                             const float4 con) __attribute__((always_inline)) {
             const FwdSlot<CDIM> &sl = s_slot[t];
-            const float4 geo = sl.geo;
-            const float4 con = sl.con;
             const float dx = geo.x - px, dy = geo.y - py;
             const float sigma = gauss_sigma(con.x, con.y, con.z, dx, dy);
             const uint64_t take_m =
                 wave_ballot(sigma >= 0.f) & wave_ballot(sigma <= geo.w) & ~done_m;
             if (take_m == 0)
-                continue;
+                return;
             // every lane runs the arithmetic (the exp clamps any sigma into
             // range); lanes that do not take the Gaussian keep their state
             // through selects
@@ -443,6 +439,40 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_fwd_kernel(
             cur_idx = upd ? slot_idx : cur_idx;
             T = upd ? next_T : T;
             done_m |= take_m & stop_m;
+        };
+        int n = 0;
+        for (int q = 0; q < n_parts; ++q) {
+        const float T_part = T;
+        const uint64_t done_part = done_m;
+        // wave-uniform loop over the part's items in pairs: the next item's
+        // slot and geometry are read one item ahead, into the other of two
+        // register sets, so the list and geometry round trips overlap the
+        // current item's arithmetic and no register copies carry them over
+        const int n_end = part_end[q];
+        if (n < n_end) {
+            int t_a = s_list[wave][n];
+            float4 geo_a = s_slot[t_a].geo, con_a = s_slot[t_a].con;
+            for (; n < n_end; n += 2) {
+                if (done_m == lanes_m) {
+                    n = n_work;
+                    break;
+                }
+                const int t_b = s_list[wave][min(n + 1, n_end - 1)];
+                const float4 geo_b = s_slot[t_b].geo, con_b = s_slot[t_b].con;
+                work_item(t_a, geo_a, con_a);
+                if (n + 1 >= n_end) {
+                    n = n_end;
+                    break;
+                }
+                if (done_m == lanes_m) {
+                    n = n_work;
+                    break;
+                }
+                t_a = s_list[wave][min(n + 2, n_end - 1)];
+                geo_a = s_slot[t_a].geo;
+                con_a = s_slot[t_a].con;
+                work_item(t_b, geo_b, con_b);
+            }
         }
         const int m = b * kReplayParts + q;
         if (rs.records != nullptr && m >= 1 &&
