@@ -25,7 +25,7 @@ __global__ void __launch_bounds__(kShThreads)
                   const uint8_t *__restrict__ masks, float *__restrict__ colors,
                   bool vec_ok) {
     using S = ShShape<DEG>;
-    __shared__ float s_coef[kShThreads * S::PITCH];
+    __shared__ alignas(16) float s_coef[kShThreads * S::PITCH];
     const int64_t r0 = (int64_t)blockIdx.x * kShThreads;
     const int nrows = (int)((M - r0) < kShThreads ? (M - r0) : kShThreads);
     stage_coeffs<DEG>(coeffs, r0, nrows, K, vec_ok, s_coef);
@@ -67,7 +67,7 @@ __global__ void __launch_bounds__(kShThreads)
                   float *__restrict__ v_coeffs, float *__restrict__ v_dirs,
                   bool vec_ok) {
     using S = ShShape<DEG>;
-    __shared__ float s_buf[kShThreads * S::PITCH];
+    __shared__ alignas(16) float s_buf[kShThreads * S::PITCH];
     const int64_t r0 = (int64_t)blockIdx.x * kShThreads;
     const int nrows = (int)((M - r0) < kShThreads ? (M - r0) : kShThreads);
     const int t = threadIdx.x;
@@ -128,12 +128,23 @@ __global__ void __launch_bounds__(kShThreads)
             sh_basis<DEG>(x, y, z, Y);
         else
             Y[0] = kY0;
-        float *o = s_buf + t * S::PITCH;
+        float g[S::ROW];
 #pragma unroll
         for (int k = 0; k < S::NB; ++k) {
-            o[k * 3 + 0] = active ? Y[k] * vc0 : 0.f;
-            o[k * 3 + 1] = active ? Y[k] * vc1 : 0.f;
-            o[k * 3 + 2] = active ? Y[k] * vc2 : 0.f;
+            g[k * 3 + 0] = active ? Y[k] * vc0 : 0.f;
+            g[k * 3 + 1] = active ? Y[k] * vc1 : 0.f;
+            g[k * 3 + 2] = active ? Y[k] * vc2 : 0.f;
+        }
+        float *o = s_buf + t * S::PITCH;
+        if constexpr (S::VEC) {
+#pragma unroll
+            for (int k = 0; k < S::ROW; k += 4)
+                *reinterpret_cast<float4 *>(o + k) =
+                    make_float4(g[k], g[k + 1], g[k + 2], g[k + 3]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < S::ROW; ++k)
+                o[k] = g[k];
         }
     }
     __syncthreads();
@@ -143,17 +154,8 @@ __global__ void __launch_bounds__(kShThreads)
     if (vec_ok && K == S::NB) {
         float4 *dst4 = reinterpret_cast<float4 *>(dst);
         const int nvec = total >> 2;
-        for (int v = threadIdx.x; v < nvec; v += kShThreads) {
-            const int e = v << 2;
-            float vals[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int ek = e + k;
-                const int r = ek / S::ROW;
-                vals[k] = s_buf[r * S::PITCH + (ek - r * S::ROW)];
-            }
-            dst4[v] = make_float4(vals[0], vals[1], vals[2], vals[3]);
-        }
+        for (int v = threadIdx.x; v < nvec; v += kShThreads)
+            dst4[v] = staged_chunk<DEG>(s_buf, v << 2);
         for (int e = (nvec << 2) + threadIdx.x; e < total; e += kShThreads) {
             const int r = e / S::ROW;
             dst[e] = s_buf[r * S::PITCH + (e - r * S::ROW)];

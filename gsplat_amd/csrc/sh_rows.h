@@ -38,8 +38,34 @@ constexpr float kY4h = 0.6258357354491763f;
 template <int DEG> struct ShShape {
     static constexpr int NB = (DEG + 1) * (DEG + 1);
     static constexpr int ROW = NB * 3;
-    static constexpr int PITCH = (ROW % 2 == 0) ? ROW + 1 : ROW;
+    // LDS pitch of a staged row.  Rows of a multiple of four floats get a
+    // pitch of an odd number of 16-byte chunks: the staging's 16-byte stores,
+    // the threads' 16-byte row reads and the write-out's 16-byte reads then
+    // take distinct banks across a wave.  Other rows get an odd pitch (4-byte
+    // row reads on distinct banks).
+    static constexpr int PITCH = (ROW % 4 == 0) ? ((ROW / 4) % 2 == 1 ? ROW : ROW + 4)
+                                 : (ROW % 2 == 0) ? ROW + 1 : ROW;
+    static constexpr bool VEC = ROW % 4 == 0;
 };
+
+// The four floats at offset e (a multiple of 4) of a span of staged rows.
+template <int DEG>
+__device__ __forceinline__ float4 staged_chunk(const float *s, int e) {
+    using S = ShShape<DEG>;
+    if constexpr (S::VEC) {
+        const int r = e / S::ROW;
+        return *reinterpret_cast<const float4 *>(s + r * S::PITCH + (e - r * S::ROW));
+    } else {
+        float v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int ek = e + k;
+            const int r = ek / S::ROW;
+            v[k] = s[r * S::PITCH + (ek - r * S::ROW)];
+        }
+        return make_float4(v[0], v[1], v[2], v[3]);
+    }
+}
 
 // Basis values Y[0..NB) at the unit direction (x, y, z).
 template <int DEG>
@@ -183,12 +209,17 @@ __device__ __forceinline__ void stage_coeffs(const float *__restrict__ coeffs,
             if ((int)threadIdx.x + i * kShThreads >= nvec)
                 break;
             const int e = ((int)threadIdx.x + i * kShThreads) << 2;
-            const float vals[4] = {q[i].x, q[i].y, q[i].z, q[i].w};
+            if constexpr (S::VEC) {
+                const int row = e / S::ROW;
+                *reinterpret_cast<float4 *>(s + row * S::PITCH + (e - row * S::ROW)) = q[i];
+            } else {
+                const float vals[4] = {q[i].x, q[i].y, q[i].z, q[i].w};
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int ek = e + k;
-                const int row = ek / S::ROW;
-                s[row * S::PITCH + (ek - row * S::ROW)] = vals[k];
+                for (int k = 0; k < 4; ++k) {
+                    const int ek = e + k;
+                    const int row = ek / S::ROW;
+                    s[row * S::PITCH + (ek - row * S::ROW)] = vals[k];
+                }
             }
         }
         for (int e = (nvec << 2) + threadIdx.x; e < total; e += kShThreads) {
@@ -371,7 +402,7 @@ __device__ __forceinline__ void sh_rows_bwd_block(const ShRowsArgs &a,
                                                   float *__restrict__ v_coeffs,
                                                   int64_t r0, float vm[3]) {
     using S = ShShape<DEG>;
-    __shared__ float s_buf[kShThreads * S::PITCH];
+    __shared__ alignas(16) float s_buf[kShThreads * S::PITCH];
     __shared__ uint8_t s_vis[kShThreads];
     const int64_t BN = a.B * a.N;
     const int nrows = (int)((BN - r0) < kShThreads ? (BN - r0) : kShThreads);
@@ -449,9 +480,16 @@ __device__ __forceinline__ void sh_rows_bwd_block(const ShRowsArgs &a,
     __syncthreads();  // every thread is done reading its staged coefficients
     if (t < nrows) {
         float *o = s_buf + t * S::PITCH;
+        if constexpr (S::VEC) {
 #pragma unroll
-        for (int k = 0; k < S::ROW; ++k)
-            o[k] = acc[k];
+            for (int k = 0; k < S::ROW; k += 4)
+                *reinterpret_cast<float4 *>(o + k) =
+                    make_float4(acc[k], acc[k + 1], acc[k + 2], acc[k + 3]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < S::ROW; ++k)
+                o[k] = acc[k];
+        }
     }
     __syncthreads();
     const int rowlen = a.K * 3;
@@ -460,17 +498,8 @@ __device__ __forceinline__ void sh_rows_bwd_block(const ShRowsArgs &a,
     if (a.vec_ok) {
         float4 *dst4 = reinterpret_cast<float4 *>(dst);
         const int nvec = total >> 2;
-        for (int v = threadIdx.x; v < nvec; v += kShThreads) {
-            const int e = v << 2;
-            float vals[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int ek = e + k;
-                const int rr = ek / S::ROW;
-                vals[k] = s_buf[rr * S::PITCH + (ek - rr * S::ROW)];
-            }
-            dst4[v] = make_float4(vals[0], vals[1], vals[2], vals[3]);
-        }
+        for (int v = threadIdx.x; v < nvec; v += kShThreads)
+            dst4[v] = staged_chunk<DEG>(s_buf, v << 2);
         for (int e = (nvec << 2) + threadIdx.x; e < total; e += kShThreads) {
             const int rr = e / S::ROW;
             dst[e] = s_buf[rr * S::PITCH + (e - rr * S::ROW)];
