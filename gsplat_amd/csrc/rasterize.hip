@@ -128,9 +128,12 @@ __device__ __forceinline__ float4 alpha_support_box(float mx, float my, float a,
         return make_float4(__builtin_inff(), __builtin_inff(),
                            -__builtin_inff(), -__builtin_inff());
     const float det = a * c - b * b;
-    const float widen = 1.001f + 1e-6f * (a * c / det);
-    const float ex = sqrtf(2.f * sig_max * c / det) * widen + 1.f;
-    const float ey = sqrtf(2.f * sig_max * a / det) * widen + 1.f;
+    // hardware reciprocal and square root: a few ulp, far inside the widening
+    const float idet = __builtin_amdgcn_rcpf(det);
+    const float widen = 1.001f + 1e-6f * (a * c * idet);
+    const float s2 = 2.f * sig_max * idet;
+    const float ex = __builtin_amdgcn_sqrtf(s2 * c) * widen + 1.f;
+    const float ey = __builtin_amdgcn_sqrtf(s2 * a) * widen + 1.f;
     if (!(det > 0.f) || !(a > 0.f) || !(c > 0.f) || !(ex < 1e30f) ||
         !(ey < 1e30f))
         return make_float4(-__builtin_inff(), -__builtin_inff(),
