@@ -8,7 +8,9 @@
 // tensor, so one launch covers all tensors without per-element tensor lookup;
 // each thread moves 16-byte vectors (4 per chunk pass) so a wave issues
 // 1 KiB-wide coalesced loads; all of a thread's loads are issued before its
-// first update, and the accesses are non-temporal (streamed once).  The arithmetic is done in the order written
+// first update, and the loads are non-temporal (streamed once; the stores
+// stay ordinary, which measured 4% faster than non-temporal ones at 3.3 GB).
+// The arithmetic is done in the order written
 // above with contraction disabled, which makes the result bit-for-bit
 // reproducible by a float32 host restatement.
 #include "common.h"
@@ -21,16 +23,12 @@ constexpr int kAdamVecPerThread = 4;
 constexpr int64_t kAdamChunk = (int64_t)kAdamThreads * kAdamVecPerThread * 4;
 constexpr int kAdamMaxTensors = 24;
 
-// Streaming (non-temporal) 16-byte accesses: every byte is touched once, so
-// the lines are not worth keeping in the caches.
+// Streaming (non-temporal) 16-byte loads: every byte is read once, so the
+// lines are not worth keeping in the caches.
 typedef float gs_v4f __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float4 stream_load(const float4 *p) {
     const gs_v4f v = __builtin_nontemporal_load(reinterpret_cast<const gs_v4f *>(p));
     return make_float4(v.x, v.y, v.z, v.w);
-}
-__device__ __forceinline__ void stream_store(float4 *p, float4 x) {
-    const gs_v4f v = {x.x, x.y, x.z, x.w};
-    __builtin_nontemporal_store(v, reinterpret_cast<gs_v4f *>(p));
 }
 
 struct AdamDesc {
@@ -131,9 +129,9 @@ __global__ void __launch_bounds__(kAdamThreads)
                 if (row_valid(d, e0 + 3))
                     adam_update(p.w, g.w, m.w, v.w, d.lr, b1, b2, eps);
             }
-            stream_store(&p4[q], p);
-            stream_store(&m4[q], m);
-            stream_store(&v4[q], v);
+            p4[q] = p;
+            m4[q] = m;
+            v4[q] = v;
         }
         // scalar tail (numel not a multiple of 4) handled by the last chunk
         const int64_t tail_begin = nvec_total << 2;
