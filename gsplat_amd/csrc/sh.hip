@@ -92,7 +92,7 @@ __global__ void __launch_bounds__(kShThreads)
     }
     // direction gradient needs the coefficients
     if (DEG > 0 && v_dirs != nullptr) {
-        stage_coeffs<DEG>(coeffs, r0, nrows, K, vec_ok, s_buf);
+        stage_coeffs<DEG, true>(coeffs, r0, nrows, K, vec_ok, s_buf);
         __syncthreads();
         if (in_range) {
             float vdx = 0.f, vdy = 0.f, vdz = 0.f;
