@@ -23,13 +23,6 @@ constexpr int kAdamVecPerThread = 4;
 constexpr int64_t kAdamChunk = (int64_t)kAdamThreads * kAdamVecPerThread * 4;
 constexpr int kAdamMaxTensors = 24;
 
-// Streaming (non-temporal) 16-byte loads: every byte is read once, so the
-// lines are not worth keeping in the caches.
-typedef float gs_v4f __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ float4 stream_load(const float4 *p) {
-    const gs_v4f v = __builtin_nontemporal_load(reinterpret_cast<const gs_v4f *>(p));
-    return make_float4(v.x, v.y, v.z, v.w);
-}
 
 struct AdamDesc {
     float *p;
@@ -100,10 +93,10 @@ __global__ void __launch_bounds__(kAdamThreads)
             const int64_t q = vbase + (int64_t)it * kAdamThreads + threadIdx.x;
             ok[it] = q < nvec_total && (q << 2) < chunk_end;
             if (ok[it]) {
-                P[it] = stream_load(&p4[q]);
-                G[it] = stream_load(&g4[q]);
-                M[it] = stream_load(&m4[q]);
-                V[it] = stream_load(&v4[q]);
+                P[it] = ld_stream4(&p4[q]);
+                G[it] = ld_stream4(&g4[q]);
+                M[it] = ld_stream4(&m4[q]);
+                V[it] = ld_stream4(&v4[q]);
             }
         }
 #pragma unroll

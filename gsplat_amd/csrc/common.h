@@ -172,6 +172,15 @@ __device__ __forceinline__ float portable_expf_nonpos(float x) {
     return __builtin_ldexpf(p, (int32_t)kf);
 }
 
+// Non-temporal 16-byte load of data read once, in whole lines per wave (its
+// lines are not worth keeping in the caches).  Per-lane pieces of a line
+// must not use it: each piece would fetch the line again.
+__device__ __forceinline__ float4 ld_stream4(const float4 *p) {
+    typedef float v4f_t __attribute__((ext_vector_type(4)));
+    const v4f_t x = __builtin_nontemporal_load(reinterpret_cast<const v4f_t *>(p));
+    return make_float4(x.x, x.y, x.z, x.w);
+}
+
 // DPP row operations (gfx9 encodings).
 constexpr int kDppQuadXor1 = 0xB1;   // quad_perm:[1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4E;   // quad_perm:[2,3,0,1]

@@ -207,10 +207,7 @@ __device__ __forceinline__ void stage_coeffs(const float *__restrict__ coeffs,
             if (!take) {
                 q[i] = make_float4(0.f, 0.f, 0.f, 0.f);
             } else if constexpr (STREAM) {
-                typedef float v4f_t __attribute__((ext_vector_type(4)));
-                const v4f_t x =
-                    __builtin_nontemporal_load(reinterpret_cast<const v4f_t *>(src + v));
-                q[i] = make_float4(x.x, x.y, x.z, x.w);
+                q[i] = ld_stream4(src + v);
             } else {
                 q[i] = src[v];
             }
