@@ -411,9 +411,8 @@ __global__ void __launch_bounds__(TILE * TILE, (fwd_min_waves<CDIM, TILE>())) ra
                                                    s_list[wave], part_end);
         const int n_parts = (batch_size + Q - 1) / Q;
         // One work item: staged Gaussian t on this wave's strip.
-        auto work_item = [&](const int t, const float4 geo,
+        auto work_item = [&](const FwdSlot<CDIM> &sl, const float4 geo,
                              const float4 con) __attribute__((always_inline)) {
-            const FwdSlot<CDIM> &sl = s_slot[t];
             const float dx = geo.x - px, dy = geo.y - py;
             const float sigma = gauss_sigma(con.x, con.y, con.z, dx, dy);
             const uint64_t take_m =
@@ -453,16 +452,23 @@ __global__ void __launch_bounds__(TILE * TILE, (fwd_min_waves<CDIM, TILE>())) ra
         // current item's arithmetic and no register copies carry them over
         const int n_end = part_end[q];
         if (n < n_end) {
-            int t_a = s_list[wave][n];
-            float4 geo_a = s_slot[t_a].geo, con_a = s_slot[t_a].con;
+            // a slot's address, formed once where its entry is read (24-bit
+            // multiply: the list holds u8 slots)
+            auto slot = [&](int i) __attribute__((always_inline)) -> const FwdSlot<CDIM> * {
+                return reinterpret_cast<const FwdSlot<CDIM> *>(
+                    reinterpret_cast<const char *>(s_slot) +
+                    __umul24((uint32_t)s_list[wave][i], (uint32_t)sizeof(FwdSlot<CDIM>)));
+            };
+            const FwdSlot<CDIM> *sl_a = slot(n);
+            float4 geo_a = sl_a->geo, con_a = sl_a->con;
             for (; n < n_end; n += 2) {
                 if (done_m == lanes_m) {
                     n = n_work;
                     break;
                 }
-                const int t_b = s_list[wave][min(n + 1, n_end - 1)];
-                const float4 geo_b = s_slot[t_b].geo, con_b = s_slot[t_b].con;
-                work_item(t_a, geo_a, con_a);
+                const FwdSlot<CDIM> *sl_b = slot(min(n + 1, n_end - 1));
+                const float4 geo_b = sl_b->geo, con_b = sl_b->con;
+                work_item(*sl_a, geo_a, con_a);
                 if (n + 1 >= n_end) {
                     n = n_end;
                     break;
@@ -471,10 +477,10 @@ __global__ void __launch_bounds__(TILE * TILE, (fwd_min_waves<CDIM, TILE>())) ra
                     n = n_work;
                     break;
                 }
-                t_a = s_list[wave][min(n + 2, n_end - 1)];
-                geo_a = s_slot[t_a].geo;
-                con_a = s_slot[t_a].con;
-                work_item(t_b, geo_b, con_b);
+                sl_a = slot(min(n + 2, n_end - 1));
+                geo_a = sl_a->geo;
+                con_a = sl_a->con;
+                work_item(*sl_b, geo_b, con_b);
             }
         }
         const int m = b * kReplayParts + q;
@@ -898,7 +904,8 @@ __device__ __forceinline__ void rasterize_bwd_tile(
         const int t0 = max(0, batch_end - wave_bin_final);
         const int n_work = wave_work_list(s_wmask, t0, batch_size, wave, s_list[wave]);
         // One work item: Gaussian t of the batch on this wave's pixels.
-        auto work_item = [&](const int t, const float4 geo,
+        auto work_item = [&](const int t, const int col_o, const int acc_o,
+                             const float4 geo,
                              const float4 con) __attribute__((always_inline)) {
             const int32_t isect = batch_end - t;
             const float dx = geo.x - px;
@@ -950,7 +957,7 @@ __device__ __forceinline__ void rasterize_bwd_tile(
                 float scv = 0.f;
 #pragma unroll
                 for (int k = 0; k < CDIM; ++k) {
-                    scv += s_col[t * CDIM + k] * v_c[p][k];
+                    scv += s_col[col_o + k] * v_c[p][k];
                     cg[k] += fac * v_c[p][k];
                 }
                 // The two terms cancel for a Gaussian in front of much of
@@ -1009,25 +1016,32 @@ __device__ __forceinline__ void rasterize_bwd_tile(
                     red[f] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
                 }
                 if (lane_id() < 16u && red_slot[f] >= 0)
-                    s_acc[wave][t * NACC + red_slot[f]] = red[f];
+                    s_acc[wave][acc_o + red_slot[f]] = red[f];
             }
         };
         // Software pipeline over pairs of items: the next item's slot and
         // geometry are read one item ahead, into the other of two register
         // sets, so the two dependent LDS round trips overlap the current
         // item's arithmetic and no register copies carry them over.
+        // a slot's colour and sum offsets are formed where its entry is read
+        // (24-bit multiplies: the list holds u8 slots)
         int t_a = n_work > 0 ? (int)s_list[wave][0] : 0;
+        int col_a = (int)__umul24((uint32_t)t_a, CDIM), acc_a = (int)__umul24((uint32_t)t_a, NACC);
         float4 geo_a = s_geo[t_a], con_a = s_con[t_a];
         for (int n = 0; n < n_work; n += 2) {
             const int t_b = s_list[wave][min(n + 1, n_work - 1)];
+            const int col_b = (int)__umul24((uint32_t)t_b, CDIM);
+            const int acc_b = (int)__umul24((uint32_t)t_b, NACC);
             const float4 geo_b = s_geo[t_b], con_b = s_con[t_b];
-            work_item(t_a, geo_a, con_a);
+            work_item(t_a, col_a, acc_a, geo_a, con_a);
             if (n + 1 >= n_work)
                 break;
             t_a = s_list[wave][min(n + 2, n_work - 1)];
+            col_a = (int)__umul24((uint32_t)t_a, CDIM);
+            acc_a = (int)__umul24((uint32_t)t_a, NACC);
             geo_a = s_geo[t_a];
             con_a = s_con[t_a];
-            work_item(t_b, geo_b, con_b);
+            work_item(t_b, col_b, acc_b, geo_b, con_b);
         }
         __syncthreads();
         // Flush: the batch's (slot, sum) pairs spread over all threads, one
