@@ -117,14 +117,18 @@ __device__ __forceinline__ float portable_logf(float x) {
     return ef * 0x1.62e3p-1f + (lnm + ef * 0x1.2fefa2p-17f);
 }
 
-// Natural exponential by Cody-Waite range reduction and a Taylor polynomial:
+// Natural exponential by Cody-Waite range reduction and a minimax polynomial:
 // x = k ln2 + r with k = rint(x log2e), |r| <= ln2/2, r computed with a
 // two-part ln2 (the high part has 9 significant bits, so k*hi is exact);
-// e^r = sum_{n<=7} r^n/n! (truncation below 2^-27 relative) in Horner form
-// with fused multiply-adds; e^x = e^r * 2^k.  Error below 1 ulp over
-// [-87, 88]; 0 below that range, +inf above, NaN passes through.  Only
-// correctly rounded IEEE operations (fma, rint, mul) are used, so the host
-// oracle reproduces every bit with fmaf and rintf.
+// e^r ~ 1 + r + r^2/2 + c3 r^3 + ... + c6 r^6, the degree-6 polynomial of
+// least maximum relative error on [-ln2/2, ln2/2] with its first three
+// coefficients fixed to those of e^r (exact in float32), fitted by linear
+// programming (oracle/exp_poly_fit.py): 6.2e-9 relative, and float32
+// coefficients.  Horner form with fused multiply-adds; e^x = e^r * 2^k.
+// Error below 0.9 ulp over every float in [-87, 88] (checked exhaustively
+// against the double exp); 0 below that range, +inf above, NaN passes
+// through.  Only correctly rounded IEEE operations (fma, rint, mul) are
+// used, so the host oracle reproduces every bit with fmaf and rintf.
 __device__ __forceinline__ float portable_expf(float x) {
 #pragma clang fp contract(off)
     if (!(x == x))
@@ -136,11 +140,10 @@ __device__ __forceinline__ float portable_expf(float x) {
     const float kf = __builtin_rintf(x * 0x1.715476p+0f);
     float r = __builtin_fmaf(-kf, 0x1.63p-1f, x);
     r = __builtin_fmaf(-kf, -0x1.bd0106p-13f, r);
-    float p = 0x1.a01a02p-13f;
-    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
-    p = __builtin_fmaf(p, r, 0x1.111112p-7f);
-    p = __builtin_fmaf(p, r, 0x1.555556p-5f);
-    p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+    float p = 0x1.6e2dp-10f;
+    p = __builtin_fmaf(p, r, 0x1.1264c4p-7f);
+    p = __builtin_fmaf(p, r, 0x1.555414p-5f);
+    p = __builtin_fmaf(p, r, 0x1.55544ap-3f);
     p = __builtin_fmaf(p, r, 0.5f);
     p = __builtin_fmaf(p, r, 1.f);
     p = __builtin_fmaf(p, r, 1.f);
@@ -148,24 +151,23 @@ __device__ __forceinline__ float portable_expf(float x) {
     return p * scale;
 }
 
-// portable_expf without its range checks, for x that the caller knows to be
-// a non-NaN value <= 0 (the rasterizer's -sigma with 0 <= sigma <= ln(255 o)).
-// x is clamped to [-87, 0] (one med3), so for every x >= -87 the result is
-// bit-identical to portable_expf(x); below -87 it returns e^-87 instead of
-// 0, which can only matter for an opacity above e^87 / 255 (about 2.4e35).
-// The scaling by 2^k (k in [-126, 0]) is one ldexp, exactly the product
-// p * 2^k that portable_expf forms.
+// portable_expf without its range checks, for the rasterizer's -sigma: for
+// every x in [-87, 0] the result is bit-identical to portable_expf(x) (the
+// scaling by 2^k, k in [-126, 0], is one ldexp, exactly the product p * 2^k
+// that portable_expf forms).  The rasterizer uses the value only where
+// 0 <= sigma <= ln(255 o), so x >= -87 unless the opacity exceeds
+// e^87 / 255 (about 2.4e35); below -87 this returns the ldexp of the
+// polynomial (e^x to ~1 ulp, or 0) where portable_expf returns 0.  Other x
+// (NaN, positive, -inf) give values the callers select away.
 __device__ __forceinline__ float portable_expf_nonpos(float x) {
 #pragma clang fp contract(off)
-    x = __builtin_amdgcn_fmed3f(x, -87.f, 0.f);
     const float kf = __builtin_rintf(x * 0x1.715476p+0f);
     float r = __builtin_fmaf(-kf, 0x1.63p-1f, x);
     r = __builtin_fmaf(-kf, -0x1.bd0106p-13f, r);
-    float p = 0x1.a01a02p-13f;
-    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
-    p = __builtin_fmaf(p, r, 0x1.111112p-7f);
-    p = __builtin_fmaf(p, r, 0x1.555556p-5f);
-    p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+    float p = 0x1.6e2dp-10f;
+    p = __builtin_fmaf(p, r, 0x1.1264c4p-7f);
+    p = __builtin_fmaf(p, r, 0x1.555414p-5f);
+    p = __builtin_fmaf(p, r, 0x1.55544ap-3f);
     p = __builtin_fmaf(p, r, 0.5f);
     p = __builtin_fmaf(p, r, 1.f);
     p = __builtin_fmaf(p, r, 1.f);

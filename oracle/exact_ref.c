@@ -71,8 +71,9 @@ void oracle_portable_logf_array(const float *x, float *y, int64_t n) {
     for (int64_t i = 0; i < n; ++i) y[i] = oracle_portable_logf(x[i]);
 }
 
-/* e^x by Cody-Waite reduction (x = k ln2 + r, two-part ln2) and the Taylor
- * polynomial of e^r to degree 7 in fused multiply-adds: the device
+/* e^x by Cody-Waite reduction (x = k ln2 + r, two-part ln2) and the
+ * degree-6 minimax polynomial of e^r with 1 + r + r^2/2 fixed (coefficients
+ * from oracle/exp_poly_fit.py) in fused multiply-adds: the device
  * portable_expf, operation for operation (fmaf and rintf are correctly
  * rounded, so the bits agree). */
 float oracle_portable_expf(float x) {
@@ -82,11 +83,10 @@ float oracle_portable_expf(float x) {
     const float kf = rintf(x * 0x1.715476p+0f);
     float r = fmaf(-kf, 0x1.63p-1f, x);
     r = fmaf(-kf, -0x1.bd0106p-13f, r);
-    float p = 0x1.a01a02p-13f;
-    p = fmaf(p, r, 0x1.6c16c2p-10f);
-    p = fmaf(p, r, 0x1.111112p-7f);
-    p = fmaf(p, r, 0x1.555556p-5f);
-    p = fmaf(p, r, 0x1.555556p-3f);
+    float p = 0x1.6e2dp-10f;
+    p = fmaf(p, r, 0x1.1264c4p-7f);
+    p = fmaf(p, r, 0x1.555414p-5f);
+    p = fmaf(p, r, 0x1.55544ap-3f);
     p = fmaf(p, r, 0.5f);
     p = fmaf(p, r, 1.f);
     p = fmaf(p, r, 1.f);
