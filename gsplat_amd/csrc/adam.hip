@@ -8,9 +8,11 @@
 // tensor, so one launch covers all tensors without per-element tensor lookup;
 // each thread moves 16-byte vectors (4 per chunk pass) so a wave issues
 // 1 KiB-wide coalesced loads; all of a thread's loads are issued before its
-// first update, and the loads are non-temporal (streamed once; the stores
-// stay ordinary, which measured 4% faster than non-temporal ones at 3.3 GB).
-// The arithmetic is done in the order written
+// first update, and the accesses are non-temporal (streamed once).  Ordinary
+// stores made this kernel 4% faster at 3.3 GB but left its lines dirty in
+// the caches: the next training step's reads of the same parameters (the
+// trainer's torch.cat of the SH coefficients) then ran 23% slower, and the
+// step 2% slower.  The arithmetic is done in the order written
 // above with contraction disabled, which makes the result bit-for-bit
 // reproducible by a float32 host restatement.
 #include "common.h"
@@ -122,9 +124,9 @@ __global__ void __launch_bounds__(kAdamThreads)
                 if (row_valid(d, e0 + 3))
                     adam_update(p.w, g.w, m.w, v.w, d.lr, b1, b2, eps);
             }
-            p4[q] = p;
-            m4[q] = m;
-            v4[q] = v;
+            st_stream4(&p4[q], p);
+            st_stream4(&m4[q], m);
+            st_stream4(&v4[q], v);
         }
         // scalar tail (numel not a multiple of 4) handled by the last chunk
         const int64_t tail_begin = nvec_total << 2;

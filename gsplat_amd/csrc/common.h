@@ -183,6 +183,13 @@ __device__ __forceinline__ float4 ld_stream4(const float4 *p) {
     return make_float4(x.x, x.y, x.z, x.w);
 }
 
+// Non-temporal 16-byte store of data written once, in whole lines per wave.
+__device__ __forceinline__ void st_stream4(float4 *p, float4 x) {
+    typedef float v4f_t __attribute__((ext_vector_type(4)));
+    const v4f_t v = {x.x, x.y, x.z, x.w};
+    __builtin_nontemporal_store(v, reinterpret_cast<v4f_t *>(p));
+}
+
 // DPP row operations (gfx9 encodings).
 constexpr int kDppQuadXor1 = 0xB1;   // quad_perm:[1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4E;   // quad_perm:[2,3,0,1]
