@@ -802,10 +802,11 @@ __global__ void __launch_bounds__(kIsectThreads)
 //   4. tile_bounds_kernel: the first slot of every tile from the sorted keys
 //      (the reference's isect_offset_encode).
 //   5. tile_depth_sort_kernel: one workgroup per tile sorts the tile's rows
-//      stably on their 32 depth bits -- in LDS up to 3,072 rows (radix
-//      passes over the top 16 bits of the tile's depth range, then the
-//      rows that tie on those bits by insertion), through global scratch
-//      above -- and writes the 64-bit ids and the rows.
+//      stably on their 32 depth bits -- in LDS up to 2,560 or 4,096 rows,
+//      by the mean tile depth (radix passes over the top 16 bits of the
+//      tile's depth range, then the rows that tie on those bits by odd-even
+//      transposition), through global scratch above -- and writes the
+//      64-bit ids and the rows.
 // The reference sorts stably on image|tile|depth over row-order emission,
 // which orders by (image|tile, depth bits, row); steps 3 and 5 produce that
 // order.  The depth order is taken per tile (~1,000 rows at config 1) in LDS
@@ -994,7 +995,7 @@ constexpr int kSegRadix = 1 << kSegDigitBits;
 constexpr int kSegPasses = 32 / kSegDigitBits;
 // Tiles of up to CAP rows are sorted in LDS, larger ones through global
 // scratch; the kernel comes in two LDS capacities (tile_depth_sort_kernel).
-constexpr int kSegCapSmall = 3072;
+constexpr int kSegCapSmall = 2560;
 constexpr int kSegCapLarge = 4096;
 
 template <int MAXK>
@@ -1432,12 +1433,13 @@ __device__ __forceinline__ SegTile seg_tile(int64_t s, int64_t n,
 // sizes share one launch: a separate launch for the few large tiles (after
 // the small ones) put their whole sort on the critical path (25 us at
 // config 1 for ~50 tiles of 2,049-2,406 rows).  The LDS holds CAP rows:
-// 3,072 (30 KB, five workgroups per CU) where tiles average up to
+// 2,560 (25 KB, six workgroups per CU) where tiles average up to
 // kSegDeepMean rows, else 4,096 (38 KB, four per CU).  At config 1 (1,158
-// rows a tile on average) 4,096 took 62.5 us against 56-58 us and 2,048
-// (seven per CU, the ~50 larger tiles through global scratch) 92 us; at
-// config 4 (1,874 on average, 729 tiles of 3,073-3,802 rows) 3,072 sends a
-// fifth of the rows through global scratch.
+// rows a tile on average, 2,406 at most) 2,560 takes 51.7 us against
+// 54.5 us for 3,072 (five per CU), 4,096 took 62.5 us and 2,048 (seven per
+// CU, the ~50 larger tiles through global scratch) 92 us; at config 4
+// (1,874 on average, 729 tiles of 3,073-3,802 rows) 3,072 sent a fifth of
+// the rows through global scratch.
 template <int CAP>
 __global__ void __launch_bounds__(kSegThreads)
     tile_depth_sort_kernel(int64_t n, const int64_t *__restrict__ n_dev,

@@ -154,10 +154,10 @@ def test_offsets_empty_and_zero_isects():
 @pytest.mark.parametrize("N", [200, 700, 1400, 2800, 11000])
 def test_tile_first_sort_every_segment_size(N):
     """The tile-first sorted intersection sorts each tile's rows on their
-    depth bits in LDS (3,072 rows where tiles average up to 1,500 rows,
+    depth bits in LDS (2,560 rows where tiles average up to 1,500 rows,
     else 4,096) and through global scratch above that.  Rows with large
     radii put about N rows into each of the 12 tiles of every image: N up to
-    1,400 takes the 1-, 3- and 6-key paths of the smaller LDS, 2,800 the
+    1,400 takes the 1-, 5- and 10-key paths of the smaller LDS, 2,800 the
     16-key path of the larger one and 11,000 its global scratch.
     Depths are quantised (many ties, which must stay in row order) and half
     of them negative (their zero-extended bits order after every positive
@@ -174,8 +174,8 @@ def test_tile_first_sort_every_segment_size(N):
     depths = (np.round(rng.uniform(-3, 3, (C, N)) * 8) / 8).astype(np.float32)
     want = exact.isect_tiles(means2d, radii, depths, ts, tw, th)
     per_tile = np.bincount(want[1] >> 32, minlength=C * tw * th)
-    lo, hi = {200: (1, 256), 700: (257, 768), 1400: (769, 1536), 2800: (1537, 3072),
-              11000: (3073, None)}[N]
+    lo, hi = {200: (1, 256), 700: (513, 1280), 1400: (1281, 2560), 2800: (2561, 4096),
+              11000: (4097, None)}[N]
     assert per_tile.max() >= lo and (hi is None or per_tile.max() <= hi), per_tile.max()
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
     tpg = torch.empty((C, N), dtype=torch.int32, device=DEV)
@@ -196,9 +196,9 @@ def test_tile_first_sort_every_segment_size(N):
 
 
 @pytest.mark.parametrize("counts", [
-    # mean 983 rows a tile: the 3,072-row LDS (1, 3, 6 or 12 keys a thread,
-    # then global scratch)
-    (200, 700, 1400, 2800, 6000, 100, 100, 100, 100, 100, 100, 100),
+    # mean 1,008 rows a tile: the 2,560-row LDS (1, 2, 5 or 10 keys a
+    # thread, then global scratch)
+    (200, 400, 700, 1400, 2800, 6000, 100, 100, 100, 100, 100, 100),
     # mean 2,950: the 4,096-row LDS (2, 4, 8 or 16 keys a thread, then global
     # scratch)
     (200, 700, 1500, 3000, 6000, 4000, 4000, 4000, 4000, 4000, 2000, 2000),
