@@ -261,7 +261,10 @@ def rasterization(
             stats_slot.means2d = means2d
             meta["grad2d_stats_slot"] = stats_slot
         nnz = means2d.shape[0]
-        image_ids = camera_ids if B * C == 1 else batch_ids * C + camera_ids
+        # the rows' image ids are formed below, only if the intersection
+        # was not started inside the front end (two int64 passes over the
+        # rows at several cameras)
+        image_ids = None
     elif packed:
         proj_results = _project(
             means, covars, quats, scales, viewmats, Ks, width, height, eps2d,
@@ -365,6 +368,8 @@ def rasterization(
         tiles_per_gauss, isect_ids, flatten_ids, isect_offsets = _ops.isect_emit_sorted(
             isect_req.pop("state"))
     else:
+        if front_end:
+            image_ids = camera_ids if B * C == 1 else batch_ids * C + camera_ids
         tiles_per_gauss, isect_ids, flatten_ids = isect_tiles(
             means2d, radii, depths, tile_size, tile_width, tile_height,
             segmented=segmented, packed=packed, n_images=I, image_ids=image_ids,
