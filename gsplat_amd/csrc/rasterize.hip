@@ -419,6 +419,20 @@ __global__ void __launch_bounds__(TILE * TILE, (fwd_min_waves<CDIM, TILE>())) ra
                 wave_ballot(sigma >= 0.f) & wave_ballot(sigma <= geo.w) & ~done_m;
             if (take_m == 0)
                 return;
+            // the slot's colours and isect index in 16-byte reads, issued
+            // before the exp so that their LDS round trip passes behind it
+            constexpr int NQ = (CDIM + 1 + 3) / 4;
+            float cq[4 * NQ];
+#pragma unroll
+            for (int c = 0; c < NQ; ++c) {
+                const float4 v = reinterpret_cast<const float4 *>(sl.col)[c];
+                cq[4 * c + 0] = v.x;
+                cq[4 * c + 1] = v.y;
+                cq[4 * c + 2] = v.z;
+                cq[4 * c + 3] = v.w;
+            }
+            // keep the reads here: the scheduler would sink them to their use
+            __builtin_amdgcn_sched_barrier(0);
             // every lane runs the arithmetic (the exp clamps any sigma into
             // range); lanes that do not take the Gaussian keep their state
             // through selects
@@ -433,11 +447,8 @@ __global__ void __launch_bounds__(TILE * TILE, (fwd_min_waves<CDIM, TILE>())) ra
             const float w = upd ? alpha * T : 0.f;
 #pragma unroll
             for (int k = 0; k < CDIM; ++k)
-                seg[k] = fmaf(sl.col[k], w, seg[k]);
-            // read unconditionally: a conditional read becomes another
-            // exec-masked branch around one LDS load
-            int32_t slot_idx = __float_as_int(sl.col[CDIM]);
-            asm volatile("" : "+v"(slot_idx));
+                seg[k] = fmaf(cq[k], w, seg[k]);
+            const int32_t slot_idx = __float_as_int(cq[CDIM]);
             cur_idx = upd ? slot_idx : cur_idx;
             T = upd ? next_T : T;
             done_m |= take_m & stop_m;
