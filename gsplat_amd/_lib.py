@@ -22,7 +22,7 @@ _P = c_void_p
 # of include/gsplat_hip.h.  load() refuses a library built from any other
 # header, and a CPU test keeps this digest and _SIGNATURES equal to the
 # header's.  Change all three together.
-_ABI_VERSION = "32d339af5a896531"
+_ABI_VERSION = "0ed8ce82e6221bc5"
 
 # name -> argtypes (restype int unless listed in _RESTYPES)
 _SIGNATURES = {
@@ -128,13 +128,13 @@ _SIGNATURES = {
         _P, _P, _P, _P, _P, _P, _P, _P],
     "gsplat_rasterize_replay_size": [c_int64, c_int32, c_int32, c_int32, c_int64, c_int32],
     "gsplat_rasterize_fwd_replay": [
-        c_int64, c_int64, c_int64, c_int32, _P, _P, _P, _P, _P, _P,
+        c_int64, c_int64, c_int64, c_int32, _P, _P, _P, _P, _P, _P, _P,
         c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P, _P,
         c_size_t, c_int32, _P, _P, c_int64, _P],
     "gsplat_rasterize_bwd_replay": [
-        c_int64, c_int64, c_int64, c_int32, _P, _P, _P, _P, _P, _P,
+        c_int64, c_int64, c_int64, c_int32, _P, _P, _P, _P, _P, _P, _P,
         c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P,
-        _P, _P, _P, _P, _P, _P, _P, c_size_t, _P, c_int32, _P],
+        _P, _P, _P, _P, _P, _P, _P, _P, c_size_t, _P, c_int32, _P],
     "gsplat_quat_scale_to_covar_preci_fwd": [c_int64, _P, _P, c_int32, _P, _P, _P],
     "gsplat_quat_scale_to_covar_preci_bwd": [
         c_int64, _P, _P, c_int32, _P, _P, _P, _P, _P],

@@ -53,7 +53,22 @@ struct RasterArgs {
     // division.  -1: no channel is divided.
     int32_t ed_channel = -1;
     float *ed_depth = nullptr;
+    // Last channel kept apart (a depth channel appended to the colours):
+    // with color_last set the rows of colors hold CDIM - 1 channels and
+    // channel CDIM - 1 of row g is color_last[g], so no concatenated copy of
+    // the two is formed; the backward then writes that channel's gradient
+    // to v_color_last [n_rows] and the others to v_colors [n_rows, CDIM - 1].
+    const float *color_last = nullptr;
+    float *v_color_last = nullptr;
 };
+
+// Channel k of row g's colour (see RasterArgs::color_last).
+template <int CDIM>
+__device__ __forceinline__ float raster_colour(const RasterArgs &a, int64_t g, int k) {
+    if (a.color_last != nullptr)
+        return k == CDIM - 1 ? a.color_last[g] : a.colors[g * (CDIM - 1) + k];
+    return a.colors[g * CDIM + k];
+}
 
 // Replay state written by the forward for a backward split into units of
 // one part: Q = tile_size^2 / 4 consecutive intersections of a tile.
@@ -389,7 +404,7 @@ __global__ void __launch_bounds__(TILE * TILE, (fwd_min_waves<CDIM, TILE>())) ra
             sl.con = make_float4(ca, cb, cc, sig_clamp);
 #pragma unroll
             for (int k = 0; k < CDIM; ++k)
-                sl.col[k] = a.colors[(int64_t)g * CDIM + k];
+                sl.col[k] = raster_colour<CDIM>(a, g, k);
             sl.col[CDIM] = __int_as_float(idx);
             s_wmask[tr] = (uint8_t)strip_mask_exact<TILE, NW, WROWS>(
                 strip_mask<TILE, NW, WROWS>(
@@ -884,7 +899,7 @@ __device__ __forceinline__ void rasterize_bwd_tile(
                 s_con[slot] = make_float4(ca, cb, cc, sig_clamp);
 #pragma unroll
                 for (int k = 0; k < CDIM; ++k)
-                    s_col[slot * CDIM + k] = a.colors[(int64_t)g * CDIM + k];
+                    s_col[slot * CDIM + k] = raster_colour<CDIM>(a, g, k);
                 // which waves' pixel strips the Gaussian's alpha support can
                 // reach (wave w holds rows w * WROWS .. of the tile)
                 constexpr int WROWS = (kWave < NT ? kWave : NT) * PX / TILE;
@@ -1090,7 +1105,9 @@ __device__ __forceinline__ void rasterize_bwd_tile(
             else if (k < 5)
                 dst = v_conics + g * 3 + (k - 2);
             else if (k < 5 + CDIM)
-                dst = v_colors + g * CDIM + (k - 5);
+                dst = a.v_color_last == nullptr ? v_colors + g * CDIM + (k - 5)
+                      : k == 4 + CDIM           ? a.v_color_last + g
+                                                : v_colors + g * (CDIM - 1) + (k - 5);
             else if (k == 5 + CDIM)
                 dst = v_opacities + g;
             else
@@ -1270,8 +1287,8 @@ int check_raster(const RasterArgs &a, int cdim) {
     GS_REQUIRE(a.n_isects < (1ll << 31), "rasterize: more than 2^31 isects");
     GS_REQUIRE(a.tile_offsets != nullptr, "rasterize: NULL tile_offsets");
     if (a.n_isects > 0)
-        GS_REQUIRE(a.flatten_ids && a.means2d && a.conics && a.colors &&
-                       a.opacities,
+        GS_REQUIRE(a.flatten_ids && a.means2d && a.conics &&
+                       (a.colors || (a.color_last && cdim == 1)) && a.opacities,
                    "rasterize: NULL Gaussian buffer");
     switch (cdim) {
     case 1: case 2: case 3: case 4: case 5: case 8: case 9: case 16: case 17:
@@ -1405,7 +1422,8 @@ int rasterize_bwd_impl(const RasterArgs &a, int32_t cdim,
     GS_REQUIRE((render_alphas || render_transmittance) && last_ids &&
                    v_render_colors,
                "rasterize_bwd: NULL input");
-    GS_REQUIRE(v_means2d && v_conics && v_colors && v_opacities,
+    GS_REQUIRE(v_means2d && v_conics && v_opacities &&
+                   (v_colors || (a.v_color_last && cdim == 1)),
                "rasterize_bwd: NULL gradient output");
     const int64_t blocks = a.I * (int64_t)a.tile_width * a.tile_height;
     GS_REQUIRE(blocks < (1ll << 31), "rasterize_bwd: too many tiles");
@@ -1475,17 +1493,19 @@ extern "C" size_t gsplat_rasterize_replay_size(int64_t I, int32_t tile_width,
 extern "C" int gsplat_rasterize_fwd_replay(
     int64_t I, int64_t n_rows, int64_t n_isects, int32_t cdim,
     const float *means2d, const float *conics, const float *colors,
-    const float *opacities, const float *backgrounds, const uint8_t *masks,
-    int32_t image_width, int32_t image_height, int32_t tile_size,
-    int32_t tile_width, int32_t tile_height, const int32_t *tile_offsets,
-    const int32_t *flatten_ids, float *render_colors, float *render_alphas,
-    int32_t *last_ids, float *render_transmittance, void *replay,
-    size_t replay_bytes, int32_t expected_depth_channel, float *expected_depth,
-    float *zero_fill, int64_t zero_fill_count, gsplat_stream_t stream) {
+    const float *color_last, const float *opacities, const float *backgrounds,
+    const uint8_t *masks, int32_t image_width, int32_t image_height,
+    int32_t tile_size, int32_t tile_width, int32_t tile_height,
+    const int32_t *tile_offsets, const int32_t *flatten_ids,
+    float *render_colors, float *render_alphas, int32_t *last_ids,
+    float *render_transmittance, void *replay, size_t replay_bytes,
+    int32_t expected_depth_channel, float *expected_depth, float *zero_fill,
+    int64_t zero_fill_count, gsplat_stream_t stream) {
     clear_error();
     RasterArgs a{I, n_rows, n_isects, means2d, conics, colors, opacities,
                  backgrounds, masks, image_width, image_height, tile_size,
                  tile_width, tile_height, tile_offsets, flatten_ids};
+    a.color_last = color_last;
     GS_TRY(check_raster(a, cdim));
     GS_REQUIRE(render_transmittance != nullptr,
                "rasterize_fwd_replay: NULL render_transmittance");
@@ -1529,20 +1549,24 @@ extern "C" int gsplat_rasterize_bwd(
 extern "C" int gsplat_rasterize_bwd_replay(
     int64_t I, int64_t n_rows, int64_t n_isects, int32_t cdim,
     const float *means2d, const float *conics, const float *colors,
-    const float *opacities, const float *backgrounds, const uint8_t *masks,
-    int32_t image_width, int32_t image_height, int32_t tile_size,
-    int32_t tile_width, int32_t tile_height, const int32_t *tile_offsets,
-    const int32_t *flatten_ids, const float *render_transmittance,
-    const int32_t *last_ids, const float *v_render_colors,
-    const float *v_render_alphas, float *v_means2d_abs, float *v_means2d,
-    float *v_conics, float *v_colors, float *v_opacities,
-    uint32_t *tile_counter, const void *replay, size_t replay_bytes,
-    const float *expected_depth, int32_t expected_depth_channel,
-    gsplat_stream_t stream) {
+    const float *color_last, const float *opacities, const float *backgrounds,
+    const uint8_t *masks, int32_t image_width, int32_t image_height,
+    int32_t tile_size, int32_t tile_width, int32_t tile_height,
+    const int32_t *tile_offsets, const int32_t *flatten_ids,
+    const float *render_transmittance, const int32_t *last_ids,
+    const float *v_render_colors, const float *v_render_alphas,
+    float *v_means2d_abs, float *v_means2d, float *v_conics, float *v_colors,
+    float *v_color_last, float *v_opacities, uint32_t *tile_counter,
+    const void *replay, size_t replay_bytes, const float *expected_depth,
+    int32_t expected_depth_channel, gsplat_stream_t stream) {
     clear_error();
     RasterArgs a{I, n_rows, n_isects, means2d, conics, colors, opacities,
                  backgrounds, masks, image_width, image_height, tile_size,
                  tile_width, tile_height, tile_offsets, flatten_ids};
+    a.color_last = color_last;
+    a.v_color_last = v_color_last;
+    GS_REQUIRE((color_last == nullptr) == (v_color_last == nullptr),
+               "rasterize_bwd_replay: color_last and v_color_last go together");
     GS_TRY(check_raster(a, cdim));
     GS_REQUIRE(render_transmittance != nullptr,
                "rasterize_bwd_replay: NULL render_transmittance");

@@ -1051,6 +1051,7 @@ def rasterize_fwd_replay(
     flatten_ids: Tensor,
     expected_depth_channel: int = -1,
     absgrad: Optional[bool] = None,
+    color_last: Optional[Tensor] = None,
 ):
     """``rasterize_fwd_with_transmittance`` that also keeps the replay state of
     ``rasterize_bwd_replay`` (per-pixel records at every batch boundary of a
@@ -1058,11 +1059,14 @@ def rasterize_fwd_replay(
     output.  With ``expected_depth_channel`` >= 0 that channel of the render
     is divided by max(alpha, 1e-10) (rendering.py:1259-1267) and kept in the
     state for the backward.  With ``absgrad`` not None the launch also
-    zero-fills the accumulators of ``rasterize_bwd_replay``."""
+    zero-fills the accumulators of ``rasterize_bwd_replay``.  With
+    ``color_last`` [..., n] the render has one channel more than ``colors``,
+    its last one taken from ``color_last`` (a depth channel, without
+    concatenating it to the colours)."""
     image_dims, I, n_rows, tw, th = _raster_common(
         means2d, conics, colors, opacities, backgrounds, masks, tile_offsets,
         flatten_ids)
-    channels = colors.shape[-1]
+    channels = _raster_channels(colors, color_last, n_rows)
     dev = means2d.device
     H, W = int(image_height), int(image_width)
     renders = torch.empty(image_dims + (H, W, channels), dtype=_F32, device=dev)
@@ -1074,13 +1078,14 @@ def rasterize_fwd_replay(
                           dtype=torch.uint8, device=dev)
     accum = None
     if absgrad is not None:
-        accum = torch.empty(_bwd_accum_words(means2d, conics, colors, opacities, absgrad),
+        accum = torch.empty(_bwd_accum_words(means2d, conics, colors, opacities, absgrad,
+                                             color_last),
                             dtype=_F32, device=dev)
     ed = None
     if expected_depth_channel >= 0:
         ed = torch.empty(image_dims + (H, W), dtype=_F32, device=dev)
     call("gsplat_rasterize_fwd_replay", I, n_rows, n_isects, channels,
-         ptr(means2d), ptr(conics), ptr(colors), ptr(opacities),
+         ptr(means2d), ptr(conics), ptr(colors), ptr(color_last), ptr(opacities),
          ptr(backgrounds), ptr(masks), W, H, int(tile_size), tw, th,
          ptr(tile_offsets), ptr(flatten_ids), ptr(renders), ptr(alphas),
          ptr(last_ids), ptr(transmittance), ptr(records), records.numel(),
@@ -1090,11 +1095,25 @@ def rasterize_fwd_replay(
             RasterReplay(records, accum, ed, int(expected_depth_channel)))
 
 
-def _bwd_accum_words(means2d, conics, colors, opacities, absgrad: bool) -> int:
+def _bwd_accum_words(means2d, conics, colors, opacities, absgrad: bool,
+                     color_last=None) -> int:
     """Floats of the backward's accumulators: v_means2d, v_conics, v_colors,
-    v_opacities (, v_means2d_abs) and the one-word unit counter."""
+    v_opacities (, v_means2d_abs) (, v_color_last) and the one-word unit
+    counter."""
     n = means2d.numel() + conics.numel() + colors.numel() + opacities.numel() + 1
+    n += color_last.numel() if color_last is not None else 0
     return n + (means2d.numel() if absgrad else 0)
+
+
+def _raster_channels(colors: Tensor, color_last: Optional[Tensor], n_rows: int) -> int:
+    """Channels of the render: those of ``colors``, plus one for a separate
+    last channel ``color_last`` (one value per row)."""
+    if color_last is None:
+        return colors.shape[-1]
+    check_input(color_last, "color_last", _F32)
+    if color_last.numel() != n_rows or colors.numel() != n_rows * colors.shape[-1]:
+        raise RuntimeError("color_last must hold one value per row of colors")
+    return colors.shape[-1] + 1
 
 
 def rasterize_to_pixels_3dgs_fwd(
@@ -1198,13 +1217,15 @@ def rasterize_bwd_replay(
     v_render_colors: Tensor,
     v_render_alphas: Optional[Tensor],
     absgrad: bool,
+    color_last: Optional[Tensor] = None,
 ):
     """``rasterize_to_pixels_3dgs_bwd`` from the state of
     ``rasterize_fwd_replay`` on the same inputs: the replay runs one unit per
     forward batch instead of one per tile.  With the forward's expected-depth
     channel the colour gradient of that channel is taken through its division
     by the alpha.  The state's zeroed accumulators are used once; a second
-    backward allocates fresh zeros."""
+    backward allocates fresh zeros.  With ``color_last`` (as in the forward)
+    a sixth output holds its gradient."""
     image_dims, I, n_rows, tw, th = _raster_common(
         means2d, conics, colors, opacities, backgrounds, masks, tile_offsets,
         flatten_ids)
@@ -1217,8 +1238,9 @@ def rasterize_bwd_replay(
     if replay.channel >= 0 and (replay.expected_depth is None or
                                 replay.expected_depth.shape != v_render_colors.shape[:-1]):
         raise RuntimeError("the expected-depth channel needs the forward's expected depth")
-    channels = colors.shape[-1]
-    likes = [means2d, conics, colors, opacities] + ([means2d] if absgrad else [])
+    channels = _raster_channels(colors, color_last, n_rows)
+    likes = ([means2d, conics, colors, opacities] + ([means2d] if absgrad else [])
+             + ([color_last] if color_last is not None else []))
     sizes = [t.numel() for t in likes] + [1]
     accum, replay.accum = replay.accum, None
     if accum is not None:
@@ -1232,16 +1254,20 @@ def rasterize_bwd_replay(
     v_means2d, v_conics, v_colors, v_opacities = (
         parts[k].view(likes[k].shape) for k in range(4))
     v_means2d_abs = parts[4].view(means2d.shape) if absgrad else None
+    v_color_last = (parts[len(likes) - 1].view(color_last.shape)
+                    if color_last is not None else None)
     tile_counter = parts[-1]
     call("gsplat_rasterize_bwd_replay", I, n_rows, flatten_ids.numel(), channels,
-         ptr(means2d), ptr(conics), ptr(colors), ptr(opacities),
+         ptr(means2d), ptr(conics), ptr(colors), ptr(color_last), ptr(opacities),
          ptr(backgrounds), ptr(masks), int(image_width), int(image_height),
          int(tile_size), tw, th, ptr(tile_offsets), ptr(flatten_ids),
          ptr(render_transmittance), ptr(last_ids), ptr(v_render_colors),
          ptr(v_render_alphas), ptr(v_means2d_abs), ptr(v_means2d),
-         ptr(v_conics), ptr(v_colors), ptr(v_opacities), ptr(tile_counter),
-         ptr(replay.records), replay.records.numel(), ptr(replay.expected_depth),
-         replay.channel, _stream(means2d))
+         ptr(v_conics), ptr(v_colors), ptr(v_color_last), ptr(v_opacities),
+         ptr(tile_counter), ptr(replay.records), replay.records.numel(),
+         ptr(replay.expected_depth), replay.channel, _stream(means2d))
+    if color_last is not None:
+        return v_means2d_abs, v_means2d, v_conics, v_colors, v_opacities, v_color_last
     return v_means2d_abs, v_means2d, v_conics, v_colors, v_opacities
 
 

@@ -335,15 +335,28 @@ def _rasterize_to_pixels(
     packed: bool = False,
     absgrad: bool = False,
     expected_depth_channel: int = -1,
+    color_last: Optional[Tensor] = None,
 ) -> Tuple[Tensor, Tensor]:
     """rasterize_to_pixels; with ``expected_depth_channel`` >= 0 (at most 33
     channels) that channel of the render comes out divided by
     max(alpha, 1e-10), the expected depth rasterization() forms for render
     modes ED and RGB+ED (rendering.py:1259-1267), inside the rasterizer
-    kernels instead of by torch ops on the render and their backward."""
+    kernels instead of by torch ops on the render and their backward.  With
+    ``color_last`` (one value per row: [nnz] packed, [..., N] otherwise) the
+    render has a last channel more, taken from it: rasterization()'s depth
+    channel (rendering.py:1025-1045), which the replay kernels read where it
+    lies instead of from a concatenated copy of the colours."""
     image_dims = means2d.shape[:-2]
     channels = colors.shape[-1]
     device = means2d.device
+    if color_last is not None:
+        assert color_last.shape == colors.shape[:-1], color_last.shape
+        if channels + 1 > SUPPORTED_CHANNELS[-1] or \
+                _pad_channels(channels + 1) != channels + 1:
+            # a padded or chunked render takes the concatenated colours
+            colors = torch.cat([colors, color_last[..., None]], dim=-1)
+            color_last = None
+        channels = colors.shape[-1] + (1 if color_last is not None else 0)
     if packed:
         nnz = means2d.size(0)
         assert means2d.shape == (nnz, 2), means2d.shape
@@ -354,7 +367,7 @@ def _rasterize_to_pixels(
         N = means2d.size(-2)
         assert means2d.shape == image_dims + (N, 2), means2d.shape
         assert conics.shape == image_dims + (N, 3), conics.shape
-        assert colors.shape == image_dims + (N, channels), colors.shape
+        assert colors.shape == image_dims + (N, colors.shape[-1]), colors.shape
         assert opacities.shape == image_dims + (N,), opacities.shape
     if backgrounds is not None:
         # one background per image: packed rows carry no image dims, so the
@@ -384,6 +397,13 @@ def _rasterize_to_pixels(
     isect_offsets = isect_offsets.contiguous()
     flatten_ids = flatten_ids.contiguous()
 
+    if color_last is not None:
+        # no padding: the channel count is a compiled one
+        return _RasterizeToPixels.apply(
+            means2d, conics, colors.contiguous(), opacities, backgrounds, masks,
+            image_width, image_height, tile_size, isect_offsets, flatten_ids,
+            absgrad, expected_depth_channel, color_last.contiguous())
+
     def one(cols: Tensor, bgs: Optional[Tensor]) -> Tuple[Tensor, Tensor]:
         c = cols.shape[-1]
         pc = _pad_channels(c)
@@ -396,7 +416,7 @@ def _rasterize_to_pixels(
         rc, ra = _RasterizeToPixels.apply(
             means2d, conics, cols.contiguous(), opacities, bgs, masks,
             image_width, image_height, tile_size, isect_offsets, flatten_ids,
-            absgrad, expected_depth_channel,
+            absgrad, expected_depth_channel, None,
         )
         if pc != c:
             rc = rc[..., :c]
@@ -931,33 +951,42 @@ class _PackedFrontEnd(torch.autograd.Function):
 
 
 class _RasterizeToPixels(torch.autograd.Function):
-    """Tile rasterizer."""
+    """Tile rasterizer.  ``color_last`` (optional, one value per row): a last
+    channel kept apart from ``colors`` (rasterization()'s depth channel); the
+    replay kernels read and write it in place, the other path concatenates
+    it."""
 
     @staticmethod
     def forward(ctx, means2d, conics, colors, opacities, backgrounds, masks,
                 width, height, tile_size, isect_offsets, flatten_ids, absgrad,
-                ed_channel=-1):
+                ed_channel=-1, color_last=None):
         # With gradients ahead the forward also keeps the replay state, so
         # the backward runs one unit per forward batch instead of one per
         # tile (the reference replays whole tiles), unless that state would
         # exceed _ops.replay_budget_bytes.
         replay = None
         ed_depth = None
-        grads = any(ctx.needs_input_grad[:5])
+        grads = any(ctx.needs_input_grad[:5]) or ctx.needs_input_grad[13]
+        channels = colors.shape[-1] + (1 if color_last is not None else 0)
         if grads:
             th, tw = isect_offsets.shape[-2:]
             n_images = math.prod(isect_offsets.shape[:-2])
             replay_bytes = _ops.rasterize_replay_bytes(
-                n_images, tw, th, tile_size, flatten_ids.numel(), colors.shape[-1])
+                n_images, tw, th, tile_size, flatten_ids.numel(), channels)
             grads_by_replay = replay_bytes <= _ops.replay_budget_bytes
+        ctx.split_last = False
         if grads and grads_by_replay:
             # the launch also zero-fills the backward's accumulators
             render_colors, render_alphas, last_ids, render_T, replay = \
                 _ops.rasterize_fwd_replay(
                     means2d, conics, colors, opacities, backgrounds, masks,
                     width, height, tile_size, isect_offsets, flatten_ids,
-                    expected_depth_channel=ed_channel, absgrad=absgrad)
+                    expected_depth_channel=ed_channel, absgrad=absgrad,
+                    color_last=color_last)
+            ctx.split_last = color_last is not None
         else:
+            if color_last is not None:
+                colors = torch.cat([colors, color_last[..., None]], dim=-1)
             render_colors, render_alphas, last_ids, render_T = \
                 _ops.rasterize_fwd_with_transmittance(
                     means2d, conics, colors, opacities, backgrounds, masks,
@@ -970,7 +999,9 @@ class _RasterizeToPixels(torch.autograd.Function):
                     ed_depth = render_colors[..., ed_channel].clone()
         ctx.save_for_backward(means2d, conics, colors, opacities, backgrounds,
                               masks, isect_offsets, flatten_ids, render_T,
-                              last_ids, ed_depth)
+                              last_ids, ed_depth,
+                              color_last if ctx.split_last else None)
+        ctx.has_last = color_last is not None
         # the replay records and zeroed accumulators; the accumulators are
         # consumed by the first backward (a second backward through a
         # retained graph takes fresh zeros)
@@ -988,19 +1019,23 @@ class _RasterizeToPixels(torch.autograd.Function):
     def backward(ctx, v_render_colors: Optional[Tensor],
                  v_render_alphas: Optional[Tensor]):
         (means2d, conics, colors, opacities, backgrounds, masks, isect_offsets,
-         flatten_ids, render_T, last_ids, ed_depth) = ctx.saved_tensors
+         flatten_ids, render_T, last_ids, ed_depth, color_last) = ctx.saved_tensors
         if v_render_colors is None and v_render_alphas is None:
-            return (None,) * 13
+            return (None,) * 14
+        channels = colors.shape[-1] + (1 if ctx.split_last else 0)
         if v_render_colors is None:
-            v_render_colors = render_T.new_zeros((*render_T.shape, colors.shape[-1]))
+            v_render_colors = render_T.new_zeros((*render_T.shape, channels))
         v_alphas = None if v_render_alphas is None else v_render_alphas.contiguous()
+        v_color_last = None
         if ctx.replay is not None:
-            (v_means2d_abs, v_means2d, v_conics, v_colors,
-             v_opacities) = _ops.rasterize_bwd_replay(
+            res = _ops.rasterize_bwd_replay(
                 means2d, conics, colors, opacities, backgrounds, masks, ctx.width,
                 ctx.height, ctx.tile_size, isect_offsets, flatten_ids,
                 render_T, last_ids, ctx.replay, v_render_colors.contiguous(), v_alphas,
-                ctx.absgrad)
+                ctx.absgrad, color_last=color_last)
+            v_means2d_abs, v_means2d, v_conics, v_colors, v_opacities = res[:5]
+            if ctx.split_last:
+                v_color_last = res[5]
         else:
             v_rc = v_render_colors
             if ctx.ed_channel >= 0:
@@ -1037,5 +1072,9 @@ class _RasterizeToPixels(torch.autograd.Function):
                 dim=(-3, -2))
         else:
             v_backgrounds = None
+        if ctx.has_last and not ctx.split_last:
+            # the concatenated colours' gradient, split back
+            v_color_last = v_colors[..., -1]
+            v_colors = v_colors[..., :-1]
         return (v_means2d, v_conics, v_colors, v_opacities, v_backgrounds,
-                None, None, None, None, None, None, None, None)
+                None, None, None, None, None, None, None, None, v_color_last)

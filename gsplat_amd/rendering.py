@@ -348,10 +348,19 @@ def rasterization(
             proj_features = (torch.cat(feature_list, dim=-1)
                              if len(feature_list) > 1 else feature_list[0])
 
+    # The depth channel, when the rasterizer reads it from the depths where
+    # they lie (one call of at most 33 channels, no extra signals) instead of
+    # from a copy of the features with the depths concatenated
+    # (rendering.py:1025-1045 concatenates).
+    depth_last = None
     if render_mode_has_depth(render_mode):
         depth_channel = depths[..., None]
         if proj_features is not None:
-            proj_features = torch.cat((proj_features, depth_channel), dim=-1)
+            if (extra_signals is None and proj_features.shape[-1] + 1
+                    <= min(channel_chunk, SUPPORTED_CHANNELS[-1])):
+                depth_last = depths
+            else:
+                proj_features = torch.cat((proj_features, depth_channel), dim=-1)
             if backgrounds is not None:
                 backgrounds = torch.cat(
                     [backgrounds,
@@ -387,13 +396,15 @@ def rasterization(
 
     # the expected depth divided by the alpha inside the rasterizer
     # (rendering.py:1259-1267 forms it with torch ops on the render)
+    n_feat = proj_features.shape[-1] + (1 if depth_last is not None else 0)
     ed_in_kernel = (render_mode_has_expected_depth(render_mode) and extra_signals is None
-                    and proj_features.shape[-1] <= min(channel_chunk, SUPPORTED_CHANNELS[-1]))
-    if ed_in_kernel:
+                    and n_feat <= min(channel_chunk, SUPPORTED_CHANNELS[-1]))
+    if ed_in_kernel or depth_last is not None:
         render_colors, render_alphas = _rasterize_to_pixels(
             means2d, conics, proj_features, opacities, width, height, tile_size,
             isect_offsets, flatten_ids, backgrounds=backgrounds, packed=packed,
-            absgrad=absgrad, expected_depth_channel=proj_features.shape[-1] - 1)
+            absgrad=absgrad, expected_depth_channel=n_feat - 1 if ed_in_kernel else -1,
+            color_last=depth_last)
     elif proj_features.shape[-1] > channel_chunk:
         n_chunks = (proj_features.shape[-1] + channel_chunk - 1) // channel_chunk
         render_colors, render_alphas = [], []

@@ -691,7 +691,15 @@ int gsplat_rasterize_bwd(
  * zero_fill, zero_fill_count (NULL, 0 for none; no counterpart in the
  *   reference): a float buffer the forward launch also sets to zero, for
  *   the gradient accumulators gsplat_rasterize_bwd_replay adds into, so
- *   that no fill runs between the forward and the backward. */
+ *   that no fill runs between the forward and the backward.
+ * color_last (NULL for none; no counterpart in the reference, whose caller
+ *   concatenates a depth channel to the colours with torch,
+ *   gsplat/rendering.py:1025-1045): the last of the cdim channels kept
+ *   apart, colors then holding cdim - 1 channels per row (NULL when cdim is
+ *   1) and color_last [n_rows] the last one; the backward then writes that
+ *   channel's gradient to v_color_last [n_rows] and the others to v_colors
+ *   [n_rows, cdim - 1].  The outputs equal those of the concatenated rows
+ *   bit for bit. */
 size_t gsplat_rasterize_replay_size(
     int64_t I, int32_t tile_width, int32_t tile_height, int32_t tile_size,
     int64_t n_isects, int32_t cdim);
@@ -699,6 +707,7 @@ size_t gsplat_rasterize_replay_size(
 int gsplat_rasterize_fwd_replay(
     int64_t I, int64_t n_rows, int64_t n_isects, int32_t cdim,
     const float *means2d, const float *conics, const float *colors,
+    const float *color_last,
     const float *opacities, const float *backgrounds, const uint8_t *masks,
     int32_t image_width, int32_t image_height, int32_t tile_size,
     int32_t tile_width, int32_t tile_height,
@@ -711,6 +720,7 @@ int gsplat_rasterize_fwd_replay(
 int gsplat_rasterize_bwd_replay(
     int64_t I, int64_t n_rows, int64_t n_isects, int32_t cdim,
     const float *means2d, const float *conics, const float *colors,
+    const float *color_last,
     const float *opacities, const float *backgrounds, const uint8_t *masks,
     int32_t image_width, int32_t image_height, int32_t tile_size,
     int32_t tile_width, int32_t tile_height,
@@ -718,7 +728,8 @@ int gsplat_rasterize_bwd_replay(
     const float *render_transmittance, const int32_t *last_ids,
     const float *v_render_colors, const float *v_render_alphas,
     float *v_means2d_abs, float *v_means2d, float *v_conics,
-    float *v_colors, float *v_opacities, uint32_t *tile_counter,
+    float *v_colors, float *v_color_last, float *v_opacities,
+    uint32_t *tile_counter,
     const void *replay, size_t replay_bytes, const float *expected_depth,
     int32_t expected_depth_channel, gsplat_stream_t stream);
 

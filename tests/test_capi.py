@@ -177,10 +177,16 @@ def test_replay_workspace_size_and_checks_without_a_gpu(lib_path):
     assert _lib.query("gsplat_rasterize_replay_size", 1, 3, 2, 16, n_isects, cdim) == want
     assert _lib.query("gsplat_rasterize_replay_size", 1, 3, 2, 16, -1, cdim) == 0
     f = 256  # a fake, aligned device address
-    args = [1, 50, n_isects, cdim, f, f, f, f, None, None, 40, 30, 16, 3, 2, f, f]
+    # I, n_rows, n_isects, cdim, means2d, conics, colors, color_last,
+    # opacities, backgrounds, masks, W, H, tile_size, tile grid, offsets, ids
+    args = [1, 50, n_isects, cdim, f, f, f, None, f, None, None, 40, 30, 16, 3, 2, f, f]
+    # bwd_replay after args: render_T, last_ids, v_render_colors,
+    # v_render_alphas, v_means2d_abs, v_means2d, v_conics, v_colors,
+    # v_color_last, v_opacities, tile_counter, replay, replay_bytes,
+    # expected_depth, expected_depth_channel, stream
     with pytest.raises(RuntimeError, match="workspace"):
-        _lib.call("gsplat_rasterize_bwd_replay", *args, f, f, f, None, None, f, f, f, f,
-                  f, f, want - 1, None, -1, None)
+        _lib.call("gsplat_rasterize_bwd_replay", *args, f, f, f, None, None, f, f, f, None,
+                  f, f, f, want - 1, None, -1, None)
     with pytest.raises(RuntimeError, match="NULL replay"):
         _lib.call("gsplat_rasterize_fwd_replay", *args, f, f, f, f, None, want, -1, None,
                   None, 0, None)
@@ -188,16 +194,22 @@ def test_replay_workspace_size_and_checks_without_a_gpu(lib_path):
         _lib.call("gsplat_rasterize_fwd_replay", *args, f, f, f, f, f, want, -1, None,
                   None, 5, None)
     with pytest.raises(RuntimeError, match="tile_counter"):
-        _lib.call("gsplat_rasterize_bwd_replay", *args, f, f, f, None, None, f, f, f, f,
-                  None, f, want, None, -1, None)
+        _lib.call("gsplat_rasterize_bwd_replay", *args, f, f, f, None, None, f, f, f, None,
+                  f, None, f, want, None, -1, None)
     # the expected-depth channel: in range, and the backward needs the
     # forward's copy of it
     with pytest.raises(RuntimeError, match="expected_depth_channel"):
         _lib.call("gsplat_rasterize_fwd_replay", *args, f, f, f, f, f, want, cdim, f,
                   None, 0, None)
     with pytest.raises(RuntimeError, match="expected_depth"):
-        _lib.call("gsplat_rasterize_bwd_replay", *args, f, f, f, None, None, f, f, f, f,
-                  f, f, want, None, cdim - 1, None)
+        _lib.call("gsplat_rasterize_bwd_replay", *args, f, f, f, None, None, f, f, f, None,
+                  f, f, f, want, None, cdim - 1, None)
+    # a separate last channel: its gradient output goes with it
+    split = list(args)
+    split[7] = f
+    with pytest.raises(RuntimeError, match="color_last and v_color_last"):
+        _lib.call("gsplat_rasterize_bwd_replay", *split, f, f, f, None, None, f, f, f, None,
+                  f, f, f, want, None, -1, None)
 
 
 def test_reference_op_schemas_registered():

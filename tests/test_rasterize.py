@@ -195,6 +195,50 @@ def test_rasterize_expected_depth_in_kernel(D, bg, packed):
     np.testing.assert_array_equal(rc1.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("ed,packed", [(True, True), (False, True), (True, False)])
+def test_separate_last_channel_matches_concatenated(ed, packed):
+    """A last channel read from its own array (color_last: rasterization()'s
+    depth channel kept apart from the colours) gives the render of the
+    concatenated colours bit for bit, and their gradients, the last
+    channel's split off, to float32 summation order (the flush's atomics add
+    in any order)."""
+    from gsplat_amd.cuda._wrapper import _rasterize_to_pixels
+    data = projected_2d(seed=77, N=2000, C=2, D=4, packed=packed)
+    W, H, ts, C = data["W"], data["H"], data["tile"], data["C"]
+    offs, fl = data["offsets"].to(DEV), data["flatten_ids"].to(DEV)
+    g = torch.Generator().manual_seed(9)
+    bg = torch.rand(C, 4, generator=g).to(DEV)
+    v_rc = torch.randn(C, H, W, 4, generator=g).to(DEV)
+    v_ra = torch.randn(C, H, W, 1, generator=g).to(DEV)
+    ch = 3 if ed else -1
+    runs = []
+    for split in (False, True):
+        geo = [data[k].clone().to(DEV).requires_grad_()
+               for k in ("means2d", "conics", "opacities")]
+        col = data["colors"].to(DEV)
+        if split:
+            cols = [col[..., :3].contiguous().requires_grad_(),
+                    col[..., 3].contiguous().requires_grad_()]
+            rc, ra = _rasterize_to_pixels(geo[0], geo[1], cols[0], geo[2], W, H, ts, offs,
+                                          fl, backgrounds=bg, packed=packed,
+                                          expected_depth_channel=ch, color_last=cols[1])
+        else:
+            cols = [col.clone().requires_grad_()]
+            rc, ra = _rasterize_to_pixels(geo[0], geo[1], cols[0], geo[2], W, H, ts, offs,
+                                          fl, backgrounds=bg, packed=packed,
+                                          expected_depth_channel=ch)
+        ((rc * v_rc).sum() + (ra * v_ra).sum()).backward()
+        v_col = (torch.cat([cols[0].grad, cols[1].grad[..., None]], dim=-1) if split
+                 else cols[0].grad)
+        runs.append((rc.detach(), ra.detach(), [t.grad for t in geo] + [v_col]))
+    np.testing.assert_array_equal(runs[1][0].cpu().numpy(), runs[0][0].cpu().numpy())
+    np.testing.assert_array_equal(runs[1][1].cpu().numpy(), runs[0][1].cpu().numpy())
+    for name, a, b in zip(("v_means2d", "v_conics", "v_opacities", "v_colors"),
+                          runs[0][2], runs[1][2]):
+        assert bool(a.abs().sum() > 0), name
+        assert_close(b.cpu(), a.cpu(), RTOL, ATOL, name)
+
+
 def test_rasterize_backward_twice_through_retained_graph():
     """The forward zero-fills the backward's accumulators; the first backward
     adds into them and a second backward through the retained graph starts
