@@ -1173,7 +1173,11 @@ __global__ void __launch_bounds__(BwdShape<TILE>::THREADS) rasterize_bwd_kernel(
 // are the forward kernel's (exact sigma order, thresholds on sigma,
 // portable_expf), so the pairs agree with rasterize_fwd bit for bit.  COUNT
 // writes the per-pixel counts; otherwise the pairs go to the per-pixel
-// starts from the scan of those counts.  One workgroup per tile.
+// starts from the scan of those counts.  One workgroup per tile.  The write
+// pass takes each staged Gaussian's id modulo N once, at staging, and stores
+// only the Gaussian ids while compositing; each pixel's constant pixel id
+// fills its range afterwards, one pixel at a time per wave, in 64-lane
+// coalesced stores.
 template <int TILE, bool COUNT>
 __global__ void __launch_bounds__(TILE * TILE) rasterize_indices_kernel(
     const RasterArgs a, int64_t N, int64_t range_start, int64_t range_end,
@@ -1215,7 +1219,8 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_indices_kernel(
         const int32_t idx = batch_start + tr;
         if (idx < range_hi) {
             const int32_t g = a.flatten_ids[idx];
-            s_id[tr] = g;
+            if constexpr (!COUNT)
+                s_id[tr] = N >= (1ll << 31) ? g : (int32_t)((uint32_t)g % (uint32_t)N);
             const float2 xy = reinterpret_cast<const float2 *>(a.means2d)[g];
             const float o = a.opacities[g];
             float sig_max, sig_clamp;
@@ -1240,17 +1245,37 @@ __global__ void __launch_bounds__(TILE * TILE) rasterize_indices_kernel(
             const float next_T = T * (1.f - alpha);
             const bool stop = next_T <= kTransmittanceThreshold;
             const bool emit = take && !stop;
-            if (!COUNT && emit) {
-                gaussian_ids[base + cnt] = s_id[t] % N;
-                pixel_ids[base + cnt] = pix;
-            }
+            if (!COUNT && emit)
+                gaussian_ids[base + cnt] = s_id[t];
             cnt += emit ? 1u : 0u;
             T = emit ? next_T : T;
             done = done || (take && stop);
         }
     }
-    if (COUNT && inside)
-        counts[pix] = cnt;
+    if constexpr (COUNT) {
+        if (inside)
+            counts[pix] = cnt;
+    } else {
+        // every thread leaves the batch loop together (its exits are
+        // workgroup-uniform), so the barrier below is reached by all
+        __shared__ uint32_t s_pbase[BS];
+        __shared__ uint32_t s_pcnt[BS];
+        s_pbase[tr] = base;
+        s_pcnt[tr] = cnt;  // 0 outside the image
+        __syncthreads();
+        // a wave's lanes: 64, or all BS threads of a smaller tile (4x4 tiles
+        // run 16 lanes, and the stride is theirs)
+        constexpr uint32_t NL = BS < kWave ? BS : kWave;
+        const int w0 = tr - (int)lane_id();  // the wave's first thread
+        for (int q = 0; q < (int)NL; ++q) {
+            const int tq = w0 + q;
+            const uint32_t sq = s_pbase[tq], cq = s_pcnt[tq];
+            const int64_t pq =
+                ((int64_t)image * a.H + ty * TILE + tq / TILE) * a.W + tx * TILE + tq % TILE;
+            for (uint32_t k = lane_id(); k < cq; k += NL)
+                pixel_ids[sq + k] = pq;
+        }
+    }
 }
 
 __global__ void indices_total_kernel(const uint32_t *__restrict__ starts,

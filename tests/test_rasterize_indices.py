@@ -34,11 +34,20 @@ def _run(d, range_start, range_end, T):
     return eg
 
 
-@pytest.mark.parametrize("tile", [16, 8])
+@pytest.mark.parametrize("tile", [16, 8, 4])
 def test_indices_full_range(tile):
     d = projected_2d(seed=3, N=600, C=1, W=64, H=48, tile=tile)
     eg = _run(d, 0, 10 ** 10, torch.ones(1, d["H"], d["W"]))
     assert eg.size > 1000
+
+
+@pytest.mark.parametrize("tile", [16, 8, 4])
+def test_indices_ragged_image(tile):
+    # image edges inside the last tile row and column: those tiles' outside
+    # pixels composite nothing and own empty ranges
+    d = projected_2d(seed=7, N=400, C=2, W=37, H=29, tile=tile)
+    eg = _run(d, 0, 10 ** 10, torch.ones(2, d["H"], d["W"]))
+    assert eg.size > 500
 
 
 def test_indices_batch_ranges_and_transmittances():
