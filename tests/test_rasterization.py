@@ -80,6 +80,30 @@ def test_cfg0_toy_packed():
     _check(make_scene(0))
 
 
+@pytest.mark.parametrize("packed", [True, False])
+def test_stacked_opaque_gaussians_clamped_alpha(packed):
+    """16 Gaussians of opacity 1.0 stacked at one depth and (nearly) one
+    spot, the scene of the reference's high-opacity regression test
+    (tests/test_basic.py:3455-3531, whose note asks for the same check on the
+    3DGS path): every covered pixel's alpha hits the 0.99 clamp, T falls
+    below 1e-4 after two of them, the backward recovers T through two
+    divisions by 0.01, and the equal depths are ordered by index.  Gradients
+    must be finite and within the gate of the float64 restatement."""
+    from gsplat_amd._helper import Scene
+    g = torch.Generator().manual_seed(123)
+    N = 16
+    means = torch.zeros(N, 3)
+    means[:, 2] = 3.0
+    means[:, :2] = torch.randn(N, 2, generator=g) * 1e-3
+    quats = torch.nn.functional.normalize(torch.randn(N, 4, generator=g), dim=-1)
+    scales = torch.full((N, 3), 0.5)
+    K = torch.tensor([[200.0, 0.0, 32.0], [0.0, 200.0, 24.0], [0.0, 0.0, 1.0]])[None]
+    scene = Scene("stacked", means, quats, scales, torch.ones(N),
+                  torch.rand(N, 3, generator=g), torch.eye(4)[None], K, 64, 48, None,
+                  torch.zeros(1, 48, 64, 3))
+    _check(scene, packed=packed)
+
+
 def test_cfg0_toy_unpacked_antialiased_bg():
     _check(make_scene(0), packed=False, rasterize_mode="antialiased", bg=True)
 
