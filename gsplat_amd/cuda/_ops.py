@@ -685,17 +685,19 @@ def projection_packed_bwd_rows_sh(
 # the packed path, rendering.py:95-213, 782, 845-873)
 # --------------------------------------------------------------------------
 def sh_rows_fwd(degree: int, means: Tensor, viewmats: Tensor, coeffs: Tensor,
-                row_of: Tensor, nnz: int) -> Tensor:
+                row_of: Tensor, nnz: int, fill: Optional[float] = None) -> Tensor:
     """colors [nnz, 3] = max(SH(normalize(mean - centre)) + 0.5, 0) for every
     packed row, centre = -R^T t of the camera; means [B, N, 3], viewmats
-    [B, C, 4, 4], coeffs [B, N, K, 3]."""
+    [B, C, 4, 4], coeffs [B, N, K, 3].  Rows that no entry of row_of names
+    hold ``fill`` (left unset when it is None)."""
     for t, n in ((means, "means"), (viewmats, "viewmats"), (coeffs, "coeffs")):
         check_input(t, n, _F32)
     check_input(row_of, "row_of", _I32)
     B, N = means.shape[0], means.shape[1]
     C = viewmats.shape[1]
     K = coeffs.shape[-2]
-    colors = torch.empty(nnz, 3, dtype=_F32, device=means.device)
+    colors = (torch.empty(nnz, 3, dtype=_F32, device=means.device) if fill is None
+              else torch.full((nnz, 3), fill, dtype=_F32, device=means.device))
     if nnz == 0:
         return colors
     call("gsplat_sh_rows_fwd", B, C, N, K, int(degree), ptr(means), ptr(viewmats),

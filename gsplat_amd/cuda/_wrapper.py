@@ -776,11 +776,14 @@ class _PackedSphericalHarmonics(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, degree: int, means: Tensor, coeffs: Tensor, viewmats: Tensor,
-                row_of: Tensor, nnz: int):
+                row_of: Tensor, nnz: int, fill: Optional[float] = None):
+        # ``fill``: the value of rows no entry of row_of names (a dense row
+        # map leaves the culled entries' rows unnamed)
         means = means.contiguous()
         coeffs = coeffs.contiguous()
         viewmats = viewmats.contiguous()
-        colors = _ops.sh_rows_fwd(degree, means, viewmats, coeffs, row_of, nnz)
+        colors = _ops.sh_rows_fwd(degree, means, viewmats, coeffs, row_of, nnz,
+                                  fill=fill)
         ctx.save_for_backward(means, coeffs, viewmats, row_of)
         ctx.degree = degree
         return colors
@@ -791,7 +794,7 @@ class _PackedSphericalHarmonics(torch.autograd.Function):
         v_coeffs, v_means = _ops.sh_rows_bwd(ctx.degree, means, viewmats, coeffs,
                                              row_of, v_colors.contiguous())
         return (None, v_means if ctx.needs_input_grad[1] else None,
-                v_coeffs if ctx.needs_input_grad[2] else None, None, None, None)
+                v_coeffs if ctx.needs_input_grad[2] else None, None, None, None, None)
 
 
 class Grad2dStatsSlot:

@@ -310,6 +310,23 @@ def rasterization(
             proj_features = _PackedSphericalHarmonics.apply(
                 colors_sh_degree, means.reshape(B, N, 3), colors.reshape(B, N, K, 3),
                 viewmats.reshape(B, C, 4, 4).detach(), row_of, nnz)
+    elif (not packed and colors_sh_degree is not None and extra_signals is None
+          and per_gaussian_colors and not viewmats.requires_grad):
+        # unpacked, per-Gaussian SH coefficients: the packed-row SH op over a
+        # dense row map (entry (b, c, g) is row (b*C + c)*N + g where its
+        # radii are positive, else -1), so the directions, the mask, the
+        # +0.5 clamp and their backward stay in its two launches
+        # (rendering.py:227-253, 845-873 run them as torch ops).  The
+        # projection gives both radii positive or both zero; entries the
+        # mask drops hold 0.5, the reference's clamp of a masked zero.
+        K = colors.shape[-2]
+        idx = torch.arange(B * C * N, device=means.device,
+                           dtype=torch.int32).view(B, C, N)
+        dense_rows = torch.where(radii.reshape(B, C, N, 2)[..., 0] > 0, idx, -1)
+        proj_features = _PackedSphericalHarmonics.apply(
+            colors_sh_degree, means.reshape(B, N, 3), colors.reshape(B, N, K, 3),
+            viewmats.reshape(B, C, 4, 4).detach(), dense_rows, B * C * N,
+            0.5).reshape(batch_dims + (C, N, 3))
     elif colors_sh_degree is None and extra_signals_sh_degree is None:
         feature_list = []
         if has_color:
